@@ -1,0 +1,109 @@
+/*
+ * hist_oracle.h -- CPU restatement of the reference's histogram tree-boosting
+ * path (tree_method='hist', depthwise growth).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker: it may be
+ * loaded by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
+ * leg, and by nothing else.  The product library never links or calls it.
+ *
+ * Every function follows a reference file:line (paths relative to the
+ * reference repository root); see the comments in hist_oracle.c.
+ */
+#ifndef HIST_ORACLE_H
+#define HIST_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Objectives (same codes as the reference: src/learner.cpp objective map). */
+enum { ORACLE_OBJ_SQUARED_ERROR = 0, ORACLE_OBJ_LOGISTIC = 1, ORACLE_OBJ_LOGITRAW = 2 };
+
+typedef struct {
+  int32_t objective;
+  int32_t max_depth;
+  int32_t max_bin;
+  int32_t fma_contract;      /* 1: binary64 gain uses fused multiply-adds (arm64 CPU build) */
+  float eta;
+  float reg_lambda;
+  float reg_alpha;
+  float min_child_weight;
+  float max_delta_step;
+  float min_split_loss;
+  float scale_pos_weight;
+  float base_score;          /* used when has_base_score != 0 */
+  int32_t has_base_score;
+  int32_t nthread;           /* histogram threads; results never depend on it */
+} OracleParams;
+
+/* One tree node; field meanings follow the reference's Node plus base_weights
+ * (include/metalgb/shared.h:27-31, src/tree.cpp:1049-1104). */
+typedef struct {
+  int32_t left, right, parent, feature;
+  float threshold, leaf, cover, gain;
+  uint32_t default_left;
+  float base_weight;
+} OracleNode;
+
+/* Best split candidate of one (node, feature) or one node; mirrors the
+ * reference's Split (include/metalgb/shared.h:124-134) restricted to the
+ * scalar numeric path. */
+typedef struct {
+  float gain, threshold, left_weight, right_weight, left_h, right_h;
+  float parent_weight, total_g, total_h;
+  int32_t feature;
+  uint32_t default_left;
+  uint32_t bin;              /* candidate bin b of the chosen split */
+  int64_t left_g, left_hs, right_g, right_hs;
+} OracleSplit;
+
+/* --- quantile sketch and bins ------------------------------------------ */
+uint32_t oracle_sketch_budget(uint32_t bins, uint32_t count);
+/* cuts: cols*max_bin floats; counts: cols; minima: cols.  weights may be NULL. */
+int oracle_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights,
+                       uint32_t max_bin, float* cuts, uint32_t* counts, float* minima);
+/* Row-major bins[r*cols+f]; 0xFFFF marks missing. */
+void oracle_quantize(const float* X, uint32_t rows, uint32_t cols, const float* cuts,
+                     const uint32_t* counts, uint32_t max_bin, uint16_t* bins);
+
+/* --- gradients ----------------------------------------------------------- */
+float oracle_base_score(int32_t objective, const float* labels, const float* weights, uint32_t rows,
+                        float scale_pos_weight);
+float oracle_base_margin(int32_t objective, float base_score);
+void oracle_gradients(int32_t objective, const float* margin, const float* labels, const float* weights,
+                      uint32_t rows, float scale_pos_weight, float* grad, float* hess);
+/* Power-of-two fixed-point scale of one gradient column. */
+float oracle_gradient_scale(const float* values, uint32_t rows);
+void oracle_quantize_gradients(const float* grad, const float* hess, uint32_t rows, float scale_g,
+                               float scale_h, int64_t* qg, int64_t* qh);
+
+/* --- histograms and splits ---------------------------------------------- */
+/* hist: cols*(max_bin+1)*2 int64 (g, h) per bin, bin max_bin = missing. */
+void oracle_histogram(const uint16_t* bins, uint32_t cols, uint32_t max_bin, const uint32_t* rows,
+                      uint32_t count, const int64_t* qg, const int64_t* qh, int64_t* hist);
+/* Evaluate one feature of one node; total_g/total_h are the node's integer sums. */
+void oracle_evaluate_feature(const int64_t* feature_hist, uint32_t count, const float* cuts, float minimum,
+                             int64_t total_g, int64_t total_h, float scale_g, float scale_h,
+                             const OracleParams* p, int32_t feature, OracleSplit* out);
+float oracle_weight(double G, double H, const OracleParams* p);
+float oracle_gain(double G, double H, float w, const OracleParams* p);
+
+/* --- training ------------------------------------------------------------ */
+uint32_t oracle_max_nodes(int32_t max_depth);
+/* Trains `rounds` trees.  trees: rounds*oracle_max_nodes(max_depth) nodes;
+ * tree_sizes: rounds; margin: rows (training margin after the last round).
+ * custom_grad/custom_hess (optional, rounds*rows) replace the objective. */
+int oracle_train(const float* X, uint32_t rows, uint32_t cols, const float* labels, const float* weights,
+                 const OracleParams* p, uint32_t rounds, const float* custom_grad, const float* custom_hess,
+                 OracleNode* trees, uint32_t* tree_sizes, float* margin, float* base_score_out,
+                 float* cuts_out, uint32_t* cut_counts_out);
+/* Margin of new rows: base_margin + sum of tree leaves (float traversal). */
+void oracle_predict_margin(const float* X, uint32_t rows, uint32_t cols, const OracleNode* trees,
+                           const uint32_t* tree_sizes, uint32_t rounds, uint32_t stride, float base_margin,
+                           float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
