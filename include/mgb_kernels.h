@@ -1,0 +1,135 @@
+/*
+ * mgb_kernels.h -- thin C ABI between the C++ host (learner, tree grower,
+ * XGBoost C API) and the HIP kernels for gfx950.
+ *
+ * Every entry point takes plain device pointers, sizes and POD parameter
+ * blocks, returns 0 on success or -1 on failure (message in
+ * mgb_last_error()), and enqueues its work on the library's single HIP
+ * stream.  It replaces the reference's Metal runtime and dispatch layer:
+ *   src/runtime.mm:37-455, include/metalgb/runtime.hpp:14-114
+ *   (Buffer, Runtime, Command::dispatch/zero/commit/wait).
+ * The POD layouts replace include/metalgb/shared.h:18-168 for this path.
+ */
+#ifndef MGB_KERNELS_H
+#define MGB_KERNELS_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime: device, stream, memory (src/runtime.mm:37-199) ---------- */
+int mgb_init(int device);
+const char* mgb_last_error(void);
+int mgb_device_count(int* count);
+int mgb_malloc(void** ptr, size_t bytes);
+int mgb_free(void* ptr);
+int mgb_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mgb_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int mgb_memcpy_d2d(void* dst, const void* src, size_t bytes);
+int mgb_memset(void* dst, int value, size_t bytes);
+int mgb_synchronize(void);
+/* Event timing on the library stream (src/runtime.mm:203-280 profiler). */
+int mgb_event_record(int slot);
+int mgb_event_elapsed_ms(int begin_slot, int end_slot, float* ms);
+
+/* ---- POD layouts ------------------------------------------------------ */
+
+/* Bin matrix: row-major, row_stride bytes per row, bin_bytes = 1 (u8) or 2
+ * (u16); code 0xFF / 0xFFFF marks a missing value. */
+typedef struct {
+  uint32_t rows, cols, row_stride, bin_bytes;
+  uint32_t max_bin;      /* histogram bins per feature; slot max_bin holds missing */
+  uint32_t cut_stride;   /* floats per feature in the cut array */
+  uint32_t missing_code;
+  uint32_t padding;
+} MgbMatrix;
+
+/* Per-round gradient statistics (replaces GradientParams/GradCert,
+ * include/metalgb/shared.h:58-62, :110-113). */
+typedef struct {
+  uint32_t rows, objective, has_weight, padding;
+  float scale_pos_weight, padding1, padding2, padding3;
+} MgbGradParams;
+
+/* Split regularisation (replaces SplitParams, include/metalgb/shared.h:114-119). */
+typedef struct {
+  float reg_lambda, reg_alpha, min_child_weight, max_delta_step;
+  float min_split_loss, eta;
+  uint32_t max_depth, fma_contract;
+} MgbSplitParams;
+
+/* One tree node as the host model consumes it (include/metalgb/shared.h:27-31
+ * plus base_weights). */
+typedef struct {
+  int32_t left, right, parent, feature;
+  float threshold, leaf, cover, gain;
+  uint32_t default_left;
+  float base_weight;
+} MgbTreeNode;
+
+/* Device-side tree workspace sizes; see mgb_tree_workspace_bytes. */
+typedef struct {
+  uint32_t rows, cols, max_bin, max_depth;
+  uint32_t rows_per_tile, features_per_group, unit_hessian, dense;
+} MgbTreeShape;
+
+/* ---- data: quantile cuts and bin matrix ------------------------------- */
+/* Weighted-quantile-sketch cuts of a row-major float matrix
+ * (src/quantile.cpp:22-212, kernels/quantile.metal.h:19-412).
+ * cuts: cols*max_bin floats, counts: cols.  weights may be NULL.  Allocates
+ * its temporary device memory and synchronises the stream (one-time set-up). */
+int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights, uint32_t max_bin,
+                    float* cuts, uint32_t* counts);
+/* bin = min(#{cuts <= v}, count-1); NaN -> missing code
+ * (kernels/boost.metal:476-499, src/data.cpp:1210-1306).  Sets *any_missing. */
+int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,
+                      uint32_t* any_missing);
+
+/* ---- gradients -------------------------------------------------------- */
+/* Objective gradients (kernels/boost.metal:553-601) written as float2 (g, h);
+ * also accumulates the exact |g|, |h| mass (kernels/gradient_quantization.metal.h:4-24)
+ * into mass[2*256] (u64 mantissa sums per binary32 exponent). */
+int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
+                  float* grad, uint64_t* mass);
+/* Mass of caller-provided gradients (custom objectives). */
+int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass);
+/* Power-of-two fixed-point scales (kernels/gradient_quantization.metal.h:26-67);
+ * writes scales[2] and clears mass for the next round. */
+int mgb_gradient_scales(uint64_t* mass, float* scales);
+/* Weighted label mean (src/learner.cpp:316-333): out[0] = binary32 mean. */
+int mgb_base_score(const float* labels, const float* weights, uint32_t rows, uint32_t objective,
+                   float scale_pos_weight, float* out);
+/* margin[r] = value for all rows. */
+int mgb_fill_f32(float* data, uint64_t count, float value);
+/* *flag (device) |= 1 if any of count floats is NaN. */
+int mgb_any_missing(const float* data, uint64_t count, uint32_t* flag);
+/* Output transform of margins: objective 1 (logistic) maps x -> 1/(1+exp(-x)). */
+int mgb_transform(float* data, uint64_t count, uint32_t objective);
+
+/* ---- one depthwise tree ---------------------------------------------- */
+size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
+/* Grows one depthwise tree on the device and adds its leaves to margin
+ * (src/tree.cpp:455-1029 GPU-driven tree + replay :1663-1717 and the
+ * prediction-cache update kernels/boost.metal:1738-1763).  Nothing is
+ * synchronised; nodes (2^(max_depth+1)-1 records) and node_count are device
+ * pointers filled by the time the stream drains. */
+int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
+                  const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
+                  void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes, uint32_t* node_count);
+
+/* ---- kernel-level entry points used by parity tests and the profiler --- */
+/* Histogram of rows [0, count) of row list `rows` (NULL = identity) into
+ * hist[cols][max_bin+1][2] int64 (kernels/boost.metal:700-733). */
+int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const uint32_t* rows,
+                  uint32_t count, const float* grad, const float* scales, int64_t* hist, void* workspace,
+                  size_t workspace_bytes);
+/* Prediction: margin[r] += leaf of each tree (kernels/boost.metal:1738-1763). */
+int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode* nodes, const uint32_t* tree_offsets,
+                uint32_t trees, float* margin);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

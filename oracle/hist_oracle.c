@@ -133,17 +133,26 @@ static uint32_t sk_combine(SkEntry* cur, uint32_t n, const SkEntry* other, uint3
   return count;
 }
 
+/* Total order on binary32 values with -0 before +0 (values are never NaN). */
+static uint32_t sk_order_key(float v) {
+  uint32_t bits;
+  memcpy(&bits, &v, 4);
+  return bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+}
+
 static int sk_run_order(const void* pa, const void* pb) {
   const SkRun* a = (const SkRun*)pa;
   const SkRun* b = (const SkRun*)pb;
-  if (a->value < b->value) return -1;
-  if (b->value < a->value) return 1;
+  uint32_t ka = sk_order_key(a->value), kb = sk_order_key(b->value);
+  if (ka != kb) return ka < kb ? -1 : 1;
   return a->order < b->order ? -1 : (a->order > b->order);
 }
 
-/* kernels/quantile.metal.h:216-240 (sketch_summarize_ordered).  Equal values
- * are merged in input order (a stable sort); the reference's libc++ tie
- * permutation only matters for weighted ties and is not restated. */
+/* kernels/quantile.metal.h:216-240 (sketch_summarize_ordered).  Runs are
+ * sorted by value (-0 before +0) and then by position, and equal values are
+ * merged in that order.  The reference instead reproduces libc++'s std::sort
+ * permutation for weighted or signed-zero ties (kernels/sketch_sort.metal.h);
+ * that tie order is not restated here (parity unpinned for such ties). */
 static uint32_t sk_summarize(SkRun* runs, uint32_t size, uint32_t limit, SkEntry* out) {
   qsort(runs, size, sizeof(SkRun), sk_run_order);
   uint32_t n = 0;

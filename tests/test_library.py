@@ -1,0 +1,67 @@
+"""The C-ABI library builds, loads without a GPU, and exports every entry
+point declared in include/*.h; the Python package imports over it."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+LIB = ROOT / "xgboost-metal_amd" / "python" / "xgboost" / "lib" / "libxgboost.so"
+
+
+def declared_functions(header):
+    text = header.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:XGB_DLL\s+)?(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s+\**([A-Za-z_][A-Za-z0-9_]*)\s*\(",
+                       text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "return")))
+
+
+@pytest.mark.parametrize("header", sorted((ROOT / "include").glob("*.h")), ids=lambda p: p.name)
+def test_exports_every_declared_symbol(header):
+    lib = ctypes.CDLL(str(LIB))
+    names = declared_functions(header)
+    assert len(names) > 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"{header.name}: not exported: {missing}"
+
+
+def test_version_and_error_without_gpu():
+    lib = ctypes.CDLL(str(LIB))
+    major, minor, patch = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    lib.XGBoostVersion(ctypes.byref(major), ctypes.byref(minor), ctypes.byref(patch))
+    assert (major.value, minor.value, patch.value) == (3, 5, 0)
+    lib.XGBGetLastError.restype = ctypes.c_char_p
+    # A null handle is rejected with a message, not a crash.
+    out = ctypes.c_uint64()
+    assert lib.XGDMatrixNumRow(None, ctypes.byref(out)) == -1
+    assert b"null" in lib.XGBGetLastError()
+
+
+def test_package_imports(xgb):
+    assert xgb.__version__ == "3.5.0-dev"
+    info = xgb.build_info()
+    assert info["USE_HIP"] is True and info["HIP_ARCH"] == "gfx950"
+
+
+def test_dmatrix_host_side(xgb):
+    import numpy as np
+    X = np.arange(12, dtype=np.float32).reshape(4, 3)
+    X[1, 2] = -999
+    d = xgb.DMatrix(X, label=[1, 2, 3, 4], missing=-999, feature_names=["a", "b", "c"])
+    assert d.num_row() == 4 and d.num_col() == 3 and d.num_nonmissing() == 11
+    np.testing.assert_array_equal(d.get_label(), [1, 2, 3, 4])
+    assert d.feature_names == ["a", "b", "c"]
+    import scipy.sparse as sp
+    csr = sp.csr_matrix(np.asarray([[0, 1.5], [2.0, 0]], np.float32))
+    d2 = xgb.DMatrix(csr)
+    assert d2.num_row() == 2 and d2.num_col() == 2 and d2.num_nonmissing() == 2
+
+
+def test_unsupported_parameters_fail_loudly(xgb):
+    import numpy as np
+    b = xgb.Booster({"tree_method": "exact"})
+    d = xgb.DMatrix(np.zeros((4, 2), np.float32), label=np.zeros(4))
+    with pytest.raises(xgb.XGBoostError, match="hist"):
+        b.update(d, 0)

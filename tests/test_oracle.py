@@ -1,0 +1,239 @@
+"""Pins the CPU oracle (oracle/hist_oracle.c) before it is trusted as the checker.
+
+- End to end: the reference's published prediction SHA-256s of stock XGBoost
+  3.4.1 CPU hist on its seed-1337 workloads.
+- Sketch/bins: closed forms for columns with few distinct values, invariants
+  otherwise, and the rank/budget rule of the sketch.
+- Quantization scale: arbitrary-precision integer arithmetic.
+- Scoring: exact-rational constructions that separate RN32(RN64(G/H)) from
+  RN32(G/H) (construction of the reference's tests/test_scalar_weight.py:29-71).
+- Trees: the constructed known answer of tests/test_histogram_present.py:66-81.
+"""
+import hashlib
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import workloads as W
+
+
+@pytest.mark.parametrize("case", ["dense100", "missing100",
+                                  pytest.param("dense262", marks=pytest.mark.slow)])
+def test_published_prediction_hashes(case):
+    spec = W.KNOWN_ANSWERS[case]
+    X, y = W.known_answer_data(case)
+    if "input_sha256" in spec:
+        assert hashlib.sha256(X.tobytes()).hexdigest() == spec["input_sha256"]
+        assert hashlib.sha256(y.tobytes()).hexdigest() == spec["label_sha256"]
+    r = O.train(X, y, O.make_params(max_depth=spec["depth"], max_bin=256, eta=0.3), 100)
+    pred = r["margin"]
+    assert hashlib.sha256(pred.tobytes()).hexdigest() == spec["prediction_sha256"]
+    rmse = float(np.sqrt(np.mean((pred.astype(np.float64) - y) ** 2)))
+    assert abs(rmse - spec["rmse"]) < 1e-12
+    # Traversal prediction of the stored trees equals the training margin.
+    again = O.predict_margin(X, r, r["base_score"])
+    np.testing.assert_array_equal(again.view(np.uint32), pred.view(np.uint32))
+
+
+def test_planted_mistake_breaks_known_answer():
+    """The known answer is sensitive: a one-ulp change of eta changes the hash."""
+    spec = W.KNOWN_ANSWERS["dense100"]
+    X, y = W.known_answer_data("dense100")
+    eta = float(np.nextafter(np.float32(0.3), np.float32(1)))
+    r = O.train(X[:20000], y[:20000], O.make_params(max_depth=6, max_bin=256, eta=eta), 5)
+    base = O.train(X[:20000], y[:20000], O.make_params(max_depth=6, max_bin=256, eta=0.3), 5)
+    assert not np.array_equal(r["margin"], base["margin"])
+    assert hashlib.sha256(base["margin"].tobytes()).hexdigest() != spec["prediction_sha256"]
+
+
+def test_sketch_budget_rule():
+    # limit = min(count, ceil(level * 2 * min(bins, count)) + 1) for the first level with 2^level*limit >= count.
+    def budget(bins, count):
+        if not count:
+            return 1
+        n = min(bins, count)
+        for level in range(1, 32):
+            limit = min(count, level * 2 * n + 1)
+            if (1 << level) * limit >= count:
+                return limit
+        return count
+    for bins, count in [(256, 100000), (256, 262144), (1024, 10_000_000), (4, 3), (256, 1), (16, 1000)]:
+        assert O.lib().oracle_sketch_budget(bins, count) == budget(bins, count)
+    assert O.lib().oracle_sketch_budget(256, 100000) == 3073
+
+
+def test_cuts_closed_form_few_distinct():
+    # At most max_bin distinct values: cuts are the distinct values after the
+    # first, then max + (|max| + 1e-5).
+    rng = np.random.default_rng(0)
+    values = np.asarray([-3.5, -1.0, 0.0, 0.25, 2.0, 7.0], np.float32)
+    X = rng.choice(values, size=(5000, 3)).astype(np.float32)
+    X[:, 2] = 4.0
+    cuts, counts, minima = O.sketch_cuts(X, 16)
+    for f in range(2):
+        d = np.unique(X[:, f])
+        want = np.append(d[1:], np.float32(d[-1] + (np.abs(d[-1]) + np.float32(1e-5))))
+        assert counts[f] == len(want)
+        np.testing.assert_array_equal(cuts[f, :counts[f]], want)
+    assert counts[2] == 1 and cuts[2, 0] == np.float32(4.0) + np.float32(4.0 + 1e-5)
+    assert np.all(np.isneginf(minima))
+
+
+def test_cuts_invariants_and_bins():
+    X, _ = W.config1(rows=50000, cols=6)
+    X[:, 1] = np.round(X[:, 1])
+    for max_bin in [4, 64, 256, 1024]:
+        cuts, counts, _ = O.sketch_cuts(X, max_bin)
+        bins = O.quantize(X, cuts, counts)
+        for f in range(X.shape[1]):
+            c = cuts[f, :counts[f]]
+            assert 1 <= counts[f] <= max_bin
+            assert np.all(np.diff(c) > 0), "strictly increasing"
+            col = X[:, f]
+            present = ~np.isnan(col)
+            assert c[-1] > np.nanmax(col)
+            # bin = min(upper_bound(cuts, v), count - 1); NaN -> missing.
+            want = np.minimum(np.searchsorted(c, col[present], side="right"), counts[f] - 1)
+            np.testing.assert_array_equal(bins[present, f], want)
+            assert np.all(bins[~present, f] == 0xFFFF)
+        # Equal-frequency property: every bin of a continuous feature holds a
+        # share close to 1/count (the sketch's rank error bound is ~1/max_bin).
+        b0 = bins[~np.isnan(X[:, 0]), 0]
+        share = np.bincount(b0, minlength=counts[0]) / len(b0)
+        assert share.max() < 3.0 / counts[0] + 0.01
+
+
+def _scale_reference(values):
+    total = sum(abs(Fraction(float(v))) for v in values) * (2 ** 149)
+    assert total.denominator == 1
+    bitlen = int(total).bit_length()
+    exponent = max(0, bitlen - 149)
+    return 2.0 ** (62 - exponent)
+
+
+@pytest.mark.parametrize("values", [
+    [1.0, -2.0, 3.5],
+    [np.finfo(np.float32).max] * 257,
+    [2.0 ** -149, 2.0 ** -149, 1e-40],
+    [0.0, -0.0],
+    list(np.random.default_rng(1).normal(size=5000).astype(np.float32)),
+    [2.0 ** 16, -(2.0 ** 16), 6.118193027759844e-7],
+])
+def test_gradient_scale_exact(values):
+    v = np.asarray(values, np.float32)
+    assert O.gradient_scale(v) == _scale_reference(v)
+
+
+def test_histogram_brute_force():
+    rng = np.random.default_rng(2)
+    X, _ = W.config1(rows=3000, cols=5)
+    cuts, counts, _ = O.sketch_cuts(X, 32)
+    bins = O.quantize(X, cuts, counts)
+    g = rng.normal(size=len(X)).astype(np.float32)
+    h = rng.uniform(0, 1, size=len(X)).astype(np.float32)
+    sg, sh = O.gradient_scale(g), O.gradient_scale(h)
+    qg = np.rint(g * np.float32(sg)).astype(np.int64)
+    qh = np.rint(h * np.float32(sh)).astype(np.int64)
+    rows = np.sort(rng.choice(len(X), 1000, replace=False)).astype(np.uint32)
+    hist = np.zeros((5, 33, 2), np.int64)
+    import ctypes
+    O.lib().oracle_histogram(O.ptr(bins), ctypes.c_uint32(5), ctypes.c_uint32(32), O.ptr(rows),
+                             ctypes.c_uint32(len(rows)), O.ptr(qg), O.ptr(qh), O.ptr(hist))
+    for f in range(5):
+        for b in range(33):
+            sel = rows[(np.where(bins[rows, f] == 0xFFFF, 32, bins[rows, f]) == b)]
+            assert hist[f, b, 0] == int(qg[sel].sum())
+            assert hist[f, b, 1] == int(qh[sel].sum())
+    # Invariant: each feature's bins (with missing) sum to the node total.
+    np.testing.assert_array_equal(hist[:, :, 0].sum(axis=1), np.full(5, qg[rows].sum()))
+
+
+def _float32_parts(value):
+    """Nonnegative binary32 values summing exactly to an integer."""
+    parts = []
+    while value:
+        part = np.float32(value)
+        if int(part) > value:
+            part = np.nextafter(part, np.float32(0))
+        parts.append(part)
+        value -= int(part)
+    return parts
+
+
+def _double_rounding_case(parity, inside_cell):
+    # Choose an exact quotient N/D just across a binary32 midpoint from its
+    # round-to-nearest-even side, so that RN32(RN64(N/D)) differs from
+    # RN32(N/D) exactly when the binary64 rounding lands on the midpoint.
+    q = 2 ** 23 + parity
+    delta = (1 if parity == 0 else -1) * (2 ** 23 + (-1 if inside_cell else 1))
+    modulus = 2 ** 24
+    denominator = 2 ** 52 + (-delta * pow(2 * q + 1, -1, modulus)) % modulus
+    numerator, remainder = divmod((2 * q + 1) * denominator + delta, modulus)
+    assert remainder == 0
+    return numerator, denominator
+
+
+@pytest.mark.parametrize("sign", [-1, 1])
+@pytest.mark.parametrize("parity", [0, 1])
+@pytest.mark.parametrize("inside_cell", [False, True])
+@pytest.mark.parametrize("split", [False, True])
+def test_weight_double_rounding(sign, parity, inside_cell, split):
+    numerator, denominator = _double_rounding_case(parity, inside_cell)
+    exact = Fraction(numerator, denominator)
+    double_rounded = np.float32(numerator / denominator)
+    direct = np.float32(float(min([Fraction(2 ** 23 + parity, 2 ** 23), Fraction(2 ** 23 + parity + 1, 2 ** 23)],
+                                  key=lambda e: abs(exact - e))))
+    assert (double_rounded != direct) == inside_cell
+    g = _float32_parts(numerator)
+    h = _float32_parts(denominator)
+    rows = max(len(g), len(h))
+    grad = np.asarray(g + [0] * (rows - len(g)), np.float32) * -sign
+    hess = np.asarray(h + [0] * (rows - len(h)), np.float32)
+    X = np.zeros((rows + int(split), 1), np.float32)
+    if split:
+        X[-1, 0] = 1
+        grad = np.append(grad, np.float32(0))
+        hess = np.append(hess, np.float32(2 ** 52))
+    p = O.make_params(max_depth=1, max_bin=4, eta=1.0, reg_lambda=0.0, min_child_weight=0.0, base_score=0.0)
+    r = O.train(X, np.zeros(len(X), np.float32), p, 1, custom_grad=grad[None, :], custom_hess=hess[None, :])
+    tree = r["trees"][0][:r["sizes"][0]]
+    assert len(tree) == (3 if split else 1)
+    got = np.float32(tree["base_weight"][1 if split else 0])
+    assert got.view(np.uint32) == np.float32(sign * double_rounded).view(np.uint32)
+
+
+def test_constructed_tree_known_answer():
+    """Leaf base weights [1, 3, -1, -3] (tests/test_histogram_present.py:66-81 of the reference)."""
+    X = np.repeat(np.asarray([[0, 0, np.nan], [0, 1, np.nan], [1, 0, np.nan], [1, 1, np.nan]], np.float32), 3, axis=0)
+    grad = np.asarray([[2.0 ** 40, -(2.0 ** 40), f] for f in [-1, -3, 1, 3]], np.float32).ravel()
+    hess = np.tile(np.asarray([-1, 1, 1], np.float32), 4)
+    p = O.make_params(max_depth=3, max_bin=4, eta=1.0, reg_lambda=0.0, min_child_weight=0.0, base_score=0.5)
+    r = O.train(X, np.zeros(len(X), np.float32), p, 1, custom_grad=grad[None, :], custom_hess=hess[None, :])
+    tree = r["trees"][0][:r["sizes"][0]]
+    assert len(tree) == 7
+    np.testing.assert_array_equal(tree["base_weight"][3:], np.asarray([1, 3, -1, -3], np.float32))
+
+
+def test_gain_forms_closed_form():
+    """w = RN32(RN64(-G/(H+lambda))); gain = RN32(-(2 G w + (H+lambda) RN32(w^2))) with
+    the products fused (fma_contract=1) or separately rounded (fma_contract=0)."""
+    rng = np.random.default_rng(9)
+    for fma in (0, 1):
+        p = O.make_params(reg_lambda=1.0, fma_contract=fma)
+        for _ in range(200):
+            G = float(rng.normal() * 1e3)
+            H = float(rng.uniform(0.5, 1e3))
+            w = O.lib().oracle_weight(G, H, p)
+            assert np.float32(w) == np.float32(-G / (H + 1.0))
+            gain = O.lib().oracle_gain(G, H, w, p)
+            sq = float(np.float32(w) * np.float32(w))
+            exact = Fraction(2) * Fraction(G) * Fraction(float(np.float32(w))) + Fraction(H + 1.0) * Fraction(sq)
+            if fma:
+                quad = (H + 1.0) * sq
+                want = np.float32(-float(Fraction(2 * G) * Fraction(float(np.float32(w))) + Fraction(quad)))
+            else:
+                want = np.float32(-((2 * G) * float(np.float32(w)) + (H + 1.0) * sq))
+            assert np.float32(gain) == want
+            assert abs(float(np.float32(gain)) + float(exact)) <= 1e-6 * abs(float(exact)) + 1e-30

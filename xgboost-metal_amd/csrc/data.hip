@@ -1,0 +1,336 @@
+// Data-side kernels: bin matrix, gradients, fixed-point scales, base score,
+// margin fill and tree prediction.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "device_common.hpp"
+
+namespace mgb {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Bin matrix (kernels/boost.metal:476-499): bin = min(#{cuts <= v}, count-1),
+// NaN -> missing code.  One thread per (row, padded feature); the row-major
+// output keeps each row's codes contiguous so a histogram workgroup reads a
+// feature group of a row with one vector load.
+// ---------------------------------------------------------------------------
+template <typename BinT>
+__global__ void k_quantize(const float* __restrict__ X, const float* __restrict__ cuts,
+                           const uint32_t* __restrict__ counts, MgbMatrix m, BinT* __restrict__ bins,
+                           uint32_t* __restrict__ any_missing) {
+  const uint32_t padded = m.row_stride / sizeof(BinT);
+  const uint64_t total = (uint64_t)m.rows * padded;
+  bool missing = false;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    uint32_t r = (uint32_t)(i / padded), f = (uint32_t)(i % padded);
+    BinT code = (BinT)m.missing_code;
+    if (f < m.cols) {
+      float v = X[(uint64_t)r * m.cols + f];
+      uint32_t count = counts[f];
+      if (!isnan(v) && count) {
+        const float* column = cuts + (uint64_t)f * m.cut_stride;
+        uint32_t lo = 0, hi = count;
+        while (lo < hi) {
+          uint32_t mid = lo + (hi - lo) / 2;
+          if (v >= column[mid]) lo = mid + 1;
+          else hi = mid;
+        }
+        code = (BinT)(lo < count - 1 ? lo : count - 1);
+      } else {
+        missing = true;
+      }
+    }
+    bins[i] = code;
+  }
+  if (__any(missing) && lane_id() == 0) atomicOr(any_missing, 1u);
+}
+
+// ---------------------------------------------------------------------------
+// Gradients (kernels/boost.metal:553-601) and exact magnitude mass
+// (kernels/gradient_quantization.metal.h:4-24).  The exact sum of |g| in
+// units of 2^-149 is kept as 256 per-exponent u64 sums of 24-bit mantissas:
+// |g| = m * 2^j units with j = max(E,1)-1, so sum = sum_j S_j * 2^j exactly.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void mass_bucket(float v, uint32_t& bucket, uint64_t& mantissa) {
+  uint32_t bits = __float_as_uint(v) & 0x7fffffffu;
+  uint32_t e = bits >> 23;
+  uint32_t m = bits & 0x7fffffu;
+  if (e) { m |= 0x800000u; bucket = e - 1; }
+  else bucket = 0;
+  mantissa = m;
+}
+
+__global__ __launch_bounds__(256) void k_gradients(MgbGradParams p, const float* __restrict__ margin,
+                                                   const float* __restrict__ labels,
+                                                   const float* __restrict__ weights, float2* __restrict__ grad,
+                                                   uint64_t* __restrict__ mass) {
+  __shared__ uint64_t local[2 * 256];
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
+  __syncthreads();
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < p.rows; r += gridDim.x * blockDim.x) {
+    float pred = margin[r], label = labels[r];
+    float weight = p.has_weight ? weights[r] : 1.0f;
+    float g = pred - label, h = 1.0f;
+    if (p.objective == 1 || p.objective == 2) {
+      float prob = 1.0f / (1.0f + expf(-pred));
+      weight *= label == 1.0f ? p.scale_pos_weight : 1.0f;
+      g = prob - label;
+      h = fmaxf(prob * (1.0f - prob), 1.0e-16f);
+    }
+    g = g * weight;
+    h = h * weight;
+    grad[r] = make_float2(g, h);
+    uint32_t bg, bh;
+    uint64_t mg, mh;
+    mass_bucket(g, bg, mg);
+    mass_bucket(h, bh, mh);
+    if (mg) atomicAdd((unsigned long long*)&local[bg], (unsigned long long)mg);
+    if (mh) atomicAdd((unsigned long long*)&local[256 + bh], (unsigned long long)mh);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x)
+    if (local[i]) atomicAdd((unsigned long long*)&mass[i], (unsigned long long)local[i]);
+}
+
+__global__ __launch_bounds__(256) void k_gradient_mass(const float2* __restrict__ grad, uint32_t rows,
+                                                       uint64_t* __restrict__ mass) {
+  __shared__ uint64_t local[2 * 256];
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
+  __syncthreads();
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+    float2 v = grad[r];
+    uint32_t bg, bh;
+    uint64_t mg, mh;
+    mass_bucket(v.x, bg, mg);
+    mass_bucket(v.y, bh, mh);
+    if (mg) atomicAdd((unsigned long long*)&local[bg], (unsigned long long)mg);
+    if (mh) atomicAdd((unsigned long long*)&local[256 + bh], (unsigned long long)mh);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x)
+    if (local[i]) atomicAdd((unsigned long long*)&mass[i], (unsigned long long)local[i]);
+}
+
+// scale = 2^(62 - max(0, bitlen(sum) - 149)); gradient_quantization.metal.h:52-63.
+__global__ void k_gradient_scales(uint64_t* __restrict__ mass, float* __restrict__ scales) {
+  if (threadIdx.x < 2) {
+    const uint64_t* s = mass + threadIdx.x * 256;
+    uint32_t limb[11] = {0};
+    for (uint32_t j = 0; j < 256; ++j) {
+      uint64_t v = s[j];
+      if (!v) continue;
+      uint32_t word = j / 32, shift = j % 32;
+      // v < 2^56, so v << shift spans at most three 32-bit limbs.
+      uint64_t lo = v << shift;
+      uint64_t hi = shift ? (v >> (64 - shift)) : 0;
+      uint32_t parts[3] = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi};
+      uint64_t carry = 0;
+      for (uint32_t w = word; w < 11; ++w) {
+        uint64_t add = (w - word < 3 ? parts[w - word] : 0u) + carry;
+        uint64_t sum = (uint64_t)limb[w] + add;
+        limb[w] = (uint32_t)sum;
+        carry = sum >> 32;
+        if (w - word >= 2 && !carry) break;
+      }
+    }
+    int exponent = 0;
+    for (int w = 10; w >= 0; --w) {
+      if (limb[w]) {
+        int bitlen = w * 32 + 32 - __clz(limb[w]);
+        exponent = bitlen - 149 > 0 ? bitlen - 149 : 0;
+        break;
+      }
+    }
+    scales[threadIdx.x] = __uint_as_float((uint32_t)(62 - exponent + 127) << 23);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) mass[i] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Base score (src/learner.cpp:316-333, kernels/boost.metal:356-423): weighted
+// label mean.  Each thread keeps a compensated binary64 sum (products of two
+// binary32 values are exact), then a fixed-order tree reduction combines them.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void two_sum_add(double& s, double& c, double x) {
+  double t = s + x;
+  c += fabs(s) >= fabs(x) ? (s - t) + x : (x - t) + s;
+  s = t;
+}
+
+__global__ __launch_bounds__(1024) void k_base_score(const float* __restrict__ labels,
+                                                     const float* __restrict__ weights, uint32_t rows,
+                                                     uint32_t objective, float spw, float* __restrict__ out) {
+  __shared__ double sh[4][1024];
+  double s = 0, c = 0, ws = 0, wc = 0;
+  for (uint32_t r = threadIdx.x; r < rows; r += blockDim.x) {
+    float w = weights ? weights[r] : 1.0f;
+    float y = labels[r];
+    if (objective == 1 || objective == 2) w *= y == 1.0f ? spw : 1.0f;
+    two_sum_add(s, c, (double)y * (double)w);
+    two_sum_add(ws, wc, (double)w);
+  }
+  sh[0][threadIdx.x] = s; sh[1][threadIdx.x] = c; sh[2][threadIdx.x] = ws; sh[3][threadIdx.x] = wc;
+  __syncthreads();
+  for (uint32_t d = blockDim.x / 2; d > 0; d >>= 1) {
+    if (threadIdx.x < d) {
+      double a = sh[0][threadIdx.x], ac = sh[1][threadIdx.x];
+      two_sum_add(a, ac, sh[0][threadIdx.x + d]);
+      ac += sh[1][threadIdx.x + d];
+      double b = sh[2][threadIdx.x], bc = sh[3][threadIdx.x];
+      two_sum_add(b, bc, sh[2][threadIdx.x + d]);
+      bc += sh[3][threadIdx.x + d];
+      sh[0][threadIdx.x] = a; sh[1][threadIdx.x] = ac; sh[2][threadIdx.x] = b; sh[3][threadIdx.x] = bc;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    double value = sh[0][0] + sh[1][0], weight = sh[2][0] + sh[3][0];
+    float result;
+    if (!(weight > 0)) result = objective == 0 && rows == 0 ? 0.0f : 0.5f;
+    else result = (float)(value / weight);
+    out[0] = result;
+  }
+}
+
+__global__ void k_any_missing(const float* __restrict__ data, uint64_t count, uint32_t* __restrict__ flag) {
+  bool missing = false;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+    missing |= isnan(data[i]);
+  if (__any(missing) && lane_id() == 0) atomicOr(flag, 1u);
+}
+
+// Prediction transform of binary:logistic (sigmoid of the margin).
+__global__ void k_transform(float* __restrict__ data, uint64_t count, uint32_t objective) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
+    if (objective == 1) data[i] = 1.0f / (1.0f + expf(-data[i]));
+  }
+}
+
+__global__ void k_fill(float* __restrict__ data, uint64_t count, float value) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+    data[i] = value;
+}
+
+// Prediction (kernels/boost.metal:1325-1329 split_left, :1738-1763 predict):
+// float traversal on the raw values; NaN follows default_left.
+__global__ void k_predict(const float* __restrict__ X, uint32_t rows, uint32_t cols,
+                          const MgbTreeNode* __restrict__ nodes, const uint32_t* __restrict__ offsets,
+                          uint32_t trees, float* __restrict__ margin) {
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+    const float* row = X + (uint64_t)r * cols;
+    float sum = margin[r];
+    for (uint32_t t = 0; t < trees; ++t) {
+      const MgbTreeNode* tree = nodes + offsets[t];
+      int32_t id = 0;
+      while (tree[id].left >= 0) {
+        float v = row[tree[id].feature];
+        bool left = isnan(v) ? tree[id].default_left != 0 : v < tree[id].threshold;
+        id = left ? tree[id].left : tree[id].right;
+      }
+      sum = sum + tree[id].leaf;
+    }
+    margin[r] = sum;
+  }
+}
+
+uint32_t grid_for(uint64_t work, uint32_t block, uint32_t cap = 8192) {
+  uint64_t g = (work + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (uint32_t)g;
+}
+
+}  // namespace
+}  // namespace mgb
+
+using namespace mgb;
+
+extern "C" {
+
+int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,
+                      uint32_t* any_missing) {
+  if (!m || !bins || !any_missing) { set_error("mgb_quantize_bins: null argument"); return -1; }
+  if (m->bin_bytes != 1 && m->bin_bytes != 2) { set_error("mgb_quantize_bins: bin_bytes must be 1 or 2"); return -1; }
+  if (m->row_stride % m->bin_bytes || m->row_stride / m->bin_bytes < m->cols) {
+    set_error("mgb_quantize_bins: row_stride too small");
+    return -1;
+  }
+  uint64_t total = (uint64_t)m->rows * (m->row_stride / m->bin_bytes);
+  if (!total) return 0;
+  uint32_t grid = grid_for(total, 256, 65535);
+  if (m->bin_bytes == 1)
+    hipLaunchKernelGGL(k_quantize<uint8_t>, dim3(grid), dim3(256), 0, stream(), X, cuts, counts, *m,
+                       (uint8_t*)bins, any_missing);
+  else
+    hipLaunchKernelGGL(k_quantize<uint16_t>, dim3(grid), dim3(256), 0, stream(), X, cuts, counts, *m,
+                       (uint16_t*)bins, any_missing);
+  MGB_LAUNCH_CHECK("k_quantize");
+  return 0;
+}
+
+int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
+                  float* grad, uint64_t* mass) {
+  if (!p->rows) return 0;
+  uint32_t grid = grid_for(p->rows, 256, 2048);
+  hipLaunchKernelGGL(k_gradients, dim3(grid), dim3(256), 0, stream(), *p, margin, labels, weights, (float2*)grad,
+                     mass);
+  MGB_LAUNCH_CHECK("k_gradients");
+  return 0;
+}
+
+int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass) {
+  if (!rows) return 0;
+  uint32_t grid = grid_for(rows, 256, 2048);
+  hipLaunchKernelGGL(k_gradient_mass, dim3(grid), dim3(256), 0, stream(), (const float2*)grad, rows, mass);
+  MGB_LAUNCH_CHECK("k_gradient_mass");
+  return 0;
+}
+
+int mgb_gradient_scales(uint64_t* mass, float* scales) {
+  hipLaunchKernelGGL(k_gradient_scales, dim3(1), dim3(256), 0, stream(), mass, scales);
+  MGB_LAUNCH_CHECK("k_gradient_scales");
+  return 0;
+}
+
+int mgb_base_score(const float* labels, const float* weights, uint32_t rows, uint32_t objective,
+                   float scale_pos_weight, float* out) {
+  hipLaunchKernelGGL(k_base_score, dim3(1), dim3(1024), 0, stream(), labels, weights, rows, objective,
+                     scale_pos_weight, out);
+  MGB_LAUNCH_CHECK("k_base_score");
+  return 0;
+}
+
+int mgb_fill_f32(float* data, uint64_t count, float value) {
+  if (!count) return 0;
+  hipLaunchKernelGGL(k_fill, dim3(grid_for(count, 256)), dim3(256), 0, stream(), data, count, value);
+  MGB_LAUNCH_CHECK("k_fill");
+  return 0;
+}
+
+int mgb_any_missing(const float* data, uint64_t count, uint32_t* flag) {
+  if (!count) return 0;
+  hipLaunchKernelGGL(k_any_missing, dim3(grid_for(count, 256, 4096)), dim3(256), 0, stream(), data, count, flag);
+  MGB_LAUNCH_CHECK("k_any_missing");
+  return 0;
+}
+
+int mgb_transform(float* data, uint64_t count, uint32_t objective) {
+  if (!count || objective != 1) return 0;
+  hipLaunchKernelGGL(k_transform, dim3(grid_for(count, 256)), dim3(256), 0, stream(), data, count, objective);
+  MGB_LAUNCH_CHECK("k_transform");
+  return 0;
+}
+
+int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode* nodes, const uint32_t* offsets,
+                uint32_t trees, float* margin) {
+  if (!rows || !trees) return 0;
+  hipLaunchKernelGGL(k_predict, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), X, rows, cols, nodes, offsets,
+                     trees, margin);
+  MGB_LAUNCH_CHECK("k_predict");
+  return 0;
+}
+
+}  // extern "C"

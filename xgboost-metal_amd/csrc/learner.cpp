@@ -1,0 +1,703 @@
+#include "learner.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <sstream>
+
+namespace mgb {
+
+void require(bool ok, const std::string& message) {
+  if (!ok) throw Error(message);
+}
+
+void kcheck(int status, const char* what) {
+  if (status != 0) throw Error(std::string(what) + ": " + mgb_last_error());
+}
+
+// ---------------------------------------------------------------------------
+// DeviceBuffer
+// ---------------------------------------------------------------------------
+void DeviceBuffer::resize(size_t bytes) {
+  release();
+  kcheck(mgb_malloc(&ptr_, bytes ? bytes : 16), "device allocation");
+  bytes_ = bytes;
+}
+void DeviceBuffer::upload(const void* host, size_t bytes) {
+  ensure(bytes);
+  kcheck(mgb_memcpy_h2d(ptr_, host, bytes), "host-to-device copy");
+}
+void DeviceBuffer::download(void* host, size_t bytes) const {
+  kcheck(mgb_memcpy_d2h(host, ptr_, bytes), "device-to-host copy");
+}
+void DeviceBuffer::release() {
+  if (ptr_) mgb_free(ptr_);
+  ptr_ = nullptr;
+  bytes_ = 0;
+}
+
+// ---------------------------------------------------------------------------
+// DMatrix (src/data.cpp:414-491 dense ingest, :1210-1306 quantize)
+// ---------------------------------------------------------------------------
+static uint64_t next_matrix_id() {
+  static std::mutex m;
+  static uint64_t id = 0;
+  std::lock_guard<std::mutex> lock(m);
+  return ++id;
+}
+
+DMatrix::DMatrix() : id(next_matrix_id()) {}
+
+void DMatrix::upload() {
+  if (data_uploaded) return;
+  d_data.upload(data.data(), data.size() * sizeof(float));
+  data_uploaded = true;
+}
+
+void DMatrix::upload_info() {
+  if (!labels_uploaded && !labels.empty()) {
+    d_labels.upload(labels.data(), labels.size() * sizeof(float));
+    labels_uploaded = true;
+  }
+  if (!weights_uploaded && !weights.empty()) {
+    d_weights.upload(weights.data(), weights.size() * sizeof(float));
+    weights_uploaded = true;
+  }
+}
+
+void DMatrix::set_info(const std::string& field, const float* values, size_t count) {
+  std::vector<float> v(values, values + count);
+  if (field == "label") { labels = std::move(v); labels_uploaded = false; }
+  else if (field == "weight") {
+    weights = std::move(v);
+    weights_uploaded = false;
+    quantized_max_bin = 0;  // the sketch is weighted
+  } else if (field == "base_margin") base_margin = std::move(v);
+  else if (field == "label_lower_bound" || field == "label_upper_bound" || field == "feature_weights" ||
+           field == "group_ptr" || field == "qid")
+    throw Error("Field '" + field + "' is not supported by this engine (single-output hist regression and "
+                "binary classification).");
+  else throw Error("Unknown float field: " + field);
+}
+
+const std::vector<float>& DMatrix::get_info(const std::string& field) const {
+  if (field == "label") return labels;
+  if (field == "weight") return weights;
+  if (field == "base_margin") return base_margin;
+  throw Error("Unknown float field: " + field);
+}
+
+static uint32_t next_pow2(uint32_t v) {
+  uint32_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+void DMatrix::quantize(uint32_t max_bin) {
+  require(max_bin >= 2, "max_bin must be at least 2.");
+  if (quantized_max_bin == max_bin) return;
+  require(!is_quantile || quantile_max_bin == max_bin, "Inconsistent max_bin between QuantileDMatrix and Booster.");
+  require(rows > 0 && cols > 0, "Data must contain at least one row and one feature.");
+  upload();
+  upload_info();
+  auto t0 = std::chrono::steady_clock::now();
+  hist_bins = std::max(1u, std::min(max_bin, rows));
+  d_cuts.ensure((size_t)cols * max_bin * sizeof(float));
+  d_counts.ensure((size_t)cols * sizeof(uint32_t));
+  const float* w = weights.empty() ? nullptr : d_weights.as<float>();
+  kcheck(mgb_sketch_cuts(d_data.as<float>(), rows, cols, w, max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
+         "quantile sketch");
+  counts_host.resize(cols);
+  cuts_host.resize((size_t)cols * max_bin);
+  d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
+  d_cuts.download(cuts_host.data(), cuts_host.size() * sizeof(float));
+  auto t1 = std::chrono::steady_clock::now();
+  uint32_t max_count = 0;
+  for (auto c : counts_host) max_count = std::max(max_count, c);
+  require(max_count <= hist_bins, "internal error: more cuts than histogram bins");
+  d_missing.ensure(sizeof(uint32_t));
+  kcheck(mgb_memset(d_missing.get(), 0, sizeof(uint32_t)), "memset");
+  kcheck(mgb_any_missing(d_data.as<float>(), (uint64_t)rows * cols, d_missing.as<uint32_t>()), "missing scan");
+  uint32_t missing = 0;
+  d_missing.download(&missing, sizeof(missing));
+  has_missing = missing != 0;
+  // u8 codes when bins 0..max_count-1 leave 0xFF free for missing values.
+  uint32_t bin_bytes = (max_count <= 255 || (max_count <= 256 && !has_missing)) && hist_bins <= 256 ? 1 : 2;
+  uint32_t G = 16;
+  while (G > 1 && (size_t)G * (hist_bins + 1) * 16 > 66000) G >>= 1;
+  G = std::min(G, next_pow2(cols));
+  features_per_group = G;
+  uint32_t groups = (cols + G - 1) / G;
+  matrix.rows = rows;
+  matrix.cols = cols;
+  matrix.bin_bytes = bin_bytes;
+  matrix.row_stride = groups * G * bin_bytes;
+  matrix.max_bin = hist_bins;
+  matrix.cut_stride = max_bin;
+  matrix.missing_code = bin_bytes == 1 ? 0xFFu : 0xFFFFu;
+  d_bins.ensure((size_t)rows * matrix.row_stride);
+  kcheck(mgb_quantize_bins(d_data.as<float>(), d_cuts.as<float>(), d_counts.as<uint32_t>(), &matrix, d_bins.get(),
+                           d_missing.as<uint32_t>()),
+         "bin matrix");
+  kcheck(mgb_synchronize(), "synchronize");
+  auto t2 = std::chrono::steady_clock::now();
+  sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
+  quantize_seconds += std::chrono::duration<double>(t2 - t1).count();
+  quantized_max_bin = max_bin;
+}
+
+// ---------------------------------------------------------------------------
+// Learner
+// ---------------------------------------------------------------------------
+Learner::Learner() = default;
+Learner::~Learner() = default;
+
+static const std::map<std::string, std::string>& aliases() {
+  static const std::map<std::string, std::string> a = {
+      {"eta", "learning_rate"}, {"lambda", "reg_lambda"}, {"alpha", "reg_alpha"}, {"gamma", "min_split_loss"},
+      {"random_state", "seed"}, {"n_jobs", "nthread"}};
+  return a;
+}
+
+void Learner::set_param(const std::string& name, const std::string& value) {
+  std::string key = name;
+  auto it = aliases().find(name);
+  if (it != aliases().end()) key = it->second;
+  params_[key] = value;
+}
+
+std::string Learner::param(const std::string& name, const std::string& fallback) const {
+  auto it = params_.find(name);
+  return it == params_.end() ? fallback : it->second;
+}
+
+double Learner::number(const std::string& name, double fallback) const {
+  auto it = params_.find(name);
+  if (it == params_.end()) return fallback;
+  try {
+    return std::stod(it->second);
+  } catch (...) {
+    throw Error("Invalid numeric value for " + name + ": " + it->second);
+  }
+}
+
+// Float parameters parse straight to binary32, as XGBoost's parameter parser does.
+float Learner::fnumber(const std::string& name, float fallback) const {
+  auto it = params_.find(name);
+  if (it == params_.end()) return fallback;
+  try {
+    return std::stof(it->second);
+  } catch (...) {
+    throw Error("Invalid numeric value for " + name + ": " + it->second);
+  }
+}
+
+int64_t Learner::integer(const std::string& name, int64_t fallback) const {
+  auto it = params_.find(name);
+  if (it == params_.end()) return fallback;
+  try {
+    return (int64_t)std::stod(it->second);
+  } catch (...) {
+    throw Error("Invalid integer value for " + name + ": " + it->second);
+  }
+}
+
+std::string Learner::objective_name() const { return param("objective", "reg:squarederror"); }
+
+// Objective codes as in the reference (src/learner.cpp objective map).
+int Learner::objective() const {
+  auto name = objective_name();
+  if (name == "reg:squarederror") return 0;
+  if (name == "binary:logistic" || name == "reg:logistic") return 1;
+  if (name == "binary:logitraw") return 2;
+  throw Error("Objective is not implemented by the HIP hist engine: " + name);
+}
+
+void Learner::configure_check() const {
+  (void)objective();
+  auto method = param("tree_method", "hist");
+  require(method == "hist" || method == "auto" || method == "approx",
+          "This engine implements tree_method='hist' only, got '" + method + "'.");
+  require(param("booster", "gbtree") == "gbtree", "Only booster='gbtree' is supported.");
+  require(param("grow_policy", "depthwise") == "depthwise", "Only grow_policy='depthwise' is supported.");
+  require(param("multi_strategy", "one_output_per_tree") == "one_output_per_tree",
+          "Only multi_strategy='one_output_per_tree' is supported.");
+  require(integer("num_parallel_tree", 1) == 1, "num_parallel_tree must be 1.");
+  require(integer("max_leaves", 0) == 0, "max_leaves is not supported (depthwise growth only).");
+  auto depth = integer("max_depth", 6);
+  require(depth >= 1 && depth <= 16, "max_depth must be in [1, 16].");
+  for (auto key : {"subsample", "colsample_bytree", "colsample_bylevel", "colsample_bynode"})
+    require(number(key, 1) == 1.0, std::string(key) + " < 1 is not supported yet.");
+  auto mono = param("monotone_constraints", "()");
+  for (char c : mono) require(c == '(' || c == ')' || c == '[' || c == ']' || c == ',' || c == '0' || c == ' ',
+                              "monotone_constraints are not supported yet.");
+  require(param("interaction_constraints", "").empty() || param("interaction_constraints", "") == "[]",
+          "interaction_constraints are not supported yet.");
+  for (auto key : {"reg_lambda", "reg_alpha", "min_child_weight", "min_split_loss", "max_delta_step", "learning_rate",
+                   "scale_pos_weight"})
+    require(number(key, 0) >= 0, std::string("Parameter must be nonnegative: ") + key);
+  auto bins = integer("max_bin", 256);
+  require(bins >= 2 && bins <= 1086, "max_bin must be in [2, 1086].");
+}
+
+float Learner::base_margin_value() const {
+  int obj = objective();
+  float value = base_score;
+  if (obj == 1) {
+    // src/objectives.cpp:17-31 (score_margins).
+    value = std::min(std::max(value, 1.0e-6f), 1.0f - 1.0e-6f);
+    value = -std::log(1.0f / value - 1.0f);
+  }
+  return value;
+}
+
+void Learner::initialize(DMatrix& data, bool custom) {
+  if (initialized) {
+    require(num_feature == data.cols, "Number of columns does not match the trained model.");
+    return;
+  }
+  num_feature = data.cols;
+  feature_names = data.feature_names;
+  feature_types = data.feature_types;
+  int obj = objective();
+  auto given = params_.find("base_score");
+  if (given != params_.end()) {
+    base_score = std::stof(given->second);
+  } else if (custom) {
+    base_score = 0.5f;
+  } else {
+    // src/learner.cpp:316-333: weighted label mean on the device.
+    d_base_.ensure(sizeof(float));
+    const float* w = data.weights.empty() ? nullptr : data.d_weights.as<float>();
+    kcheck(mgb_base_score(data.d_labels.as<float>(), w, data.rows, (uint32_t)obj, fnumber("scale_pos_weight", 1.0f),
+                          d_base_.as<float>()),
+           "base score");
+    d_base_.download(&base_score, sizeof(float));
+    if (obj == 2) {
+      float v = std::min(std::max(base_score, 1.0e-6f), 1.0f - 1.0e-6f);
+      base_score = std::log(v / (1 - v));
+    }
+  }
+  if (obj == 1) require(base_score >= 0 && base_score <= 1, "base_score must be in [0,1] for logistic loss.");
+  initialized = true;
+}
+
+void Learner::upload_model() {
+  if (uploaded_trees_ == trees.size() && model_version_ == trees.size()) return;
+  std::vector<MgbTreeNode> nodes;
+  std::vector<uint32_t> offsets;
+  for (auto const& t : trees) {
+    offsets.push_back((uint32_t)nodes.size());
+    nodes.insert(nodes.end(), t.nodes.begin(), t.nodes.end());
+  }
+  if (nodes.empty()) nodes.resize(1);
+  if (offsets.empty()) offsets.resize(1);
+  d_model_nodes_.upload(nodes.data(), nodes.size() * sizeof(MgbTreeNode));
+  d_model_offsets_.upload(offsets.data(), offsets.size() * sizeof(uint32_t));
+  uploaded_trees_ = trees.size();
+  model_version_ = trees.size();
+}
+
+DeviceBuffer* Learner::margin_cache(DMatrix& data) {
+  if (cache_id_ == data.id && cache_trees_ == trees.size() && d_margin_.get()) return &d_margin_;
+  data.upload();
+  d_margin_.ensure((size_t)data.rows * sizeof(float));
+  if (!data.base_margin.empty()) {
+    require(data.base_margin.size() == data.rows, "base_margin must have one value per row.");
+    d_margin_.upload(data.base_margin.data(), data.rows * sizeof(float));
+  } else {
+    kcheck(mgb_fill_f32(d_margin_.as<float>(), data.rows, base_margin_value()), "margin fill");
+  }
+  if (!trees.empty()) {
+    upload_model();
+    kcheck(mgb_predict(data.d_data.as<float>(), data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
+                       d_model_offsets_.as<uint32_t>(), (uint32_t)trees.size(), d_margin_.as<float>()),
+           "prediction");
+  }
+  cache_id_ = data.id;
+  cache_trees_ = trees.size();
+  return &d_margin_;
+}
+
+void Learner::grow(DMatrix& data, bool unit_hessian) {
+  const uint32_t depth = (uint32_t)integer("max_depth", 6);
+  MgbTreeShape shape{};
+  shape.rows = data.rows;
+  shape.cols = data.cols;
+  shape.max_bin = data.hist_bins;
+  shape.max_depth = depth;
+  shape.rows_per_tile = (uint32_t)integer("hip_histogram_rows", data.rows >= 262144 ? 4096 : 2048);
+  shape.features_per_group = data.features_per_group;
+  shape.unit_hessian = unit_hessian ? 1 : 0;
+  shape.dense = data.has_missing ? 0 : 1;
+  size_t ws = mgb_tree_workspace_bytes(&shape);
+  d_tree_ws_.ensure(ws);
+  const uint32_t max_nodes = (2u << depth) - 1u;
+  const size_t node_bytes = (size_t)max_nodes * sizeof(MgbTreeNode);
+  d_nodes_.ensure(node_bytes + 16);
+  MgbSplitParams sp{};
+  sp.reg_lambda = fnumber("reg_lambda", 1.0f);
+  sp.reg_alpha = fnumber("reg_alpha", 0.0f);
+  sp.min_child_weight = fnumber("min_child_weight", 1.0f);
+  sp.max_delta_step = fnumber("max_delta_step", 0.0f);
+  sp.min_split_loss = fnumber("min_split_loss", 0.0f);
+  sp.eta = fnumber("learning_rate", 0.3f);
+  sp.max_depth = depth;
+  sp.fma_contract = (uint32_t)integer("fma_contract", 1);
+  DeviceBuffer* margin = margin_cache(data);
+  auto* nodes = d_nodes_.as<MgbTreeNode>();
+  auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
+  kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
+                       d_grad_.as<float>(), d_scales_.as<float>(), &sp, d_tree_ws_.get(), d_tree_ws_.bytes(),
+                       margin->as<float>(), nodes, count),
+         "tree growth");
+  // One device-to-host copy per round: node records followed by the count.
+  std::vector<uint8_t> host(node_bytes + 16);
+  d_nodes_.download(host.data(), node_bytes + sizeof(uint32_t));
+  uint32_t n = 0;
+  std::memcpy(&n, host.data() + node_bytes, sizeof(uint32_t));
+  require(n >= 1 && n <= max_nodes, "device tree driver produced an invalid node count");
+  Tree tree;
+  tree.nodes.resize(n);
+  std::memcpy(tree.nodes.data(), host.data(), (size_t)n * sizeof(MgbTreeNode));
+  trees.push_back(std::move(tree));
+  cache_trees_ = trees.size();  // the kernels added the new leaves to the cached margin
+}
+
+void Learner::update(DMatrix& data, int /*iteration*/) {
+  configure_check();
+  require(data.labels.size() == data.rows, "Labels must be provided for training (one per row).");
+  require(data.weights.empty() || data.weights.size() == data.rows, "Number of weights must equal the number of rows.");
+  int obj = objective();
+  if (obj == 1 || obj == 2)
+    for (float y : data.labels) require(y >= 0 && y <= 1, "label must be in [0,1] for logistic loss.");
+  data.quantize((uint32_t)integer("max_bin", 256));
+  auto t0 = std::chrono::steady_clock::now();
+  initialize(data, false);
+  DeviceBuffer* margin = margin_cache(data);
+  d_grad_.ensure((size_t)data.rows * 2 * sizeof(float));
+  if (!d_mass_.get()) {
+    d_mass_.ensure(512 * sizeof(uint64_t));
+    kcheck(mgb_memset(d_mass_.get(), 0, 512 * sizeof(uint64_t)), "memset");
+  }
+  d_scales_.ensure(2 * sizeof(float));
+  MgbGradParams gp{};
+  gp.rows = data.rows;
+  gp.objective = (uint32_t)obj;
+  gp.has_weight = data.weights.empty() ? 0 : 1;
+  gp.scale_pos_weight = fnumber("scale_pos_weight", 1.0f);
+  kcheck(mgb_gradients(&gp, margin->as<float>(), data.d_labels.as<float>(),
+                       gp.has_weight ? data.d_weights.as<float>() : nullptr, d_grad_.as<float>(),
+                       d_mass_.as<uint64_t>()),
+         "gradients");
+  kcheck(mgb_gradient_scales(d_mass_.as<uint64_t>(), d_scales_.as<float>()), "gradient scales");
+  grow(data, obj == 0 && data.weights.empty());
+  seconds_["train_rounds"] += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  seconds_["quantiles"] = data.sketch_seconds;
+  seconds_["bin_matrix"] = data.quantize_seconds;
+  ++rounds_timed_;
+}
+
+void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t count) {
+  configure_check();
+  require(count == data.rows, "Gradient and Hessian must have one entry per row.");
+  data.quantize((uint32_t)integer("max_bin", 256));
+  initialize(data, true);
+  std::vector<float> gh(2 * count);
+  for (size_t i = 0; i < count; ++i) { gh[2 * i] = grad[i]; gh[2 * i + 1] = hess[i]; }
+  d_grad_.upload(gh.data(), gh.size() * sizeof(float));
+  if (!d_mass_.get()) {
+    d_mass_.ensure(512 * sizeof(uint64_t));
+    kcheck(mgb_memset(d_mass_.get(), 0, 512 * sizeof(uint64_t)), "memset");
+  }
+  d_scales_.ensure(2 * sizeof(float));
+  kcheck(mgb_gradient_mass(d_grad_.as<float>(), data.rows, d_mass_.as<uint64_t>()), "gradient mass");
+  kcheck(mgb_gradient_scales(d_mass_.as<uint64_t>(), d_scales_.as<float>()), "gradient scales");
+  grow(data, false);
+}
+
+std::vector<float> Learner::predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end) {
+  if (!initialized) {
+    // An untrained model predicts its base score.
+    std::vector<float> out(data.rows, output_margin ? base_margin_value() : base_score);
+    return out;
+  }
+  require(data.cols == num_feature, "Feature shape mismatch: expected " + std::to_string(num_feature) + ", got " +
+                                        std::to_string(data.cols));
+  if (end == 0 || end > trees.size()) end = (uint32_t)trees.size();
+  require(begin <= end, "Invalid iteration range.");
+  std::vector<float> out(data.rows);
+  DeviceBuffer tmp;
+  float* d_out;
+  if (begin == 0 && end == trees.size() && data.base_margin.empty() == true && cache_id_ == data.id &&
+      cache_trees_ == trees.size()) {
+    d_out = d_margin_.as<float>();
+    if (!output_margin && objective() == 1) {
+      tmp.ensure((size_t)data.rows * sizeof(float));
+      kcheck(mgb_memcpy_d2d(tmp.get(), d_out, data.rows * sizeof(float)), "copy");
+      d_out = tmp.as<float>();
+    }
+  } else {
+    data.upload();
+    tmp.ensure((size_t)data.rows * sizeof(float));
+    d_out = tmp.as<float>();
+    if (!data.base_margin.empty()) {
+      require(data.base_margin.size() == data.rows, "base_margin must have one value per row.");
+      tmp.upload(data.base_margin.data(), data.rows * sizeof(float));
+    } else {
+      kcheck(mgb_fill_f32(d_out, data.rows, base_margin_value()), "margin fill");
+    }
+    if (end > begin) {
+      upload_model();
+      kcheck(mgb_predict(data.d_data.as<float>(), data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
+                         d_model_offsets_.as<uint32_t>() + begin, end - begin, d_out),
+             "prediction");
+    }
+  }
+  if (!output_margin) kcheck(mgb_transform(d_out, data.rows, (uint32_t)objective()), "transform");
+  kcheck(mgb_memcpy_d2h(out.data(), d_out, out.size() * sizeof(float)), "device-to-host copy");
+  return out;
+}
+
+std::string Learner::evaluate(int iteration, const std::vector<DMatrix*>& data, const std::vector<std::string>& names) {
+  std::ostringstream os;
+  os << "[" << iteration << "]";
+  int obj = objective();
+  std::string metric = param("eval_metric", obj == 0 ? "rmse" : "logloss");
+  for (size_t k = 0; k < data.size(); ++k) {
+    DMatrix& d = *data[k];
+    auto pred = predict(d, false, 0, 0);
+    const auto& y = d.labels;
+    require(y.size() == d.rows, "Evaluation data must have labels.");
+    double num = 0, den = 0;
+    for (uint32_t r = 0; r < d.rows; ++r) {
+      double w = d.weights.empty() ? 1.0 : d.weights[r];
+      double p = pred[r], t = y[r];
+      if (metric == "rmse" || metric == "mse") num += w * (p - t) * (p - t);
+      else if (metric == "mae") num += w * std::fabs(p - t);
+      else if (metric == "logloss") {
+        double e = 1e-16;
+        double q = std::min(std::max(p, e), 1 - e);
+        num += -w * (t * std::log(q) + (1 - t) * std::log(1 - q));
+      } else if (metric == "error") num += w * ((p > 0.5 ? 1.0 : 0.0) != t);
+      else throw Error("eval_metric is not supported: " + metric);
+      den += w;
+    }
+    double value = den > 0 ? num / den : 0;
+    if (metric == "rmse") value = std::sqrt(value);
+    char buf[64];
+    std::snprintf(buf, sizeof(buf), "%.5f", value);
+    os << "\t" << names[k] << "-" << metric << ":" << buf;
+  }
+  return os.str();
+}
+
+// ---------------------------------------------------------------------------
+// Model (src/model.cpp:28-74: XGBoost JSON schema, version [3, 5, 0])
+// ---------------------------------------------------------------------------
+Json Learner::model() const {
+  Json trees_json = Json::array(), tree_info = Json::array(), indptr = Json::array();
+  for (size_t t = 0; t < trees.size(); ++t) {
+    const auto& tree = trees[t];
+    Json v = Json::object();
+    v["id"] = Json((int64_t)t);
+    Json tp = Json::object();
+    tp["num_deleted"] = "0";
+    tp["num_feature"] = std::to_string(num_feature);
+    tp["num_nodes"] = std::to_string(tree.nodes.size());
+    tp["size_leaf_vector"] = "1";
+    v["tree_param"] = tp;
+    Json bw = Json::array(), cats = Json::array(), dl = Json::array(), lc = Json::array(), rc = Json::array(),
+         loss = Json::array(), parents = Json::array(), cond = Json::array(), idx = Json::array(),
+         stype = Json::array(), hess = Json::array();
+    for (const auto& n : tree.nodes) {
+      bw.push_back(Json(n.base_weight));
+      dl.push_back(Json((int64_t)n.default_left));
+      lc.push_back(Json((int64_t)n.left));
+      rc.push_back(Json((int64_t)n.right));
+      loss.push_back(Json(n.gain));
+      parents.push_back(Json((int64_t)(n.parent < 0 ? 2147483647 : n.parent)));
+      cond.push_back(Json(n.left < 0 ? n.leaf : n.threshold));
+      idx.push_back(Json((int64_t)(n.feature < 0 ? 0 : n.feature)));
+      stype.push_back(Json((int64_t)0));
+      hess.push_back(Json(n.cover));
+    }
+    v["base_weights"] = bw;
+    v["categories"] = Json::array();
+    v["categories_nodes"] = Json::array();
+    v["categories_segments"] = Json::array();
+    v["categories_sizes"] = Json::array();
+    v["default_left"] = dl;
+    v["left_children"] = lc;
+    v["loss_changes"] = loss;
+    v["parents"] = parents;
+    v["right_children"] = rc;
+    v["split_conditions"] = cond;
+    v["split_indices"] = idx;
+    v["split_type"] = stype;
+    v["sum_hessian"] = hess;
+    trees_json.push_back(v);
+    tree_info.push_back(Json((int64_t)tree.group));
+  }
+  for (size_t r = 0; r <= trees.size(); ++r) indptr.push_back(Json((int64_t)r));
+  Json gbm = Json::object();
+  Json gbtree_param = Json::object();
+  gbtree_param["num_parallel_tree"] = "1";
+  gbtree_param["num_trees"] = std::to_string(trees.size());
+  gbm["gbtree_model_param"] = gbtree_param;
+  gbm["iteration_indptr"] = indptr;
+  gbm["tree_info"] = tree_info;
+  gbm["trees"] = trees_json;
+  Json booster = Json::object();
+  booster["model"] = gbm;
+  booster["name"] = "gbtree";
+  Json lmp = Json::object();
+  lmp["base_score"] = "[" + format_float(base_score) + "]";
+  lmp["boost_from_average"] = params_.count("base_score") ? "0" : "1";
+  lmp["num_class"] = "0";
+  lmp["num_feature"] = std::to_string(num_feature);
+  lmp["num_target"] = "1";
+  Json objective_json = Json::object();
+  objective_json["name"] = objective_name();
+  int obj = objective();
+  if (obj == 1 || obj == 2) {
+    Json rp = Json::object();
+    rp["scale_pos_weight"] = param("scale_pos_weight", "1");
+    objective_json["reg_loss_param"] = rp;
+  } else {
+    objective_json["reg_loss_param"] = Json::object();
+    objective_json["reg_loss_param"]["scale_pos_weight"] = "1";
+  }
+  Json attrs = Json::object();
+  for (auto const& kv : attributes) attrs[kv.first] = kv.second;
+  Json fnames = Json::array(), ftypes = Json::array();
+  for (auto const& s : feature_names) fnames.push_back(s);
+  for (auto const& s : feature_types) ftypes.push_back(s);
+  Json learner = Json::object();
+  learner["attributes"] = attrs;
+  learner["feature_names"] = fnames;
+  learner["feature_types"] = ftypes;
+  learner["gradient_booster"] = booster;
+  learner["learner_model_param"] = lmp;
+  learner["objective"] = objective_json;
+  Json root = Json::object();
+  root["learner"] = learner;
+  Json version = Json::array();
+  version.push_back(3); version.push_back(5); version.push_back(0);
+  root["version"] = version;
+  return root;
+}
+
+static float json_float(const Json& v) {
+  if (v.is_string()) return std::stof(v.string());
+  return (float)v.number();
+}
+
+void Learner::load_model(const Json& input) {
+  const Json& learner = input.at("learner");
+  const Json& booster = learner.at("gradient_booster");
+  require(booster.at("name").string() == "gbtree", "Only gbtree models can be loaded.");
+  const Json& mp = learner.at("learner_model_param");
+  auto as_uint = [](const Json& v) -> uint32_t {
+    return v.is_string() ? (uint32_t)std::stoul(v.string()) : (uint32_t)v.integer();
+  };
+  num_feature = as_uint(mp.at("num_feature"));
+  std::string bs = mp.at("base_score").is_string() ? mp.at("base_score").string() : mp.at("base_score").dump();
+  if (!bs.empty() && bs[0] == '[') {
+    Json arr = Json::parse(bs);
+    require(arr.size() == 1, "Only single-output models are supported.");
+    base_score = json_float(arr.items().front());
+  } else {
+    base_score = std::stof(bs);
+  }
+  if (learner.contains("objective")) params_["objective"] = learner.at("objective").at("name").string();
+  const Json& source = booster.at("model").at("trees");
+  std::vector<Tree> loaded;
+  for (const Json& t : source.items()) {
+    Tree tree;
+    const auto& lc = t.at("left_children");
+    size_t n = lc.size();
+    tree.nodes.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+      MgbTreeNode& node = tree.nodes[i];
+      node.left = (int32_t)t.at("left_children")[i].integer();
+      node.right = (int32_t)t.at("right_children")[i].integer();
+      int64_t parent = t.at("parents")[i].integer();
+      node.parent = parent == 2147483647 ? -1 : (int32_t)parent;
+      node.default_left = (uint32_t)t.at("default_left")[i].integer();
+      node.gain = json_float(t.at("loss_changes")[i]);
+      node.cover = json_float(t.at("sum_hessian")[i]);
+      node.base_weight = json_float(t.at("base_weights")[i]);
+      float cond = json_float(t.at("split_conditions")[i]);
+      if (node.left < 0) {
+        node.leaf = cond;
+        node.threshold = 0;
+        node.feature = -1;
+      } else {
+        node.threshold = cond;
+        node.leaf = 0;
+        node.feature = (int32_t)t.at("split_indices")[i].integer();
+      }
+    }
+    loaded.push_back(std::move(tree));
+  }
+  trees = std::move(loaded);
+  feature_names.clear();
+  feature_types.clear();
+  if (learner.contains("feature_names"))
+    for (auto const& s : learner.at("feature_names").items()) feature_names.push_back(s.string());
+  if (learner.contains("feature_types"))
+    for (auto const& s : learner.at("feature_types").items()) feature_types.push_back(s.string());
+  attributes.clear();
+  if (learner.contains("attributes"))
+    for (auto const& kv : learner.at("attributes").members()) attributes.emplace_back(kv.first, kv.second.string());
+  initialized = true;
+  cache_id_ = 0;
+  cache_trees_ = 0;
+  model_version_ = SIZE_MAX;
+}
+
+Json Learner::config() const {
+  Json p = Json::object();
+  for (auto const& kv : params_) p[kv.first] = kv.second;
+  Json learner = Json::object();
+  learner["params"] = p;
+  Json ltp = Json::object();
+  ltp["objective"] = objective_name();
+  ltp["booster"] = "gbtree";
+  learner["learner_train_param"] = ltp;
+  Json root = Json::object();
+  root["learner"] = learner;
+  Json version = Json::array();
+  version.push_back(3); version.push_back(5); version.push_back(0);
+  root["version"] = version;
+  return root;
+}
+
+void Learner::load_config(const Json& cfg) {
+  const Json& learner = cfg.at("learner");
+  if (learner.contains("params"))
+    for (auto const& kv : learner.at("params").members())
+      params_[kv.first] = kv.second.is_string() ? kv.second.string() : kv.second.dump();
+}
+
+void Learner::reset() {
+  d_margin_.release();
+  d_grad_.release();
+  d_tree_ws_.release();
+  d_nodes_.release();
+  cache_id_ = 0;
+  cache_trees_ = 0;
+}
+
+Json Learner::profile() const {
+  Json out = Json::object();
+  Json secs = Json::object();
+  for (auto const& kv : seconds_) secs[kv.first] = Json(kv.second);
+  out["seconds"] = secs;
+  out["rounds"] = Json((uint64_t)rounds_timed_);
+  return out;
+}
+
+}  // namespace mgb

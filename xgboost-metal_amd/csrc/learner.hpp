@@ -1,0 +1,145 @@
+// Host side of the hist engine: data matrices, the boosting loop and the
+// XGBoost JSON model.  All numeric work on the path runs in the HIP kernels
+// behind include/mgb_kernels.h; this layer owns device buffers, parameters,
+// tree records and the model format.
+//
+// Reference counterparts: include/metalgb/engine.hpp:86-427 (Matrix, Tree,
+// Learner), src/learner.cpp:207-985 (initialize, update), src/data.cpp
+// (dense/CSR ingest, quantize), src/model.cpp:28-74 (JSON model).
+#pragma once
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "json.hpp"
+#include "mgb_kernels.h"
+
+namespace mgb {
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+void require(bool ok, const std::string& message);
+
+// Owning device allocation (hipMalloc through the kernel C ABI).
+class DeviceBuffer {
+ public:
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  ~DeviceBuffer() { release(); }
+  void* get() const { return ptr_; }
+  template <class T> T* as() const { return static_cast<T*>(ptr_); }
+  size_t bytes() const { return bytes_; }
+  void resize(size_t bytes);          // contents are not preserved
+  void ensure(size_t bytes) { if (bytes > bytes_ || !ptr_) resize(bytes); }
+  void upload(const void* host, size_t bytes);
+  void download(void* host, size_t bytes) const;
+  void release();
+
+ private:
+  void* ptr_ = nullptr;
+  size_t bytes_ = 0;
+};
+
+void kcheck(int status, const char* what);
+
+struct DMatrix {
+  uint64_t id = 0;                    // unique per matrix; keys the prediction cache
+  uint32_t rows = 0, cols = 0;
+  std::vector<float> data;            // row-major, NaN marks missing
+  std::vector<float> labels, weights, base_margin;
+  std::vector<std::string> feature_names, feature_types;
+  bool is_quantile = false;
+  uint32_t quantile_max_bin = 0;
+
+  // Device state.
+  DeviceBuffer d_data, d_labels, d_weights;
+  bool data_uploaded = false, labels_uploaded = false, weights_uploaded = false;
+  uint32_t quantized_max_bin = 0;     // requested max_bin of the bins below (0: none)
+  uint32_t hist_bins = 0;             // bins per feature in histograms = min(max_bin, rows)
+  uint32_t features_per_group = 16;
+  bool has_missing = false;
+  MgbMatrix matrix{};
+  DeviceBuffer d_cuts, d_counts, d_bins, d_missing;
+  std::vector<float> cuts_host;        // cols * max_bin, host copy for export
+  std::vector<uint32_t> counts_host;
+  double sketch_seconds = 0, quantize_seconds = 0;
+
+  DMatrix();
+  void upload();
+  void upload_info();
+  void quantize(uint32_t max_bin);
+  void set_info(const std::string& field, const float* values, size_t count);
+  const std::vector<float>& get_info(const std::string& field) const;
+};
+
+struct Tree {
+  std::vector<MgbTreeNode> nodes;
+  uint32_t group = 0;
+};
+
+class Learner {
+ public:
+  Learner();
+  ~Learner();
+  std::recursive_mutex mutex;
+
+  void set_param(const std::string& name, const std::string& value);
+  std::string param(const std::string& name, const std::string& fallback) const;
+  double number(const std::string& name, double fallback) const;
+  float fnumber(const std::string& name, float fallback) const;
+  int64_t integer(const std::string& name, int64_t fallback) const;
+
+  // One boosting round with the configured objective (src/learner.cpp:632-985).
+  void update(DMatrix& data, int iteration);
+  // One round with caller gradients (custom objective).
+  void boost(DMatrix& data, const float* grad, const float* hess, size_t count);
+  // Predictions (margin when output_margin) for rounds [begin, end); end 0 = all.
+  std::vector<float> predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end);
+  std::string evaluate(int iteration, const std::vector<DMatrix*>& data, const std::vector<std::string>& names);
+
+  Json model() const;
+  void load_model(const Json& model);
+  Json config() const;
+  void load_config(const Json& config);
+  void reset();
+  Json profile() const;
+
+  uint32_t boosted_rounds() const { return (uint32_t)trees.size(); }
+  uint32_t num_feature = 0;
+  std::vector<Tree> trees;
+  std::vector<std::pair<std::string, std::string>> attributes;
+  std::vector<std::string> feature_names, feature_types;
+  float base_score = 0.5f;
+  bool initialized = false;
+
+ private:
+  int objective() const;
+  std::string objective_name() const;
+  void configure_check() const;
+  void initialize(DMatrix& data, bool custom);
+  void grow(DMatrix& data, bool unit_hessian);
+  float base_margin_value() const;
+  void upload_model();
+  DeviceBuffer* margin_cache(DMatrix& data);
+
+  std::map<std::string, std::string> params_;
+  // Training-matrix prediction cache.
+  uint64_t cache_id_ = 0;
+  size_t cache_trees_ = 0;
+  DeviceBuffer d_margin_;
+  // Round buffers.
+  DeviceBuffer d_grad_, d_mass_, d_scales_, d_tree_ws_, d_nodes_, d_node_count_, d_base_;
+  // Model on the device for prediction.
+  DeviceBuffer d_model_nodes_, d_model_offsets_;
+  size_t model_version_ = SIZE_MAX, model_trees_ = 0;
+  size_t uploaded_trees_ = 0;
+  std::map<std::string, double> seconds_;
+  uint64_t rounds_timed_ = 0;
+};
+
+}  // namespace mgb

@@ -1,0 +1,1018 @@
+// One depthwise tree on gfx950: per level
+//   plan (smaller child of each sibling pair) -> clear multi-tile histograms
+//   -> LDS-private integer histograms (row tiles x feature groups)
+//   -> fused sibling subtraction + wave64 prefix-scan split evaluation
+//   -> select/apply (argmax over features, node records, child ids)
+//   -> stable ballot+prefix row partition with the margin update fused in.
+// All control lives on the device: kernels read work counts written by the
+// previous kernel, so the host enqueues a whole tree without a wait
+// (the reference's GPU-driven tree, src/tree.cpp:455-1029, uses indirect
+// dispatch for the same purpose).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "device_common.hpp"
+
+namespace mgb {
+namespace {
+
+constexpr uint32_t kPartTile = 2048;      // rows per partition task
+constexpr uint32_t kSelectThreads = 1024;
+constexpr uint32_t kHistThreads = 256;
+constexpr uint32_t kSplitThreads = 256;   // four waves, one (node pair, feature) each
+
+enum : uint32_t { kOpNone = 0, kOpLeaf = 1, kOpSplit = 2, kOpFinal = 3 };
+
+struct LevelState {
+  uint32_t n_nodes;       // frontier size of the current level
+  uint32_t n_hist_tasks;
+  uint32_t n_zero;
+  uint32_t n_part_tasks;
+  uint32_t node_count;    // tree nodes allocated so far
+  uint32_t error;
+  uint32_t padding[10];
+};
+
+struct Frontier {
+  int32_t id;             // tree node id
+  uint32_t begin, count;  // segment of this level's row buffer
+  uint32_t parent_slot;   // parent's slot in the previous level's histogram bank
+  int64_t sum_g, sum_h;   // node integer totals (the parent's chosen child sums)
+  uint32_t built;         // histogram built directly (1) or by subtraction (0)
+  uint32_t padding;
+};
+
+struct Cand {
+  float gain;
+  int32_t feature;
+  uint32_t bin, default_left;
+  float threshold, left_w, right_w, left_h, right_h;
+  float parent_w, total_h;
+  uint32_t padding;
+  int64_t lg, lh, rg, rh;
+};
+
+struct NodeOp {
+  uint32_t op, feature;
+  int32_t last_left_bin;
+  uint32_t default_left;
+  float leaf, left_leaf, right_leaf;
+  uint32_t child_slot;
+};
+
+struct HistTask { uint32_t slot, begin, end, single; };
+struct PartTask { uint32_t slot, begin, end, first, ntasks, padding[3]; };
+
+// Device pointers of one tree workspace.
+struct Tree {
+  LevelState* state;
+  uint32_t* rows[2];
+  int64_t* hist[2];
+  Frontier* frontier[2];
+  Cand* cands;
+  NodeOp* ops;
+  HistTask* hist_tasks;
+  uint32_t* zero_list;
+  PartTask* part_tasks;
+  uint32_t* part_counts;
+  // Inputs.
+  const void* bins;
+  const float* cuts;
+  const uint32_t* counts;
+  const float2* grad;
+  const float* scales;
+  float* margin;
+  MgbTreeNode* nodes;
+  uint32_t* node_count_out;
+  // Shape.
+  uint32_t rows_n, cols, max_bin, bins1;     // bins1 = max_bin + 1
+  uint32_t row_stride, bin_bytes, missing_code, cut_stride;
+  uint32_t max_depth, slots, rows_per_tile, groups;
+  uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
+  uint64_t hist_entry;                       // int64 words per node histogram
+  MgbSplitParams sp;
+};
+
+__host__ __device__ inline uint32_t div_up(uint64_t a, uint32_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------
+// Scoring arithmetic (native binary64 restatement of the reference's
+// software-binary64 scorer).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double stat_value(int64_t v, int exponent) { return ldexp((double)v, -exponent); }
+
+__device__ __forceinline__ int scale_exponent(float scale) {
+  return (int)((__float_as_uint(scale) >> 23) & 255) - 127;
+}
+
+// kernels/scalar_gain.metal.h:56-82, split_statistics.metal.h:124-140.
+__device__ __forceinline__ float calc_weight(double G, double H, const MgbSplitParams& p) {
+  if (!(H > 0)) return 0.0f;
+  double alpha = fabs((double)p.reg_alpha);
+  double g = G;
+  if (fabs(g) <= alpha) g = 0;
+  else g = g + (g < 0 ? alpha : -alpha);
+  double den = H + (double)p.reg_lambda;
+  float w = (float)(-g / den);
+  float limit = fabsf(p.max_delta_step);
+  if (limit != 0.0f && fabsf(w) > limit) w = copysignf(limit, w);
+  return w;
+}
+
+// kernels/scalar_gain.metal.h:91-103.
+__device__ __forceinline__ float calc_gain(double G, double H, float w, const MgbSplitParams& p) {
+  if (!(H > 0)) return 0.0f;
+  double wd = (double)w;
+  double square = (double)(w * w);
+  double quadratic = (H + (double)p.reg_lambda) * square;
+  double alpha2 = (double)p.reg_alpha + (double)p.reg_alpha;
+  double sum;
+  if (p.fma_contract) {
+    sum = fma(G + G, wd, quadratic);
+    sum = fma(alpha2, fabs(wd), sum);
+  } else {
+    sum = __dadd_rn(__dmul_rn(G + G, wd), quadratic);
+    sum = __dadd_rn(__dmul_rn(alpha2, fabs(wd)), sum);
+  }
+  return (float)(-sum);
+}
+
+// ---------------------------------------------------------------------------
+// Level 0 set-up: root frontier, root histogram tasks, root tree record.
+// ---------------------------------------------------------------------------
+__global__ void k_level0(Tree t) {
+  LevelState* st = t.state;
+  uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.rows_per_tile) : 0;
+  for (uint32_t i = threadIdx.x; i < tiles; i += blockDim.x) {
+    uint32_t begin = i * t.rows_per_tile;
+    uint32_t end = begin + t.rows_per_tile < t.rows_n ? begin + t.rows_per_tile : t.rows_n;
+    t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
+  }
+  if (threadIdx.x == 0) {
+    st->n_nodes = 1;
+    st->n_hist_tasks = tiles;
+    st->n_zero = tiles == 1 ? 0u : 1u;
+    st->n_part_tasks = 0;
+    st->node_count = 1;
+    st->error = 0;
+    t.zero_list[0] = 0;
+    Frontier root;
+    root.id = 0; root.begin = 0; root.count = t.rows_n; root.parent_slot = 0;
+    root.sum_g = 0; root.sum_h = 0; root.built = 1; root.padding = 0;
+    t.frontier[0][0] = root;
+    MgbTreeNode n;
+    n.left = -1; n.right = -1; n.parent = -1; n.feature = -1;
+    n.threshold = 0; n.leaf = 0; n.cover = 0; n.gain = 0; n.default_left = 0; n.base_weight = 0;
+    t.nodes[0] = n;
+  }
+}
+
+// Level d >= 1: build the smaller child of every sibling pair (ties build the
+// left child, kernels/boost.metal:661-698); the other comes from subtraction.
+__global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth) {
+  __shared__ uint32_t scan[kSelectThreads / kWave + 1];
+  LevelState* st = t.state;
+  Frontier* fr = t.frontier[depth & 1];
+  uint32_t pairs = st->n_nodes / 2;
+  uint32_t carry_tasks = 0, carry_zero = 0;
+  for (uint32_t base = 0; base < pairs; base += blockDim.x) {
+    uint32_t p = base + threadIdx.x;
+    uint32_t tiles = 0, zero = 0, built = 0, count = 0, begin = 0;
+    if (p < pairs) {
+      uint32_t c0 = fr[2 * p].count, c1 = fr[2 * p + 1].count;
+      built = c0 <= c1 ? 2 * p : 2 * p + 1;
+      fr[built].built = 1;
+      fr[built ^ 1u].built = 0;
+      count = fr[built].count;
+      begin = fr[built].begin;
+      tiles = div_up(count, t.rows_per_tile);
+      zero = tiles != 1;
+    }
+    uint32_t total_tasks, total_zero;
+    uint32_t off = block_exclusive_u32(tiles, scan, &total_tasks) + carry_tasks;
+    uint32_t zoff = block_exclusive_u32(zero, scan, &total_zero) + carry_zero;
+    for (uint32_t k = 0; k < tiles; ++k) {
+      uint32_t b = begin + k * t.rows_per_tile;
+      uint32_t e = b + t.rows_per_tile < begin + count ? b + t.rows_per_tile : begin + count;
+      t.hist_tasks[off + k] = HistTask{built, b, e, tiles == 1 ? 1u : 0u};
+    }
+    if (zero) t.zero_list[zoff] = built;
+    carry_tasks += total_tasks;
+    carry_zero += total_zero;
+  }
+  if (threadIdx.x == 0) {
+    st->n_hist_tasks = carry_tasks;
+    st->n_zero = carry_zero;
+  }
+}
+
+// Clear the histograms that several row tiles accumulate into atomically.
+__global__ void k_zero(Tree t, uint32_t depth) {
+  const LevelState* st = t.state;
+  uint32_t n = st->n_zero;
+  uint64_t vecs = t.hist_entry / 2;  // 16-byte vectors per node histogram
+  int4* bank = reinterpret_cast<int4*>(t.hist[depth & 1]);
+  uint64_t total = (uint64_t)n * vecs;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
+    uint32_t slot = t.zero_list[i / vecs];
+    bank[(uint64_t)slot * vecs + i % vecs] = make_int4(0, 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Histogram build (kernels/boost.metal:700-773, histogram_tiled.metal.h).
+// One workgroup owns one (row tile, feature group): an LDS-private
+// [G features][max_bin+1] int64 gradient histogram plus a u32 row count
+// (unit Hessians) or an int64 Hessian histogram, accumulated with LDS
+// integer atomics.  Lanes rotate through the group's features so the 64
+// lanes of a wave hit different features at once.  Gradients are quantized
+// on the fly: q = (int64) rint(g * scale), exactly as a stored int64 pair.
+// The flush is a plain store when the tile is the node's only tile, else a
+// 64-bit global atomic add into a cleared histogram.
+// ---------------------------------------------------------------------------
+template <typename BinT, int G>
+struct Codes {
+  static constexpr int kBytes = G * (int)sizeof(BinT);
+  static constexpr int kWords = (kBytes + 7) / 8;
+  uint64_t w[kWords];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    if constexpr (kBytes >= 16) {
+#pragma unroll
+      for (int i = 0; i < kBytes / 16; ++i) {
+        uint4 v = reinterpret_cast<const uint4*>(p)[i];
+        w[2 * i] = (uint64_t)v.x | ((uint64_t)v.y << 32);
+        w[2 * i + 1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
+      }
+    } else if constexpr (kBytes == 8) {
+      uint2 v = *reinterpret_cast<const uint2*>(p);
+      w[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
+    } else if constexpr (kBytes == 4) {
+      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else if constexpr (kBytes == 2) {
+      w[0] = *reinterpret_cast<const uint16_t*>(p);
+    } else {
+      w[0] = *p;
+    }
+  }
+  __device__ __forceinline__ uint32_t get(uint32_t j) const {
+    constexpr uint32_t bits = 8 * sizeof(BinT);
+    constexpr uint32_t per_word = 64 / bits;
+    uint32_t word = j / per_word, shift = (j % per_word) * bits;
+    uint64_t v = w[0];
+#pragma unroll
+    for (int i = 1; i < kWords; ++i) v = word == (uint32_t)i ? w[i] : v;
+    return (uint32_t)(v >> shift) & ((1u << bits) - 1u);
+  }
+};
+
+template <typename BinT, int G, bool UNIT, bool IDENTITY>
+__global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t depth) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const uint32_t B1 = t.bins1;
+  unsigned long long* lg = reinterpret_cast<unsigned long long*>(smem);
+  unsigned long long* lh = lg + G * B1;                        // !UNIT
+  uint32_t* lc = reinterpret_cast<uint32_t*>(lg + G * B1);     // UNIT
+  const LevelState* st = t.state;
+  const uint32_t ntasks = st->n_hist_tasks;
+  const uint32_t total = ntasks * t.groups;
+  const float sg = t.scales[0], sh = t.scales[1];
+  const int64_t unit_q = UNIT ? (int64_t)rintf(1.0f * sh) : 0;
+  const uint32_t nwg = gridDim.x;
+  const uint32_t vb = (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8;  // XCD-aware: tiles of one task stay on one XCD
+  const uint32_t lane = lane_id();
+  const uint32_t entries = G * B1;
+  const uint32_t* rows = t.rows[depth & 1];
+  int64_t* bank = t.hist[depth & 1];
+  const uint8_t* bins = reinterpret_cast<const uint8_t*>(t.bins);
+  for (uint32_t item = vb; item < total; item += nwg) {
+    const HistTask task = t.hist_tasks[item / t.groups];
+    const uint32_t group = item % t.groups;
+    for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
+      lg[i] = 0;
+      if constexpr (UNIT) lc[i] = 0;
+      else lh[i] = 0;
+    }
+    __syncthreads();
+    const uint32_t fbase = group * G;
+    const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
+    const uint32_t goff = group * G * sizeof(BinT);
+    for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
+      const uint32_t row = IDENTITY ? i : rows[i];
+      const float2 gh = t.grad[row];
+      const unsigned long long qg = (unsigned long long)(long long)rintf(gh.x * sg);
+      const unsigned long long qh = UNIT ? 0ull : (unsigned long long)(long long)rintf(gh.y * sh);
+      Codes<BinT, G> c;
+      c.load(bins + (uint64_t)row * t.row_stride + goff);
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const uint32_t j = (k + lane) & (G - 1);
+        uint32_t code = c.get(j);
+        uint32_t bin = code == t.missing_code ? t.max_bin : code;
+        if (j < fcount) {
+          atomicAdd(&lg[j * B1 + bin], qg);
+          if constexpr (UNIT) atomicAdd(&lc[j * B1 + bin], 1u);
+          else atomicAdd(&lh[j * B1 + bin], qh);
+        }
+      }
+    }
+    __syncthreads();
+    int64_t* out = bank + ((uint64_t)task.slot * t.cols + fbase) * B1 * 2;
+    const uint32_t valid = fcount * B1;
+    if (task.single) {
+      for (uint32_t i = threadIdx.x; i < valid; i += blockDim.x) {
+        int64_t g = (int64_t)lg[i];
+        int64_t h = UNIT ? (int64_t)((uint64_t)lc[i] * (uint64_t)unit_q) : (int64_t)lh[i];
+        reinterpret_cast<int4*>(out)[i] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
+                                                    (int)(uint32_t)h, (int)(uint32_t)((uint64_t)h >> 32));
+      }
+    } else {
+      for (uint32_t i = threadIdx.x; i < valid; i += blockDim.x) {
+        uint64_t g = lg[i];
+        uint64_t h = UNIT ? (uint64_t)lc[i] * (uint64_t)unit_q : (uint64_t)lh[i];
+        if (g) atomicAdd(reinterpret_cast<unsigned long long*>(out + 2 * i), (unsigned long long)g);
+        if (h) atomicAdd(reinterpret_cast<unsigned long long*>(out + 2 * i + 1), (unsigned long long)h);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split evaluation (kernels/boost.metal:902-1005, scalar_parallel.metal.h).
+// One wave per (node pair, feature): subtract the built child from the
+// parent (mod 2^64), store the sibling for the next level, then scan both
+// children.  Lane l holds bins [l*K, l*K+K); a wave64 exclusive scan of the
+// lane sums gives exact int64 prefix sums.  Candidates are ranked by
+// (gain, order) with order = b for the forward pass (missing right) and
+// 2*count-1-b for the backward pass (missing left): the maximum gain with the
+// smallest order is the reference's first strictly greater candidate.
+// ---------------------------------------------------------------------------
+template <int K>
+__device__ void evaluate_node(const int64_t (&hg)[K], const int64_t (&hh)[K], uint32_t count, int64_t total_g,
+                              int64_t total_h, const float* cuts_f, int eg, int eh, const MgbSplitParams& p,
+                              uint32_t feature, Cand* out) {
+  const uint32_t lane = lane_id();
+  // Present sums and lane prefix.
+  uint64_t lsum_g = 0, lsum_h = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    uint32_t b = lane * K + k;
+    if (b < count) { lsum_g += (uint64_t)hg[k]; lsum_h += (uint64_t)hh[k]; }
+  }
+  uint64_t inc_g = wave_inclusive_u64(lsum_g), inc_h = wave_inclusive_u64(lsum_h);
+  uint64_t present_g = __shfl(inc_g, kWave - 1, kWave), present_h = __shfl(inc_h, kWave - 1, kWave);
+  uint64_t pre_g = inc_g - lsum_g, pre_h = inc_h - lsum_h;
+  const uint64_t tg = (uint64_t)total_g, th = (uint64_t)total_h;
+  const bool has_missing = (tg - present_g) != 0 || (th - present_h) != 0;
+  const double G = stat_value(total_g, eg), H = stat_value(total_h, eh);
+  const float w = calc_weight(G, H, p);
+  const float parent_gain = calc_gain(G, H, w, p);
+  float best_gain = -INFINITY;
+  uint32_t best_order = 0xffffffffu;
+  Cand best;
+  best.gain = -INFINITY; best.feature = -1; best.bin = 0; best.default_left = 0; best.threshold = 0;
+  best.left_w = w; best.right_w = w; best.left_h = 0; best.right_h = 0;
+  best.lg = best.lh = best.rg = best.rh = 0;
+  const float mcw = fabsf(p.min_child_weight);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const uint32_t b = lane * K + k;
+    if (b >= count) break;
+    uint64_t excl_g = pre_g, excl_h = pre_h;
+    pre_g += (uint64_t)hg[k];
+    pre_h += (uint64_t)hh[k];
+    // Forward: left = bins [0, b], missing right.
+    // Backward (missing != 0): right = bins [b, count), missing left.
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass == 1 && !has_missing) break;
+      uint64_t lgv, lhv, rgv, rhv;
+      if (pass == 0) {
+        lgv = pre_g; lhv = pre_h; rgv = tg - pre_g; rhv = th - pre_h;
+      } else {
+        rgv = present_g - excl_g; rhv = present_h - excl_h; lgv = tg - rgv; lhv = th - rhv;
+      }
+      double GL = stat_value((int64_t)lgv, eg), HL = stat_value((int64_t)lhv, eh);
+      double GR = stat_value((int64_t)rgv, eg), HR = stat_value((int64_t)rhv, eh);
+      if (!(HL > 0 && HL >= (double)mcw && HR > 0 && HR >= (double)mcw)) continue;
+      float lw = calc_weight(GL, HL, p), rw = calc_weight(GR, HR, p);
+      float gain = (calc_gain(GL, HL, lw, p) + calc_gain(GR, HR, rw, p)) - parent_gain;
+      uint32_t order = pass == 0 ? b : 2 * count - 1 - b;
+      if (gain > -INFINITY && (gain > best_gain || (gain == best_gain && order < best_order))) {
+        best_gain = gain;
+        best_order = order;
+        best.gain = gain; best.feature = (int32_t)feature; best.bin = b; best.default_left = pass;
+        best.threshold = pass == 0 ? cuts_f[b] : (b == 0 ? -INFINITY : cuts_f[b - 1]);
+        best.left_w = lw; best.right_w = rw;
+        best.left_h = (float)HL; best.right_h = (float)HR;
+        best.lg = (int64_t)lgv; best.lh = (int64_t)lhv; best.rg = (int64_t)rgv; best.rh = (int64_t)rhv;
+      }
+    }
+  }
+  // Wave argmax of (gain, order).
+  float g = best_gain;
+  uint32_t o = best_order;
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) {
+    float og = __shfl_xor(g, d, kWave);
+    uint32_t oo = __shfl_xor(o, d, kWave);
+    if (og > g || (og == g && oo < o)) { g = og; o = oo; }
+  }
+  best.parent_w = w;
+  best.total_h = (float)H;
+  if (o == 0xffffffffu) {
+    if (lane == 0) *out = best;  // no valid candidate: feature -1, gain -inf
+  } else if (best_order == o && best_gain == g) {
+    *out = best;
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth) {
+  const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const uint32_t lane = lane_id();
+  const LevelState* st = t.state;
+  const uint32_t n = st->n_nodes;
+  const uint32_t F = t.cols, B1 = t.bins1;
+  const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
+  const Frontier* fr = t.frontier[depth & 1];
+  int64_t* cur = t.hist[depth & 1];
+  if (depth == 0) {
+    if (wave >= F) return;
+    const uint32_t f = wave;
+    const int64_t* h = cur + (uint64_t)f * B1 * 2;
+    int64_t hg[K], hh[K];
+    uint64_t sg = 0, shv = 0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      uint32_t b = lane * K + k;
+      hg[k] = b < B1 ? h[2 * b] : 0;
+      hh[k] = b < B1 ? h[2 * b + 1] : 0;
+      sg += (uint64_t)hg[k];
+      shv += (uint64_t)hh[k];
+    }
+    // Root total: present + missing of this feature (equal for all features).
+    int64_t total_g = (int64_t)wave_sum_u64(sg), total_h = (int64_t)wave_sum_u64(shv);
+    evaluate_node<K>(hg, hh, t.counts[f], total_g, total_h, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f,
+                     t.cands + f);
+    return;
+  }
+  const uint32_t pairs = n / 2;
+  if (wave >= pairs * F) return;
+  const uint32_t pair = wave / F, f = wave % F;
+  const Frontier a = fr[2 * pair], b = fr[2 * pair + 1];
+  const uint32_t built = a.built ? 2 * pair : 2 * pair + 1, other = built ^ 1u;
+  const int64_t* parent = t.hist[(depth - 1) & 1] + ((uint64_t)a.parent_slot * F + f) * B1 * 2;
+  const int64_t* xb = cur + ((uint64_t)built * F + f) * B1 * 2;
+  int64_t* ob = cur + ((uint64_t)other * F + f) * B1 * 2;
+  const bool store_other = depth + 1 < t.max_depth;
+  int64_t xg[K], xh[K], og[K], oh[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    uint32_t bb = lane * K + k;
+    if (bb < B1) {
+      xg[k] = xb[2 * bb]; xh[k] = xb[2 * bb + 1];
+      og[k] = (int64_t)((uint64_t)parent[2 * bb] - (uint64_t)xg[k]);
+      oh[k] = (int64_t)((uint64_t)parent[2 * bb + 1] - (uint64_t)xh[k]);
+      if (store_other) {
+        ob[2 * bb] = og[k];
+        ob[2 * bb + 1] = oh[k];
+      }
+    } else {
+      xg[k] = xh[k] = og[k] = oh[k] = 0;
+    }
+  }
+  const Frontier& fb = built == 2 * pair ? a : b;
+  const Frontier& fo = built == 2 * pair ? b : a;
+  const float* cuts_f = t.cuts + (uint64_t)f * t.cut_stride;
+  const uint32_t count = t.counts[f];
+  evaluate_node<K>(xg, xh, count, fb.sum_g, fb.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f);
+  evaluate_node<K>(og, oh, count, fo.sum_g, fo.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f);
+}
+
+// ---------------------------------------------------------------------------
+// Select and apply (kernels/boost.metal:1245-1313 select_splits,
+// kernels/scalar_root.metal.h:107-186 dense root, src/tree.cpp:1031-1104
+// pop/apply, :1663-1717 replay).  One workgroup handles the whole level in
+// node-id order, so child ids follow XGBoost's numbering.
+// ---------------------------------------------------------------------------
+__device__ void ordered_sum(const int64_t* fh, uint32_t first, uint32_t steps, bool reverse, uint32_t count, int eg,
+                            int eh, double* g, double* h) {
+  double a = 0, b = 0;
+  for (uint32_t s = 0; s < steps; ++s) {
+    uint32_t bin = reverse ? count - s - 1 : first + s;
+    a += stat_value(fh[2 * bin], eg);
+    b += stat_value(fh[2 * bin + 1], eh);
+  }
+  *g = a;
+  *h = b;
+}
+
+__global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t depth) {
+  __shared__ uint32_t scan[kSelectThreads / kWave + 1];
+  LevelState* st = t.state;
+  const uint32_t n = st->n_nodes;
+  const uint32_t F = t.cols;
+  const Frontier* fr = t.frontier[depth & 1];
+  Frontier* next = t.frontier[(depth + 1) & 1];
+  const bool final_level = depth + 1 >= t.max_depth;
+  const uint32_t node_base = st->node_count;
+  const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
+  const MgbSplitParams& p = t.sp;
+  uint32_t carry_expanded = 0, carry_tasks = 0;
+  for (uint32_t base = 0; base < n; base += blockDim.x) {
+    const uint32_t i = base + threadIdx.x;
+    const bool valid = i < n;
+    Cand best;
+    bool expand = false;
+    float applied_w = 0, applied_h = 0, parent_w = 0, total_h = 0;
+    Frontier node;
+    if (valid) {
+      node = fr[i];
+      const Cand* row = t.cands + (uint64_t)i * F;
+      best = row[0];
+      for (uint32_t f = 1; f < F; ++f) {
+        float g = row[f].gain;
+        if (g > best.gain) best = row[f];
+      }
+      parent_w = best.parent_w;
+      total_h = best.total_h;
+      expand = best.feature >= 0 && best.gain > 1.0e-6f && best.gain >= p.min_split_loss &&
+               depth < t.max_depth;
+      if (depth == 0 && t.dense) {
+        // Dense root: ordered binary64 sums of feature 0's bins, and of the
+        // chosen child's bin range (kernels/scalar_root.metal.h:1-105).
+        const int64_t* hist = t.hist[0];
+        const uint32_t c0 = t.counts[0];
+        double tg, th;
+        ordered_sum(hist, 0, c0, false, c0, eg, eh, &tg, &th);
+        parent_w = calc_weight(tg, th, p);
+        total_h = (float)th;
+        if (best.feature >= 0) {
+          const uint32_t f = (uint32_t)best.feature, count = t.counts[f];
+          const float* column = t.cuts + (uint64_t)f * t.cut_stride;
+          uint32_t lo = 0, hi = count;
+          while (lo < hi) {
+            uint32_t mid = lo + (hi - lo) / 2;
+            if (column[mid] < best.threshold) lo = mid + 1;
+            else hi = mid;
+          }
+          uint32_t steps = lo + 1 < count ? lo + 1 : count;
+          if (best.default_left) {
+            uint32_t bin = best.threshold == -INFINITY ? 0 : lo + 1;
+            steps = bin < count ? count - bin : 0;
+          }
+          double cg, ch;
+          ordered_sum(hist + (uint64_t)f * t.bins1 * 2, 0, steps, best.default_left != 0, count, eg, eh, &cg, &ch);
+          double og = tg - cg, oh = th - ch;
+          double ag = cg + og, ah = ch + oh;
+          applied_w = calc_weight(ag, ah, p);
+          applied_h = (float)ah;
+        }
+      } else if (best.feature >= 0) {
+        double ag = stat_value(best.lg, eg) + stat_value(best.rg, eg);
+        double ah = stat_value(best.lh, eh) + stat_value(best.rh, eh);
+        applied_w = calc_weight(ag, ah, p);
+        applied_h = (float)ah;
+      }
+    }
+    uint32_t total_expanded;
+    const uint32_t rank = block_exclusive_u32(expand ? 1u : 0u, scan, &total_expanded) + carry_expanded;
+    uint32_t tiles = 0;
+    if (valid) tiles = div_up(node.count, kPartTile);
+    uint32_t total_tasks;
+    const uint32_t toff = block_exclusive_u32(tiles, scan, &total_tasks) + carry_tasks;
+    if (valid) {
+      MgbTreeNode* rec = t.nodes + node.id;
+      rec->cover = total_h;
+      if (node.id == 0) {
+        rec->base_weight = parent_w;
+        rec->leaf = parent_w * p.eta;
+      }
+      NodeOp op;
+      op.feature = 0; op.last_left_bin = -1; op.default_left = 0;
+      op.leaf = rec->leaf; op.left_leaf = 0; op.right_leaf = 0; op.child_slot = 0;
+      if (!expand) {
+        op.op = kOpLeaf;
+      } else {
+        const int32_t left = (int32_t)(node_base + 2 * rank), right = left + 1;
+        rec->left = left; rec->right = right;
+        rec->feature = best.feature;
+        rec->threshold = best.threshold;
+        rec->default_left = best.default_left;
+        rec->gain = best.gain;
+        rec->base_weight = applied_w;
+        rec->cover = applied_h;
+        MgbTreeNode l, r;
+        l.left = l.right = -1; l.parent = node.id; l.feature = -1; l.threshold = 0;
+        l.leaf = best.left_w * p.eta; l.cover = best.left_h; l.gain = 0; l.default_left = 0; l.base_weight = l.leaf;
+        r = l;
+        r.leaf = best.right_w * p.eta; r.cover = best.right_h; r.base_weight = r.leaf;
+        t.nodes[left] = l;
+        t.nodes[right] = r;
+        op.op = final_level ? kOpFinal : kOpSplit;
+        op.feature = (uint32_t)best.feature;
+        op.last_left_bin = best.default_left ? (int32_t)best.bin - 1 : (int32_t)best.bin;
+        op.default_left = best.default_left;
+        op.left_leaf = l.leaf;
+        op.right_leaf = r.leaf;
+        op.child_slot = 2 * rank;
+        if (!final_level) {
+          Frontier lf, rf;
+          lf.id = left; lf.begin = 0; lf.count = 0; lf.parent_slot = i; lf.sum_g = best.lg; lf.sum_h = best.lh;
+          lf.built = 0; lf.padding = 0;
+          rf = lf;
+          rf.id = right; rf.sum_g = best.rg; rf.sum_h = best.rh;
+          next[2 * rank] = lf;
+          next[2 * rank + 1] = rf;
+        }
+      }
+      t.ops[i] = op;
+      for (uint32_t k = 0; k < tiles; ++k) {
+        uint32_t b = node.begin + k * kPartTile;
+        uint32_t e = b + kPartTile < node.begin + node.count ? b + kPartTile : node.begin + node.count;
+        PartTask task;
+        task.slot = i; task.begin = b; task.end = e; task.first = toff; task.ntasks = tiles;
+        task.padding[0] = task.padding[1] = task.padding[2] = 0;
+        t.part_tasks[toff + k] = task;
+      }
+    }
+    carry_expanded += total_expanded;
+    carry_tasks += total_tasks;
+  }
+  if (threadIdx.x == 0) {
+    st->node_count = node_base + 2 * carry_expanded;
+    st->n_part_tasks = carry_tasks;
+    st->n_nodes = final_level ? 0 : 2 * carry_expanded;  // becomes the next level's frontier size
+    if (t.node_count_out) *t.node_count_out = node_base + 2 * carry_expanded;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row partition (kernels/boost.metal:1316-1614): stable ballot + prefix
+// scatter.  value < threshold <=> bin <= last_left_bin; missing follows
+// default_left.  Rows of nodes that stop here get their leaf added to the
+// training margin (prediction cache, kernels/boost.metal:1738-1763).
+// ---------------------------------------------------------------------------
+template <typename BinT>
+__device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint32_t row) {
+  const BinT* rowp = reinterpret_cast<const BinT*>(reinterpret_cast<const uint8_t*>(t.bins) +
+                                                   (uint64_t)row * t.row_stride);
+  uint32_t code = rowp[op.feature];
+  if (code == t.missing_code) return op.default_left != 0;
+  return (int32_t)code <= op.last_left_bin;
+}
+
+template <typename BinT, bool IDENTITY>
+__global__ __launch_bounds__(256) void k_part_count(Tree t, uint32_t depth) {
+  __shared__ uint32_t partial[256 / kWave];
+  const LevelState* st = t.state;
+  const uint32_t ntasks = st->n_part_tasks;
+  const uint32_t* rows = t.rows[depth & 1];
+  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
+    const PartTask task = t.part_tasks[w];
+    const NodeOp op = t.ops[task.slot];
+    if (op.op != kOpSplit) continue;
+    uint32_t c = 0;
+    for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
+      uint32_t row = IDENTITY ? i : rows[i];
+      c += goes_left<BinT>(t, op, row) ? 1u : 0u;
+    }
+    uint64_t sum = wave_sum_u64(c);
+    if (lane_id() == 0) partial[threadIdx.x / kWave] = (uint32_t)sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t s = 0;
+      for (uint32_t k = 0; k < blockDim.x / kWave; ++k) s += partial[k];
+      t.part_counts[w] = s;
+    }
+    __syncthreads();
+  }
+}
+
+template <typename BinT, bool IDENTITY>
+__global__ __launch_bounds__(256) void k_part_scatter(Tree t, uint32_t depth) {
+  __shared__ uint32_t wave_left[256 / kWave];
+  __shared__ uint32_t sums[2];
+  const LevelState* st = t.state;
+  const uint32_t ntasks = st->n_part_tasks;
+  const uint32_t* rows = t.rows[depth & 1];
+  uint32_t* out = t.rows[(depth + 1) & 1];
+  const Frontier* fr = t.frontier[depth & 1];
+  Frontier* next = t.frontier[(depth + 1) & 1];
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
+  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
+    const PartTask task = t.part_tasks[w];
+    const NodeOp op = t.ops[task.slot];
+    if (op.op == kOpLeaf) {
+      for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
+        uint32_t row = IDENTITY ? i : rows[i];
+        t.margin[row] = t.margin[row] + op.leaf;
+      }
+      continue;
+    }
+    if (op.op == kOpFinal) {
+      for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
+        uint32_t row = IDENTITY ? i : rows[i];
+        t.margin[row] = t.margin[row] + (goes_left<BinT>(t, op, row) ? op.left_leaf : op.right_leaf);
+      }
+      continue;
+    }
+    if (op.op != kOpSplit) continue;
+    // Left rows of earlier tiles of this node, and of the whole node.
+    if (threadIdx.x < 2) sums[threadIdx.x] = 0;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t k = threadIdx.x; k < task.ntasks; k += blockDim.x) {
+      uint32_t c = t.part_counts[task.first + k];
+      all += c;
+      if (task.first + k < w) before += c;
+    }
+    uint64_t sb = wave_sum_u64(before), sa = wave_sum_u64(all);
+    if (lane == 0) {
+      atomicAdd(&sums[0], (uint32_t)sb);
+      atomicAdd(&sums[1], (uint32_t)sa);
+    }
+    __syncthreads();
+    const Frontier node = fr[task.slot];
+    uint32_t left_before = sums[0];
+    const uint32_t left_total = sums[1];
+    uint32_t right_before = (task.begin - node.begin) - left_before;
+    for (uint32_t chunk = task.begin; chunk < task.end; chunk += blockDim.x) {
+      const uint32_t i = chunk + threadIdx.x;
+      const bool active = i < task.end;
+      uint32_t row = 0;
+      bool left = false;
+      if (active) {
+        row = IDENTITY ? i : rows[i];
+        left = goes_left<BinT>(t, op, row);
+      }
+      const uint64_t lmask = __ballot(active && left);
+      const uint64_t amask = __ballot(active);
+      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+      const uint32_t lrank = (uint32_t)__popcll(lmask & below);
+      const uint32_t arank = (uint32_t)__popcll(amask & below);
+      if (lane == 0) wave_left[wave] = (uint32_t)__popcll(lmask);
+      __syncthreads();
+      uint32_t wl_before = 0, wa_before = 0, chunk_left = 0;
+      for (uint32_t k = 0; k < blockDim.x / kWave; ++k) {
+        uint32_t wl = wave_left[k];
+        if (k < wave) wl_before += wl;
+        chunk_left += wl;
+      }
+      wa_before = wave * kWave;  // all lanes of earlier waves are active except in the last chunk
+      const uint32_t active_in_chunk = (task.end - chunk) < blockDim.x ? task.end - chunk : blockDim.x;
+      if (active) {
+        if (left) {
+          out[node.begin + left_before + wl_before + lrank] = row;
+        } else {
+          uint32_t rrank = (wa_before - wl_before) + (arank - lrank);
+          out[node.begin + left_total + right_before + rrank] = row;
+        }
+      }
+      left_before += chunk_left;
+      right_before += active_in_chunk - chunk_left;
+      __syncthreads();
+    }
+    if (w == task.first && threadIdx.x == 0) {
+      Frontier* l = next + op.child_slot;
+      Frontier* r = l + 1;
+      l->begin = node.begin;
+      l->count = left_total;
+      r->begin = node.begin + left_total;
+      r->count = node.count - left_total;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: workspace layout and the per-level launch sequence.
+// ---------------------------------------------------------------------------
+struct Layout {
+  size_t state, rows, hist, frontier, cands, ops, hist_tasks, zero, part_tasks, part_counts, total;
+  uint32_t slots, max_hist_tasks, max_part_tasks;
+  uint64_t hist_entry;
+};
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+Layout layout(const MgbTreeShape& s) {
+  Layout L;
+  uint32_t depth = s.max_depth ? s.max_depth : 1;
+  L.slots = 1u << (depth - 1);
+  L.hist_entry = (uint64_t)s.cols * (s.max_bin + 1) * 2;
+  L.max_hist_tasks = div_up(s.rows ? s.rows : 1, s.rows_per_tile) + L.slots + 1;
+  L.max_part_tasks = div_up(s.rows ? s.rows : 1, kPartTile) + 2 * L.slots + 1;
+  size_t off = 0;
+  L.state = off; off = align_up(off + sizeof(LevelState));
+  L.rows = off; off = align_up(off + 2 * (size_t)s.rows * sizeof(uint32_t));
+  L.hist = off; off = align_up(off + 2 * (size_t)L.slots * L.hist_entry * sizeof(int64_t));
+  L.frontier = off; off = align_up(off + 2 * (size_t)(2 * L.slots) * sizeof(Frontier));
+  L.cands = off; off = align_up(off + (size_t)(2 * L.slots) * s.cols * sizeof(Cand));
+  L.ops = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(NodeOp));
+  L.hist_tasks = off; off = align_up(off + (size_t)L.max_hist_tasks * sizeof(HistTask));
+  L.zero = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint32_t));
+  L.part_tasks = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(PartTask));
+  L.part_counts = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
+  L.total = off;
+  return L;
+}
+
+template <typename BinT, int G>
+int launch_hist(const Tree& t, uint32_t depth, bool unit, uint32_t grid) {
+  size_t lds = (size_t)G * t.bins1 * (8 + (unit ? 4 : 8));
+  bool identity = depth == 0;
+#define MGB_HIST_CASE(U, I)                                                                           \
+  {                                                                                                   \
+    auto fn = k_histogram<BinT, G, U, I>;                                                             \
+    if (hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
+        hipSuccess) {                                                                                 \
+      set_error("hipFuncSetAttribute(histogram LDS) failed");                                         \
+      return -1;                                                                                      \
+    }                                                                                                 \
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(kHistThreads), lds, stream(), t, depth);                  \
+  }
+  if (unit && identity) MGB_HIST_CASE(true, true)
+  else if (unit) MGB_HIST_CASE(true, false)
+  else if (identity) MGB_HIST_CASE(false, true)
+  else MGB_HIST_CASE(false, false)
+#undef MGB_HIST_CASE
+  MGB_LAUNCH_CHECK("k_histogram");
+  return 0;
+}
+
+template <typename BinT>
+int dispatch_hist(const Tree& t, uint32_t depth, uint32_t grid) {
+  bool unit = t.unit_hessian != 0;
+  switch (t.features_per_group) {
+    case 1: return launch_hist<BinT, 1>(t, depth, unit, grid);
+    case 2: return launch_hist<BinT, 2>(t, depth, unit, grid);
+    case 4: return launch_hist<BinT, 4>(t, depth, unit, grid);
+    case 8: return launch_hist<BinT, 8>(t, depth, unit, grid);
+    case 16: return launch_hist<BinT, 16>(t, depth, unit, grid);
+  }
+  set_error("features_per_group must be 1, 2, 4, 8 or 16");
+  return -1;
+}
+
+int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
+  uint32_t blocks = div_up(items ? items : 1, kSplitThreads / kWave);
+  uint32_t k = div_up(t.bins1, kWave);
+  if (k <= 1) hipLaunchKernelGGL(k_split<1>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
+  else if (k <= 2) hipLaunchKernelGGL(k_split<2>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
+  else if (k <= 5) hipLaunchKernelGGL(k_split<5>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
+  else if (k <= 9) hipLaunchKernelGGL(k_split<9>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
+  else if (k <= 17) hipLaunchKernelGGL(k_split<17>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
+  else {
+    set_error("max_bin above 1087 is not supported by the split kernel");
+    return -1;
+  }
+  MGB_LAUNCH_CHECK("k_split");
+  return 0;
+}
+
+template <typename BinT>
+int launch_partition(const Tree& t, uint32_t depth, uint32_t grid) {
+  if (depth == 0) {
+    hipLaunchKernelGGL((k_part_count<BinT, true>), dim3(grid), dim3(256), 0, stream(), t, depth);
+    MGB_LAUNCH_CHECK("k_part_count");
+    hipLaunchKernelGGL((k_part_scatter<BinT, true>), dim3(grid), dim3(256), 0, stream(), t, depth);
+  } else {
+    hipLaunchKernelGGL((k_part_count<BinT, false>), dim3(grid), dim3(256), 0, stream(), t, depth);
+    MGB_LAUNCH_CHECK("k_part_count");
+    hipLaunchKernelGGL((k_part_scatter<BinT, false>), dim3(grid), dim3(256), 0, stream(), t, depth);
+  }
+  MGB_LAUNCH_CHECK("k_part_scatter");
+  return 0;
+}
+
+int validate(const MgbTreeShape* s, const MgbMatrix* m) {
+  if (!s || !m) { set_error("null shape or matrix"); return -1; }
+  if (s->max_depth < 1 || s->max_depth > 16) { set_error("max_depth must be in [1, 16]"); return -1; }
+  if (s->rows != m->rows || s->cols != m->cols || s->max_bin != m->max_bin) {
+    set_error("tree shape does not match the bin matrix");
+    return -1;
+  }
+  if (m->bin_bytes != 1 && m->bin_bytes != 2) { set_error("bin_bytes must be 1 or 2"); return -1; }
+  uint32_t G = s->features_per_group;
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) { set_error("features_per_group must be a power of two <= 16"); return -1; }
+  uint32_t groups = div_up(m->cols, G);
+  if ((uint64_t)groups * G * m->bin_bytes > m->row_stride) { set_error("row_stride does not cover the feature groups"); return -1; }
+  if ((G * m->bin_bytes) % 4 == 0 && m->row_stride % 4) { set_error("row_stride must be 4-byte aligned"); return -1; }
+  if (G * m->bin_bytes >= 16 && m->row_stride % 16) { set_error("row_stride must be 16-byte aligned"); return -1; }
+  if (s->rows_per_tile < 64) { set_error("rows_per_tile must be >= 64"); return -1; }
+  if (m->max_bin < 1 || m->max_bin > 1086) { set_error("max_bin must be in [1, 1086]"); return -1; }
+  if ((size_t)G * (m->max_bin + 1) * 16 > 160 * 1024) { set_error("feature group does not fit in LDS"); return -1; }
+  return 0;
+}
+
+Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8_t* ws) {
+  Tree t;
+  std::memset(&t, 0, sizeof(t));
+  t.state = reinterpret_cast<LevelState*>(ws + L.state);
+  uint32_t* rows = reinterpret_cast<uint32_t*>(ws + L.rows);
+  t.rows[0] = rows;
+  t.rows[1] = rows + s->rows;
+  int64_t* hist = reinterpret_cast<int64_t*>(ws + L.hist);
+  t.hist[0] = hist;
+  t.hist[1] = hist + (size_t)L.slots * L.hist_entry;
+  Frontier* fr = reinterpret_cast<Frontier*>(ws + L.frontier);
+  t.frontier[0] = fr;
+  t.frontier[1] = fr + 2 * L.slots;
+  t.cands = reinterpret_cast<Cand*>(ws + L.cands);
+  t.ops = reinterpret_cast<NodeOp*>(ws + L.ops);
+  t.hist_tasks = reinterpret_cast<HistTask*>(ws + L.hist_tasks);
+  t.zero_list = reinterpret_cast<uint32_t*>(ws + L.zero);
+  t.part_tasks = reinterpret_cast<PartTask*>(ws + L.part_tasks);
+  t.part_counts = reinterpret_cast<uint32_t*>(ws + L.part_counts);
+  t.rows_n = s->rows; t.cols = s->cols; t.max_bin = m->max_bin; t.bins1 = m->max_bin + 1;
+  t.row_stride = m->row_stride; t.bin_bytes = m->bin_bytes; t.missing_code = m->missing_code;
+  t.cut_stride = m->cut_stride;
+  t.max_depth = s->max_depth; t.slots = L.slots; t.rows_per_tile = s->rows_per_tile;
+  t.features_per_group = s->features_per_group;
+  t.groups = div_up(s->cols, s->features_per_group);
+  t.unit_hessian = s->unit_hessian; t.dense = s->dense; t.max_hist_tasks = L.max_hist_tasks;
+  t.hist_entry = L.hist_entry;
+  return t;
+}
+
+uint32_t hist_grid(const Tree& t) {
+  uint64_t items = (uint64_t)t.max_hist_tasks * t.groups;
+  uint64_t g = items < 2048 ? items : 2048;
+  g = (g + 7) / 8 * 8;
+  return (uint32_t)(g ? g : 8);
+}
+
+}  // namespace
+}  // namespace mgb
+
+using namespace mgb;
+
+extern "C" {
+
+size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape) { return layout(*shape).total; }
+
+int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
+                  const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
+                  void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes, uint32_t* node_count) {
+  if (validate(shape, m)) return -1;
+  Layout L = layout(*shape);
+  if (!workspace || workspace_bytes < L.total) { set_error("mgb_grow_tree: workspace too small"); return -1; }
+  Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
+  t.bins = bins; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
+  t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
+  hipStream_t s = stream();
+  hipLaunchKernelGGL(k_level0, dim3(1), dim3(256), 0, s, t);
+  MGB_LAUNCH_CHECK("k_level0");
+  const uint32_t hgrid = hist_grid(t);
+  const uint32_t pgrid = 1024;
+  for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
+    if (depth > 0) {
+      hipLaunchKernelGGL(k_plan, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
+      MGB_LAUNCH_CHECK("k_plan");
+    }
+    hipLaunchKernelGGL(k_zero, dim3(512), dim3(256), 0, s, t, depth);
+    MGB_LAUNCH_CHECK("k_zero");
+    if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, hgrid) : dispatch_hist<uint16_t>(t, depth, hgrid)))
+      return -1;
+    uint32_t max_nodes = 1u << depth;
+    uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
+    if (launch_split(t, depth, items)) return -1;
+    hipLaunchKernelGGL(k_select, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
+    MGB_LAUNCH_CHECK("k_select");
+    if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
+      return -1;
+  }
+  return 0;
+}
+
+int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const uint32_t* rows,
+                  uint32_t count, const float* grad, const float* scales, int64_t* hist, void* workspace,
+                  size_t workspace_bytes) {
+  if (validate(shape, m)) return -1;
+  Layout L = layout(*shape);
+  if (!workspace || workspace_bytes < L.total) { set_error("mgb_histogram: workspace too small"); return -1; }
+  if (count > shape->rows) { set_error("mgb_histogram: count exceeds rows"); return -1; }
+  Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
+  t.bins = bins; t.grad = reinterpret_cast<const float2*>(grad); t.scales = scales;
+  // Level-0 layout with the caller's row list copied into the row buffer.
+  t.rows_n = count;
+  hipStream_t s = stream();
+  hipLaunchKernelGGL(k_level0, dim3(1), dim3(256), 0, s, t);
+  MGB_LAUNCH_CHECK("k_level0");
+  hipLaunchKernelGGL(k_zero, dim3(512), dim3(256), 0, s, t, 0u);
+  MGB_LAUNCH_CHECK("k_zero");
+  uint32_t depth = 0;
+  if (rows) {
+    MGB_CHECK(hipMemcpyAsync(t.rows[0], rows, (size_t)count * sizeof(uint32_t), hipMemcpyDeviceToDevice, s));
+    depth = 2;  // even depth selects bank 0 and row buffer 0 without the identity shortcut
+  }
+  t.nodes = nullptr;
+  const uint32_t grid = hist_grid(t);
+  if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, grid) : dispatch_hist<uint16_t>(t, depth, grid))) return -1;
+  MGB_CHECK(hipMemcpyAsync(hist, t.hist[0], (size_t)L.hist_entry * sizeof(int64_t), hipMemcpyDeviceToDevice, s));
+  return 0;
+}
+
+}  // extern "C"
