@@ -37,7 +37,9 @@ int mgb_event_elapsed_ms(int begin_slot, int end_slot, float* ms);
 /* ---- POD layouts ------------------------------------------------------ */
 
 /* Bin matrix: row-major, row_stride bytes per row, bin_bytes = 1 (u8) or 2
- * (u16); code 0xFF / 0xFFFF marks a missing value. */
+ * (u16).  missing_code marks a missing value: 0xFF / 0xFFFF when the matrix
+ * has missing values, 0xFFFFFFFF (matches no code) when it has none, so a
+ * dense matrix keeps u8 codes for all 256 bins. */
 typedef struct {
   uint32_t rows, cols, row_stride, bin_bytes;
   uint32_t max_bin;      /* histogram bins per feature; slot max_bin holds missing */

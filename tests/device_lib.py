@@ -84,11 +84,11 @@ def layout(cols, hist_bins, bin_bytes, G):
     return groups * G * bin_bytes
 
 
-def quantize_bins(X, cuts, counts, hist_bins, bin_bytes, G):
+def quantize_bins(X, cuts, counts, hist_bins, bin_bytes, G, dense=False):
     X = np.ascontiguousarray(X, np.float32)
     rows, cols = X.shape
-    m = MgbMatrix(rows, cols, layout(cols, hist_bins, bin_bytes, G), bin_bytes, hist_bins, cuts.shape[1],
-                  0xFF if bin_bytes == 1 else 0xFFFF, 0)
+    code = 0xFFFFFFFF if dense else (0xFF if bin_bytes == 1 else 0xFFFF)
+    m = MgbMatrix(rows, cols, layout(cols, hist_bins, bin_bytes, G), bin_bytes, hist_bins, cuts.shape[1], code, 0)
     dX = Device.of(X)
     dcuts = Device.of(np.ascontiguousarray(cuts, np.float32))
     dcounts = Device.of(np.ascontiguousarray(counts, np.uint32))

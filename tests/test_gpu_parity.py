@@ -104,6 +104,24 @@ def test_bins_and_histogram_match_oracle(bin_bytes, G):
             np.testing.assert_array_equal(hist[f, :, 1].astype(np.uint64), eh)
 
 
+def test_dense_u8_uses_all_256_codes():
+    """A matrix without missing values keeps u8 codes for 256 bins: code 255 is
+    a real bin, counted in bin 255 of the histogram, not in the missing slot."""
+    X, _ = W.config0(rows=20000, cols=4)
+    ocuts, ocounts, _ = O.sketch_cuts(X, 256)
+    assert ocounts.max() == 256
+    obins = O.quantize(X, ocuts, ocounts)
+    m, dbins, bins, missing = D.quantize_bins(X, ocuts, ocounts, 256, 1, 4, dense=True)
+    assert not missing
+    np.testing.assert_array_equal(bins[:, :4], obins)
+    grad = np.ones(len(X), np.float32)
+    hist = D.histogram(m, dbins, None, grad, grad, [O.gradient_scale(grad)] * 2, 4)
+    counts = hist[:, :, 1] // int(np.float32(O.gradient_scale(grad)))
+    for f in range(4):
+        np.testing.assert_array_equal(counts[f, :256], np.bincount(obins[:, f], minlength=256))
+        assert counts[f, 256] == 0
+
+
 # ---------------------------------------------------------------------------
 # End to end through the drop-in API
 # ---------------------------------------------------------------------------

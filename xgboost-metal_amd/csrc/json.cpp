@@ -185,9 +185,13 @@ bool Json::contains(const std::string& key) const {
 std::string format_float(float v) {
   if (std::isnan(v)) return "NaN";
   if (std::isinf(v)) return v > 0 ? "Infinity" : "-Infinity";
-  char buf[32];
+  char buf[40];
   std::snprintf(buf, sizeof(buf), "%.9g", (double)v);
-  return buf;
+  // Keep a float literal ("-0" would read back as the integer 0 and lose
+  // the sign of zero).
+  std::string out = buf;
+  if (out.find_first_of(".eE") == std::string::npos) out += ".0";
+  return out;
 }
 
 void Json::dump_to(std::string& out) const {

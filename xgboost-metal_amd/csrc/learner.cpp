@@ -122,8 +122,10 @@ void DMatrix::quantize(uint32_t max_bin) {
   uint32_t missing = 0;
   d_missing.download(&missing, sizeof(missing));
   has_missing = missing != 0;
-  // u8 codes when bins 0..max_count-1 leave 0xFF free for missing values.
-  uint32_t bin_bytes = (max_count <= 255 || (max_count <= 256 && !has_missing)) && hist_bins <= 256 ? 1 : 2;
+  // u8 codes when every bin fits in a byte: with missing values 0xFF is the
+  // missing code (so at most 255 bins); a matrix without missing values uses
+  // all 256 codes and a missing code no byte can equal.
+  uint32_t bin_bytes = (has_missing ? max_count <= 255 : max_count <= 256) ? 1 : 2;
   uint32_t G = 16;
   while (G > 1 && (size_t)G * (hist_bins + 1) * 16 > 66000) G >>= 1;
   G = std::min(G, next_pow2(cols));
@@ -135,7 +137,7 @@ void DMatrix::quantize(uint32_t max_bin) {
   matrix.row_stride = groups * G * bin_bytes;
   matrix.max_bin = hist_bins;
   matrix.cut_stride = max_bin;
-  matrix.missing_code = bin_bytes == 1 ? 0xFFu : 0xFFFFu;
+  matrix.missing_code = !has_missing ? 0xFFFFFFFFu : (bin_bytes == 1 ? 0xFFu : 0xFFFFu);
   d_bins.ensure((size_t)rows * matrix.row_stride);
   kcheck(mgb_quantize_bins(d_data.as<float>(), d_cuts.as<float>(), d_counts.as<uint32_t>(), &matrix, d_bins.get(),
                            d_missing.as<uint32_t>()),

@@ -115,7 +115,11 @@ __device__ __forceinline__ float calc_weight(double G, double H, const MgbSplitP
   if (fabs(g) <= alpha) g = 0;
   else g = g + (g < 0 ? alpha : -alpha);
   double den = H + (double)p.reg_lambda;
-  float w = (float)(-g / den);
+  // -0/den is -0 in IEEE arithmetic, but the device's binary64 division
+  // sequence refines the quotient with fused multiply-adds that can return +0
+  // for a zero numerator; the zero case is therefore explicit (as in the
+  // reference's scorer, kernels/scalar_gain.metal.h:66-77).
+  float w = g == 0 ? -0.0f : (float)(-g / den);
   float limit = fabsf(p.max_delta_step);
   if (limit != 0.0f && fabsf(w) > limit) w = copysignf(limit, w);
   return w;
@@ -165,7 +169,7 @@ __global__ void k_level0(Tree t) {
     MgbTreeNode n;
     n.left = -1; n.right = -1; n.parent = -1; n.feature = -1;
     n.threshold = 0; n.leaf = 0; n.cover = 0; n.gain = 0; n.default_left = 0; n.base_weight = 0;
-    t.nodes[0] = n;
+    if (t.nodes) t.nodes[0] = n;  // the histogram-only entry point has no tree
   }
 }
 
@@ -996,6 +1000,7 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   if (count > shape->rows) { set_error("mgb_histogram: count exceeds rows"); return -1; }
   Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
   t.bins = bins; t.grad = reinterpret_cast<const float2*>(grad); t.scales = scales;
+  t.nodes = nullptr;  // no tree records: k_level0 skips the root record
   // Level-0 layout with the caller's row list copied into the row buffer.
   t.rows_n = count;
   hipStream_t s = stream();
@@ -1008,7 +1013,6 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
     MGB_CHECK(hipMemcpyAsync(t.rows[0], rows, (size_t)count * sizeof(uint32_t), hipMemcpyDeviceToDevice, s));
     depth = 2;  // even depth selects bank 0 and row buffer 0 without the identity shortcut
   }
-  t.nodes = nullptr;
   const uint32_t grid = hist_grid(t);
   if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, grid) : dispatch_hist<uint16_t>(t, depth, grid))) return -1;
   MGB_CHECK(hipMemcpyAsync(hist, t.hist[0], (size_t)L.hist_entry * sizeof(int64_t), hipMemcpyDeviceToDevice, s));
