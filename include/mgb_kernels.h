@@ -33,6 +33,20 @@ int mgb_synchronize(void);
 /* Event timing on the library stream (src/runtime.mm:203-280 profiler). */
 int mgb_event_record(int slot);
 int mgb_event_elapsed_ms(int begin_slot, int end_slot, float* ms);
+/* Per-kernel-class timing: when enabled, every launch of the classes below is
+ * bracketed by HIP events on the library stream; mgb_profile_collect waits
+ * for the stream and adds the elapsed times (src/runtime.mm:203-280). */
+enum {
+  MGB_PROF_GRADIENT = 0, MGB_PROF_HISTOGRAM = 1, MGB_PROF_SPLIT = 2, MGB_PROF_CONTROL = 3,
+  MGB_PROF_PARTITION = 4, MGB_PROF_PREDICT = 5, MGB_PROF_KINDS = 6
+};
+int mgb_profile_enable(int on);
+int mgb_profile_collect(void);
+int mgb_profile_read(double* ms, uint64_t* launches, int kinds);
+int mgb_profile_reset(void);
+/* Plain device copy (dst, src 16-byte aligned); the bandwidth reference for
+ * the roofline and the calibration kernel for HBM counters. */
+int mgb_stream_copy(void* dst, const void* src, size_t bytes);
 
 /* ---- POD layouts ------------------------------------------------------ */
 
@@ -120,6 +134,11 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
 int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
                   const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
                   void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes, uint32_t* node_count);
+
+/* Rows and nodes whose histograms each level built directly (not by
+ * subtraction), from the last mgb_grow_tree on this workspace; synchronises. */
+int mgb_tree_level_stats(const MgbTreeShape* shape, const void* workspace, uint64_t* rows_built,
+                         uint32_t* nodes_built, uint32_t levels);
 
 /* ---- kernel-level entry points used by parity tests and the profiler --- */
 /* Histogram of rows [0, count) of row list `rows` (NULL = identity) into

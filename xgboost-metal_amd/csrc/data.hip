@@ -209,6 +209,11 @@ __global__ void k_transform(float* __restrict__ data, uint64_t count, uint32_t o
   }
 }
 
+__global__ __launch_bounds__(256) void k_copy(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
 __global__ void k_fill(float* __restrict__ data, uint64_t count, float value) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
     data[i] = value;
@@ -275,8 +280,10 @@ int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labe
                   float* grad, uint64_t* mass) {
   if (!p->rows) return 0;
   uint32_t grid = grid_for(p->rows, 256, 2048);
+  prof_begin(MGB_PROF_GRADIENT);
   hipLaunchKernelGGL(k_gradients, dim3(grid), dim3(256), 0, stream(), *p, margin, labels, weights, (float2*)grad,
                      mass);
+  prof_end(MGB_PROF_GRADIENT);
   MGB_LAUNCH_CHECK("k_gradients");
   return 0;
 }
@@ -290,7 +297,9 @@ int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass) {
 }
 
 int mgb_gradient_scales(uint64_t* mass, float* scales) {
+  prof_begin(MGB_PROF_GRADIENT);
   hipLaunchKernelGGL(k_gradient_scales, dim3(1), dim3(256), 0, stream(), mass, scales);
+  prof_end(MGB_PROF_GRADIENT);
   MGB_LAUNCH_CHECK("k_gradient_scales");
   return 0;
 }
@@ -300,6 +309,18 @@ int mgb_base_score(const float* labels, const float* weights, uint32_t rows, uin
   hipLaunchKernelGGL(k_base_score, dim3(1), dim3(1024), 0, stream(), labels, weights, rows, objective,
                      scale_pos_weight, out);
   MGB_LAUNCH_CHECK("k_base_score");
+  return 0;
+}
+
+int mgb_stream_copy(void* dst, const void* src, size_t bytes) {
+  if (bytes % 16 || ((uintptr_t)dst % 16) || ((uintptr_t)src % 16)) {
+    set_error("mgb_stream_copy: 16-byte aligned buffers and sizes only");
+    return -1;
+  }
+  uint64_t n = bytes / 16;
+  if (!n) return 0;
+  hipLaunchKernelGGL(k_copy, dim3(grid_for(n, 256, 8192)), dim3(256), 0, stream(), (uint4*)dst, (const uint4*)src, n);
+  MGB_LAUNCH_CHECK("k_copy");
   return 0;
 }
 
@@ -327,8 +348,10 @@ int mgb_transform(float* data, uint64_t count, uint32_t objective) {
 int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode* nodes, const uint32_t* offsets,
                 uint32_t trees, float* margin) {
   if (!rows || !trees) return 0;
+  prof_begin(MGB_PROF_PREDICT);
   hipLaunchKernelGGL(k_predict, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), X, rows, cols, nodes, offsets,
                      trees, margin);
+  prof_end(MGB_PROF_PREDICT);
   MGB_LAUNCH_CHECK("k_predict");
   return 0;
 }

@@ -26,6 +26,10 @@ int check(hipError_t status, const char* what);
     if (::mgb::check(hipGetLastError(), name) != 0) return -1; \
   } while (0)
 
+// Profiling brackets around launches (no-ops unless mgb_profile_enable(1)).
+void prof_begin(int kind);
+void prof_end(int kind);
+
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
 // Inclusive wave64 prefix sum of a 32-bit value.

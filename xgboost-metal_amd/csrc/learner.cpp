@@ -348,6 +348,8 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   sp.max_depth = depth;
   sp.fma_contract = (uint32_t)integer("fma_contract", 1);
   DeviceBuffer* margin = margin_cache(data);
+  const bool profiling = integer("hip_profile", 0) != 0;
+  kcheck(mgb_profile_enable(profiling ? 1 : 0), "profile");
   auto* nodes = d_nodes_.as<MgbTreeNode>();
   auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
   kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
@@ -360,6 +362,19 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   uint32_t n = 0;
   std::memcpy(&n, host.data() + node_bytes, sizeof(uint32_t));
   require(n >= 1 && n <= max_nodes, "device tree driver produced an invalid node count");
+  if (profiling) {
+    // Algorithmic histogram bytes per level: rows built x (F codes + 4-byte
+    // row id + 8-byte gradient pair) + nodes built x F x (B+1) x 16 bytes.
+    kcheck(mgb_profile_collect(), "profile collect");
+    uint64_t rows[32] = {0};
+    uint32_t built[32] = {0};
+    kcheck(mgb_tree_level_stats(&shape, d_tree_ws_.get(), rows, built, 32), "level statistics");
+    for (uint32_t d = 0; d < depth && d < 32; ++d) {
+      hist_bytes_ += rows[d] * ((uint64_t)data.cols * data.matrix.bin_bytes + 12) +
+                     (uint64_t)built[d] * data.cols * (data.hist_bins + 1) * 16;
+      hist_rows_ += rows[d];
+    }
+  }
   Tree tree;
   tree.nodes.resize(n);
   std::memcpy(tree.nodes.data(), host.data(), (size_t)n * sizeof(MgbTreeNode));
@@ -699,6 +714,20 @@ Json Learner::profile() const {
   for (auto const& kv : seconds_) secs[kv.first] = Json(kv.second);
   out["seconds"] = secs;
   out["rounds"] = Json((uint64_t)rounds_timed_);
+  static const char* names[MGB_PROF_KINDS] = {"gradient", "histogram", "split", "control", "partition", "predict"};
+  double ms[MGB_PROF_KINDS] = {0};
+  uint64_t launches[MGB_PROF_KINDS] = {0};
+  mgb_profile_read(ms, launches, MGB_PROF_KINDS);
+  Json kernels = Json::object();
+  for (int k = 0; k < MGB_PROF_KINDS; ++k) {
+    Json e = Json::object();
+    e["ms"] = Json(ms[k]);
+    e["launches"] = Json(launches[k]);
+    kernels[names[k]] = e;
+  }
+  out["kernels"] = kernels;
+  out["histogram_bytes"] = Json(hist_bytes_);
+  out["histogram_rows"] = Json(hist_rows_);
   return out;
 }
 

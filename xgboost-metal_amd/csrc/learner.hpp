@@ -140,6 +140,7 @@ class Learner {
   size_t uploaded_trees_ = 0;
   std::map<std::string, double> seconds_;
   uint64_t rounds_timed_ = 0;
+  uint64_t hist_bytes_ = 0, hist_rows_ = 0;
 };
 
 }  // namespace mgb

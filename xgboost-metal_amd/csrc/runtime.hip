@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "device_common.hpp"
 
@@ -19,7 +20,38 @@ std::mutex g_init_mutex;
 hipEvent_t g_events[16] = {};
 }  // namespace
 
+struct Profile {
+  bool on = false;
+  std::vector<hipEvent_t> free_events;
+  struct Pending { int kind; hipEvent_t begin, end; };
+  std::vector<Pending> pending;
+  hipEvent_t open[MGB_PROF_KINDS] = {};
+  double ms[MGB_PROF_KINDS] = {};
+  uint64_t launches[MGB_PROF_KINDS] = {};
+  hipEvent_t take() {
+    hipEvent_t e = nullptr;
+    if (!free_events.empty()) { e = free_events.back(); free_events.pop_back(); }
+    else if (hipEventCreate(&e) != hipSuccess) e = nullptr;
+    return e;
+  }
+};
+Profile g_profile;
+
 hipStream_t stream() { return g_stream; }
+
+void prof_begin(int kind) {
+  if (!g_profile.on || kind < 0 || kind >= MGB_PROF_KINDS) return;
+  hipEvent_t e = g_profile.take();
+  if (e && hipEventRecord(e, g_stream) == hipSuccess) g_profile.open[kind] = e;
+}
+
+void prof_end(int kind) {
+  if (!g_profile.on || kind < 0 || kind >= MGB_PROF_KINDS || !g_profile.open[kind]) return;
+  hipEvent_t e = g_profile.take();
+  if (e && hipEventRecord(e, g_stream) == hipSuccess)
+    g_profile.pending.push_back({kind, g_profile.open[kind], e});
+  g_profile.open[kind] = nullptr;
+}
 void set_error(std::string message) { g_error = std::move(message); }
 
 int check(hipError_t status, const char* what) {
@@ -117,6 +149,40 @@ int mgb_event_record(int slot) {
   if (ensure_init()) return -1;
   if (slot < 0 || slot >= 16) { set_error("mgb_event_record: slot out of range"); return -1; }
   MGB_CHECK(hipEventRecord(g_events[slot], g_stream));
+  return 0;
+}
+
+int mgb_profile_enable(int on) {
+  if (ensure_init()) return -1;
+  g_profile.on = on != 0;
+  return 0;
+}
+
+int mgb_profile_collect(void) {
+  if (ensure_init()) return -1;
+  MGB_CHECK(hipStreamSynchronize(g_stream));
+  for (auto& p : g_profile.pending) {
+    float ms = 0;
+    MGB_CHECK(hipEventElapsedTime(&ms, p.begin, p.end));
+    g_profile.ms[p.kind] += ms;
+    g_profile.launches[p.kind] += 1;
+    g_profile.free_events.push_back(p.begin);
+    g_profile.free_events.push_back(p.end);
+  }
+  g_profile.pending.clear();
+  return 0;
+}
+
+int mgb_profile_read(double* ms, uint64_t* launches, int kinds) {
+  for (int k = 0; k < kinds && k < MGB_PROF_KINDS; ++k) {
+    if (ms) ms[k] = g_profile.ms[k];
+    if (launches) launches[k] = g_profile.launches[k];
+  }
+  return 0;
+}
+
+int mgb_profile_reset(void) {
+  for (int k = 0; k < MGB_PROF_KINDS; ++k) { g_profile.ms[k] = 0; g_profile.launches[k] = 0; }
   return 0;
 }
 

@@ -25,6 +25,8 @@ constexpr uint32_t kSplitThreads = 256;   // four waves, one (node pair, feature
 
 enum : uint32_t { kOpNone = 0, kOpLeaf = 1, kOpSplit = 2, kOpFinal = 3 };
 
+constexpr uint32_t kMaxLevels = 32;
+
 struct LevelState {
   uint32_t n_nodes;       // frontier size of the current level
   uint32_t n_hist_tasks;
@@ -33,6 +35,9 @@ struct LevelState {
   uint32_t node_count;    // tree nodes allocated so far
   uint32_t error;
   uint32_t padding[10];
+  // Per level: rows and nodes whose histograms were built directly.
+  uint64_t rows_built[kMaxLevels];
+  uint32_t nodes_built[kMaxLevels];
 };
 
 struct Frontier {
@@ -155,6 +160,8 @@ __global__ void k_level0(Tree t) {
     t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
   }
   if (threadIdx.x == 0) {
+    st->rows_built[0] = t.rows_n;
+    st->nodes_built[0] = 1;
     st->n_nodes = 1;
     st->n_hist_tasks = tiles;
     st->n_zero = tiles == 1 ? 0u : 1u;
@@ -180,7 +187,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
   LevelState* st = t.state;
   Frontier* fr = t.frontier[depth & 1];
   uint32_t pairs = st->n_nodes / 2;
-  uint32_t carry_tasks = 0, carry_zero = 0;
+  uint32_t carry_tasks = 0, carry_zero = 0, carry_rows = 0;
   for (uint32_t base = 0; base < pairs; base += blockDim.x) {
     uint32_t p = base + threadIdx.x;
     uint32_t tiles = 0, zero = 0, built = 0, count = 0, begin = 0;
@@ -194,9 +201,11 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
       tiles = div_up(count, t.rows_per_tile);
       zero = tiles != 1;
     }
-    uint32_t total_tasks, total_zero;
+    uint32_t total_tasks, total_zero, total_rows;
     uint32_t off = block_exclusive_u32(tiles, scan, &total_tasks) + carry_tasks;
     uint32_t zoff = block_exclusive_u32(zero, scan, &total_zero) + carry_zero;
+    block_exclusive_u32(count, scan, &total_rows);
+    carry_rows += total_rows;
     for (uint32_t k = 0; k < tiles; ++k) {
       uint32_t b = begin + k * t.rows_per_tile;
       uint32_t e = b + t.rows_per_tile < begin + count ? b + t.rows_per_tile : begin + count;
@@ -209,6 +218,10 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
   if (threadIdx.x == 0) {
     st->n_hist_tasks = carry_tasks;
     st->n_zero = carry_zero;
+    if (depth < kMaxLevels) {
+      st->rows_built[depth] = carry_rows;
+      st->nodes_built[depth] = pairs;
+    }
   }
 }
 
@@ -967,26 +980,53 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   t.bins = bins; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
   hipStream_t s = stream();
+  prof_begin(MGB_PROF_CONTROL);
   hipLaunchKernelGGL(k_level0, dim3(1), dim3(256), 0, s, t);
+  prof_end(MGB_PROF_CONTROL);
   MGB_LAUNCH_CHECK("k_level0");
   const uint32_t hgrid = hist_grid(t);
   const uint32_t pgrid = 1024;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
+    prof_begin(MGB_PROF_CONTROL);
     if (depth > 0) {
       hipLaunchKernelGGL(k_plan, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
     hipLaunchKernelGGL(k_zero, dim3(512), dim3(256), 0, s, t, depth);
+    prof_end(MGB_PROF_CONTROL);
     MGB_LAUNCH_CHECK("k_zero");
+    prof_begin(MGB_PROF_HISTOGRAM);
     if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, hgrid) : dispatch_hist<uint16_t>(t, depth, hgrid)))
       return -1;
+    prof_end(MGB_PROF_HISTOGRAM);
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
+    prof_begin(MGB_PROF_SPLIT);
     if (launch_split(t, depth, items)) return -1;
+    prof_end(MGB_PROF_SPLIT);
+    prof_begin(MGB_PROF_CONTROL);
     hipLaunchKernelGGL(k_select, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
+    prof_end(MGB_PROF_CONTROL);
     MGB_LAUNCH_CHECK("k_select");
+    prof_begin(MGB_PROF_PARTITION);
     if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
       return -1;
+    prof_end(MGB_PROF_PARTITION);
+  }
+  return 0;
+}
+
+int mgb_tree_level_stats(const MgbTreeShape* shape, const void* workspace, uint64_t* rows_built,
+                         uint32_t* nodes_built, uint32_t levels) {
+  Layout L = layout(*shape);
+  LevelState st;
+  MGB_CHECK(hipMemcpyAsync(&st, reinterpret_cast<const uint8_t*>(workspace) + L.state, sizeof(st),
+                           hipMemcpyDeviceToHost, stream()));
+  MGB_CHECK(hipStreamSynchronize(stream()));
+  for (uint32_t d = 0; d < levels && d < kMaxLevels; ++d) {
+    bool valid = d < shape->max_depth;
+    if (rows_built) rows_built[d] = valid ? st.rows_built[d] : 0;
+    if (nodes_built) nodes_built[d] = valid ? st.nodes_built[d] : 0;
   }
   return 0;
 }
