@@ -38,7 +38,7 @@ int mgb_event_elapsed_ms(int begin_slot, int end_slot, float* ms);
  * for the stream and adds the elapsed times (src/runtime.mm:203-280). */
 enum {
   MGB_PROF_GRADIENT = 0, MGB_PROF_HISTOGRAM = 1, MGB_PROF_SPLIT = 2, MGB_PROF_CONTROL = 3,
-  MGB_PROF_PARTITION = 4, MGB_PROF_PREDICT = 5, MGB_PROF_KINDS = 6
+  MGB_PROF_PARTITION = 4, MGB_PROF_PREDICT = 5, MGB_PROF_REDUCE = 6, MGB_PROF_KINDS = 7
 };
 int mgb_profile_enable(int on);
 int mgb_profile_collect(void);

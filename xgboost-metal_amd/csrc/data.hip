@@ -115,8 +115,11 @@ __global__ __launch_bounds__(256) void k_gradient_mass(const float2* __restrict_
 
 // scale = 2^(62 - max(0, bitlen(sum) - 149)); gradient_quantization.metal.h:52-63.
 __global__ void k_gradient_scales(uint64_t* __restrict__ mass, float* __restrict__ scales) {
+  __shared__ uint64_t staged[512];
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) staged[i] = mass[i];
+  __syncthreads();
   if (threadIdx.x < 2) {
-    const uint64_t* s = mass + threadIdx.x * 256;
+    const uint64_t* s = staged + threadIdx.x * 256;
     uint32_t limb[11] = {0};
     for (uint32_t j = 0; j < 256; ++j) {
       uint64_t v = s[j];

@@ -714,7 +714,8 @@ Json Learner::profile() const {
   for (auto const& kv : seconds_) secs[kv.first] = Json(kv.second);
   out["seconds"] = secs;
   out["rounds"] = Json((uint64_t)rounds_timed_);
-  static const char* names[MGB_PROF_KINDS] = {"gradient", "histogram", "split", "control", "partition", "predict"};
+  static const char* names[MGB_PROF_KINDS] = {"gradient", "histogram", "split", "control", "partition", "predict",
+                                              "reduce"};
   double ms[MGB_PROF_KINDS] = {0};
   uint64_t launches[MGB_PROF_KINDS] = {0};
   mgb_profile_read(ms, launches, MGB_PROF_KINDS);

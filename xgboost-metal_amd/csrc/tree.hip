@@ -20,7 +20,8 @@ namespace {
 
 constexpr uint32_t kPartTile = 2048;      // rows per partition task
 constexpr uint32_t kSelectThreads = 1024;
-constexpr uint32_t kHistThreads = 256;
+constexpr uint32_t kHistThreads = 1024;
+constexpr int kHistUnroll = 4;          // rows in flight per thread
 constexpr uint32_t kSplitThreads = 256;   // four waves, one (node pair, feature) each
 
 enum : uint32_t { kOpNone = 0, kOpLeaf = 1, kOpSplit = 2, kOpFinal = 3 };
@@ -46,6 +47,8 @@ struct Frontier {
   uint32_t parent_slot;   // parent's slot in the previous level's histogram bank
   int64_t sum_g, sum_h;   // node integer totals (the parent's chosen child sums)
   uint32_t built;         // histogram built directly (1) or by subtraction (0)
+  uint32_t first_task;    // built nodes: first histogram task (row tile)
+  uint32_t ntiles;        // built nodes: number of row tiles
   uint32_t padding;
 };
 
@@ -68,6 +71,16 @@ struct NodeOp {
 };
 
 struct HistTask { uint32_t slot, begin, end, single; };
+
+// Per-node best-feature key: (gain order << 32) | ~feature, so the maximum is
+// the largest gain and, among equal gains, the lowest feature -- the serial
+// first-strictly-greater scan over features (kernels/boost.metal:1245-1265).
+// +0 and -0 map to one key; 0 means no valid candidate.
+__device__ __forceinline__ uint64_t best_key(float gain, uint32_t feature) {
+  uint32_t bits = gain == 0.0f ? 0u : __float_as_uint(gain);
+  uint32_t order = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+  return ((uint64_t)order << 32) | (uint64_t)(~feature);
+}
 struct PartTask { uint32_t slot, begin, end, first, ntasks, padding[3]; };
 
 // Device pointers of one tree workspace.
@@ -77,9 +90,11 @@ struct Tree {
   int64_t* hist[2];
   Frontier* frontier[2];
   Cand* cands;
+  unsigned long long* best;   // per frontier slot, see best_key
   NodeOp* ops;
   HistTask* hist_tasks;
-  uint32_t* zero_list;
+  uint32_t* zero_list;        // built nodes with several row tiles (reduced from partials)
+  int64_t* partials;          // per (task, feature group): G x (max_bin+1) (g, h) partial histograms
   PartTask* part_tasks;
   uint32_t* part_counts;
   // Inputs.
@@ -154,6 +169,8 @@ __device__ __forceinline__ float calc_gain(double G, double H, float w, const Mg
 __global__ void k_level0(Tree t) {
   LevelState* st = t.state;
   uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.rows_per_tile) : 0;
+  if (t.best)
+    for (uint32_t i = threadIdx.x; i < 2 * t.slots; i += blockDim.x) t.best[i] = 0;
   for (uint32_t i = threadIdx.x; i < tiles; i += blockDim.x) {
     uint32_t begin = i * t.rows_per_tile;
     uint32_t end = begin + t.rows_per_tile < t.rows_n ? begin + t.rows_per_tile : t.rows_n;
@@ -171,7 +188,7 @@ __global__ void k_level0(Tree t) {
     t.zero_list[0] = 0;
     Frontier root;
     root.id = 0; root.begin = 0; root.count = t.rows_n; root.parent_slot = 0;
-    root.sum_g = 0; root.sum_h = 0; root.built = 1; root.padding = 0;
+    root.sum_g = 0; root.sum_h = 0; root.built = 1; root.first_task = 0; root.ntiles = tiles; root.padding = 0;
     t.frontier[0][0] = root;
     MgbTreeNode n;
     n.left = -1; n.right = -1; n.parent = -1; n.feature = -1;
@@ -211,6 +228,10 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
       uint32_t e = b + t.rows_per_tile < begin + count ? b + t.rows_per_tile : begin + count;
       t.hist_tasks[off + k] = HistTask{built, b, e, tiles == 1 ? 1u : 0u};
     }
+    if (p < pairs) {
+      fr[built].first_task = off;
+      fr[built].ntiles = tiles;
+    }
     if (zero) t.zero_list[zoff] = built;
     carry_tasks += total_tasks;
     carry_zero += total_zero;
@@ -225,16 +246,34 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
   }
 }
 
-// Clear the histograms that several row tiles accumulate into atomically.
-__global__ void k_zero(Tree t, uint32_t depth) {
+// Sum the row-tile partials of every multi-tile built node into its histogram
+// slot: entry (feature f, bin b) adds partial[(task * groups + f / G) * G + f % G][b]
+// over the node's tasks, in task order (exact integers, mod 2^64).
+__global__ __launch_bounds__(256) void k_reduce_hist(Tree t, uint32_t depth) {
   const LevelState* st = t.state;
-  uint32_t n = st->n_zero;
-  uint64_t vecs = t.hist_entry / 2;  // 16-byte vectors per node histogram
-  int4* bank = reinterpret_cast<int4*>(t.hist[depth & 1]);
-  uint64_t total = (uint64_t)n * vecs;
+  const uint32_t n = st->n_zero;
+  const uint32_t F = t.cols, B1 = t.bins1, G = t.features_per_group;
+  const uint64_t entries = (uint64_t)F * B1;
+  const uint64_t total = (uint64_t)n * entries;
+  const Frontier* fr = t.frontier[depth & 1];
+  int64_t* bank = t.hist[depth & 1];
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
-    uint32_t slot = t.zero_list[i / vecs];
-    bank[(uint64_t)slot * vecs + i % vecs] = make_int4(0, 0, 0, 0);
+    const uint32_t slot = t.zero_list[i / entries];
+    const uint32_t e = (uint32_t)(i % entries);
+    const uint32_t f = e / B1, b = e % B1;
+    const Frontier node = fr[slot];
+    const uint64_t stride = (uint64_t)t.groups * G * B1 * 2;  // int64 words per task
+    const int64_t* src = t.partials + (uint64_t)node.first_task * stride + ((uint64_t)(f / G) * G + f % G) * B1 * 2 +
+                         (uint64_t)b * 2;
+    uint64_t g = 0, h = 0;
+    for (uint32_t k = 0; k < node.ntiles; ++k) {
+      const int4 v = *reinterpret_cast<const int4*>(src + k * stride);
+      g += (uint64_t)(uint32_t)v.x | ((uint64_t)(uint32_t)v.y << 32);
+      h += (uint64_t)(uint32_t)v.z | ((uint64_t)(uint32_t)v.w << 32);
+    }
+    int64_t* dst = bank + ((uint64_t)slot * F + f) * B1 * 2 + (uint64_t)b * 2;
+    *reinterpret_cast<int4*>(dst) = make_int4((int)(uint32_t)g, (int)(uint32_t)(g >> 32), (int)(uint32_t)h,
+                                              (int)(uint32_t)(h >> 32));
   }
 }
 
@@ -296,16 +335,21 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
   const uint32_t total = ntasks * t.groups;
   const float sg = t.scales[0], sh = t.scales[1];
   const int64_t unit_q = UNIT ? (int64_t)rintf(1.0f * sh) : 0;
-  const uint32_t nwg = gridDim.x;
-  const uint32_t vb = (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8;  // XCD-aware: tiles of one task stay on one XCD
+  // XCD-aware schedule: workgroup b runs on XCD b % 8.  Tasks are dealt
+  // round-robin over the 8 XCDs and every feature group of a task runs on the
+  // task's XCD, so the groups share the task's row lines in that XCD's L2.
+  const uint32_t xcd = blockIdx.x % 8, local = blockIdx.x / 8, per_xcd = gridDim.x / 8;
+  const uint32_t xcd_tasks = ntasks > xcd ? (ntasks - xcd + 7) / 8 : 0;
+  const uint32_t xcd_items = xcd_tasks * t.groups;
   const uint32_t lane = lane_id();
   const uint32_t entries = G * B1;
   const uint32_t* rows = t.rows[depth & 1];
   int64_t* bank = t.hist[depth & 1];
   const uint8_t* bins = reinterpret_cast<const uint8_t*>(t.bins);
-  for (uint32_t item = vb; item < total; item += nwg) {
-    const HistTask task = t.hist_tasks[item / t.groups];
-    const uint32_t group = item % t.groups;
+  (void)total;
+  for (uint32_t j = local; j < xcd_items; j += per_xcd) {
+    const HistTask task = t.hist_tasks[xcd + 8 * (j / t.groups)];
+    const uint32_t group = j % t.groups;
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
       lg[i] = 0;
       if constexpr (UNIT) lc[i] = 0;
@@ -315,42 +359,58 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     const uint32_t fbase = group * G;
     const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
     const uint32_t goff = group * G * sizeof(BinT);
-    for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
-      const uint32_t row = IDENTITY ? i : rows[i];
-      const float2 gh = t.grad[row];
-      const unsigned long long qg = (unsigned long long)(long long)rintf(gh.x * sg);
-      const unsigned long long qh = UNIT ? 0ull : (unsigned long long)(long long)rintf(gh.y * sh);
-      Codes<BinT, G> c;
-      c.load(bins + (uint64_t)row * t.row_stride + goff);
+    // kHistUnroll rows per thread per pass: every row id, gradient pair and
+    // code chunk is requested before the first LDS atomic, so each wave keeps
+    // several gathered loads in flight.
+    for (uint32_t base = task.begin; base < task.end; base += kHistThreads * kHistUnroll) {
+      uint32_t row[kHistUnroll];
+      bool valid[kHistUnroll];
 #pragma unroll
-      for (int k = 0; k < G; ++k) {
-        const uint32_t j = (k + lane) & (G - 1);
-        uint32_t code = c.get(j);
-        uint32_t bin = code == t.missing_code ? t.max_bin : code;
-        if (j < fcount) {
-          atomicAdd(&lg[j * B1 + bin], qg);
-          if constexpr (UNIT) atomicAdd(&lc[j * B1 + bin], 1u);
-          else atomicAdd(&lh[j * B1 + bin], qh);
+      for (int u = 0; u < kHistUnroll; ++u) {
+        const uint32_t i = base + u * kHistThreads + threadIdx.x;
+        valid[u] = i < task.end;
+        row[u] = valid[u] ? (IDENTITY ? i : rows[i]) : 0u;
+      }
+      float2 gh[kHistUnroll];
+      Codes<BinT, G> c[kHistUnroll];
+#pragma unroll
+      for (int u = 0; u < kHistUnroll; ++u) {
+        if (valid[u]) {
+          gh[u] = t.grad[row[u]];
+          c[u].load(bins + (uint64_t)row[u] * t.row_stride + goff);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kHistUnroll; ++u) {
+        if (!valid[u]) continue;
+        const unsigned long long qg = (unsigned long long)(long long)rintf(gh[u].x * sg);
+        const unsigned long long qh = UNIT ? 0ull : (unsigned long long)(long long)rintf(gh[u].y * sh);
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+          const uint32_t j = (k + lane) & (G - 1);
+          uint32_t code = c[u].get(j);
+          uint32_t bin = code == t.missing_code ? t.max_bin : code;
+          if (j < fcount) {
+            atomicAdd(&lg[j * B1 + bin], qg);
+            if constexpr (UNIT) atomicAdd(&lc[j * B1 + bin], 1u);
+            else atomicAdd(&lh[j * B1 + bin], qh);
+          }
         }
       }
     }
     __syncthreads();
-    int64_t* out = bank + ((uint64_t)task.slot * t.cols + fbase) * B1 * 2;
+    // A node's only tile writes its histogram; tiles of larger nodes write a
+    // partial that k_reduce_hist sums (plain stores: no device-scope atomics
+    // across XCDs, and the sum is independent of scheduling).
+    const uint32_t task_index = xcd + 8 * (j / t.groups);
+    int64_t* out = task.single ? bank + ((uint64_t)task.slot * t.cols + fbase) * B1 * 2
+                               : t.partials + ((uint64_t)task_index * t.groups + group) * G * B1 * 2;
     const uint32_t valid = fcount * B1;
-    if (task.single) {
-      for (uint32_t i = threadIdx.x; i < valid; i += blockDim.x) {
-        int64_t g = (int64_t)lg[i];
-        int64_t h = UNIT ? (int64_t)((uint64_t)lc[i] * (uint64_t)unit_q) : (int64_t)lh[i];
-        reinterpret_cast<int4*>(out)[i] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
-                                                    (int)(uint32_t)h, (int)(uint32_t)((uint64_t)h >> 32));
-      }
-    } else {
-      for (uint32_t i = threadIdx.x; i < valid; i += blockDim.x) {
-        uint64_t g = lg[i];
-        uint64_t h = UNIT ? (uint64_t)lc[i] * (uint64_t)unit_q : (uint64_t)lh[i];
-        if (g) atomicAdd(reinterpret_cast<unsigned long long*>(out + 2 * i), (unsigned long long)g);
-        if (h) atomicAdd(reinterpret_cast<unsigned long long*>(out + 2 * i + 1), (unsigned long long)h);
-      }
+    for (uint32_t i = threadIdx.x; i < valid; i += blockDim.x) {
+      int64_t g = (int64_t)lg[i];
+      int64_t h = UNIT ? (int64_t)((uint64_t)lc[i] * (uint64_t)unit_q) : (int64_t)lh[i];
+      reinterpret_cast<int4*>(out)[i] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
+                                                  (int)(uint32_t)h, (int)(uint32_t)((uint64_t)h >> 32));
     }
     __syncthreads();
   }
@@ -369,7 +429,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
 template <int K>
 __device__ void evaluate_node(const int64_t (&hg)[K], const int64_t (&hh)[K], uint32_t count, int64_t total_g,
                               int64_t total_h, const float* cuts_f, int eg, int eh, const MgbSplitParams& p,
-                              uint32_t feature, Cand* out) {
+                              uint32_t feature, Cand* out, unsigned long long* node_best) {
   const uint32_t lane = lane_id();
   // Present sums and lane prefix.
   uint64_t lsum_g = 0, lsum_h = 0;
@@ -442,6 +502,7 @@ __device__ void evaluate_node(const int64_t (&hg)[K], const int64_t (&hh)[K], ui
     if (lane == 0) *out = best;  // no valid candidate: feature -1, gain -inf
   } else if (best_order == o && best_gain == g) {
     *out = best;
+    atomicMax(node_best, best_key(best.gain, feature));
   }
 }
 
@@ -472,7 +533,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
     // Root total: present + missing of this feature (equal for all features).
     int64_t total_g = (int64_t)wave_sum_u64(sg), total_h = (int64_t)wave_sum_u64(shv);
     evaluate_node<K>(hg, hh, t.counts[f], total_g, total_h, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f,
-                     t.cands + f);
+                     t.cands + f, t.best);
     return;
   }
   const uint32_t pairs = n / 2;
@@ -504,8 +565,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
   const Frontier& fo = built == 2 * pair ? b : a;
   const float* cuts_f = t.cuts + (uint64_t)f * t.cut_stride;
   const uint32_t count = t.counts[f];
-  evaluate_node<K>(xg, xh, count, fb.sum_g, fb.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f);
-  evaluate_node<K>(og, oh, count, fo.sum_g, fo.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f);
+  evaluate_node<K>(xg, xh, count, fb.sum_g, fb.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f,
+                   t.best + built);
+  evaluate_node<K>(og, oh, count, fo.sum_g, fo.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f,
+                   t.best + other);
 }
 
 // ---------------------------------------------------------------------------
@@ -547,12 +610,10 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
     Frontier node;
     if (valid) {
       node = fr[i];
-      const Cand* row = t.cands + (uint64_t)i * F;
-      best = row[0];
-      for (uint32_t f = 1; f < F; ++f) {
-        float g = row[f].gain;
-        if (g > best.gain) best = row[f];
-      }
+      const uint64_t key = t.best[i];
+      t.best[i] = 0;  // cleared for the next level, which reuses the slot
+      const uint32_t f = key ? ~(uint32_t)key : 0u;
+      best = t.cands[(uint64_t)i * F + f];
       parent_w = best.parent_w;
       total_h = best.total_h;
       expand = best.feature >= 0 && best.gain > 1.0e-6f && best.gain >= p.min_split_loss &&
@@ -681,9 +742,24 @@ __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint3
   return (int32_t)code <= op.last_left_bin;
 }
 
+constexpr uint32_t kPartThreads = 256;
+constexpr int kPartPer = kPartTile / kPartThreads;  // rows per thread, all loaded up front
+
+// Row ids of a partition tile for this thread (positions begin + k*256 + tid).
+template <bool IDENTITY>
+__device__ __forceinline__ void load_tile_rows(const uint32_t* rows, const PartTask& task, uint32_t (&row)[kPartPer],
+                                               bool (&active)[kPartPer]) {
+#pragma unroll
+  for (int k = 0; k < kPartPer; ++k) {
+    const uint32_t i = task.begin + k * kPartThreads + threadIdx.x;
+    active[k] = i < task.end;
+    row[k] = active[k] ? (IDENTITY ? i : rows[i]) : 0u;
+  }
+}
+
 template <typename BinT, bool IDENTITY>
-__global__ __launch_bounds__(256) void k_part_count(Tree t, uint32_t depth) {
-  __shared__ uint32_t partial[256 / kWave];
+__global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t depth) {
+  __shared__ uint32_t partial[kPartThreads / kWave];
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part_tasks;
   const uint32_t* rows = t.rows[depth & 1];
@@ -691,11 +767,12 @@ __global__ __launch_bounds__(256) void k_part_count(Tree t, uint32_t depth) {
     const PartTask task = t.part_tasks[w];
     const NodeOp op = t.ops[task.slot];
     if (op.op != kOpSplit) continue;
+    uint32_t row[kPartPer];
+    bool active[kPartPer];
+    load_tile_rows<IDENTITY>(rows, task, row, active);
     uint32_t c = 0;
-    for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
-      uint32_t row = IDENTITY ? i : rows[i];
-      c += goes_left<BinT>(t, op, row) ? 1u : 0u;
-    }
+#pragma unroll
+    for (int k = 0; k < kPartPer; ++k) c += (active[k] && goes_left<BinT>(t, op, row[k])) ? 1u : 0u;
     uint64_t sum = wave_sum_u64(c);
     if (lane_id() == 0) partial[threadIdx.x / kWave] = (uint32_t)sum;
     __syncthreads();
@@ -709,8 +786,8 @@ __global__ __launch_bounds__(256) void k_part_count(Tree t, uint32_t depth) {
 }
 
 template <typename BinT, bool IDENTITY>
-__global__ __launch_bounds__(256) void k_part_scatter(Tree t, uint32_t depth) {
-  __shared__ uint32_t wave_left[256 / kWave];
+__global__ __launch_bounds__(kPartThreads) void k_part_scatter(Tree t, uint32_t depth) {
+  __shared__ uint32_t wave_left[kPartThreads / kWave];
   __shared__ uint32_t sums[2];
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part_tasks;
@@ -722,21 +799,25 @@ __global__ __launch_bounds__(256) void k_part_scatter(Tree t, uint32_t depth) {
   for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
     const PartTask task = t.part_tasks[w];
     const NodeOp op = t.ops[task.slot];
+    if (op.op != kOpLeaf && op.op != kOpFinal && op.op != kOpSplit) continue;
+    uint32_t row[kPartPer];
+    bool active[kPartPer];
+    load_tile_rows<IDENTITY>(rows, task, row, active);
     if (op.op == kOpLeaf) {
-      for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
-        uint32_t row = IDENTITY ? i : rows[i];
-        t.margin[row] = t.margin[row] + op.leaf;
-      }
+#pragma unroll
+      for (int k = 0; k < kPartPer; ++k)
+        if (active[k]) t.margin[row[k]] = t.margin[row[k]] + op.leaf;
       continue;
     }
+    bool flag[kPartPer];
+#pragma unroll
+    for (int k = 0; k < kPartPer; ++k) flag[k] = active[k] && goes_left<BinT>(t, op, row[k]);
     if (op.op == kOpFinal) {
-      for (uint32_t i = task.begin + threadIdx.x; i < task.end; i += blockDim.x) {
-        uint32_t row = IDENTITY ? i : rows[i];
-        t.margin[row] = t.margin[row] + (goes_left<BinT>(t, op, row) ? op.left_leaf : op.right_leaf);
-      }
+#pragma unroll
+      for (int k = 0; k < kPartPer; ++k)
+        if (active[k]) t.margin[row[k]] = t.margin[row[k]] + (flag[k] ? op.left_leaf : op.right_leaf);
       continue;
     }
-    if (op.op != kOpSplit) continue;
     // Left rows of earlier tiles of this node, and of the whole node.
     if (threadIdx.x < 2) sums[threadIdx.x] = 0;
     __syncthreads();
@@ -756,36 +837,34 @@ __global__ __launch_bounds__(256) void k_part_scatter(Tree t, uint32_t depth) {
     uint32_t left_before = sums[0];
     const uint32_t left_total = sums[1];
     uint32_t right_before = (task.begin - node.begin) - left_before;
-    for (uint32_t chunk = task.begin; chunk < task.end; chunk += blockDim.x) {
-      const uint32_t i = chunk + threadIdx.x;
-      const bool active = i < task.end;
-      uint32_t row = 0;
-      bool left = false;
-      if (active) {
-        row = IDENTITY ? i : rows[i];
-        left = goes_left<BinT>(t, op, row);
-      }
-      const uint64_t lmask = __ballot(active && left);
-      const uint64_t amask = __ballot(active);
+#pragma unroll
+    for (int k = 0; k < kPartPer; ++k) {
+      const uint32_t chunk = task.begin + k * kPartThreads;
+      if (chunk >= task.end) break;
+      const bool act = active[k];
+      const uint32_t rowk = row[k];
+      const bool left = flag[k];
+      const uint64_t lmask = __ballot(act && left);
+      const uint64_t amask = __ballot(act);
       const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
       const uint32_t lrank = (uint32_t)__popcll(lmask & below);
       const uint32_t arank = (uint32_t)__popcll(amask & below);
       if (lane == 0) wave_left[wave] = (uint32_t)__popcll(lmask);
       __syncthreads();
       uint32_t wl_before = 0, wa_before = 0, chunk_left = 0;
-      for (uint32_t k = 0; k < blockDim.x / kWave; ++k) {
-        uint32_t wl = wave_left[k];
-        if (k < wave) wl_before += wl;
+      for (uint32_t q = 0; q < kPartThreads / kWave; ++q) {
+        uint32_t wl = wave_left[q];
+        if (q < wave) wl_before += wl;
         chunk_left += wl;
       }
       wa_before = wave * kWave;  // all lanes of earlier waves are active except in the last chunk
-      const uint32_t active_in_chunk = (task.end - chunk) < blockDim.x ? task.end - chunk : blockDim.x;
-      if (active) {
+      const uint32_t active_in_chunk = (task.end - chunk) < kPartThreads ? task.end - chunk : kPartThreads;
+      if (act) {
         if (left) {
-          out[node.begin + left_before + wl_before + lrank] = row;
+          out[node.begin + left_before + wl_before + lrank] = rowk;
         } else {
           uint32_t rrank = (wa_before - wl_before) + (arank - lrank);
-          out[node.begin + left_total + right_before + rrank] = row;
+          out[node.begin + left_total + right_before + rrank] = rowk;
         }
       }
       left_before += chunk_left;
@@ -807,7 +886,7 @@ __global__ __launch_bounds__(256) void k_part_scatter(Tree t, uint32_t depth) {
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, cands, ops, hist_tasks, zero, part_tasks, part_counts, total;
+  size_t state, rows, hist, frontier, cands, best, ops, hist_tasks, zero, part_tasks, part_counts, partials, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -827,11 +906,17 @@ Layout layout(const MgbTreeShape& s) {
   L.hist = off; off = align_up(off + 2 * (size_t)L.slots * L.hist_entry * sizeof(int64_t));
   L.frontier = off; off = align_up(off + 2 * (size_t)(2 * L.slots) * sizeof(Frontier));
   L.cands = off; off = align_up(off + (size_t)(2 * L.slots) * s.cols * sizeof(Cand));
+  L.best = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint64_t));
   L.ops = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(NodeOp));
   L.hist_tasks = off; off = align_up(off + (size_t)L.max_hist_tasks * sizeof(HistTask));
   L.zero = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint32_t));
   L.part_tasks = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(PartTask));
   L.part_counts = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
+  {
+    const uint64_t groups = div_up(s.cols, s.features_per_group);
+    L.partials = off;
+    off = align_up(off + (size_t)L.max_hist_tasks * groups * s.features_per_group * (s.max_bin + 1) * 16);
+  }
   L.total = off;
   return L;
 }
@@ -892,13 +977,13 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
 template <typename BinT>
 int launch_partition(const Tree& t, uint32_t depth, uint32_t grid) {
   if (depth == 0) {
-    hipLaunchKernelGGL((k_part_count<BinT, true>), dim3(grid), dim3(256), 0, stream(), t, depth);
+    hipLaunchKernelGGL((k_part_count<BinT, true>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
     MGB_LAUNCH_CHECK("k_part_count");
-    hipLaunchKernelGGL((k_part_scatter<BinT, true>), dim3(grid), dim3(256), 0, stream(), t, depth);
+    hipLaunchKernelGGL((k_part_scatter<BinT, true>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
   } else {
-    hipLaunchKernelGGL((k_part_count<BinT, false>), dim3(grid), dim3(256), 0, stream(), t, depth);
+    hipLaunchKernelGGL((k_part_count<BinT, false>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
     MGB_LAUNCH_CHECK("k_part_count");
-    hipLaunchKernelGGL((k_part_scatter<BinT, false>), dim3(grid), dim3(256), 0, stream(), t, depth);
+    hipLaunchKernelGGL((k_part_scatter<BinT, false>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
   }
   MGB_LAUNCH_CHECK("k_part_scatter");
   return 0;
@@ -938,11 +1023,13 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.frontier[0] = fr;
   t.frontier[1] = fr + 2 * L.slots;
   t.cands = reinterpret_cast<Cand*>(ws + L.cands);
+  t.best = reinterpret_cast<unsigned long long*>(ws + L.best);
   t.ops = reinterpret_cast<NodeOp*>(ws + L.ops);
   t.hist_tasks = reinterpret_cast<HistTask*>(ws + L.hist_tasks);
   t.zero_list = reinterpret_cast<uint32_t*>(ws + L.zero);
   t.part_tasks = reinterpret_cast<PartTask*>(ws + L.part_tasks);
   t.part_counts = reinterpret_cast<uint32_t*>(ws + L.part_counts);
+  t.partials = reinterpret_cast<int64_t*>(ws + L.partials);
   t.rows_n = s->rows; t.cols = s->cols; t.max_bin = m->max_bin; t.bins1 = m->max_bin + 1;
   t.row_stride = m->row_stride; t.bin_bytes = m->bin_bytes; t.missing_code = m->missing_code;
   t.cut_stride = m->cut_stride;
@@ -952,6 +1039,14 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.unit_hessian = s->unit_hessian; t.dense = s->dense; t.max_hist_tasks = L.max_hist_tasks;
   t.hist_entry = L.hist_entry;
   return t;
+}
+
+uint32_t reduce_grid(const Tree& t) {
+  // Enough threads for the largest case (every row tile of one level in
+  // multi-tile nodes); the kernel strides over the real work.
+  uint64_t entries = (uint64_t)t.cols * t.bins1;
+  uint64_t blocks = (entries * 4 + 255) / 256;
+  return (uint32_t)(blocks < 1024 ? (blocks ? blocks : 1) : 1024);
 }
 
 uint32_t hist_grid(const Tree& t) {
@@ -987,18 +1082,20 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   const uint32_t hgrid = hist_grid(t);
   const uint32_t pgrid = 1024;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
-    prof_begin(MGB_PROF_CONTROL);
     if (depth > 0) {
+      prof_begin(MGB_PROF_CONTROL);
       hipLaunchKernelGGL(k_plan, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
+      prof_end(MGB_PROF_CONTROL);
       MGB_LAUNCH_CHECK("k_plan");
     }
-    hipLaunchKernelGGL(k_zero, dim3(512), dim3(256), 0, s, t, depth);
-    prof_end(MGB_PROF_CONTROL);
-    MGB_LAUNCH_CHECK("k_zero");
     prof_begin(MGB_PROF_HISTOGRAM);
     if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, hgrid) : dispatch_hist<uint16_t>(t, depth, hgrid)))
       return -1;
     prof_end(MGB_PROF_HISTOGRAM);
+    prof_begin(MGB_PROF_REDUCE);
+    hipLaunchKernelGGL(k_reduce_hist, dim3(reduce_grid(t)), dim3(256), 0, s, t, depth);
+    prof_end(MGB_PROF_REDUCE);
+    MGB_LAUNCH_CHECK("k_reduce_hist");
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
     prof_begin(MGB_PROF_SPLIT);
@@ -1046,8 +1143,6 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   hipStream_t s = stream();
   hipLaunchKernelGGL(k_level0, dim3(1), dim3(256), 0, s, t);
   MGB_LAUNCH_CHECK("k_level0");
-  hipLaunchKernelGGL(k_zero, dim3(512), dim3(256), 0, s, t, 0u);
-  MGB_LAUNCH_CHECK("k_zero");
   uint32_t depth = 0;
   if (rows) {
     MGB_CHECK(hipMemcpyAsync(t.rows[0], rows, (size_t)count * sizeof(uint32_t), hipMemcpyDeviceToDevice, s));
@@ -1055,6 +1150,8 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   }
   const uint32_t grid = hist_grid(t);
   if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, grid) : dispatch_hist<uint16_t>(t, depth, grid))) return -1;
+  hipLaunchKernelGGL(k_reduce_hist, dim3(reduce_grid(t)), dim3(256), 0, s, t, depth);
+  MGB_LAUNCH_CHECK("k_reduce_hist");
   MGB_CHECK(hipMemcpyAsync(hist, t.hist[0], (size_t)L.hist_entry * sizeof(int64_t), hipMemcpyDeviceToDevice, s));
   return 0;
 }
