@@ -104,15 +104,19 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
                       uint32_t* any_missing);
 
 /* ---- gradients -------------------------------------------------------- */
-/* Objective gradients (kernels/boost.metal:553-601) written as float2 (g, h);
- * also accumulates the exact |g|, |h| mass (kernels/gradient_quantization.metal.h:4-24)
- * into mass[2*256] (u64 mantissa sums per binary32 exponent). */
+/* Words of the exact-mass accumulator: 2 x 256 u64 mantissa sums per binary32
+ * exponent (|g| then |h|), a completion counter and padding.  Zero it once;
+ * every call below leaves it zeroed again. */
+#define MGB_MASS_WORDS 520
+/* Objective gradients (kernels/boost.metal:553-601) written as float2 (g, h),
+ * the exact |g|, |h| mass (kernels/gradient_quantization.metal.h:4-24) and,
+ * from it, the power-of-two fixed-point scales[2]
+ * (kernels/gradient_quantization.metal.h:26-67), in one launch. */
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
-                  float* grad, uint64_t* mass);
-/* Mass of caller-provided gradients (custom objectives). */
-int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass);
-/* Power-of-two fixed-point scales (kernels/gradient_quantization.metal.h:26-67);
- * writes scales[2] and clears mass for the next round. */
+                  float* grad, uint64_t* mass, float* scales);
+/* Mass and scales of caller-provided gradients (custom objectives). */
+int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales);
+/* Scales from an already accumulated mass[0..511]; clears mass. */
 int mgb_gradient_scales(uint64_t* mass, float* scales);
 /* Weighted label mean (src/learner.cpp:316-333): out[0] = binary32 mean. */
 int mgb_base_score(const float* labels, const float* weights, uint32_t rows, uint32_t objective,

@@ -62,10 +62,99 @@ __device__ __forceinline__ void mass_bucket(float v, uint32_t& bucket, uint64_t&
   mantissa = m;
 }
 
-__global__ __launch_bounds__(256) void k_gradients(MgbGradParams p, const float* __restrict__ margin,
-                                                   const float* __restrict__ labels,
-                                                   const float* __restrict__ weights, float2* __restrict__ grad,
-                                                   uint64_t* __restrict__ mass) {
+constexpr uint32_t kGradThreads = 1024;
+constexpr uint32_t kLimbs = 11;     // 352 bits > 255 + 56 bits of the largest exact sum
+constexpr uint32_t kTicket = 512;   // completion counter word of the mass buffer
+
+// scale = 2^(62 - max(0, bitlen(sum) - 149)); gradient_quantization.metal.h:52-63.
+// staged[q*256 + j] = S_j of quantity q (0: |g|, 1: |h|), sum = sum_j S_j 2^j.
+// Carry-save: thread (q, w) adds the 32-bit pieces that land in limb w (each
+// S_j < 2^56 shifted by j % 32 spans limbs j/32 .. j/32+2; at most 96
+// exponents reach one limb, so the u64 lane sum cannot overflow); one thread
+// per quantity then propagates the carries.  Exact, as a serial add would be.
+__device__ void scales_from_mass(const uint64_t* staged, uint64_t* limbs, float* scales) {
+  const uint32_t tid = threadIdx.x;
+  if (tid < 2 * kLimbs) {
+    const uint32_t q = tid / kLimbs, w = tid % kLimbs;
+    const uint64_t* s = staged + q * 256;
+    const uint32_t jlo = w >= 2 ? 32 * (w - 2) : 0, jhi = 32 * (w + 1) < 256 ? 32 * (w + 1) : 256;
+    uint64_t acc = 0;
+    for (uint32_t j = jlo; j < jhi; ++j) {
+      const uint64_t v = s[j];
+      const uint32_t shift = j % 32, part = w - j / 32;
+      const uint64_t lo = v << shift, hi = shift ? (v >> (64 - shift)) : 0;
+      acc += part == 0 ? (uint32_t)lo : part == 1 ? (uint32_t)(lo >> 32) : (uint32_t)hi;
+    }
+    limbs[tid] = acc;
+  }
+  __syncthreads();
+  if (tid < 2) {
+    uint32_t limb[kLimbs];
+    uint64_t carry = 0;
+    for (uint32_t w = 0; w < kLimbs; ++w) {
+      const uint64_t v = limbs[tid * kLimbs + w] + carry;
+      limb[w] = (uint32_t)v;
+      carry = v >> 32;
+    }
+    int exponent = 0;
+    for (int w = kLimbs - 1; w >= 0; --w) {
+      if (limb[w]) {
+        const int bitlen = w * 32 + 32 - __clz(limb[w]);
+        exponent = bitlen - 149 > 0 ? bitlen - 149 : 0;
+        break;
+      }
+    }
+    scales[tid] = __uint_as_float((uint32_t)(62 - exponent + 127) << 23);
+  }
+}
+
+// Per-workgroup exponent buckets in LDS, one device atomic per non-empty
+// bucket, then the last workgroup to finish (completion counter) turns the
+// global buckets into the scales and leaves the buffer zeroed for the next
+// call.  Every access to the shared buckets and the counter is a
+// device-scope atomic.  The bucket adds return their old values and the
+// workgroup waits for them (the values feed an LDS store) before its counter
+// increment: a returned value means the add has been performed at the
+// device's point of coherence, so the last workgroup's atomic loads see every
+// add, without an agent-scope fence (which would write back the whole L2).
+__device__ void mass_flush_and_scale(uint64_t* local, uint64_t* mass, float* scales) {
+  __shared__ uint64_t limbs[2 * kLimbs];
+  __shared__ uint32_t last;
+  __shared__ volatile uint64_t sink;
+  __syncthreads();
+  uint64_t seen = 0;
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x)
+    if (local[i]) seen |= __hip_atomic_fetch_add(&mass[i], local[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  sink = seen;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(&mass[kTicket], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint64_t)(gridDim.x - 1);
+  __syncthreads();
+  if (!last) return;
+  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) {
+    local[i] = __hip_atomic_load(&mass[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&mass[i], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&mass[kTicket], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  scales_from_mass(local, limbs, scales);
+}
+
+__device__ __forceinline__ void mass_add(uint64_t* local, float g, float h) {
+  uint32_t bg, bh;
+  uint64_t mg, mh;
+  mass_bucket(g, bg, mg);
+  mass_bucket(h, bh, mh);
+  if (mg) atomicAdd((unsigned long long*)&local[bg], (unsigned long long)mg);
+  if (mh) atomicAdd((unsigned long long*)&local[256 + bh], (unsigned long long)mh);
+}
+
+__global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, const float* __restrict__ margin,
+                                                            const float* __restrict__ labels,
+                                                            const float* __restrict__ weights,
+                                                            float2* __restrict__ grad, uint64_t* __restrict__ mass,
+                                                            float* __restrict__ scales) {
   __shared__ uint64_t local[2 * 256];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
@@ -82,72 +171,30 @@ __global__ __launch_bounds__(256) void k_gradients(MgbGradParams p, const float*
     g = g * weight;
     h = h * weight;
     grad[r] = make_float2(g, h);
-    uint32_t bg, bh;
-    uint64_t mg, mh;
-    mass_bucket(g, bg, mg);
-    mass_bucket(h, bh, mh);
-    if (mg) atomicAdd((unsigned long long*)&local[bg], (unsigned long long)mg);
-    if (mh) atomicAdd((unsigned long long*)&local[256 + bh], (unsigned long long)mh);
+    mass_add(local, g, h);
   }
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x)
-    if (local[i]) atomicAdd((unsigned long long*)&mass[i], (unsigned long long)local[i]);
+  mass_flush_and_scale(local, mass, scales);
 }
 
-__global__ __launch_bounds__(256) void k_gradient_mass(const float2* __restrict__ grad, uint32_t rows,
-                                                       uint64_t* __restrict__ mass) {
+__global__ __launch_bounds__(kGradThreads) void k_gradient_mass(const float2* __restrict__ grad, uint32_t rows,
+                                                                uint64_t* __restrict__ mass,
+                                                                float* __restrict__ scales) {
   __shared__ uint64_t local[2 * 256];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
   for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
-    float2 v = grad[r];
-    uint32_t bg, bh;
-    uint64_t mg, mh;
-    mass_bucket(v.x, bg, mg);
-    mass_bucket(v.y, bh, mh);
-    if (mg) atomicAdd((unsigned long long*)&local[bg], (unsigned long long)mg);
-    if (mh) atomicAdd((unsigned long long*)&local[256 + bh], (unsigned long long)mh);
+    const float2 v = grad[r];
+    mass_add(local, v.x, v.y);
   }
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x)
-    if (local[i]) atomicAdd((unsigned long long*)&mass[i], (unsigned long long)local[i]);
+  mass_flush_and_scale(local, mass, scales);
 }
 
-// scale = 2^(62 - max(0, bitlen(sum) - 149)); gradient_quantization.metal.h:52-63.
 __global__ void k_gradient_scales(uint64_t* __restrict__ mass, float* __restrict__ scales) {
   __shared__ uint64_t staged[512];
+  __shared__ uint64_t limbs[2 * kLimbs];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) staged[i] = mass[i];
   __syncthreads();
-  if (threadIdx.x < 2) {
-    const uint64_t* s = staged + threadIdx.x * 256;
-    uint32_t limb[11] = {0};
-    for (uint32_t j = 0; j < 256; ++j) {
-      uint64_t v = s[j];
-      if (!v) continue;
-      uint32_t word = j / 32, shift = j % 32;
-      // v < 2^56, so v << shift spans at most three 32-bit limbs.
-      uint64_t lo = v << shift;
-      uint64_t hi = shift ? (v >> (64 - shift)) : 0;
-      uint32_t parts[3] = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi};
-      uint64_t carry = 0;
-      for (uint32_t w = word; w < 11; ++w) {
-        uint64_t add = (w - word < 3 ? parts[w - word] : 0u) + carry;
-        uint64_t sum = (uint64_t)limb[w] + add;
-        limb[w] = (uint32_t)sum;
-        carry = sum >> 32;
-        if (w - word >= 2 && !carry) break;
-      }
-    }
-    int exponent = 0;
-    for (int w = 10; w >= 0; --w) {
-      if (limb[w]) {
-        int bitlen = w * 32 + 32 - __clz(limb[w]);
-        exponent = bitlen - 149 > 0 ? bitlen - 149 : 0;
-        break;
-      }
-    }
-    scales[threadIdx.x] = __uint_as_float((uint32_t)(62 - exponent + 127) << 23);
-  }
+  scales_from_mass(staged, limbs, scales);
   __syncthreads();
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) mass[i] = 0;
 }
@@ -280,21 +327,24 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
 }
 
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
-                  float* grad, uint64_t* mass) {
-  if (!p->rows) return 0;
-  uint32_t grid = grid_for(p->rows, 256, 2048);
+                  float* grad, uint64_t* mass, float* scales) {
+  if (!p->rows) return mgb_gradient_scales(mass, scales);
+  uint32_t grid = grid_for(p->rows, kGradThreads, 256);
   prof_begin(MGB_PROF_GRADIENT);
-  hipLaunchKernelGGL(k_gradients, dim3(grid), dim3(256), 0, stream(), *p, margin, labels, weights, (float2*)grad,
-                     mass);
+  hipLaunchKernelGGL(k_gradients, dim3(grid), dim3(kGradThreads), 0, stream(), *p, margin, labels, weights,
+                     (float2*)grad, mass, scales);
   prof_end(MGB_PROF_GRADIENT);
   MGB_LAUNCH_CHECK("k_gradients");
   return 0;
 }
 
-int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass) {
-  if (!rows) return 0;
-  uint32_t grid = grid_for(rows, 256, 2048);
-  hipLaunchKernelGGL(k_gradient_mass, dim3(grid), dim3(256), 0, stream(), (const float2*)grad, rows, mass);
+int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales) {
+  if (!rows) return mgb_gradient_scales(mass, scales);
+  uint32_t grid = grid_for(rows, kGradThreads, 256);
+  prof_begin(MGB_PROF_GRADIENT);
+  hipLaunchKernelGGL(k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, stream(), (const float2*)grad, rows, mass,
+                     scales);
+  prof_end(MGB_PROF_GRADIENT);
   MGB_LAUNCH_CHECK("k_gradient_mass");
   return 0;
 }

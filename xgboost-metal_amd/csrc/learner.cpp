@@ -395,8 +395,8 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
   DeviceBuffer* margin = margin_cache(data);
   d_grad_.ensure((size_t)data.rows * 2 * sizeof(float));
   if (!d_mass_.get()) {
-    d_mass_.ensure(512 * sizeof(uint64_t));
-    kcheck(mgb_memset(d_mass_.get(), 0, 512 * sizeof(uint64_t)), "memset");
+    d_mass_.ensure(MGB_MASS_WORDS * sizeof(uint64_t));
+    kcheck(mgb_memset(d_mass_.get(), 0, MGB_MASS_WORDS * sizeof(uint64_t)), "memset");
   }
   d_scales_.ensure(2 * sizeof(float));
   MgbGradParams gp{};
@@ -406,9 +406,8 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
   gp.scale_pos_weight = fnumber("scale_pos_weight", 1.0f);
   kcheck(mgb_gradients(&gp, margin->as<float>(), data.d_labels.as<float>(),
                        gp.has_weight ? data.d_weights.as<float>() : nullptr, d_grad_.as<float>(),
-                       d_mass_.as<uint64_t>()),
+                       d_mass_.as<uint64_t>(), d_scales_.as<float>()),
          "gradients");
-  kcheck(mgb_gradient_scales(d_mass_.as<uint64_t>(), d_scales_.as<float>()), "gradient scales");
   grow(data, obj == 0 && data.weights.empty());
   seconds_["train_rounds"] += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   seconds_["quantiles"] = data.sketch_seconds;
@@ -425,12 +424,12 @@ void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t 
   for (size_t i = 0; i < count; ++i) { gh[2 * i] = grad[i]; gh[2 * i + 1] = hess[i]; }
   d_grad_.upload(gh.data(), gh.size() * sizeof(float));
   if (!d_mass_.get()) {
-    d_mass_.ensure(512 * sizeof(uint64_t));
-    kcheck(mgb_memset(d_mass_.get(), 0, 512 * sizeof(uint64_t)), "memset");
+    d_mass_.ensure(MGB_MASS_WORDS * sizeof(uint64_t));
+    kcheck(mgb_memset(d_mass_.get(), 0, MGB_MASS_WORDS * sizeof(uint64_t)), "memset");
   }
   d_scales_.ensure(2 * sizeof(float));
-  kcheck(mgb_gradient_mass(d_grad_.as<float>(), data.rows, d_mass_.as<uint64_t>()), "gradient mass");
-  kcheck(mgb_gradient_scales(d_mass_.as<uint64_t>(), d_scales_.as<float>()), "gradient scales");
+  kcheck(mgb_gradient_mass(d_grad_.as<float>(), data.rows, d_mass_.as<uint64_t>(), d_scales_.as<float>()),
+         "gradient mass");
   grow(data, false);
 }
 

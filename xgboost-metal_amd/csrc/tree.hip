@@ -18,7 +18,7 @@
 namespace mgb {
 namespace {
 
-constexpr uint32_t kPartTile = 2048;      // rows per partition task
+constexpr uint32_t kPartTile = 1024;      // rows per partition task
 constexpr uint32_t kSelectThreads = 1024;
 constexpr uint32_t kHistThreads = 1024;
 constexpr int kHistUnroll = 4;          // rows in flight per thread
@@ -96,7 +96,7 @@ struct Tree {
   uint32_t* zero_list;        // built nodes with several row tiles (reduced from partials)
   int64_t* partials;          // per (task, feature group): G x (max_bin+1) (g, h) partial histograms
   PartTask* part_tasks;
-  uint32_t* part_counts;
+  uint32_t* cursors;          // per split node: next left position, end of the free right range
   // Inputs.
   const void* bins;
   const float* cuts;
@@ -209,7 +209,15 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     uint32_t p = base + threadIdx.x;
     uint32_t tiles = 0, zero = 0, built = 0, count = 0, begin = 0;
     if (p < pairs) {
-      uint32_t c0 = fr[2 * p].count, c1 = fr[2 * p + 1].count;
+      // Child segments from the partition's cursor: the left child holds the
+      // rows below the parent's final left cursor, the right child the rest.
+      Frontier& lf = fr[2 * p];
+      Frontier& rf = fr[2 * p + 1];
+      const uint32_t total = lf.count;
+      const uint32_t c0 = t.cursors[2 * lf.parent_slot] - lf.begin, c1 = total - c0;
+      lf.count = c0;
+      rf.begin = lf.begin + c0;
+      rf.count = c1;
       built = c0 <= c1 ? 2 * p : 2 * p + 1;
       fr[built].built = 1;
       fr[built ^ 1u].built = 0;
@@ -418,122 +426,174 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
 
 // ---------------------------------------------------------------------------
 // Split evaluation (kernels/boost.metal:902-1005, scalar_parallel.metal.h).
-// One wave per (node pair, feature): subtract the built child from the
-// parent (mod 2^64), store the sibling for the next level, then scan both
-// children.  Lane l holds bins [l*K, l*K+K); a wave64 exclusive scan of the
-// lane sums gives exact int64 prefix sums.  Candidates are ranked by
-// (gain, order) with order = b for the forward pass (missing right) and
-// 2*count-1-b for the backward pass (missing left): the maximum gain with the
-// smallest order is the reference's first strictly greater candidate.
+// One wave per (node pair, feature).  The wave walks the feature's bins
+// [0, count) in chunks of 64, one bin per lane: it subtracts the built child
+// from the parent (mod 2^64), stores the sibling for the next level, and
+// extends exact int64 prefix sums of both children with a wave64 scan.  Each
+// lane keeps its best candidate as (gain, order, left sums) only; the lane
+// that wins the wave argmax rebuilds the full candidate at the end.  Order is
+// b for the forward pass (missing right) and 2*count-1-b for the backward
+// pass (missing left): the maximum gain with the smallest order is the
+// reference's first strictly greater candidate.  The sums over present bins
+// come from the node total minus the missing slot (bin max_bin), so one pass
+// suffices.
 // ---------------------------------------------------------------------------
-template <int K>
-__device__ void evaluate_node(const int64_t (&hg)[K], const int64_t (&hh)[K], uint32_t count, int64_t total_g,
-                              int64_t total_h, const float* cuts_f, int eg, int eh, const MgbSplitParams& p,
-                              uint32_t feature, Cand* out, unsigned long long* node_best) {
-  const uint32_t lane = lane_id();
-  // Present sums and lane prefix.
-  uint64_t lsum_g = 0, lsum_h = 0;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    uint32_t b = lane * K + k;
-    if (b < count) { lsum_g += (uint64_t)hg[k]; lsum_h += (uint64_t)hh[k]; }
-  }
-  uint64_t inc_g = wave_inclusive_u64(lsum_g), inc_h = wave_inclusive_u64(lsum_h);
-  uint64_t present_g = __shfl(inc_g, kWave - 1, kWave), present_h = __shfl(inc_h, kWave - 1, kWave);
-  uint64_t pre_g = inc_g - lsum_g, pre_h = inc_h - lsum_h;
-  const uint64_t tg = (uint64_t)total_g, th = (uint64_t)total_h;
-  const bool has_missing = (tg - present_g) != 0 || (th - present_h) != 0;
-  const double G = stat_value(total_g, eg), H = stat_value(total_h, eh);
-  const float w = calc_weight(G, H, p);
-  const float parent_gain = calc_gain(G, H, w, p);
-  float best_gain = -INFINITY;
-  uint32_t best_order = 0xffffffffu;
-  Cand best;
-  best.gain = -INFINITY; best.feature = -1; best.bin = 0; best.default_left = 0; best.threshold = 0;
-  best.left_w = w; best.right_w = w; best.left_h = 0; best.right_h = 0;
-  best.lg = best.lh = best.rg = best.rh = 0;
-  const float mcw = fabsf(p.min_child_weight);
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const uint32_t b = lane * K + k;
-    if (b >= count) break;
-    uint64_t excl_g = pre_g, excl_h = pre_h;
-    pre_g += (uint64_t)hg[k];
-    pre_h += (uint64_t)hh[k];
-    // Forward: left = bins [0, b], missing right.
-    // Backward (missing != 0): right = bins [b, count), missing left.
-    for (int pass = 0; pass < 2; ++pass) {
-      if (pass == 1 && !has_missing) break;
-      uint64_t lgv, lhv, rgv, rhv;
-      if (pass == 0) {
-        lgv = pre_g; lhv = pre_h; rgv = tg - pre_g; rhv = th - pre_h;
-      } else {
-        rgv = present_g - excl_g; rhv = present_h - excl_h; lgv = tg - rgv; lhv = th - rhv;
-      }
-      double GL = stat_value((int64_t)lgv, eg), HL = stat_value((int64_t)lhv, eh);
-      double GR = stat_value((int64_t)rgv, eg), HR = stat_value((int64_t)rhv, eh);
-      if (!(HL > 0 && HL >= (double)mcw && HR > 0 && HR >= (double)mcw)) continue;
-      float lw = calc_weight(GL, HL, p), rw = calc_weight(GR, HR, p);
-      float gain = (calc_gain(GL, HL, lw, p) + calc_gain(GR, HR, rw, p)) - parent_gain;
-      uint32_t order = pass == 0 ? b : 2 * count - 1 - b;
-      if (gain > -INFINITY && (gain > best_gain || (gain == best_gain && order < best_order))) {
-        best_gain = gain;
-        best_order = order;
-        best.gain = gain; best.feature = (int32_t)feature; best.bin = b; best.default_left = pass;
-        best.threshold = pass == 0 ? cuts_f[b] : (b == 0 ? -INFINITY : cuts_f[b - 1]);
-        best.left_w = lw; best.right_w = rw;
-        best.left_h = (float)HL; best.right_h = (float)HR;
-        best.lg = (int64_t)lgv; best.lh = (int64_t)lhv; best.rg = (int64_t)rgv; best.rh = (int64_t)rhv;
-      }
-    }
-  }
-  // Wave argmax of (gain, order).
-  float g = best_gain;
-  uint32_t o = best_order;
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) {
-    float og = __shfl_xor(g, d, kWave);
-    uint32_t oo = __shfl_xor(o, d, kWave);
-    if (og > g || (og == g && oo < o)) { g = og; o = oo; }
-  }
-  best.parent_w = w;
-  best.total_h = (float)H;
-  if (o == 0xffffffffu) {
-    if (lane == 0) *out = best;  // no valid candidate: feature -1, gain -inf
-  } else if (best_order == o && best_gain == g) {
-    *out = best;
-    atomicMax(node_best, best_key(best.gain, feature));
+// Lane 63's value, read into scalar registers (wave-uniform).
+__device__ __forceinline__ uint64_t lane63(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, kWave - 1);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), kWave - 1);
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+struct NodeEval {
+  uint64_t tg, th;        // node totals (present + missing)
+  uint64_t pg, ph;        // present-bin totals
+  uint64_t carry_g, carry_h;  // prefix of the chunks already scanned
+  double G, H;
+  float w, parent_gain;
+  bool has_missing;
+  // This lane's best candidate.
+  float best_gain;
+  uint32_t best_order;
+  uint64_t best_lg, best_lh;
+};
+
+__device__ __forceinline__ void node_begin(NodeEval& n, uint64_t tg, uint64_t th, uint64_t mg, uint64_t mh, int eg,
+                                           int eh, const MgbSplitParams& p) {
+  n.tg = tg; n.th = th;
+  n.pg = tg - mg; n.ph = th - mh;
+  n.has_missing = mg != 0 || mh != 0;
+  n.carry_g = n.carry_h = 0;
+  n.G = stat_value((int64_t)tg, eg);
+  n.H = stat_value((int64_t)th, eh);
+  n.w = calc_weight(n.G, n.H, p);
+  n.parent_gain = calc_gain(n.G, n.H, n.w, p);
+  n.best_gain = -INFINITY;
+  n.best_order = 0xffffffffu;
+  n.best_lg = n.best_lh = 0;
+}
+
+__device__ __forceinline__ void try_candidate(NodeEval& n, uint64_t lg, uint64_t lh, uint32_t order, int eg, int eh,
+                                              float mcw, const MgbSplitParams& p) {
+  const uint64_t rg = n.tg - lg, rh = n.th - lh;
+  const double GL = stat_value((int64_t)lg, eg), HL = stat_value((int64_t)lh, eh);
+  const double GR = stat_value((int64_t)rg, eg), HR = stat_value((int64_t)rh, eh);
+  if (!(HL > 0 && HL >= (double)mcw && HR > 0 && HR >= (double)mcw)) return;
+  const float lw = calc_weight(GL, HL, p), rw = calc_weight(GR, HR, p);
+  const float gain = (calc_gain(GL, HL, lw, p) + calc_gain(GR, HR, rw, p)) - n.parent_gain;
+  if (gain > -INFINITY && (gain > n.best_gain || (gain == n.best_gain && order < n.best_order))) {
+    n.best_gain = gain;
+    n.best_order = order;
+    n.best_lg = lg;
+    n.best_lh = lh;
   }
 }
 
-template <int K>
+// Bins of one chunk (v = this lane's bin, zero past count).
+__device__ __forceinline__ void scan_chunk(NodeEval& n, uint64_t vg, uint64_t vh, uint32_t b, uint32_t count, int eg,
+                                           int eh, float mcw, const MgbSplitParams& p) {
+  const uint64_t ig = wave_inclusive_u64(vg), ih = wave_inclusive_u64(vh);
+  const uint64_t lg = n.carry_g + ig, lh = n.carry_h + ih;  // bins [0, b]
+  n.carry_g += lane63(ig);
+  n.carry_h += lane63(ih);
+  if (b < count) {
+    try_candidate(n, lg, lh, b, eg, eh, mcw, p);  // forward: missing right
+    if (n.has_missing) {                           // backward: right = bins [b, count)
+      const uint64_t rg = n.pg - (lg - vg), rh = n.ph - (lh - vh);
+      try_candidate(n, n.tg - rg, n.th - rh, 2 * count - 1 - b, eg, eh, mcw, p);
+    }
+  }
+}
+
+// Wave argmax; the winning lane writes the full candidate and offers
+// (gain, feature) to the node's best key.
+__device__ void node_finish(const NodeEval& n, uint32_t count, const float* cuts_f, int eg, int eh,
+                            const MgbSplitParams& p, uint32_t feature, Cand* out, unsigned long long* node_best) {
+  float g = n.best_gain;
+  uint32_t o = n.best_order;
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) {
+    const float og = __shfl_xor(g, d, kWave);
+    const uint32_t oo = __shfl_xor(o, d, kWave);
+    if (og > g || (og == g && oo < o)) { g = og; o = oo; }
+  }
+  const uint32_t lane = lane_id();
+  Cand c;
+  c.parent_w = n.w;
+  c.total_h = (float)n.H;
+  c.padding = 0;
+  if (o == 0xffffffffu) {
+    if (lane != 0) return;  // no valid candidate: feature -1, gain -inf
+    c.gain = -INFINITY; c.feature = -1; c.bin = 0; c.default_left = 0; c.threshold = 0;
+    c.left_w = n.w; c.right_w = n.w; c.left_h = 0; c.right_h = 0;
+    c.lg = c.lh = c.rg = c.rh = 0;
+    *out = c;
+    return;
+  }
+  if (!(n.best_order == o && n.best_gain == g)) return;
+  const uint32_t backward = o >= count ? 1u : 0u;
+  const uint32_t b = backward ? 2 * count - 1 - o : o;
+  const uint64_t lg = n.best_lg, lh = n.best_lh, rg = n.tg - lg, rh = n.th - lh;
+  const double GL = stat_value((int64_t)lg, eg), HL = stat_value((int64_t)lh, eh);
+  const double GR = stat_value((int64_t)rg, eg), HR = stat_value((int64_t)rh, eh);
+  c.gain = g;
+  c.feature = (int32_t)feature;
+  c.bin = b;
+  c.default_left = backward;
+  c.threshold = backward ? (b == 0 ? -INFINITY : cuts_f[b - 1]) : cuts_f[b];
+  c.left_w = calc_weight(GL, HL, p);
+  c.right_w = calc_weight(GR, HR, p);
+  c.left_h = (float)HL;
+  c.right_h = (float)HR;
+  c.lg = (int64_t)lg; c.lh = (int64_t)lh; c.rg = (int64_t)rg; c.rh = (int64_t)rh;
+  *out = c;
+  atomicMax(node_best, best_key(g, feature));
+}
+
+__device__ __forceinline__ void load_pair(const int64_t* h, uint32_t bin, uint64_t& g, uint64_t& v) {
+  const int4 x = *reinterpret_cast<const int4*>(h + 2 * (uint64_t)bin);
+  g = (uint64_t)(uint32_t)x.x | ((uint64_t)(uint32_t)x.y << 32);
+  v = (uint64_t)(uint32_t)x.z | ((uint64_t)(uint32_t)x.w << 32);
+}
+
+__device__ __forceinline__ void store_pair(int64_t* h, uint32_t bin, uint64_t g, uint64_t v) {
+  *reinterpret_cast<int4*>(h + 2 * (uint64_t)bin) =
+      make_int4((int)(uint32_t)g, (int)(uint32_t)(g >> 32), (int)(uint32_t)v, (int)(uint32_t)(v >> 32));
+}
+
 __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth) {
-  const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  // Wave-uniform from here on: node and feature values live in scalar registers.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
   const uint32_t lane = lane_id();
   const LevelState* st = t.state;
   const uint32_t n = st->n_nodes;
-  const uint32_t F = t.cols, B1 = t.bins1;
+  const uint32_t F = t.cols, B1 = t.bins1, MB = t.max_bin;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
+  const float mcw = fabsf(t.sp.min_child_weight);
   const Frontier* fr = t.frontier[depth & 1];
   int64_t* cur = t.hist[depth & 1];
   if (depth == 0) {
     if (wave >= F) return;
-    const uint32_t f = wave;
+    const uint32_t f = wave, count = t.counts[f];
     const int64_t* h = cur + (uint64_t)f * B1 * 2;
-    int64_t hg[K], hh[K];
-    uint64_t sg = 0, shv = 0;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      uint32_t b = lane * K + k;
-      hg[k] = b < B1 ? h[2 * b] : 0;
-      hh[k] = b < B1 ? h[2 * b + 1] : 0;
-      sg += (uint64_t)hg[k];
-      shv += (uint64_t)hh[k];
+    // Root totals: every bin of the feature, missing slot included.
+    uint64_t sg = 0, sh = 0;
+    for (uint32_t b = lane; b < count; b += kWave) {
+      uint64_t g, v;
+      load_pair(h, b, g, v);
+      sg += g; sh += v;
     }
-    // Root total: present + missing of this feature (equal for all features).
-    int64_t total_g = (int64_t)wave_sum_u64(sg), total_h = (int64_t)wave_sum_u64(shv);
-    evaluate_node<K>(hg, hh, t.counts[f], total_g, total_h, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f,
-                     t.cands + f, t.best);
+    uint64_t mg, mh;
+    load_pair(h, MB, mg, mh);
+    NodeEval e;
+    node_begin(e, wave_sum_u64(sg) + mg, wave_sum_u64(sh) + mh, mg, mh, eg, eh, t.sp);
+    for (uint32_t base = 0; base < count; base += kWave) {
+      const uint32_t b = base + lane;
+      uint64_t g = 0, v = 0;
+      if (b < count) load_pair(h, b, g, v);
+      scan_chunk(e, g, v, b, count, eg, eh, mcw, t.sp);
+    }
+    node_finish(e, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f, t.cands + f, t.best);
     return;
   }
   const uint32_t pairs = n / 2;
@@ -541,34 +601,39 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
   const uint32_t pair = wave / F, f = wave % F;
   const Frontier a = fr[2 * pair], b = fr[2 * pair + 1];
   const uint32_t built = a.built ? 2 * pair : 2 * pair + 1, other = built ^ 1u;
+  const Frontier& fb = a.built ? a : b;
+  const Frontier& fo = a.built ? b : a;
   const int64_t* parent = t.hist[(depth - 1) & 1] + ((uint64_t)a.parent_slot * F + f) * B1 * 2;
   const int64_t* xb = cur + ((uint64_t)built * F + f) * B1 * 2;
   int64_t* ob = cur + ((uint64_t)other * F + f) * B1 * 2;
   const bool store_other = depth + 1 < t.max_depth;
-  int64_t xg[K], xh[K], og[K], oh[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    uint32_t bb = lane * K + k;
-    if (bb < B1) {
-      xg[k] = xb[2 * bb]; xh[k] = xb[2 * bb + 1];
-      og[k] = (int64_t)((uint64_t)parent[2 * bb] - (uint64_t)xg[k]);
-      oh[k] = (int64_t)((uint64_t)parent[2 * bb + 1] - (uint64_t)xh[k]);
-      if (store_other) {
-        ob[2 * bb] = og[k];
-        ob[2 * bb + 1] = oh[k];
-      }
-    } else {
-      xg[k] = xh[k] = og[k] = oh[k] = 0;
-    }
-  }
-  const Frontier& fb = built == 2 * pair ? a : b;
-  const Frontier& fo = built == 2 * pair ? b : a;
-  const float* cuts_f = t.cuts + (uint64_t)f * t.cut_stride;
   const uint32_t count = t.counts[f];
-  evaluate_node<K>(xg, xh, count, fb.sum_g, fb.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f,
-                   t.best + built);
-  evaluate_node<K>(og, oh, count, fo.sum_g, fo.sum_h, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f,
-                   t.best + other);
+  // Missing slots first: they give each child's present-bin totals.
+  uint64_t pmg, pmh, xmg, xmh;
+  load_pair(parent, MB, pmg, pmh);
+  load_pair(xb, MB, xmg, xmh);
+  const uint64_t omg = pmg - xmg, omh = pmh - xmh;
+  if (store_other && lane == 0) store_pair(ob, MB, omg, omh);
+  NodeEval ex, eo;
+  node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
+  node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
+  for (uint32_t base = 0; base < count; base += kWave) {
+    const uint32_t bin = base + lane;
+    uint64_t xg = 0, xh = 0, og = 0, oh = 0;
+    if (bin < count) {
+      uint64_t pg, ph;
+      load_pair(parent, bin, pg, ph);
+      load_pair(xb, bin, xg, xh);
+      og = pg - xg;
+      oh = ph - xh;
+      if (store_other) store_pair(ob, bin, og, oh);
+    }
+    scan_chunk(ex, xg, xh, bin, count, eg, eh, mcw, t.sp);
+    scan_chunk(eo, og, oh, bin, count, eg, eh, mcw, t.sp);
+  }
+  const float* cuts_f = t.cuts + (uint64_t)f * t.cut_stride;
+  node_finish(ex, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f, t.best + built);
+  node_finish(eo, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f, t.best + other);
 }
 
 // ---------------------------------------------------------------------------
@@ -577,16 +642,28 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
 // pop/apply, :1663-1717 replay).  One workgroup handles the whole level in
 // node-id order, so child ids follow XGBoost's numbering.
 // ---------------------------------------------------------------------------
-__device__ void ordered_sum(const int64_t* fh, uint32_t first, uint32_t steps, bool reverse, uint32_t count, int eg,
-                            int eh, double* g, double* h) {
+// Serial binary64 sums of `steps` bins of a feature staged in LDS (forward
+// from bin 0, or backward from bin count-1), in the reference's order.
+__device__ void ordered_sum(const double* sg, const double* sh, uint32_t steps, bool reverse, uint32_t count,
+                            double* g, double* h) {
   double a = 0, b = 0;
   for (uint32_t s = 0; s < steps; ++s) {
-    uint32_t bin = reverse ? count - s - 1 : first + s;
-    a += stat_value(fh[2 * bin], eg);
-    b += stat_value(fh[2 * bin + 1], eh);
+    uint32_t bin = reverse ? count - s - 1 : s;
+    a += sg[bin];
+    b += sh[bin];
   }
   *g = a;
   *h = b;
+}
+
+constexpr uint32_t kMaxBins1 = 1088;  // max_bin + 1 for max_bin <= 1087
+
+// Stage feature f's bins as binary64 statistics: out[0][b] = g, out[1][b] = h.
+__device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh, double (*out)[kMaxBins1]) {
+  for (uint32_t b = threadIdx.x; b < count; b += blockDim.x) {
+    out[0][b] = stat_value(fh[2 * b], eg);
+    out[1][b] = stat_value(fh[2 * b + 1], eh);
+  }
 }
 
 __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t depth) {
@@ -600,6 +677,17 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
   const uint32_t node_base = st->node_count;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const MgbSplitParams& p = t.sp;
+  // Dense root: feature 0 and the chosen feature staged in LDS by all threads
+  // so the serial ordered sums below read LDS, not scattered global words.
+  __shared__ double root0[2][kMaxBins1], rootf[2][kMaxBins1];
+  const bool dense_root = depth == 0 && t.dense && n > 0;
+  if (dense_root) {
+    const uint64_t key = t.best[0];
+    const uint32_t f = key ? ~(uint32_t)key : 0u;
+    stage_feature(t.hist[0], t.counts[0], eg, eh, root0);
+    stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, t.counts[f], eg, eh, rootf);
+    __syncthreads();
+  }
   uint32_t carry_expanded = 0, carry_tasks = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
     const uint32_t i = base + threadIdx.x;
@@ -618,13 +706,12 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
       total_h = best.total_h;
       expand = best.feature >= 0 && best.gain > 1.0e-6f && best.gain >= p.min_split_loss &&
                depth < t.max_depth;
-      if (depth == 0 && t.dense) {
+      if (dense_root) {
         // Dense root: ordered binary64 sums of feature 0's bins, and of the
         // chosen child's bin range (kernels/scalar_root.metal.h:1-105).
-        const int64_t* hist = t.hist[0];
         const uint32_t c0 = t.counts[0];
         double tg, th;
-        ordered_sum(hist, 0, c0, false, c0, eg, eh, &tg, &th);
+        ordered_sum(root0[0], root0[1], c0, false, c0, &tg, &th);
         parent_w = calc_weight(tg, th, p);
         total_h = (float)th;
         if (best.feature >= 0) {
@@ -642,7 +729,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
             steps = bin < count ? count - bin : 0;
           }
           double cg, ch;
-          ordered_sum(hist + (uint64_t)f * t.bins1 * 2, 0, steps, best.default_left != 0, count, eg, eh, &cg, &ch);
+          ordered_sum(rootf[0], rootf[1], steps, best.default_left != 0, count, &cg, &ch);
           double og = tg - cg, oh = th - ch;
           double ag = cg + og, ah = ch + oh;
           applied_w = calc_weight(ag, ah, p);
@@ -697,9 +784,13 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         op.right_leaf = r.leaf;
         op.child_slot = 2 * rank;
         if (!final_level) {
+          // Both children carry the parent's segment until the next level's
+          // plan splits it at the partition's final left cursor.
+          t.cursors[2 * i] = node.begin;
+          t.cursors[2 * i + 1] = node.begin + node.count;
           Frontier lf, rf;
-          lf.id = left; lf.begin = 0; lf.count = 0; lf.parent_slot = i; lf.sum_g = best.lg; lf.sum_h = best.lh;
-          lf.built = 0; lf.padding = 0;
+          lf.id = left; lf.begin = node.begin; lf.count = node.count; lf.parent_slot = i; lf.sum_g = best.lg;
+          lf.sum_h = best.lh; lf.built = 0; lf.first_task = 0; lf.ntiles = 0; lf.padding = 0;
           rf = lf;
           rf.id = right; rf.sum_g = best.rg; rf.sum_h = best.rh;
           next[2 * rank] = lf;
@@ -757,45 +848,24 @@ __device__ __forceinline__ void load_tile_rows(const uint32_t* rows, const PartT
   }
 }
 
+// One workgroup per tile of up to kPartTile rows of one node.  A split node's
+// left rows fill its segment upwards from the start and its right rows
+// downwards from the end: each tile claims its ranges with one atomic on
+// each of the node's two cursors, then writes ranks (chunk, wave, lane) into
+// them.  The order of rows inside a child depends on which tile claims first;
+// nothing downstream depends on it (histograms are exact integer sums and the
+// margin update is per row).
 template <typename BinT, bool IDENTITY>
-__global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t depth) {
-  __shared__ uint32_t partial[kPartThreads / kWave];
-  const LevelState* st = t.state;
-  const uint32_t ntasks = st->n_part_tasks;
-  const uint32_t* rows = t.rows[depth & 1];
-  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
-    const PartTask task = t.part_tasks[w];
-    const NodeOp op = t.ops[task.slot];
-    if (op.op != kOpSplit) continue;
-    uint32_t row[kPartPer];
-    bool active[kPartPer];
-    load_tile_rows<IDENTITY>(rows, task, row, active);
-    uint32_t c = 0;
-#pragma unroll
-    for (int k = 0; k < kPartPer; ++k) c += (active[k] && goes_left<BinT>(t, op, row[k])) ? 1u : 0u;
-    uint64_t sum = wave_sum_u64(c);
-    if (lane_id() == 0) partial[threadIdx.x / kWave] = (uint32_t)sum;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t s = 0;
-      for (uint32_t k = 0; k < blockDim.x / kWave; ++k) s += partial[k];
-      t.part_counts[w] = s;
-    }
-    __syncthreads();
-  }
-}
-
-template <typename BinT, bool IDENTITY>
-__global__ __launch_bounds__(kPartThreads) void k_part_scatter(Tree t, uint32_t depth) {
-  __shared__ uint32_t wave_left[kPartThreads / kWave];
-  __shared__ uint32_t sums[2];
+__global__ __launch_bounds__(kPartThreads) void k_partition(Tree t, uint32_t depth) {
+  constexpr uint32_t kWaves = kPartThreads / kWave;
+  __shared__ uint32_t wave_left[kPartPer][kWaves], wave_active[kPartPer][kWaves];
+  __shared__ uint32_t base_left, base_right;
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part_tasks;
   const uint32_t* rows = t.rows[depth & 1];
   uint32_t* out = t.rows[(depth + 1) & 1];
-  const Frontier* fr = t.frontier[depth & 1];
-  Frontier* next = t.frontier[(depth + 1) & 1];
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
     const PartTask task = t.part_tasks[w];
     const NodeOp op = t.ops[task.slot];
@@ -818,67 +888,44 @@ __global__ __launch_bounds__(kPartThreads) void k_part_scatter(Tree t, uint32_t 
         if (active[k]) t.margin[row[k]] = t.margin[row[k]] + (flag[k] ? op.left_leaf : op.right_leaf);
       continue;
     }
-    // Left rows of earlier tiles of this node, and of the whole node.
-    if (threadIdx.x < 2) sums[threadIdx.x] = 0;
-    __syncthreads();
-    uint32_t before = 0, all = 0;
-    for (uint32_t k = threadIdx.x; k < task.ntasks; k += blockDim.x) {
-      uint32_t c = t.part_counts[task.first + k];
-      all += c;
-      if (task.first + k < w) before += c;
-    }
-    uint64_t sb = wave_sum_u64(before), sa = wave_sum_u64(all);
-    if (lane == 0) {
-      atomicAdd(&sums[0], (uint32_t)sb);
-      atomicAdd(&sums[1], (uint32_t)sa);
-    }
-    __syncthreads();
-    const Frontier node = fr[task.slot];
-    uint32_t left_before = sums[0];
-    const uint32_t left_total = sums[1];
-    uint32_t right_before = (task.begin - node.begin) - left_before;
+    uint32_t lrank[kPartPer], arank[kPartPer];
 #pragma unroll
     for (int k = 0; k < kPartPer; ++k) {
-      const uint32_t chunk = task.begin + k * kPartThreads;
-      if (chunk >= task.end) break;
-      const bool act = active[k];
-      const uint32_t rowk = row[k];
-      const bool left = flag[k];
-      const uint64_t lmask = __ballot(act && left);
-      const uint64_t amask = __ballot(act);
-      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-      const uint32_t lrank = (uint32_t)__popcll(lmask & below);
-      const uint32_t arank = (uint32_t)__popcll(amask & below);
-      if (lane == 0) wave_left[wave] = (uint32_t)__popcll(lmask);
-      __syncthreads();
-      uint32_t wl_before = 0, wa_before = 0, chunk_left = 0;
-      for (uint32_t q = 0; q < kPartThreads / kWave; ++q) {
-        uint32_t wl = wave_left[q];
-        if (q < wave) wl_before += wl;
-        chunk_left += wl;
+      const uint64_t lmask = __ballot(flag[k]);
+      const uint64_t amask = __ballot(active[k]);
+      lrank[k] = (uint32_t)__popcll(lmask & below);
+      arank[k] = (uint32_t)__popcll(amask & below);
+      if (lane == 0) {
+        wave_left[k][wave] = (uint32_t)__popcll(lmask);
+        wave_active[k][wave] = (uint32_t)__popcll(amask);
       }
-      wa_before = wave * kWave;  // all lanes of earlier waves are active except in the last chunk
-      const uint32_t active_in_chunk = (task.end - chunk) < kPartThreads ? task.end - chunk : kPartThreads;
-      if (act) {
-        if (left) {
-          out[node.begin + left_before + wl_before + lrank] = rowk;
-        } else {
-          uint32_t rrank = (wa_before - wl_before) + (arank - lrank);
-          out[node.begin + left_total + right_before + rrank] = rowk;
-        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t tl = 0, ta = 0;
+      for (int k = 0; k < kPartPer; ++k)
+        for (uint32_t q = 0; q < kWaves; ++q) { tl += wave_left[k][q]; ta += wave_active[k][q]; }
+      base_left = atomicAdd(&t.cursors[2 * task.slot], tl);
+      base_right = atomicSub(&t.cursors[2 * task.slot + 1], ta - tl) - (ta - tl);
+    }
+    __syncthreads();
+    uint32_t done_left = 0, done_active = 0;  // rows of earlier chunks
+#pragma unroll
+    for (int k = 0; k < kPartPer; ++k) {
+      uint32_t wl = 0, wa = 0, cl = 0, ca = 0;
+      for (uint32_t q = 0; q < kWaves; ++q) {
+        const uint32_t l = wave_left[k][q], a = wave_active[k][q];
+        if (q < wave) { wl += l; wa += a; }
+        cl += l; ca += a;
       }
-      left_before += chunk_left;
-      right_before += active_in_chunk - chunk_left;
-      __syncthreads();
+      if (active[k]) {
+        if (flag[k]) out[base_left + done_left + wl + lrank[k]] = row[k];
+        else out[base_right + (done_active - done_left) + (wa - wl) + (arank[k] - lrank[k])] = row[k];
+      }
+      done_left += cl;
+      done_active += ca;
     }
-    if (w == task.first && threadIdx.x == 0) {
-      Frontier* l = next + op.child_slot;
-      Frontier* r = l + 1;
-      l->begin = node.begin;
-      l->count = left_total;
-      r->begin = node.begin + left_total;
-      r->count = node.count - left_total;
-    }
+    __syncthreads();
   }
 }
 
@@ -886,7 +933,7 @@ __global__ __launch_bounds__(kPartThreads) void k_part_scatter(Tree t, uint32_t 
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, cands, best, ops, hist_tasks, zero, part_tasks, part_counts, partials, total;
+  size_t state, rows, hist, frontier, cands, best, ops, hist_tasks, zero, part_tasks, cursors, partials, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -911,7 +958,7 @@ Layout layout(const MgbTreeShape& s) {
   L.hist_tasks = off; off = align_up(off + (size_t)L.max_hist_tasks * sizeof(HistTask));
   L.zero = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint32_t));
   L.part_tasks = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(PartTask));
-  L.part_counts = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
+  L.cursors = off; off = align_up(off + (size_t)(2 * 2 * L.slots) * sizeof(uint32_t));
   {
     const uint64_t groups = div_up(s.cols, s.features_per_group);
     L.partials = off;
@@ -960,32 +1007,18 @@ int dispatch_hist(const Tree& t, uint32_t depth, uint32_t grid) {
 
 int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
   uint32_t blocks = div_up(items ? items : 1, kSplitThreads / kWave);
-  uint32_t k = div_up(t.bins1, kWave);
-  if (k <= 1) hipLaunchKernelGGL(k_split<1>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
-  else if (k <= 2) hipLaunchKernelGGL(k_split<2>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
-  else if (k <= 5) hipLaunchKernelGGL(k_split<5>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
-  else if (k <= 9) hipLaunchKernelGGL(k_split<9>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
-  else if (k <= 17) hipLaunchKernelGGL(k_split<17>, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
-  else {
-    set_error("max_bin above 1087 is not supported by the split kernel");
-    return -1;
-  }
+  hipLaunchKernelGGL(k_split, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
   MGB_LAUNCH_CHECK("k_split");
   return 0;
 }
 
 template <typename BinT>
 int launch_partition(const Tree& t, uint32_t depth, uint32_t grid) {
-  if (depth == 0) {
-    hipLaunchKernelGGL((k_part_count<BinT, true>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
-    MGB_LAUNCH_CHECK("k_part_count");
-    hipLaunchKernelGGL((k_part_scatter<BinT, true>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
-  } else {
-    hipLaunchKernelGGL((k_part_count<BinT, false>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
-    MGB_LAUNCH_CHECK("k_part_count");
-    hipLaunchKernelGGL((k_part_scatter<BinT, false>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
-  }
-  MGB_LAUNCH_CHECK("k_part_scatter");
+  if (depth == 0)
+    hipLaunchKernelGGL((k_partition<BinT, true>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
+  else
+    hipLaunchKernelGGL((k_partition<BinT, false>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
+  MGB_LAUNCH_CHECK("k_partition");
   return 0;
 }
 
@@ -1028,7 +1061,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.hist_tasks = reinterpret_cast<HistTask*>(ws + L.hist_tasks);
   t.zero_list = reinterpret_cast<uint32_t*>(ws + L.zero);
   t.part_tasks = reinterpret_cast<PartTask*>(ws + L.part_tasks);
-  t.part_counts = reinterpret_cast<uint32_t*>(ws + L.part_counts);
+  t.cursors = reinterpret_cast<uint32_t*>(ws + L.cursors);
   t.partials = reinterpret_cast<int64_t*>(ws + L.partials);
   t.rows_n = s->rows; t.cols = s->cols; t.max_bin = m->max_bin; t.bins1 = m->max_bin + 1;
   t.row_stride = m->row_stride; t.bin_bytes = m->bin_bytes; t.missing_code = m->missing_code;
