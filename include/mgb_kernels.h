@@ -104,10 +104,10 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
                       uint32_t* any_missing);
 
 /* ---- gradients -------------------------------------------------------- */
-/* Words of the exact-mass accumulator: 2 x 256 u64 mantissa sums per binary32
- * exponent (|g| then |h|), a completion counter and padding.  Zero it once;
- * every call below leaves it zeroed again. */
-#define MGB_MASS_WORDS 520
+/* Words of the gradient-mass scratch of mgb_gradients / mgb_gradient_mass:
+ * per-workgroup exact partial sums of |g| and |h| and a completion counter.
+ * Zero it once; every call leaves the counter zeroed again. */
+#define MGB_MASS_WORDS 5640
 /* Objective gradients (kernels/boost.metal:553-601) written as float2 (g, h),
  * the exact |g|, |h| mass (kernels/gradient_quantization.metal.h:4-24) and,
  * from it, the power-of-two fixed-point scales[2]
@@ -116,7 +116,8 @@ int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labe
                   float* grad, uint64_t* mass, float* scales);
 /* Mass and scales of caller-provided gradients (custom objectives). */
 int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales);
-/* Scales from an already accumulated mass[0..511]; clears mass. */
+/* Scales from 2 x 256 u64 mantissa sums per binary32 exponent (|g| then |h|)
+ * in mass[0..511]; clears them. */
 int mgb_gradient_scales(uint64_t* mass, float* scales);
 /* Weighted label mean (src/learner.cpp:316-333): out[0] = binary32 mean. */
 int mgb_base_score(const float* labels, const float* weights, uint32_t rows, uint32_t objective,

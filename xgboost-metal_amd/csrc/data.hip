@@ -63,41 +63,58 @@ __device__ __forceinline__ void mass_bucket(float v, uint32_t& bucket, uint64_t&
 }
 
 constexpr uint32_t kGradThreads = 1024;
-constexpr uint32_t kLimbs = 11;     // 352 bits > 255 + 56 bits of the largest exact sum
-constexpr uint32_t kTicket = 512;   // completion counter word of the mass buffer
+constexpr uint32_t kGradBlocks = 256;  // at most; one partial per workgroup
+constexpr uint32_t kLimbs = 11;        // 352 bits > 255 + 56 bits of the largest exact sum
+constexpr uint32_t kTicket = 2 * kLimbs * kGradBlocks;  // completion counter word of the mass buffer
+static_assert(kTicket < MGB_MASS_WORDS, "mass buffer too small");
 
-// scale = 2^(62 - max(0, bitlen(sum) - 149)); gradient_quantization.metal.h:52-63.
-// staged[q*256 + j] = S_j of quantity q (0: |g|, 1: |h|), sum = sum_j S_j 2^j.
-// Carry-save: thread (q, w) adds the 32-bit pieces that land in limb w (each
-// S_j < 2^56 shifted by j % 32 spans limbs j/32 .. j/32+2; at most 96
-// exponents reach one limb, so the u64 lane sum cannot overflow); one thread
-// per quantity then propagates the carries.  Exact, as a serial add would be.
-__device__ void scales_from_mass(const uint64_t* staged, uint64_t* limbs, float* scales) {
-  const uint32_t tid = threadIdx.x;
-  if (tid < 2 * kLimbs) {
-    const uint32_t q = tid / kLimbs, w = tid % kLimbs;
-    const uint64_t* s = staged + q * 256;
-    const uint32_t jlo = w >= 2 ? 32 * (w - 2) : 0, jhi = 32 * (w + 1) < 256 ? 32 * (w + 1) : 256;
-    uint64_t acc = 0;
-    for (uint32_t j = jlo; j < jhi; ++j) {
-      const uint64_t v = s[j];
-      const uint32_t shift = j % 32, part = w - j / 32;
-      const uint64_t lo = v << shift, hi = shift ? (v >> (64 - shift)) : 0;
-      acc += part == 0 ? (uint32_t)lo : part == 1 ? (uint32_t)(lo >> 32) : (uint32_t)hi;
-    }
-    limbs[tid] = acc;
+// Carry-save limbs of sum_j S_j 2^j for both quantities: limbs[q*11 + w]
+// receives the 32-bit pieces of every S_j << (j % 32) that land in limb w
+// (S_j < 2^56 spans limbs j/32 .. j/32+2).  staged[q*256 + j] = S_j of
+// quantity q (0: |g|, 1: |h|).  Thread t < 512 takes bucket (t / 256, t % 256);
+// the 32 buckets sharing j/32 are one half-wave, which sums its pieces with
+// shuffles (each sum < 2^37) and adds them to three limbs.  limbs must be
+// zero on entry; blockDim.x >= 512.  Ends with a barrier.
+__device__ void block_carry_save(const uint64_t* staged, uint64_t* limbs) {
+  const uint32_t t = threadIdx.x;
+  uint64_t p0 = 0, p1 = 0, p2 = 0;
+  if (t < 512) {
+    const uint64_t v = staged[t];
+    const uint32_t shift = t % 32;
+    const uint64_t lo = v << shift, hi = shift ? (v >> (64 - shift)) : 0;
+    p0 = (uint32_t)lo; p1 = (uint32_t)(lo >> 32); p2 = (uint32_t)hi;
+  }
+#pragma unroll
+  for (int d = 16; d > 0; d >>= 1) {
+    p0 += __shfl_xor(p0, d, kWave);
+    p1 += __shfl_xor(p1, d, kWave);
+    p2 += __shfl_xor(p2, d, kWave);
+  }
+  if (t < 512 && t % 32 == 0) {
+    const uint32_t q = t / 256, w = (t % 256) / 32;
+    atomicAdd((unsigned long long*)&limbs[q * kLimbs + w], (unsigned long long)p0);
+    atomicAdd((unsigned long long*)&limbs[q * kLimbs + w + 1], (unsigned long long)p1);
+    atomicAdd((unsigned long long*)&limbs[q * kLimbs + w + 2], (unsigned long long)p2);
   }
   __syncthreads();
+}
+
+// scale = 2^(62 - max(0, bitlen(sum) - 149)); gradient_quantization.metal.h:52-63.
+// limbs: carry-save limbs of both sums (any entries below 2^63); threads 0
+// and 1 propagate the carries, exactly as a serial big-integer add would.
+__device__ void scales_from_limbs(const uint64_t* limbs, float* scales) {
+  const uint32_t tid = threadIdx.x;
   if (tid < 2) {
-    uint32_t limb[kLimbs];
+    uint32_t limb[kLimbs + 1];
     uint64_t carry = 0;
     for (uint32_t w = 0; w < kLimbs; ++w) {
-      const uint64_t v = limbs[tid * kLimbs + w] + carry;
+      const uint64_t v = (limbs[tid * kLimbs + w] & 0xffffffffull) + carry;
       limb[w] = (uint32_t)v;
-      carry = v >> 32;
+      carry = (v >> 32) + (limbs[tid * kLimbs + w] >> 32);
     }
+    limb[kLimbs] = (uint32_t)carry;
     int exponent = 0;
-    for (int w = kLimbs - 1; w >= 0; --w) {
+    for (int w = kLimbs; w >= 0; --w) {
       if (limb[w]) {
         const int bitlen = w * 32 + 32 - __clz(limb[w]);
         exponent = bitlen - 149 > 0 ? bitlen - 149 : 0;
@@ -108,37 +125,60 @@ __device__ void scales_from_mass(const uint64_t* staged, uint64_t* limbs, float*
   }
 }
 
-// Per-workgroup exponent buckets in LDS, one device atomic per non-empty
-// bucket, then the last workgroup to finish (completion counter) turns the
-// global buckets into the scales and leaves the buffer zeroed for the next
-// call.  Every access to the shared buckets and the counter is a
-// device-scope atomic.  The bucket adds return their old values and the
-// workgroup waits for them (the values feed an LDS store) before its counter
-// increment: a returned value means the add has been performed at the
-// device's point of coherence, so the last workgroup's atomic loads see every
-// add, without an agent-scope fence (which would write back the whole L2).
+// Per-workgroup exponent buckets in LDS, reduced to 22 carry-save limbs and
+// published to the workgroup's own slot of the mass buffer; the last
+// workgroup to finish (completion counter) sums the slots and writes the
+// scales.  Every cross-workgroup access is a device-scope atomic: the slot
+// writes are exchanges whose returned values the workgroup waits for (they
+// feed an LDS store) before its counter increment, so they have been
+// performed at the device's point of coherence when the counter moves --
+// without an agent-scope fence, which would write back the whole L2.  No two
+// workgroups touch the same word except the counter.
 __device__ void mass_flush_and_scale(uint64_t* local, uint64_t* mass, float* scales) {
   __shared__ uint64_t limbs[2 * kLimbs];
+  constexpr uint32_t kShare = 32;                  // threads per limb in the final sum
+  constexpr uint32_t kPer = kGradBlocks / kShare;  // slots per thread, loaded together
+  __shared__ uint64_t partial[2 * kLimbs][kShare];
   __shared__ uint32_t last;
   __shared__ volatile uint64_t sink;
+  const uint32_t tid = threadIdx.x;
+  if (tid < 2 * kLimbs) limbs[tid] = 0;
   __syncthreads();
-  uint64_t seen = 0;
-  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x)
-    if (local[i]) seen |= __hip_atomic_fetch_add(&mass[i], local[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  sink = seen;
+  block_carry_save(local, limbs);
+  if (tid < 2 * kLimbs)
+    sink = __hip_atomic_exchange(&mass[(uint64_t)blockIdx.x * 2 * kLimbs + tid], limbs[tid], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (threadIdx.x == 0)
+  if (tid == 0)
     last = __hip_atomic_fetch_add(&mass[kTicket], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
            (uint64_t)(gridDim.x - 1);
   __syncthreads();
   if (!last) return;
-  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) {
-    local[i] = __hip_atomic_load(&mass[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&mass[i], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // kShare threads per limb, each loading its kPer workgroup slots at once.
+  if (tid < 2 * kLimbs * kShare) {
+    const uint32_t l = tid / kShare, part = tid % kShare;
+    uint64_t v[kPer];
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+      const uint32_t b = part + k * kShare;
+      v[k] = b < gridDim.x ? __hip_atomic_load(&mass[(uint64_t)b * 2 * kLimbs + l], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)
+                           : 0;
+    }
+    uint64_t acc = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) acc += v[k];
+    partial[l][part] = acc;
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&mass[kTicket], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(&mass[kTicket], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  scales_from_mass(local, limbs, scales);
+  if (tid < 2 * kLimbs) {
+    uint64_t acc = 0;
+    for (uint32_t k = 0; k < kShare; ++k) acc += partial[tid][k];
+    limbs[tid] = acc;
+  }
+  __syncthreads();
+  scales_from_limbs(limbs, scales);
 }
 
 __device__ __forceinline__ void mass_add(uint64_t* local, float g, float h) {
@@ -193,8 +233,10 @@ __global__ void k_gradient_scales(uint64_t* __restrict__ mass, float* __restrict
   __shared__ uint64_t staged[512];
   __shared__ uint64_t limbs[2 * kLimbs];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) staged[i] = mass[i];
+  if (threadIdx.x < 2 * kLimbs) limbs[threadIdx.x] = 0;
   __syncthreads();
-  scales_from_mass(staged, limbs, scales);
+  block_carry_save(staged, limbs);
+  scales_from_limbs(limbs, scales);
   __syncthreads();
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) mass[i] = 0;
 }
@@ -328,8 +370,7 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
 
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
                   float* grad, uint64_t* mass, float* scales) {
-  if (!p->rows) return mgb_gradient_scales(mass, scales);
-  uint32_t grid = grid_for(p->rows, kGradThreads, 256);
+  uint32_t grid = grid_for(p->rows, kGradThreads, kGradBlocks);
   prof_begin(MGB_PROF_GRADIENT);
   hipLaunchKernelGGL(k_gradients, dim3(grid), dim3(kGradThreads), 0, stream(), *p, margin, labels, weights,
                      (float2*)grad, mass, scales);
@@ -339,8 +380,7 @@ int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labe
 }
 
 int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales) {
-  if (!rows) return mgb_gradient_scales(mass, scales);
-  uint32_t grid = grid_for(rows, kGradThreads, 256);
+  uint32_t grid = grid_for(rows, kGradThreads, kGradBlocks);
   prof_begin(MGB_PROF_GRADIENT);
   hipLaunchKernelGGL(k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, stream(), (const float2*)grad, rows, mass,
                      scales);
@@ -351,7 +391,7 @@ int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* s
 
 int mgb_gradient_scales(uint64_t* mass, float* scales) {
   prof_begin(MGB_PROF_GRADIENT);
-  hipLaunchKernelGGL(k_gradient_scales, dim3(1), dim3(256), 0, stream(), mass, scales);
+  hipLaunchKernelGGL(k_gradient_scales, dim3(1), dim3(512), 0, stream(), mass, scales);
   prof_end(MGB_PROF_GRADIENT);
   MGB_LAUNCH_CHECK("k_gradient_scales");
   return 0;

@@ -32,24 +32,43 @@ void prof_end(int kind);
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
-// Inclusive wave64 prefix sum of a 32-bit value.
+// Wave64 inclusive prefix sums with DPP lane moves (no LDS round trip).
+// Within each row of 16 lanes: row_shr 1, 2, 4, 8 (lanes whose source lies
+// before the row start keep the identity 0).  Across rows: row_bcast:15 adds
+// lane 15's (then lane 47's) total to rows 1 and 3, row_bcast:31 adds lane
+// 31's total to rows 2 and 3.  Call with every lane of the wave active.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, kRowMask, 0xf, false);
+}
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint64_t dpp_move64(uint64_t v) {
+  const uint32_t lo = dpp_move<kCtrl, kRowMask>((uint32_t)v);
+  const uint32_t hi = dpp_move<kCtrl, kRowMask>((uint32_t)(v >> 32));
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
 __device__ __forceinline__ uint32_t wave_inclusive_u32(uint32_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    uint32_t other = __shfl_up(v, d, kWave);
-    if (lane >= (uint32_t)d) v += other;
-  }
+  v += dpp_move<kRowShr1, 0xf>(v);
+  v += dpp_move<kRowShr2, 0xf>(v);
+  v += dpp_move<kRowShr4, 0xf>(v);
+  v += dpp_move<kRowShr8, 0xf>(v);
+  v += dpp_move<kRowBcast15, 0xa>(v);
+  v += dpp_move<kRowBcast31, 0xc>(v);
   return v;
 }
 
 __device__ __forceinline__ uint64_t wave_inclusive_u64(uint64_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    uint64_t other = __shfl_up(v, d, kWave);
-    if (lane >= (uint32_t)d) v += other;
-  }
+  v += dpp_move64<kRowShr1, 0xf>(v);
+  v += dpp_move64<kRowShr2, 0xf>(v);
+  v += dpp_move64<kRowShr4, 0xf>(v);
+  v += dpp_move64<kRowShr8, 0xf>(v);
+  v += dpp_move64<kRowBcast15, 0xa>(v);
+  v += dpp_move64<kRowBcast31, 0xc>(v);
   return v;
 }
 

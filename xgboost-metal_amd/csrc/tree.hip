@@ -22,7 +22,6 @@ constexpr uint32_t kPartTile = 1024;      // rows per partition task
 constexpr uint32_t kSelectThreads = 1024;
 constexpr uint32_t kHistThreads = 1024;
 constexpr int kHistUnroll = 4;          // rows in flight per thread
-constexpr uint32_t kSplitThreads = 256;   // four waves, one (node pair, feature) each
 
 enum : uint32_t { kOpNone = 0, kOpLeaf = 1, kOpSplit = 2, kOpFinal = 3 };
 
@@ -117,6 +116,19 @@ struct Tree {
 
 __host__ __device__ inline uint32_t div_up(uint64_t a, uint32_t b) { return (uint32_t)((a + b - 1) / b); }
 
+// Index of the batch item that owns task j: the last k < nitems with
+// off[k] <= j, where off holds the items' ascending exclusive task offsets in
+// LDS (items without tasks share their successor's offset).
+__device__ __forceinline__ uint32_t owner_of(const uint32_t* off, uint32_t nitems, uint32_t j) {
+  uint32_t lo = 0, hi = nitems;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (off[mid] <= j) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
 // ---------------------------------------------------------------------------
 // Scoring arithmetic (native binary64 restatement of the reference's
 // software-binary64 scorer).
@@ -201,6 +213,7 @@ __global__ void k_level0(Tree t) {
 // left child, kernels/boost.metal:661-698); the other comes from subtraction.
 __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth) {
   __shared__ uint32_t scan[kSelectThreads / kWave + 1];
+  __shared__ uint32_t s_off[kSelectThreads], s_slot[kSelectThreads], s_begin[kSelectThreads], s_end[kSelectThreads];
   LevelState* st = t.state;
   Frontier* fr = t.frontier[depth & 1];
   uint32_t pairs = st->n_nodes / 2;
@@ -231,10 +244,19 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     uint32_t zoff = block_exclusive_u32(zero, scan, &total_zero) + carry_zero;
     block_exclusive_u32(count, scan, &total_rows);
     carry_rows += total_rows;
-    for (uint32_t k = 0; k < tiles; ++k) {
-      uint32_t b = begin + k * t.rows_per_tile;
-      uint32_t e = b + t.rows_per_tile < begin + count ? b + t.rows_per_tile : begin + count;
-      t.hist_tasks[off + k] = HistTask{built, b, e, tiles == 1 ? 1u : 0u};
+    // Row tiles of this batch's built nodes, written by the whole block.
+    s_off[threadIdx.x] = off - carry_tasks;
+    s_slot[threadIdx.x] = built;
+    s_begin[threadIdx.x] = begin;
+    s_end[threadIdx.x] = begin + count;
+    __syncthreads();
+    const uint32_t nitems = pairs - base < blockDim.x ? pairs - base : blockDim.x;
+    for (uint32_t j = threadIdx.x; j < total_tasks; j += blockDim.x) {
+      const uint32_t k = owner_of(s_off, nitems, j);
+      const uint32_t b = s_begin[k] + (j - s_off[k]) * t.rows_per_tile;
+      const uint32_t e = b + t.rows_per_tile < s_end[k] ? b + t.rows_per_tile : s_end[k];
+      const uint32_t ntiles = (k + 1 < nitems ? s_off[k + 1] : total_tasks) - s_off[k];
+      t.hist_tasks[carry_tasks + j] = HistTask{s_slot[k], b, e, ntiles == 1 ? 1u : 0u};
     }
     if (p < pairs) {
       fr[built].first_task = off;
@@ -243,6 +265,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     if (zero) t.zero_list[zoff] = built;
     carry_tasks += total_tasks;
     carry_zero += total_zero;
+    __syncthreads();
   }
   if (threadIdx.x == 0) {
     st->n_hist_tasks = carry_tasks;
@@ -426,29 +449,22 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
 
 // ---------------------------------------------------------------------------
 // Split evaluation (kernels/boost.metal:902-1005, scalar_parallel.metal.h).
-// One wave per (node pair, feature).  The wave walks the feature's bins
-// [0, count) in chunks of 64, one bin per lane: it subtracts the built child
-// from the parent (mod 2^64), stores the sibling for the next level, and
-// extends exact int64 prefix sums of both children with a wave64 scan.  Each
-// lane keeps its best candidate as (gain, order, left sums) only; the lane
-// that wins the wave argmax rebuilds the full candidate at the end.  Order is
-// b for the forward pass (missing right) and 2*count-1-b for the backward
-// pass (missing left): the maximum gain with the smallest order is the
-// reference's first strictly greater candidate.  The sums over present bins
-// come from the node total minus the missing slot (bin max_bin), so one pass
-// suffices.
+// One workgroup of W waves per (node pair, feature); wave c takes bins
+// [64c, 64c+64) of the feature's [0, count), one bin per lane, so every load
+// of the feature is in flight at once.  Each lane subtracts the built child
+// from the parent (mod 2^64) and stores the sibling for the next level; wave64
+// scans plus the earlier waves' chunk totals (exchanged in LDS) give exact
+// int64 prefix sums of both children.  Each lane keeps its best candidate as
+// (gain, order, left sums) only; the winner of the workgroup argmax rebuilds
+// the full candidate.  Order is b for the forward pass (missing right) and
+// 2*count-1-b for the backward pass (missing left): the maximum gain with the
+// smallest order is the reference's first strictly greater candidate.  The
+// sums over present bins are the node total minus the missing slot (bin
+// max_bin), so one pass over the bins suffices below the root.
 // ---------------------------------------------------------------------------
-// Lane 63's value, read into scalar registers (wave-uniform).
-__device__ __forceinline__ uint64_t lane63(uint64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, kWave - 1);
-  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), kWave - 1);
-  return (uint64_t)lo | ((uint64_t)hi << 32);
-}
-
 struct NodeEval {
   uint64_t tg, th;        // node totals (present + missing)
   uint64_t pg, ph;        // present-bin totals
-  uint64_t carry_g, carry_h;  // prefix of the chunks already scanned
   double G, H;
   float w, parent_gain;
   bool has_missing;
@@ -463,7 +479,6 @@ __device__ __forceinline__ void node_begin(NodeEval& n, uint64_t tg, uint64_t th
   n.tg = tg; n.th = th;
   n.pg = tg - mg; n.ph = th - mh;
   n.has_missing = mg != 0 || mh != 0;
-  n.carry_g = n.carry_h = 0;
   n.G = stat_value((int64_t)tg, eg);
   n.H = stat_value((int64_t)th, eh);
   n.w = calc_weight(n.G, n.H, p);
@@ -489,26 +504,26 @@ __device__ __forceinline__ void try_candidate(NodeEval& n, uint64_t lg, uint64_t
   }
 }
 
-// Bins of one chunk (v = this lane's bin, zero past count).
-__device__ __forceinline__ void scan_chunk(NodeEval& n, uint64_t vg, uint64_t vh, uint32_t b, uint32_t count, int eg,
-                                           int eh, float mcw, const MgbSplitParams& p) {
-  const uint64_t ig = wave_inclusive_u64(vg), ih = wave_inclusive_u64(vh);
-  const uint64_t lg = n.carry_g + ig, lh = n.carry_h + ih;  // bins [0, b]
-  n.carry_g += lane63(ig);
-  n.carry_h += lane63(ih);
-  if (b < count) {
-    try_candidate(n, lg, lh, b, eg, eh, mcw, p);  // forward: missing right
-    if (n.has_missing) {                           // backward: right = bins [b, count)
-      const uint64_t rg = n.pg - (lg - vg), rh = n.ph - (lh - vh);
-      try_candidate(n, n.tg - rg, n.th - rh, 2 * count - 1 - b, eg, eh, mcw, p);
-    }
+// Candidates at this lane's bin b: v = the bin's (g, h), (lg, lh) = exact
+// sums of bins [0, b].
+__device__ __forceinline__ void eval_bin(NodeEval& n, uint64_t vg, uint64_t vh, uint64_t lg, uint64_t lh, uint32_t b,
+                                         uint32_t count, int eg, int eh, float mcw, const MgbSplitParams& p) {
+  if (b >= count) return;
+  try_candidate(n, lg, lh, b, eg, eh, mcw, p);  // forward: missing right
+  if (n.has_missing) {                           // backward: right = bins [b, count)
+    const uint64_t rg = n.pg - (lg - vg), rh = n.ph - (lh - vh);
+    try_candidate(n, n.tg - rg, n.th - rh, 2 * count - 1 - b, eg, eh, mcw, p);
   }
 }
 
-// Wave argmax; the winning lane writes the full candidate and offers
-// (gain, feature) to the node's best key.
-__device__ void node_finish(const NodeEval& n, uint32_t count, const float* cuts_f, int eg, int eh,
-                            const MgbSplitParams& p, uint32_t feature, Cand* out, unsigned long long* node_best) {
+// Per-wave best of one node, parked in LDS for the workgroup argmax.
+struct WaveBest {
+  float gain;
+  uint32_t order;
+  uint64_t lg, lh;
+};
+
+__device__ __forceinline__ void wave_best(const NodeEval& n, WaveBest* slot) {
   float g = n.best_gain;
   uint32_t o = n.best_order;
 #pragma unroll
@@ -517,37 +532,50 @@ __device__ void node_finish(const NodeEval& n, uint32_t count, const float* cuts
     const uint32_t oo = __shfl_xor(o, d, kWave);
     if (og > g || (og == g && oo < o)) { g = og; o = oo; }
   }
-  const uint32_t lane = lane_id();
+  if (o == 0xffffffffu) {
+    if (lane_id() == 0) *slot = WaveBest{-INFINITY, 0xffffffffu, 0, 0};
+  } else if (n.best_order == o && n.best_gain == g) {
+    *slot = WaveBest{g, o, n.best_lg, n.best_lh};
+  }
+}
+
+// One thread: argmax over the waves' bests, then the full candidate.
+__device__ void node_finish(const NodeEval& n, const WaveBest* waves, uint32_t nwaves, uint32_t count,
+                            const float* cuts_f, int eg, int eh, const MgbSplitParams& p, uint32_t feature, Cand* out,
+                            unsigned long long* node_best) {
+  WaveBest b = waves[0];
+  for (uint32_t k = 1; k < nwaves; ++k) {
+    const WaveBest o = waves[k];
+    if (o.gain > b.gain || (o.gain == b.gain && o.order < b.order)) b = o;
+  }
   Cand c;
   c.parent_w = n.w;
   c.total_h = (float)n.H;
   c.padding = 0;
-  if (o == 0xffffffffu) {
-    if (lane != 0) return;  // no valid candidate: feature -1, gain -inf
+  if (b.order == 0xffffffffu) {  // no valid candidate: feature -1, gain -inf
     c.gain = -INFINITY; c.feature = -1; c.bin = 0; c.default_left = 0; c.threshold = 0;
     c.left_w = n.w; c.right_w = n.w; c.left_h = 0; c.right_h = 0;
     c.lg = c.lh = c.rg = c.rh = 0;
     *out = c;
     return;
   }
-  if (!(n.best_order == o && n.best_gain == g)) return;
-  const uint32_t backward = o >= count ? 1u : 0u;
-  const uint32_t b = backward ? 2 * count - 1 - o : o;
-  const uint64_t lg = n.best_lg, lh = n.best_lh, rg = n.tg - lg, rh = n.th - lh;
-  const double GL = stat_value((int64_t)lg, eg), HL = stat_value((int64_t)lh, eh);
+  const uint32_t backward = b.order >= count ? 1u : 0u;
+  const uint32_t bin = backward ? 2 * count - 1 - b.order : b.order;
+  const uint64_t rg = n.tg - b.lg, rh = n.th - b.lh;
+  const double GL = stat_value((int64_t)b.lg, eg), HL = stat_value((int64_t)b.lh, eh);
   const double GR = stat_value((int64_t)rg, eg), HR = stat_value((int64_t)rh, eh);
-  c.gain = g;
+  c.gain = b.gain;
   c.feature = (int32_t)feature;
-  c.bin = b;
+  c.bin = bin;
   c.default_left = backward;
-  c.threshold = backward ? (b == 0 ? -INFINITY : cuts_f[b - 1]) : cuts_f[b];
+  c.threshold = backward ? (bin == 0 ? -INFINITY : cuts_f[bin - 1]) : cuts_f[bin];
   c.left_w = calc_weight(GL, HL, p);
   c.right_w = calc_weight(GR, HR, p);
   c.left_h = (float)HL;
   c.right_h = (float)HR;
-  c.lg = (int64_t)lg; c.lh = (int64_t)lh; c.rg = (int64_t)rg; c.rh = (int64_t)rh;
+  c.lg = (int64_t)b.lg; c.lh = (int64_t)b.lh; c.rg = (int64_t)rg; c.rh = (int64_t)rh;
   *out = c;
-  atomicMax(node_best, best_key(g, feature));
+  atomicMax(node_best, best_key(b.gain, feature));
 }
 
 __device__ __forceinline__ void load_pair(const int64_t* h, uint32_t bin, uint64_t& g, uint64_t& v) {
@@ -561,44 +589,90 @@ __device__ __forceinline__ void store_pair(int64_t* h, uint32_t bin, uint64_t g,
       make_int4((int)(uint32_t)g, (int)(uint32_t)(g >> 32), (int)(uint32_t)v, (int)(uint32_t)(v >> 32));
 }
 
-__global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth) {
-  // Wave-uniform from here on: node and feature values live in scalar registers.
-  const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+// A wave-uniform 64-bit value moved to scalar registers.
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// Exclusive prefix (over waves < wave) and total of the chunk sums in LDS,
+// kept in scalar registers.
+__device__ __forceinline__ void wave_carry(const uint64_t (*tot)[4], uint32_t nwaves, uint32_t wave, uint64_t (&pre)[4],
+                                           uint64_t (&all)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) pre[q] = all[q] = 0;
+  for (uint32_t k = 0; k < nwaves; ++k) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint64_t v = uniform_u64(tot[k][q]);
+      if (k < wave) pre[q] += v;
+      all[q] += v;
+    }
+  }
+}
+
+template <int W>
+__global__ __launch_bounds__(W * kWave) void k_split(Tree t, uint32_t depth) {
+  __shared__ uint64_t tot[W][4];
+  __shared__ WaveBest best[2][W];
+  __shared__ uint64_t root_sum[W][2];
+  const uint32_t item = blockIdx.x;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t lane = lane_id();
   const LevelState* st = t.state;
-  const uint32_t n = st->n_nodes;
   const uint32_t F = t.cols, B1 = t.bins1, MB = t.max_bin;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const float mcw = fabsf(t.sp.min_child_weight);
-  const Frontier* fr = t.frontier[depth & 1];
   int64_t* cur = t.hist[depth & 1];
+  constexpr uint32_t span = W * kWave;  // bins per pass of the workgroup
   if (depth == 0) {
-    if (wave >= F) return;
-    const uint32_t f = wave, count = t.counts[f];
+    if (item >= F) return;
+    const uint32_t f = item, count = t.counts[f];
     const int64_t* h = cur + (uint64_t)f * B1 * 2;
     // Root totals: every bin of the feature, missing slot included.
     uint64_t sg = 0, sh = 0;
-    for (uint32_t b = lane; b < count; b += kWave) {
+    for (uint32_t b = threadIdx.x; b < count; b += span) {
       uint64_t g, v;
       load_pair(h, b, g, v);
       sg += g; sh += v;
     }
+    sg = wave_sum_u64(sg);
+    sh = wave_sum_u64(sh);
+    if (lane == 0) { root_sum[wave][0] = sg; root_sum[wave][1] = sh; }
+    __syncthreads();
     uint64_t mg, mh;
     load_pair(h, MB, mg, mh);
+    uint64_t tg = mg, th = mh;
+    for (uint32_t k = 0; k < W; ++k) { tg += uniform_u64(root_sum[k][0]); th += uniform_u64(root_sum[k][1]); }
     NodeEval e;
-    node_begin(e, wave_sum_u64(sg) + mg, wave_sum_u64(sh) + mh, mg, mh, eg, eh, t.sp);
-    for (uint32_t base = 0; base < count; base += kWave) {
-      const uint32_t b = base + lane;
+    node_begin(e, tg, th, mg, mh, eg, eh, t.sp);
+    uint64_t carry_g = 0, carry_h = 0;
+    for (uint32_t base = 0; base < count; base += span) {
+      const uint32_t b = base + wave * kWave + lane;
       uint64_t g = 0, v = 0;
       if (b < count) load_pair(h, b, g, v);
-      scan_chunk(e, g, v, b, count, eg, eh, mcw, t.sp);
+      const uint64_t ig = wave_inclusive_u64(g), ih = wave_inclusive_u64(v);
+      if (lane == kWave - 1) { tot[wave][0] = ig; tot[wave][1] = ih; tot[wave][2] = 0; tot[wave][3] = 0; }
+      __syncthreads();
+      uint64_t pre[4], all[4];
+      wave_carry(tot, W, wave, pre, all);
+      eval_bin(e, g, v, carry_g + pre[0] + ig, carry_h + pre[1] + ih, b, count, eg, eh, mcw, t.sp);
+      carry_g += all[0];
+      carry_h += all[1];
+      __syncthreads();
     }
-    node_finish(e, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f, t.cands + f, t.best);
+    wave_best(e, &best[0][wave]);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      node_finish(e, best[0], W, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f, t.cands + f, t.best);
     return;
   }
+  const uint32_t n = st->n_nodes;
   const uint32_t pairs = n / 2;
-  if (wave >= pairs * F) return;
-  const uint32_t pair = wave / F, f = wave % F;
+  if (item >= pairs * F) return;
+  const uint32_t pair = item / F, f = item % F;
+  const Frontier* fr = t.frontier[depth & 1];
   const Frontier a = fr[2 * pair], b = fr[2 * pair + 1];
   const uint32_t built = a.built ? 2 * pair : 2 * pair + 1, other = built ^ 1u;
   const Frontier& fb = a.built ? a : b;
@@ -613,12 +687,13 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
   load_pair(parent, MB, pmg, pmh);
   load_pair(xb, MB, xmg, xmh);
   const uint64_t omg = pmg - xmg, omh = pmh - xmh;
-  if (store_other && lane == 0) store_pair(ob, MB, omg, omh);
+  if (store_other && threadIdx.x == 0) store_pair(ob, MB, omg, omh);
   NodeEval ex, eo;
   node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
   node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
-  for (uint32_t base = 0; base < count; base += kWave) {
-    const uint32_t bin = base + lane;
+  uint64_t carry[4] = {0, 0, 0, 0};
+  for (uint32_t base = 0; base < count; base += span) {
+    const uint32_t bin = base + wave * kWave + lane;
     uint64_t xg = 0, xh = 0, og = 0, oh = 0;
     if (bin < count) {
       uint64_t pg, ph;
@@ -628,12 +703,27 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
       oh = ph - xh;
       if (store_other) store_pair(ob, bin, og, oh);
     }
-    scan_chunk(ex, xg, xh, bin, count, eg, eh, mcw, t.sp);
-    scan_chunk(eo, og, oh, bin, count, eg, eh, mcw, t.sp);
+    const uint64_t ixg = wave_inclusive_u64(xg), ixh = wave_inclusive_u64(xh);
+    const uint64_t iog = wave_inclusive_u64(og), ioh = wave_inclusive_u64(oh);
+    if (lane == kWave - 1) { tot[wave][0] = ixg; tot[wave][1] = ixh; tot[wave][2] = iog; tot[wave][3] = ioh; }
+    __syncthreads();
+    uint64_t pre[4], all[4];
+    wave_carry(tot, W, wave, pre, all);
+    eval_bin(ex, xg, xh, carry[0] + pre[0] + ixg, carry[1] + pre[1] + ixh, bin, count, eg, eh, mcw, t.sp);
+    eval_bin(eo, og, oh, carry[2] + pre[2] + iog, carry[3] + pre[3] + ioh, bin, count, eg, eh, mcw, t.sp);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) carry[q] += all[q];
+    __syncthreads();
   }
+  wave_best(ex, &best[0][wave]);
+  wave_best(eo, &best[1][wave]);
+  __syncthreads();
   const float* cuts_f = t.cuts + (uint64_t)f * t.cut_stride;
-  node_finish(ex, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f, t.best + built);
-  node_finish(eo, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f, t.best + other);
+  // Threads 0 and 1 finish the two children (both exist for every W).
+  if (threadIdx.x == 0)
+    node_finish(ex, best[0], W, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f, t.best + built);
+  else if (threadIdx.x == 1)
+    node_finish(eo, best[1], W, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f, t.best + other);
 }
 
 // ---------------------------------------------------------------------------
@@ -647,6 +737,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_split(Tree t, uint32_t depth)
 __device__ void ordered_sum(const double* sg, const double* sh, uint32_t steps, bool reverse, uint32_t count,
                             double* g, double* h) {
   double a = 0, b = 0;
+#pragma unroll 16
   for (uint32_t s = 0; s < steps; ++s) {
     uint32_t bin = reverse ? count - s - 1 : s;
     a += sg[bin];
@@ -668,6 +759,7 @@ __device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh,
 
 __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t depth) {
   __shared__ uint32_t scan[kSelectThreads / kWave + 1];
+  __shared__ uint32_t s_off[kSelectThreads], s_begin[kSelectThreads], s_end[kSelectThreads];
   LevelState* st = t.state;
   const uint32_t n = st->n_nodes;
   const uint32_t F = t.cols;
@@ -704,8 +796,8 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
       best = t.cands[(uint64_t)i * F + f];
       parent_w = best.parent_w;
       total_h = best.total_h;
-      expand = best.feature >= 0 && best.gain > 1.0e-6f && best.gain >= p.min_split_loss &&
-               depth < t.max_depth;
+      expand = best.feature >= 0 && (uint32_t)best.feature < F && best.gain > 1.0e-6f &&
+               best.gain >= p.min_split_loss && depth < t.max_depth;
       if (dense_root) {
         // Dense root: ordered binary64 sums of feature 0's bins, and of the
         // chosen child's bin range (kernels/scalar_root.metal.h:1-105).
@@ -714,7 +806,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         ordered_sum(root0[0], root0[1], c0, false, c0, &tg, &th);
         parent_w = calc_weight(tg, th, p);
         total_h = (float)th;
-        if (best.feature >= 0) {
+        if (best.feature >= 0 && (uint32_t)best.feature < F) {
           const uint32_t f = (uint32_t)best.feature, count = t.counts[f];
           const float* column = t.cuts + (uint64_t)f * t.cut_stride;
           uint32_t lo = 0, hi = count;
@@ -798,17 +890,28 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         }
       }
       t.ops[i] = op;
-      for (uint32_t k = 0; k < tiles; ++k) {
-        uint32_t b = node.begin + k * kPartTile;
-        uint32_t e = b + kPartTile < node.begin + node.count ? b + kPartTile : node.begin + node.count;
-        PartTask task;
-        task.slot = i; task.begin = b; task.end = e; task.first = toff; task.ntasks = tiles;
-        task.padding[0] = task.padding[1] = task.padding[2] = 0;
-        t.part_tasks[toff + k] = task;
-      }
+    }
+    // Partition tiles of this batch's nodes, written by the whole block.
+    s_off[threadIdx.x] = toff - carry_tasks;
+    s_begin[threadIdx.x] = valid ? node.begin : 0;
+    s_end[threadIdx.x] = valid ? node.begin + node.count : 0;
+    __syncthreads();
+    const uint32_t nitems = n - base < blockDim.x ? n - base : blockDim.x;
+    for (uint32_t j = threadIdx.x; j < total_tasks; j += blockDim.x) {
+      const uint32_t k = owner_of(s_off, nitems, j);
+      const uint32_t b = s_begin[k] + (j - s_off[k]) * kPartTile;
+      PartTask task;
+      task.slot = base + k;
+      task.begin = b;
+      task.end = b + kPartTile < s_end[k] ? b + kPartTile : s_end[k];
+      task.first = carry_tasks + s_off[k];
+      task.ntasks = (k + 1 < nitems ? s_off[k + 1] : total_tasks) - s_off[k];
+      task.padding[0] = task.padding[1] = task.padding[2] = 0;
+      t.part_tasks[carry_tasks + j] = task;
     }
     carry_expanded += total_expanded;
     carry_tasks += total_tasks;
+    __syncthreads();
   }
   if (threadIdx.x == 0) {
     st->node_count = node_base + 2 * carry_expanded;
@@ -1005,9 +1108,22 @@ int dispatch_hist(const Tree& t, uint32_t depth, uint32_t grid) {
   return -1;
 }
 
+// Waves per split workgroup: enough for max_bin bins in one pass, at most 16.
+uint32_t split_waves(uint32_t max_bin) {
+  uint32_t w = 1;
+  while (w < 16 && w * kWave < max_bin) w *= 2;
+  return w;
+}
+
 int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
-  uint32_t blocks = div_up(items ? items : 1, kSplitThreads / kWave);
-  hipLaunchKernelGGL(k_split, dim3(blocks), dim3(kSplitThreads), 0, stream(), t, depth);
+  const dim3 grid(items ? items : 1);
+  switch (split_waves(t.max_bin)) {
+    case 1: hipLaunchKernelGGL(k_split<1>, grid, dim3(kWave), 0, stream(), t, depth); break;
+    case 2: hipLaunchKernelGGL(k_split<2>, grid, dim3(2 * kWave), 0, stream(), t, depth); break;
+    case 4: hipLaunchKernelGGL(k_split<4>, grid, dim3(4 * kWave), 0, stream(), t, depth); break;
+    case 8: hipLaunchKernelGGL(k_split<8>, grid, dim3(8 * kWave), 0, stream(), t, depth); break;
+    default: hipLaunchKernelGGL(k_split<16>, grid, dim3(16 * kWave), 0, stream(), t, depth); break;
+  }
   MGB_LAUNCH_CHECK("k_split");
   return 0;
 }
