@@ -371,28 +371,22 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
                   float* grad, uint64_t* mass, float* scales) {
   uint32_t grid = grid_for(p->rows, kGradThreads, kGradBlocks);
-  prof_begin(MGB_PROF_GRADIENT);
-  hipLaunchKernelGGL(k_gradients, dim3(grid), dim3(kGradThreads), 0, stream(), *p, margin, labels, weights,
-                     (float2*)grad, mass, scales);
-  prof_end(MGB_PROF_GRADIENT);
+  launch(MGB_PROF_GRADIENT, k_gradients, dim3(grid), dim3(kGradThreads), 0, *p, margin, labels, weights,
+         (float2*)grad, mass, scales);
   MGB_LAUNCH_CHECK("k_gradients");
   return 0;
 }
 
 int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales) {
   uint32_t grid = grid_for(rows, kGradThreads, kGradBlocks);
-  prof_begin(MGB_PROF_GRADIENT);
-  hipLaunchKernelGGL(k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, stream(), (const float2*)grad, rows, mass,
-                     scales);
-  prof_end(MGB_PROF_GRADIENT);
+  launch(MGB_PROF_GRADIENT, k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, (const float2*)grad, rows, mass,
+         scales);
   MGB_LAUNCH_CHECK("k_gradient_mass");
   return 0;
 }
 
 int mgb_gradient_scales(uint64_t* mass, float* scales) {
-  prof_begin(MGB_PROF_GRADIENT);
-  hipLaunchKernelGGL(k_gradient_scales, dim3(1), dim3(512), 0, stream(), mass, scales);
-  prof_end(MGB_PROF_GRADIENT);
+  launch(MGB_PROF_GRADIENT, k_gradient_scales, dim3(1), dim3(512), 0, mass, scales);
   MGB_LAUNCH_CHECK("k_gradient_scales");
   return 0;
 }
@@ -441,10 +435,8 @@ int mgb_transform(float* data, uint64_t count, uint32_t objective) {
 int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode* nodes, const uint32_t* offsets,
                 uint32_t trees, float* margin) {
   if (!rows || !trees) return 0;
-  prof_begin(MGB_PROF_PREDICT);
-  hipLaunchKernelGGL(k_predict, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), X, rows, cols, nodes, offsets,
-                     trees, margin);
-  prof_end(MGB_PROF_PREDICT);
+  launch(MGB_PROF_PREDICT, k_predict, dim3(grid_for(rows, 256)), dim3(256), 0, X, rows, cols, nodes, offsets, trees,
+         margin);
   MGB_LAUNCH_CHECK("k_predict");
   return 0;
 }

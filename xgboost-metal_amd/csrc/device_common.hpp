@@ -1,6 +1,7 @@
 // Shared device helpers for the gfx950 kernels (wave64, LDS scans, error
 // reporting).  Included only by .hip translation units.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -26,9 +27,23 @@ int check(hipError_t status, const char* what);
     if (::mgb::check(hipGetLastError(), name) != 0) return -1; \
   } while (0)
 
-// Profiling brackets around launches (no-ops unless mgb_profile_enable(1)).
-void prof_begin(int kind);
-void prof_end(int kind);
+// Per-kernel-class timing (mgb_profile_enable).  When it is on, a launch
+// through launch() records start and stop timestamps of the dispatch itself
+// (hipExtLaunchKernelGGL events), so the time is the kernel's own duration
+// with no marker packets between launches.
+bool prof_events(int kind, hipEvent_t* begin, hipEvent_t* end);
+void prof_record(int kind, hipEvent_t begin, hipEvent_t end);
+
+template <typename... P, typename... A>
+void launch(int kind, void (*fn)(P...), dim3 grid, dim3 block, uint32_t lds, A... args) {
+  hipEvent_t begin = nullptr, end = nullptr;
+  if (prof_events(kind, &begin, &end)) {
+    hipExtLaunchKernelGGL(fn, grid, block, lds, stream(), begin, end, 0u, args...);
+    prof_record(kind, begin, end);
+  } else {
+    hipLaunchKernelGGL(fn, grid, block, lds, stream(), args...);
+  }
+}
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 

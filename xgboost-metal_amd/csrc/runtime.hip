@@ -25,7 +25,6 @@ struct Profile {
   std::vector<hipEvent_t> free_events;
   struct Pending { int kind; hipEvent_t begin, end; };
   std::vector<Pending> pending;
-  hipEvent_t open[MGB_PROF_KINDS] = {};
   double ms[MGB_PROF_KINDS] = {};
   uint64_t launches[MGB_PROF_KINDS] = {};
   hipEvent_t take() {
@@ -39,19 +38,18 @@ Profile g_profile;
 
 hipStream_t stream() { return g_stream; }
 
-void prof_begin(int kind) {
-  if (!g_profile.on || kind < 0 || kind >= MGB_PROF_KINDS) return;
-  hipEvent_t e = g_profile.take();
-  if (e && hipEventRecord(e, g_stream) == hipSuccess) g_profile.open[kind] = e;
+bool prof_events(int kind, hipEvent_t* begin, hipEvent_t* end) {
+  if (!g_profile.on || kind < 0 || kind >= MGB_PROF_KINDS) return false;
+  *begin = g_profile.take();
+  *end = g_profile.take();
+  if (*begin && *end) return true;
+  if (*begin) g_profile.free_events.push_back(*begin);
+  if (*end) g_profile.free_events.push_back(*end);
+  return false;
 }
 
-void prof_end(int kind) {
-  if (!g_profile.on || kind < 0 || kind >= MGB_PROF_KINDS || !g_profile.open[kind]) return;
-  hipEvent_t e = g_profile.take();
-  if (e && hipEventRecord(e, g_stream) == hipSuccess)
-    g_profile.pending.push_back({kind, g_profile.open[kind], e});
-  g_profile.open[kind] = nullptr;
-}
+void prof_record(int kind, hipEvent_t begin, hipEvent_t end) { g_profile.pending.push_back({kind, begin, end}); }
+
 void set_error(std::string message) { g_error = std::move(message); }
 
 int check(hipError_t status, const char* what) {

@@ -278,33 +278,53 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
 }
 
 // Sum the row-tile partials of every multi-tile built node into its histogram
-// slot: entry (feature f, bin b) adds partial[(task * groups + f / G) * G + f % G][b]
-// over the node's tasks, in task order (exact integers, mod 2^64).
-__global__ __launch_bounds__(256) void k_reduce_hist(Tree t, uint32_t depth) {
+// slot: entry e = f * (max_bin+1) + b of the node adds partial[task][e] over
+// the node's tasks (exact integers mod 2^64, so any order gives the same
+// bits).  A block takes 64 consecutive entries of one node; its four waves
+// take every fourth tile each, four loads in flight per lane, and combine in
+// LDS.
+constexpr uint32_t kReduceWaves = 4;
+__global__ __launch_bounds__(kReduceWaves * kWave) void k_reduce_hist(Tree t, uint32_t depth) {
+  __shared__ uint64_t part[kReduceWaves][kWave][2];
   const LevelState* st = t.state;
   const uint32_t n = st->n_zero;
-  const uint32_t F = t.cols, B1 = t.bins1, G = t.features_per_group;
-  const uint64_t entries = (uint64_t)F * B1;
-  const uint64_t total = (uint64_t)n * entries;
+  const uint32_t E = t.cols * t.bins1;
+  const uint32_t eblocks = div_up(E, kWave);
   const Frontier* fr = t.frontier[depth & 1];
   int64_t* bank = t.hist[depth & 1];
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t slot = t.zero_list[i / entries];
-    const uint32_t e = (uint32_t)(i % entries);
-    const uint32_t f = e / B1, b = e % B1;
-    const Frontier node = fr[slot];
-    const uint64_t stride = (uint64_t)t.groups * G * B1 * 2;  // int64 words per task
-    const int64_t* src = t.partials + (uint64_t)node.first_task * stride + ((uint64_t)(f / G) * G + f % G) * B1 * 2 +
-                         (uint64_t)b * 2;
+  const uint64_t stride = (uint64_t)t.groups * t.features_per_group * t.bins1 * 2;  // int64 words per task
+  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (uint32_t blk = blockIdx.x; blk < n * eblocks; blk += gridDim.x) {
+    const uint32_t slot = t.zero_list[blk / eblocks];
+    const uint32_t e = (blk % eblocks) * kWave + lane;
+    const uint32_t first = fr[slot].first_task, ntiles = fr[slot].ntiles;
     uint64_t g = 0, h = 0;
-    for (uint32_t k = 0; k < node.ntiles; ++k) {
-      const int4 v = *reinterpret_cast<const int4*>(src + k * stride);
-      g += (uint64_t)(uint32_t)v.x | ((uint64_t)(uint32_t)v.y << 32);
-      h += (uint64_t)(uint32_t)v.z | ((uint64_t)(uint32_t)v.w << 32);
+    if (e < E) {
+      const int64_t* src = t.partials + (uint64_t)first * stride + (uint64_t)e * 2;
+      for (uint32_t k = wave; k < ntiles; k += 4 * kReduceWaves) {
+        int4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t kk = k + u * kReduceWaves;
+          v[u] = kk < ntiles ? *reinterpret_cast<const int4*>(src + kk * stride) : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          g += (uint64_t)(uint32_t)v[u].x | ((uint64_t)(uint32_t)v[u].y << 32);
+          h += (uint64_t)(uint32_t)v[u].z | ((uint64_t)(uint32_t)v[u].w << 32);
+        }
+      }
     }
-    int64_t* dst = bank + ((uint64_t)slot * F + f) * B1 * 2 + (uint64_t)b * 2;
-    *reinterpret_cast<int4*>(dst) = make_int4((int)(uint32_t)g, (int)(uint32_t)(g >> 32), (int)(uint32_t)h,
-                                              (int)(uint32_t)(h >> 32));
+    part[wave][lane][0] = g;
+    part[wave][lane][1] = h;
+    __syncthreads();
+    if (wave == 0 && e < E) {
+      for (uint32_t q = 1; q < kReduceWaves; ++q) { g += part[q][lane][0]; h += part[q][lane][1]; }
+      int64_t* dst = bank + (uint64_t)slot * E * 2 + (uint64_t)e * 2;
+      *reinterpret_cast<int4*>(dst) = make_int4((int)(uint32_t)g, (int)(uint32_t)(g >> 32), (int)(uint32_t)h,
+                                                (int)(uint32_t)(h >> 32));
+    }
+    __syncthreads();
   }
 }
 
@@ -1083,7 +1103,7 @@ int launch_hist(const Tree& t, uint32_t depth, bool unit, uint32_t grid) {
       set_error("hipFuncSetAttribute(histogram LDS) failed");                                         \
       return -1;                                                                                      \
     }                                                                                                 \
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(kHistThreads), lds, stream(), t, depth);                  \
+    launch(MGB_PROF_HISTOGRAM, fn, dim3(grid), dim3(kHistThreads), (uint32_t)lds, t, depth);          \
   }
   if (unit && identity) MGB_HIST_CASE(true, true)
   else if (unit) MGB_HIST_CASE(true, false)
@@ -1118,11 +1138,11 @@ uint32_t split_waves(uint32_t max_bin) {
 int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
   const dim3 grid(items ? items : 1);
   switch (split_waves(t.max_bin)) {
-    case 1: hipLaunchKernelGGL(k_split<1>, grid, dim3(kWave), 0, stream(), t, depth); break;
-    case 2: hipLaunchKernelGGL(k_split<2>, grid, dim3(2 * kWave), 0, stream(), t, depth); break;
-    case 4: hipLaunchKernelGGL(k_split<4>, grid, dim3(4 * kWave), 0, stream(), t, depth); break;
-    case 8: hipLaunchKernelGGL(k_split<8>, grid, dim3(8 * kWave), 0, stream(), t, depth); break;
-    default: hipLaunchKernelGGL(k_split<16>, grid, dim3(16 * kWave), 0, stream(), t, depth); break;
+    case 1: launch(MGB_PROF_SPLIT, k_split<1>, grid, dim3(kWave), 0, t, depth); break;
+    case 2: launch(MGB_PROF_SPLIT, k_split<2>, grid, dim3(2 * kWave), 0, t, depth); break;
+    case 4: launch(MGB_PROF_SPLIT, k_split<4>, grid, dim3(4 * kWave), 0, t, depth); break;
+    case 8: launch(MGB_PROF_SPLIT, k_split<8>, grid, dim3(8 * kWave), 0, t, depth); break;
+    default: launch(MGB_PROF_SPLIT, k_split<16>, grid, dim3(16 * kWave), 0, t, depth); break;
   }
   MGB_LAUNCH_CHECK("k_split");
   return 0;
@@ -1131,9 +1151,9 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
 template <typename BinT>
 int launch_partition(const Tree& t, uint32_t depth, uint32_t grid) {
   if (depth == 0)
-    hipLaunchKernelGGL((k_partition<BinT, true>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
+    launch(MGB_PROF_PARTITION, k_partition<BinT, true>, dim3(grid), dim3(kPartThreads), 0, t, depth);
   else
-    hipLaunchKernelGGL((k_partition<BinT, false>), dim3(grid), dim3(kPartThreads), 0, stream(), t, depth);
+    launch(MGB_PROF_PARTITION, k_partition<BinT, false>, dim3(grid), dim3(kPartThreads), 0, t, depth);
   MGB_LAUNCH_CHECK("k_partition");
   return 0;
 }
@@ -1191,11 +1211,11 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
 }
 
 uint32_t reduce_grid(const Tree& t) {
-  // Enough threads for the largest case (every row tile of one level in
-  // multi-tile nodes); the kernel strides over the real work.
-  uint64_t entries = (uint64_t)t.cols * t.bins1;
-  uint64_t blocks = (entries * 4 + 255) / 256;
-  return (uint32_t)(blocks < 1024 ? (blocks ? blocks : 1) : 1024);
+  // Blocks stride over (multi-tile node, 64-entry block) pairs; enough blocks
+  // to fill the device when one node's entries are all there is.
+  const uint64_t eblocks = div_up((uint64_t)t.cols * t.bins1, kWave);
+  const uint64_t g = eblocks * 4 < 2048 ? eblocks * 4 : 2048;
+  return (uint32_t)(g ? g : 1);
 }
 
 uint32_t hist_grid(const Tree& t) {
@@ -1223,41 +1243,26 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
   t.bins = bins; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
-  hipStream_t s = stream();
-  prof_begin(MGB_PROF_CONTROL);
-  hipLaunchKernelGGL(k_level0, dim3(1), dim3(256), 0, s, t);
-  prof_end(MGB_PROF_CONTROL);
+  launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
   const uint32_t hgrid = hist_grid(t);
   const uint32_t pgrid = 1024;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
     if (depth > 0) {
-      prof_begin(MGB_PROF_CONTROL);
-      hipLaunchKernelGGL(k_plan, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
-      prof_end(MGB_PROF_CONTROL);
+      launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
-    prof_begin(MGB_PROF_HISTOGRAM);
     if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, hgrid) : dispatch_hist<uint16_t>(t, depth, hgrid)))
       return -1;
-    prof_end(MGB_PROF_HISTOGRAM);
-    prof_begin(MGB_PROF_REDUCE);
-    hipLaunchKernelGGL(k_reduce_hist, dim3(reduce_grid(t)), dim3(256), 0, s, t, depth);
-    prof_end(MGB_PROF_REDUCE);
+    launch(MGB_PROF_REDUCE, k_reduce_hist, dim3(reduce_grid(t)), dim3(kReduceWaves * kWave), 0, t, depth);
     MGB_LAUNCH_CHECK("k_reduce_hist");
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
-    prof_begin(MGB_PROF_SPLIT);
     if (launch_split(t, depth, items)) return -1;
-    prof_end(MGB_PROF_SPLIT);
-    prof_begin(MGB_PROF_CONTROL);
-    hipLaunchKernelGGL(k_select, dim3(1), dim3(kSelectThreads), 0, s, t, depth);
-    prof_end(MGB_PROF_CONTROL);
+    launch(MGB_PROF_CONTROL, k_select, dim3(1), dim3(kSelectThreads), 0, t, depth);
     MGB_LAUNCH_CHECK("k_select");
-    prof_begin(MGB_PROF_PARTITION);
     if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
       return -1;
-    prof_end(MGB_PROF_PARTITION);
   }
   return 0;
 }
@@ -1299,7 +1304,7 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   }
   const uint32_t grid = hist_grid(t);
   if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, grid) : dispatch_hist<uint16_t>(t, depth, grid))) return -1;
-  hipLaunchKernelGGL(k_reduce_hist, dim3(reduce_grid(t)), dim3(256), 0, s, t, depth);
+  hipLaunchKernelGGL(k_reduce_hist, dim3(reduce_grid(t)), dim3(kReduceWaves * kWave), 0, s, t, depth);
   MGB_LAUNCH_CHECK("k_reduce_hist");
   MGB_CHECK(hipMemcpyAsync(hist, t.hist[0], (size_t)L.hist_entry * sizeof(int64_t), hipMemcpyDeviceToDevice, s));
   return 0;
