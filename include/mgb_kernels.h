@@ -28,6 +28,9 @@ int mgb_free(void* ptr);
 int mgb_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int mgb_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int mgb_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Enqueued host-to-device copy; returns once src may be reused (pageable
+ * memory is staged before the call returns). */
+int mgb_memcpy_h2d_async(void* dst, const void* src, size_t bytes);
 int mgb_memset(void* dst, int value, size_t bytes);
 int mgb_synchronize(void);
 /* Event timing on the library stream (src/runtime.mm:203-280 profiler). */
@@ -63,10 +66,12 @@ typedef struct {
 } MgbMatrix;
 
 /* Per-round gradient statistics (replaces GradientParams/GradCert,
- * include/metalgb/shared.h:58-62, :110-113). */
+ * include/metalgb/shared.h:58-62, :110-113, and the uniform-sampling part of
+ * SamplingParams, :63-67).  subsample < 1 keeps a row iff its draw from the
+ * round's sample_seed is below subsample; dropped rows get (0, 0). */
 typedef struct {
-  uint32_t rows, objective, has_weight, padding;
-  float scale_pos_weight, padding1, padding2, padding3;
+  uint32_t rows, objective, has_weight, sample_seed;
+  float scale_pos_weight, subsample, padding1, padding2;
 } MgbGradParams;
 
 /* Split regularisation (replaces SplitParams, include/metalgb/shared.h:114-119). */
@@ -114,8 +119,10 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
  * (kernels/gradient_quantization.metal.h:26-67), in one launch. */
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
                   float* grad, uint64_t* mass, float* scales);
-/* Mass and scales of caller-provided gradients (custom objectives). */
-int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales);
+/* Row sampling (p->subsample < 1, applied in place), mass and scales of
+ * caller-provided gradients (custom objectives); p->objective and
+ * p->has_weight are not used. */
+int mgb_gradient_mass(const MgbGradParams* p, float* grad, uint64_t* mass, float* scales);
 /* Scales from 2 x 256 u64 mantissa sums per binary32 exponent (|g| then |h|)
  * in mass[0..511]; clears them. */
 int mgb_gradient_scales(uint64_t* mass, float* scales);
@@ -135,10 +142,13 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
  * (src/tree.cpp:455-1029 GPU-driven tree + replay :1663-1717 and the
  * prediction-cache update kernels/boost.metal:1738-1763).  Nothing is
  * synchronised; nodes (2^(max_depth+1)-1 records) and node_count are device
- * pointers filled by the time the stream drains. */
+ * pointers filled by the time the stream drains.  features (device, cols
+ * flags, may be NULL for all) restricts the split search to the tree's
+ * column sample (src/tree.cpp:179-180). */
 int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
                   const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
-                  void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes, uint32_t* node_count);
+                  const uint32_t* features, void* workspace, size_t workspace_bytes, float* margin,
+                  MgbTreeNode* nodes, uint32_t* node_count);
 
 /* Rows and nodes whose histograms each level built directly (not by
  * subtraction), from the last mgb_grow_tree on this workspace; synchronises. */

@@ -607,8 +607,7 @@ static void ordered_sum(const int64_t* fh, uint32_t first, uint32_t steps, int r
  * kernels/boost.metal:1245-1265 (select_splits). */
 static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64_t* qg, const int64_t* qh,
                           float sg, float sh, uint32_t* row_buf, uint32_t* tmp_buf, int64_t* hist,
-                          OracleNode* nodes, const float* grad_rows_unused, uint32_t* leaf_of_row) {
-  (void)grad_rows_unused;
+                          OracleNode* nodes, const uint8_t* allowed, uint32_t* leaf_of_row) {
   uint32_t max_nodes = oracle_max_nodes(p->max_depth);
   size_t stride = (size_t)(q->max_bin + 1) * 2;
   for (uint32_t i = 0; i < max_nodes; ++i) {
@@ -645,6 +644,11 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
         OracleSplit cand;
         oracle_evaluate_feature(hist + (size_t)f * stride, q->counts[f], q->cuts + (size_t)f * q->max_bin,
                                 q->minima[f], total_g, total_h, sg, sh, p, (int32_t)f, &cand);
+        if (allowed && !allowed[f]) {
+          /* A feature outside the tree's sample offers no split. */
+          cand.gain = -INFINITY;
+          cand.feature = -1;
+        }
         if (f == 0 || cand.gain > best.gain) best = cand;
       }
       float applied_weight = 0, applied_hessian = 0;
@@ -738,6 +742,90 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
   return node_count;
 }
 
+/* ---------------------------------------------------------------------------
+ * Sampling.
+ * MT19937: the published generator (Matsumoto and Nishimura, ACM TOMACS 8(1),
+ * 1998) with the C++ standard's seeding (std::mersenne_twister_engine::seed:
+ * x[i] = 1812433253 (x[i-1] ^ (x[i-1] >> 30)) + i) -- block twist of all
+ * 624 words, then tempering.  The standard fixes the 10000th output of a
+ * default-seeded (5489) engine at 4123659995.
+ * ------------------------------------------------------------------------- */
+void oracle_mt_seed(OracleMT* g, uint32_t seed) {
+  g->state[0] = seed;
+  for (uint32_t i = 1; i < 624; ++i) g->state[i] = 1812433253u * (g->state[i - 1] ^ (g->state[i - 1] >> 30)) + i;
+  g->next = 624;
+}
+
+uint32_t oracle_mt_next(OracleMT* g) {
+  if (g->next >= 624) {
+    for (uint32_t i = 0; i < 624; ++i) {
+      uint32_t y = (g->state[i] & 0x80000000u) | (g->state[(i + 1) % 624] & 0x7fffffffu);
+      g->state[i] = g->state[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+    }
+    g->next = 0;
+  }
+  uint32_t y = g->state[g->next++];
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  y ^= y >> 18;
+  return y;
+}
+
+/* kernels/sampling.metal.h:1-30: the row's engine state is the round seed
+ * times 16807^(row+1) modulo 2^63 (a multiplicative generator stepped row+1
+ * times); the row is kept when the canonical binary64 draw
+ * RN53(state - 1) / 2^63 (libc++ bernoulli_distribution over a 63-bit engine)
+ * is below subsample.  For subsample < 2^-39 the comparison is made in
+ * binary32, as the reference does. */
+int oracle_sample_row(uint32_t seed, uint32_t row, float subsample) {
+  const uint64_t mask = 0x7fffffffffffffffull;
+  uint64_t state = seed ? seed : 1u, factor = 16807u;
+  for (uint64_t e = (uint64_t)row + 1; e; e >>= 1) {
+    if (e & 1) state = (state * factor) & mask;
+    factor = (factor * factor) & mask;
+  }
+  uint64_t numerator = state - 1;
+  /* Round to 53 significant bits, ties to even (the int -> binary64 conversion). */
+  double rounded = (double)numerator;
+  float limit = subsample * 0x1p63f;
+  if (limit < 0x1p24f) return (float)rounded < limit;
+  return rounded < (double)limit;
+}
+
+/* src/tree.cpp:28-45 with libc++'s std::shuffle (as the reference models it,
+ * kernels/tree_sample_columns.metal.h): a fresh engine seeded with `seed`,
+ * Fisher-Yates from the front where position pos swaps with pos + u, u drawn
+ * uniformly from [0, n - pos) by masking engine outputs to the bit width of
+ * n - pos - 1 and rejecting values >= n - pos.  The first
+ * max(1, floor(n * fraction)) features (binary32 product) are kept, sorted. */
+uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, uint32_t* out) {
+  for (uint32_t i = 0; i < n; ++i) out[i] = i;
+  if (!(fraction < 1.0f) || n == 0) return n;
+  float scaled = floorf((float)n * fraction);
+  uint32_t keep = scaled < 1.0f ? 1u : (uint32_t)scaled;
+  if (keep > n) keep = n;
+  OracleMT g;
+  oracle_mt_seed(&g, seed);
+  for (uint32_t pos = 0; pos < keep && pos + 1 < n; ++pos) {
+    uint32_t range = n - pos;
+    uint32_t width = 32u - (uint32_t)__builtin_clz(range - 1u);
+    uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
+    uint32_t u;
+    do u = oracle_mt_next(&g) & mask; while (u >= range);
+    uint32_t tmp = out[pos];
+    out[pos] = out[pos + u];
+    out[pos + u] = tmp;
+  }
+  /* Sort the kept prefix (insertion sort; n is a feature count). */
+  for (uint32_t i = 1; i < keep; ++i) {
+    uint32_t v = out[i], j = i;
+    while (j > 0 && out[j - 1] > v) { out[j] = out[j - 1]; --j; }
+    out[j] = v;
+  }
+  return keep;
+}
+
 static int has_nan(const float* X, size_t n) {
   for (size_t i = 0; i < n; ++i) if (isnan(X[i])) return 1;
   return 0;
@@ -787,6 +875,16 @@ int oracle_train(const float* X, uint32_t rows, uint32_t cols, const float* labe
   uint32_t* leaf_of_row = (uint32_t*)malloc((size_t)rows * sizeof(uint32_t) + 4);
   int64_t* hist = (int64_t*)malloc((size_t)cols * (hist_bins + 1) * 2 * sizeof(int64_t));
   uint32_t max_nodes = oracle_max_nodes(p->max_depth);
+  /* The learner's engine: default state (seed 5489) unless a nonzero seed
+   * parameter reseeds it (src/learner.cpp:94-103). */
+  OracleMT rng;
+  oracle_mt_seed(&rng, p->seed ? p->seed : 5489u);
+  /* Row sampling runs when floor(float(rows) * subsample) < rows (src/learner.cpp:679). */
+  double subsample = p->subsample > 0 ? (double)p->subsample : 1.0;
+  int sampling = (uint64_t)((double)(float)rows * subsample) < (uint64_t)rows;
+  int colsample = p->colsample_bytree > 0 && p->colsample_bytree < 1.0f;
+  uint8_t* allowed = colsample ? (uint8_t*)malloc(cols) : NULL;
+  uint32_t* features = colsample ? (uint32_t*)malloc((size_t)cols * sizeof(uint32_t)) : NULL;
   for (uint32_t t = 0; t < rounds; ++t) {
     if (custom_grad) {
       memcpy(grad, custom_grad + (size_t)t * rows, (size_t)rows * sizeof(float));
@@ -794,13 +892,26 @@ int oracle_train(const float* X, uint32_t rows, uint32_t cols, const float* labe
     } else {
       oracle_gradients(p->objective, margin, labels, weights, rows, p->scale_pos_weight, grad, hess);
     }
+    if (sampling) {
+      /* src/sampling.cpp:11-74: one engine draw seeds the round; dropped rows
+       * carry a zero gradient pair (and so add nothing to any histogram). */
+      uint32_t seed = oracle_mt_next(&rng);
+      for (uint32_t r = 0; r < rows; ++r)
+        if (!oracle_sample_row(seed, r, p->subsample)) grad[r] = hess[r] = 0.0f;
+    }
+    if (colsample) {
+      uint32_t keep = oracle_sample_columns(cols, p->colsample_bytree, oracle_mt_next(&rng), features);
+      memset(allowed, 0, cols);
+      for (uint32_t i = 0; i < keep; ++i) allowed[features[i]] = 1;
+    }
     float sg = oracle_gradient_scale(grad, rows), sh = oracle_gradient_scale(hess, rows);
     oracle_quantize_gradients(grad, hess, rows, sg, sh, qg, qh);
     OracleNode* nodes = trees + (size_t)t * max_nodes;
-    tree_sizes[t] = grow_tree(&q, p, qg, qh, sg, sh, row_buf, tmp_buf, hist, nodes, NULL, leaf_of_row);
+    tree_sizes[t] = grow_tree(&q, p, qg, qh, sg, sh, row_buf, tmp_buf, hist, nodes, allowed, leaf_of_row);
     /* Prediction-cache update: kernels/boost.metal:1738-1763, one float add per row. */
     for (uint32_t r = 0; r < rows; ++r) margin[r] = margin[r] + nodes[leaf_of_row[r]].leaf;
   }
+  free(allowed); free(features);
   free(grad); free(hess); free(qg); free(qh); free(row_buf); free(tmp_buf); free(leaf_of_row); free(hist);
   free(bins); free(bins_cm); free(cuts); free(counts); free(minima);
   return 0;

@@ -35,6 +35,9 @@ typedef struct {
   float base_score;          /* used when has_base_score != 0 */
   int32_t has_base_score;
   int32_t nthread;           /* histogram threads; results never depend on it */
+  float subsample;           /* uniform row sampling when < 1 (src/sampling.cpp:11-74) */
+  float colsample_bytree;    /* per-tree feature sampling when < 1 (src/tree.cpp:28-45) */
+  uint32_t seed;             /* "seed" parameter; 0 keeps the engine's default state */
 } OracleParams;
 
 /* One tree node; field meanings follow the reference's Node plus base_weights
@@ -88,6 +91,18 @@ void oracle_evaluate_feature(const int64_t* feature_hist, uint32_t count, const 
                              const OracleParams* p, int32_t feature, OracleSplit* out);
 float oracle_weight(double G, double H, const OracleParams* p);
 float oracle_gain(double G, double H, float w, const OracleParams* p);
+
+/* --- sampling ------------------------------------------------------------ */
+/* MT19937 (Matsumoto and Nishimura 1998), the engine behind std::mt19937. */
+typedef struct { uint32_t state[624]; uint32_t next; } OracleMT;
+void oracle_mt_seed(OracleMT* g, uint32_t seed);
+uint32_t oracle_mt_next(OracleMT* g);
+/* Uniform row sampling: 1 if row `row` is kept in a round whose seed is `seed`
+ * (kernels/sampling.metal.h:1-30). */
+int oracle_sample_row(uint32_t seed, uint32_t row, float subsample);
+/* Per-tree feature sample of n features: writes the sorted subset to out and
+ * returns its size (src/tree.cpp:28-45 with libc++'s std::shuffle). */
+uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, uint32_t* out);
 
 /* --- training ------------------------------------------------------------ */
 uint32_t oracle_max_nodes(int32_t max_depth);

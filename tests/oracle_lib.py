@@ -19,7 +19,8 @@ class OracleParams(ctypes.Structure):
                 ("reg_alpha", ctypes.c_float), ("min_child_weight", ctypes.c_float),
                 ("max_delta_step", ctypes.c_float), ("min_split_loss", ctypes.c_float),
                 ("scale_pos_weight", ctypes.c_float), ("base_score", ctypes.c_float),
-                ("has_base_score", ctypes.c_int32), ("nthread", ctypes.c_int32)]
+                ("has_base_score", ctypes.c_int32), ("nthread", ctypes.c_int32),
+                ("subsample", ctypes.c_float), ("colsample_bytree", ctypes.c_float), ("seed", ctypes.c_uint32)]
 
 
 NODE_DTYPE = np.dtype([("left", "<i4"), ("right", "<i4"), ("parent", "<i4"), ("feature", "<i4"),
@@ -61,10 +62,11 @@ def ptr(a):
 
 def make_params(objective="reg:squarederror", max_depth=6, max_bin=256, eta=0.3, reg_lambda=1.0, reg_alpha=0.0,
                 min_child_weight=1.0, max_delta_step=0.0, min_split_loss=0.0, scale_pos_weight=1.0,
-                base_score=None, fma_contract=1, nthread=0):
+                base_score=None, fma_contract=1, nthread=0, subsample=1.0, colsample_bytree=1.0, seed=0):
     return OracleParams(OBJECTIVES[objective], max_depth, max_bin, fma_contract, eta, reg_lambda, reg_alpha,
                         min_child_weight, max_delta_step, min_split_loss, scale_pos_weight,
-                        0.0 if base_score is None else base_score, 0 if base_score is None else 1, nthread)
+                        0.0 if base_score is None else base_score, 0 if base_score is None else 1, nthread,
+                        subsample, colsample_bytree, seed)
 
 
 def sketch_cuts(X, max_bin, weights=None):
@@ -125,3 +127,31 @@ def predict_margin(X, result, base_margin):
                                 ptr(result["sizes"]), ctypes.c_uint32(trees.shape[0]),
                                 ctypes.c_uint32(trees.shape[1]), ctypes.c_float(base_margin), ptr(out))
     return out
+
+
+class OracleMT(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_uint32 * 624), ("next", ctypes.c_uint32)]
+
+
+def mt_outputs(seed, count):
+    """First `count` outputs of the oracle's MT19937 seeded with `seed`."""
+    g = OracleMT()
+    lib().oracle_mt_seed(ctypes.byref(g), ctypes.c_uint32(seed))
+    lib().oracle_mt_next.restype = ctypes.c_uint32
+    return np.array([lib().oracle_mt_next(ctypes.byref(g)) for _ in range(count)], np.uint32)
+
+
+def sample_rows(seed, rows, subsample):
+    """Keep mask of uniform row sampling for one round."""
+    f = lib().oracle_sample_row
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]
+    return np.array([f(seed, r, subsample) for r in range(rows)], bool)
+
+
+def sample_columns(n, fraction, seed):
+    out = np.zeros(max(n, 1), np.uint32)
+    f = lib().oracle_sample_columns
+    f.restype = ctypes.c_uint32
+    k = f(ctypes.c_uint32(n), ctypes.c_float(fraction), ctypes.c_uint32(seed), ptr(out))
+    return out[:k]

@@ -22,7 +22,10 @@ def _oracle_params(params, rounds_override=None):
                          min_child_weight=float(params.get("min_child_weight", 1.0)),
                          max_delta_step=float(params.get("max_delta_step", 0.0)),
                          min_split_loss=float(params.get("gamma", 0.0)),
-                         base_score=params.get("base_score"))
+                         base_score=params.get("base_score"),
+                         subsample=float(params.get("subsample", 1.0)),
+                         colsample_bytree=float(params.get("colsample_bytree", 1.0)),
+                         seed=int(params.get("seed", 0)))
 
 
 def assert_trees_equal(bst, oracle_result):
@@ -243,3 +246,82 @@ def test_sklearn_estimators(xgb):
     cls = xgb.XGBClassifier(n_estimators=10, max_depth=3).fit(X, (y > 0).astype(int))
     assert cls.score(X, (y > 0).astype(int)) > 0.7
     assert cls.predict_proba(X).shape == (len(X), 2)
+
+
+@pytest.mark.parametrize("params", [
+    {"max_depth": 6, "max_bin": 256, "subsample": 0.8},
+    {"max_depth": 5, "max_bin": 64, "colsample_bytree": 0.5, "seed": 7},
+    {"max_depth": 6, "max_bin": 128, "subsample": 0.6, "colsample_bytree": 0.8, "seed": 42},
+])
+def test_sampling_parity(xgb, params):
+    """Row sampling (one engine draw per round, dropped rows carry (0, 0)) and
+    per-tree column sampling give the oracle's trees and margins bit for bit."""
+    X, y = W.config1(rows=30000, cols=24)
+    full = dict(params, objective="reg:squarederror", tree_method="hist")
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train(full, d, 8)
+    ref = O.train(X, y, _oracle_params(full), 8)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def _config4_small(rows=40000, seed=5):
+    """The config-4 column recipe at a small size: N(0,1), U(0,1) and integer
+    columns, labels from a logistic model of the first 16 columns."""
+    rng = np.random.default_rng(seed)
+    X = np.empty((rows, 32), np.float32)
+    X[:, :16] = rng.normal(size=(rows, 16))
+    X[:, 16:24] = rng.random((rows, 8))
+    X[:, 24:] = rng.integers(0, 1000, size=(rows, 8))
+    w = rng.normal(size=16).astype(np.float32)
+    y = (X[:, :16] @ w + 0.3 * rng.normal(size=rows) > 0).astype(np.float32)
+    return X, y
+
+
+def test_sampled_1024_bins_depth10_parity(xgb):
+    """1024 bins (u16 codes, 4 features per histogram workgroup), depth 10,
+    subsample 0.8 and colsample_bytree 0.8: bit-identical trees and margins."""
+    X, y = _config4_small()
+    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
+              "subsample": 0.8, "colsample_bytree": 0.8}
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train(params, d, 5)
+    ref = O.train(X, y, _oracle_params(params), 5)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def test_sampled_logistic_parity(xgb):
+    """The config-4 objective and sampling at a small size.  The first tree is
+    bit-identical; later trees see logistic gradients from the device expf,
+    which agree with libm's to rounding (bitwise parity unpinned), so margins
+    are compared to 1e-5."""
+    X, y = _config4_small()
+    params = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
+              "subsample": 0.8, "colsample_bytree": 0.8}
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train(params, d, 5)
+    ref = O.train(X, y, _oracle_params(params), 5)
+    tree0 = bst.trees_to_json()[0]
+    n0 = int(ref["sizes"][0])
+    np.testing.assert_array_equal(tree0["left_children"], ref["trees"][0]["left"][:n0])
+    np.testing.assert_array_equal(np.asarray(tree0["split_conditions"], np.float32).view(np.uint32),
+                                  np.where(ref["trees"][0]["left"][:n0] < 0, ref["trees"][0]["leaf"][:n0],
+                                           ref["trees"][0]["threshold"][:n0]).astype(np.float32).view(np.uint32))
+    margin = bst.predict(d, output_margin=True)
+    np.testing.assert_allclose(margin, ref["margin"], rtol=1e-5, atol=1e-5)
+
+
+def test_sampling_stream_survives_pickle(xgb):
+    """A pickled booster continues the engine's stream: training 3 + 3 rounds
+    across a pickle equals 6 rounds in one go."""
+    import pickle
+    X, y = W.config0(rows=8000, cols=10)
+    params = {"tree_method": "hist", "max_depth": 4, "max_bin": 64, "subsample": 0.7, "colsample_bytree": 0.6,
+              "seed": 3}
+    d = xgb.DMatrix(X, label=y)
+    whole = xgb.train(params, d, 6)
+    half = xgb.train(params, d, 3)
+    half = pickle.loads(pickle.dumps(half))
+    resumed = xgb.train(params, d, 3, xgb_model=half)
+    np.testing.assert_array_equal(resumed.predict(d).view(np.uint32), whole.predict(d).view(np.uint32))

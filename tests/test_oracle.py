@@ -237,3 +237,89 @@ def test_gain_forms_closed_form():
                 want = np.float32(-((2 * G) * float(np.float32(w)) + (H + 1.0) * sq))
             assert np.float32(gain) == want
             assert abs(float(np.float32(gain)) + float(exact)) <= 1e-6 * abs(float(exact)) + 1e-30
+
+
+# ---------------------------------------------------------------------------
+# Sampling (src/sampling.cpp:11-74, kernels/sampling.metal.h:1-30,
+# src/tree.cpp:28-45).
+# ---------------------------------------------------------------------------
+def _mt_standard_state(seed):
+    """std::mersenne_twister_engine::seed for mt19937 (the C++ standard's recurrence)."""
+    key = np.zeros(624, np.uint32)
+    key[0] = seed
+    for i in range(1, 624):
+        prev = int(key[i - 1])
+        key[i] = (1812433253 * (prev ^ (prev >> 30)) + i) & 0xFFFFFFFF
+    return key
+
+
+def test_mt19937_standard_known_answer():
+    """[rand.predef]: the 10000th output of a default-constructed std::mt19937 is 4123659995."""
+    out = O.mt_outputs(5489, 10000)
+    assert int(out[-1]) == 4123659995
+
+
+@pytest.mark.parametrize("seed", [0, 1, 42, 123456789, 0xFFFFFFFF])
+def test_mt19937_matches_numpy_generator(seed):
+    """numpy's MT19937 bit generator, loaded with the standard-seeded state,
+    is an independent implementation of the same twist and tempering."""
+    bg = np.random.MT19937(0)
+    bg.state = {"bit_generator": "MT19937", "state": {"key": _mt_standard_state(seed), "pos": 624}}
+    want = np.array([bg.random_raw() for _ in range(1500)], np.uint64).astype(np.uint32)
+    np.testing.assert_array_equal(O.mt_outputs(seed, 1500), want)
+
+
+@pytest.mark.parametrize("seed,subsample", [(0, 0.8), (7, 0.5), (3737844653, 0.8), (99, 1e-3)])
+def test_row_sampling_closed_form(seed, subsample):
+    """state = seed * 16807^(row+1) mod 2^63 (seed 0 -> 1); keep iff the
+    binary64 value of state-1, over 2^63, is below subsample (binary32)."""
+    rows = 3000
+    got = O.sample_rows(seed, rows, subsample)
+    s = np.float32(subsample)
+    limit = int(np.float64(s) * 2.0 ** 63)
+    want = []
+    for r in range(rows):
+        state = ((seed or 1) * pow(16807, r + 1, 1 << 63)) % (1 << 63)
+        want.append(float(state - 1) < limit)
+    np.testing.assert_array_equal(got, np.array(want))
+    if subsample >= 0.5:
+        assert abs(got.mean() - subsample) < 0.05
+
+
+def test_row_sampling_planted_mistake_is_caught():
+    """Stepping the generator row times instead of row+1 changes the mask."""
+    got = O.sample_rows(11, 2000, 0.5)
+    wrong = np.array([float(((11 * pow(16807, r, 1 << 63)) % (1 << 63)) - 1) < 2.0 ** 62 for r in range(2000)])
+    assert (got != wrong).any()
+
+
+@pytest.mark.parametrize("n,fraction", [(128, 0.8), (64, 0.5), (7, 0.1), (1, 0.5), (33, 0.999)])
+def test_column_sampling_invariants(n, fraction):
+    """Sorted distinct features, max(1, floor(n * fraction)) of them, a
+    deterministic function of the seed; different seeds give different sets.
+    (The draw order models libc++'s std::shuffle: parity unpinned, no libc++
+    headers in this image.)"""
+    keep = max(1, int(np.floor(np.float32(n) * np.float32(fraction))))
+    a = O.sample_columns(n, fraction, 12345)
+    assert len(a) == keep
+    assert np.all(np.diff(a.astype(np.int64)) > 0) and a.max() < n
+    np.testing.assert_array_equal(a, O.sample_columns(n, fraction, 12345))
+    if 1 < keep < n:
+        sets = {tuple(O.sample_columns(n, fraction, s)) for s in range(20)}
+        assert len(sets) > 1
+
+
+def test_sampled_training_drops_rows_and_features():
+    """With subsample and colsample_bytree the oracle's trees only split on
+    sampled features and differ from the unsampled trees; covers shrink to
+    the sampled rows' Hessians."""
+    X, y = W.config0(rows=6000, cols=12)
+    full = O.train(X, y, O.make_params(max_depth=4, max_bin=64), 3)
+    samp = O.train(X, y, O.make_params(max_depth=4, max_bin=64, subsample=0.7, colsample_bytree=0.5, seed=3), 3)
+    assert samp["trees"][0]["cover"][0] < 0.8 * full["trees"][0]["cover"][0]
+    # Reproduce the engine draws: round t uses draw 2t for rows, 2t+1 for columns.
+    draws = O.mt_outputs(3, 6)
+    for t in range(3):
+        feats = set(O.sample_columns(12, 0.5, int(draws[2 * t + 1])).tolist())
+        used = {int(f) for f in samp["trees"][t]["feature"][: samp["sizes"][t]] if f >= 0}
+        assert used <= feats

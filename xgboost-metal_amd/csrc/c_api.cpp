@@ -567,8 +567,10 @@ int XGBoosterUnserializeFromBuffer(BoosterHandle handle, const void* buf, bst_ul
   auto& b = booster(handle);
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   Json all = Json::parse_ubj(std::string(static_cast<const char*>(buf), (size_t)len));
-  b.load_config(all.at("Config"));
+  // Model first: loading a model restarts the engine, the configuration then
+  // restores the serialised engine state.
   b.load_model(all.at("Model"));
+  b.load_config(all.at("Config"));
   API_END
 }
 

@@ -141,6 +141,7 @@ __device__ void mass_flush_and_scale(uint64_t* local, uint64_t* mass, float* sca
   __shared__ uint64_t partial[2 * kLimbs][kShare];
   __shared__ uint32_t last;
   __shared__ volatile uint64_t sink;
+  (void)sink;
   const uint32_t tid = threadIdx.x;
   if (tid < 2 * kLimbs) limbs[tid] = 0;
   __syncthreads();
@@ -181,6 +182,23 @@ __device__ void mass_flush_and_scale(uint64_t* local, uint64_t* mass, float* sca
   scales_from_limbs(limbs, scales);
 }
 
+// Uniform row sampling (kernels/sampling.metal.h:1-30): the row's state is
+// the round seed times 16807^(row+1) modulo 2^63; the row is kept when the
+// binary64 value of state-1 over 2^63 (the canonical draw of a 63-bit engine)
+// is below subsample, compared in binary32 when subsample < 2^-39.
+__device__ __forceinline__ bool sample_keep(uint32_t seed, uint32_t row, float subsample) {
+  const uint64_t mask = 0x7fffffffffffffffull;
+  uint64_t state = seed ? seed : 1u, factor = 16807u;
+  for (uint64_t e = (uint64_t)row + 1; e; e >>= 1) {
+    if (e & 1) state = (state * factor) & mask;
+    factor = (factor * factor) & mask;
+  }
+  const double rounded = (double)(state - 1);
+  const float limit = subsample * 0x1p63f;
+  if (limit < 0x1p24f) return (float)rounded < limit;
+  return rounded < (double)limit;
+}
+
 __device__ __forceinline__ void mass_add(uint64_t* local, float g, float h) {
   uint32_t bg, bh;
   uint64_t mg, mh;
@@ -210,20 +228,25 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
     }
     g = g * weight;
     h = h * weight;
+    if (p.subsample < 1.0f && !sample_keep(p.sample_seed, r, p.subsample)) g = h = 0.0f;
     grad[r] = make_float2(g, h);
     mass_add(local, g, h);
   }
   mass_flush_and_scale(local, mass, scales);
 }
 
-__global__ __launch_bounds__(kGradThreads) void k_gradient_mass(const float2* __restrict__ grad, uint32_t rows,
+__global__ __launch_bounds__(kGradThreads) void k_gradient_mass(MgbGradParams p, float2* __restrict__ grad,
                                                                 uint64_t* __restrict__ mass,
                                                                 float* __restrict__ scales) {
   __shared__ uint64_t local[2 * 256];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
-    const float2 v = grad[r];
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < p.rows; r += gridDim.x * blockDim.x) {
+    float2 v = grad[r];
+    if (p.subsample < 1.0f && !sample_keep(p.sample_seed, r, p.subsample)) {
+      v = make_float2(0.0f, 0.0f);
+      grad[r] = v;
+    }
     mass_add(local, v.x, v.y);
   }
   mass_flush_and_scale(local, mass, scales);
@@ -377,10 +400,9 @@ int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labe
   return 0;
 }
 
-int mgb_gradient_mass(const float* grad, uint32_t rows, uint64_t* mass, float* scales) {
-  uint32_t grid = grid_for(rows, kGradThreads, kGradBlocks);
-  launch(MGB_PROF_GRADIENT, k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, (const float2*)grad, rows, mass,
-         scales);
+int mgb_gradient_mass(const MgbGradParams* p, float* grad, uint64_t* mass, float* scales) {
+  uint32_t grid = grid_for(p->rows, kGradThreads, kGradBlocks);
+  launch(MGB_PROF_GRADIENT, k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, *p, (float2*)grad, mass, scales);
   MGB_LAUNCH_CHECK("k_gradient_mass");
   return 0;
 }

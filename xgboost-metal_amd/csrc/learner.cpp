@@ -229,8 +229,13 @@ void Learner::configure_check() const {
   require(integer("max_leaves", 0) == 0, "max_leaves is not supported (depthwise growth only).");
   auto depth = integer("max_depth", 6);
   require(depth >= 1 && depth <= 16, "max_depth must be in [1, 16].");
-  for (auto key : {"subsample", "colsample_bytree", "colsample_bylevel", "colsample_bynode"})
+  for (auto key : {"subsample", "colsample_bytree"}) {
+    const double v = number(key, 1);
+    require(v > 0 && v <= 1, std::string(key) + " must be in (0, 1].");
+  }
+  for (auto key : {"colsample_bylevel", "colsample_bynode"})
     require(number(key, 1) == 1.0, std::string(key) + " < 1 is not supported yet.");
+  require(param("sampling_method", "uniform") == "uniform", "Only sampling_method='uniform' is supported.");
   auto mono = param("monotone_constraints", "()");
   for (char c : mono) require(c == '(' || c == ')' || c == '[' || c == ']' || c == ',' || c == '0' || c == ' ',
                               "monotone_constraints are not supported yet.");
@@ -322,6 +327,67 @@ DeviceBuffer* Learner::margin_cache(DMatrix& data) {
   return &d_margin_;
 }
 
+void Learner::configure_rng() {
+  const std::string seed = param("seed", "0");
+  if (seed != rng_seed_) {
+    size_t read = 0;
+    long long value = 0;
+    try {
+      value = std::stoll(seed, &read);
+    } catch (...) {
+      read = 0;
+    }
+    require(read == seed.size(), "Invalid random seed.");
+    rng_.seed(static_cast<std::mt19937::result_type>(value));
+    rng_seed_ = seed;
+  }
+}
+
+void Learner::sample_rows(DMatrix& data, MgbGradParams& gp) {
+  configure_rng();
+  if (integer("seed_per_iteration", 0))
+    rng_.seed(static_cast<std::mt19937::result_type>((uint32_t)std::stoll(param("seed", "0")) * 127u +
+                                                     (uint32_t)trees.size()));
+  const double subsample = number("subsample", 1);
+  const auto budget = static_cast<uint64_t>(static_cast<float>(data.rows) * subsample);
+  gp.subsample = 1.0f;
+  gp.sample_seed = 0;
+  if (budget < data.rows) {
+    gp.sample_seed = static_cast<uint32_t>(rng_());
+    gp.subsample = static_cast<float>(subsample);
+  }
+}
+
+// src/tree.cpp:28-45 with libc++'s std::shuffle, the reference's model of it
+// (kernels/tree_sample_columns.metal.h): a fresh engine seeded by one draw,
+// Fisher-Yates from the front (position pos swaps with pos + u, u uniform in
+// [0, n - pos) by masking to the bit width of n - pos - 1 and rejecting),
+// then the first max(1, floor(n * fraction)) features, sorted.
+const uint32_t* Learner::sample_columns(uint32_t cols) {
+  const float fraction = fnumber("colsample_bytree", 1.0f);
+  if (!(fraction < 1.0f) || cols == 0) return nullptr;
+  std::mt19937 engine(rng_());
+  std::vector<uint32_t> order(cols);
+  for (uint32_t i = 0; i < cols; ++i) order[i] = i;
+  const float scaled = std::floor(static_cast<float>(cols) * fraction);
+  const uint32_t keep = std::min<uint32_t>(cols, scaled < 1.0f ? 1u : static_cast<uint32_t>(scaled));
+  for (uint32_t pos = 0; pos < keep && pos + 1 < cols; ++pos) {
+    const uint32_t range = cols - pos;
+    uint32_t width = 0;
+    while (width < 32 && ((range - 1) >> width)) ++width;
+    const uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
+    uint32_t u;
+    do u = static_cast<uint32_t>(engine()) & mask; while (u >= range);
+    std::swap(order[pos], order[pos + u]);
+  }
+  feature_flags_.assign(cols, 0u);
+  for (uint32_t i = 0; i < keep; ++i) feature_flags_[order[i]] = 1u;
+  d_features_.ensure((size_t)cols * sizeof(uint32_t));
+  kcheck(mgb_memcpy_h2d_async(d_features_.get(), feature_flags_.data(), (size_t)cols * sizeof(uint32_t)),
+         "feature sample upload");
+  return d_features_.as<uint32_t>();
+}
+
 void Learner::grow(DMatrix& data, bool unit_hessian) {
   const uint32_t depth = (uint32_t)integer("max_depth", 6);
   MgbTreeShape shape{};
@@ -352,9 +418,10 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   kcheck(mgb_profile_enable(profiling ? 1 : 0), "profile");
   auto* nodes = d_nodes_.as<MgbTreeNode>();
   auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
+  const uint32_t* features = sample_columns(data.cols);
   kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
-                       d_grad_.as<float>(), d_scales_.as<float>(), &sp, d_tree_ws_.get(), d_tree_ws_.bytes(),
-                       margin->as<float>(), nodes, count),
+                       d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, d_tree_ws_.get(),
+                       d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
          "tree growth");
   // One device-to-host copy per round: node records followed by the count.
   std::vector<uint8_t> host(node_bytes + 16);
@@ -404,11 +471,14 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
   gp.objective = (uint32_t)obj;
   gp.has_weight = data.weights.empty() ? 0 : 1;
   gp.scale_pos_weight = fnumber("scale_pos_weight", 1.0f);
+  sample_rows(data, gp);
   kcheck(mgb_gradients(&gp, margin->as<float>(), data.d_labels.as<float>(),
                        gp.has_weight ? data.d_weights.as<float>() : nullptr, d_grad_.as<float>(),
                        d_mass_.as<uint64_t>(), d_scales_.as<float>()),
          "gradients");
-  grow(data, obj == 0 && data.weights.empty());
+  // Unit Hessians (every h = 1, so a row count stands in for the Hessian
+  // sum) hold for unweighted squared error unless sampling zeroed some rows.
+  grow(data, obj == 0 && data.weights.empty() && gp.subsample >= 1.0f);
   seconds_["train_rounds"] += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   seconds_["quantiles"] = data.sketch_seconds;
   seconds_["bin_matrix"] = data.quantize_seconds;
@@ -428,7 +498,10 @@ void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t 
     kcheck(mgb_memset(d_mass_.get(), 0, MGB_MASS_WORDS * sizeof(uint64_t)), "memset");
   }
   d_scales_.ensure(2 * sizeof(float));
-  kcheck(mgb_gradient_mass(d_grad_.as<float>(), data.rows, d_mass_.as<uint64_t>(), d_scales_.as<float>()),
+  MgbGradParams gp{};
+  gp.rows = data.rows;
+  sample_rows(data, gp);
+  kcheck(mgb_gradient_mass(&gp, d_grad_.as<float>(), d_mass_.as<uint64_t>(), d_scales_.as<float>()),
          "gradient mass");
   grow(data, false);
 }
@@ -672,6 +745,9 @@ void Learner::load_model(const Json& input) {
   cache_id_ = 0;
   cache_trees_ = 0;
   model_version_ = SIZE_MAX;
+  // A loaded model restarts the engine from seed 0 (src/model.cpp:225).
+  rng_.seed(0);
+  rng_seed_ = "0";
 }
 
 Json Learner::config() const {
@@ -683,6 +759,13 @@ Json Learner::config() const {
   ltp["objective"] = objective_name();
   ltp["booster"] = "gbtree";
   learner["learner_train_param"] = ltp;
+  // The engine's state, so a serialised booster continues the same stream.
+  std::ostringstream state;
+  state << rng_;
+  Json generic = Json::object();
+  generic["seed"] = rng_seed_;
+  generic["rng_state"] = state.str();
+  learner["generic_param"] = generic;
   Json root = Json::object();
   root["learner"] = learner;
   Json version = Json::array();
@@ -696,6 +779,15 @@ void Learner::load_config(const Json& cfg) {
   if (learner.contains("params"))
     for (auto const& kv : learner.at("params").members())
       params_[kv.first] = kv.second.is_string() ? kv.second.string() : kv.second.dump();
+  if (learner.contains("generic_param")) {
+    const Json& generic = learner.at("generic_param");
+    if (generic.contains("rng_state") && generic.contains("seed")) {
+      std::istringstream state(generic.at("rng_state").string());
+      state >> rng_;
+      require(!state.fail(), "Invalid rng_state in the booster configuration.");
+      rng_seed_ = generic.at("seed").string();
+    }
+  }
 }
 
 void Learner::reset() {

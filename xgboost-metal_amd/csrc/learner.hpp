@@ -11,6 +11,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -123,6 +124,11 @@ class Learner {
   void configure_check() const;
   void initialize(DMatrix& data, bool custom);
   void grow(DMatrix& data, bool unit_hessian);
+  void configure_rng();
+  // Per-round row-sampling parameters (src/learner.cpp:679, src/sampling.cpp:11-17).
+  void sample_rows(DMatrix& data, MgbGradParams& gp);
+  // The tree's column sample as per-feature flags on the device, or NULL.
+  const uint32_t* sample_columns(uint32_t cols);
   float base_margin_value() const;
   void upload_model();
   DeviceBuffer* margin_cache(DMatrix& data);
@@ -141,6 +147,12 @@ class Learner {
   std::map<std::string, double> seconds_;
   uint64_t rounds_timed_ = 0;
   uint64_t hist_bytes_ = 0, hist_rows_ = 0;
+  // The learner's engine (src/learner.cpp:94-103): default-constructed state
+  // until a "seed" other than the last one applied reseeds it.
+  std::mt19937 rng_;
+  std::string rng_seed_ = "0";
+  DeviceBuffer d_features_;
+  std::vector<uint32_t> feature_flags_;
 };
 
 }  // namespace mgb

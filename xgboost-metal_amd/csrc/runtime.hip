@@ -130,6 +130,13 @@ int mgb_memcpy_d2d(void* dst, const void* src, size_t bytes) {
   return 0;
 }
 
+int mgb_memcpy_h2d_async(void* dst, const void* src, size_t bytes) {
+  if (ensure_init()) return -1;
+  if (!bytes) return 0;
+  MGB_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  return 0;
+}
+
 int mgb_memset(void* dst, int value, size_t bytes) {
   if (ensure_init()) return -1;
   if (!bytes) return 0;

@@ -100,6 +100,7 @@ struct Tree {
   const void* bins;
   const float* cuts;
   const uint32_t* counts;
+  const uint32_t* allowed;    // per feature: nonzero if in the tree's column sample (NULL: all)
   const float2* grad;
   const float* scales;
   float* margin;
@@ -667,6 +668,15 @@ __global__ __launch_bounds__(W * kWave) void k_split(Tree t, uint32_t depth) {
     for (uint32_t k = 0; k < W; ++k) { tg += uniform_u64(root_sum[k][0]); th += uniform_u64(root_sum[k][1]); }
     NodeEval e;
     node_begin(e, tg, th, mg, mh, eg, eh, t.sp);
+    if (t.allowed && !t.allowed[f]) {
+      // Outside the tree's column sample: the candidate only carries the
+      // node's weight and cover (select reads them for feature 0).
+      if (threadIdx.x == 0) {
+        const WaveBest none{-INFINITY, 0xffffffffu, 0, 0};
+        node_finish(e, &none, 1, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f, t.cands + f, t.best);
+      }
+      return;
+    }
     uint64_t carry_g = 0, carry_h = 0;
     for (uint32_t base = 0; base < count; base += span) {
       const uint32_t b = base + wave * kWave + lane;
@@ -702,6 +712,21 @@ __global__ __launch_bounds__(W * kWave) void k_split(Tree t, uint32_t depth) {
   int64_t* ob = cur + ((uint64_t)other * F + f) * B1 * 2;
   const bool store_other = depth + 1 < t.max_depth;
   const uint32_t count = t.counts[f];
+  if (t.allowed && !t.allowed[f]) {
+    // Outside the tree's column sample: no candidate and no sibling histogram
+    // (this tree never scores the feature).  The candidates still carry the
+    // nodes' weights and covers.
+    if (threadIdx.x < 2) {
+      const Frontier& fn = threadIdx.x == 0 ? fb : fo;
+      const uint32_t slot = threadIdx.x == 0 ? built : other;
+      NodeEval e;
+      node_begin(e, (uint64_t)fn.sum_g, (uint64_t)fn.sum_h, 0, 0, eg, eh, t.sp);
+      const WaveBest none{-INFINITY, 0xffffffffu, 0, 0};
+      node_finish(e, &none, 1, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f,
+                  t.cands + (uint64_t)slot * F + f, t.best + slot);
+    }
+    return;
+  }
   // Missing slots first: they give each child's present-bin totals.
   uint64_t pmg, pmh, xmg, xmh;
   load_pair(parent, MB, pmg, pmh);
@@ -1236,13 +1261,15 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape) { return layout(*shap
 
 int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
                   const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
-                  void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes, uint32_t* node_count) {
+                  const uint32_t* features, void* workspace, size_t workspace_bytes, float* margin,
+                  MgbTreeNode* nodes, uint32_t* node_count) {
   if (validate(shape, m)) return -1;
   Layout L = layout(*shape);
   if (!workspace || workspace_bytes < L.total) { set_error("mgb_grow_tree: workspace too small"); return -1; }
   Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
   t.bins = bins; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
+  t.allowed = features;
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
   const uint32_t hgrid = hist_grid(t);

@@ -297,7 +297,14 @@ class Booster:
             self.feature_names = cache[0].feature_names
             self.feature_types = cache[0].feature_types
         if isinstance(model_file, Booster):
-            self.load_model(model_file.save_raw("json"))
+            # A memory snapshot of the other booster (model, configuration and
+            # random-engine state), as upstream's copy does.
+            state = model_file.__getstate__()
+            raw = state["raw"]
+            buf = (ctypes.c_char * len(raw)).from_buffer_copy(raw)
+            _check_call(_LIB.XGBoosterUnserializeFromBuffer(self.handle, buf, c_bst_ulong(len(raw))))
+            self.feature_names = state.get("feature_names")
+            self.feature_types = state.get("feature_types")
         elif model_file is not None:
             self.load_model(model_file)
         self.set_param(params or {})
