@@ -46,9 +46,31 @@ def config2(rows=262144, cols=64, seed=1337):
 PARAMS = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 8, "max_bin": 256, "eta": 0.3,
           "lambda": 1}
 
+C4_PARAMS = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
+             "subsample": 0.8, "colsample_bytree": 0.8}
 
-def time_rounds(xgb, dtrain, rounds, profile):
-    params = dict(PARAMS, hip_profile=1 if profile else 0)
+
+def config4(rows=10_000_000, seed=1337, chunk=1 << 20):
+    """columns 0-63 N(0,1), 64-95 U(0,1), 96-127 integers in
+    [0, 999] as float32; y ~ Bernoulli(sigmoid(X[:, :16] . w + 0.3 N)).  Drawn
+    in row chunks (float32 storage) so the float64 temporaries stay small."""
+    rng = np.random.default_rng(seed)
+    w = rng.normal(size=16)
+    X = np.empty((rows, 128), np.float32)
+    y = np.empty(rows, np.float32)
+    for a in range(0, rows, chunk):
+        b = min(rows, a + chunk)
+        n = b - a
+        X[a:b, :64] = rng.normal(size=(n, 64))
+        X[a:b, 64:96] = rng.random((n, 32))
+        X[a:b, 96:] = rng.integers(0, 1000, size=(n, 32))
+        s = X[a:b, :16].astype(np.float64) @ w + 0.3 * rng.normal(size=n)
+        y[a:b] = rng.random(n) < 1.0 / (1.0 + np.exp(-s))
+    return X, y
+
+
+def time_rounds(xgb, dtrain, rounds, profile, base=PARAMS):
+    params = dict(base, hip_profile=1 if profile else 0)
     bst = xgb.Booster(params, [dtrain])
     bst.update(dtrain, 0)  # initialise (base score, buffers); not timed
     start = time.perf_counter()
@@ -103,12 +125,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--config", choices=["c2", "c4"], default="c2",
+                    help="c2 (default): the headline metric; c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(row-sharded multi-GPU training is a design note, not implemented).", file=sys.stderr)
         sys.exit(2)
     import xgboost as xgb
+    if args.config == "c4":
+        return bench_c4(xgb, args)
 
     X, y = config2()
     dtrain = xgb.DMatrix(X, label=y)
@@ -189,6 +215,53 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(X, y, args.cpu_seconds)
+    print(json.dumps(line))
+
+
+def bench_c4(xgb, args):
+    """Config 4: one GPU, rounds on the resident 2.56 GB u16 bin matrix."""
+    steps = args.steps if args.steps != 100 else 20
+    warmup = args.warmup if args.warmup != 10 else 2
+    t0 = time.perf_counter()
+    X, y = config4()
+    gen_s = time.perf_counter() - t0
+    print(f"c4: generated {X.shape} in {gen_s:.1f} s", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    dtrain = xgb.DMatrix(X, label=y)
+    print(f"c4: DMatrix in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    warm = xgb.train(dict(C4_PARAMS), dtrain, max(1, warmup))
+    setup_s = time.perf_counter() - t0
+    print(f"c4: sketch, bins and {warmup} warm-up rounds in {setup_s:.1f} s", file=sys.stderr, flush=True)
+    prof0 = warm.profile()["seconds"]
+    _, elapsed = time_rounds(xgb, dtrain, steps, profile=False, base=C4_PARAMS)
+    ms_per_step = elapsed * 1e3 / steps
+    print(f"c4: {steps} timed rounds, {ms_per_step:.2f} ms each", file=sys.stderr, flush=True)
+    import device_lib as D
+    D.lib().mgb_profile_reset()
+    bst_p, _ = time_rounds(xgb, dtrain, steps, profile=True, base=C4_PARAMS)
+    prof = bst_p.profile()
+    kernels = prof["kernels"]
+    hist = kernels["histogram"]
+    launches = max(hist["launches"], 1)
+    achieved = prof["histogram_bytes"] / (hist["ms"] * 1e-3) / 1e9 if hist["ms"] > 0 else 0.0
+    line = {
+        "metric": "ms/200 rounds @10,000,000x128 d10 1024 bins (config 4); histogram build HBM GB/s vs peak",
+        "value": round(ms_per_step * 200, 2), "unit": "ms/200 rounds", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int64", "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: X 10,000,000x128 (N(0,1) | U(0,1) | integers 0-999), logistic "
+                               "labels; binary:logistic, depth 10, max_bin 1024 (u16 codes), eta 0.1, subsample 0.8, "
+                               "colsample_bytree 0.8; step = one boosting round on the resident bin matrix",
+                   "rows": 10_000_000, "features": 128, "max_depth": 10, "max_bin": 1024},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_histogram",
+                     "launches": launches, "algorithmic_bytes_per_launch": round(prof["histogram_bytes"] / launches),
+                     "avg_launch_us": round(hist["ms"] * 1e3 / launches, 3)},
+        "kernel_ms_per_round": {k: round(v["ms"] / (steps + 1), 4) for k, v in kernels.items() if v["launches"]},
+        "one_time_s": {"generate": round(gen_s, 2), "dmatrix_sketch_bins_and_warmup": round(setup_s, 2),
+                       "quantile_sketch": round(prof0.get("quantiles", 0.0), 3),
+                       "bin_matrix": round(prof0.get("bin_matrix", 0.0), 3)},
+    }
     print(json.dumps(line))
 
 

@@ -53,16 +53,26 @@ int mgb_stream_copy(void* dst, const void* src, size_t bytes);
 
 /* ---- POD layouts ------------------------------------------------------ */
 
-/* Bin matrix: row-major, row_stride bytes per row, bin_bytes = 1 (u8) or 2
- * (u16).  missing_code marks a missing value: 0xFF / 0xFFFF when the matrix
- * has missing values, 0xFFFFFFFF (matches no code) when it has none, so a
- * dense matrix keeps u8 codes for all 256 bins. */
+/* Bin matrix of bin_bytes = 1 (u8) or 2 (u16) codes.  Features form groups
+ * of group_features (4, 8 or 16; the last group padded with missing codes);
+ * the code of (row, f) is at
+ *   bins + (f / group_features) * group_stride + row * row_stride
+ *        + (f % group_features) * bin_bytes.
+ * Row-major: row_stride = groups * group_features * bin_bytes and
+ * group_stride = group_features * bin_bytes (a row's codes are contiguous).
+ * Group-major: row_stride = group_features * bin_bytes and group_stride =
+ * rows * row_stride (each feature group's codes are contiguous over rows), so
+ * a workgroup that histograms one group streams only that group's bytes.
+ * missing_code marks a missing value: 0xFF / 0xFFFF when the matrix has
+ * missing values, 0xFFFFFFFF (matches no code) when it has none, so a dense
+ * matrix keeps u8 codes for all 256 bins. */
 typedef struct {
   uint32_t rows, cols, row_stride, bin_bytes;
-  uint32_t max_bin;      /* histogram bins per feature; slot max_bin holds missing */
-  uint32_t cut_stride;   /* floats per feature in the cut array */
+  uint32_t max_bin;         /* histogram bins per feature; slot max_bin holds missing */
+  uint32_t cut_stride;      /* floats per feature in the cut array */
   uint32_t missing_code;
-  uint32_t padding;
+  uint32_t group_features;
+  uint64_t group_stride;    /* bytes */
 } MgbMatrix;
 
 /* Per-round gradient statistics (replaces GradientParams/GradCert,

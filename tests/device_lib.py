@@ -12,7 +12,8 @@ LIB_PATH = ROOT / "xgboost-metal_amd" / "python" / "xgboost" / "lib" / "libxgboo
 class MgbMatrix(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("cols", ctypes.c_uint32), ("row_stride", ctypes.c_uint32),
                 ("bin_bytes", ctypes.c_uint32), ("max_bin", ctypes.c_uint32), ("cut_stride", ctypes.c_uint32),
-                ("missing_code", ctypes.c_uint32), ("padding", ctypes.c_uint32)]
+                ("missing_code", ctypes.c_uint32), ("group_features", ctypes.c_uint32),
+                ("group_stride", ctypes.c_uint64)]
 
 
 class MgbTreeShape(ctypes.Structure):
@@ -84,19 +85,28 @@ def layout(cols, hist_bins, bin_bytes, G):
     return groups * G * bin_bytes
 
 
-def quantize_bins(X, cuts, counts, hist_bins, bin_bytes, G, dense=False):
+def quantize_bins(X, cuts, counts, hist_bins, bin_bytes, G, dense=False, group_major=False):
+    """Device bin matrix; `bins` is returned row-major ([rows, groups*G]) for
+    either layout."""
     X = np.ascontiguousarray(X, np.float32)
     rows, cols = X.shape
     code = 0xFFFFFFFF if dense else (0xFF if bin_bytes == 1 else 0xFFFF)
-    m = MgbMatrix(rows, cols, layout(cols, hist_bins, bin_bytes, G), bin_bytes, hist_bins, cuts.shape[1], code, 0)
+    groups = (cols + G - 1) // G
+    gbytes = G * bin_bytes
+    row_stride, group_stride = (gbytes, rows * gbytes) if group_major else (groups * gbytes, gbytes)
+    m = MgbMatrix(rows, cols, row_stride, bin_bytes, hist_bins, cuts.shape[1], code, G, group_stride)
     dX = Device.of(X)
     dcuts = Device.of(np.ascontiguousarray(cuts, np.float32))
     dcounts = Device.of(np.ascontiguousarray(counts, np.uint32))
-    dbins = Device(rows * m.row_stride)
+    dbins = Device(rows * groups * gbytes)
     flag = Device(4)
     check(lib().mgb_quantize_bins(dX.ptr, dcuts.ptr, dcounts.ptr, ctypes.byref(m), dbins.ptr, flag.ptr))
     dtype = np.uint8 if bin_bytes == 1 else np.uint16
-    bins = dbins.read(dtype, rows * m.row_stride // bin_bytes).reshape(rows, -1)
+    flat = dbins.read(dtype, rows * groups * G)
+    if group_major:
+        bins = flat.reshape(groups, rows, G).transpose(1, 0, 2).reshape(rows, groups * G)
+    else:
+        bins = flat.reshape(rows, groups * G)
     return m, dbins, bins, bool(flag.read(np.uint32, 1)[0])
 
 

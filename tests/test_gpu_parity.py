@@ -75,13 +75,14 @@ def test_sketch_cuts_weighted_match_oracle():
         np.testing.assert_array_equal(cuts[f, :counts[f]].view(np.uint32), ocuts[f, :counts[f]].view(np.uint32))
 
 
-@pytest.mark.parametrize("bin_bytes,G", [(1, 16), (1, 4), (2, 8)])
-def test_bins_and_histogram_match_oracle(bin_bytes, G):
+@pytest.mark.parametrize("bin_bytes,G,group_major", [(1, 16, False), (1, 4, False), (2, 8, False), (1, 4, True),
+                                                     (2, 4, True), (1, 16, True)])
+def test_bins_and_histogram_match_oracle(bin_bytes, G, group_major):
     rng = np.random.default_rng(11)
     X, y = W.config1(rows=9000, cols=21)
     ocuts, ocounts, _ = O.sketch_cuts(X, 64)
     obins = O.quantize(X, ocuts, ocounts)
-    m, dbins, bins, missing = D.quantize_bins(X, ocuts, ocounts, 64, bin_bytes, G)
+    m, dbins, bins, missing = D.quantize_bins(X, ocuts, ocounts, 64, bin_bytes, G, group_major=group_major)
     assert missing
     code = 0xFF if bin_bytes == 1 else 0xFFFF
     got = bins[:, :X.shape[1]].astype(np.int64)
@@ -325,3 +326,16 @@ def test_sampling_stream_survives_pickle(xgb):
     half = pickle.loads(pickle.dumps(half))
     resumed = xgb.train(params, d, 3, xgb_model=half)
     np.testing.assert_array_equal(resumed.predict(d).view(np.uint32), whole.predict(d).view(np.uint32))
+
+
+@pytest.mark.parametrize("layout", ["row", "group"])
+def test_bin_layouts_give_identical_trees(xgb, layout):
+    """Row-major and group-major bin matrices (forced either way) grow the
+    oracle's trees, with missing values and 1024-bin u16 codes."""
+    X, y = W.config1(rows=20000, cols=40)
+    params = {"tree_method": "hist", "max_depth": 6, "max_bin": 1024, "hip_bin_layout": layout}
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train(params, d, 4)
+    ref = O.train(X, y, _oracle_params(params), 4)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))

@@ -136,6 +136,17 @@ std::vector<float> to_vector(const ArrayView& v) {
   int64_t n = 1;
   for (auto d : v.shape) n *= d;
   std::vector<float> out((size_t)n);
+  // C-contiguous float32: one copy.
+  bool contiguous = v.kind == 'f' && v.itemsize == 4;
+  for (size_t k = 0, step = 4; contiguous && k < v.shape.size(); ++k) {
+    const size_t axis = v.shape.size() - 1 - k;
+    contiguous = v.shape[axis] <= 1 || v.strides[axis] == (int64_t)step;
+    step *= (size_t)v.shape[axis];
+  }
+  if (contiguous) {
+    if (n) std::memcpy(out.data(), v.data, (size_t)n * sizeof(float));
+    return out;
+  }
   if (v.shape.size() == 1) {
     for (int64_t i = 0; i < n; ++i) out[i] = load_value(v, i * v.strides[0]);
   } else if (v.shape.size() == 2) {
@@ -374,7 +385,7 @@ int XGDMatrixGetQuantileCut(DMatrixHandle const handle, char const* config, char
   }
   if (!max_bin && d.is_quantile) max_bin = d.quantile_max_bin;
   require(max_bin != 0, "The DMatrix has no quantile cuts yet; train a booster on it first.");
-  d.quantize(max_bin);
+  d.quantize(max_bin, d.quantized_max_bin == max_bin ? d.quantized_layout : 0);
   g_results.indptr.assign(1, 0);
   g_results.values.clear();
   for (uint32_t f = 0; f < d.cols; ++f) {

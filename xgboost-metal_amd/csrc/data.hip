@@ -19,12 +19,28 @@ template <typename BinT>
 __global__ void k_quantize(const float* __restrict__ X, const float* __restrict__ cuts,
                            const uint32_t* __restrict__ counts, MgbMatrix m, BinT* __restrict__ bins,
                            uint32_t* __restrict__ any_missing) {
-  const uint32_t padded = m.row_stride / sizeof(BinT);
-  const uint64_t total = (uint64_t)m.rows * padded;
+  const uint32_t G = m.group_features;
+  const uint32_t groups = (m.cols + G - 1) / G;
+  const uint64_t total = (uint64_t)m.rows * groups * G;
+  // Output order: consecutive threads write consecutive codes of the layout
+  // (a row's groups for row-major, a group's rows for group-major).
+  const bool group_major = m.group_stride != (uint64_t)G * sizeof(BinT);
   bool missing = false;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (uint64_t)gridDim.x * blockDim.x) {
-    uint32_t r = (uint32_t)(i / padded), f = (uint32_t)(i % padded);
+    uint32_t r, g, j;
+    if (group_major) {
+      g = (uint32_t)(i / ((uint64_t)m.rows * G));
+      const uint64_t rem = i % ((uint64_t)m.rows * G);
+      r = (uint32_t)(rem / G);
+      j = (uint32_t)(rem % G);
+    } else {
+      r = (uint32_t)(i / ((uint64_t)groups * G));
+      const uint32_t k = (uint32_t)(i % ((uint64_t)groups * G));
+      g = k / G;
+      j = k % G;
+    }
+    const uint32_t f = g * G + j;
     BinT code = (BinT)m.missing_code;
     if (f < m.cols) {
       float v = X[(uint64_t)r * m.cols + f];
@@ -42,7 +58,8 @@ __global__ void k_quantize(const float* __restrict__ X, const float* __restrict_
         missing = true;
       }
     }
-    bins[i] = code;
+    reinterpret_cast<BinT*>(reinterpret_cast<uint8_t*>(bins) + (uint64_t)g * m.group_stride +
+                            (uint64_t)r * m.row_stride)[j] = code;
   }
   if (__any(missing) && lane_id() == 0) atomicOr(any_missing, 1u);
 }
@@ -374,11 +391,19 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
                       uint32_t* any_missing) {
   if (!m || !bins || !any_missing) { set_error("mgb_quantize_bins: null argument"); return -1; }
   if (m->bin_bytes != 1 && m->bin_bytes != 2) { set_error("mgb_quantize_bins: bin_bytes must be 1 or 2"); return -1; }
-  if (m->row_stride % m->bin_bytes || m->row_stride / m->bin_bytes < m->cols) {
-    set_error("mgb_quantize_bins: row_stride too small");
+  const uint32_t G = m->group_features;
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) {
+    set_error("mgb_quantize_bins: group_features must be a power of two <= 16");
     return -1;
   }
-  uint64_t total = (uint64_t)m->rows * (m->row_stride / m->bin_bytes);
+  const uint64_t groups = (m->cols + G - 1) / G, gbytes = (uint64_t)G * m->bin_bytes;
+  const bool row_major = m->group_stride == gbytes && m->row_stride == groups * gbytes;
+  const bool group_major = m->row_stride == gbytes && m->group_stride == (uint64_t)m->rows * gbytes;
+  if (!row_major && !group_major) {
+    set_error("mgb_quantize_bins: row_stride/group_stride describe neither the row-major nor the group-major layout");
+    return -1;
+  }
+  uint64_t total = (uint64_t)m->rows * groups * G;
   if (!total) return 0;
   uint32_t grid = grid_for(total, 256, 65535);
   if (m->bin_bytes == 1)

@@ -68,7 +68,7 @@ void DMatrix::upload_info() {
 
 void DMatrix::set_info(const std::string& field, const float* values, size_t count) {
   std::vector<float> v(values, values + count);
-  if (field == "label") { labels = std::move(v); labels_uploaded = false; }
+  if (field == "label") { labels = std::move(v); labels_uploaded = false; labels_in_unit = -1; }
   else if (field == "weight") {
     weights = std::move(v);
     weights_uploaded = false;
@@ -94,9 +94,14 @@ static uint32_t next_pow2(uint32_t v) {
   return p;
 }
 
-void DMatrix::quantize(uint32_t max_bin) {
+void DMatrix::quantize(uint32_t max_bin, int layout) {
   require(max_bin >= 2, "max_bin must be at least 2.");
-  if (quantized_max_bin == max_bin) return;
+  require(layout >= 0 && layout <= 2, "hip_bin_layout must be auto, row or group.");
+  if (quantized_max_bin == max_bin && quantized_layout == layout) return;
+  if (quantized_max_bin == max_bin) {
+    relayout(layout);
+    return;
+  }
   require(!is_quantile || quantile_max_bin == max_bin, "Inconsistent max_bin between QuantileDMatrix and Booster.");
   require(rows > 0 && cols > 0, "Data must contain at least one row and one feature.");
   upload();
@@ -130,23 +135,39 @@ void DMatrix::quantize(uint32_t max_bin) {
   while (G > 1 && (size_t)G * (hist_bins + 1) * 16 > 66000) G >>= 1;
   G = std::min(G, next_pow2(cols));
   features_per_group = G;
-  uint32_t groups = (cols + G - 1) / G;
   matrix.rows = rows;
   matrix.cols = cols;
   matrix.bin_bytes = bin_bytes;
-  matrix.row_stride = groups * G * bin_bytes;
   matrix.max_bin = hist_bins;
   matrix.cut_stride = max_bin;
   matrix.missing_code = !has_missing ? 0xFFFFFFFFu : (bin_bytes == 1 ? 0xFFu : 0xFFFFu);
-  d_bins.ensure((size_t)rows * matrix.row_stride);
+  matrix.group_features = G;
+  quantized_max_bin = max_bin;
+  sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
+  relayout(layout);
+}
+
+// Bin matrix in the requested layout (the cuts stay).  Row-major is the
+// default (auto): below the root the histogram gathers rows by index, and a
+// row's codes then share one cache line that every feature group's workgroup
+// reuses from L2.  Group-major (each group's codes contiguous over rows) is
+// faster only for the dense root level; measured on 10M x 128 u16 bins, it
+// halves the root pass but doubles the deeper gathered levels.
+void DMatrix::relayout(int layout) {
+  auto t0 = std::chrono::steady_clock::now();
+  const uint32_t G = features_per_group, groups = (cols + G - 1) / G;
+  const uint32_t gbytes = G * matrix.bin_bytes;
+  const bool group_major = layout == 2;
+  matrix.row_stride = group_major ? gbytes : groups * gbytes;
+  matrix.group_stride = group_major ? (uint64_t)rows * gbytes : gbytes;
+  d_bins.ensure((size_t)rows * groups * gbytes);
+  kcheck(mgb_memset(d_missing.get(), 0, sizeof(uint32_t)), "memset");
   kcheck(mgb_quantize_bins(d_data.as<float>(), d_cuts.as<float>(), d_counts.as<uint32_t>(), &matrix, d_bins.get(),
                            d_missing.as<uint32_t>()),
          "bin matrix");
   kcheck(mgb_synchronize(), "synchronize");
-  auto t2 = std::chrono::steady_clock::now();
-  sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
-  quantize_seconds += std::chrono::duration<double>(t2 - t1).count();
-  quantized_max_bin = max_bin;
+  quantize_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  quantized_layout = layout;
 }
 
 // ---------------------------------------------------------------------------
@@ -327,6 +348,14 @@ DeviceBuffer* Learner::margin_cache(DMatrix& data) {
   return &d_margin_;
 }
 
+int Learner::bin_layout() const {
+  const std::string v = param("hip_bin_layout", "auto");
+  if (v == "auto") return 0;
+  if (v == "row") return 1;
+  if (v == "group") return 2;
+  throw Error("hip_bin_layout must be auto, row or group, got '" + v + "'.");
+}
+
 void Learner::configure_rng() {
   const std::string seed = param("seed", "0");
   if (seed != rng_seed_) {
@@ -395,7 +424,12 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   shape.cols = data.cols;
   shape.max_bin = data.hist_bins;
   shape.max_depth = depth;
-  shape.rows_per_tile = (uint32_t)integer("hip_histogram_rows", data.rows >= 262144 ? 4096 : 2048);
+  // Rows per histogram tile: small enough for a few hundred workgroups at the
+  // root, large enough that the per-tile partial histograms (F x (bins+1) x
+  // 16 bytes each) stay well below the bin matrix they summarise.
+  uint32_t tile = data.rows >= 262144 ? 4096 : 2048;
+  while (tile < 65536 && (uint64_t)tile * 160 < data.rows) tile *= 2;
+  shape.rows_per_tile = (uint32_t)integer("hip_histogram_rows", tile);
   shape.features_per_group = data.features_per_group;
   shape.unit_hessian = unit_hessian ? 1 : 0;
   shape.dense = data.has_missing ? 0 : 1;
@@ -454,9 +488,16 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
   require(data.labels.size() == data.rows, "Labels must be provided for training (one per row).");
   require(data.weights.empty() || data.weights.size() == data.rows, "Number of weights must equal the number of rows.");
   int obj = objective();
-  if (obj == 1 || obj == 2)
-    for (float y : data.labels) require(y >= 0 && y <= 1, "label must be in [0,1] for logistic loss.");
-  data.quantize((uint32_t)integer("max_bin", 256));
+  if (obj == 1 || obj == 2) {
+    if (data.labels_in_unit < 0) {
+      // Checked once per label assignment, not every round.
+      data.labels_in_unit = 1;
+      for (float y : data.labels)
+        if (!(y >= 0 && y <= 1)) { data.labels_in_unit = 0; break; }
+    }
+    require(data.labels_in_unit == 1, "label must be in [0,1] for logistic loss.");
+  }
+  data.quantize((uint32_t)integer("max_bin", 256), bin_layout());
   auto t0 = std::chrono::steady_clock::now();
   initialize(data, false);
   DeviceBuffer* margin = margin_cache(data);
@@ -488,7 +529,7 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
 void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t count) {
   configure_check();
   require(count == data.rows, "Gradient and Hessian must have one entry per row.");
-  data.quantize((uint32_t)integer("max_bin", 256));
+  data.quantize((uint32_t)integer("max_bin", 256), bin_layout());
   initialize(data, true);
   std::vector<float> gh(2 * count);
   for (size_t i = 0; i < count; ++i) { gh[2 * i] = grad[i]; gh[2 * i + 1] = hess[i]; }

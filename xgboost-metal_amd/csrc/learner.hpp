@@ -60,7 +60,9 @@ struct DMatrix {
   // Device state.
   DeviceBuffer d_data, d_labels, d_weights;
   bool data_uploaded = false, labels_uploaded = false, weights_uploaded = false;
+  int labels_in_unit = -1;            // all labels in [0, 1]: 1 / 0, -1 = not checked since set
   uint32_t quantized_max_bin = 0;     // requested max_bin of the bins below (0: none)
+  int quantized_layout = 0;           // layout request the bins below were built for
   uint32_t hist_bins = 0;             // bins per feature in histograms = min(max_bin, rows)
   uint32_t features_per_group = 16;
   bool has_missing = false;
@@ -73,7 +75,10 @@ struct DMatrix {
   DMatrix();
   void upload();
   void upload_info();
-  void quantize(uint32_t max_bin);
+  // Cuts and bin matrix for max_bin; layout 0 = automatic (group-major when a
+  // row's codes exceed 128 bytes), 1 = row-major, 2 = group-major.
+  void quantize(uint32_t max_bin, int layout = 0);
+  void relayout(int layout);
   void set_info(const std::string& field, const float* values, size_t count);
   const std::vector<float>& get_info(const std::string& field) const;
 };
@@ -125,6 +130,7 @@ class Learner {
   void initialize(DMatrix& data, bool custom);
   void grow(DMatrix& data, bool unit_hessian);
   void configure_rng();
+  int bin_layout() const;
   // Per-round row-sampling parameters (src/learner.cpp:679, src/sampling.cpp:11-17).
   void sample_rows(DMatrix& data, MgbGradParams& gp);
   // The tree's column sample as per-feature flags on the device, or NULL.

@@ -543,6 +543,8 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
   if (!cols) return 0;
   hipStream_t s = stream();
   const uint64_t total = (uint64_t)rows * cols;
+  // Element indices are 32-bit and the segmented sort counts in int.
+  if (total >= (1ull << 31)) { set_error("sketch: rows*cols must be below 2^31"); return -1; }
   DeviceBuffer xt, run_v, run_w, run_start, elem_w, stats_d, keys_in, keys_out;
   if (xt.alloc(total * 4) || run_v.alloc(total * 4) || run_w.alloc(total * 4) || run_start.alloc(total * 4) ||
       stats_d.alloc(cols * sizeof(SkStats)) || keys_in.alloc(total * 8) || keys_out.alloc(total * 8))
@@ -591,7 +593,6 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
     work_total += 2 * (2ull * limit + 2);
     scratch_total += 2ull * limit + 4;
   }
-  if (total >= (1ull << 32)) { set_error("sketch: rows*cols must be below 2^32"); return -1; }
   DeviceBuffer levels_d, work_d, scratch_d, feat_d, values_d, seg_b, seg_e, temp;
   if (levels_d.alloc(lvl_total * sizeof(SkEntry)) || work_d.alloc(work_total * sizeof(SkEntry)) ||
       feat_d.alloc(cols * sizeof(SkFeature)) || values_d.alloc((uint64_t)cols * max_bin * 4))

@@ -112,6 +112,7 @@ struct Tree {
   uint32_t max_depth, slots, rows_per_tile, groups;
   uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
   uint64_t hist_entry;                       // int64 words per node histogram
+  uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
 };
 
@@ -410,7 +411,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     __syncthreads();
     const uint32_t fbase = group * G;
     const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
-    const uint32_t goff = group * G * sizeof(BinT);
+    const uint8_t* gbins = bins + (uint64_t)group * t.group_stride;
     // kHistUnroll rows per thread per pass: every row id, gradient pair and
     // code chunk is requested before the first LDS atomic, so each wave keeps
     // several gathered loads in flight.
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
       for (int u = 0; u < kHistUnroll; ++u) {
         if (valid[u]) {
           gh[u] = t.grad[row[u]];
-          c[u].load(bins + (uint64_t)row[u] * t.row_stride + goff);
+          c[u].load(gbins + (uint64_t)row[u] * t.row_stride);
         }
       }
 #pragma unroll
@@ -974,9 +975,11 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
 // ---------------------------------------------------------------------------
 template <typename BinT>
 __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint32_t row) {
-  const BinT* rowp = reinterpret_cast<const BinT*>(reinterpret_cast<const uint8_t*>(t.bins) +
-                                                   (uint64_t)row * t.row_stride);
-  uint32_t code = rowp[op.feature];
+  const uint32_t G = t.features_per_group;
+  const BinT* codes = reinterpret_cast<const BinT*>(reinterpret_cast<const uint8_t*>(t.bins) +
+                                                    (uint64_t)(op.feature / G) * t.group_stride +
+                                                    (uint64_t)row * t.row_stride);
+  uint32_t code = codes[op.feature % G];
   if (code == t.missing_code) return op.default_left != 0;
   return (int32_t)code <= op.last_left_bin;
 }
@@ -1194,9 +1197,11 @@ int validate(const MgbTreeShape* s, const MgbMatrix* m) {
   uint32_t G = s->features_per_group;
   if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) { set_error("features_per_group must be a power of two <= 16"); return -1; }
   uint32_t groups = div_up(m->cols, G);
-  if ((uint64_t)groups * G * m->bin_bytes > m->row_stride) { set_error("row_stride does not cover the feature groups"); return -1; }
-  if ((G * m->bin_bytes) % 4 == 0 && m->row_stride % 4) { set_error("row_stride must be 4-byte aligned"); return -1; }
-  if (G * m->bin_bytes >= 16 && m->row_stride % 16) { set_error("row_stride must be 16-byte aligned"); return -1; }
+  if (m->group_features != G) { set_error("features_per_group does not match the bin matrix's groups"); return -1; }
+  const uint64_t gbytes = (uint64_t)G * m->bin_bytes;
+  const bool row_major = m->group_stride == gbytes && m->row_stride == groups * gbytes;
+  const bool group_major = m->row_stride == gbytes && m->group_stride == (uint64_t)m->rows * gbytes;
+  if (!row_major && !group_major) { set_error("bin matrix strides describe neither layout"); return -1; }
   if (s->rows_per_tile < 64) { set_error("rows_per_tile must be >= 64"); return -1; }
   if (m->max_bin < 1 || m->max_bin > 1086) { set_error("max_bin must be in [1, 1086]"); return -1; }
   if ((size_t)G * (m->max_bin + 1) * 16 > 160 * 1024) { set_error("feature group does not fit in LDS"); return -1; }
@@ -1226,6 +1231,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.partials = reinterpret_cast<int64_t*>(ws + L.partials);
   t.rows_n = s->rows; t.cols = s->cols; t.max_bin = m->max_bin; t.bins1 = m->max_bin + 1;
   t.row_stride = m->row_stride; t.bin_bytes = m->bin_bytes; t.missing_code = m->missing_code;
+  t.group_stride = m->group_stride;
   t.cut_stride = m->cut_stride;
   t.max_depth = s->max_depth; t.slots = L.slots; t.rows_per_tile = s->rows_per_tile;
   t.features_per_group = s->features_per_group;
