@@ -181,6 +181,43 @@ def test_regularisation_parity(xgb, params):
     np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
 
 
+def _tie_matrix(rows, seed):
+    """Columns that repeat or monotonically transform earlier ones (equal
+    partitions, so equal gains across features) beside few-valued integer
+    columns (many equal Hessian counts at bin edges)."""
+    rng = np.random.default_rng(seed)
+    base = rng.normal(size=(rows, 4)).astype(np.float32)
+    ints = rng.integers(0, 6, size=(rows, 3)).astype(np.float32)
+    X = np.concatenate([base, base[:, :2], 2.0 * base[:, 2:3] + 1.0, ints, ints[:, :1]], axis=1).astype(np.float32)
+    y = (base[:, 0] - 0.5 * base[:, 1] + 0.3 * ints[:, 0] + 0.1 * rng.normal(size=rows)).astype(np.float32)
+    return X, y
+
+
+@pytest.mark.parametrize("label_scale,params", [
+    (1.0, {"max_depth": 6, "max_bin": 64, "min_child_weight": 5}),
+    (1.0, {"max_depth": 6, "max_bin": 256, "lambda": 0.0, "min_child_weight": 0}),
+    (1e-2, {"max_depth": 5, "max_bin": 32, "lambda": 0.001, "min_child_weight": 0}),
+    (1e12, {"max_depth": 5, "max_bin": 32}),
+    (1e15, {"max_depth": 5, "max_bin": 32, "min_child_weight": 2}),
+    (1e18, {"max_depth": 5, "max_bin": 32, "min_child_weight": 2}),
+    (1.0, {"max_depth": 5, "max_bin": 64, "alpha": 0.2, "min_child_weight": 3}),
+])
+def test_split_gain_bounds_parity(xgb, label_scale, params):
+    """The split kernel scores exactly only the candidates whose division-free
+    gain bounds reach the node's best lower bound; equal gains across
+    features, Hessian sums on the min_child_weight boundary, and gradient
+    magnitudes near the ends of the float range must still pick the oracle's
+    first strictly greater candidate."""
+    X, y = _tie_matrix(3000, 11)
+    y = (y * np.float32(label_scale)).astype(np.float32)
+    params = dict(params, objective="reg:squarederror", tree_method="hist", eta=0.3)
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train(params, d, 4)
+    ref = O.train(X, y, _oracle_params(params), 4)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+
+
 def test_weighted_regression_parity(xgb):
     X, y = W.config0(rows=20000, cols=8)
     w = np.random.default_rng(144).uniform(0.1, 2.0, len(X)).astype(np.float32)
@@ -279,12 +316,14 @@ def _config4_small(rows=40000, seed=5):
     return X, y
 
 
-def test_sampled_1024_bins_depth10_parity(xgb):
-    """1024 bins (u16 codes, 4 features per histogram workgroup), depth 10,
-    subsample 0.8 and colsample_bytree 0.8: bit-identical trees and margins."""
+@pytest.mark.parametrize("group", [0, 4])
+def test_sampled_1024_bins_depth10_parity(xgb, group):
+    """1024 bins (u16 codes; 8 features per histogram workgroup by the LDS
+    rule, or 4 on request), depth 10, subsample 0.8 and colsample_bytree 0.8:
+    bit-identical trees and margins."""
     X, y = _config4_small()
     params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
-              "subsample": 0.8, "colsample_bytree": 0.8}
+              "subsample": 0.8, "colsample_bytree": 0.8, "hip_histogram_features": group}
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(params, d, 5)
     ref = O.train(X, y, _oracle_params(params), 5)

@@ -385,7 +385,8 @@ int XGDMatrixGetQuantileCut(DMatrixHandle const handle, char const* config, char
   }
   if (!max_bin && d.is_quantile) max_bin = d.quantile_max_bin;
   require(max_bin != 0, "The DMatrix has no quantile cuts yet; train a booster on it first.");
-  d.quantize(max_bin, d.quantized_max_bin == max_bin ? d.quantized_layout : 0);
+  const bool same = d.quantized_max_bin == max_bin;
+  d.quantize(max_bin, same ? d.quantized_layout : 0, same ? d.quantized_group_request : 0);
   g_results.indptr.assign(1, 0);
   g_results.values.clear();
   for (uint32_t f = 0; f < d.cols; ++f) {

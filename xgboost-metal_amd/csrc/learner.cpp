@@ -94,11 +94,33 @@ static uint32_t next_pow2(uint32_t v) {
   return p;
 }
 
-void DMatrix::quantize(uint32_t max_bin, int layout) {
+// Features per histogram workgroup: the largest power of two (at most 16, at
+// most the feature count rounded up) whose LDS histogram (16 bytes per bin)
+// fits in the 160 KB of a CU.  Wider groups cut the bytes each row-major row
+// costs the L2->L1 path per workgroup; on 10M x 128 rows with 1024 bins, 8
+// features (one workgroup per CU) build the histograms 1.7x faster than 4
+// (two per CU).  A request (hip_histogram_features) overrides the rule.
+uint32_t DMatrix::choose_group(uint32_t request) const {
+  if (request) {
+    require(request <= 16 && (request & (request - 1)) == 0, "hip_histogram_features must be 1, 2, 4, 8 or 16.");
+    require((size_t)request * (hist_bins + 1) * 16 <= 160 * 1024,
+            "hip_histogram_features: the feature group's histogram does not fit in 160 KB of LDS.");
+    return request;
+  }
+  uint32_t G = 16;
+  while (G > 1 && (size_t)G * (hist_bins + 1) * 16 > 160 * 1024) G >>= 1;
+  return std::min(G, next_pow2(cols));
+}
+
+void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
   require(max_bin >= 2, "max_bin must be at least 2.");
   require(layout >= 0 && layout <= 2, "hip_bin_layout must be auto, row or group.");
-  if (quantized_max_bin == max_bin && quantized_layout == layout) return;
   if (quantized_max_bin == max_bin) {
+    if (quantized_layout == layout && quantized_group_request == group_request) return;
+    const uint32_t G = choose_group(group_request);
+    features_per_group = G;
+    matrix.group_features = G;
+    quantized_group_request = group_request;
     relayout(layout);
     return;
   }
@@ -131,10 +153,9 @@ void DMatrix::quantize(uint32_t max_bin, int layout) {
   // missing code (so at most 255 bins); a matrix without missing values uses
   // all 256 codes and a missing code no byte can equal.
   uint32_t bin_bytes = (has_missing ? max_count <= 255 : max_count <= 256) ? 1 : 2;
-  uint32_t G = 16;
-  while (G > 1 && (size_t)G * (hist_bins + 1) * 16 > 66000) G >>= 1;
-  G = std::min(G, next_pow2(cols));
+  const uint32_t G = choose_group(group_request);
   features_per_group = G;
+  quantized_group_request = group_request;
   matrix.rows = rows;
   matrix.cols = cols;
   matrix.bin_bytes = bin_bytes;
@@ -497,7 +518,7 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
     }
     require(data.labels_in_unit == 1, "label must be in [0,1] for logistic loss.");
   }
-  data.quantize((uint32_t)integer("max_bin", 256), bin_layout());
+  data.quantize((uint32_t)integer("max_bin", 256), bin_layout(), (uint32_t)integer("hip_histogram_features", 0));
   auto t0 = std::chrono::steady_clock::now();
   initialize(data, false);
   DeviceBuffer* margin = margin_cache(data);
@@ -529,7 +550,7 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
 void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t count) {
   configure_check();
   require(count == data.rows, "Gradient and Hessian must have one entry per row.");
-  data.quantize((uint32_t)integer("max_bin", 256), bin_layout());
+  data.quantize((uint32_t)integer("max_bin", 256), bin_layout(), (uint32_t)integer("hip_histogram_features", 0));
   initialize(data, true);
   std::vector<float> gh(2 * count);
   for (size_t i = 0; i < count; ++i) { gh[2 * i] = grad[i]; gh[2 * i + 1] = hess[i]; }

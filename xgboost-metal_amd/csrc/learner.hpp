@@ -63,6 +63,7 @@ struct DMatrix {
   int labels_in_unit = -1;            // all labels in [0, 1]: 1 / 0, -1 = not checked since set
   uint32_t quantized_max_bin = 0;     // requested max_bin of the bins below (0: none)
   int quantized_layout = 0;           // layout request the bins below were built for
+  uint32_t quantized_group_request = 0;  // hip_histogram_features request (0: rule)
   uint32_t hist_bins = 0;             // bins per feature in histograms = min(max_bin, rows)
   uint32_t features_per_group = 16;
   bool has_missing = false;
@@ -77,7 +78,8 @@ struct DMatrix {
   void upload_info();
   // Cuts and bin matrix for max_bin; layout 0 = automatic (group-major when a
   // row's codes exceed 128 bytes), 1 = row-major, 2 = group-major.
-  void quantize(uint32_t max_bin, int layout = 0);
+  void quantize(uint32_t max_bin, int layout = 0, uint32_t group_request = 0);
+  uint32_t choose_group(uint32_t request) const;
   void relayout(int layout);
   void set_info(const std::string& field, const float* values, size_t count);
   const std::vector<float>& get_info(const std::string& field) const;

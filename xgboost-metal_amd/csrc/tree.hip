@@ -61,6 +61,14 @@ struct Cand {
   int64_t lg, lh, rg, rh;
 };
 
+// Per (node, feature): the feature's best candidate, rebuilt in full by the
+// select kernel for the node's winning feature only.
+struct SplitRec {
+  float gain;
+  uint32_t order;   // b (missing right) or 2*count-1-b (missing left)
+  int64_t lg, lh;   // left child sums
+};
+
 struct NodeOp {
   uint32_t op, feature;
   int32_t last_left_bin;
@@ -88,7 +96,7 @@ struct Tree {
   uint32_t* rows[2];
   int64_t* hist[2];
   Frontier* frontier[2];
-  Cand* cands;
+  SplitRec* recs;             // per (frontier slot, feature): the feature's best candidate
   unsigned long long* best;   // per frontier slot, see best_key
   NodeOp* ops;
   HistTask* hist_tasks;
@@ -526,78 +534,87 @@ __device__ __forceinline__ void try_candidate(NodeEval& n, uint64_t lg, uint64_t
   }
 }
 
-// Candidates at this lane's bin b: v = the bin's (g, h), (lg, lh) = exact
-// sums of bins [0, b].
-__device__ __forceinline__ void eval_bin(NodeEval& n, uint64_t vg, uint64_t vh, uint64_t lg, uint64_t lh, uint32_t b,
-                                         uint32_t count, int eg, int eh, float mcw, const MgbSplitParams& p) {
+// Division-free bounds on a candidate's float gain.  With reg_alpha = 0 and
+// max_delta_step = 0 the scorer's child gain is -(2Gw + (H+lambda)w^2) for the
+// float weight w = -G/(H+lambda) (1+d), |d| <= 2^-24, which is exactly
+// G^2/(H+lambda) (1 - d^2); after the binary64 and float roundings the
+// candidate's gain lies within M * 2^-20.2 of the fp32 estimate
+// GL^2/(HL+l) + GR^2/(HR+l) - parent, M = the magnitudes summed (fp32
+// conversions, reciprocal and products contribute at most 2^-20.6 relative).
+// The bounds below use M * 2^-17 + 2^-120, so every candidate whose gain can
+// reach the best lower bound of its node is scored exactly; the rest cannot
+// be the first strictly greater candidate.  lo = -inf: not certainly valid
+// (it takes no part in the node's best lower bound); hi = -inf: certainly
+// invalid (Hessian sums not positive or below min_child_weight).
+__device__ __forceinline__ float magnitude_f32(uint64_t v) {
+  const uint64_t m = (int64_t)v < 0 ? 0 - v : v;
+  return fmaf((float)(uint32_t)(m >> 32), 4294967296.0f, (float)(uint32_t)m);
+}
+
+__device__ __forceinline__ void gain_bounds(const NodeEval& n, uint64_t lg, uint64_t lh, int eg, int eh, float mcw,
+                                            bool filter, float lambda, float& lo, float& hi) {
+  const uint64_t rg = n.tg - lg, rh = n.th - lh;
+  lo = -INFINITY;
+  hi = -INFINITY;
+  if ((int64_t)lh <= 0 || (int64_t)rh <= 0) return;  // HL > 0 or HR > 0 fails (the conversion keeps the sign)
+  // hl, hr are within 2^-22 of HL, HR while they stay normal floats.
+  const float hl = ldexpf(magnitude_f32(lh), -eh), hr = ldexpf(magnitude_f32(rh), -eh);
+  constexpr float tol = 0x1p-20f;
+  if (mcw > 0x1p-100f && (hl < mcw * (1.0f - tol) || hr < mcw * (1.0f - tol))) return;
+  const float need = fmaxf(mcw * (1.0f + tol), 0x1p-100f);
+  const bool certain = mcw == 0.0f || (hl >= need && hr >= need);
+  hi = INFINITY;
+  if (!filter) return;
+  // Every operand a normal float away from both ends of the range, so each
+  // rounding is relative; otherwise the candidate is scored exactly.
+  const float dl = hl + lambda, dr = hr + lambda;
+  if (!(dl >= 0x1p-100f && dr >= 0x1p-100f && dl <= 0x1p100f && dr <= 0x1p100f)) return;
+  const float gl = ldexpf(magnitude_f32(lg), -eg), gr = ldexpf(magnitude_f32(rg), -eg);
+  if ((gl != 0.0f && gl < 0x1p-50f) || (gr != 0.0f && gr < 0x1p-50f)) return;
+  const float al = (gl * gl) * __builtin_amdgcn_rcpf(dl);
+  const float ar = (gr * gr) * __builtin_amdgcn_rcpf(dr);
+  const float m = (al + ar) + fabsf(n.parent_gain);
+  if (!(m <= 0x1p100f)) return;  // huge, infinite or NaN
+  const float a = (al + ar) - n.parent_gain;
+  const float e = m * 0x1p-17f + 0x1p-120f;
+  hi = a + e;
+  if (certain) lo = a - e;
+}
+
+// Bounds of this lane's forward and backward candidates at bin b (same
+// arguments as eval_bin); folds certain lower bounds into best_lo.
+__device__ __forceinline__ void bound_bin(const NodeEval& n, uint64_t vg, uint64_t vh, uint64_t lg, uint64_t lh,
+                                          uint32_t b, uint32_t count, int eg, int eh, float mcw, bool filter,
+                                          float lambda, float& hi_f, float& hi_b, float& best_lo) {
+  hi_f = hi_b = -INFINITY;
   if (b >= count) return;
-  try_candidate(n, lg, lh, b, eg, eh, mcw, p);  // forward: missing right
-  if (n.has_missing) {                           // backward: right = bins [b, count)
+  float lo;
+  gain_bounds(n, lg, lh, eg, eh, mcw, filter, lambda, lo, hi_f);
+  best_lo = fmaxf(best_lo, lo);
+  if (n.has_missing) {
+    const uint64_t rg = n.pg - (lg - vg), rh = n.ph - (lh - vh);
+    gain_bounds(n, n.tg - rg, n.th - rh, eg, eh, mcw, filter, lambda, lo, hi_b);
+    best_lo = fmaxf(best_lo, lo);
+  }
+}
+
+// Exact scoring of the candidates whose upper bound reaches the node's best
+// lower bound.
+__device__ __forceinline__ void eval_bin_bounded(NodeEval& n, uint64_t vg, uint64_t vh, uint64_t lg, uint64_t lh,
+                                                 uint32_t b, uint32_t count, int eg, int eh, float mcw,
+                                                 const MgbSplitParams& p, float hi_f, float hi_b, float node_lo) {
+  if (b >= count) return;
+  if (hi_f > -INFINITY && hi_f >= node_lo) try_candidate(n, lg, lh, b, eg, eh, mcw, p);
+  if (n.has_missing && hi_b > -INFINITY && hi_b >= node_lo) {
     const uint64_t rg = n.pg - (lg - vg), rh = n.ph - (lh - vh);
     try_candidate(n, n.tg - rg, n.th - rh, 2 * count - 1 - b, eg, eh, mcw, p);
   }
 }
 
-// Per-wave best of one node, parked in LDS for the workgroup argmax.
-struct WaveBest {
-  float gain;
-  uint32_t order;
-  uint64_t lg, lh;
-};
-
-__device__ __forceinline__ void wave_best(const NodeEval& n, WaveBest* slot) {
-  float g = n.best_gain;
-  uint32_t o = n.best_order;
+__device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) {
-    const float og = __shfl_xor(g, d, kWave);
-    const uint32_t oo = __shfl_xor(o, d, kWave);
-    if (og > g || (og == g && oo < o)) { g = og; o = oo; }
-  }
-  if (o == 0xffffffffu) {
-    if (lane_id() == 0) *slot = WaveBest{-INFINITY, 0xffffffffu, 0, 0};
-  } else if (n.best_order == o && n.best_gain == g) {
-    *slot = WaveBest{g, o, n.best_lg, n.best_lh};
-  }
-}
-
-// One thread: argmax over the waves' bests, then the full candidate.
-__device__ void node_finish(const NodeEval& n, const WaveBest* waves, uint32_t nwaves, uint32_t count,
-                            const float* cuts_f, int eg, int eh, const MgbSplitParams& p, uint32_t feature, Cand* out,
-                            unsigned long long* node_best) {
-  WaveBest b = waves[0];
-  for (uint32_t k = 1; k < nwaves; ++k) {
-    const WaveBest o = waves[k];
-    if (o.gain > b.gain || (o.gain == b.gain && o.order < b.order)) b = o;
-  }
-  Cand c;
-  c.parent_w = n.w;
-  c.total_h = (float)n.H;
-  c.padding = 0;
-  if (b.order == 0xffffffffu) {  // no valid candidate: feature -1, gain -inf
-    c.gain = -INFINITY; c.feature = -1; c.bin = 0; c.default_left = 0; c.threshold = 0;
-    c.left_w = n.w; c.right_w = n.w; c.left_h = 0; c.right_h = 0;
-    c.lg = c.lh = c.rg = c.rh = 0;
-    *out = c;
-    return;
-  }
-  const uint32_t backward = b.order >= count ? 1u : 0u;
-  const uint32_t bin = backward ? 2 * count - 1 - b.order : b.order;
-  const uint64_t rg = n.tg - b.lg, rh = n.th - b.lh;
-  const double GL = stat_value((int64_t)b.lg, eg), HL = stat_value((int64_t)b.lh, eh);
-  const double GR = stat_value((int64_t)rg, eg), HR = stat_value((int64_t)rh, eh);
-  c.gain = b.gain;
-  c.feature = (int32_t)feature;
-  c.bin = bin;
-  c.default_left = backward;
-  c.threshold = backward ? (bin == 0 ? -INFINITY : cuts_f[bin - 1]) : cuts_f[bin];
-  c.left_w = calc_weight(GL, HL, p);
-  c.right_w = calc_weight(GR, HR, p);
-  c.left_h = (float)HL;
-  c.right_h = (float)HR;
-  c.lg = (int64_t)b.lg; c.lh = (int64_t)b.lh; c.rg = (int64_t)rg; c.rh = (int64_t)rh;
-  *out = c;
-  atomicMax(node_best, best_key(b.gain, feature));
+  for (int d = kWave / 2; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, kWave));
+  return v;
 }
 
 __device__ __forceinline__ void load_pair(const int64_t* h, uint32_t bin, uint64_t& g, uint64_t& v) {
@@ -618,91 +635,192 @@ __device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
   return (uint64_t)lo | ((uint64_t)hi << 32);
 }
 
-// Exclusive prefix (over waves < wave) and total of the chunk sums in LDS,
-// kept in scalar registers.
-__device__ __forceinline__ void wave_carry(const uint64_t (*tot)[4], uint32_t nwaves, uint32_t wave, uint64_t (&pre)[4],
-                                           uint64_t (&all)[4]) {
+__device__ __forceinline__ uint64_t lane63_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, kWave - 1);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), kWave - 1);
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) pre[q] = all[q] = 0;
-  for (uint32_t k = 0; k < nwaves; ++k) {
+  for (int d = kWave / 2; d > 0; d >>= 1) {
+    const uint64_t o = __shfl_xor(v, d, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// A lane's best candidate of one node as a key whose maximum is the largest
+// gain and, among equal gains, the smallest order; 0 = no candidate.
+__device__ __forceinline__ uint64_t candidate_key(const NodeEval& n) {
+  if (n.best_order == 0xffffffffu) return 0;
+  const uint32_t bits = n.best_gain == 0.0f ? 0u : __float_as_uint(n.best_gain);
+  const uint32_t order = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+  return ((uint64_t)order << 32) | (uint64_t)(~n.best_order);
+}
+
+constexpr int kSplitBins = 4;  // consecutive bins per lane
+
+// Bins of one (node pair or root, feature) item held by a lane: inclusive
+// in-lane prefix sums of kSplitBins consecutive bins.
+struct LaneBins {
+  uint64_t g[kSplitBins], h[kSplitBins];
+};
+
+// Exclusive prefix of a lane's bin totals over the item's W waves: the wave
+// scan plus (W > 1) the earlier waves' totals exchanged in LDS.  Returns the
+// item total in `all`.  Every wave of the block calls it (barrier inside for
+// W > 1).
+template <int W>
+__device__ __forceinline__ void item_prefix(const uint64_t (&tot_lane)[4], uint64_t (&pre)[4], uint64_t (&all)[4],
+                                            uint64_t (*xchg)[4], uint32_t wave_in_item) {
+  uint64_t inc[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint64_t v = uniform_u64(tot[k][q]);
-      if (k < wave) pre[q] += v;
-      all[q] += v;
+  for (int q = 0; q < 4; ++q) {
+    inc[q] = wave_inclusive_u64(tot_lane[q]);
+    pre[q] = inc[q] - tot_lane[q];
+    all[q] = lane63_u64(inc[q]);
+  }
+  if constexpr (W > 1) {
+    if (lane_id() == 0)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xchg[wave_in_item][q] = all[q];
+    __syncthreads();
+    uint64_t carry[4] = {0, 0, 0, 0}, sum[4] = {0, 0, 0, 0};
+    for (uint32_t k = 0; k < (uint32_t)W; ++k) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint64_t v = uniform_u64(xchg[k][q]);
+        if (k < wave_in_item) carry[q] += v;
+        sum[q] += v;
+      }
     }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) { pre[q] += carry[q]; all[q] = sum[q]; }
   }
 }
 
+// Maximum over the item's waves of a per-wave value (W > 1: LDS + barrier).
 template <int W>
-__global__ __launch_bounds__(W * kWave) void k_split(Tree t, uint32_t depth) {
-  __shared__ uint64_t tot[W][4];
-  __shared__ WaveBest best[2][W];
-  __shared__ uint64_t root_sum[W][2];
-  const uint32_t item = blockIdx.x;
+__device__ __forceinline__ float item_max_f32(float v, float* xchg, uint32_t wave_in_item) {
+  v = wave_max_f32(v);
+  if constexpr (W > 1) {
+    if (lane_id() == 0) xchg[wave_in_item] = v;
+    __syncthreads();
+    v = xchg[0];
+    for (uint32_t k = 1; k < (uint32_t)W; ++k) v = fmaxf(v, xchg[k]);
+  }
+  return v;
+}
+
+template <int W>
+__device__ __forceinline__ uint64_t item_max_u64(uint64_t v, uint64_t* xchg, uint32_t wave_in_item) {
+  v = wave_max_u64(v);
+  if constexpr (W > 1) {
+    if (lane_id() == 0) xchg[wave_in_item] = v;
+    __syncthreads();
+    v = uniform_u64(xchg[0]);
+    for (uint32_t k = 1; k < (uint32_t)W; ++k) {
+      const uint64_t o = uniform_u64(xchg[k]);
+      v = o > v ? o : v;
+    }
+  }
+  return v;
+}
+
+// Scores one node's candidates held by this lane (bins b0 .. b0+kSplitBins-1,
+// in-lane inclusive sums in `lb`, item-exclusive prefix pre_g/pre_h):
+// division-free bounds first, then the exact scorer for every candidate whose
+// upper bound reaches the node's best certain lower bound.  The winner (if
+// any) records its SplitRec and offers its feature to the node's best key.
+template <int W>
+__device__ __forceinline__ void score_node(NodeEval& n, const LaneBins& lb, uint64_t pre_g, uint64_t pre_h, uint32_t b0,
+                                           uint32_t count, int eg, int eh, float mcw, bool filter, float lambda,
+                                           const MgbSplitParams& p, float* xf, uint64_t* xk, uint32_t wave_in_item,
+                                           SplitRec* rec, unsigned long long* node_best, uint32_t feature) {
+  float hi_f[kSplitBins], hi_b[kSplitBins];
+  float lo = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kSplitBins; ++j) {
+    const uint64_t vg = lb.g[j] - (j ? lb.g[j - 1] : 0), vh = lb.h[j] - (j ? lb.h[j - 1] : 0);
+    bound_bin(n, vg, vh, pre_g + lb.g[j], pre_h + lb.h[j], b0 + j, count, eg, eh, mcw, filter, lambda, hi_f[j],
+              hi_b[j], lo);
+  }
+  const float node_lo = item_max_f32<W>(lo, xf, wave_in_item);
+#pragma unroll
+  for (int j = 0; j < kSplitBins; ++j) {
+    const uint64_t vg = lb.g[j] - (j ? lb.g[j - 1] : 0), vh = lb.h[j] - (j ? lb.h[j - 1] : 0);
+    eval_bin_bounded(n, vg, vh, pre_g + lb.g[j], pre_h + lb.h[j], b0 + j, count, eg, eh, mcw, p, hi_f[j], hi_b[j],
+                     node_lo);
+  }
+  const uint64_t mine = candidate_key(n);
+  const uint64_t top = item_max_u64<W>(mine, xk, wave_in_item);
+  if (top != 0 && mine == top) {
+    *rec = SplitRec{n.best_gain, n.best_order, (int64_t)n.best_lg, (int64_t)n.best_lh};
+    atomicMax(node_best, best_key(n.best_gain, feature));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One item = (node pair, feature) below the root, (feature) at the root, and
+// W waves per item with kSplitBins consecutive bins per lane, so every bin of
+// the feature is in registers at once (W * 64 * kSplitBins >= count).  W = 1
+// packs four independent items into a 256-thread block with no barrier; for
+// W > 1 a block is one item, so early exits stay block-uniform.
+// ---------------------------------------------------------------------------
+template <int W>
+__global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t, uint32_t depth) {
+  constexpr uint32_t kItemsPerBlock = W == 1 ? 4 : 1;  // barriers (W > 1) need whole-block items
+  __shared__ uint64_t xtot[kItemsPerBlock][W][4];
+  __shared__ float xlo[kItemsPerBlock][2][W];
+  __shared__ uint64_t xkey[kItemsPerBlock][2][W];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t slot_in_block = wave / W, wave_in_item = wave % W;
+  const uint32_t item = blockIdx.x * kItemsPerBlock + slot_in_block;
   const uint32_t lane = lane_id();
   const LevelState* st = t.state;
   const uint32_t F = t.cols, B1 = t.bins1, MB = t.max_bin;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const float mcw = fabsf(t.sp.min_child_weight);
+  const bool filter = t.sp.reg_alpha == 0.0f && t.sp.max_delta_step == 0.0f;
+  const float lambda = t.sp.reg_lambda;
   int64_t* cur = t.hist[depth & 1];
-  constexpr uint32_t span = W * kWave;  // bins per pass of the workgroup
+  const uint32_t b0 = (wave_in_item * kWave + lane) * kSplitBins;
   if (depth == 0) {
-    if (item >= F) return;
+    if (item >= F) return;  // uniform per item (W > 1: one item per block)
     const uint32_t f = item, count = t.counts[f];
     const int64_t* h = cur + (uint64_t)f * B1 * 2;
-    // Root totals: every bin of the feature, missing slot included.
-    uint64_t sg = 0, sh = 0;
-    for (uint32_t b = threadIdx.x; b < count; b += span) {
-      uint64_t g, v;
-      load_pair(h, b, g, v);
-      sg += g; sh += v;
+    LaneBins x;
+#pragma unroll
+    for (int j = 0; j < kSplitBins; ++j) {
+      uint64_t g = 0, v = 0;
+      if (b0 + j < count) load_pair(h, b0 + j, g, v);
+      x.g[j] = (j ? x.g[j - 1] : 0) + g;
+      x.h[j] = (j ? x.h[j - 1] : 0) + v;
     }
-    sg = wave_sum_u64(sg);
-    sh = wave_sum_u64(sh);
-    if (lane == 0) { root_sum[wave][0] = sg; root_sum[wave][1] = sh; }
-    __syncthreads();
     uint64_t mg, mh;
     load_pair(h, MB, mg, mh);
-    uint64_t tg = mg, th = mh;
-    for (uint32_t k = 0; k < W; ++k) { tg += uniform_u64(root_sum[k][0]); th += uniform_u64(root_sum[k][1]); }
+    const uint64_t lt[4] = {x.g[kSplitBins - 1], x.h[kSplitBins - 1], 0, 0};
+    uint64_t pre[4], all[4];
+    item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
+    // Root totals: every bin of the feature plus its missing slot.
+    const uint64_t tg = all[0] + mg, th = all[1] + mh;
+    if (f == 0 && wave_in_item == 0 && lane == 0) {
+      t.frontier[0][0].sum_g = (int64_t)tg;
+      t.frontier[0][0].sum_h = (int64_t)th;
+    }
+    if (t.allowed && !t.allowed[f]) return;  // outside the tree's column sample
     NodeEval e;
     node_begin(e, tg, th, mg, mh, eg, eh, t.sp);
-    if (t.allowed && !t.allowed[f]) {
-      // Outside the tree's column sample: the candidate only carries the
-      // node's weight and cover (select reads them for feature 0).
-      if (threadIdx.x == 0) {
-        const WaveBest none{-INFINITY, 0xffffffffu, 0, 0};
-        node_finish(e, &none, 1, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f, t.cands + f, t.best);
-      }
-      return;
-    }
-    uint64_t carry_g = 0, carry_h = 0;
-    for (uint32_t base = 0; base < count; base += span) {
-      const uint32_t b = base + wave * kWave + lane;
-      uint64_t g = 0, v = 0;
-      if (b < count) load_pair(h, b, g, v);
-      const uint64_t ig = wave_inclusive_u64(g), ih = wave_inclusive_u64(v);
-      if (lane == kWave - 1) { tot[wave][0] = ig; tot[wave][1] = ih; tot[wave][2] = 0; tot[wave][3] = 0; }
-      __syncthreads();
-      uint64_t pre[4], all[4];
-      wave_carry(tot, W, wave, pre, all);
-      eval_bin(e, g, v, carry_g + pre[0] + ig, carry_h + pre[1] + ih, b, count, eg, eh, mcw, t.sp);
-      carry_g += all[0];
-      carry_h += all[1];
-      __syncthreads();
-    }
-    wave_best(e, &best[0][wave]);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      node_finish(e, best[0], W, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f, t.cands + f, t.best);
+    score_node<W>(e, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
+                  xkey[slot_in_block][0], wave_in_item, t.recs + f, t.best, f);
     return;
   }
   const uint32_t n = st->n_nodes;
   const uint32_t pairs = n / 2;
   if (item >= pairs * F) return;
   const uint32_t pair = item / F, f = item % F;
+  if (t.allowed && !t.allowed[f]) return;  // this tree never scores the feature: no sibling either
   const Frontier* fr = t.frontier[depth & 1];
   const Frontier a = fr[2 * pair], b = fr[2 * pair + 1];
   const uint32_t built = a.built ? 2 * pair : 2 * pair + 1, other = built ^ 1u;
@@ -713,63 +831,39 @@ __global__ __launch_bounds__(W * kWave) void k_split(Tree t, uint32_t depth) {
   int64_t* ob = cur + ((uint64_t)other * F + f) * B1 * 2;
   const bool store_other = depth + 1 < t.max_depth;
   const uint32_t count = t.counts[f];
-  if (t.allowed && !t.allowed[f]) {
-    // Outside the tree's column sample: no candidate and no sibling histogram
-    // (this tree never scores the feature).  The candidates still carry the
-    // nodes' weights and covers.
-    if (threadIdx.x < 2) {
-      const Frontier& fn = threadIdx.x == 0 ? fb : fo;
-      const uint32_t slot = threadIdx.x == 0 ? built : other;
-      NodeEval e;
-      node_begin(e, (uint64_t)fn.sum_g, (uint64_t)fn.sum_h, 0, 0, eg, eh, t.sp);
-      const WaveBest none{-INFINITY, 0xffffffffu, 0, 0};
-      node_finish(e, &none, 1, count, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, t.sp, f,
-                  t.cands + (uint64_t)slot * F + f, t.best + slot);
-    }
-    return;
-  }
   // Missing slots first: they give each child's present-bin totals.
   uint64_t pmg, pmh, xmg, xmh;
   load_pair(parent, MB, pmg, pmh);
   load_pair(xb, MB, xmg, xmh);
   const uint64_t omg = pmg - xmg, omh = pmh - xmh;
-  if (store_other && threadIdx.x == 0) store_pair(ob, MB, omg, omh);
+  if (store_other && wave_in_item == 0 && lane == 0) store_pair(ob, MB, omg, omh);
+  LaneBins x, o;
+#pragma unroll
+  for (int j = 0; j < kSplitBins; ++j) {
+    uint64_t xg = 0, xh = 0, og = 0, oh = 0;
+    if (b0 + j < count) {
+      uint64_t pg, ph;
+      load_pair(parent, b0 + j, pg, ph);
+      load_pair(xb, b0 + j, xg, xh);
+      og = pg - xg;
+      oh = ph - xh;
+      if (store_other) store_pair(ob, b0 + j, og, oh);
+    }
+    x.g[j] = (j ? x.g[j - 1] : 0) + xg;
+    x.h[j] = (j ? x.h[j - 1] : 0) + xh;
+    o.g[j] = (j ? o.g[j - 1] : 0) + og;
+    o.h[j] = (j ? o.h[j - 1] : 0) + oh;
+  }
+  const uint64_t lt[4] = {x.g[kSplitBins - 1], x.h[kSplitBins - 1], o.g[kSplitBins - 1], o.h[kSplitBins - 1]};
+  uint64_t pre[4], all[4];
+  item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
   NodeEval ex, eo;
   node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
   node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
-  uint64_t carry[4] = {0, 0, 0, 0};
-  for (uint32_t base = 0; base < count; base += span) {
-    const uint32_t bin = base + wave * kWave + lane;
-    uint64_t xg = 0, xh = 0, og = 0, oh = 0;
-    if (bin < count) {
-      uint64_t pg, ph;
-      load_pair(parent, bin, pg, ph);
-      load_pair(xb, bin, xg, xh);
-      og = pg - xg;
-      oh = ph - xh;
-      if (store_other) store_pair(ob, bin, og, oh);
-    }
-    const uint64_t ixg = wave_inclusive_u64(xg), ixh = wave_inclusive_u64(xh);
-    const uint64_t iog = wave_inclusive_u64(og), ioh = wave_inclusive_u64(oh);
-    if (lane == kWave - 1) { tot[wave][0] = ixg; tot[wave][1] = ixh; tot[wave][2] = iog; tot[wave][3] = ioh; }
-    __syncthreads();
-    uint64_t pre[4], all[4];
-    wave_carry(tot, W, wave, pre, all);
-    eval_bin(ex, xg, xh, carry[0] + pre[0] + ixg, carry[1] + pre[1] + ixh, bin, count, eg, eh, mcw, t.sp);
-    eval_bin(eo, og, oh, carry[2] + pre[2] + iog, carry[3] + pre[3] + ioh, bin, count, eg, eh, mcw, t.sp);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) carry[q] += all[q];
-    __syncthreads();
-  }
-  wave_best(ex, &best[0][wave]);
-  wave_best(eo, &best[1][wave]);
-  __syncthreads();
-  const float* cuts_f = t.cuts + (uint64_t)f * t.cut_stride;
-  // Threads 0 and 1 finish the two children (both exist for every W).
-  if (threadIdx.x == 0)
-    node_finish(ex, best[0], W, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)built * F + f, t.best + built);
-  else if (threadIdx.x == 1)
-    node_finish(eo, best[1], W, count, cuts_f, eg, eh, t.sp, f, t.cands + (uint64_t)other * F + f, t.best + other);
+  score_node<W>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
+                xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f, t.best + built, f);
+  score_node<W>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
+                xkey[slot_in_block][1], wave_in_item, t.recs + (uint64_t)other * F + f, t.best + other, f);
 }
 
 // ---------------------------------------------------------------------------
@@ -778,6 +872,32 @@ __global__ __launch_bounds__(W * kWave) void k_split(Tree t, uint32_t depth) {
 // pop/apply, :1663-1717 replay).  One workgroup handles the whole level in
 // node-id order, so child ids follow XGBoost's numbering.
 // ---------------------------------------------------------------------------
+// Full candidate of a node (totals in n) from its winning feature's record:
+// the split kernel's scorer arithmetic for the chosen bin and direction.
+__device__ Cand make_cand(const NodeEval& n, const SplitRec& r, uint32_t feature, uint32_t count, const float* cuts_f,
+                          int eg, int eh, const MgbSplitParams& p) {
+  Cand c;
+  c.parent_w = n.w;
+  c.total_h = (float)n.H;
+  c.padding = 0;
+  const uint32_t backward = r.order >= count ? 1u : 0u;
+  const uint32_t bin = backward ? 2 * count - 1 - r.order : r.order;
+  const uint64_t lg = (uint64_t)r.lg, lh = (uint64_t)r.lh, rg = n.tg - lg, rh = n.th - lh;
+  const double GL = stat_value((int64_t)lg, eg), HL = stat_value((int64_t)lh, eh);
+  const double GR = stat_value((int64_t)rg, eg), HR = stat_value((int64_t)rh, eh);
+  c.gain = r.gain;
+  c.feature = (int32_t)feature;
+  c.bin = bin;
+  c.default_left = backward;
+  c.threshold = backward ? (bin == 0 ? -INFINITY : cuts_f[bin - 1]) : cuts_f[bin];
+  c.left_w = calc_weight(GL, HL, p);
+  c.right_w = calc_weight(GR, HR, p);
+  c.left_h = (float)HL;
+  c.right_h = (float)HR;
+  c.lg = (int64_t)lg; c.lh = (int64_t)lh; c.rg = (int64_t)rg; c.rh = (int64_t)rh;
+  return c;
+}
+
 // Serial binary64 sums of `steps` bins of a feature staged in LDS (forward
 // from bin 0, or backward from bin count-1), in the reference's order.
 __device__ void ordered_sum(const double* sg, const double* sh, uint32_t steps, bool reverse, uint32_t count,
@@ -817,13 +937,18 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
   const MgbSplitParams& p = t.sp;
   // Dense root: feature 0 and the chosen feature staged in LDS by all threads
   // so the serial ordered sums below read LDS, not scattered global words.
+  // The chosen feature's cuts are staged too: the threshold search below
+  // would otherwise be a chain of dependent global loads.
   __shared__ double root0[2][kMaxBins1], rootf[2][kMaxBins1];
+  __shared__ float rootcut[kMaxBins1];
   const bool dense_root = depth == 0 && t.dense && n > 0;
   if (dense_root) {
     const uint64_t key = t.best[0];
     const uint32_t f = key ? ~(uint32_t)key : 0u;
+    const uint32_t cf = t.counts[f];
     stage_feature(t.hist[0], t.counts[0], eg, eh, root0);
-    stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, t.counts[f], eg, eh, rootf);
+    stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, cf, eg, eh, rootf);
+    for (uint32_t b = threadIdx.x; b < cf; b += blockDim.x) rootcut[b] = t.cuts[(uint64_t)f * t.cut_stride + b];
     __syncthreads();
   }
   uint32_t carry_expanded = 0, carry_tasks = 0;
@@ -838,10 +963,17 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
       node = fr[i];
       const uint64_t key = t.best[i];
       t.best[i] = 0;  // cleared for the next level, which reuses the slot
-      const uint32_t f = key ? ~(uint32_t)key : 0u;
-      best = t.cands[(uint64_t)i * F + f];
-      parent_w = best.parent_w;
-      total_h = best.total_h;
+      NodeEval ne;
+      node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p);
+      parent_w = ne.w;
+      total_h = (float)ne.H;
+      best.feature = -1;
+      best.gain = -INFINITY;
+      if (key) {
+        const uint32_t f = ~(uint32_t)key;
+        best = make_cand(ne, t.recs[(uint64_t)i * F + f], f, t.counts[f], t.cuts + (uint64_t)f * t.cut_stride, eg, eh,
+                         p);
+      }
       expand = best.feature >= 0 && (uint32_t)best.feature < F && best.gain > 1.0e-6f &&
                best.gain >= p.min_split_loss && depth < t.max_depth;
       if (dense_root) {
@@ -853,12 +985,12 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         parent_w = calc_weight(tg, th, p);
         total_h = (float)th;
         if (best.feature >= 0 && (uint32_t)best.feature < F) {
+          // best.feature is the feature of t.best[0], staged in rootcut.
           const uint32_t f = (uint32_t)best.feature, count = t.counts[f];
-          const float* column = t.cuts + (uint64_t)f * t.cut_stride;
           uint32_t lo = 0, hi = count;
           while (lo < hi) {
             uint32_t mid = lo + (hi - lo) / 2;
-            if (column[mid] < best.threshold) lo = mid + 1;
+            if (rootcut[mid] < best.threshold) lo = mid + 1;
             else hi = mid;
           }
           uint32_t steps = lo + 1 < count ? lo + 1 : count;
@@ -1084,7 +1216,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(Tree t, uint32_t dep
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, cands, best, ops, hist_tasks, zero, part_tasks, cursors, partials, total;
+  size_t state, rows, hist, frontier, recs, best, ops, hist_tasks, zero, part_tasks, cursors, partials, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -1103,7 +1235,7 @@ Layout layout(const MgbTreeShape& s) {
   L.rows = off; off = align_up(off + 2 * (size_t)s.rows * sizeof(uint32_t));
   L.hist = off; off = align_up(off + 2 * (size_t)L.slots * L.hist_entry * sizeof(int64_t));
   L.frontier = off; off = align_up(off + 2 * (size_t)(2 * L.slots) * sizeof(Frontier));
-  L.cands = off; off = align_up(off + (size_t)(2 * L.slots) * s.cols * sizeof(Cand));
+  L.recs = off; off = align_up(off + (size_t)(2 * L.slots) * s.cols * sizeof(SplitRec));
   L.best = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint64_t));
   L.ops = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(NodeOp));
   L.hist_tasks = off; off = align_up(off + (size_t)L.max_hist_tasks * sizeof(HistTask));
@@ -1156,21 +1288,22 @@ int dispatch_hist(const Tree& t, uint32_t depth, uint32_t grid) {
   return -1;
 }
 
-// Waves per split workgroup: enough for max_bin bins in one pass, at most 16.
+// Waves per split item: every bin in registers, kSplitBins per lane.
 uint32_t split_waves(uint32_t max_bin) {
   uint32_t w = 1;
-  while (w < 16 && w * kWave < max_bin) w *= 2;
+  while (w < 8 && w * kWave * kSplitBins < max_bin) w *= 2;
   return w;
 }
 
 int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
-  const dim3 grid(items ? items : 1);
-  switch (split_waves(t.max_bin)) {
-    case 1: launch(MGB_PROF_SPLIT, k_split<1>, grid, dim3(kWave), 0, t, depth); break;
-    case 2: launch(MGB_PROF_SPLIT, k_split<2>, grid, dim3(2 * kWave), 0, t, depth); break;
-    case 4: launch(MGB_PROF_SPLIT, k_split<4>, grid, dim3(4 * kWave), 0, t, depth); break;
-    case 8: launch(MGB_PROF_SPLIT, k_split<8>, grid, dim3(8 * kWave), 0, t, depth); break;
-    default: launch(MGB_PROF_SPLIT, k_split<16>, grid, dim3(16 * kWave), 0, t, depth); break;
+  const uint32_t w = split_waves(t.max_bin);
+  if (w * kWave * kSplitBins < t.max_bin) { set_error("max_bin too large for the split kernel"); return -1; }
+  items = items ? items : 1;
+  switch (w) {
+    case 1: launch(MGB_PROF_SPLIT, k_split<1>, dim3(div_up(items, 4)), dim3(4 * kWave), 0, t, depth); break;
+    case 2: launch(MGB_PROF_SPLIT, k_split<2>, dim3(items), dim3(2 * kWave), 0, t, depth); break;
+    case 4: launch(MGB_PROF_SPLIT, k_split<4>, dim3(items), dim3(4 * kWave), 0, t, depth); break;
+    default: launch(MGB_PROF_SPLIT, k_split<8>, dim3(items), dim3(8 * kWave), 0, t, depth); break;
   }
   MGB_LAUNCH_CHECK("k_split");
   return 0;
@@ -1221,7 +1354,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   Frontier* fr = reinterpret_cast<Frontier*>(ws + L.frontier);
   t.frontier[0] = fr;
   t.frontier[1] = fr + 2 * L.slots;
-  t.cands = reinterpret_cast<Cand*>(ws + L.cands);
+  t.recs = reinterpret_cast<SplitRec*>(ws + L.recs);
   t.best = reinterpret_cast<unsigned long long*>(ws + L.best);
   t.ops = reinterpret_cast<NodeOp*>(ws + L.ops);
   t.hist_tasks = reinterpret_cast<HistTask*>(ws + L.hist_tasks);
