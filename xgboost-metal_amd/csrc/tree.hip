@@ -341,10 +341,14 @@ __global__ __launch_bounds__(kReduceWaves * kWave) void k_reduce_hist(Tree t, ui
 // ---------------------------------------------------------------------------
 // Histogram build (kernels/boost.metal:700-773, histogram_tiled.metal.h).
 // One workgroup owns one (row tile, feature group): an LDS-private
-// [G features][max_bin+1] int64 gradient histogram plus a u32 row count
+// [max_bin+1 bins][G features] int64 gradient histogram plus a u32 row count
 // (unit Hessians) or an int64 Hessian histogram, accumulated with LDS
 // integer atomics.  Lanes rotate through the group's features so the 64
-// lanes of a wave hit different features at once.  Gradients are quantized
+// lanes of a wave hit different features at once; with the bin-major,
+// feature-minor layout a feature's entries all sit in the same LDS banks, so
+// at G = 16 the 64 lanes of an atomic spread exactly evenly over the banks
+// whatever the bins are (a feature-major layout leaves the banks to the
+// data, about twice the conflict cycles).  Gradients are quantized
 // on the fly: q = (int64) rint(g * scale), exactly as a stored int64 pair.
 // The flush is a plain store when the tile is the node's only tile, else a
 // 64-bit global atomic add into a cleared histogram.
@@ -452,9 +456,9 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
           uint32_t code = c[u].get(j);
           uint32_t bin = code == t.missing_code ? t.max_bin : code;
           if (j < fcount) {
-            atomicAdd(&lg[j * B1 + bin], qg);
-            if constexpr (UNIT) atomicAdd(&lc[j * B1 + bin], 1u);
-            else atomicAdd(&lh[j * B1 + bin], qh);
+            atomicAdd(&lg[bin * G + j], qg);
+            if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
+            else atomicAdd(&lh[bin * G + j], qh);
           }
         }
       }
@@ -466,12 +470,15 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     const uint32_t task_index = xcd + 8 * (j / t.groups);
     int64_t* out = task.single ? bank + ((uint64_t)task.slot * t.cols + fbase) * B1 * 2
                                : t.partials + ((uint64_t)task_index * t.groups + group) * G * B1 * 2;
-    const uint32_t valid = fcount * B1;
-    for (uint32_t i = threadIdx.x; i < valid; i += blockDim.x) {
+    // LDS is read in its own (bin-major) order, conflict free; each group of
+    // lanes of one feature writes consecutive bins of the feature-major output.
+    for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
+      const uint32_t bin = i / G, j = i % G;
+      if (j >= fcount) continue;
       int64_t g = (int64_t)lg[i];
       int64_t h = UNIT ? (int64_t)((uint64_t)lc[i] * (uint64_t)unit_q) : (int64_t)lh[i];
-      reinterpret_cast<int4*>(out)[i] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
-                                                  (int)(uint32_t)h, (int)(uint32_t)((uint64_t)h >> 32));
+      reinterpret_cast<int4*>(out)[j * B1 + bin] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
+                                                             (int)(uint32_t)h, (int)(uint32_t)((uint64_t)h >> 32));
     }
     __syncthreads();
   }
@@ -659,12 +666,11 @@ __device__ __forceinline__ uint64_t candidate_key(const NodeEval& n) {
   return ((uint64_t)order << 32) | (uint64_t)(~n.best_order);
 }
 
-constexpr int kSplitBins = 4;  // consecutive bins per lane
-
 // Bins of one (node pair or root, feature) item held by a lane: inclusive
-// in-lane prefix sums of kSplitBins consecutive bins.
+// in-lane prefix sums of CH consecutive bins.
+template <int CH>
 struct LaneBins {
-  uint64_t g[kSplitBins], h[kSplitBins];
+  uint64_t g[CH], h[CH];
 };
 
 // Exclusive prefix of a lane's bin totals over the item's W waves: the wave
@@ -728,27 +734,27 @@ __device__ __forceinline__ uint64_t item_max_u64(uint64_t v, uint64_t* xchg, uin
   return v;
 }
 
-// Scores one node's candidates held by this lane (bins b0 .. b0+kSplitBins-1,
+// Scores one node's candidates held by this lane (bins b0 .. b0+CH-1,
 // in-lane inclusive sums in `lb`, item-exclusive prefix pre_g/pre_h):
 // division-free bounds first, then the exact scorer for every candidate whose
 // upper bound reaches the node's best certain lower bound.  The winner (if
 // any) records its SplitRec and offers its feature to the node's best key.
-template <int W>
-__device__ __forceinline__ void score_node(NodeEval& n, const LaneBins& lb, uint64_t pre_g, uint64_t pre_h, uint32_t b0,
+template <int W, int CH>
+__device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, uint64_t pre_g, uint64_t pre_h, uint32_t b0,
                                            uint32_t count, int eg, int eh, float mcw, bool filter, float lambda,
                                            const MgbSplitParams& p, float* xf, uint64_t* xk, uint32_t wave_in_item,
                                            SplitRec* rec, unsigned long long* node_best, uint32_t feature) {
-  float hi_f[kSplitBins], hi_b[kSplitBins];
+  float hi_f[CH], hi_b[CH];
   float lo = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kSplitBins; ++j) {
+  for (int j = 0; j < CH; ++j) {
     const uint64_t vg = lb.g[j] - (j ? lb.g[j - 1] : 0), vh = lb.h[j] - (j ? lb.h[j - 1] : 0);
     bound_bin(n, vg, vh, pre_g + lb.g[j], pre_h + lb.h[j], b0 + j, count, eg, eh, mcw, filter, lambda, hi_f[j],
               hi_b[j], lo);
   }
   const float node_lo = item_max_f32<W>(lo, xf, wave_in_item);
 #pragma unroll
-  for (int j = 0; j < kSplitBins; ++j) {
+  for (int j = 0; j < CH; ++j) {
     const uint64_t vg = lb.g[j] - (j ? lb.g[j - 1] : 0), vh = lb.h[j] - (j ? lb.h[j - 1] : 0);
     eval_bin_bounded(n, vg, vh, pre_g + lb.g[j], pre_h + lb.h[j], b0 + j, count, eg, eh, mcw, p, hi_f[j], hi_b[j],
                      node_lo);
@@ -763,12 +769,13 @@ __device__ __forceinline__ void score_node(NodeEval& n, const LaneBins& lb, uint
 
 // ---------------------------------------------------------------------------
 // One item = (node pair, feature) below the root, (feature) at the root, and
-// W waves per item with kSplitBins consecutive bins per lane, so every bin of
-// the feature is in registers at once (W * 64 * kSplitBins >= count).  W = 1
-// packs four independent items into a 256-thread block with no barrier; for
-// W > 1 a block is one item, so early exits stay block-uniform.
+// W waves per item with CH consecutive bins per lane, so every bin of the
+// feature is in registers at once (W * 64 * CH >= count).  W = 1 packs four
+// independent items into a 256-thread block with no barrier; for W > 1 a
+// block is one item, so early exits stay block-uniform.  Levels with few
+// items spread each over more waves (CH = 1), wide levels use CH = 4.
 // ---------------------------------------------------------------------------
-template <int W>
+template <int W, int CH>
 __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t, uint32_t depth) {
   constexpr uint32_t kItemsPerBlock = W == 1 ? 4 : 1;  // barriers (W > 1) need whole-block items
   __shared__ uint64_t xtot[kItemsPerBlock][W][4];
@@ -785,14 +792,14 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const bool filter = t.sp.reg_alpha == 0.0f && t.sp.max_delta_step == 0.0f;
   const float lambda = t.sp.reg_lambda;
   int64_t* cur = t.hist[depth & 1];
-  const uint32_t b0 = (wave_in_item * kWave + lane) * kSplitBins;
+  const uint32_t b0 = (wave_in_item * kWave + lane) * CH;
   if (depth == 0) {
     if (item >= F) return;  // uniform per item (W > 1: one item per block)
     const uint32_t f = item, count = t.counts[f];
     const int64_t* h = cur + (uint64_t)f * B1 * 2;
-    LaneBins x;
+    LaneBins<CH> x;
 #pragma unroll
-    for (int j = 0; j < kSplitBins; ++j) {
+    for (int j = 0; j < CH; ++j) {
       uint64_t g = 0, v = 0;
       if (b0 + j < count) load_pair(h, b0 + j, g, v);
       x.g[j] = (j ? x.g[j - 1] : 0) + g;
@@ -800,7 +807,7 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
     }
     uint64_t mg, mh;
     load_pair(h, MB, mg, mh);
-    const uint64_t lt[4] = {x.g[kSplitBins - 1], x.h[kSplitBins - 1], 0, 0};
+    const uint64_t lt[4] = {x.g[CH - 1], x.h[CH - 1], 0, 0};
     uint64_t pre[4], all[4];
     item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
     // Root totals: every bin of the feature plus its missing slot.
@@ -812,7 +819,7 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
     if (t.allowed && !t.allowed[f]) return;  // outside the tree's column sample
     NodeEval e;
     node_begin(e, tg, th, mg, mh, eg, eh, t.sp);
-    score_node<W>(e, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
+    score_node<W, CH>(e, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
                   xkey[slot_in_block][0], wave_in_item, t.recs + f, t.best, f);
     return;
   }
@@ -837,9 +844,9 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   load_pair(xb, MB, xmg, xmh);
   const uint64_t omg = pmg - xmg, omh = pmh - xmh;
   if (store_other && wave_in_item == 0 && lane == 0) store_pair(ob, MB, omg, omh);
-  LaneBins x, o;
+  LaneBins<CH> x, o;
 #pragma unroll
-  for (int j = 0; j < kSplitBins; ++j) {
+  for (int j = 0; j < CH; ++j) {
     uint64_t xg = 0, xh = 0, og = 0, oh = 0;
     if (b0 + j < count) {
       uint64_t pg, ph;
@@ -854,15 +861,15 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
     o.g[j] = (j ? o.g[j - 1] : 0) + og;
     o.h[j] = (j ? o.h[j - 1] : 0) + oh;
   }
-  const uint64_t lt[4] = {x.g[kSplitBins - 1], x.h[kSplitBins - 1], o.g[kSplitBins - 1], o.h[kSplitBins - 1]};
+  const uint64_t lt[4] = {x.g[CH - 1], x.h[CH - 1], o.g[CH - 1], o.h[CH - 1]};
   uint64_t pre[4], all[4];
   item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
   NodeEval ex, eo;
   node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
   node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
-  score_node<W>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
+  score_node<W, CH>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
                 xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f, t.best + built, f);
-  score_node<W>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
+  score_node<W, CH>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
                 xkey[slot_in_block][1], wave_in_item, t.recs + (uint64_t)other * F + f, t.best + other, f);
 }
 
@@ -1288,22 +1295,36 @@ int dispatch_hist(const Tree& t, uint32_t depth, uint32_t grid) {
   return -1;
 }
 
-// Waves per split item: every bin in registers, kSplitBins per lane.
+// Waves per split item with four bins per lane (every bin in registers).
 uint32_t split_waves(uint32_t max_bin) {
   uint32_t w = 1;
-  while (w < 8 && w * kWave * kSplitBins < max_bin) w *= 2;
+  while (w < 8 && w * kWave * 4 < max_bin) w *= 2;
   return w;
 }
 
+// Items of a level (upper bound known on the host) below about eight waves
+// per CU take one bin per lane on four times the waves: shallow levels are
+// latency bound, deep ones throughput bound.
 int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
-  const uint32_t w = split_waves(t.max_bin);
-  if (w * kWave * kSplitBins < t.max_bin) { set_error("max_bin too large for the split kernel"); return -1; }
+  const uint32_t w4 = split_waves(t.max_bin);
+  if (w4 * kWave * 4 < t.max_bin) { set_error("max_bin too large for the split kernel"); return -1; }
   items = items ? items : 1;
-  switch (w) {
-    case 1: launch(MGB_PROF_SPLIT, k_split<1>, dim3(div_up(items, 4)), dim3(4 * kWave), 0, t, depth); break;
-    case 2: launch(MGB_PROF_SPLIT, k_split<2>, dim3(items), dim3(2 * kWave), 0, t, depth); break;
-    case 4: launch(MGB_PROF_SPLIT, k_split<4>, dim3(items), dim3(4 * kWave), 0, t, depth); break;
-    default: launch(MGB_PROF_SPLIT, k_split<8>, dim3(items), dim3(8 * kWave), 0, t, depth); break;
+  const bool spread = (uint64_t)items * w4 < 2048 && w4 * 4 <= 16;
+  const uint32_t w = spread ? 4 * w4 : w4;
+  const dim3 grid(w == 1 ? div_up(items, 4) : items), block(w == 1 ? 4 * kWave : w * kWave);
+  if (!spread) {
+    switch (w) {
+      case 1: launch(MGB_PROF_SPLIT, k_split<1, 4>, grid, block, 0, t, depth); break;
+      case 2: launch(MGB_PROF_SPLIT, k_split<2, 4>, grid, block, 0, t, depth); break;
+      case 4: launch(MGB_PROF_SPLIT, k_split<4, 4>, grid, block, 0, t, depth); break;
+      default: launch(MGB_PROF_SPLIT, k_split<8, 4>, grid, block, 0, t, depth); break;
+    }
+  } else {
+    switch (w) {
+      case 4: launch(MGB_PROF_SPLIT, k_split<4, 1>, grid, block, 0, t, depth); break;
+      case 8: launch(MGB_PROF_SPLIT, k_split<8, 1>, grid, block, 0, t, depth); break;
+      default: launch(MGB_PROF_SPLIT, k_split<16, 1>, grid, block, 0, t, depth); break;
+    }
   }
   MGB_LAUNCH_CHECK("k_split");
   return 0;
