@@ -154,8 +154,11 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
  * synchronised; nodes (2^(max_depth+1)-1 records) and node_count are device
  * pointers filled by the time the stream drains.  features (device, cols
  * flags, may be NULL for all) restricts the split search to the tree's
- * column sample (src/tree.cpp:179-180). */
-int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
+ * column sample (src/tree.cpp:179-180).  columns (device, may be NULL) holds
+ * the same codes column-major, code(row, f) at columns + (f * rows + row) *
+ * bin_bytes: the row partition then reads its split feature's codes from one
+ * column instead of one cache line of the row-major matrix per row. */
+int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const void* columns, const float* cuts,
                   const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
                   const uint32_t* features, void* workspace, size_t workspace_bytes, float* margin,
                   MgbTreeNode* nodes, uint32_t* node_count);

@@ -367,12 +367,15 @@ def test_sampling_stream_survives_pickle(xgb):
     np.testing.assert_array_equal(resumed.predict(d).view(np.uint32), whole.predict(d).view(np.uint32))
 
 
-@pytest.mark.parametrize("layout", ["row", "group"])
-def test_bin_layouts_give_identical_trees(xgb, layout):
-    """Row-major and group-major bin matrices (forced either way) grow the
-    oracle's trees, with missing values and 1024-bin u16 codes."""
+@pytest.mark.parametrize("layout,columns", [("row", 1), ("group", 1), ("row", 0), ("group", 0)])
+def test_bin_layouts_give_identical_trees(xgb, layout, columns):
+    """Row-major and group-major bin matrices (forced either way), with the
+    row partition reading the column-major copy of the codes or the bin
+    matrix itself, grow the oracle's trees, with missing values and 1024-bin
+    u16 codes."""
     X, y = W.config1(rows=20000, cols=40)
-    params = {"tree_method": "hist", "max_depth": 6, "max_bin": 1024, "hip_bin_layout": layout}
+    params = {"tree_method": "hist", "max_depth": 6, "max_bin": 1024, "hip_bin_layout": layout,
+              "hip_partition_columns": columns}
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(params, d, 4)
     ref = O.train(X, y, _oracle_params(params), 4)

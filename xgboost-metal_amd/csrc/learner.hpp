@@ -69,6 +69,7 @@ struct DMatrix {
   bool has_missing = false;
   MgbMatrix matrix{};
   DeviceBuffer d_cuts, d_counts, d_bins, d_missing;
+  DeviceBuffer d_columns;             // the codes again, column-major, for the row partition
   std::vector<float> cuts_host;        // cols * max_bin, host copy for export
   std::vector<uint32_t> counts_host;
   double sketch_seconds = 0, quantize_seconds = 0;

@@ -106,6 +106,7 @@ struct Tree {
   uint32_t* cursors;          // per split node: next left position, end of the free right range
   // Inputs.
   const void* bins;
+  const void* columns;        // column-major codes for the partition (NULL: read bins)
   const float* cuts;
   const uint32_t* counts;
   const uint32_t* allowed;    // per feature: nonzero if in the tree's column sample (NULL: all)
@@ -1114,11 +1115,16 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
 // ---------------------------------------------------------------------------
 template <typename BinT>
 __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint32_t row) {
-  const uint32_t G = t.features_per_group;
-  const BinT* codes = reinterpret_cast<const BinT*>(reinterpret_cast<const uint8_t*>(t.bins) +
-                                                    (uint64_t)(op.feature / G) * t.group_stride +
-                                                    (uint64_t)row * t.row_stride);
-  uint32_t code = codes[op.feature % G];
+  uint32_t code;
+  if (t.columns) {
+    code = reinterpret_cast<const BinT*>(t.columns)[(uint64_t)op.feature * t.rows_n + row];
+  } else {
+    const uint32_t G = t.features_per_group;
+    const BinT* codes = reinterpret_cast<const BinT*>(reinterpret_cast<const uint8_t*>(t.bins) +
+                                                      (uint64_t)(op.feature / G) * t.group_stride +
+                                                      (uint64_t)row * t.row_stride);
+    code = codes[op.feature % G];
+  }
   if (code == t.missing_code) return op.default_left != 0;
   return (int32_t)code <= op.last_left_bin;
 }
@@ -1419,15 +1425,15 @@ extern "C" {
 
 size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape) { return layout(*shape).total; }
 
-int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const float* cuts,
-                  const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
-                  const uint32_t* features, void* workspace, size_t workspace_bytes, float* margin,
-                  MgbTreeNode* nodes, uint32_t* node_count) {
+int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const void* columns,
+                  const float* cuts, const uint32_t* counts, const float* grad, const float* scales,
+                  const MgbSplitParams* sp, const uint32_t* features, void* workspace, size_t workspace_bytes,
+                  float* margin, MgbTreeNode* nodes, uint32_t* node_count) {
   if (validate(shape, m)) return -1;
   Layout L = layout(*shape);
   if (!workspace || workspace_bytes < L.total) { set_error("mgb_grow_tree: workspace too small"); return -1; }
   Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
-  t.bins = bins; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
+  t.bins = bins; t.columns = columns; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
   t.allowed = features;
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
