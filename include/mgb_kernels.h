@@ -100,10 +100,15 @@ typedef struct {
   float base_weight;
 } MgbTreeNode;
 
-/* Device-side tree workspace sizes; see mgb_tree_workspace_bytes. */
+/* Device-side tree workspace sizes; see mgb_tree_workspace_bytes.
+ * column_levels: levels (from the root) whose histograms read the
+ * column-major codes passed to mgb_grow_tree instead of the bin matrix; the
+ * rows of shallow nodes are dense enough that one feature column per load
+ * beats partial rows of the row-major matrix (0: never). */
 typedef struct {
   uint32_t rows, cols, max_bin, max_depth;
   uint32_t rows_per_tile, features_per_group, unit_hessian, dense;
+  uint32_t column_levels, padding[3];
 } MgbTreeShape;
 
 /* ---- data: quantile cuts and bin matrix ------------------------------- */

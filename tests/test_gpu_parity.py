@@ -367,15 +367,18 @@ def test_sampling_stream_survives_pickle(xgb):
     np.testing.assert_array_equal(resumed.predict(d).view(np.uint32), whole.predict(d).view(np.uint32))
 
 
-@pytest.mark.parametrize("layout,columns", [("row", 1), ("group", 1), ("row", 0), ("group", 0)])
-def test_bin_layouts_give_identical_trees(xgb, layout, columns):
+@pytest.mark.parametrize("layout,columns,column_levels", [("row", 1, 2), ("group", 1, 2), ("row", 0, 0),
+                                                           ("group", 0, 0), ("row", 1, 16), ("row", 1, 0)])
+@pytest.mark.parametrize("max_bin", [64, 1024])
+def test_bin_layouts_give_identical_trees(xgb, layout, columns, column_levels, max_bin):
     """Row-major and group-major bin matrices (forced either way), with the
     row partition reading the column-major copy of the codes or the bin
-    matrix itself, grow the oracle's trees, with missing values and 1024-bin
-    u16 codes."""
+    matrix itself, and histograms of the first column_levels levels read from
+    the column-major copy, grow the oracle's trees, with missing values and
+    u8 or u16 codes (40 features: a partial last feature group)."""
     X, y = W.config1(rows=20000, cols=40)
-    params = {"tree_method": "hist", "max_depth": 6, "max_bin": 1024, "hip_bin_layout": layout,
-              "hip_partition_columns": columns}
+    params = {"tree_method": "hist", "max_depth": 6, "max_bin": max_bin, "hip_bin_layout": layout,
+              "hip_partition_columns": columns, "hip_histogram_column_levels": column_levels}
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(params, d, 4)
     ref = O.train(X, y, _oracle_params(params), 4)

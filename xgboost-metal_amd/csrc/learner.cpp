@@ -465,6 +465,13 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   shape.features_per_group = data.features_per_group;
   shape.unit_hessian = unit_hessian ? 1 : 0;
   shape.dense = data.has_missing ? 0 : 1;
+  // The root's histogram reads every row: it takes the column-major codes
+  // (whole cache lines of one feature) rather than a few bytes of each
+  // row-major row.  Deeper levels gather rows, where a row-major row's lines
+  // serve every feature group from L2 (10M x 128, 1024 bins: the root level
+  // 20% faster, deeper levels slower from columns).
+  const bool columns_on = integer("hip_partition_columns", 1) != 0;
+  shape.column_levels = columns_on ? (uint32_t)integer("hip_histogram_column_levels", 1) : 0;
   size_t ws = mgb_tree_workspace_bytes(&shape);
   d_tree_ws_.ensure(ws);
   const uint32_t max_nodes = (2u << depth) - 1u;
@@ -485,7 +492,7 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   auto* nodes = d_nodes_.as<MgbTreeNode>();
   auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
   const uint32_t* features = sample_columns(data.cols);
-  const void* columns = integer("hip_partition_columns", 1) != 0 ? data.d_columns.get() : nullptr;
+  const void* columns = columns_on ? data.d_columns.get() : nullptr;
   kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), columns, data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
                        d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, d_tree_ws_.get(),
                        d_tree_ws_.bytes(), margin->as<float>(), nodes, count),

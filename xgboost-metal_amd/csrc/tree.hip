@@ -120,6 +120,7 @@ struct Tree {
   uint32_t row_stride, bin_bytes, missing_code, cut_stride;
   uint32_t max_depth, slots, rows_per_tile, groups;
   uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
+  uint32_t column_levels;                    // histogram levels that read `columns`
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
@@ -288,8 +289,10 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
   }
 }
 
-// Sum the row-tile partials of every multi-tile built node into its histogram
-// slot: entry e = f * (max_bin+1) + b of the node adds partial[task][e] over
+// Single-histogram entry point (mgb_histogram): sum the row-tile partials of
+// a multi-tile node into its histogram slot (the tree's split kernel sums the
+// partials of its built nodes itself, see built_pair): entry
+// e = f * (max_bin+1) + b of the node adds partial[task][e] over
 // the node's tasks (exact integers mod 2^64, so any order gives the same
 // bits).  A block takes 64 consecutive entries of one node; its four waves
 // take every fourth tile each, four loads in flight per lane, and combine in
@@ -378,6 +381,21 @@ struct Codes {
       w[0] = *p;
     }
   }
+  // Codes of G features of one row from the column-major copy (column j at
+  // col0 + j * stride); columns past the group's last feature (fcount) read
+  // the first column instead and are never accumulated.
+  __device__ __forceinline__ void load_cols(const BinT* col0, uint64_t stride, uint32_t row, uint32_t fcount) {
+    constexpr uint32_t bits = 8 * sizeof(BinT);
+    constexpr uint32_t per_word = 64 / bits;
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) w[i] = 0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const uint32_t jj = (uint32_t)j < fcount ? (uint32_t)j : 0u;
+      const uint64_t code = col0[jj * stride + row];
+      w[j / per_word] |= code << ((j % per_word) * bits);
+    }
+  }
   __device__ __forceinline__ uint32_t get(uint32_t j) const {
     constexpr uint32_t bits = 8 * sizeof(BinT);
     constexpr uint32_t per_word = 64 / bits;
@@ -389,8 +407,9 @@ struct Codes {
   }
 };
 
-template <typename BinT, int G, bool UNIT, bool IDENTITY>
+template <typename BinT, int G, bool UNIT, bool IDENTITY, bool COLS>
 __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t depth) {
+  constexpr int kU = Codes<BinT, G>::kBytes >= 32 ? 2 : kHistUnroll;
   extern __shared__ __align__(16) uint8_t smem[];
   const uint32_t B1 = t.bins1;
   unsigned long long* lg = reinterpret_cast<unsigned long long*>(smem);
@@ -425,49 +444,91 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     const uint32_t fbase = group * G;
     const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
     const uint8_t* gbins = bins + (uint64_t)group * t.group_stride;
-    // kHistUnroll rows per thread per pass: every row id, gradient pair and
-    // code chunk is requested before the first LDS atomic, so each wave keeps
-    // several gathered loads in flight.
-    for (uint32_t base = task.begin; base < task.end; base += kHistThreads * kHistUnroll) {
-      uint32_t row[kHistUnroll];
-      bool valid[kHistUnroll];
+    const BinT* gcols = COLS ? reinterpret_cast<const BinT*>(t.columns) + (uint64_t)fbase * t.rows_n : nullptr;
+    // kU rows per thread per batch (fewer for 32-byte code chunks, which
+    // would spill), software pipelined: while a
+    // batch's LDS atomics run, the next batch's gradients and codes and the
+    // row ids of the one after are already in flight, so the waves of the
+    // CU (one 1024-thread workgroup when the histogram fills the LDS) keep
+    // memory busy instead of alternating between loading and accumulating.
+    constexpr uint32_t kStep = kHistThreads * kU;
+    // Loads are unconditional (a slot past the task's end reads the task's
+    // first row instead and is skipped when accumulating): with no branch
+    // around them the compiler waits for exactly the batch it consumes.
+    auto fetch_rows = [&](uint32_t base, uint32_t (&row)[kU], bool (&valid)[kU]) {
 #pragma unroll
-      for (int u = 0; u < kHistUnroll; ++u) {
+      for (int u = 0; u < kU; ++u) {
         const uint32_t i = base + u * kHistThreads + threadIdx.x;
-        valid[u] = i < task.end;
-        row[u] = valid[u] ? (IDENTITY ? i : rows[i]) : 0u;
+        valid[u] = base < task.end && i < task.end;
+        const uint32_t at = valid[u] ? i : task.begin;
+        row[u] = IDENTITY ? at : rows[at];
       }
-      float2 gh[kHistUnroll];
-      Codes<BinT, G> c[kHistUnroll];
+    };
+    auto fetch_data = [&](const uint32_t (&row)[kU], const bool (&valid)[kU],
+                          float2 (&gh)[kU], Codes<BinT, G> (&c)[kU]) {
 #pragma unroll
-      for (int u = 0; u < kHistUnroll; ++u) {
-        if (valid[u]) {
-          gh[u] = t.grad[row[u]];
-          c[u].load(gbins + (uint64_t)row[u] * t.row_stride);
-        }
+      for (int u = 0; u < kU; ++u) {
+        gh[u] = t.grad[row[u]];
+        if constexpr (COLS) c[u].load_cols(gcols, t.rows_n, row[u], fcount);
+        else c[u].load(gbins + (uint64_t)row[u] * t.row_stride);
       }
+    };
+    uint32_t row_a[kU], row_b[kU];
+    bool valid_a[kU], valid_b[kU];
+    float2 gh_a[kU];
+    Codes<BinT, G> c_a[kU];
+    fetch_rows(task.begin, row_a, valid_a);
+    fetch_data(row_a, valid_a, gh_a, c_a);
+    fetch_rows(task.begin + kStep, row_b, valid_b);
+    for (uint32_t base = task.begin; base < task.end; base += kStep) {
+      float2 gh_b[kU];
+      Codes<BinT, G> c_b[kU];
+      fetch_data(row_b, valid_b, gh_b, c_b);
+      uint32_t row_c[kU];
+      bool valid_c[kU];
+      fetch_rows(base + 2 * kStep, row_c, valid_c);
 #pragma unroll
-      for (int u = 0; u < kHistUnroll; ++u) {
-        if (!valid[u]) continue;
-        const unsigned long long qg = (unsigned long long)(long long)rintf(gh[u].x * sg);
-        const unsigned long long qh = UNIT ? 0ull : (unsigned long long)(long long)rintf(gh[u].y * sh);
+      for (int u = 0; u < kU; ++u) {
+        if (!valid_a[u]) continue;
+        const unsigned long long qg = (unsigned long long)(long long)rintf(gh_a[u].x * sg);
+        const unsigned long long qh = UNIT ? 0ull : (unsigned long long)(long long)rintf(gh_a[u].y * sh);
+        if (fcount == (uint32_t)G) {  // full group (uniform): no per-feature test
 #pragma unroll
-        for (int k = 0; k < G; ++k) {
-          const uint32_t j = (k + lane) & (G - 1);
-          uint32_t code = c[u].get(j);
-          uint32_t bin = code == t.missing_code ? t.max_bin : code;
-          if (j < fcount) {
+          for (int k = 0; k < G; ++k) {
+            const uint32_t j = (k + lane) & (G - 1);
+            const uint32_t code = c_a[u].get(j);
+            const uint32_t bin = code == t.missing_code ? t.max_bin : code;
             atomicAdd(&lg[bin * G + j], qg);
             if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
             else atomicAdd(&lh[bin * G + j], qh);
           }
+        } else {
+#pragma unroll
+          for (int k = 0; k < G; ++k) {
+            const uint32_t j = (k + lane) & (G - 1);
+            const uint32_t code = c_a[u].get(j);
+            const uint32_t bin = code == t.missing_code ? t.max_bin : code;
+            if (j < fcount) {
+              atomicAdd(&lg[bin * G + j], qg);
+              if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
+              else atomicAdd(&lh[bin * G + j], qh);
+            }
+          }
         }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        valid_a[u] = valid_b[u];
+        gh_a[u] = gh_b[u];
+        c_a[u] = c_b[u];
+        row_b[u] = row_c[u];
+        valid_b[u] = valid_c[u];
       }
     }
     __syncthreads();
     // A node's only tile writes its histogram; tiles of larger nodes write a
-    // partial that k_reduce_hist sums (plain stores: no device-scope atomics
-    // across XCDs, and the sum is independent of scheduling).
+    // partial that the split kernel sums (plain stores: no device-scope
+    // atomics across XCDs, and the sum is independent of scheduling).
     const uint32_t task_index = xcd + 8 * (j / t.groups);
     int64_t* out = task.single ? bank + ((uint64_t)task.slot * t.cols + fbase) * B1 * 2
                                : t.partials + ((uint64_t)task_index * t.groups + group) * G * B1 * 2;
@@ -667,6 +728,53 @@ __device__ __forceinline__ uint64_t candidate_key(const NodeEval& n) {
   return ((uint64_t)order << 32) | (uint64_t)(~n.best_order);
 }
 
+// A built node's histogram row for one feature: its bank row, or, for a node
+// of several row tiles, the sum of the tiles' partial histograms (exact
+// integers mod 2^64, any order), which is then written to the bank row that
+// the next level reads as a parent.
+struct BuiltHist {
+  int64_t* bank;
+  const int64_t* part;  // first tile's partial row (several tiles), else null
+  uint64_t stride;      // int64 words between consecutive tiles' partials
+  uint32_t ntiles;
+};
+
+__device__ __forceinline__ BuiltHist built_hist(const Tree& t, int64_t* bank_row, const Frontier& fb, uint32_t f) {
+  BuiltHist h;
+  h.bank = bank_row;
+  h.part = nullptr;
+  h.stride = 0;
+  h.ntiles = fb.ntiles;
+  if (fb.ntiles > 1) {
+    h.stride = (uint64_t)t.groups * t.features_per_group * t.bins1 * 2;
+    h.part = t.partials + (uint64_t)fb.first_task * h.stride + (uint64_t)f * t.bins1 * 2;
+  }
+  return h;
+}
+
+__device__ __forceinline__ void built_pair(const BuiltHist& hb, uint32_t bin, bool store, uint64_t& g, uint64_t& v) {
+  if (!hb.part) {
+    load_pair(hb.bank, bin, g, v);
+    return;
+  }
+  g = v = 0;
+  uint32_t k = 0;
+  for (; k + 4 <= hb.ntiles; k += 4) {
+    uint64_t a[4], c[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_pair(hb.part + (uint64_t)(k + u) * hb.stride, bin, a[u], c[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { g += a[u]; v += c[u]; }
+  }
+  for (; k < hb.ntiles; ++k) {
+    uint64_t a, c;
+    load_pair(hb.part + (uint64_t)k * hb.stride, bin, a, c);
+    g += a;
+    v += c;
+  }
+  if (store) store_pair(hb.bank, bin, g, v);
+}
+
 // Bins of one (node pair or root, feature) item held by a lane: inclusive
 // in-lane prefix sums of CH consecutive bins.
 template <int CH>
@@ -797,17 +905,19 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   if (depth == 0) {
     if (item >= F) return;  // uniform per item (W > 1: one item per block)
     const uint32_t f = item, count = t.counts[f];
-    const int64_t* h = cur + (uint64_t)f * B1 * 2;
+    // The root's histogram row is always completed: the select kernel's dense
+    // root sums read it (every feature, sampled or not, is reduced here).
+    const BuiltHist hb = built_hist(t, cur + (uint64_t)f * B1 * 2, t.frontier[0][0], f);
     LaneBins<CH> x;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       uint64_t g = 0, v = 0;
-      if (b0 + j < count) load_pair(h, b0 + j, g, v);
+      if (b0 + j < count) built_pair(hb, b0 + j, true, g, v);
       x.g[j] = (j ? x.g[j - 1] : 0) + g;
       x.h[j] = (j ? x.h[j - 1] : 0) + v;
     }
     uint64_t mg, mh;
-    load_pair(h, MB, mg, mh);
+    built_pair(hb, MB, wave_in_item == 0 && lane == 0, mg, mh);
     const uint64_t lt[4] = {x.g[CH - 1], x.h[CH - 1], 0, 0};
     uint64_t pre[4], all[4];
     item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
@@ -835,14 +945,14 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const Frontier& fb = a.built ? a : b;
   const Frontier& fo = a.built ? b : a;
   const int64_t* parent = t.hist[(depth - 1) & 1] + ((uint64_t)a.parent_slot * F + f) * B1 * 2;
-  const int64_t* xb = cur + ((uint64_t)built * F + f) * B1 * 2;
   int64_t* ob = cur + ((uint64_t)other * F + f) * B1 * 2;
-  const bool store_other = depth + 1 < t.max_depth;
+  const bool store_other = depth + 1 < t.max_depth;  // both children are parents at the next level
+  const BuiltHist hb = built_hist(t, cur + ((uint64_t)built * F + f) * B1 * 2, fb, f);
   const uint32_t count = t.counts[f];
   // Missing slots first: they give each child's present-bin totals.
   uint64_t pmg, pmh, xmg, xmh;
   load_pair(parent, MB, pmg, pmh);
-  load_pair(xb, MB, xmg, xmh);
+  built_pair(hb, MB, store_other && wave_in_item == 0 && lane == 0, xmg, xmh);
   const uint64_t omg = pmg - xmg, omh = pmh - xmh;
   if (store_other && wave_in_item == 0 && lane == 0) store_pair(ob, MB, omg, omh);
   LaneBins<CH> x, o;
@@ -852,7 +962,7 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
     if (b0 + j < count) {
       uint64_t pg, ph;
       load_pair(parent, b0 + j, pg, ph);
-      load_pair(xb, b0 + j, xg, xh);
+      built_pair(hb, b0 + j, store_other, xg, xh);
       og = pg - xg;
       oh = ph - xh;
       if (store_other) store_pair(ob, b0 + j, og, oh);
@@ -1268,9 +1378,10 @@ template <typename BinT, int G>
 int launch_hist(const Tree& t, uint32_t depth, bool unit, uint32_t grid) {
   size_t lds = (size_t)G * t.bins1 * (8 + (unit ? 4 : 8));
   bool identity = depth == 0;
+  const bool cols = t.columns != nullptr && depth < t.column_levels;
 #define MGB_HIST_CASE(U, I)                                                                           \
   {                                                                                                   \
-    auto fn = k_histogram<BinT, G, U, I>;                                                             \
+    auto fn = cols ? k_histogram<BinT, G, U, I, true> : k_histogram<BinT, G, U, I, false>;            \
     if (hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
         hipSuccess) {                                                                                 \
       set_error("hipFuncSetAttribute(histogram LDS) failed");                                         \
@@ -1397,6 +1508,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.features_per_group = s->features_per_group;
   t.groups = div_up(s->cols, s->features_per_group);
   t.unit_hessian = s->unit_hessian; t.dense = s->dense; t.max_hist_tasks = L.max_hist_tasks;
+  t.column_levels = s->column_levels;
   t.hist_entry = L.hist_entry;
   return t;
 }
@@ -1447,8 +1559,6 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
     }
     if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, hgrid) : dispatch_hist<uint16_t>(t, depth, hgrid)))
       return -1;
-    launch(MGB_PROF_REDUCE, k_reduce_hist, dim3(reduce_grid(t)), dim3(kReduceWaves * kWave), 0, t, depth);
-    MGB_LAUNCH_CHECK("k_reduce_hist");
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
     if (launch_split(t, depth, items)) return -1;
