@@ -108,7 +108,9 @@ typedef struct {
 typedef struct {
   uint32_t rows, cols, max_bin, max_depth;
   uint32_t rows_per_tile, features_per_group, unit_hessian, dense;
-  uint32_t column_levels, padding[3];
+  uint32_t column_levels;
+  uint32_t sparse;  /* 1: the workspace is for mgb_grow_tree_csr (no per-tile partial histograms) */
+  uint32_t padding[2];
 } MgbTreeShape;
 
 /* ---- data: quantile cuts and bin matrix ------------------------------- */
@@ -167,6 +169,43 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
                   const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
                   const uint32_t* features, void* workspace, size_t workspace_bytes, float* margin,
                   MgbTreeNode* nodes, uint32_t* node_count);
+
+/* ---- CSR input (src/data.cpp:721-870 Matrix::sparse) ----------------- *
+ * indptr holds rows+1 offsets into indices/values; column indices are
+ * strictly increasing within a row; absent entries are missing values. */
+typedef struct {
+  uint32_t rows, cols, max_bin, cut_stride;
+  uint32_t bin_bytes, missing_code;  /* codes per nonzero: u8 or u16; NaN values carry missing_code */
+  uint64_t nnz;
+} MgbCsrMatrix;
+
+/* Column-major copy of a CSR matrix: colptr (cols+1 offsets) and, grouped by
+ * column in row order, every nonzero's row and value.  Synchronises. */
+int mgb_csr_to_csc(const uint64_t* indptr, const uint32_t* indices, const float* values, uint32_t rows, uint32_t cols,
+                   uint64_t nnz, uint64_t* colptr, uint32_t* csc_rows, float* csc_values);
+/* Quantile cuts from the column-major copy: the cuts mgb_sketch_cuts gives
+ * for the dense matrix with NaN at the absent entries (src/quantile.cpp:22-212
+ * over the present values of each column).  Synchronises. */
+int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint64_t* colptr, uint32_t rows,
+                        uint32_t cols, const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts);
+/* Bin code of every nonzero with the dense bin rule; NaN -> missing_code
+ * (kernels/sparse_data.metal.h:460-498 sparse_quantize_csr). */
+int mgb_quantize_csr(const uint32_t* indices, const float* values, uint64_t nnz, const float* cuts,
+                     const uint32_t* counts, uint32_t cut_stride, uint32_t bin_bytes, uint32_t missing_code,
+                     void* codes);
+/* mgb_grow_tree over a CSR bin matrix (codes per nonzero, see
+ * mgb_quantize_csr): histograms of the nonzeros with 64-bit device atomics
+ * and each feature's missing slot as the node total minus its present bins
+ * (kernels/histogram_csr.metal.h:22-153), the partition looking up the split
+ * feature in each row (:155-262).  The shape must have sparse = 1. */
+int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const uint64_t* indptr,
+                      const uint32_t* indices, const void* codes, const float* cuts, const uint32_t* counts,
+                      const float* grad, const float* scales, const MgbSplitParams* sp, const uint32_t* features,
+                      void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
+                      uint32_t* node_count);
+/* mgb_predict over a CSR matrix of raw values. */
+int mgb_predict_csr(const uint64_t* indptr, const uint32_t* indices, const float* values, uint32_t rows,
+                    const MgbTreeNode* nodes, const uint32_t* tree_offsets, uint32_t trees, float* margin);
 
 /* Rows and nodes whose histograms each level built directly (not by
  * subtraction), from the last mgb_grow_tree on this workspace; synchronises. */

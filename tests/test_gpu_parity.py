@@ -246,6 +246,75 @@ def test_logistic_parity(xgb):
     np.testing.assert_allclose(prob, 1 / (1 + np.exp(-ref["margin"].astype(np.float64))), rtol=1e-5, atol=1e-6)
 
 
+# ---------------------------------------------------------------------------
+# CSR input (the sparse path: per-nonzero codes, atomics histogram, missing
+# slots from node totals, row lookups in the partition and the predictor)
+# ---------------------------------------------------------------------------
+def _csr(indptr, indices, values, cols):
+    import scipy.sparse as sp
+    return sp.csr_matrix((values, indices, indptr), shape=(len(indptr) - 1, cols))
+
+
+@pytest.mark.parametrize("max_bin", [64, 256, 1024])
+def test_csr_regression_matches_oracle(xgb, max_bin):
+    """Squared error on a config-3 style CSR matrix: cuts, trees and margins
+    bit-identical to the oracle run on the dense matrix with NaN at the
+    absent entries (u8 codes, and u16 at 1024 bins)."""
+    cols = 300
+    indptr, indices, values, _ = W.config3(rows=12000, cols=cols, nnz=20, informative=40, seed=21)
+    X = W.csr_to_dense(indptr, indices, values, cols)
+    y = (np.nan_to_num(X[:, :40]).sum(axis=1) + 0.1 * np.random.default_rng(3).normal(size=len(X))).astype(np.float32)
+    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 6, "max_bin": max_bin, "eta": 0.3}
+    d = xgb.DMatrix(_csr(indptr, indices, values, cols), label=y)
+    bst = xgb.train(params, d, 5)
+    ref = O.train(X, y, _oracle_params(params), 5)
+    cut_ptr, cut_values = d.get_quantile_cut()
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    for f in range(cols):
+        c = ref["cut_counts"][f]
+        np.testing.assert_array_equal(cut_values[cut_ptr[f]:cut_ptr[f + 1]].view(np.uint32),
+                                      ref["cuts"][f, :c].view(np.uint32))
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+    # Fresh CSR and dense matrices predict the same bytes.
+    np.testing.assert_array_equal(bst.predict(xgb.DMatrix(_csr(indptr, indices, values, cols))).view(np.uint32),
+                                  ref["margin"].view(np.uint32))
+    np.testing.assert_array_equal(bst.predict(xgb.DMatrix(X)).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def test_csr_logistic_weighted_equals_dense(xgb):
+    """binary:logistic with sample weights, explicit NaN entries, an empty
+    column, a row with every column and sampling: the CSR path grows the same
+    trees, bit for bit, as the dense path on the same matrix (both on the
+    device), and the dense path is pinned to the oracle elsewhere."""
+    cols = 200
+    indptr, indices, values, y = W.config3(rows=15000, cols=cols, nnz=12, informative=30, seed=33)
+    values = values.copy()
+    values[::97] = np.nan                       # explicit missing entries
+    keep = indices != 7                          # column 7 has no entries at all
+    counts = np.add.reduceat(keep, indptr[:-1])
+    indices, values = indices[keep], values[keep]
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    # Row 0 holds every column.
+    full_idx = np.arange(cols, dtype=np.int32)
+    full_val = np.random.default_rng(8).lognormal(size=cols).astype(np.float32)
+    indices = np.concatenate([full_idx, indices[indptr[1]:]])
+    values = np.concatenate([full_val, values[indptr[1]:]])
+    indptr = np.concatenate([[0], indptr[1:] - indptr[1] + cols]).astype(np.int64)
+    X = W.csr_to_dense(indptr, indices, values, cols)
+    w = np.random.default_rng(9).uniform(0.2, 2.0, len(y)).astype(np.float32)
+    params = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 7, "max_bin": 128, "eta": 0.2,
+              "subsample": 0.8, "colsample_bytree": 0.7, "seed": 5}
+    ds = xgb.DMatrix(_csr(indptr, indices, values, cols), label=y, weight=w)
+    dd = xgb.DMatrix(X, label=y, weight=w)
+    bs = xgb.train(params, ds, 6)
+    bd = xgb.train(params, dd, 6)
+    assert bs.trees_to_json() == bd.trees_to_json()
+    np.testing.assert_array_equal(bs.predict(ds, output_margin=True).view(np.uint32),
+                                  bd.predict(dd, output_margin=True).view(np.uint32))
+    np.testing.assert_array_equal(bs.predict(dd).view(np.uint32), bd.predict(ds).view(np.uint32))
+
+
 def test_custom_objective_known_answer(xgb):
     """Negative Hessians and 2^40 cancellation across a depth-3 tree: leaf base
     weights [1, 3, -1, -3] (reference tests/test_histogram_present.py:66-81)."""

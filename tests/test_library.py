@@ -59,6 +59,21 @@ def test_dmatrix_host_side(xgb):
     assert d2.num_row() == 2 and d2.num_col() == 2 and d2.num_nonmissing() == 2
 
 
+def test_csr_ingest_sorts_rows_and_rejects_repeats(xgb):
+    """CSR rows arrive in any column order (sorted on ingest); a stored entry
+    equal to `missing` is missing; a repeated column in a row is an error."""
+    import numpy as np
+    import scipy.sparse as sp
+    indptr = np.array([0, 3, 5, 5])
+    indices = np.array([2, 0, 1, 1, 0])
+    data = np.array([1.0, 2.0, -1.0, 4.0, 5.0], np.float32)
+    d = xgb.DMatrix(sp.csr_matrix((data, indices, indptr), shape=(3, 3)), missing=-1.0)
+    assert d.num_row() == 3 and d.num_col() == 3 and d.num_nonmissing() == 4
+    dup = sp.csr_matrix((np.ones(3, np.float32), np.array([1, 0, 1]), np.array([0, 3])), shape=(1, 3))
+    with pytest.raises(xgb.XGBoostError, match="repeats a column"):
+        xgb.DMatrix(dup)
+
+
 def test_unsupported_parameters_fail_loudly(xgb):
     import numpy as np
     b = xgb.Booster({"tree_method": "exact"})

@@ -59,6 +59,49 @@ def config2(rows=262144, cols=64, seed=1337):
     return X, y
 
 
+def config3(rows=1_000_000, cols=2000, nnz=20, informative=200, seed=1337):
+    """CSR classification.  Per row `nnz` distinct columns
+    drawn uniformly (24 draws a row, the first `nnz` distinct ones in draw
+    order; rows with fewer are drawn again), sorted; values lognormal(0, 1);
+    w ~ N(0, sd 0.25) on `informative` random columns; y ~ Bernoulli(sigmoid(
+    sum v w)).  Draw order: columns, values, informative columns, their
+    weights, labels.  Returns (indptr int64, indices int32, values float32,
+    labels float32)."""
+    rng = np.random.default_rng(seed)
+    idx = np.empty((rows, nnz), np.int64)
+    todo = np.arange(rows)
+    while len(todo):
+        draw = rng.integers(0, cols, size=(len(todo), 24))
+        order = np.argsort(draw, axis=1, kind="stable")
+        srt = np.take_along_axis(draw, order, axis=1)
+        dup_sorted = np.zeros_like(srt, dtype=bool)
+        dup_sorted[:, 1:] = srt[:, 1:] == srt[:, :-1]
+        dup = np.empty_like(dup_sorted)
+        np.put_along_axis(dup, order, dup_sorted, axis=1)
+        keep = ~dup & (np.cumsum(~dup, axis=1) <= nnz)
+        ok = keep.sum(axis=1) == nnz
+        idx[todo[ok]] = draw[ok][keep[ok]].reshape(-1, nnz)
+        todo = todo[~ok]
+    idx.sort(axis=1)
+    values = rng.lognormal(0.0, 1.0, size=(rows, nnz)).astype(np.float32)
+    wcols = rng.choice(cols, size=informative, replace=False)
+    w = np.zeros(cols, np.float32)
+    w[wcols] = rng.normal(0.0, 0.25, size=informative).astype(np.float32)
+    s = (values * w[idx]).sum(axis=1)
+    y = (rng.random(rows) < 1.0 / (1.0 + np.exp(-s))).astype(np.float32)
+    indptr = np.arange(0, (rows + 1) * nnz, nnz, dtype=np.int64)
+    return indptr, idx.reshape(-1).astype(np.int32), values.reshape(-1), y
+
+
+def csr_to_dense(indptr, indices, values, cols):
+    """The dense matrix of a CSR matrix, NaN at the absent entries."""
+    rows = len(indptr) - 1
+    X = np.full((rows, cols), np.nan, np.float32)
+    r = np.repeat(np.arange(rows), np.diff(indptr))
+    X[r, indices] = values
+    return X
+
+
 CONFIG_PARAMS = {
     0: {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 6, "max_bin": 256, "eta": 0.3,
         "lambda": 1, "min_child_weight": 1},
@@ -66,4 +109,5 @@ CONFIG_PARAMS = {
         "lambda": 1, "min_child_weight": 1},
     2: {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 8, "max_bin": 256, "eta": 0.3,
         "lambda": 1},
+    3: {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 8, "max_bin": 256, "eta": 0.1},
 }

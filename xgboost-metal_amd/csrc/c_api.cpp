@@ -5,6 +5,7 @@
 // until the next call on the same thread.
 #include "xgboost_c_api.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <fstream>
@@ -281,22 +282,42 @@ int XGDMatrixCreateFromCSR(char const* indptr, char const* indices, char const* 
   require(ip.shape.size() == 1 && ix.shape.size() == 1 && dv.shape.size() == 1, "CSR arrays must be 1-dimensional.");
   auto d = std::make_shared<DMatrix>();
   int64_t rows = ip.shape[0] - 1;
-  require(rows >= 0, "Invalid CSR indptr.");
+  require(rows >= 0 && rows < (int64_t)1 << 32, "Invalid CSR indptr.");
+  require(ncol < ((bst_ulong)1 << 32), "Too many CSR columns.");
   d->rows = (uint32_t)rows;
   d->cols = (uint32_t)ncol;
+  d->sparse = true;
   float missing = config_missing(config);
-  // Entries absent from the CSR structure are missing values.
-  d->data.assign((size_t)rows * ncol, NAN);
+  // Entries absent from the CSR structure are missing values; stored entries
+  // equal to `missing` too (NaN).  Each row's columns are sorted (stable, so
+  // a repeated column keeps its first entry's position and is rejected).
+  d->indptr.resize((size_t)rows + 1);
+  d->indptr[0] = 0;
+  std::vector<std::pair<uint32_t, float>> row;
   for (int64_t r = 0; r < rows; ++r) {
     int64_t b = (int64_t)load_value(ip, r * ip.strides[0]);
     int64_t e = (int64_t)load_value(ip, (r + 1) * ip.strides[0]);
+    require(b >= 0 && e >= b && e <= ix.shape[0] && e <= dv.shape[0], "Invalid CSR indptr.");
+    row.clear();
+    bool sorted = true;
     for (int64_t k = b; k < e; ++k) {
       int64_t c = (int64_t)load_value(ix, k * ix.strides[0]);
       require(c >= 0 && (uint64_t)c < ncol, "CSR column index out of range.");
       float x = load_value(dv, k * dv.strides[0]);
       if (!std::isnan(missing) && x == missing) x = NAN;
-      d->data[(size_t)r * ncol + c] = x;
+      if (!row.empty() && (uint32_t)c <= row.back().first) sorted = false;
+      row.emplace_back((uint32_t)c, x);
     }
+    if (!sorted) {
+      std::stable_sort(row.begin(), row.end(), [](const auto& a, const auto& z) { return a.first < z.first; });
+      for (size_t i = 1; i < row.size(); ++i)
+        require(row[i].first != row[i - 1].first, "CSR row " + std::to_string(r) + " repeats a column index.");
+    }
+    for (const auto& [c, x] : row) {
+      d->indices.push_back(c);
+      d->values.push_back(x);
+    }
+    d->indptr[(size_t)r + 1] = d->indices.size();
   }
   set_quantile(*d, config);
   *out = new_handle(std::move(d));
@@ -368,9 +389,7 @@ int XGDMatrixNumCol(DMatrixHandle handle, bst_ulong* out) {
 
 int XGDMatrixNumNonMissing(DMatrixHandle handle, bst_ulong* out) {
   API_BEGIN
-  uint64_t n = 0;
-  for (float x : matrix(handle)->data) n += !std::isnan(x);
-  *out = n;
+  *out = matrix(handle)->nonmissing();
   API_END
 }
 

@@ -51,8 +51,20 @@ DMatrix::DMatrix() : id(next_matrix_id()) {}
 
 void DMatrix::upload() {
   if (data_uploaded) return;
-  d_data.upload(data.data(), data.size() * sizeof(float));
+  if (sparse) {
+    d_indptr.upload(indptr.data(), indptr.size() * sizeof(uint64_t));
+    d_indices.upload(indices.data(), indices.size() * sizeof(uint32_t));
+    d_values.upload(values.data(), values.size() * sizeof(float));
+  } else {
+    d_data.upload(data.data(), data.size() * sizeof(float));
+  }
   data_uploaded = true;
+}
+
+uint64_t DMatrix::nonmissing() const {
+  uint64_t n = 0;
+  for (float x : sparse ? values : data) n += !std::isnan(x);
+  return n;
 }
 
 void DMatrix::upload_info() {
@@ -115,6 +127,13 @@ uint32_t DMatrix::choose_group(uint32_t request) const {
 void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
   require(max_bin >= 2, "max_bin must be at least 2.");
   require(layout >= 0 && layout <= 2, "hip_bin_layout must be auto, row or group.");
+  if (sparse) {
+    // One layout: codes per nonzero (the CSR structure is the layout).
+    if (quantized_max_bin != max_bin) quantize_sparse(max_bin);
+    quantized_layout = layout;
+    quantized_group_request = group_request;
+    return;
+  }
   if (quantized_max_bin == max_bin) {
     if (quantized_layout == layout && quantized_group_request == group_request) return;
     const uint32_t G = choose_group(group_request);
@@ -166,6 +185,63 @@ void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
   quantized_max_bin = max_bin;
   sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
   relayout(layout);
+}
+
+// CSR matrices (src/data.cpp:721-870): the sketch reads a column-major copy
+// of the nonzeros (each column in row order, so the cuts equal the dense
+// matrix's with NaN at the absent entries); the bins are one code per nonzero.
+void DMatrix::quantize_sparse(uint32_t max_bin) {
+  require(!is_quantile || quantile_max_bin == max_bin, "Inconsistent max_bin between QuantileDMatrix and Booster.");
+  require(rows > 0 && cols > 0, "Data must contain at least one row and one feature.");
+  const uint64_t nnz = values.size();
+  require(nnz < (1ull << 31), "CSR matrices are limited to 2^31 - 1 stored entries.");
+  upload();
+  upload_info();
+  auto t0 = std::chrono::steady_clock::now();
+  hist_bins = std::max(1u, std::min(max_bin, rows));
+  d_cuts.ensure((size_t)cols * max_bin * sizeof(float));
+  d_counts.ensure((size_t)cols * sizeof(uint32_t));
+  {
+    DeviceBuffer colptr, csc_rows, csc_values;
+    colptr.ensure(((size_t)cols + 1) * sizeof(uint64_t));
+    csc_rows.ensure(std::max<size_t>(nnz, 1) * sizeof(uint32_t));
+    csc_values.ensure(std::max<size_t>(nnz, 1) * sizeof(float));
+    kcheck(mgb_csr_to_csc(d_indptr.as<uint64_t>(), d_indices.as<uint32_t>(), d_values.as<float>(), rows, cols, nnz,
+                          colptr.as<uint64_t>(), csc_rows.as<uint32_t>(), csc_values.as<float>()),
+           "CSR column copy");
+    const float* w = weights.empty() ? nullptr : d_weights.as<float>();
+    kcheck(mgb_sketch_cuts_csc(csc_values.as<float>(), csc_rows.as<uint32_t>(), colptr.as<uint64_t>(), rows, cols, w,
+                               max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
+           "quantile sketch");
+  }
+  counts_host.resize(cols);
+  cuts_host.resize((size_t)cols * max_bin);
+  d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
+  d_cuts.download(cuts_host.data(), cuts_host.size() * sizeof(float));
+  auto t1 = std::chrono::steady_clock::now();
+  uint32_t max_count = 0;
+  for (auto c : counts_host) max_count = std::max(max_count, c);
+  require(max_count <= hist_bins, "internal error: more cuts than histogram bins");
+  has_missing = nnz < (uint64_t)rows * cols || nonmissing() < nnz;
+  const uint32_t bin_bytes = (has_missing ? max_count <= 255 : max_count <= 256) ? 1 : 2;
+  matrix = MgbMatrix{};
+  matrix.rows = rows;
+  matrix.cols = cols;
+  matrix.bin_bytes = bin_bytes;
+  matrix.max_bin = hist_bins;
+  matrix.cut_stride = max_bin;
+  matrix.missing_code = !has_missing ? 0xFFFFFFFFu : (bin_bytes == 1 ? 0xFFu : 0xFFFFu);
+  matrix.group_features = 1;
+  features_per_group = 1;
+  csr = MgbCsrMatrix{rows, cols, hist_bins, max_bin, bin_bytes, matrix.missing_code, nnz};
+  d_codes.ensure(std::max<size_t>(nnz, 1) * bin_bytes);
+  kcheck(mgb_quantize_csr(d_indices.as<uint32_t>(), d_values.as<float>(), nnz, d_cuts.as<float>(),
+                          d_counts.as<uint32_t>(), max_bin, bin_bytes, matrix.missing_code, d_codes.get()),
+         "CSR codes");
+  kcheck(mgb_synchronize(), "synchronize");
+  quantized_max_bin = max_bin;
+  sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
+  quantize_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
 }
 
 // Bin matrix in the requested layout (the cuts stay).  Row-major is the
@@ -359,6 +435,19 @@ void Learner::upload_model() {
   model_version_ = trees.size();
 }
 
+// Adds trees [offsets, offsets + count) of the uploaded model to margin.
+void Learner::predict_into(DMatrix& data, const uint32_t* offsets, uint32_t count, float* margin) {
+  data.upload();
+  if (data.sparse)
+    kcheck(mgb_predict_csr(data.d_indptr.as<uint64_t>(), data.d_indices.as<uint32_t>(), data.d_values.as<float>(),
+                           data.rows, d_model_nodes_.as<MgbTreeNode>(), offsets, count, margin),
+           "prediction");
+  else
+    kcheck(mgb_predict(data.d_data.as<float>(), data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(), offsets,
+                       count, margin),
+           "prediction");
+}
+
 DeviceBuffer* Learner::margin_cache(DMatrix& data) {
   if (cache_id_ == data.id && cache_trees_ == trees.size() && d_margin_.get()) return &d_margin_;
   data.upload();
@@ -371,9 +460,7 @@ DeviceBuffer* Learner::margin_cache(DMatrix& data) {
   }
   if (!trees.empty()) {
     upload_model();
-    kcheck(mgb_predict(data.d_data.as<float>(), data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
-                       d_model_offsets_.as<uint32_t>(), (uint32_t)trees.size(), d_margin_.as<float>()),
-           "prediction");
+    predict_into(data, d_model_offsets_.as<uint32_t>(), (uint32_t)trees.size(), d_margin_.as<float>());
   }
   cache_id_ = data.id;
   cache_trees_ = trees.size();
@@ -472,6 +559,13 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   // 20% faster, deeper levels slower from columns).
   const bool columns_on = integer("hip_partition_columns", 1) != 0;
   shape.column_levels = columns_on ? (uint32_t)integer("hip_histogram_column_levels", 1) : 0;
+  if (data.sparse) {
+    // CSR: row tiles are only work units (every tile adds into the node's
+    // histogram), so small tiles spread a level over many workgroups.
+    shape.sparse = 1;
+    shape.column_levels = 0;
+    shape.rows_per_tile = (uint32_t)integer("hip_histogram_rows", 512);
+  }
   size_t ws = mgb_tree_workspace_bytes(&shape);
   d_tree_ws_.ensure(ws);
   const uint32_t max_nodes = (2u << depth) - 1u;
@@ -492,11 +586,19 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   auto* nodes = d_nodes_.as<MgbTreeNode>();
   auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
   const uint32_t* features = sample_columns(data.cols);
-  const void* columns = columns_on ? data.d_columns.get() : nullptr;
-  kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), columns, data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
-                       d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, d_tree_ws_.get(),
-                       d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
-         "tree growth");
+  if (data.sparse) {
+    kcheck(mgb_grow_tree_csr(&shape, &data.csr, data.d_indptr.as<uint64_t>(), data.d_indices.as<uint32_t>(),
+                             data.d_codes.get(), data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
+                             d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, d_tree_ws_.get(),
+                             d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
+           "tree growth");
+  } else {
+    const void* columns = columns_on ? data.d_columns.get() : nullptr;
+    kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), columns, data.d_cuts.as<float>(),
+                         data.d_counts.as<uint32_t>(), d_grad_.as<float>(), d_scales_.as<float>(), &sp, features,
+                         d_tree_ws_.get(), d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
+           "tree growth");
+  }
   // One device-to-host copy per round: node records followed by the count.
   std::vector<uint8_t> host(node_bytes + 16);
   d_nodes_.download(host.data(), node_bytes + sizeof(uint32_t));
@@ -510,9 +612,12 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
     uint64_t rows[32] = {0};
     uint32_t built[32] = {0};
     kcheck(mgb_tree_level_stats(&shape, d_tree_ws_.get(), rows, built, 32), "level statistics");
+    // CSR rows: their nonzeros (4-byte column + code each) and 8-byte offsets.
+    const double row_bytes =
+        data.sparse ? (double)data.values.size() / std::max(1u, data.rows) * (4 + data.matrix.bin_bytes) + 8 + 12
+                    : (double)data.cols * data.matrix.bin_bytes + 12;
     for (uint32_t d = 0; d < depth && d < 32; ++d) {
-      hist_bytes_ += rows[d] * ((uint64_t)data.cols * data.matrix.bin_bytes + 12) +
-                     (uint64_t)built[d] * data.cols * (data.hist_bins + 1) * 16;
+      hist_bytes_ += (uint64_t)(rows[d] * row_bytes) + (uint64_t)built[d] * data.cols * (data.hist_bins + 1) * 16;
       hist_rows_ += rows[d];
     }
   }
@@ -620,9 +725,7 @@ std::vector<float> Learner::predict(DMatrix& data, bool output_margin, uint32_t 
     }
     if (end > begin) {
       upload_model();
-      kcheck(mgb_predict(data.d_data.as<float>(), data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
-                         d_model_offsets_.as<uint32_t>() + begin, end - begin, d_out),
-             "prediction");
+      predict_into(data, d_model_offsets_.as<uint32_t>() + begin, end - begin, d_out);
     }
   }
   if (!output_margin) kcheck(mgb_transform(d_out, data.rows, (uint32_t)objective()), "transform");

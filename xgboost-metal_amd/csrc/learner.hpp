@@ -51,7 +51,15 @@ void kcheck(int status, const char* what);
 struct DMatrix {
   uint64_t id = 0;                    // unique per matrix; keys the prediction cache
   uint32_t rows = 0, cols = 0;
-  std::vector<float> data;            // row-major, NaN marks missing
+  std::vector<float> data;            // row-major, NaN marks missing (dense matrices)
+  // CSR matrices (sparse = true): rows+1 offsets, strictly increasing column
+  // indices within a row, values (NaN marks missing; absent entries too).
+  bool sparse = false;
+  std::vector<uint64_t> indptr;
+  std::vector<uint32_t> indices;
+  std::vector<float> values;
+  DeviceBuffer d_indptr, d_indices, d_values, d_codes;
+  MgbCsrMatrix csr{};
   std::vector<float> labels, weights, base_margin;
   std::vector<std::string> feature_names, feature_types;
   bool is_quantile = false;
@@ -82,6 +90,8 @@ struct DMatrix {
   void quantize(uint32_t max_bin, int layout = 0, uint32_t group_request = 0);
   uint32_t choose_group(uint32_t request) const;
   void relayout(int layout);
+  void quantize_sparse(uint32_t max_bin);
+  uint64_t nonmissing() const;
   void set_info(const std::string& field, const float* values, size_t count);
   const std::vector<float>& get_info(const std::string& field) const;
 };
@@ -141,6 +151,7 @@ class Learner {
   float base_margin_value() const;
   void upload_model();
   DeviceBuffer* margin_cache(DMatrix& data);
+  void predict_into(DMatrix& data, const uint32_t* offsets, uint32_t count, float* margin);
 
   std::map<std::string, std::string> params_;
   // Training-matrix prediction cache.

@@ -58,8 +58,13 @@ __global__ void k_transpose(const float* __restrict__ X, uint32_t rows, uint32_t
 }
 
 // Runs of equal values over a feature's non-missing, nonzero-weight entries in
-// row order (kernels/quantile.metal.h:19-140).
-__global__ __launch_bounds__(kSketchThreads) void k_runs(const float* __restrict__ Xt, uint32_t rows,
+// row order (kernels/quantile.metal.h:19-140).  Feature f's entries are
+// vals[seg[f] .. seg[f+1]) in row order: a column of the transposed dense
+// matrix (row = position) or of the column-major copy of a CSR matrix (row =
+// row_of[position]); entries absent from a CSR column are missing values and
+// take no part, exactly like NaN entries of a dense column.
+__global__ __launch_bounds__(kSketchThreads) void k_runs(const float* __restrict__ vals, const uint64_t* __restrict__ seg,
+                                                         const uint32_t* __restrict__ row_of,
                                                          const float* __restrict__ weights,
                                                          float* __restrict__ run_v, float* __restrict__ run_w,
                                                          uint32_t* __restrict__ run_start, float* __restrict__ elem_w,
@@ -70,8 +75,9 @@ __global__ __launch_bounds__(kSketchThreads) void k_runs(const float* __restrict
   __shared__ uint32_t carry_has;
   __shared__ float carry_last;
   const uint32_t f = blockIdx.x;
-  const float* col = Xt + (uint64_t)f * rows;
-  const uint64_t base = (uint64_t)f * rows;
+  const uint64_t base = seg[f];
+  const uint32_t rows = (uint32_t)(seg[f + 1] - base);  // entries of this feature
+  const float* col = vals + base;
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
   uint32_t elements = 0, runs = 0, nonmissing = 0;
   if (threadIdx.x == 0) { carry_has = 0; carry_last = 0; }
@@ -79,7 +85,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_runs(const float* __restrict
   for (uint32_t t0 = 0; t0 < rows; t0 += blockDim.x) {
     const uint32_t r = t0 + threadIdx.x;
     float v = r < rows ? col[r] : __uint_as_float(0x7fc00000u);
-    float w = (r < rows && weights) ? weights[r] : 1.0f;
+    float w = (r < rows && weights) ? weights[row_of ? row_of[base + r] : r] : 1.0f;
     const bool present = !isnan(v);
     const bool valid = present && (__float_as_uint(w) & 0x7fffffffu) != 0;
     const uint64_t mask = __ballot(valid);
@@ -130,13 +136,14 @@ __global__ __launch_bounds__(kSketchThreads) void k_runs(const float* __restrict
   if (threadIdx.x == 0) stats[f] = SkStats{nonmissing, elements, runs, 0};
 }
 
-__global__ void k_keys(const float* __restrict__ run_v, const SkStats* __restrict__ stats, uint32_t rows,
-                       uint32_t cols, uint64_t* __restrict__ keys) {
-  uint64_t total = (uint64_t)rows * cols;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
-    uint32_t f = (uint32_t)(i / rows), k = (uint32_t)(i % rows);
-    if (k < stats[f].runs) keys[i] = ((uint64_t)order_key(run_v[i]) << 32) | k;
-  }
+// One workgroup per feature: sort keys (value order, run index) of its runs.
+__global__ void k_keys(const float* __restrict__ run_v, const SkStats* __restrict__ stats,
+                       const uint64_t* __restrict__ seg, uint64_t* __restrict__ keys) {
+  const uint32_t f = blockIdx.x;
+  const uint64_t base = seg[f];
+  const uint32_t runs = stats[f].runs;
+  for (uint32_t k = threadIdx.x; k < runs; k += blockDim.x)
+    keys[base + k] = ((uint64_t)order_key(run_v[base + k]) << 32) | k;
 }
 
 // ---------------------------------------------------------------------------
@@ -394,7 +401,8 @@ __global__ __launch_bounds__(kSketchThreads) void k_reduce(const uint64_t* __res
                                                            const float* __restrict__ run_v,
                                                            const float* __restrict__ run_w,
                                                            const SkStats* __restrict__ stats,
-                                                           const SkFeature* __restrict__ features, uint32_t rows,
+                                                           const SkFeature* __restrict__ features,
+                                                           const uint64_t* __restrict__ seg,
                                                            uint32_t max_bin, SkEntry* __restrict__ levels,
                                                            SkEntry* __restrict__ work, uint32_t* __restrict__ scratch_u,
                                                            float* __restrict__ cut_values, float* __restrict__ cuts,
@@ -404,7 +412,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_reduce(const uint64_t* __res
   const uint32_t f = blockIdx.x;
   const SkFeature fe = features[f];
   const SkStats st = stats[f];
-  const uint64_t base = (uint64_t)f * rows;
+  const uint64_t base = seg[f];
   const uint32_t limit = fe.limit;
   const uint32_t cap = 2 * limit + 2;
   SkEntry* bufA = work + fe.work_offset;
@@ -530,32 +538,23 @@ struct DeviceBuffer {
   int alloc(size_t bytes) { return check(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc(sketch)"); }
 };
 
-}  // namespace
-}  // namespace mgb
-
-using namespace mgb;
-
-extern "C" {
-
-int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights, uint32_t max_bin,
-                    float* cuts, uint32_t* counts) {
-  if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
-  if (!cols) return 0;
+// Cuts of `cols` features whose entries are vals[seg[f] .. seg[f+1]) (device
+// values; host and device copies of the offsets), see k_runs.
+int sketch_segments(const float* vals, const std::vector<uint64_t>& seg_host, const uint32_t* row_of,
+                    uint32_t cols, const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
   hipStream_t s = stream();
-  const uint64_t total = (uint64_t)rows * cols;
-  // Element indices are 32-bit and the segmented sort counts in int.
-  if (total >= (1ull << 31)) { set_error("sketch: rows*cols must be below 2^31"); return -1; }
-  DeviceBuffer xt, run_v, run_w, run_start, elem_w, stats_d, keys_in, keys_out;
-  if (xt.alloc(total * 4) || run_v.alloc(total * 4) || run_w.alloc(total * 4) || run_start.alloc(total * 4) ||
-      stats_d.alloc(cols * sizeof(SkStats)) || keys_in.alloc(total * 8) || keys_out.alloc(total * 8))
+  const uint64_t total = seg_host[cols];
+  // Positions are 32-bit and the segmented sort counts in int.
+  if (total >= (1ull << 31)) { set_error("sketch: more than 2^31 - 1 entries"); return -1; }
+  const uint64_t alloc = total ? total : 1;
+  DeviceBuffer seg_d, run_v, run_w, run_start, elem_w, stats_d, keys_in, keys_out;
+  if (seg_d.alloc((cols + 1) * sizeof(uint64_t)) || run_v.alloc(alloc * 4) || run_w.alloc(alloc * 4) ||
+      run_start.alloc(alloc * 4) || stats_d.alloc(cols * sizeof(SkStats)) || keys_in.alloc(alloc * 8) ||
+      keys_out.alloc(alloc * 8))
     return -1;
-  if (weights && elem_w.alloc(total * 4)) return -1;
-  if (rows) {
-    dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(32, 8);
-    hipLaunchKernelGGL(k_transpose, grid, block, 0, s, X, rows, cols, (float*)xt.p);
-    MGB_LAUNCH_CHECK("k_transpose");
-  }
-  hipLaunchKernelGGL(k_runs, dim3(cols), dim3(kSketchThreads), 0, s, (const float*)xt.p, rows, weights,
+  if (weights && elem_w.alloc(alloc * 4)) return -1;
+  MGB_CHECK(hipMemcpyAsync(seg_d.p, seg_host.data(), (cols + 1) * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  hipLaunchKernelGGL(k_runs, dim3(cols), dim3(kSketchThreads), 0, s, vals, (const uint64_t*)seg_d.p, row_of, weights,
                      (float*)run_v.p, (float*)run_w.p, (uint32_t*)run_start.p, (float*)elem_w.p,
                      (SkStats*)stats_d.p);
   MGB_LAUNCH_CHECK("k_runs");
@@ -574,8 +573,8 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
     uint32_t batches = 0;
     for (uint64_t b = 0; b < st.runs; b += capacity) {
       uint64_t size = std::min<uint64_t>(capacity, st.runs - b);
-      seg_begin.push_back((uint32_t)((uint64_t)f * rows + b));
-      seg_end.push_back((uint32_t)((uint64_t)f * rows + b + size));
+      seg_begin.push_back((uint32_t)(seg_host[f] + b));
+      seg_end.push_back((uint32_t)(seg_host[f] + b + size));
       ++batches;
     }
     uint32_t levels = bit_width(std::max(1u, batches)) + 1;
@@ -600,8 +599,8 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
   if (scratch_d.alloc(scratch_total * 4)) return -1;
   MGB_CHECK(hipMemcpyAsync(feat_d.p, features.data(), cols * sizeof(SkFeature), hipMemcpyHostToDevice, s));
   if (!seg_begin.empty()) {
-    hipLaunchKernelGGL(k_keys, dim3(4096), dim3(256), 0, s, (const float*)run_v.p, (const SkStats*)stats_d.p, rows,
-                       cols, (uint64_t*)keys_in.p);
+    hipLaunchKernelGGL(k_keys, dim3(cols), dim3(256), 0, s, (const float*)run_v.p, (const SkStats*)stats_d.p,
+                       (const uint64_t*)seg_d.p, (uint64_t*)keys_in.p);
     MGB_LAUNCH_CHECK("k_keys");
     if (seg_b.alloc(seg_begin.size() * 4) || seg_e.alloc(seg_end.size() * 4)) return -1;
     MGB_CHECK(hipMemcpyAsync(seg_b.p, seg_begin.data(), seg_begin.size() * 4, hipMemcpyHostToDevice, s));
@@ -619,11 +618,47 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
   }
   hipLaunchKernelGGL(k_reduce, dim3(cols), dim3(kSketchThreads), 0, s, (const uint64_t*)keys_out.p,
                      (const float*)run_v.p, (const float*)run_w.p, (const SkStats*)stats_d.p,
-                     (const SkFeature*)feat_d.p, rows, max_bin, (SkEntry*)levels_d.p, (SkEntry*)work_d.p,
-                     (uint32_t*)scratch_d.p, (float*)values_d.p, cuts, counts);
+                     (const SkFeature*)feat_d.p, (const uint64_t*)seg_d.p, max_bin, (SkEntry*)levels_d.p,
+                     (SkEntry*)work_d.p, (uint32_t*)scratch_d.p, (float*)values_d.p, cuts, counts);
   MGB_LAUNCH_CHECK("k_reduce");
   MGB_CHECK(hipStreamSynchronize(s));
   return 0;
+}
+
+}  // namespace
+}  // namespace mgb
+
+using namespace mgb;
+
+extern "C" {
+
+int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights, uint32_t max_bin,
+                    float* cuts, uint32_t* counts) {
+  if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
+  if (!cols) return 0;
+  const uint64_t total = (uint64_t)rows * cols;
+  if (total >= (1ull << 31)) { set_error("sketch: rows*cols must be below 2^31"); return -1; }
+  DeviceBuffer xt;
+  if (xt.alloc((total ? total : 1) * 4)) return -1;
+  if (rows) {
+    dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(32, 8);
+    hipLaunchKernelGGL(k_transpose, grid, block, 0, stream(), X, rows, cols, (float*)xt.p);
+    MGB_LAUNCH_CHECK("k_transpose");
+  }
+  std::vector<uint64_t> seg(cols + 1);
+  for (uint32_t f = 0; f <= cols; ++f) seg[f] = (uint64_t)f * rows;
+  return sketch_segments((const float*)xt.p, seg, nullptr, cols, weights, max_bin, cuts, counts);
+}
+
+int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint64_t* colptr, uint32_t rows,
+                        uint32_t cols, const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
+  if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
+  if (!cols) return 0;
+  (void)rows;
+  std::vector<uint64_t> seg(cols + 1);
+  MGB_CHECK(hipMemcpyAsync(seg.data(), colptr, (cols + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost, stream()));
+  MGB_CHECK(hipStreamSynchronize(stream()));
+  return sketch_segments(values, seg, row_of, cols, weights, max_bin, cuts, counts);
 }
 
 }  // extern "C"

@@ -107,6 +107,9 @@ struct Tree {
   // Inputs.
   const void* bins;
   const void* columns;        // column-major codes for the partition (NULL: read bins)
+  const uint64_t* csr_indptr; // CSR bin matrix (mgb_grow_tree_csr; NULL for a dense matrix)
+  const uint32_t* csr_indices;
+  const void* csr_codes;
   const float* cuts;
   const uint32_t* counts;
   const uint32_t* allowed;    // per feature: nonzero if in the tree's column sample (NULL: all)
@@ -121,6 +124,7 @@ struct Tree {
   uint32_t max_depth, slots, rows_per_tile, groups;
   uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
   uint32_t column_levels;                    // histogram levels that read `columns`
+  uint32_t sparse;                           // CSR: missing slots from node totals, no partials
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
@@ -547,6 +551,101 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
 }
 
 // ---------------------------------------------------------------------------
+// CSR histograms (kernels/histogram_csr.metal.h:22-153).  A built node's
+// histogram (present entries only: the split kernel derives each feature's
+// missing slot from the node total) is cleared, then every row tile of the
+// node adds its nonzeros with 64-bit device atomics: the tile's rows are
+// flattened into one nonzero index space (block scan of the rows' counts),
+// each lane finds its entry's row by binary search over the prefix, and the
+// row's fixed-point gradient pair is read from LDS.  Integer adds commute, so
+// the result is independent of the order the atomics land in.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kCsrThreads = 256;
+
+// Root totals over every row (the dense path reads them off a feature's bins
+// plus its missing slot; a CSR row may lack any feature).
+__global__ __launch_bounds__(kCsrThreads) void k_root_totals(Tree t) {
+  __shared__ uint64_t part[kCsrThreads / kWave][2];
+  const float sg = t.scales[0], sh = t.scales[1];
+  uint64_t g = 0, h = 0;
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < t.rows_n; r += gridDim.x * blockDim.x) {
+    const float2 v = t.grad[r];
+    g += (uint64_t)(int64_t)rintf(v.x * sg);
+    h += (uint64_t)(int64_t)rintf(v.y * sh);
+  }
+  g = wave_sum_u64(g);
+  h = wave_sum_u64(h);
+  const uint32_t wave = threadIdx.x / kWave;
+  if (lane_id() == 0) { part[wave][0] = g; part[wave][1] = h; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (uint32_t k = 1; k < kCsrThreads / kWave; ++k) { g += part[k][0]; h += part[k][1]; }
+    atomicAdd(reinterpret_cast<unsigned long long*>(&t.frontier[0][0].sum_g), (unsigned long long)g);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&t.frontier[0][0].sum_h), (unsigned long long)h);
+  }
+}
+
+// Zero the histogram rows of the level's directly built nodes.
+__global__ void k_zero_built(Tree t, uint32_t depth) {
+  const uint32_t n = t.state->n_nodes;
+  const Frontier* fr = t.frontier[depth & 1];
+  int4* bank = reinterpret_cast<int4*>(t.hist[depth & 1]);
+  const uint64_t per = (uint64_t)t.cols * t.bins1;  // int4 (g, h) pairs per node
+  for (uint32_t slot = blockIdx.y; slot < n; slot += gridDim.y) {
+    if (!fr[slot].built) continue;
+    int4* row = bank + (uint64_t)slot * per;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < per; i += (uint64_t)gridDim.x * blockDim.x)
+      row[i] = make_int4(0, 0, 0, 0);
+  }
+}
+
+template <typename BinT, bool IDENTITY>
+__global__ __launch_bounds__(kCsrThreads) void k_histogram_csr(Tree t, uint32_t depth) {
+  __shared__ uint64_t s_begin[kCsrThreads];
+  __shared__ uint32_t s_off[kCsrThreads];
+  __shared__ unsigned long long s_qg[kCsrThreads], s_qh[kCsrThreads];
+  __shared__ uint32_t scan[kCsrThreads / kWave + 1];
+  const uint32_t ntasks = t.state->n_hist_tasks;
+  const uint32_t* rows = t.rows[depth & 1];
+  int64_t* bank = t.hist[depth & 1];
+  const float sg = t.scales[0], sh = t.scales[1];
+  const uint32_t B1 = t.bins1;
+  const BinT* codes = reinterpret_cast<const BinT*>(t.csr_codes);
+  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
+    const HistTask task = t.hist_tasks[w];
+    unsigned long long* node =
+        reinterpret_cast<unsigned long long*>(bank + (uint64_t)task.slot * t.cols * B1 * 2);
+    for (uint32_t base = task.begin; base < task.end; base += kCsrThreads) {
+      const uint32_t i = base + threadIdx.x;
+      uint32_t cnt = 0;
+      if (i < task.end) {
+        const uint32_t r = IDENTITY ? i : rows[i];
+        const uint64_t b = t.csr_indptr[r];
+        cnt = (uint32_t)(t.csr_indptr[r + 1] - b);
+        s_begin[threadIdx.x] = b;
+        const float2 v = t.grad[r];
+        s_qg[threadIdx.x] = (unsigned long long)(long long)rintf(v.x * sg);
+        s_qh[threadIdx.x] = (unsigned long long)(long long)rintf(v.y * sh);
+      }
+      uint32_t total;
+      s_off[threadIdx.x] = block_exclusive_u32(cnt, scan, &total);
+      __syncthreads();
+      const uint32_t nrows = task.end - base < kCsrThreads ? task.end - base : kCsrThreads;
+      for (uint32_t j = threadIdx.x; j < total; j += kCsrThreads) {
+        const uint32_t q = owner_of(s_off, nrows, j);
+        const uint64_t k = s_begin[q] + (j - s_off[q]);
+        const uint32_t code = codes[k];
+        if (code == t.missing_code) continue;
+        unsigned long long* p = node + ((uint64_t)t.csr_indices[k] * B1 + code) * 2;
+        atomicAdd(p, s_qg[q]);
+        atomicAdd(p + 1, s_qh[q]);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Split evaluation (kernels/boost.metal:902-1005, scalar_parallel.metal.h).
 // One workgroup of W waves per (node pair, feature); wave c takes bins
 // [64c, 64c+64) of the feature's [0, count), one bin per lane, so every load
@@ -745,7 +844,7 @@ __device__ __forceinline__ BuiltHist built_hist(const Tree& t, int64_t* bank_row
   h.part = nullptr;
   h.stride = 0;
   h.ntiles = fb.ntiles;
-  if (fb.ntiles > 1) {
+  if (fb.ntiles > 1 && !t.sparse) {
     h.stride = (uint64_t)t.groups * t.features_per_group * t.bins1 * 2;
     h.part = t.partials + (uint64_t)fb.first_task * h.stride + (uint64_t)f * t.bins1 * 2;
   }
@@ -916,16 +1015,28 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
       x.g[j] = (j ? x.g[j - 1] : 0) + g;
       x.h[j] = (j ? x.h[j - 1] : 0) + v;
     }
-    uint64_t mg, mh;
-    built_pair(hb, MB, wave_in_item == 0 && lane == 0, mg, mh);
+    uint64_t mg = 0, mh = 0;
+    if (!t.sparse) built_pair(hb, MB, wave_in_item == 0 && lane == 0, mg, mh);
     const uint64_t lt[4] = {x.g[CH - 1], x.h[CH - 1], 0, 0};
     uint64_t pre[4], all[4];
     item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
-    // Root totals: every bin of the feature plus its missing slot.
-    const uint64_t tg = all[0] + mg, th = all[1] + mh;
-    if (f == 0 && wave_in_item == 0 && lane == 0) {
-      t.frontier[0][0].sum_g = (int64_t)tg;
-      t.frontier[0][0].sum_h = (int64_t)th;
+    uint64_t tg, th;
+    if (t.sparse) {
+      // CSR: the root totals come from every row (k_root_totals); a feature's
+      // missing slot is what its present bins leave of them.
+      tg = (uint64_t)t.frontier[0][0].sum_g;
+      th = (uint64_t)t.frontier[0][0].sum_h;
+      mg = tg - all[0];
+      mh = th - all[1];
+      if (wave_in_item == 0 && lane == 0) store_pair(hb.bank, MB, mg, mh);
+    } else {
+      // Root totals: every bin of the feature plus its missing slot.
+      tg = all[0] + mg;
+      th = all[1] + mh;
+      if (f == 0 && wave_in_item == 0 && lane == 0) {
+        t.frontier[0][0].sum_g = (int64_t)tg;
+        t.frontier[0][0].sum_h = (int64_t)th;
+      }
     }
     if (t.allowed && !t.allowed[f]) return;  // outside the tree's column sample
     NodeEval e;
@@ -949,12 +1060,10 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const bool store_other = depth + 1 < t.max_depth;  // both children are parents at the next level
   const BuiltHist hb = built_hist(t, cur + ((uint64_t)built * F + f) * B1 * 2, fb, f);
   const uint32_t count = t.counts[f];
-  // Missing slots first: they give each child's present-bin totals.
-  uint64_t pmg, pmh, xmg, xmh;
+  // Missing slots: they give each child's present-bin totals.
+  uint64_t pmg, pmh, xmg = 0, xmh = 0;
   load_pair(parent, MB, pmg, pmh);
-  built_pair(hb, MB, store_other && wave_in_item == 0 && lane == 0, xmg, xmh);
-  const uint64_t omg = pmg - xmg, omh = pmh - xmh;
-  if (store_other && wave_in_item == 0 && lane == 0) store_pair(ob, MB, omg, omh);
+  if (!t.sparse) built_pair(hb, MB, store_other && wave_in_item == 0 && lane == 0, xmg, xmh);
   LaneBins<CH> x, o;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
@@ -975,6 +1084,16 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const uint64_t lt[4] = {x.g[CH - 1], x.h[CH - 1], o.g[CH - 1], o.h[CH - 1]};
   uint64_t pre[4], all[4];
   item_prefix<W>(lt, pre, all, xtot[slot_in_block], wave_in_item);
+  if (t.sparse) {
+    // CSR: the built child's missing slot is its total minus its present
+    // bins (the sibling's present bins above already subtract to the right
+    // values: its present parent bins minus the built child's).
+    xmg = (uint64_t)fb.sum_g - all[0];
+    xmh = (uint64_t)fb.sum_h - all[1];
+    if (store_other && wave_in_item == 0 && lane == 0) store_pair(hb.bank, MB, xmg, xmh);
+  }
+  const uint64_t omg = pmg - xmg, omh = pmh - xmh;
+  if (store_other && wave_in_item == 0 && lane == 0) store_pair(ob, MB, omg, omh);
   NodeEval ex, eo;
   node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
   node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
@@ -1226,7 +1345,19 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
 template <typename BinT>
 __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint32_t row) {
   uint32_t code;
-  if (t.columns) {
+  if (t.csr_indptr) {
+    // CSR: binary search of the split feature among the row's sorted columns;
+    // an absent entry is missing.
+    uint64_t lo = t.csr_indptr[row], hi = t.csr_indptr[row + 1];
+    const uint64_t end = hi;
+    while (lo < hi) {
+      const uint64_t mid = lo + (hi - lo) / 2;
+      if (t.csr_indices[mid] < op.feature) lo = mid + 1;
+      else hi = mid;
+    }
+    if (lo == end || t.csr_indices[lo] != op.feature) return op.default_left != 0;
+    code = reinterpret_cast<const BinT*>(t.csr_codes)[lo];
+  } else if (t.columns) {
     code = reinterpret_cast<const BinT*>(t.columns)[(uint64_t)op.feature * t.rows_n + row];
   } else {
     const uint32_t G = t.features_per_group;
@@ -1366,9 +1497,12 @@ Layout layout(const MgbTreeShape& s) {
   L.part_tasks = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(PartTask));
   L.cursors = off; off = align_up(off + (size_t)(2 * 2 * L.slots) * sizeof(uint32_t));
   {
-    const uint64_t groups = div_up(s.cols, s.features_per_group);
+    // Per-tile partial histograms of multi-tile nodes (dense path only: the
+    // CSR histogram adds every tile into the node's own row).
+    const uint64_t groups = div_up(s.cols, s.features_per_group ? s.features_per_group : 1);
     L.partials = off;
-    off = align_up(off + (size_t)L.max_hist_tasks * groups * s.features_per_group * (s.max_bin + 1) * 16);
+    if (!s.sparse)
+      off = align_up(off + (size_t)L.max_hist_tasks * groups * s.features_per_group * (s.max_bin + 1) * 16);
   }
   L.total = off;
   return L;
@@ -1509,6 +1643,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.groups = div_up(s->cols, s->features_per_group);
   t.unit_hessian = s->unit_hessian; t.dense = s->dense; t.max_hist_tasks = L.max_hist_tasks;
   t.column_levels = s->column_levels;
+  t.sparse = s->sparse;
   t.hist_entry = L.hist_entry;
   return t;
 }
@@ -1565,6 +1700,69 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
     launch(MGB_PROF_CONTROL, k_select, dim3(1), dim3(kSelectThreads), 0, t, depth);
     MGB_LAUNCH_CHECK("k_select");
     if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
+      return -1;
+  }
+  return 0;
+}
+
+int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const uint64_t* indptr,
+                      const uint32_t* indices, const void* codes, const float* cuts, const uint32_t* counts,
+                      const float* grad, const float* scales, const MgbSplitParams* sp, const uint32_t* features,
+                      void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
+                      uint32_t* node_count) {
+  if (!shape || !m) { set_error("null shape or matrix"); return -1; }
+  if (!shape->sparse) { set_error("mgb_grow_tree_csr: the tree shape must have sparse = 1"); return -1; }
+  if (shape->max_depth < 1 || shape->max_depth > 16) { set_error("max_depth must be in [1, 16]"); return -1; }
+  if (shape->rows != m->rows || shape->cols != m->cols || shape->max_bin != m->max_bin) {
+    set_error("tree shape does not match the CSR matrix");
+    return -1;
+  }
+  if (m->bin_bytes != 1 && m->bin_bytes != 2) { set_error("bin_bytes must be 1 or 2"); return -1; }
+  if (m->max_bin < 1 || m->max_bin > 1086) { set_error("max_bin must be in [1, 1086]"); return -1; }
+  if (shape->rows_per_tile < 64) { set_error("rows_per_tile must be >= 64"); return -1; }
+  if (!shape->features_per_group) { set_error("features_per_group must be at least 1"); return -1; }
+  Layout L = layout(*shape);
+  if (!workspace || workspace_bytes < L.total) { set_error("mgb_grow_tree_csr: workspace too small"); return -1; }
+  MgbMatrix dm;
+  std::memset(&dm, 0, sizeof(dm));
+  dm.rows = m->rows; dm.cols = m->cols; dm.bin_bytes = m->bin_bytes; dm.max_bin = m->max_bin;
+  dm.cut_stride = m->cut_stride; dm.missing_code = m->missing_code; dm.group_features = shape->features_per_group;
+  Tree t = make_tree(shape, &dm, L, reinterpret_cast<uint8_t*>(workspace));
+  t.csr_indptr = indptr; t.csr_indices = indices; t.csr_codes = codes;
+  t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
+  t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
+  t.allowed = features;
+  t.column_levels = 0;
+  launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
+  MGB_LAUNCH_CHECK("k_level0");
+  launch(MGB_PROF_HISTOGRAM, k_root_totals, dim3(m->rows ? div_up(m->rows, kCsrThreads * 8) : 1),
+         dim3(kCsrThreads), 0, t);
+  MGB_LAUNCH_CHECK("k_root_totals");
+  const uint32_t hgrid = t.max_hist_tasks < 4096 ? (t.max_hist_tasks ? t.max_hist_tasks : 1) : 4096;
+  const uint64_t row_int4 = (uint64_t)t.cols * t.bins1;
+  const uint32_t zx = (uint32_t)(row_int4 / (256 * 8) + 1 < 64 ? row_int4 / (256 * 8) + 1 : 64);
+  for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
+    if (depth > 0) {
+      launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
+      MGB_LAUNCH_CHECK("k_plan");
+    }
+    const uint32_t zy = depth == 0 ? 1 : (1u << depth) < 1024 ? (1u << depth) : 1024;
+    launch(MGB_PROF_HISTOGRAM, k_zero_built, dim3(zx, zy), dim3(256), 0, t, depth);
+    MGB_LAUNCH_CHECK("k_zero_built");
+    if (m->bin_bytes == 1) {
+      if (depth == 0) launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint8_t, true>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
+      else launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint8_t, false>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
+    } else {
+      if (depth == 0) launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint16_t, true>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
+      else launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint16_t, false>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
+    }
+    MGB_LAUNCH_CHECK("k_histogram_csr");
+    uint32_t max_nodes = 1u << depth;
+    uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
+    if (launch_split(t, depth, items)) return -1;
+    launch(MGB_PROF_CONTROL, k_select, dim3(1), dim3(kSelectThreads), 0, t, depth);
+    MGB_LAUNCH_CHECK("k_select");
+    if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, 1024) : launch_partition<uint16_t>(t, depth, 1024)))
       return -1;
   }
   return 0;
