@@ -125,16 +125,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--config", choices=["c2", "c4"], default="c2",
-                    help="c2 (default): the headline metric; c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
+    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
+                    help="c2 (default): the headline metric; c3: 1M x 2000 CSR, 20 nonzeros a row; "
+                         "c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(row-sharded multi-GPU training is a design note, not implemented).", file=sys.stderr)
         sys.exit(2)
     import xgboost as xgb
-    if args.config == "c4":
-        return bench_c4(xgb, args)
+    if args.config in LARGE:
+        return bench_large(xgb, args, args.config)
 
     X, y = config2()
     dtrain = xgb.DMatrix(X, label=y)
@@ -218,43 +219,68 @@ def main():
     print(json.dumps(line))
 
 
-def bench_c4(xgb, args):
-    """Config 4: one GPU, rounds on the resident 2.56 GB u16 bin matrix."""
+C3_PARAMS = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 8, "max_bin": 256, "eta": 0.1}
+
+LARGE = {
+    "c3": dict(rounds=100, params=C3_PARAMS,
+               metric="ms/100 rounds @1,000,000x2,000 CSR, 20 nonzeros/row, d8 (config 3); histogram build GB/s vs peak",
+               workload="BASELINE config 3: CSR 1,000,000x2,000 with 20 distinct uniform columns per row, "
+                        "lognormal(0,1) values, logistic labels from 200 informative columns (seed 1337); "
+                        "binary:logistic, depth 8, max_bin 256, eta 0.1; step = one boosting round on the resident "
+                        "per-nonzero codes (atomics histogram, missing slots from node totals)",
+               shape={"rows": 1_000_000, "features": 2000, "nonzeros_per_row": 20, "max_depth": 8, "max_bin": 256}),
+    "c4": dict(rounds=200, params=C4_PARAMS,
+               metric="ms/200 rounds @10,000,000x128 d10 1024 bins (config 4); histogram build HBM GB/s vs peak",
+               workload="BASELINE config 4: X 10,000,000x128 (N(0,1) | U(0,1) | integers 0-999), logistic "
+                        "labels; binary:logistic, depth 10, max_bin 1024 (u16 codes), eta 0.1, subsample 0.8, "
+                        "colsample_bytree 0.8; step = one boosting round on the resident bin matrix",
+               shape={"rows": 10_000_000, "features": 128, "max_depth": 10, "max_bin": 1024}),
+}
+
+
+def bench_large(xgb, args, which):
+    """Configs 3 and 4: one GPU, timed rounds on the resident quantized matrix
+    (the other configs' workloads; the headline metric is config 2)."""
+    spec = LARGE[which]
     steps = args.steps if args.steps != 100 else 20
     warmup = args.warmup if args.warmup != 10 else 2
     t0 = time.perf_counter()
-    X, y = config4()
+    if which == "c4":
+        X, y = config4()
+    else:
+        import scipy.sparse as sp
+        import workloads as W
+        indptr, indices, values, y = W.config3()
+        X = sp.csr_matrix((values, indices, indptr), shape=(len(indptr) - 1, 2000))
     gen_s = time.perf_counter() - t0
-    print(f"c4: generated {X.shape} in {gen_s:.1f} s", file=sys.stderr, flush=True)
+    print(f"{which}: generated {X.shape} in {gen_s:.1f} s", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     dtrain = xgb.DMatrix(X, label=y)
-    print(f"c4: DMatrix in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
-    warm = xgb.train(dict(C4_PARAMS), dtrain, max(1, warmup))
+    print(f"{which}: DMatrix in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    warm = xgb.train(dict(spec["params"]), dtrain, max(1, warmup))
     setup_s = time.perf_counter() - t0
-    print(f"c4: sketch, bins and {warmup} warm-up rounds in {setup_s:.1f} s", file=sys.stderr, flush=True)
+    print(f"{which}: sketch, bins and {warmup} warm-up rounds in {setup_s:.1f} s", file=sys.stderr, flush=True)
     prof0 = warm.profile()["seconds"]
-    _, elapsed = time_rounds(xgb, dtrain, steps, profile=False, base=C4_PARAMS)
+    _, elapsed = time_rounds(xgb, dtrain, steps, profile=False, base=spec["params"])
     ms_per_step = elapsed * 1e3 / steps
-    print(f"c4: {steps} timed rounds, {ms_per_step:.2f} ms each", file=sys.stderr, flush=True)
+    print(f"{which}: {steps} timed rounds, {ms_per_step:.2f} ms each", file=sys.stderr, flush=True)
     import device_lib as D
     D.lib().mgb_profile_reset()
-    bst_p, _ = time_rounds(xgb, dtrain, steps, profile=True, base=C4_PARAMS)
+    bst_p, _ = time_rounds(xgb, dtrain, steps, profile=True, base=spec["params"])
     prof = bst_p.profile()
     kernels = prof["kernels"]
     hist = kernels["histogram"]
     launches = max(hist["launches"], 1)
     achieved = prof["histogram_bytes"] / (hist["ms"] * 1e-3) / 1e9 if hist["ms"] > 0 else 0.0
+    rounds = spec["rounds"]
     line = {
-        "metric": "ms/200 rounds @10,000,000x128 d10 1024 bins (config 4); histogram build HBM GB/s vs peak",
-        "value": round(ms_per_step * 200, 2), "unit": "ms/200 rounds", "n_gpus": 1, "steps": steps, "warmup": warmup,
-        "ms_per_step": round(ms_per_step, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int64", "data": "synthetic",
-        "config": {"workload": "BASELINE config 4: X 10,000,000x128 (N(0,1) | U(0,1) | integers 0-999), logistic "
-                               "labels; binary:logistic, depth 10, max_bin 1024 (u16 codes), eta 0.1, subsample 0.8, "
-                               "colsample_bytree 0.8; step = one boosting round on the resident bin matrix",
-                   "rows": 10_000_000, "features": 128, "max_depth": 10, "max_bin": 1024},
+        "metric": spec["metric"], "value": round(ms_per_step * rounds, 2), "unit": f"ms/{rounds} rounds",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int64", "data": "synthetic",
+        "config": dict({"workload": spec["workload"]}, **spec["shape"]),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_histogram",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "k_histogram" if which == "c4" else "k_histogram_csr (+ k_zero_built, k_root_totals)",
                      "launches": launches, "algorithmic_bytes_per_launch": round(prof["histogram_bytes"] / launches),
                      "avg_launch_us": round(hist["ms"] * 1e3 / launches, 3)},
         "kernel_ms_per_round": {k: round(v["ms"] / (steps + 1), 4) for k, v in kernels.items() if v["launches"]},

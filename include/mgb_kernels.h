@@ -180,9 +180,10 @@ typedef struct {
 } MgbCsrMatrix;
 
 /* Column-major copy of a CSR matrix: colptr (cols+1 offsets) and, grouped by
- * column in row order, every nonzero's row and value.  Synchronises. */
+ * column in row order, every nonzero's row and value (and its column in
+ * csc_cols unless NULL).  Synchronises. */
 int mgb_csr_to_csc(const uint64_t* indptr, const uint32_t* indices, const float* values, uint32_t rows, uint32_t cols,
-                   uint64_t nnz, uint64_t* colptr, uint32_t* csc_rows, float* csc_values);
+                   uint64_t nnz, uint64_t* colptr, uint32_t* csc_rows, float* csc_values, uint32_t* csc_cols);
 /* Quantile cuts from the column-major copy: the cuts mgb_sketch_cuts gives
  * for the dense matrix with NaN at the absent entries (src/quantile.cpp:22-212
  * over the present values of each column).  Synchronises. */
@@ -197,9 +198,14 @@ int mgb_quantize_csr(const uint32_t* indices, const float* values, uint64_t nnz,
  * mgb_quantize_csr): histograms of the nonzeros with 64-bit device atomics
  * and each feature's missing slot as the node total minus its present bins
  * (kernels/histogram_csr.metal.h:22-153), the partition looking up the split
- * feature in each row (:155-262).  The shape must have sparse = 1. */
+ * feature in each row (:155-262).  The root, which holds every row, builds
+ * its histogram from the column-major codes instead (colptr, csc_rows as
+ * from mgb_csr_to_csc, csc_codes its columns' codes): a few features per
+ * workgroup in LDS and plain stores, no device atomics.  The shape must have
+ * sparse = 1. */
 int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const uint64_t* indptr,
-                      const uint32_t* indices, const void* codes, const float* cuts, const uint32_t* counts,
+                      const uint32_t* indices, const void* codes, const uint64_t* colptr, const uint32_t* csc_rows,
+                      const void* csc_codes, const float* cuts, const uint32_t* counts,
                       const float* grad, const float* scales, const MgbSplitParams* sp, const uint32_t* features,
                       void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
                       uint32_t* node_count);

@@ -255,8 +255,8 @@ def _csr(indptr, indices, values, cols):
     return sp.csr_matrix((values, indices, indptr), shape=(len(indptr) - 1, cols))
 
 
-@pytest.mark.parametrize("max_bin", [64, 256, 1024])
-def test_csr_regression_matches_oracle(xgb, max_bin):
+@pytest.mark.parametrize("max_bin,root_columns", [(64, 1), (256, 1), (1024, 1), (256, 0)])
+def test_csr_regression_matches_oracle(xgb, max_bin, root_columns):
     """Squared error on a config-3 style CSR matrix: cuts, trees and margins
     bit-identical to the oracle run on the dense matrix with NaN at the
     absent entries (u8 codes, and u16 at 1024 bins)."""
@@ -264,7 +264,8 @@ def test_csr_regression_matches_oracle(xgb, max_bin):
     indptr, indices, values, _ = W.config3(rows=12000, cols=cols, nnz=20, informative=40, seed=21)
     X = W.csr_to_dense(indptr, indices, values, cols)
     y = (np.nan_to_num(X[:, :40]).sum(axis=1) + 0.1 * np.random.default_rng(3).normal(size=len(X))).astype(np.float32)
-    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 6, "max_bin": max_bin, "eta": 0.3}
+    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 6, "max_bin": max_bin, "eta": 0.3,
+              "hip_csr_root_columns": root_columns}
     d = xgb.DMatrix(_csr(indptr, indices, values, cols), label=y)
     bst = xgb.train(params, d, 5)
     ref = O.train(X, y, _oracle_params(params), 5)

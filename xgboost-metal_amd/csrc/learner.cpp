@@ -201,19 +201,21 @@ void DMatrix::quantize_sparse(uint32_t max_bin) {
   hist_bins = std::max(1u, std::min(max_bin, rows));
   d_cuts.ensure((size_t)cols * max_bin * sizeof(float));
   d_counts.ensure((size_t)cols * sizeof(uint32_t));
-  {
-    DeviceBuffer colptr, csc_rows, csc_values;
-    colptr.ensure(((size_t)cols + 1) * sizeof(uint64_t));
-    csc_rows.ensure(std::max<size_t>(nnz, 1) * sizeof(uint32_t));
-    csc_values.ensure(std::max<size_t>(nnz, 1) * sizeof(float));
-    kcheck(mgb_csr_to_csc(d_indptr.as<uint64_t>(), d_indices.as<uint32_t>(), d_values.as<float>(), rows, cols, nnz,
-                          colptr.as<uint64_t>(), csc_rows.as<uint32_t>(), csc_values.as<float>()),
-           "CSR column copy");
-    const float* w = weights.empty() ? nullptr : d_weights.as<float>();
-    kcheck(mgb_sketch_cuts_csc(csc_values.as<float>(), csc_rows.as<uint32_t>(), colptr.as<uint64_t>(), rows, cols, w,
-                               max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
-           "quantile sketch");
-  }
+  // Column-major copy: the sketch's input, and (with its codes) the root
+  // histogram's.
+  DeviceBuffer csc_values, csc_cols;
+  d_colptr.ensure(((size_t)cols + 1) * sizeof(uint64_t));
+  d_csc_rows.ensure(std::max<size_t>(nnz, 1) * sizeof(uint32_t));
+  csc_values.ensure(std::max<size_t>(nnz, 1) * sizeof(float));
+  csc_cols.ensure(std::max<size_t>(nnz, 1) * sizeof(uint32_t));
+  kcheck(mgb_csr_to_csc(d_indptr.as<uint64_t>(), d_indices.as<uint32_t>(), d_values.as<float>(), rows, cols, nnz,
+                        d_colptr.as<uint64_t>(), d_csc_rows.as<uint32_t>(), csc_values.as<float>(),
+                        csc_cols.as<uint32_t>()),
+         "CSR column copy");
+  const float* w = weights.empty() ? nullptr : d_weights.as<float>();
+  kcheck(mgb_sketch_cuts_csc(csc_values.as<float>(), d_csc_rows.as<uint32_t>(), d_colptr.as<uint64_t>(), rows, cols,
+                             w, max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
+         "quantile sketch");
   counts_host.resize(cols);
   cuts_host.resize((size_t)cols * max_bin);
   d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
@@ -238,6 +240,10 @@ void DMatrix::quantize_sparse(uint32_t max_bin) {
   kcheck(mgb_quantize_csr(d_indices.as<uint32_t>(), d_values.as<float>(), nnz, d_cuts.as<float>(),
                           d_counts.as<uint32_t>(), max_bin, bin_bytes, matrix.missing_code, d_codes.get()),
          "CSR codes");
+  d_csc_codes.ensure(std::max<size_t>(nnz, 1) * bin_bytes);
+  kcheck(mgb_quantize_csr(csc_cols.as<uint32_t>(), csc_values.as<float>(), nnz, d_cuts.as<float>(),
+                          d_counts.as<uint32_t>(), max_bin, bin_bytes, matrix.missing_code, d_csc_codes.get()),
+         "CSR column codes");
   kcheck(mgb_synchronize(), "synchronize");
   quantized_max_bin = max_bin;
   sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
@@ -587,8 +593,12 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
   const uint32_t* features = sample_columns(data.cols);
   if (data.sparse) {
+    const bool root_columns = integer("hip_csr_root_columns", 1) != 0;
     kcheck(mgb_grow_tree_csr(&shape, &data.csr, data.d_indptr.as<uint64_t>(), data.d_indices.as<uint32_t>(),
-                             data.d_codes.get(), data.d_cuts.as<float>(), data.d_counts.as<uint32_t>(),
+                             data.d_codes.get(), root_columns ? data.d_colptr.as<uint64_t>() : nullptr,
+                             root_columns ? data.d_csc_rows.as<uint32_t>() : nullptr,
+                             root_columns ? data.d_csc_codes.get() : nullptr, data.d_cuts.as<float>(),
+                             data.d_counts.as<uint32_t>(),
                              d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, d_tree_ws_.get(),
                              d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
            "tree growth");

@@ -59,6 +59,7 @@ struct DMatrix {
   std::vector<uint32_t> indices;
   std::vector<float> values;
   DeviceBuffer d_indptr, d_indices, d_values, d_codes;
+  DeviceBuffer d_colptr, d_csc_rows, d_csc_codes;  // column-major copy (root histogram)
   MgbCsrMatrix csr{};
   std::vector<float> labels, weights, base_margin;
   std::vector<std::string> feature_names, feature_types;

@@ -128,7 +128,7 @@ using namespace mgb;
 extern "C" {
 
 int mgb_csr_to_csc(const uint64_t* indptr, const uint32_t* indices, const float* values, uint32_t rows, uint32_t cols,
-                   uint64_t nnz, uint64_t* colptr, uint32_t* csc_rows, float* csc_values) {
+                   uint64_t nnz, uint64_t* colptr, uint32_t* csc_rows, float* csc_values, uint32_t* csc_cols) {
   if (nnz >= (1ull << 31)) { set_error("mgb_csr_to_csc: more than 2^31 - 1 nonzeros"); return -1; }
   hipStream_t s = stream();
   if (!nnz) {
@@ -161,6 +161,7 @@ int mgb_csr_to_csc(const uint64_t* indptr, const uint32_t* indices, const float*
   hipLaunchKernelGGL(k_colptr, dim3(grid_of(cols + 1, 256, 1024)), dim3(256), 0, s, (const uint32_t*)keys_out.p, nnz,
                      cols, colptr);
   MGB_LAUNCH_CHECK("k_colptr");
+  if (csc_cols) MGB_CHECK(hipMemcpyAsync(csc_cols, keys_out.p, nnz * 4, hipMemcpyDeviceToDevice, s));
   MGB_CHECK(hipStreamSynchronize(s));  // the scratch buffers are freed on return
   return 0;
 }

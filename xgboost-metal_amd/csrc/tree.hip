@@ -110,6 +110,9 @@ struct Tree {
   const uint64_t* csr_indptr; // CSR bin matrix (mgb_grow_tree_csr; NULL for a dense matrix)
   const uint32_t* csr_indices;
   const void* csr_codes;
+  const uint64_t* csc_colptr; // its column-major copy, for the root histogram (NULL: atomics at the root too)
+  const uint32_t* csc_rows;
+  const void* csc_codes;
   const float* cuts;
   const uint32_t* counts;
   const uint32_t* allowed;    // per feature: nonzero if in the tree's column sample (NULL: all)
@@ -596,6 +599,46 @@ __global__ void k_zero_built(Tree t, uint32_t depth) {
     int4* row = bank + (uint64_t)slot * per;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < per; i += (uint64_t)gridDim.x * blockDim.x)
       row[i] = make_int4(0, 0, 0, 0);
+  }
+}
+
+// CSR root histogram from the column-major codes: every row belongs to the
+// root, so a workgroup takes kRootFeatures consecutive features, accumulates
+// all their nonzeros in LDS and writes the features' whole bank rows with
+// plain stores -- no device atomics, which at the root would all land on one
+// node's histogram from every XCD at once.
+constexpr uint32_t kRootFeatures = 4;
+constexpr uint32_t kRootThreads = 512;
+template <typename BinT>
+__global__ __launch_bounds__(kRootThreads) void k_histogram_csc_root(Tree t) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  unsigned long long* lh = reinterpret_cast<unsigned long long*>(smem);  // [feature][bin][g, h]
+  const uint32_t B1 = t.bins1;
+  const uint32_t f0 = blockIdx.x * kRootFeatures;
+  const uint32_t nf = t.cols - f0 < kRootFeatures ? t.cols - f0 : kRootFeatures;
+  for (uint32_t i = threadIdx.x; i < kRootFeatures * B1 * 2; i += blockDim.x) lh[i] = 0;
+  uint64_t bound[kRootFeatures + 1];
+#pragma unroll
+  for (uint32_t j = 0; j <= kRootFeatures; ++j) bound[j] = t.csc_colptr[f0 + (j < nf ? j : nf)];
+  __syncthreads();
+  const float sg = t.scales[0], sh = t.scales[1];
+  const BinT* codes = reinterpret_cast<const BinT*>(t.csc_codes);
+  for (uint64_t i = bound[0] + threadIdx.x; i < bound[nf]; i += blockDim.x) {
+    const uint32_t code = codes[i];
+    if (code == t.missing_code) continue;
+    uint32_t j = 0;
+#pragma unroll
+    for (uint32_t q = 1; q < kRootFeatures; ++q) j += i >= bound[q] && q < nf ? 1u : 0u;
+    const float2 v = t.grad[t.csc_rows[i]];
+    unsigned long long* p = lh + ((uint64_t)j * B1 + code) * 2;
+    atomicAdd(p, (unsigned long long)(long long)rintf(v.x * sg));
+    atomicAdd(p + 1, (unsigned long long)(long long)rintf(v.y * sh));
+  }
+  __syncthreads();
+  int4* out = reinterpret_cast<int4*>(t.hist[0] + (uint64_t)f0 * B1 * 2);
+  for (uint32_t k = threadIdx.x; k < nf * B1; k += blockDim.x) {
+    const uint64_t g = lh[2 * k], h = lh[2 * k + 1];
+    out[k] = make_int4((int)(uint32_t)g, (int)(uint32_t)(g >> 32), (int)(uint32_t)h, (int)(uint32_t)(h >> 32));
   }
 }
 
@@ -1705,8 +1748,44 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   return 0;
 }
 
+}  // extern "C"
+
+namespace mgb {
+namespace {
+
+// One level's CSR histograms: the root from the column-major codes when
+// given, else clear the built nodes' rows and add their rows' nonzeros.
+int csr_histogram(const Tree& t, uint32_t bin_bytes, uint32_t depth, bool root_columns, uint32_t hgrid, uint32_t zx) {
+  if (depth == 0 && root_columns) {
+    const uint32_t lds = kRootFeatures * t.bins1 * 16;
+    const dim3 grid(div_up(t.cols, kRootFeatures));
+    auto fn = bin_bytes == 1 ? k_histogram_csc_root<uint8_t> : k_histogram_csc_root<uint16_t>;
+    if (hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      set_error("hipFuncSetAttribute(root histogram LDS) failed");
+      return -1;
+    }
+    launch(MGB_PROF_HISTOGRAM, fn, grid, dim3(kRootThreads), lds, t);
+    MGB_LAUNCH_CHECK("k_histogram_csc_root");
+    return 0;
+  }
+  const uint32_t zy = depth == 0 ? 1 : (1u << depth) < 1024 ? (1u << depth) : 1024;
+  launch(MGB_PROF_HISTOGRAM, k_zero_built, dim3(zx, zy), dim3(256), 0, t, depth);
+  MGB_LAUNCH_CHECK("k_zero_built");
+  auto fn = bin_bytes == 1 ? (depth == 0 ? k_histogram_csr<uint8_t, true> : k_histogram_csr<uint8_t, false>)
+                           : (depth == 0 ? k_histogram_csr<uint16_t, true> : k_histogram_csr<uint16_t, false>);
+  launch(MGB_PROF_HISTOGRAM, fn, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
+  MGB_LAUNCH_CHECK("k_histogram_csr");
+  return 0;
+}
+
+}  // namespace
+}  // namespace mgb
+
+extern "C" {
+
 int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const uint64_t* indptr,
-                      const uint32_t* indices, const void* codes, const float* cuts, const uint32_t* counts,
+                      const uint32_t* indices, const void* codes, const uint64_t* colptr, const uint32_t* csc_rows,
+                      const void* csc_codes, const float* cuts, const uint32_t* counts,
                       const float* grad, const float* scales, const MgbSplitParams* sp, const uint32_t* features,
                       void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
                       uint32_t* node_count) {
@@ -1729,6 +1808,8 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
   dm.cut_stride = m->cut_stride; dm.missing_code = m->missing_code; dm.group_features = shape->features_per_group;
   Tree t = make_tree(shape, &dm, L, reinterpret_cast<uint8_t*>(workspace));
   t.csr_indptr = indptr; t.csr_indices = indices; t.csr_codes = codes;
+  const bool root_columns = colptr && csc_rows && csc_codes;
+  t.csc_colptr = colptr; t.csc_rows = csc_rows; t.csc_codes = csc_codes;
   t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
   t.allowed = features;
@@ -1746,17 +1827,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
       launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
-    const uint32_t zy = depth == 0 ? 1 : (1u << depth) < 1024 ? (1u << depth) : 1024;
-    launch(MGB_PROF_HISTOGRAM, k_zero_built, dim3(zx, zy), dim3(256), 0, t, depth);
-    MGB_LAUNCH_CHECK("k_zero_built");
-    if (m->bin_bytes == 1) {
-      if (depth == 0) launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint8_t, true>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
-      else launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint8_t, false>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
-    } else {
-      if (depth == 0) launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint16_t, true>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
-      else launch(MGB_PROF_HISTOGRAM, k_histogram_csr<uint16_t, false>, dim3(hgrid), dim3(kCsrThreads), 0, t, depth);
-    }
-    MGB_LAUNCH_CHECK("k_histogram_csr");
+    if (csr_histogram(t, m->bin_bytes, depth, root_columns, hgrid, zx)) return -1;
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
     if (launch_split(t, depth, items)) return -1;
