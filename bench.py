@@ -273,13 +273,17 @@ def bench_large(xgb, args, which):
     launches = max(hist["launches"], 1)
     achieved = prof["histogram_bytes"] / (hist["ms"] * 1e-3) / 1e9 if hist["ms"] > 0 else 0.0
     rounds = spec["rounds"]
+    traffic = None
+    tfile = ROOT / "profiles" / f"histogram_traffic_config{which[1]}.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     line = {
         "metric": spec["metric"], "value": round(ms_per_step * rounds, 2), "unit": f"ms/{rounds} rounds",
         "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 3),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int64", "data": "synthetic",
         "config": dict({"workload": spec["workload"]}, **spec["shape"]),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": "k_histogram" if which == "c4" else "k_histogram_csr (+ k_zero_built, k_root_totals)",
                      "launches": launches, "algorithmic_bytes_per_launch": round(prof["histogram_bytes"] / launches),
                      "avg_launch_us": round(hist["ms"] * 1e3 / launches, 3)},

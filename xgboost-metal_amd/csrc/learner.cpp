@@ -224,15 +224,18 @@ void DMatrix::quantize_sparse(uint32_t max_bin) {
   uint32_t max_count = 0;
   for (auto c : counts_host) max_count = std::max(max_count, c);
   require(max_count <= hist_bins, "internal error: more cuts than histogram bins");
-  has_missing = nnz < (uint64_t)rows * cols || nonmissing() < nnz;
-  const uint32_t bin_bytes = (has_missing ? max_count <= 255 : max_count <= 256) ? 1 : 2;
+  // Absent entries carry no code, so a missing code is needed only for
+  // stored NaN entries: without them 256 cuts still fit u8 codes.
+  const bool stored_nan = nonmissing() < nnz;
+  has_missing = nnz < (uint64_t)rows * cols || stored_nan;
+  const uint32_t bin_bytes = (stored_nan ? max_count <= 255 : max_count <= 256) ? 1 : 2;
   matrix = MgbMatrix{};
   matrix.rows = rows;
   matrix.cols = cols;
   matrix.bin_bytes = bin_bytes;
   matrix.max_bin = hist_bins;
   matrix.cut_stride = max_bin;
-  matrix.missing_code = !has_missing ? 0xFFFFFFFFu : (bin_bytes == 1 ? 0xFFu : 0xFFFFu);
+  matrix.missing_code = !stored_nan ? 0xFFFFFFFFu : (bin_bytes == 1 ? 0xFFu : 0xFFFFu);
   matrix.group_features = 1;
   features_per_group = 1;
   csr = MgbCsrMatrix{rows, cols, hist_bins, max_bin, bin_bytes, matrix.missing_code, nnz};
