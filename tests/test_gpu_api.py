@@ -1,0 +1,123 @@
+"""GPU checks of the API surface around training: iterator-fed matrices train
+the same trees as one matrix, a `ref` matrix shares its cuts, in-place
+prediction equals DMatrix prediction, and model slices predict like
+iteration ranges (reference src/c_api.cpp:222-239, :503-518)."""
+import ctypes
+import json
+
+import numpy as np
+import pytest
+
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+PARAMS = {"tree_method": "hist", "max_depth": 5, "max_bin": 64, "eta": 0.3, "objective": "reg:squarederror"}
+
+
+def _batches(xgb):
+    class Batches(xgb.DataIter):
+        def __init__(self, parts):
+            self.parts = parts
+            self.i = 0
+            super().__init__()
+
+        def next(self, input_data):
+            if self.i == len(self.parts):
+                return False
+            input_data(**self.parts[self.i])
+            self.i += 1
+            return True
+
+        def reset(self):
+            self.i = 0
+
+    return Batches
+
+
+def _trees(bst):
+    return json.loads(bst.save_raw("json"))["learner"]["gradient_booster"]["model"]["trees"]
+
+
+def test_iterator_matrices_train_like_one_matrix(xgb):
+    X, y = W.config1(rows=6000, cols=10)
+    Batches = _batches(xgb)
+    splits = [0, 1500, 4000, 6000]
+    parts = [dict(data=X[a:b], label=y[a:b]) for a, b in zip(splits, splits[1:])]
+    whole = xgb.train(PARAMS, xgb.DMatrix(X, label=y), 8)
+    it = xgb.train(PARAMS, xgb.DMatrix(Batches(parts)), 8)
+    assert _trees(it) == _trees(whole)
+    q_whole = xgb.train(PARAMS, xgb.QuantileDMatrix(X, label=y, max_bin=64), 8)
+    q_it = xgb.train(PARAMS, xgb.QuantileDMatrix(Batches(parts), max_bin=64), 8)
+    assert _trees(q_it) == _trees(q_whole) == _trees(whole)
+
+
+def test_ref_matrix_shares_cuts(xgb):
+    X, y = W.config1(rows=5000, cols=8)
+    train = xgb.QuantileDMatrix(X, label=y, max_bin=32)
+    xgb.train({**PARAMS, "max_bin": 32}, train, 2)
+    sub = X[:700] * 0.5  # a different distribution: its own sketch would differ
+    ev = xgb.QuantileDMatrix(sub, label=y[:700], ref=train, max_bin=32)
+    own = xgb.QuantileDMatrix(sub, label=y[:700], max_bin=32)
+    bst = xgb.train({**PARAMS, "max_bin": 32}, ev, 1)
+    ip_ref, cut_ref = train.get_quantile_cut()
+    ip_ev, cut_ev = ev.get_quantile_cut()
+    np.testing.assert_array_equal(ip_ev, ip_ref)
+    np.testing.assert_array_equal(cut_ev.view(np.uint32), cut_ref.view(np.uint32))
+    xgb.train({**PARAMS, "max_bin": 32}, own, 1)
+    _, cut_own = own.get_quantile_cut()
+    assert cut_own.shape != cut_ref.shape or not np.array_equal(cut_own, cut_ref)
+    assert bst.num_boosted_rounds() == 1
+
+
+def test_inplace_predict_equals_dmatrix_predict(xgb):
+    import scipy.sparse as sp
+    X, y = W.config1(rows=3000, cols=12)
+    bst = xgb.train(PARAMS, xgb.DMatrix(X, label=y), 10)
+    d = xgb.DMatrix(X)
+    for kind, margin in (("value", False), ("margin", True)):
+        expect = bst.predict(d, output_margin=margin)
+        np.testing.assert_array_equal(bst.inplace_predict(X, predict_type=kind), expect)
+    np.testing.assert_array_equal(bst.inplace_predict(X, iteration_range=(2, 7)),
+                                  bst.predict(d, iteration_range=(2, 7)))
+    Xs = np.where(np.isnan(X), 0, X)
+    Xs[np.abs(Xs) < 0.5] = 0
+    ds = xgb.DMatrix(sp.csr_matrix(Xs))
+    np.testing.assert_array_equal(bst.inplace_predict(sp.csr_matrix(Xs)), bst.predict(ds))
+    # `missing` applies to in-place input as to a DMatrix.
+    Xm = np.where(np.isnan(X), -999.0, X).astype(np.float32)
+    np.testing.assert_array_equal(bst.inplace_predict(Xm, missing=-999.0), bst.predict(d))
+
+
+def test_model_slices_predict_like_iteration_ranges(xgb):
+    X, y = W.config1(rows=2000, cols=6)
+    bst = xgb.train(PARAMS, xgb.DMatrix(X, label=y), 9)
+    d = xgb.DMatrix(X)
+    for a, b in ((0, 3), (3, 9), (4, 5)):
+        np.testing.assert_array_equal(bst[a:b].predict(d), bst.predict(d, iteration_range=(a, b)))
+    # A stepped slice holds rounds 0, 3 and 6: its margin is the base margin
+    # plus those three trees.
+    base = float(json.loads(bst.save_raw("json"))["learner"]["learner_model_param"]["base_score"].strip("[]"))
+    single = [bst[r:r + 1].predict(d, output_margin=True).astype(np.float64) - base for r in (0, 3, 6)]
+    np.testing.assert_allclose(bst[0:9:3].predict(d, output_margin=True), base + sum(single), rtol=1e-6, atol=1e-6)
+
+
+def test_predict_to_buffer(xgb):
+    X, y = W.config1(rows=500, cols=5)
+    bst = xgb.train(PARAMS, xgb.DMatrix(X, label=y), 3)
+    d = xgb.DMatrix(X)
+    lib = xgb.core._LIB
+    buf = np.zeros(500, np.float32)
+    shape = ctypes.POINTER(ctypes.c_uint64)()
+    dims = ctypes.c_uint64()
+    cfg = json.dumps({"type": 0, "training": False, "iteration_begin": 0, "iteration_end": 0,
+                      "strict_shape": False}).encode()
+    assert lib.XGBoosterPredictToBuffer(bst.handle, d.handle, cfg, buf.ctypes.data_as(ctypes.c_void_p),
+                                        ctypes.c_uint64(500), ctypes.byref(shape), ctypes.byref(dims)) == 0
+    assert dims.value == 1 and shape[0] == 500
+    np.testing.assert_array_equal(buf, bst.predict(d))
+    small = np.zeros(10, np.float32)
+    assert lib.XGBoosterPredictToBuffer(bst.handle, d.handle, cfg, small.ctypes.data_as(ctypes.c_void_p),
+                                        ctypes.c_uint64(10), ctypes.byref(shape), ctypes.byref(dims)) == -1
+    assert b"capacity" in lib.XGBGetLastError()
+    assert not small.any()

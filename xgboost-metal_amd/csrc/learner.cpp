@@ -151,16 +151,21 @@ void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
   hist_bins = std::max(1u, std::min(max_bin, rows));
   d_cuts.ensure((size_t)cols * max_bin * sizeof(float));
   d_counts.ensure((size_t)cols * sizeof(uint32_t));
-  const float* w = weights.empty() ? nullptr : d_weights.as<float>();
-  kcheck(mgb_sketch_cuts(d_data.as<float>(), rows, cols, w, max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
-         "quantile sketch");
-  counts_host.resize(cols);
-  cuts_host.resize((size_t)cols * max_bin);
-  d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
-  d_cuts.download(cuts_host.data(), cuts_host.size() * sizeof(float));
+  if (cut_source) {
+    take_cuts(max_bin);
+  } else {
+    const float* w = weights.empty() ? nullptr : d_weights.as<float>();
+    kcheck(mgb_sketch_cuts(d_data.as<float>(), rows, cols, w, max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
+           "quantile sketch");
+    counts_host.resize(cols);
+    cuts_host.resize((size_t)cols * max_bin);
+    d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
+    d_cuts.download(cuts_host.data(), cuts_host.size() * sizeof(float));
+  }
   auto t1 = std::chrono::steady_clock::now();
   uint32_t max_count = 0;
   for (auto c : counts_host) max_count = std::max(max_count, c);
+  hist_bins = std::max(hist_bins, max_count);  // a reference matrix's cuts may outnumber these rows
   require(max_count <= hist_bins, "internal error: more cuts than histogram bins");
   d_missing.ensure(sizeof(uint32_t));
   kcheck(mgb_memset(d_missing.get(), 0, sizeof(uint32_t)), "memset");
@@ -185,6 +190,19 @@ void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
   quantized_max_bin = max_bin;
   sketch_seconds += std::chrono::duration<double>(t1 - t0).count();
   relayout(layout);
+}
+
+// Cuts of the reference matrix (QuantileDMatrix ref=, src/c_api.cpp:225-239):
+// evaluation data binned exactly like the training data.
+void DMatrix::take_cuts(uint32_t max_bin) {
+  DMatrix& src = *cut_source;
+  require(src.cols == cols, "The reference DMatrix has " + std::to_string(src.cols) + " features, this one " +
+                                std::to_string(cols) + ".");
+  src.quantize(max_bin, src.quantized_layout, src.quantized_group_request);
+  counts_host = src.counts_host;
+  cuts_host = src.cuts_host;
+  d_cuts.upload(cuts_host.data(), cuts_host.size() * sizeof(float));
+  d_counts.upload(counts_host.data(), counts_host.size() * sizeof(uint32_t));
 }
 
 // CSR matrices (src/data.cpp:721-870): the sketch reads a column-major copy
@@ -212,17 +230,22 @@ void DMatrix::quantize_sparse(uint32_t max_bin) {
                         d_colptr.as<uint64_t>(), d_csc_rows.as<uint32_t>(), csc_values.as<float>(),
                         csc_cols.as<uint32_t>()),
          "CSR column copy");
-  const float* w = weights.empty() ? nullptr : d_weights.as<float>();
-  kcheck(mgb_sketch_cuts_csc(csc_values.as<float>(), d_csc_rows.as<uint32_t>(), d_colptr.as<uint64_t>(), rows, cols,
-                             w, max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
-         "quantile sketch");
-  counts_host.resize(cols);
-  cuts_host.resize((size_t)cols * max_bin);
-  d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
-  d_cuts.download(cuts_host.data(), cuts_host.size() * sizeof(float));
+  if (cut_source) {
+    take_cuts(max_bin);
+  } else {
+    const float* w = weights.empty() ? nullptr : d_weights.as<float>();
+    kcheck(mgb_sketch_cuts_csc(csc_values.as<float>(), d_csc_rows.as<uint32_t>(), d_colptr.as<uint64_t>(), rows,
+                               cols, w, max_bin, d_cuts.as<float>(), d_counts.as<uint32_t>()),
+           "quantile sketch");
+    counts_host.resize(cols);
+    cuts_host.resize((size_t)cols * max_bin);
+    d_counts.download(counts_host.data(), cols * sizeof(uint32_t));
+    d_cuts.download(cuts_host.data(), cuts_host.size() * sizeof(float));
+  }
   auto t1 = std::chrono::steady_clock::now();
   uint32_t max_count = 0;
   for (auto c : counts_host) max_count = std::max(max_count, c);
+  hist_bins = std::max(hist_bins, max_count);
   require(max_count <= hist_bins, "internal error: more cuts than histogram bins");
   // Absent entries carry no code, so a missing code is needed only for
   // stored NaN entries: without them 256 cuts still fit u8 codes.

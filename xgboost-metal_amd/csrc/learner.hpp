@@ -92,6 +92,8 @@ struct DMatrix {
   uint32_t choose_group(uint32_t request) const;
   void relayout(int layout);
   void quantize_sparse(uint32_t max_bin);
+  void take_cuts(uint32_t max_bin);
+  std::shared_ptr<DMatrix> cut_source;  // QuantileDMatrix ref: take its cuts instead of sketching
   uint64_t nonmissing() const;
   void set_info(const std::string& field, const float* values, size_t count);
   const std::vector<float>& get_info(const std::string& field) const;

@@ -10,7 +10,10 @@ from __future__ import annotations
 import ctypes
 import json
 import os
-from typing import Any, Dict, Iterable, List, Optional, Sequence, Tuple, Union
+import sys
+import weakref
+from abc import ABC, abstractmethod
+from typing import Any, Callable, Dict, Iterable, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
@@ -92,6 +95,108 @@ def _feature_names_of(data: Any) -> Optional[List[str]]:
     return None
 
 
+def _missing_value(missing: Optional[float]) -> Optional[float]:
+    return None if missing is None or np.isnan(missing) else float(missing)
+
+
+class DataIter(ABC):
+    """User-defined batch iterator (reference core.py:275).
+
+    ``next(input_data)`` calls ``input_data(data=..., label=..., ...)`` once per
+    batch and returns False after the last; ``reset()`` rewinds.  The batches
+    are concatenated in host memory: ``cache_prefix`` (external memory) is
+    rejected.  Exceptions raised inside the callbacks are held and re-raised
+    after the C call returns, as upstream does.
+    """
+
+    def __init__(self, cache_prefix: Optional[str] = None, release_data: bool = True, *, on_host: bool = True,
+                 min_cache_page_bytes: Optional[int] = None) -> None:
+        self.cache_prefix = cache_prefix
+        self.on_host = on_host
+        self.min_cache_page_bytes = min_cache_page_bytes
+        self._handle = _ProxyDMatrix()
+        self._exception: Optional[BaseException] = None
+        self._enable_categorical = False
+        self._release = release_data
+        self._temporary_data: Optional[Any] = None
+        self._callbacks: Optional[Tuple[Callable, Callable]] = None
+
+    def get_callbacks(self, enable_categorical: bool) -> Tuple[Callable, Callable]:
+        """C function pointers for reset and next; kept alive by the iterator."""
+        reset = ctypes.CFUNCTYPE(None, ctypes.c_void_p)(self._reset_wrapper)
+        nxt = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)(self._next_wrapper)
+        self._enable_categorical = enable_categorical
+        self._callbacks = (reset, nxt)
+        return reset, nxt
+
+    @property
+    def proxy(self) -> "_ProxyDMatrix":
+        return self._handle
+
+    def _handle_exception(self, fn: Callable, default: Any) -> Any:
+        if self._exception is not None:
+            return default
+        try:
+            return fn()
+        except Exception as e:  # pylint: disable=broad-except
+            # A Python exception cannot cross the C callback: keep it, end
+            # the iteration, and raise it after the C call returns.
+            self._exception = e.with_traceback(sys.exc_info()[2])
+        return default
+
+    def reraise(self) -> None:
+        self._temporary_data = None
+        if self._exception is not None:
+            exc, self._exception = self._exception, None
+            raise exc
+
+    def _reset_wrapper(self, this: None) -> None:
+        if self._release:
+            self._temporary_data = None
+        self._handle_exception(self.reset, None)
+
+    def _next_wrapper(self, this: None) -> int:
+        def input_data(*, data: Any, feature_names: Optional[Sequence[str]] = None,
+                       feature_types: Optional[Sequence[str]] = None, **kwargs: Any) -> None:
+            if feature_names is None:
+                feature_names = _feature_names_of(data)
+            self._temporary_data = self.proxy._set_data(data)
+            self.proxy.set_info(feature_names=feature_names, feature_types=feature_types, **kwargs)
+
+        if self._release:
+            self._temporary_data = None
+        return self._handle_exception(lambda: int(self.next(input_data)), 0)
+
+    @abstractmethod
+    def reset(self) -> None:
+        """Rewind the iterator."""
+        raise NotImplementedError()
+
+    @abstractmethod
+    def next(self, input_data: Callable) -> bool:
+        """Pass the next batch to ``input_data``; False when there is none."""
+        raise NotImplementedError()
+
+
+class _SingleBatchIter(DataIter):
+    """One in-memory batch as an iterator (QuantileDMatrix with ``ref``)."""
+
+    def __init__(self, **kwargs: Any) -> None:
+        self._kwargs = kwargs
+        self._done = False
+        super().__init__(release_data=False)
+
+    def next(self, input_data: Callable) -> bool:
+        if self._done:
+            return False
+        self._done = True
+        input_data(**self._kwargs)
+        return True
+
+    def reset(self) -> None:
+        self._done = False
+
+
 class DMatrix:
     """Data matrix for training and prediction (reference core.py:676)."""
 
@@ -99,7 +204,16 @@ class DMatrix:
                  missing: Optional[float] = None, silent: bool = False, feature_names: Optional[Sequence[str]] = None,
                  feature_types: Optional[Sequence[str]] = None, nthread: Optional[int] = None,
                  enable_categorical: bool = False, **kwargs: Any) -> None:
+        if isinstance(data, ctypes.c_void_p):
+            # A handle the C API returned (slices).
+            self.handle = data
+            return
         self.handle = ctypes.c_void_p()
+        if isinstance(data, DataIter):
+            self._init_from_iter(data, missing)
+            self.set_info(label=label, weight=weight, base_margin=base_margin, feature_names=feature_names,
+                          feature_types=feature_types)
+            return
         self._init(data, missing, kwargs.pop("_config", None))
         if feature_names is None:
             feature_names = _feature_names_of(data)
@@ -127,10 +241,45 @@ class DMatrix:
         arr = _to_numpy_2d(data)
         _check_call(_LIB.XGDMatrixCreateFromDense(_array_interface(arr), cfg, ctypes.byref(self.handle)))
 
+    def _init_from_iter(self, it: "DataIter", missing: Optional[float]) -> None:
+        """Concatenate an iterator's batches in memory (reference core.py:862)."""
+        if it.cache_prefix:
+            raise XGBoostError("External memory (cache_prefix) is not supported by this engine")
+        reset, nxt = it.get_callbacks(False)
+        config = json.dumps({"missing": _missing_value(missing), "cache_prefix": "", "nthread": 0}).encode()
+        ret = _LIB.XGDMatrixCreateFromCallback(None, it.proxy.handle, reset, nxt, config, ctypes.byref(self.handle))
+        it.reraise()
+        _check_call(ret)
+
     def __del__(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:
             _check_call(_LIB.XGDMatrixFree(self.handle))
             self.handle = None
+
+    def slice(self, rindex: Union[List[int], np.ndarray], allow_groups: bool = False) -> "DMatrix":
+        """A new DMatrix holding the rows ``rindex`` (reference core.py:1264)."""
+        idx = np.ascontiguousarray(np.asarray(rindex, dtype=np.int32).reshape(-1))
+        handle = ctypes.c_void_p()
+        _check_call(_LIB.XGDMatrixSliceDMatrixEx(self.handle, idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                                                 c_bst_ulong(idx.size), ctypes.byref(handle),
+                                                 ctypes.c_int(1 if allow_groups else 0)))
+        return DMatrix(handle)
+
+    def get_data(self) -> Any:
+        """The predictors as a scipy CSR matrix of the stored values (reference core.py:1122)."""
+        import scipy.sparse
+
+        nnz = self.num_nonmissing()
+        indptr = np.empty(self.num_row() + 1, dtype=np.uint64)
+        indices = np.empty(nnz, dtype=np.uint32)
+        data = np.empty(nnz, dtype=np.float32)
+        _check_call(_LIB.XGDMatrixGetDataAsCSR(self.handle, b"{}", indptr.ctypes.data_as(ctypes.POINTER(c_bst_ulong)),
+                                               indices.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                               data.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return scipy.sparse.csr_matrix((data, indices, indptr), shape=(self.num_row(), self.num_col()))
+
+    def save_binary(self, fname: Union[str, os.PathLike], silent: bool = True) -> None:
+        _check_call(_LIB.XGDMatrixSaveBinary(self.handle, c_str(os.fspath(fname)), ctypes.c_int(silent)))
 
     # ---- info ----------------------------------------------------------------
     def set_info(self, *, label: Any = None, weight: Any = None, base_margin: Any = None,
@@ -238,6 +387,32 @@ class DMatrix:
         return _from_interface(indptr.value), _from_interface(values.value)
 
 
+class _ProxyDMatrix(DMatrix):
+    """Staging matrix an iterator fills one batch at a time (reference core.py:1430).
+
+    The C side copies each batch when it is set.
+    """
+
+    def __init__(self) -> None:  # pylint: disable=super-init-not-called
+        self.handle = ctypes.c_void_p()
+        _check_call(_LIB.XGProxyDMatrixCreate(ctypes.byref(self.handle)))
+
+    def _set_data(self, data: Any) -> Any:
+        if type(data).__name__ in ("csc_matrix", "csc_array", "coo_matrix", "coo_array"):
+            data = data.tocsr()
+        if _is_scipy_csr(data):
+            indptr = np.ascontiguousarray(data.indptr, dtype=np.int64)
+            indices = np.ascontiguousarray(data.indices, dtype=np.int32)
+            values = np.ascontiguousarray(data.data, dtype=np.float32)
+            _check_call(_LIB.XGProxyDMatrixSetDataCSR(self.handle, _array_interface(indptr),
+                                                      _array_interface(indices), _array_interface(values),
+                                                      c_bst_ulong(data.shape[1])))
+            return indptr, indices, values
+        arr = _to_numpy_2d(data)
+        _check_call(_LIB.XGProxyDMatrixSetDataDense(self.handle, _array_interface(arr)))
+        return arr
+
+
 def _from_interface(text: bytes) -> np.ndarray:
     inter = json.loads(text)
     n = inter["shape"][0]
@@ -259,6 +434,33 @@ class QuantileDMatrix(DMatrix):
                  feature_types: Optional[Sequence[str]] = None, nthread: Optional[int] = None, max_bin: int = 256,
                  ref: Optional[DMatrix] = None, enable_categorical: bool = False, **kwargs: Any) -> None:
         self.max_bin = int(max_bin)
+        if isinstance(data, ctypes.c_void_p):
+            self.handle = data
+            return
+        if isinstance(data, DataIter) or ref is not None:
+            # Iterator path (reference core.py:1620-1660): batches are
+            # concatenated; ``ref`` makes this matrix use the cuts of the
+            # reference matrix instead of sketching its own.
+            it = data
+            if not isinstance(it, DataIter):
+                it = _SingleBatchIter(data=data, label=label, weight=weight, base_margin=base_margin,
+                                      feature_names=feature_names if feature_names is not None
+                                      else _feature_names_of(data), feature_types=feature_types)
+                label = weight = base_margin = None
+                feature_names = feature_types = None
+            if it.cache_prefix:
+                raise XGBoostError("External memory (cache_prefix) is not supported by this engine")
+            self.handle = ctypes.c_void_p()
+            reset, nxt = it.get_callbacks(enable_categorical)
+            config = json.dumps({"missing": _missing_value(missing), "nthread": 0, "max_bin": self.max_bin}).encode()
+            ret = _LIB.XGQuantileDMatrixCreateFromCallback(None, it.proxy.handle,
+                                                           ref.handle if ref is not None else None, reset, nxt,
+                                                           config, ctypes.byref(self.handle))
+            it.reraise()
+            _check_call(ret)
+            self.set_info(label=label, weight=weight, base_margin=base_margin, feature_names=feature_names,
+                          feature_types=feature_types)
+            return
         super().__init__(data, label, weight=weight, base_margin=base_margin, missing=missing,
                          feature_names=feature_names, feature_types=feature_types,
                          _config={"max_bin": self.max_bin, "quantile": True})
@@ -433,9 +635,116 @@ class Booster:
         return out.reshape(dims_v)
 
     def inplace_predict(self, data: Any, iteration_range: Tuple[int, int] = (0, 0), predict_type: str = "value",
-                        missing: float = np.nan, **kwargs: Any) -> np.ndarray:
-        dmat = DMatrix(data, missing=missing)
-        return self.predict(dmat, output_margin=predict_type == "margin", iteration_range=iteration_range)
+                        missing: float = np.nan, validate_features: bool = True, base_margin: Any = None,
+                        strict_shape: bool = False) -> np.ndarray:
+        """Predict straight from a numpy array, DataFrame or scipy CSR matrix (reference core.py:2642)."""
+        if predict_type not in ("value", "margin"):
+            raise ValueError(f"predict_type must be 'value' or 'margin', got {predict_type!r}")
+        if base_margin is not None:
+            dmat = DMatrix(data, base_margin=base_margin, missing=missing)
+            return self.predict(dmat, output_margin=predict_type == "margin", iteration_range=iteration_range,
+                                strict_shape=strict_shape)
+        config = json.dumps({"type": 1 if predict_type == "margin" else 0, "training": False,
+                             "iteration_begin": int(iteration_range[0]), "iteration_end": int(iteration_range[1]),
+                             "missing": _missing_value(missing), "strict_shape": bool(strict_shape),
+                             "cache_id": 0}).encode()
+        shape = ctypes.POINTER(c_bst_ulong)()
+        dims = c_bst_ulong()
+        result = ctypes.POINTER(ctypes.c_float)()
+        if type(data).__name__ in ("csc_matrix", "csc_array", "coo_matrix", "coo_array"):
+            data = data.tocsr()
+        if _is_scipy_csr(data):
+            indptr = np.ascontiguousarray(data.indptr, dtype=np.int64)
+            indices = np.ascontiguousarray(data.indices, dtype=np.int32)
+            values = np.ascontiguousarray(data.data, dtype=np.float32)
+            _check_call(_LIB.XGBoosterPredictFromCSR(self.handle, _array_interface(indptr), _array_interface(indices),
+                                                     _array_interface(values), c_bst_ulong(data.shape[1]), config,
+                                                     None, ctypes.byref(shape), ctypes.byref(dims),
+                                                     ctypes.byref(result)))
+        else:
+            arr = _to_numpy_2d(data)
+            _check_call(_LIB.XGBoosterPredictFromDense(self.handle, _array_interface(arr), config, None,
+                                                       ctypes.byref(shape), ctypes.byref(dims),
+                                                       ctypes.byref(result)))
+        dims_v = [shape[i] for i in range(dims.value)]
+        n = int(np.prod(dims_v)) if dims_v else 0
+        out = np.ctypeslib.as_array(result, shape=(n,)).copy() if n else np.zeros(0, np.float32)
+        return out.reshape(dims_v)
+
+    # ---- model inspection ----------------------------------------------------------
+    def __getitem__(self, val: Union[int, slice, Any]) -> "Booster":
+        """Trees of the rounds in ``val`` as a new Booster (reference core.py:1981)."""
+        if isinstance(val, (int, np.integer)) and not isinstance(val, bool):
+            val = slice(int(val), int(val) + 1)
+        if val is Ellipsis:
+            val = slice(0, 0)
+        if isinstance(val, tuple):
+            raise ValueError("Only supports slicing through 1 dimension.")
+        if not isinstance(val, slice):
+            raise TypeError(f"Expecting an int, slice or Ellipsis, got {type(val).__name__}")
+        start = 0 if val.start is None or val.start is Ellipsis else val.start
+        stop = 0 if val.stop is None or val.stop is Ellipsis else val.stop
+        if val.stop is not None and val.stop is not Ellipsis and stop < start:
+            raise ValueError("Invalid slice", val)
+        step = val.step if val.step is not None else 1
+        handle = ctypes.c_void_p()
+        status = _LIB.XGBoosterSlice(self.handle, ctypes.c_int(start), ctypes.c_int(stop), ctypes.c_int(step),
+                                     ctypes.byref(handle))
+        if status == -2:
+            raise IndexError("Layer index out of range")
+        _check_call(status)
+        sliced = Booster()
+        _check_call(_LIB.XGBoosterFree(sliced.handle))
+        sliced.handle = handle
+        sliced.feature_names = self.feature_names
+        sliced.feature_types = self.feature_types
+        return sliced
+
+    def __iter__(self) -> Iterable["Booster"]:
+        for i in range(self.num_boosted_rounds()):
+            yield self[i]
+
+    def get_dump(self, fmap: Union[str, os.PathLike] = "", with_stats: bool = False,
+                 dump_format: str = "text") -> List[str]:
+        """One string per tree in the text, JSON or dot format (reference core.py:3198)."""
+        fmap = os.fspath(os.path.expanduser(fmap))
+        length = c_bst_ulong()
+        sarr = ctypes.POINTER(ctypes.c_char_p)()
+        _check_call(_LIB.XGBoosterDumpModelEx(self.handle, c_str(fmap), ctypes.c_int(with_stats), c_str(dump_format),
+                                              ctypes.byref(length), ctypes.byref(sarr)))
+        return [sarr[i].decode() for i in range(length.value)]
+
+    def dump_model(self, fout: Any, fmap: Union[str, os.PathLike] = "", with_stats: bool = False,
+                   dump_format: str = "text") -> None:
+        """Write the dump to a file or stream (reference core.py:3153)."""
+        dumps = self.get_dump(fmap, with_stats, dump_format)
+        own = isinstance(fout, (str, os.PathLike))
+        f = open(os.fspath(os.path.expanduser(fout)), "w", encoding="utf-8") if own else fout
+        try:
+            if dump_format == "json":
+                f.write("[\n" + ",\n".join(dumps) + "\n]")
+            else:
+                for i, d in enumerate(dumps):
+                    f.write(f"booster[{i}]:\n{d}")
+        finally:
+            if own:
+                f.close()
+
+    def get_score(self, fmap: Union[str, os.PathLike] = "", importance_type: str = "weight") -> Dict[str, float]:
+        """Per-feature importance over the split nodes (reference core.py:3250)."""
+        fmap = os.fspath(os.path.expanduser(fmap))
+        features = ctypes.POINTER(ctypes.c_char_p)()
+        scores = ctypes.POINTER(ctypes.c_float)()
+        n_features = c_bst_ulong()
+        dims = c_bst_ulong()
+        shape = ctypes.POINTER(c_bst_ulong)()
+        config = json.dumps({"importance_type": importance_type, "feature_map": fmap}).encode()
+        _check_call(_LIB.XGBoosterFeatureScore(self.handle, config, ctypes.byref(n_features), ctypes.byref(features),
+                                               ctypes.byref(dims), ctypes.byref(shape), ctypes.byref(scores)))
+        return {features[i].decode(): float(scores[i]) for i in range(n_features.value)}
+
+    def get_fscore(self, fmap: Union[str, os.PathLike] = "") -> Dict[str, float]:
+        return self.get_score(fmap, importance_type="weight")
 
     # ---- model IO ----------------------------------------------------------------
     def save_model(self, fname: Union[str, os.PathLike]) -> None:

@@ -108,15 +108,13 @@ class XGBModel:
 
     @property
     def feature_importances_(self) -> np.ndarray:
-        trees = self.get_booster().trees_to_json()
-        n = self.get_booster().num_features()
-        gain = np.zeros(n)
-        for tree in trees:
-            for left, feat, loss in zip(tree["left_children"], tree["split_indices"], tree["loss_changes"]):
-                if left >= 0:
-                    gain[feat] += loss
-        total = gain.sum()
-        return (gain / total if total > 0 else gain).astype(np.float32)
+        """Normalised ``get_score(importance_type or "gain")`` per feature (reference sklearn.py:1609)."""
+        b = self.get_booster()
+        score = b.get_score(importance_type=self.importance_type or "gain")
+        names = b.feature_names if b.feature_names is not None else [f"f{i}" for i in range(b.num_features())]
+        values = np.array([score.get(f, 0.0) for f in names], dtype=np.float32)
+        total = values.sum()
+        return values if total == 0 else values / total
 
 
 class XGBRegressor(XGBModel):
