@@ -228,6 +228,30 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
 int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode* nodes, const uint32_t* tree_offsets,
                 uint32_t trees, float* margin);
 
+/* ---- evaluation metrics (src/metrics.cpp:8-159) ------------------------- */
+/* Elementwise metric kinds, numbered as the reference's metric table
+ * (src/metrics.cpp:13-16). */
+enum {
+  MGB_METRIC_RMSE = 0, MGB_METRIC_MAE = 1, MGB_METRIC_RMSLE = 2, MGB_METRIC_LOGLOSS = 3, MGB_METRIC_ERROR = 6,
+  MGB_METRIC_MAPE = 7, MGB_METRIC_MPHE = 8, MGB_METRIC_POISSON = 9, MGB_METRIC_GAMMA_DEVIANCE = 10,
+  MGB_METRIC_TWEEDIE = 11, MGB_METRIC_GAMMA_NLOGLIK = 12
+};
+/* Scratch bytes mgb_metric_sum and mgb_metric_auc need for `rows`. */
+size_t mgb_metric_workspace_bytes(uint32_t rows);
+/* (sum of weight * loss, sum of weight) over rows into out[2] (host), with
+ * the reference's summation order: a 256-element pairwise tree per block,
+ * compensated sums over blocks, a final tree (kernels/boost.metal:2225-2295).
+ * weights NULL = 1; parameter = error threshold, huber slope or tweedie
+ * power.  Synchronises. */
+int mgb_metric_sum(const float* pred, const float* labels, const float* weights, uint32_t rows, uint32_t kind,
+                   float parameter, float* out, void* workspace, size_t workspace_bytes);
+/* ROC-AUC area (pr = 0) or PR-AUC area (pr = 1) in binary64 over the rows
+ * sorted by descending prediction, tied predictions forming one step; out =
+ * {area, positive weight, negative weight} on the host
+ * (kernels/radix_sort.metal.h:427-790).  Synchronises. */
+int mgb_metric_auc(const float* pred, const float* labels, const float* weights, uint32_t rows, int pr, double* out,
+                   void* workspace, size_t workspace_bytes);
+
 #ifdef __cplusplus
 }
 #endif

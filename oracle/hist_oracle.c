@@ -938,3 +938,216 @@ void oracle_predict_margin(const float* X, uint32_t rows, uint32_t cols, const O
     out[r] = sum;
   }
 }
+
+/* ---- evaluation metrics ------------------------------------------------- */
+/* kernels/boost.metal:51: log(1 + x) with the rounding of 1 + x compensated. */
+static float log1p_compensated(float x) {
+  float y = 1.0f + x;
+  return y == 1.0f ? x : logf(y) * x / (y - 1.0f);
+}
+
+/* kernels/boost.metal:2245-2264 (per-row loss). */
+static float metric_loss(uint32_t kind, float pred, float label, float parameter) {
+  switch (kind) {
+    case 0: { float d = pred - label; return d * d; }
+    case 1: return fabsf(pred - label);
+    case 2: { float d = log1p_compensated(pred) - log1p_compensated(label); return d * d; }
+    case 3: return -label * logf(fmaxf(pred, 1.0e-16f)) - (1.0f - label) * logf(fmaxf(1.0f - pred, 1.0e-16f));
+    case 6: return pred > parameter ? 1.0f - label : label;
+    case 7: return fabsf((pred - label) / label);
+    case 8: { float z = (pred - label) / parameter; return parameter * parameter * (sqrtf(1.0f + z * z) - 1.0f); }
+    case 9: return lgammaf(label + 1.0f) + pred - label * logf(fmaxf(pred, 1.0e-16f));
+    case 10: { float r = label / pred; return 2.0f * (-logf(r) + r - 1.0f); }
+    case 11:
+      return -label * powf(pred, 1.0f - parameter) / (1.0f - parameter) +
+             powf(pred, 2.0f - parameter) / (2.0f - parameter);
+    case 12: return label / pred + logf(pred);
+  }
+  return 0.0f;
+}
+
+/* The threadgroup tree of kernels/boost.metal:2267-2272 / 2286-2290:
+ * v[t] += v[t + d] for d = 128 .. 1 over 256 pairs; the result is v[0]. */
+static void tree256(float* gx, float* gy) {
+  for (uint32_t d = 128; d; d >>= 1)
+    for (uint32_t t = 0; t < d; ++t) {
+      gx[t] = gx[t] + gx[t + d];
+      gy[t] = gy[t] + gy[t + d];
+    }
+}
+
+void oracle_metric_sum(const float* pred, const float* labels, const float* weights, uint32_t rows, uint32_t kind,
+                       float parameter, float out[2]) {
+  const uint32_t blocks = (uint32_t)(((uint64_t)rows + 255) / 256);
+  float* px = (float*)calloc(blocks ? blocks : 1, sizeof(float));
+  float* py = (float*)calloc(blocks ? blocks : 1, sizeof(float));
+  float vx[256], vy[256];
+  /* metric_partial (:2225-2275): one 256-row block per workgroup. */
+  for (uint32_t b = 0; b < blocks; ++b) {
+    for (uint32_t t = 0; t < 256; ++t) {
+      uint64_t i = (uint64_t)b * 256 + t;
+      vx[t] = vy[t] = 0.0f;
+      if (i < rows) {
+        float w = weights ? weights[i] : 1.0f;
+        vx[t] = w * metric_loss(kind, pred[i], labels[i], parameter);
+        vy[t] = w;
+      }
+    }
+    tree256(vx, vy);
+    px[b] = vx[0];
+    py[b] = vy[0];
+  }
+  /* metric_reduce (:2276-2295): thread t sums blocks t, t + 256, ... with
+   * compensation, then the tree. */
+  for (uint32_t t = 0; t < 256; ++t) {
+    float sx = 0.0f, sy = 0.0f, cx = 0.0f, cy = 0.0f;
+    for (uint32_t i = t; i < blocks; i += 256) {
+      float yx = px[i] - cx, yy = py[i] - cy;
+      float nx = sx + yx, ny = sy + yy;
+      cx = (nx - sx) - yx;
+      cy = (ny - sy) - yy;
+      sx = nx;
+      sy = ny;
+    }
+    vx[t] = sx;
+    vy[t] = sy;
+  }
+  tree256(vx, vy);
+  out[0] = vx[0];
+  out[1] = vy[0];
+  free(px);
+  free(py);
+}
+
+/* Descending prediction order as ascending uint32 keys; +0 and -0 tie
+ * (kernels/radix_sort.metal.h:20-23). */
+static uint32_t descending_key(float p) {
+  uint32_t b;
+  memcpy(&b, &p, 4);
+  if ((b & 0x7fffffffu) == 0) b = 0;
+  uint32_t ascending = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ~ascending;
+}
+
+typedef struct {
+  uint32_t key, row;
+} KeyRow;
+
+static int key_row_cmp(const void* a, const void* b) {
+  const KeyRow *x = (const KeyRow*)a, *y = (const KeyRow*)b;
+  if (x->key != y->key) return x->key < y->key ? -1 : 1;
+  return x->row < y->row ? -1 : (x->row > y->row);
+}
+
+/* 1 - log(1 + u) / u for 0 < u <= 1/4 by its alternating series. */
+static double one_minus_log1p_ratio(double u) {
+  double term = u, sum = 0.0;
+  for (int k = 1; k <= 40; ++k) {
+    double add = term / (double)(k + 1);
+    sum = (k & 1) ? sum + add : sum - add;
+    term *= u;
+  }
+  return sum;
+}
+
+/* kernels/radix_sort.metal.h:354-398 (auc_pr_segment_d64): precision
+ * integrated over the recall rise of one step, precision linear in (TP, FP)
+ * between the step's end points. */
+static double pr_step_area(double prev_tp, double prev_fp, double tp, double fp, double positives) {
+  if (tp == 0.0 || positives == 0.0) return 0.0;
+  double mass = tp + fp;
+  if (mass == 0.0) return 0.0;
+  double rise = tp / positives, q = tp / mass;
+  double cumulative = prev_tp + prev_fp;
+  if (cumulative == 0.0) return rise * q;
+  double r = prev_tp / cumulative, retained, added;
+  if (mass <= cumulative) {
+    double u = mass / cumulative;
+    if (u <= 0.25) {
+      added = one_minus_log1p_ratio(u);
+      retained = 1.0 - added;
+    } else {
+      retained = log1p(u) / u;
+      added = 1.0 - retained;
+    }
+  } else {
+    double v = cumulative / mass;
+    retained = v == 0.0 ? 0.0 : v * (log1p(v) - log(v));
+    added = 1.0 - retained;
+  }
+  return rise * (r * retained + q * added);
+}
+
+void oracle_metric_auc(const float* pred, const float* labels, const float* weights, uint32_t rows, int pr,
+                       double out[3]) {
+  out[0] = out[1] = out[2] = 0.0;
+  if (!rows) return;
+  KeyRow* order = (KeyRow*)malloc(sizeof(KeyRow) * rows);
+  double positives = 0.0, negatives = 0.0;
+  for (uint32_t r = 0; r < rows; ++r) {
+    order[r].key = descending_key(pred[r]);
+    order[r].row = r;
+    float w = weights ? weights[r] : 1.0f;
+    positives += (double)fabsf(labels[r] * w);
+    negatives += (double)fabsf((1.0f - labels[r]) * w);
+  }
+  qsort(order, rows, sizeof(KeyRow), key_row_cmp);
+  double tp_before = 0.0, fp_before = 0.0, area = 0.0;
+  for (uint32_t i = 0; i < rows;) {
+    double tp = 0.0, fp = 0.0;
+    uint32_t j = i;
+    for (; j < rows && order[j].key == order[i].key; ++j) {
+      uint32_t r = order[j].row;
+      float w = weights ? weights[r] : 1.0f;
+      tp += (double)fabsf(labels[r] * w);
+      fp += (double)fabsf((1.0f - labels[r]) * w);
+    }
+    /* ROC: trapezoid under the step (kernels/radix_sort.metal.h:740-744). */
+    area += pr ? pr_step_area(tp_before, fp_before, tp, fp, positives) : fp * (2.0 * tp_before + tp) * 0.5;
+    tp_before += tp;
+    fp_before += fp;
+    i = j;
+  }
+  out[0] = area;
+  out[1] = positives;
+  out[2] = negatives;
+  free(order);
+}
+
+void oracle_cv_folds(uint32_t rows, int nfold, uint32_t seed, int shuffle, int stratified, const float* labels,
+                     int32_t* fold) {
+  uint32_t* order = (uint32_t*)malloc(sizeof(uint32_t) * (rows ? rows : 1));
+  for (uint32_t r = 0; r < rows; ++r) order[r] = r;
+  if (shuffle && rows > 1) {
+    /* libc++ std::shuffle with mt19937(seed): the same draws as the feature
+     * sample's, over every position. */
+    OracleMT g;
+    oracle_mt_seed(&g, seed);
+    for (uint32_t pos = 0; pos + 1 < rows; ++pos) {
+      uint32_t range = rows - pos;
+      uint32_t width = 32u - (uint32_t)__builtin_clz(range - 1u);
+      uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
+      uint32_t u;
+      do u = oracle_mt_next(&g) & mask; while (u >= range);
+      uint32_t tmp = order[pos];
+      order[pos] = order[pos + u];
+      order[pos + u] = tmp;
+    }
+  }
+  if (stratified) {
+    /* Stable insertion sort by label (test sizes are small). */
+    for (uint32_t i = 1; i < rows; ++i) {
+      uint32_t v = order[i], j = i;
+      while (j > 0 && labels[order[j - 1]] > labels[v]) { order[j] = order[j - 1]; --j; }
+      order[j] = v;
+    }
+    for (uint32_t pos = 0; pos < rows; ++pos) fold[order[pos]] = (int32_t)(pos % (uint32_t)nfold);
+  } else {
+    uint32_t pos = 0;
+    for (int k = 0; k < nfold; ++k) {
+      uint32_t chunk = rows / (uint32_t)nfold + ((uint32_t)k < rows % (uint32_t)nfold ? 1u : 0u);
+      for (uint32_t j = 0; j < chunk; ++j) fold[order[pos++]] = k;
+    }
+  }
+  free(order);
+}

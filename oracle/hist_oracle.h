@@ -118,6 +118,21 @@ void oracle_predict_margin(const float* X, uint32_t rows, uint32_t cols, const O
                            const uint32_t* tree_sizes, uint32_t rounds, uint32_t stride, float base_margin,
                            float* out);
 
+/* Evaluation metrics (src/metrics.cpp:8-159).  kind numbers follow the
+ * reference's metric table: 0 rmse, 1 mae, 2 rmsle, 3 logloss, 6 error,
+ * 7 mape, 8 mphe, 9 poisson-nloglik, 10 gamma-deviance, 11 tweedie-nloglik,
+ * 12 gamma-nloglik.  out = (sum of weight * loss, sum of weight) in the
+ * reference's fp32 order (kernels/boost.metal:2225-2295). */
+void oracle_metric_sum(const float* pred, const float* labels, const float* weights, uint32_t rows, uint32_t kind,
+                       float parameter, float out[2]);
+/* ROC-AUC (pr = 0) or PR-AUC (pr = 1) area, positive and negative weight in
+ * binary64 (kernels/radix_sort.metal.h:427-790). */
+void oracle_metric_auc(const float* pred, const float* labels, const float* weights, uint32_t rows, int pr,
+                       double out[3]);
+/* Fold of each row for xgboost.cv (src/c_api.cpp:1018-1110). */
+void oracle_cv_folds(uint32_t rows, int nfold, uint32_t seed, int shuffle, int stratified, const float* labels,
+                     int32_t* fold);
+
 #ifdef __cplusplus
 }
 #endif

@@ -125,3 +125,30 @@ def histogram(m, dbins, rows_list, grad, hess, scales, G, unit=False, rows_per_t
     check(lib().mgb_histogram(ctypes.byref(shape), ctypes.byref(m), dbins.ptr, drows.ptr if drows else None,
                               ctypes.c_uint32(count), dgh.ptr, dsc.ptr, out.ptr, ws.ptr, ctypes.c_size_t(ws_bytes)))
     return out.read(np.int64, m.cols * (m.max_bin + 1) * 2).reshape(m.cols, m.max_bin + 1, 2)
+
+
+def metric_sum(pred, labels, kind, weights=None, parameter=0.0):
+    """mgb_metric_sum on device copies of the inputs."""
+    pred = np.ascontiguousarray(pred, np.float32)
+    dp, dl = Device.of(pred), Device.of(np.ascontiguousarray(labels, np.float32))
+    dw = None if weights is None else Device.of(np.ascontiguousarray(weights, np.float32))
+    lib().mgb_metric_workspace_bytes.restype = ctypes.c_size_t
+    nbytes = lib().mgb_metric_workspace_bytes(ctypes.c_uint32(pred.size))
+    ws = Device(nbytes)
+    out = np.zeros(2, np.float32)
+    check(lib().mgb_metric_sum(dp.ptr, dl.ptr, dw.ptr if dw else None, ctypes.c_uint32(pred.size),
+                               ctypes.c_uint32(kind), ctypes.c_float(parameter), out.ctypes.data_as(ctypes.c_void_p),
+                               ws.ptr, ctypes.c_size_t(ws.nbytes)))
+    return out
+
+
+def metric_auc(pred, labels, pr=False, weights=None):
+    pred = np.ascontiguousarray(pred, np.float32)
+    dp, dl = Device.of(pred), Device.of(np.ascontiguousarray(labels, np.float32))
+    dw = None if weights is None else Device.of(np.ascontiguousarray(weights, np.float32))
+    lib().mgb_metric_workspace_bytes.restype = ctypes.c_size_t
+    ws = Device(lib().mgb_metric_workspace_bytes(ctypes.c_uint32(pred.size)))
+    out = np.zeros(3, np.float64)
+    check(lib().mgb_metric_auc(dp.ptr, dl.ptr, dw.ptr if dw else None, ctypes.c_uint32(pred.size), ctypes.c_int(int(pr)),
+                               out.ctypes.data_as(ctypes.c_void_p), ws.ptr, ctypes.c_size_t(ws.nbytes)))
+    return out

@@ -155,3 +155,33 @@ def sample_columns(n, fraction, seed):
     f.restype = ctypes.c_uint32
     k = f(ctypes.c_uint32(n), ctypes.c_float(fraction), ctypes.c_uint32(seed), ptr(out))
     return out[:k]
+
+
+def metric_sum(pred, labels, kind, weights=None, parameter=0.0):
+    """(sum of weight * loss, sum of weight) in the reference's fp32 order."""
+    pred = np.ascontiguousarray(pred, np.float32)
+    labels = np.ascontiguousarray(labels, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    out = np.zeros(2, np.float32)
+    lib().oracle_metric_sum(ptr(pred), ptr(labels), ptr(w), ctypes.c_uint32(pred.size), ctypes.c_uint32(kind),
+                            ctypes.c_float(parameter), ptr(out))
+    return out
+
+
+def metric_auc(pred, labels, pr=False, weights=None):
+    """(area, positive weight, negative weight) in binary64."""
+    pred = np.ascontiguousarray(pred, np.float32)
+    labels = np.ascontiguousarray(labels, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    out = np.zeros(3, np.float64)
+    lib().oracle_metric_auc(ptr(pred), ptr(labels), ptr(w), ctypes.c_uint32(pred.size), ctypes.c_int(int(pr)),
+                            ptr(out))
+    return out
+
+
+def cv_folds(rows, nfold, seed, shuffle=True, stratified=False, labels=None):
+    fold = np.zeros(max(rows, 1), np.int32)
+    y = None if labels is None else np.ascontiguousarray(labels, np.float32)
+    lib().oracle_cv_folds(ctypes.c_uint32(rows), ctypes.c_int(nfold), ctypes.c_uint32(seed), ctypes.c_int(int(shuffle)),
+                          ctypes.c_int(int(stratified)), ptr(y), ptr(fold))
+    return fold[:rows]

@@ -388,6 +388,44 @@ void read_feature_map(const std::string& path, std::vector<std::string>& names) 
   }
 }
 
+// Rows `index` of `source` with their labels, weights and base margins
+// (src/data.cpp:1451); a slice of a quantile matrix keeps the source's cuts.
+std::shared_ptr<DMatrix> slice_rows(const std::shared_ptr<DMatrix>& source, const int* index, size_t len) {
+  const DMatrix& src = *source;
+  for (size_t i = 0; i < len; ++i)
+    require(index[i] >= 0 && (uint32_t)index[i] < src.rows, "Slice index out of range.");
+  std::shared_ptr<DMatrix> d;
+  if (src.sparse) {
+    d = csr_matrix(len, src.cols, NAN, [&](uint64_t i, std::vector<std::pair<uint32_t, float>>& row) {
+      const uint32_t r = (uint32_t)index[i];
+      for (uint64_t k = src.indptr[r]; k < src.indptr[r + 1]; ++k) row.emplace_back(src.indices[k], src.values[k]);
+    });
+  } else {
+    d = std::make_shared<DMatrix>();
+    d->rows = (uint32_t)len;
+    d->cols = src.cols;
+    d->data.resize(len * src.cols);
+    for (size_t i = 0; i < len; ++i)
+      std::memcpy(d->data.data() + i * src.cols, src.data.data() + (size_t)index[i] * src.cols, src.cols * 4);
+  }
+  auto pick = [&](const std::vector<float>& v, std::vector<float>& o) {
+    if (v.empty()) return;
+    o.resize(len);
+    for (size_t i = 0; i < len; ++i) o[i] = v[(size_t)index[i]];
+  };
+  pick(src.labels, d->labels);
+  pick(src.weights, d->weights);
+  pick(src.base_margin, d->base_margin);
+  d->feature_names = src.feature_names;
+  d->feature_types = src.feature_types;
+  if (src.is_quantile) {
+    d->is_quantile = true;
+    d->quantile_max_bin = src.quantile_max_bin;
+    d->cut_source = source;
+  }
+  return d;
+}
+
 std::vector<std::string> feature_names_of(const Learner& b) {
   std::vector<std::string> names = b.feature_names;
   if (names.empty())
@@ -1123,40 +1161,7 @@ int XGDMatrixSliceDMatrixEx(DMatrixHandle handle, int const* idxset, bst_ulong l
   API_BEGIN
   (void)allow_groups;  // no query groups in this engine
   require(idxset || !len, "Null slice indices.");
-  const DMatrix& src = *matrix(handle);
-  for (bst_ulong i = 0; i < len; ++i)
-    require(idxset[i] >= 0 && (uint32_t)idxset[i] < src.rows, "Slice index out of range.");
-  std::shared_ptr<DMatrix> d;
-  if (src.sparse) {
-    d = csr_matrix(len, src.cols, NAN, [&](uint64_t i, std::vector<std::pair<uint32_t, float>>& row) {
-      const uint32_t r = (uint32_t)idxset[i];
-      for (uint64_t k = src.indptr[r]; k < src.indptr[r + 1]; ++k) row.emplace_back(src.indices[k], src.values[k]);
-    });
-  } else {
-    d = std::make_shared<DMatrix>();
-    d->rows = (uint32_t)len;
-    d->cols = src.cols;
-    d->data.resize((size_t)len * src.cols);
-    for (bst_ulong i = 0; i < len; ++i)
-      std::memcpy(d->data.data() + i * src.cols, src.data.data() + (size_t)idxset[i] * src.cols, src.cols * 4);
-  }
-  auto pick = [&](const std::vector<float>& v, std::vector<float>& o) {
-    if (v.empty()) return;
-    o.resize(len);
-    for (bst_ulong i = 0; i < len; ++i) o[i] = v[(size_t)idxset[i]];
-  };
-  pick(src.labels, d->labels);
-  pick(src.weights, d->weights);
-  pick(src.base_margin, d->base_margin);
-  d->feature_names = src.feature_names;
-  d->feature_types = src.feature_types;
-  if (src.is_quantile) {
-    // A slice of a QuantileDMatrix keeps the original's cuts.
-    d->is_quantile = true;
-    d->quantile_max_bin = src.quantile_max_bin;
-    d->cut_source = matrix(handle);
-  }
-  *out = new_handle(std::move(d));
+  *out = new_handle(slice_rows(matrix(handle), idxset, len));
   API_END
 }
 
@@ -1435,8 +1440,48 @@ int XGBoosterTrainOneIterWithSplitGrad(BoosterHandle, DMatrixHandle, int, char c
                                        char const*) {
   return unsupported("Separate split and leaf gradients");
 }
-int XGDMatrixBuildCVFolds(DMatrixHandle, int, unsigned, int, int, DMatrixHandle*, DMatrixHandle*) {
-  return unsupported("Native cross-validation folds");
+// Row folds for xgboost.cv (src/c_api.cpp:1018-1110): rows shuffled by
+// libc++'s std::shuffle over mt19937(seed) when `shuffle`; plain folds take
+// consecutive chunks of that order (the first nrows % nfold folds one row
+// longer), stratified folds deal the order, stably sorted by label, round
+// robin.  Fold k tests its rows and trains on the others, both in row order.
+int XGDMatrixBuildCVFolds(DMatrixHandle handle, int nfold, unsigned seed, int shuffle, int stratified,
+                          DMatrixHandle* out_train, DMatrixHandle* out_test) {
+  API_BEGIN
+  require(out_train && out_test, "Null CV fold output arrays.");
+  require(nfold >= 2, "nfold must be at least 2.");
+  std::shared_ptr<DMatrix> m = matrix(handle);
+  const uint32_t nrows = m->rows;
+  require((uint32_t)nfold <= nrows, "Number of folds cannot exceed number of rows.");
+  std::mt19937 rng(seed);
+  std::vector<uint32_t> order(nrows);
+  for (uint32_t r = 0; r < nrows; ++r) order[r] = r;
+  if (shuffle && nrows > 1) shuffle_prefix(order, rng, nrows - 1);
+  std::vector<int> fold(nrows, 0);
+  if (stratified) {
+    const auto& y = m->labels;
+    require(y.size() == nrows, "Stratified CV requires 1D labels matching the number of rows.");
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return y[a] < y[b]; });
+    for (uint32_t pos = 0; pos < nrows; ++pos) fold[order[pos]] = (int)(pos % (uint32_t)nfold);
+  } else {
+    uint32_t pos = 0;
+    for (int k = 0; k < nfold; ++k) {
+      const uint32_t chunk = nrows / (uint32_t)nfold + ((uint32_t)k < nrows % (uint32_t)nfold ? 1u : 0u);
+      for (uint32_t j = 0; j < chunk; ++j) fold[order[pos++]] = k;
+    }
+  }
+  std::vector<std::shared_ptr<DMatrix>> train(nfold), test(nfold);
+  for (int k = 0; k < nfold; ++k) {
+    std::vector<int> train_rows, test_rows;
+    for (uint32_t r = 0; r < nrows; ++r) (fold[r] == k ? test_rows : train_rows).push_back((int)r);
+    train[k] = slice_rows(m, train_rows.data(), train_rows.size());
+    test[k] = slice_rows(m, test_rows.data(), test_rows.size());
+  }
+  for (int k = 0; k < nfold; ++k) {
+    out_train[k] = new_handle(std::move(train[k]));
+    out_test[k] = new_handle(std::move(test[k]));
+  }
+  API_END
 }
 int XGDMatrixSaveBinary(DMatrixHandle, char const*, int) { return unsupported("Saving a DMatrix"); }
 int XGDMatrixGetCategories(DMatrixHandle handle, char const*, CategoriesHandle* out) {

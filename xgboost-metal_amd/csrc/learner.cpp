@@ -4,6 +4,8 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <iomanip>
+#include <limits>
 #include <sstream>
 
 namespace mgb {
@@ -327,6 +329,10 @@ void Learner::set_param(const std::string& name, const std::string& value) {
   std::string key = name;
   auto it = aliases().find(name);
   if (it != aliases().end()) key = it->second;
+  if (key == "eval_metric") {  // a list: each value once, in order (src/learner.cpp:119-126)
+    if (std::find(metrics.begin(), metrics.end(), value) == metrics.end()) metrics.push_back(value);
+    return;
+  }
   params_[key] = value;
 }
 
@@ -538,11 +544,27 @@ void Learner::sample_rows(DMatrix& data, MgbGradParams& gp) {
   }
 }
 
-// src/tree.cpp:28-45 with libc++'s std::shuffle, the reference's model of it
-// (kernels/tree_sample_columns.metal.h): a fresh engine seeded by one draw,
-// Fisher-Yates from the front (position pos swaps with pos + u, u uniform in
-// [0, n - pos) by masking to the bit width of n - pos - 1 and rejecting),
-// then the first max(1, floor(n * fraction)) features, sorted.
+// libc++'s std::shuffle over a 32-bit engine, which the reference's builds
+// use: Fisher-Yates from the front, position pos swapping with pos + u, u
+// uniform in [0, n - pos) drawn by masking one engine output to the bit
+// width of n - pos - 1 and rejecting values >= n - pos.  Only the first
+// `positions` positions are drawn (all n - 1 for a full shuffle).
+void shuffle_prefix(std::vector<uint32_t>& order, std::mt19937& engine, size_t positions) {
+  const size_t n = order.size();
+  for (size_t pos = 0; pos < positions && pos + 1 < n; ++pos) {
+    const uint64_t range = n - pos;
+    uint32_t width = 0;
+    while (width < 32 && ((range - 1) >> width)) ++width;
+    const uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
+    uint32_t u;
+    do u = static_cast<uint32_t>(engine()) & mask; while (u >= range);
+    std::swap(order[pos], order[pos + u]);
+  }
+}
+
+// src/tree.cpp:28-45 (kernels/tree_sample_columns.metal.h): a fresh engine
+// seeded by one draw shuffles the features; the first
+// max(1, floor(n * fraction)) of them are kept.
 const uint32_t* Learner::sample_columns(uint32_t cols) {
   const float fraction = fnumber("colsample_bytree", 1.0f);
   if (!(fraction < 1.0f) || cols == 0) return nullptr;
@@ -551,15 +573,7 @@ const uint32_t* Learner::sample_columns(uint32_t cols) {
   for (uint32_t i = 0; i < cols; ++i) order[i] = i;
   const float scaled = std::floor(static_cast<float>(cols) * fraction);
   const uint32_t keep = std::min<uint32_t>(cols, scaled < 1.0f ? 1u : static_cast<uint32_t>(scaled));
-  for (uint32_t pos = 0; pos < keep && pos + 1 < cols; ++pos) {
-    const uint32_t range = cols - pos;
-    uint32_t width = 0;
-    while (width < 32 && ((range - 1) >> width)) ++width;
-    const uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
-    uint32_t u;
-    do u = static_cast<uint32_t>(engine()) & mask; while (u >= range);
-    std::swap(order[pos], order[pos + u]);
-  }
+  shuffle_prefix(order, engine, keep);
   feature_flags_.assign(cols, 0u);
   for (uint32_t i = 0; i < keep; ++i) feature_flags_[order[i]] = 1u;
   d_features_.ensure((size_t)cols * sizeof(uint32_t));
@@ -728,34 +742,28 @@ void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t 
   grow(data, false);
 }
 
-std::vector<float> Learner::predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end) {
+const float* Learner::predict_device(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end,
+                                    DeviceBuffer& scratch) {
+  scratch.ensure((size_t)std::max<uint32_t>(data.rows, 1) * sizeof(float));
+  float* d_out = scratch.as<float>();
   if (!initialized) {
     // An untrained model predicts its base score.
-    std::vector<float> out(data.rows, output_margin ? base_margin_value() : base_score);
-    return out;
+    kcheck(mgb_fill_f32(d_out, data.rows, output_margin ? base_margin_value() : base_score), "fill");
+    return d_out;
   }
   require(data.cols == num_feature, "Feature shape mismatch: expected " + std::to_string(num_feature) + ", got " +
                                         std::to_string(data.cols));
   if (end == 0 || end > trees.size()) end = (uint32_t)trees.size();
   require(begin <= end, "Invalid iteration range.");
-  std::vector<float> out(data.rows);
-  DeviceBuffer tmp;
-  float* d_out;
-  if (begin == 0 && end == trees.size() && data.base_margin.empty() == true && cache_id_ == data.id &&
+  if (begin == 0 && end == trees.size() && data.base_margin.empty() && cache_id_ == data.id &&
       cache_trees_ == trees.size()) {
-    d_out = d_margin_.as<float>();
-    if (!output_margin && objective() == 1) {
-      tmp.ensure((size_t)data.rows * sizeof(float));
-      kcheck(mgb_memcpy_d2d(tmp.get(), d_out, data.rows * sizeof(float)), "copy");
-      d_out = tmp.as<float>();
-    }
+    if (output_margin || objective() != 1) return d_margin_.as<float>();
+    kcheck(mgb_memcpy_d2d(d_out, d_margin_.get(), data.rows * sizeof(float)), "copy");
   } else {
     data.upload();
-    tmp.ensure((size_t)data.rows * sizeof(float));
-    d_out = tmp.as<float>();
     if (!data.base_margin.empty()) {
       require(data.base_margin.size() == data.rows, "base_margin must have one value per row.");
-      tmp.upload(data.base_margin.data(), data.rows * sizeof(float));
+      scratch.upload(data.base_margin.data(), data.rows * sizeof(float));
     } else {
       kcheck(mgb_fill_f32(d_out, data.rows, base_margin_value()), "margin fill");
     }
@@ -765,39 +773,78 @@ std::vector<float> Learner::predict(DMatrix& data, bool output_margin, uint32_t 
     }
   }
   if (!output_margin) kcheck(mgb_transform(d_out, data.rows, (uint32_t)objective()), "transform");
+  return d_out;
+}
+
+std::vector<float> Learner::predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end) {
+  std::vector<float> out(data.rows);
+  if (!data.rows) return out;
+  DeviceBuffer scratch;
+  const float* d_out = predict_device(data, output_margin, begin, end, scratch);
   kcheck(mgb_memcpy_d2h(out.data(), d_out, out.size() * sizeof(float)), "device-to-host copy");
   return out;
 }
 
+// Default metric of the objective (src/learner.cpp:1012-1023).
+std::string Learner::default_metric() const {
+  const int obj = objective();
+  return (obj == 1 && objective_name() != "reg:logistic") || obj == 2 ? "logloss" : "rmse";
+}
+
+double Learner::metric(DMatrix& d, const float* pred, const std::string& name) {
+  static const std::map<std::string, uint32_t> kinds{
+      {"rmse", MGB_METRIC_RMSE}, {"mae", MGB_METRIC_MAE}, {"rmsle", MGB_METRIC_RMSLE},
+      {"logloss", MGB_METRIC_LOGLOSS}, {"error", MGB_METRIC_ERROR}, {"mape", MGB_METRIC_MAPE},
+      {"mphe", MGB_METRIC_MPHE}, {"poisson-nloglik", MGB_METRIC_POISSON},
+      {"gamma-deviance", MGB_METRIC_GAMMA_DEVIANCE}, {"tweedie-nloglik", MGB_METRIC_TWEEDIE},
+      {"gamma-nloglik", MGB_METRIC_GAMMA_NLOGLIK}, {"auc", 13}, {"aucpr", 14}};
+  const size_t sep = name.find('@');
+  const std::string base = name.substr(0, sep);
+  auto it = kinds.find(base);
+  require(base != "merror" && base != "mlogloss", "Multiclass metrics need a multiclass objective: " + name);
+  require(it != kinds.end(), "Metric has not been implemented yet: " + name);
+  require(d.weights.empty() || d.weights.size() == d.rows, "Evaluation weights must have one entry per row.");
+  d.upload_info();
+  const float* w = d.weights.empty() ? nullptr : d.d_weights.as<float>();
+  d_metric_ws_.ensure(std::max<size_t>(mgb_metric_workspace_bytes(d.rows), 256));
+  if (it->second >= 13) {
+    for (float y : d.labels) require(y >= 0 && y <= 1, "AUC labels must be in [0,1].");
+    if (!d.rows) return std::numeric_limits<double>::quiet_NaN();
+    double out[3];
+    kcheck(mgb_metric_auc(pred, d.d_labels.as<float>(), w, d.rows, it->second == 14, out, d_metric_ws_.get(),
+                          d_metric_ws_.bytes()),
+           "auc");
+    if (!(out[1] > 0 && out[2] > 0)) return std::numeric_limits<double>::quiet_NaN();
+    return it->second == 13 ? out[0] / (out[1] * out[2]) : out[0];
+  }
+  float parameter = 0;
+  if (base == "error") parameter = sep == std::string::npos ? 0.5f : std::stof(name.substr(sep + 1));
+  if (base == "mphe") parameter = (float)number("huber_slope", 1);
+  if (base == "tweedie-nloglik") {
+    require(sep != std::string::npos, "tweedie-nloglik requires a variance power after @.");
+    parameter = std::stof(name.substr(sep + 1));
+    require(parameter >= 1 && parameter < 2, "Tweedie variance power must be in [1, 2).");
+  }
+  float out[2];
+  kcheck(mgb_metric_sum(pred, d.d_labels.as<float>(), w, d.rows, it->second, parameter, out, d_metric_ws_.get(),
+                        d_metric_ws_.bytes()),
+         "metric");
+  const double mean = out[1] > 0 ? (double)out[0] / (double)out[1] : std::numeric_limits<double>::quiet_NaN();
+  return base == "rmse" || base == "rmsle" ? std::sqrt(mean) : mean;
+}
+
 std::string Learner::evaluate(int iteration, const std::vector<DMatrix*>& data, const std::vector<std::string>& names) {
+  require(initialized, "Model is not yet initialized (not fitted).");
+  if (metrics.empty() && integer("disable_default_eval_metric", 0) == 0) metrics.push_back(default_metric());
   std::ostringstream os;
-  os << "[" << iteration << "]";
-  int obj = objective();
-  std::string metric = param("eval_metric", obj == 0 ? "rmse" : "logloss");
+  os << '[' << iteration << ']' << std::setprecision(10);
   for (size_t k = 0; k < data.size(); ++k) {
     DMatrix& d = *data[k];
-    auto pred = predict(d, false, 0, 0);
-    const auto& y = d.labels;
-    require(y.size() == d.rows, "Evaluation data must have labels.");
-    double num = 0, den = 0;
-    for (uint32_t r = 0; r < d.rows; ++r) {
-      double w = d.weights.empty() ? 1.0 : d.weights[r];
-      double p = pred[r], t = y[r];
-      if (metric == "rmse" || metric == "mse") num += w * (p - t) * (p - t);
-      else if (metric == "mae") num += w * std::fabs(p - t);
-      else if (metric == "logloss") {
-        double e = 1e-16;
-        double q = std::min(std::max(p, e), 1 - e);
-        num += -w * (t * std::log(q) + (1 - t) * std::log(1 - q));
-      } else if (metric == "error") num += w * ((p > 0.5 ? 1.0 : 0.0) != t);
-      else throw Error("eval_metric is not supported: " + metric);
-      den += w;
+    const float* pred = predict_device(d, false, 0, 0, d_eval_pred_);
+    for (auto const& name : metrics) {
+      require(d.labels.size() == d.rows, "Evaluation data requires labels.");
+      os << '\t' << names[k] << '-' << name << ':' << metric(d, pred, name);
     }
-    double value = den > 0 ? num / den : 0;
-    if (metric == "rmse") value = std::sqrt(value);
-    char buf[64];
-    std::snprintf(buf, sizeof(buf), "%.5f", value);
-    os << "\t" << names[k] << "-" << metric << ":" << buf;
   }
   return os.str();
 }
@@ -965,6 +1012,7 @@ void Learner::load_model(const Json& input) {
   cache_id_ = 0;
   cache_trees_ = 0;
   model_version_ = SIZE_MAX;
+  metrics.clear();  // src/model.cpp:224
   // A loaded model restarts the engine from seed 0 (src/model.cpp:225).
   rng_.seed(0);
   rng_seed_ = "0";
@@ -975,6 +1023,13 @@ Json Learner::config() const {
   for (auto const& kv : params_) p[kv.first] = kv.second;
   Json learner = Json::object();
   learner["params"] = p;
+  Json metric_list = Json::array();
+  for (auto const& m : metrics) {
+    Json entry = Json::object();
+    entry["name"] = m;
+    metric_list.push_back(entry);
+  }
+  learner["metrics"] = metric_list;
   Json ltp = Json::object();
   ltp["objective"] = objective_name();
   ltp["booster"] = "gbtree";
@@ -999,6 +1054,10 @@ void Learner::load_config(const Json& cfg) {
   if (learner.contains("params"))
     for (auto const& kv : learner.at("params").members())
       params_[kv.first] = kv.second.is_string() ? kv.second.string() : kv.second.dump();
+  if (learner.contains("metrics")) {
+    metrics.clear();
+    for (auto const& m : learner.at("metrics").items()) metrics.push_back(m.at("name").string());
+  }
   if (learner.contains("generic_param")) {
     const Json& generic = learner.at("generic_param");
     if (generic.contains("rng_state") && generic.contains("seed")) {

@@ -99,6 +99,10 @@ struct DMatrix {
   const std::vector<float>& get_info(const std::string& field) const;
 };
 
+// libc++'s std::shuffle of `order` with a 32-bit engine, stopped after the
+// first `positions` positions (order.size() - 1 for a full shuffle).
+void shuffle_prefix(std::vector<uint32_t>& order, std::mt19937& engine, size_t positions);
+
 struct Tree {
   std::vector<MgbTreeNode> nodes;
   uint32_t group = 0;
@@ -122,7 +126,18 @@ class Learner {
   void boost(DMatrix& data, const float* grad, const float* hess, size_t count);
   // Predictions (margin when output_margin) for rounds [begin, end); end 0 = all.
   std::vector<float> predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end);
+  // The same predictions left on the device: in `scratch`, or in the
+  // training-matrix cache when that holds them already.
+  const float* predict_device(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end, DeviceBuffer& scratch);
+  // "[iteration]\t<name>-<metric>:<value>..." over every metric and matrix
+  // (src/learner.cpp:1025-1048).
   std::string evaluate(int iteration, const std::vector<DMatrix*>& data, const std::vector<std::string>& names);
+  // One metric of predictions `pred` (device) against data's labels
+  // (src/metrics.cpp:8-159).
+  double metric(DMatrix& data, const float* pred, const std::string& name);
+  std::string default_metric() const;
+  // eval_metric values in the order first set, each once.
+  std::vector<std::string> metrics;
 
   Json model() const;
   void load_model(const Json& model);
@@ -176,6 +191,7 @@ class Learner {
   std::string rng_seed_ = "0";
   DeviceBuffer d_features_;
   std::vector<uint32_t> feature_flags_;
+  DeviceBuffer d_eval_pred_, d_metric_ws_;
 };
 
 }  // namespace mgb

@@ -4,11 +4,12 @@ Mirrors the reference's python-package/xgboost surface for tree_method='hist'
 with depthwise growth: DMatrix, QuantileDMatrix, Booster, train and the
 XGBRegressor/XGBClassifier estimators.
 """
+from . import callback
 from .core import Booster, DataIter, DMatrix, QuantileDMatrix, XGBoostError, build_info
 from .sklearn import XGBClassifier, XGBModel, XGBRegressor
 from .training import cv, train
 
 __version__ = "3.5.0-dev"
 
-__all__ = ["Booster", "DataIter", "DMatrix", "QuantileDMatrix", "XGBoostError", "XGBClassifier", "XGBModel", "XGBRegressor",
+__all__ = ["Booster", "callback", "DataIter", "DMatrix", "QuantileDMatrix", "XGBoostError", "XGBClassifier", "XGBModel", "XGBRegressor",
            "build_info", "cv", "train", "__version__"]

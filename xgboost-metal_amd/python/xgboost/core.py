@@ -550,7 +550,10 @@ class Booster:
             if val is None:
                 continue
             if key == "eval_metric" and isinstance(val, (list, tuple)):
-                val = val[-1] if val else "rmse"
+                # Each listed metric is one eval_metric setting, in order.
+                for metric in val:
+                    _check_call(_LIB.XGBoosterSetParam(self.handle, c_str("eval_metric"), c_str(str(metric))))
+                continue
             _check_call(_LIB.XGBoosterSetParam(self.handle, c_str(str(key)), c_str(_param_value(val))))
 
     def attr(self, key: str) -> Optional[str]:
@@ -772,6 +775,29 @@ class Booster:
 
     def load_config(self, config: str) -> None:
         _check_call(_LIB.XGBoosterLoadJsonConfig(self.handle, config.encode()))
+
+    @property
+    def best_iteration(self) -> int:
+        """Best round of early stopping, kept as the ``best_iteration`` attribute (reference core.py:3107)."""
+        best = self.attr("best_iteration")
+        if best is not None:
+            return int(best)
+        raise AttributeError("`best_iteration` is only defined when early stopping is used.")
+
+    @best_iteration.setter
+    def best_iteration(self, iteration: int) -> None:
+        self.set_attr(best_iteration=iteration)
+
+    @property
+    def best_score(self) -> float:
+        best = self.attr("best_score")
+        if best is not None:
+            return float(best)
+        raise AttributeError("`best_score` is only defined when early stopping is used.")
+
+    @best_score.setter
+    def best_score(self, score: float) -> None:
+        self.set_attr(best_score=score)
 
     def num_boosted_rounds(self) -> int:
         out = ctypes.c_int()

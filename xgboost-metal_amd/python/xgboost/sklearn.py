@@ -1,7 +1,7 @@
 """scikit-learn estimators (reference python-package/xgboost/sklearn.py:867, 1309-1410, 1728-1840)."""
 from __future__ import annotations
 
-from typing import Any, Dict, Optional
+from typing import Any, Dict, Optional, Tuple
 
 import numpy as np
 
@@ -91,9 +91,26 @@ class XGBModel:
             xgb_model = xgb_model.get_booster()
         self._Booster = train(params, dtrain, self._n_estimators(), evals=evals, obj=obj,
                               early_stopping_rounds=self.early_stopping_rounds, evals_result=self.evals_result_,
-                              verbose_eval=verbose, xgb_model=xgb_model)
+                              verbose_eval=verbose, xgb_model=xgb_model, callbacks=self.callbacks)
         self.n_features_in_ = dtrain.num_col()
         return self
+
+    def _iteration_range(self, iteration_range: Any) -> Tuple[int, int]:
+        """The caller's range, else the rounds up to the early-stopping best (reference sklearn.py:1178)."""
+        if iteration_range is not None:
+            return tuple(iteration_range)
+        try:
+            return (0, self.get_booster().best_iteration + 1)
+        except AttributeError:
+            return (0, 0)
+
+    @property
+    def best_iteration(self) -> int:
+        return self.get_booster().best_iteration
+
+    @property
+    def best_score(self) -> float:
+        return self.get_booster().best_score
 
     def evals_result(self) -> Dict[str, Dict[str, list]]:
         return self.evals_result_
@@ -132,7 +149,7 @@ class XGBRegressor(XGBModel):
     def predict(self, X: Any, output_margin: bool = False, validate_features: bool = True, base_margin: Any = None,
                 iteration_range: Any = None) -> np.ndarray:
         d = self._dmatrix(X, base_margin=base_margin)
-        return self.get_booster().predict(d, output_margin=output_margin, iteration_range=iteration_range or (0, 0))
+        return self.get_booster().predict(d, output_margin=output_margin, iteration_range=self._iteration_range(iteration_range))
 
     def score(self, X: Any, y: Any, sample_weight: Any = None) -> float:
         pred = self.predict(X)
@@ -166,13 +183,13 @@ class XGBClassifier(XGBModel):
     def predict_proba(self, X: Any, validate_features: bool = True, base_margin: Any = None,
                       iteration_range: Any = None) -> np.ndarray:
         d = self._dmatrix(X, base_margin=base_margin)
-        p = self.get_booster().predict(d, iteration_range=iteration_range or (0, 0))
+        p = self.get_booster().predict(d, iteration_range=self._iteration_range(iteration_range))
         return np.column_stack([1 - p, p])
 
     def predict(self, X: Any, output_margin: bool = False, validate_features: bool = True, base_margin: Any = None,
                 iteration_range: Any = None) -> np.ndarray:
         d = self._dmatrix(X, base_margin=base_margin)
-        p = self.get_booster().predict(d, output_margin=output_margin, iteration_range=iteration_range or (0, 0))
+        p = self.get_booster().predict(d, output_margin=output_margin, iteration_range=self._iteration_range(iteration_range))
         if output_margin:
             return p
         return self.classes_[(p > 0.5).astype(int)]
