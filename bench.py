@@ -128,7 +128,18 @@ def main():
     ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
                     help="c2 (default): the headline metric; c3: 1M x 2000 CSR, 20 nonzeros a row; "
                          "c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
+    ap.add_argument("--param", action="append", default=[], metavar="KEY=VALUE",
+                    help="extra booster parameter for the timed rounds (repeatable), e.g. hip_histogram_rows=2048")
     args = ap.parse_args()
+    extra = {}
+    for item in args.param:
+        key, sep, value = item.partition("=")
+        if not sep:
+            ap.error(f"--param expects KEY=VALUE, got {item!r}")
+        extra[key] = value
+    PARAMS.update(extra)
+    for spec in LARGE.values():
+        spec["params"].update(extra)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(row-sharded multi-GPU training is a design note, not implemented).", file=sys.stderr)

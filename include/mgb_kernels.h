@@ -110,7 +110,11 @@ typedef struct {
   uint32_t rows_per_tile, features_per_group, unit_hessian, dense;
   uint32_t column_levels;
   uint32_t sparse;  /* 1: the workspace is for mgb_grow_tree_csr (no per-tile partial histograms) */
-  uint32_t padding[2];
+  /* Rows per histogram tile at the root (0: rows_per_tile).  The root reads
+   * every row in order, so longer tiles cost no locality and leave fewer
+   * per-tile partial histograms for the split kernel to sum. */
+  uint32_t root_rows_per_tile;
+  uint32_t padding;
 } MgbTreeShape;
 
 /* ---- data: quantile cuts and bin matrix ------------------------------- */

@@ -20,7 +20,8 @@ class MgbTreeShape(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("cols", ctypes.c_uint32), ("max_bin", ctypes.c_uint32),
                 ("max_depth", ctypes.c_uint32), ("rows_per_tile", ctypes.c_uint32),
                 ("features_per_group", ctypes.c_uint32), ("unit_hessian", ctypes.c_uint32), ("dense", ctypes.c_uint32),
-                ("column_levels", ctypes.c_uint32), ("sparse", ctypes.c_uint32), ("padding", ctypes.c_uint32 * 2)]
+                ("column_levels", ctypes.c_uint32), ("sparse", ctypes.c_uint32), ("root_rows_per_tile", ctypes.c_uint32),
+                ("padding", ctypes.c_uint32)]
 
 
 _lib = None

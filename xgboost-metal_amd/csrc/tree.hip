@@ -125,6 +125,7 @@ struct Tree {
   uint32_t rows_n, cols, max_bin, bins1;     // bins1 = max_bin + 1
   uint32_t row_stride, bin_bytes, missing_code, cut_stride;
   uint32_t max_depth, slots, rows_per_tile, groups;
+  uint32_t root_tile;                        // rows per histogram tile at the root
   uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
   uint32_t column_levels;                    // histogram levels that read `columns`
   uint32_t sparse;                           // CSR: missing slots from node totals, no partials
@@ -199,12 +200,12 @@ __device__ __forceinline__ float calc_gain(double G, double H, float w, const Mg
 // ---------------------------------------------------------------------------
 __global__ void k_level0(Tree t) {
   LevelState* st = t.state;
-  uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.rows_per_tile) : 0;
+  uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.root_tile) : 0;
   if (t.best)
     for (uint32_t i = threadIdx.x; i < 2 * t.slots; i += blockDim.x) t.best[i] = 0;
   for (uint32_t i = threadIdx.x; i < tiles; i += blockDim.x) {
-    uint32_t begin = i * t.rows_per_tile;
-    uint32_t end = begin + t.rows_per_tile < t.rows_n ? begin + t.rows_per_tile : t.rows_n;
+    uint32_t begin = i * t.root_tile;
+    uint32_t end = begin + t.root_tile < t.rows_n ? begin + t.root_tile : t.rows_n;
     t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
   }
   if (threadIdx.x == 0) {
@@ -1651,6 +1652,10 @@ int validate(const MgbTreeShape* s, const MgbMatrix* m) {
   const bool group_major = m->row_stride == gbytes && m->group_stride == (uint64_t)m->rows * gbytes;
   if (!row_major && !group_major) { set_error("bin matrix strides describe neither layout"); return -1; }
   if (s->rows_per_tile < 64) { set_error("rows_per_tile must be >= 64"); return -1; }
+  if (s->root_rows_per_tile && s->root_rows_per_tile < s->rows_per_tile) {
+    set_error("root_rows_per_tile must be 0 or >= rows_per_tile");
+    return -1;
+  }
   if (m->max_bin < 1 || m->max_bin > 1086) { set_error("max_bin must be in [1, 1086]"); return -1; }
   if ((size_t)G * (m->max_bin + 1) * 16 > 160 * 1024) { set_error("feature group does not fit in LDS"); return -1; }
   return 0;
@@ -1682,6 +1687,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.group_stride = m->group_stride;
   t.cut_stride = m->cut_stride;
   t.max_depth = s->max_depth; t.slots = L.slots; t.rows_per_tile = s->rows_per_tile;
+  t.root_tile = s->root_rows_per_tile ? s->root_rows_per_tile : s->rows_per_tile;
   t.features_per_group = s->features_per_group;
   t.groups = div_up(s->cols, s->features_per_group);
   t.unit_hessian = s->unit_hessian; t.dense = s->dense; t.max_hist_tasks = L.max_hist_tasks;
@@ -1699,11 +1705,41 @@ uint32_t reduce_grid(const Tree& t) {
   return (uint32_t)(g ? g : 1);
 }
 
-uint32_t hist_grid(const Tree& t) {
-  uint64_t items = (uint64_t)t.max_hist_tasks * t.groups;
+// Workgroups for `tasks` histogram tasks: one per (task, feature group), at
+// most 2048 (the kernel loops), a multiple of 8 for the XCD-aware schedule.
+uint32_t hist_grid_for(const Tree& t, uint64_t tasks) {
+  uint64_t items = tasks * t.groups;
   uint64_t g = items < 2048 ? items : 2048;
   g = (g + 7) / 8 * 8;
   return (uint32_t)(g ? g : 8);
+}
+
+uint32_t hist_grid(const Tree& t) { return hist_grid_for(t, t.max_hist_tasks); }
+
+// A level's histogram tasks are bounded on the host without reading the
+// device: the root has ceil(N / tile) row tiles; below it the built (smaller)
+// children of at most 2^(depth-1) sibling pairs hold at most N/2 rows, so
+// their tiles number at most floor(N/2 / tile) + 2^(depth-1) (each node adds
+// at most one partial tile).  Idle 1024-thread workgroups are not free: each
+// costs a dispatch, so the grid follows the level's bound.
+uint64_t level_hist_tasks(const Tree& t, uint32_t depth) {
+  uint64_t tasks;
+  if (depth == 0) {
+    tasks = t.rows_n ? div_up(t.rows_n, t.root_tile) : 0;
+  } else {
+    const uint64_t nodes = depth - 1 < 32 ? (1ull << (depth - 1)) : ~0ull >> 1;
+    tasks = (uint64_t)(t.rows_n / 2) / t.rows_per_tile + nodes;
+  }
+  return tasks < t.max_hist_tasks ? tasks : t.max_hist_tasks;
+}
+
+// Partition workgroups at a level: nodes at depth d (at most 2^d) hold at
+// most N rows, in at most floor(N / tile) + 2^d tiles; the kernel loops over
+// tasks, so 1024 workgroups cover any level.
+uint32_t level_part_grid(const Tree& t, uint32_t depth) {
+  const uint64_t nodes = depth < 32 ? (1ull << depth) : ~0ull >> 1;
+  const uint64_t tasks = (uint64_t)t.rows_n / kPartTile + nodes;
+  return (uint32_t)(tasks < 1024 ? tasks : 1024);
 }
 
 }  // namespace
@@ -1728,13 +1764,13 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   t.allowed = features;
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
-  const uint32_t hgrid = hist_grid(t);
-  const uint32_t pgrid = 1024;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
     if (depth > 0) {
       launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
+    const uint32_t hgrid = hist_grid_for(t, level_hist_tasks(t, depth));
+    const uint32_t pgrid = level_part_grid(t, depth);
     if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, hgrid) : dispatch_hist<uint16_t>(t, depth, hgrid)))
       return -1;
     uint32_t max_nodes = 1u << depth;
@@ -1819,7 +1855,6 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
   launch(MGB_PROF_HISTOGRAM, k_root_totals, dim3(m->rows ? div_up(m->rows, kCsrThreads * 8) : 1),
          dim3(kCsrThreads), 0, t);
   MGB_LAUNCH_CHECK("k_root_totals");
-  const uint32_t hgrid = t.max_hist_tasks < 4096 ? (t.max_hist_tasks ? t.max_hist_tasks : 1) : 4096;
   const uint64_t row_int4 = (uint64_t)t.cols * t.bins1;
   const uint32_t zx = (uint32_t)(row_int4 / (256 * 8) + 1 < 64 ? row_int4 / (256 * 8) + 1 : 64);
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
@@ -1827,13 +1862,16 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
       launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
+    const uint64_t tasks = level_hist_tasks(t, depth);
+    const uint32_t hgrid = (uint32_t)(tasks < 4096 ? (tasks ? tasks : 1) : 4096);
     if (csr_histogram(t, m->bin_bytes, depth, root_columns, hgrid, zx)) return -1;
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
     if (launch_split(t, depth, items)) return -1;
     launch(MGB_PROF_CONTROL, k_select, dim3(1), dim3(kSelectThreads), 0, t, depth);
     MGB_LAUNCH_CHECK("k_select");
-    if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, 1024) : launch_partition<uint16_t>(t, depth, 1024)))
+    const uint32_t pgrid = level_part_grid(t, depth);
+    if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
       return -1;
   }
   return 0;
