@@ -128,6 +128,7 @@ struct Tree {
   uint32_t root_tile;                        // rows per histogram tile at the root
   uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
   uint32_t column_levels;                    // histogram levels that read `columns`
+  uint32_t select_plans;                     // unit Hessians, dense: k_select plans the next level
   uint32_t sparse;                           // CSR: missing slots from node totals, no partials
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
@@ -1207,12 +1208,19 @@ __device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh,
 __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t depth) {
   __shared__ uint32_t scan[kSelectThreads / kWave + 1];
   __shared__ uint32_t s_off[kSelectThreads], s_begin[kSelectThreads], s_end[kSelectThreads];
+  __shared__ uint32_t scan_slot[kSelectThreads];
   LevelState* st = t.state;
   const uint32_t n = st->n_nodes;
   const uint32_t F = t.cols;
   const Frontier* fr = t.frontier[depth & 1];
   Frontier* next = t.frontier[(depth + 1) & 1];
   const bool final_level = depth + 1 >= t.max_depth;
+  // With unit Hessians every row's quantized h is unit_q, so a child's row
+  // count is its Hessian sum / unit_q -- exactly the rows the partition will
+  // send it -- and the next level can be planned here (k_plan's work) instead
+  // of after the partition.
+  const bool plan_next = t.select_plans && !final_level;
+  const uint64_t unit_q = plan_next ? (uint64_t)(int64_t)rintf(1.0f * t.scales[1]) : 1;
   const uint32_t node_base = st->node_count;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const MgbSplitParams& p = t.sp;
@@ -1232,7 +1240,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
     for (uint32_t b = threadIdx.x; b < cf; b += blockDim.x) rootcut[b] = t.cuts[(uint64_t)f * t.cut_stride + b];
     __syncthreads();
   }
-  uint32_t carry_expanded = 0, carry_tasks = 0;
+  uint32_t carry_expanded = 0, carry_tasks = 0, carry_htasks = 0, carry_zero = 0, carry_rows = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
     const uint32_t i = base + threadIdx.x;
     const bool valid = i < n;
@@ -1299,6 +1307,23 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
     if (valid) tiles = div_up(node.count, kPartTile);
     uint32_t total_tasks;
     const uint32_t toff = block_exclusive_u32(tiles, scan, &total_tasks) + carry_tasks;
+    // Next level's plan (plan_next): the smaller child is built (ties left,
+    // kernels/boost.metal:661-698) in row tiles, the other subtracted.
+    uint32_t lcount = 0, htiles = 0, hzero = 0, hrows = 0;
+    if (plan_next && valid && expand) {
+      lcount = (uint32_t)((uint64_t)best.lh / unit_q);
+      const uint32_t rcount = node.count - lcount;
+      hrows = lcount <= rcount ? lcount : rcount;
+      htiles = div_up(hrows, t.rows_per_tile);
+      hzero = htiles != 1;
+    }
+    uint32_t total_htasks = 0, total_zero = 0, total_rows = 0;
+    uint32_t hoff = 0, zoff = 0;
+    if (plan_next) {
+      hoff = block_exclusive_u32(htiles, scan, &total_htasks) + carry_htasks;
+      zoff = block_exclusive_u32(hzero, scan, &total_zero) + carry_zero;
+      block_exclusive_u32(hrows, scan, &total_rows);
+    }
     if (valid) {
       MgbTreeNode* rec = t.nodes + node.id;
       rec->cover = total_h;
@@ -1344,6 +1369,16 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
           lf.sum_h = best.lh; lf.built = 0; lf.first_task = 0; lf.ntiles = 0; lf.padding = 0;
           rf = lf;
           rf.id = right; rf.sum_g = best.rg; rf.sum_h = best.rh;
+          if (plan_next) {
+            lf.count = lcount;
+            rf.begin = node.begin + lcount;
+            rf.count = node.count - lcount;
+            Frontier& b = lcount <= rf.count ? lf : rf;
+            b.built = 1;
+            b.first_task = hoff;
+            b.ntiles = htiles;
+            if (hzero) t.zero_list[zoff] = lcount <= rf.count ? 2 * rank : 2 * rank + 1;
+          }
           next[2 * rank] = lf;
           next[2 * rank + 1] = rf;
         }
@@ -1368,11 +1403,39 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
       task.padding[0] = task.padding[1] = task.padding[2] = 0;
       t.part_tasks[carry_tasks + j] = task;
     }
+    if (plan_next) {
+      // Row tiles of the next level's built children, in pair order.
+      __syncthreads();
+      const bool built_left = plan_next && valid && expand && lcount <= node.count - lcount;
+      s_off[threadIdx.x] = hoff - carry_htasks;
+      s_begin[threadIdx.x] = valid && expand ? (built_left ? node.begin : node.begin + lcount) : 0;
+      s_end[threadIdx.x] = s_begin[threadIdx.x] + hrows;
+      scan_slot[threadIdx.x] = expand ? 2 * rank + (built_left ? 0u : 1u) : 0u;
+      __syncthreads();
+      for (uint32_t j = threadIdx.x; j < total_htasks; j += blockDim.x) {
+        const uint32_t k = owner_of(s_off, nitems, j);
+        const uint32_t b = s_begin[k] + (j - s_off[k]) * t.rows_per_tile;
+        const uint32_t e = b + t.rows_per_tile < s_end[k] ? b + t.rows_per_tile : s_end[k];
+        const uint32_t ntiles = (k + 1 < nitems ? s_off[k + 1] : total_htasks) - s_off[k];
+        t.hist_tasks[carry_htasks + j] = HistTask{scan_slot[k], b, e, ntiles == 1 ? 1u : 0u};
+      }
+      carry_htasks += total_htasks;
+      carry_zero += total_zero;
+      carry_rows += total_rows;
+    }
     carry_expanded += total_expanded;
     carry_tasks += total_tasks;
     __syncthreads();
   }
   if (threadIdx.x == 0) {
+    if (plan_next) {
+      st->n_hist_tasks = carry_htasks;
+      st->n_zero = carry_zero;
+      if (depth + 1 < kMaxLevels) {
+        st->rows_built[depth + 1] = carry_rows;
+        st->nodes_built[depth + 1] = carry_expanded;
+      }
+    }
     st->node_count = node_base + 2 * carry_expanded;
     st->n_part_tasks = carry_tasks;
     st->n_nodes = final_level ? 0 : 2 * carry_expanded;  // becomes the next level's frontier size
@@ -1764,8 +1827,11 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   t.allowed = features;
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
+  // Unit Hessians: k_select plans each next level (child counts are known
+  // from the count histograms), so k_plan is not launched.
+  t.select_plans = t.unit_hessian ? 1u : 0u;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
-    if (depth > 0) {
+    if (depth > 0 && !t.select_plans) {
       launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
