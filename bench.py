@@ -73,9 +73,14 @@ def time_rounds(xgb, dtrain, rounds, profile, base=PARAMS):
     params = dict(base, hip_profile=1 if profile else 0)
     bst = xgb.Booster(params, [dtrain])
     bst.update(dtrain, 0)  # initialise (base score, buffers); not timed
+    bst.num_boosted_rounds()  # the library queues rounds: wait for the untimed one
     start = time.perf_counter()
     for i in range(rounds):
         bst.update(dtrain, i + 1)
+    # Rounds are queued on the device without host synchronisation; the round
+    # count waits for all of them and copies their trees to the host, so the
+    # timed region covers every round's kernels and its model transfer.
+    bst.num_boosted_rounds()
     elapsed = time.perf_counter() - start
     return bst, elapsed
 

@@ -121,3 +121,30 @@ def test_predict_to_buffer(xgb):
                                         ctypes.c_uint64(10), ctypes.byref(shape), ctypes.byref(dims)) == -1
     assert b"capacity" in lib.XGBGetLastError()
     assert not small.any()
+
+
+def test_queued_rounds_equal_drained_rounds(xgb):
+    """Rounds queued without host synchronisation (trees copied back only when
+    the model is read, or when 64 are pending) give the same model as rounds
+    read back one at a time, with parameter and attribute calls in between."""
+    X, y = W.config1(rows=4000, cols=10)
+    d = xgb.DMatrix(X, label=y)
+    params = {"max_depth": 5, "max_bin": 64, "subsample": 0.8, "colsample_bytree": 0.7, "seed": 3}
+    queued = xgb.Booster(params, [d])
+    stepwise = xgb.Booster(params, [d])
+    for i in range(70):  # more than one queue's worth
+        queued.update(d, i)
+        queued.set_attr(note=str(i))
+        if i == 30:
+            queued.set_param("learning_rate", 0.1)
+        stepwise.update(d, i)
+        assert stepwise.num_boosted_rounds() == i + 1
+        if i == 30:
+            stepwise.set_param("learning_rate", 0.1)
+    assert queued.num_boosted_rounds() == 70
+    assert _trees(queued) == _trees(stepwise)
+    np.testing.assert_array_equal(queued.predict(d), stepwise.predict(d))
+    profiled = xgb.Booster(dict(params, hip_profile=1), [d])  # profiled rounds stay synchronous
+    for i in range(5):
+        profiled.update(d, i)
+    assert _trees(profiled) == _trees(stepwise[:5])

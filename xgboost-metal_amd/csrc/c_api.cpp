@@ -46,7 +46,20 @@ MatrixPtr& matrix(DMatrixHandle h) {
   require(h != nullptr, "DMatrix handle is null.");
   return *static_cast<MatrixPtr*>(h);
 }
+// The booster with its queued rounds completed: every entry point that reads
+// the model uses this one.
 Learner& booster(BoosterHandle h) {
+  require(h != nullptr, "Booster handle is null.");
+  Learner& b = *static_cast<Learner*>(h);
+  std::lock_guard<std::recursive_mutex> lock(b.mutex);
+  b.drain();
+  return b;
+}
+
+// The booster as it is, rounds possibly still queued on the device: for the
+// per-round entry points (updates, parameters, attributes), which never read
+// the trees and must not wait for the device.
+Learner& booster_queued(BoosterHandle h) {
   require(h != nullptr, "Booster handle is null.");
   return *static_cast<Learner*>(h);
 }
@@ -807,7 +820,7 @@ int XGBoosterReset(BoosterHandle handle) {
 
 int XGBoosterSetParam(BoosterHandle handle, const char* name, const char* value) {
   API_BEGIN
-  auto& b = booster(handle);
+  auto& b = booster_queued(handle);
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   b.set_param(name, value ? value : "");
   API_END
@@ -815,7 +828,7 @@ int XGBoosterSetParam(BoosterHandle handle, const char* name, const char* value)
 
 int XGBoosterSetParams(BoosterHandle handle, char const* config) {
   API_BEGIN
-  auto& b = booster(handle);
+  auto& b = booster_queued(handle);
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   Json c = Json::parse(config);
   for (auto const& kv : c.members()) b.set_param(kv.first, kv.second.is_string() ? kv.second.string() : kv.second.dump());
@@ -824,7 +837,7 @@ int XGBoosterSetParams(BoosterHandle handle, char const* config) {
 
 int XGBoosterUpdateOneIter(BoosterHandle handle, int iter, DMatrixHandle dtrain) {
   API_BEGIN
-  auto& b = booster(handle);
+  auto& b = booster_queued(handle);
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   b.update(*matrix(dtrain), iter);
   API_END
@@ -832,7 +845,7 @@ int XGBoosterUpdateOneIter(BoosterHandle handle, int iter, DMatrixHandle dtrain)
 
 int XGBoosterBoostOneIter(BoosterHandle handle, DMatrixHandle dtrain, float* grad, float* hess, bst_ulong len) {
   API_BEGIN
-  auto& b = booster(handle);
+  auto& b = booster_queued(handle);
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   b.boost(*matrix(dtrain), grad, hess, (size_t)len);
   API_END
@@ -841,7 +854,7 @@ int XGBoosterBoostOneIter(BoosterHandle handle, DMatrixHandle dtrain, float* gra
 int XGBoosterTrainOneIter(BoosterHandle handle, DMatrixHandle dtrain, int /*iter*/, char const* grad,
                           char const* hess) {
   API_BEGIN
-  auto& b = booster(handle);
+  auto& b = booster_queued(handle);
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   ArrayView g = parse_interface(grad), h = parse_interface(hess);
   require(g.shape == h.shape, "Gradient and Hessian shapes must match.");
@@ -989,7 +1002,7 @@ int XGBoosterGetNumFeature(BoosterHandle handle, bst_ulong* out) {
 int XGBoosterGetAttr(BoosterHandle handle, const char* key, const char** out, int* success) {
   API_BEGIN
   *success = 0;
-  for (auto const& kv : booster(handle).attributes)
+  for (auto const& kv : booster_queued(handle).attributes)
     if (kv.first == key) {
       g_results.str = kv.second;
       *out = g_results.str.c_str();
@@ -1000,7 +1013,7 @@ int XGBoosterGetAttr(BoosterHandle handle, const char* key, const char** out, in
 
 int XGBoosterSetAttr(BoosterHandle handle, const char* key, const char* value) {
   API_BEGIN
-  auto& attrs = booster(handle).attributes;
+  auto& attrs = booster_queued(handle).attributes;
   for (size_t i = 0; i < attrs.size(); ++i)
     if (attrs[i].first == key) {
       if (value) attrs[i].second = value;
@@ -1014,7 +1027,7 @@ int XGBoosterSetAttr(BoosterHandle handle, const char* key, const char* value) {
 int XGBoosterGetAttrNames(BoosterHandle handle, bst_ulong* out_len, const char*** out) {
   API_BEGIN
   g_results.strings.clear();
-  for (auto const& kv : booster(handle).attributes) g_results.strings.push_back(kv.first);
+  for (auto const& kv : booster_queued(handle).attributes) g_results.strings.push_back(kv.first);
   g_results.pointers.clear();
   for (auto const& s : g_results.strings) g_results.pointers.push_back(s.c_str());
   *out_len = g_results.strings.size();

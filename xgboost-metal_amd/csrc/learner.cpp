@@ -494,7 +494,8 @@ void Learner::predict_into(DMatrix& data, const uint32_t* offsets, uint32_t coun
 }
 
 DeviceBuffer* Learner::margin_cache(DMatrix& data) {
-  if (cache_id_ == data.id && cache_trees_ == trees.size() && d_margin_.get()) return &d_margin_;
+  if (cache_id_ == data.id && cache_trees_ == boosted_rounds() && d_margin_.get()) return &d_margin_;
+  drain();  // the margin is rebuilt from every tree
   data.upload();
   d_margin_.ensure((size_t)data.rows * sizeof(float));
   if (!data.base_margin.empty()) {
@@ -640,7 +641,15 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   d_tree_ws_.ensure(ws);
   const uint32_t max_nodes = (2u << depth) - 1u;
   const size_t node_bytes = (size_t)max_nodes * sizeof(MgbTreeNode);
-  d_nodes_.ensure(node_bytes + 16);
+  // This round's slot in the queue of rounds not yet copied to the host
+  // (up to 64 rounds or 64 MB; a full queue is drained first).
+  const size_t slot_bytes = (node_bytes + 16 + 255) / 256 * 256;
+  if (pending_bytes_ + slot_bytes > d_pending_.bytes()) {
+    drain();
+    const size_t rounds = std::max<size_t>(1, std::min<size_t>(64, (64u << 20) / slot_bytes));
+    if (d_pending_.bytes() < rounds * slot_bytes) d_pending_.resize(rounds * slot_bytes);
+  }
+  const size_t slot_offset = pending_bytes_;
   MgbSplitParams sp{};
   sp.reg_lambda = fnumber("reg_lambda", 1.0f);
   sp.reg_alpha = fnumber("reg_alpha", 0.0f);
@@ -653,8 +662,8 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   DeviceBuffer* margin = margin_cache(data);
   const bool profiling = integer("hip_profile", 0) != 0;
   kcheck(mgb_profile_enable(profiling ? 1 : 0), "profile");
-  auto* nodes = d_nodes_.as<MgbTreeNode>();
-  auto* count = reinterpret_cast<uint32_t*>(d_nodes_.as<uint8_t>() + node_bytes);
+  auto* nodes = reinterpret_cast<MgbTreeNode*>(d_pending_.as<uint8_t>() + slot_offset);
+  auto* count = reinterpret_cast<uint32_t*>(d_pending_.as<uint8_t>() + slot_offset + node_bytes);
   const uint32_t* features = sample_columns(data.cols);
   if (data.sparse) {
     const bool root_columns = integer("hip_csr_root_columns", 1) != 0;
@@ -673,13 +682,11 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
                          d_tree_ws_.get(), d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
            "tree growth");
   }
-  // One device-to-host copy per round: node records followed by the count.
-  std::vector<uint8_t> host(node_bytes + 16);
-  d_nodes_.download(host.data(), node_bytes + sizeof(uint32_t));
-  uint32_t n = 0;
-  std::memcpy(&n, host.data() + node_bytes, sizeof(uint32_t));
-  require(n >= 1 && n <= max_nodes, "device tree driver produced an invalid node count");
+  pending_.push_back(Pending{slot_offset, node_bytes, max_nodes});
+  pending_bytes_ += slot_bytes;
+  cache_trees_ = boosted_rounds();  // the kernels add the new leaves to the cached margin
   if (profiling) {
+    drain();  // profiled rounds stay synchronous: their statistics are read back now
     // Algorithmic histogram bytes per level: rows built x (F codes + 4-byte
     // row id + 8-byte gradient pair) + nodes built x F x (B+1) x 16 bytes.
     kcheck(mgb_profile_collect(), "profile collect");
@@ -695,11 +702,26 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
       hist_rows_ += rows[d];
     }
   }
-  Tree tree;
-  tree.nodes.resize(n);
-  std::memcpy(tree.nodes.data(), host.data(), (size_t)n * sizeof(MgbTreeNode));
-  trees.push_back(std::move(tree));
-  cache_trees_ = trees.size();  // the kernels added the new leaves to the cached margin
+}
+
+void Learner::drain() {
+  if (pending_.empty()) return;
+  // One device-to-host copy (it waits for the queued rounds) of every
+  // pending slot: node records followed by the node count.
+  std::vector<uint8_t> host(pending_bytes_);
+  d_pending_.download(host.data(), pending_bytes_);
+  std::vector<Pending> rounds;
+  rounds.swap(pending_);
+  pending_bytes_ = 0;
+  for (const Pending& p : rounds) {
+    uint32_t n = 0;
+    std::memcpy(&n, host.data() + p.offset + p.node_bytes, sizeof(uint32_t));
+    require(n >= 1 && n <= p.max_nodes, "device tree driver produced an invalid node count");
+    Tree tree;
+    tree.nodes.resize(n);
+    std::memcpy(tree.nodes.data(), host.data() + p.offset, (size_t)n * sizeof(MgbTreeNode));
+    trees.push_back(std::move(tree));
+  }
 }
 
 void Learner::update(DMatrix& data, int /*iteration*/) {
@@ -768,6 +790,7 @@ void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t 
 
 const float* Learner::predict_device(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end,
                                     DeviceBuffer& scratch) {
+  drain();
   scratch.ensure((size_t)std::max<uint32_t>(data.rows, 1) * sizeof(float));
   float* d_out = scratch.as<float>();
   if (!initialized) {
@@ -975,6 +998,7 @@ static float json_float(const Json& v) {
 }
 
 void Learner::load_model(const Json& input) {
+  drain();  // queued rounds finish before the model they belong to is replaced
   const Json& learner = input.at("learner");
   const Json& booster = learner.at("gradient_booster");
   require(booster.at("name").string() == "gbtree", "Only gbtree models can be loaded.");
@@ -1094,10 +1118,11 @@ void Learner::load_config(const Json& cfg) {
 }
 
 void Learner::reset() {
+  drain();
   d_margin_.release();
   d_grad_.release();
   d_tree_ws_.release();
-  d_nodes_.release();
+  d_pending_.release();
   cache_id_ = 0;
   cache_trees_ = 0;
 }

@@ -146,7 +146,11 @@ class Learner {
   void reset();
   Json profile() const;
 
-  uint32_t boosted_rounds() const { return (uint32_t)trees.size(); }
+  // Rounds whose node records are still only on the device: each round's
+  // kernels are queued without a host synchronisation; drain() waits for them
+  // and appends their trees.  Everything that reads the model drains first.
+  void drain();
+  uint32_t boosted_rounds() const { return (uint32_t)(trees.size() + pending_.size()); }
   uint32_t num_feature = 0;
   std::vector<Tree> trees;
   std::vector<std::pair<std::string, std::string>> attributes;
@@ -177,7 +181,7 @@ class Learner {
   size_t cache_trees_ = 0;
   DeviceBuffer d_margin_;
   // Round buffers.
-  DeviceBuffer d_grad_, d_mass_, d_scales_, d_tree_ws_, d_nodes_, d_node_count_, d_base_;
+  DeviceBuffer d_grad_, d_mass_, d_scales_, d_tree_ws_, d_node_count_, d_base_;
   // Model on the device for prediction.
   DeviceBuffer d_model_nodes_, d_model_offsets_;
   size_t model_version_ = SIZE_MAX, model_trees_ = 0;
@@ -192,6 +196,14 @@ class Learner {
   DeviceBuffer d_features_;
   std::vector<uint32_t> feature_flags_;
   DeviceBuffer d_eval_pred_, d_metric_ws_;
+  // Queued rounds: node records (then the node count) at `offset` in d_pending_.
+  struct Pending {
+    size_t offset, node_bytes;
+    uint32_t max_nodes;
+  };
+  std::vector<Pending> pending_;
+  DeviceBuffer d_pending_;
+  size_t pending_bytes_ = 0;
 };
 
 }  // namespace mgb
