@@ -19,7 +19,8 @@ namespace mgb {
 namespace {
 
 constexpr uint32_t kPartTile = 1024;      // rows per partition task
-constexpr uint32_t kSelectThreads = 1024;
+constexpr uint32_t kPartThreads = 256;    // partition (and select bookkeeping) workgroup
+constexpr uint32_t kSelectThreads = 256;
 constexpr uint32_t kHistThreads = 1024;
 constexpr int kHistUnroll = 4;          // rows in flight per thread
 
@@ -31,10 +32,11 @@ struct LevelState {
   uint32_t n_nodes;       // frontier size of the current level
   uint32_t n_hist_tasks;
   uint32_t n_zero;
-  uint32_t n_part_tasks;
+  uint32_t n_part[2];     // partition tasks of the levels of each parity (banked: the
+                          // apply kernel of one level plans the next while it runs)
   uint32_t node_count;    // tree nodes allocated so far
   uint32_t error;
-  uint32_t padding[10];
+  uint32_t padding[9];
   // Per level: rows and nodes whose histograms were built directly.
   uint64_t rows_built[kMaxLevels];
   uint32_t nodes_built[kMaxLevels];
@@ -48,7 +50,7 @@ struct Frontier {
   uint32_t built;         // histogram built directly (1) or by subtraction (0)
   uint32_t first_task;    // built nodes: first histogram task (row tile)
   uint32_t ntiles;        // built nodes: number of row tiles
-  uint32_t padding;
+  float leaf;             // the node's leaf value if it does not split
 };
 
 struct Cand {
@@ -88,7 +90,7 @@ __device__ __forceinline__ uint64_t best_key(float gain, uint32_t feature) {
   uint32_t order = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
   return ((uint64_t)order << 32) | (uint64_t)(~feature);
 }
-struct PartTask { uint32_t slot, begin, end, first, ntasks, padding[3]; };
+struct PartTask { uint32_t slot, begin, end, padding; };
 
 // Device pointers of one tree workspace.
 struct Tree {
@@ -98,11 +100,10 @@ struct Tree {
   Frontier* frontier[2];
   SplitRec* recs;             // per (frontier slot, feature): the feature's best candidate
   unsigned long long* best;   // per frontier slot, see best_key
-  NodeOp* ops;
   HistTask* hist_tasks;
   uint32_t* zero_list;        // built nodes with several row tiles (reduced from partials)
   int64_t* partials;          // per (task, feature group): G x (max_bin+1) (g, h) partial histograms
-  PartTask* part_tasks;
+  PartTask* part_tasks;       // two banks of max_part_tasks, by level parity
   uint32_t* cursors;          // per split node: next left position, end of the free right range
   // Inputs.
   const void* bins;
@@ -127,13 +128,27 @@ struct Tree {
   uint32_t max_depth, slots, rows_per_tile, groups;
   uint32_t root_tile;                        // rows per histogram tile at the root
   uint32_t features_per_group, unit_hessian, dense, max_hist_tasks;
+  uint32_t max_part_tasks;
   uint32_t column_levels;                    // histogram levels that read `columns`
-  uint32_t select_plans;                     // unit Hessians, dense: k_select plans the next level
+  uint32_t select_plans;                     // unit Hessians, dense: the select bookkeeping plans the next level
   uint32_t sparse;                           // CSR: missing slots from node totals, no partials
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
 };
+
+// Per-level banks, by depth parity: the apply kernel of level d reads level
+// d's partition tasks, cursors and best keys while its bookkeeping workgroup
+// writes level d+1's.
+__device__ __forceinline__ PartTask* part_bank(const Tree& t, uint32_t depth) {
+  return t.part_tasks + (uint64_t)(depth & 1) * t.max_part_tasks;
+}
+__device__ __forceinline__ uint32_t* cursor_bank(const Tree& t, uint32_t depth) {
+  return t.cursors + (uint64_t)(depth & 1) * 2 * t.slots;
+}
+__device__ __forceinline__ unsigned long long* best_bank(const Tree& t, uint32_t depth) {
+  return t.best + (uint64_t)(depth & 1) * t.slots;
+}
 
 __host__ __device__ inline uint32_t div_up(uint64_t a, uint32_t b) { return (uint32_t)((a + b - 1) / b); }
 
@@ -209,19 +224,29 @@ __global__ void k_level0(Tree t) {
     uint32_t end = begin + t.root_tile < t.rows_n ? begin + t.root_tile : t.rows_n;
     t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
   }
+  // The root's partition tasks (row tiles of [0, N)) and cursors.
+  const uint32_t ptiles = t.rows_n ? div_up(t.rows_n, kPartTile) : 0;
+  if (t.part_tasks)
+    for (uint32_t i = threadIdx.x; i < ptiles; i += blockDim.x) {
+      const uint32_t b = i * kPartTile;
+      t.part_tasks[i] = PartTask{0u, b, b + kPartTile < t.rows_n ? b + kPartTile : t.rows_n, 0u};
+    }
   if (threadIdx.x == 0) {
     st->rows_built[0] = t.rows_n;
     st->nodes_built[0] = 1;
     st->n_nodes = 1;
     st->n_hist_tasks = tiles;
     st->n_zero = tiles == 1 ? 0u : 1u;
-    st->n_part_tasks = 0;
+    st->n_part[0] = ptiles;
+    st->n_part[1] = 0;
+    t.cursors[0] = 0;
+    t.cursors[1] = t.rows_n;
     st->node_count = 1;
     st->error = 0;
     t.zero_list[0] = 0;
     Frontier root;
     root.id = 0; root.begin = 0; root.count = t.rows_n; root.parent_slot = 0;
-    root.sum_g = 0; root.sum_h = 0; root.built = 1; root.first_task = 0; root.ntiles = tiles; root.padding = 0;
+    root.sum_g = 0; root.sum_h = 0; root.built = 1; root.first_task = 0; root.ntiles = tiles; root.leaf = 0.0f;
     t.frontier[0][0] = root;
     MgbTreeNode n;
     n.left = -1; n.right = -1; n.parent = -1; n.feature = -1;
@@ -235,23 +260,38 @@ __global__ void k_level0(Tree t) {
 __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth) {
   __shared__ uint32_t scan[kSelectThreads / kWave + 1];
   __shared__ uint32_t s_off[kSelectThreads], s_slot[kSelectThreads], s_begin[kSelectThreads], s_end[kSelectThreads];
+  __shared__ uint32_t scan_right[kSelectThreads];
   LevelState* st = t.state;
   Frontier* fr = t.frontier[depth & 1];
   uint32_t pairs = st->n_nodes / 2;
-  uint32_t carry_tasks = 0, carry_zero = 0, carry_rows = 0;
+  const uint32_t* parent_cursors = cursor_bank(t, depth - 1);
+  uint32_t* cursors = cursor_bank(t, depth);
+  unsigned long long* best = best_bank(t, depth);
+  PartTask* ptasks = part_bank(t, depth);
+  uint32_t carry_tasks = 0, carry_zero = 0, carry_rows = 0, carry_part = 0;
   for (uint32_t base = 0; base < pairs; base += blockDim.x) {
     uint32_t p = base + threadIdx.x;
     uint32_t tiles = 0, zero = 0, built = 0, count = 0, begin = 0;
+    uint32_t lbegin = 0, c0 = 0, c1 = 0;
     if (p < pairs) {
       // Child segments from the partition's cursor: the left child holds the
       // rows below the parent's final left cursor, the right child the rest.
       Frontier& lf = fr[2 * p];
       Frontier& rf = fr[2 * p + 1];
       const uint32_t total = lf.count;
-      const uint32_t c0 = t.cursors[2 * lf.parent_slot] - lf.begin, c1 = total - c0;
+      c0 = parent_cursors[2 * lf.parent_slot] - lf.begin;
+      c1 = total - c0;
+      lbegin = lf.begin;
       lf.count = c0;
       rf.begin = lf.begin + c0;
       rf.count = c1;
+      // This level's partition cursors and best-feature keys.
+      cursors[4 * p] = lbegin;
+      cursors[4 * p + 1] = lbegin + c0;
+      cursors[4 * p + 2] = lbegin + c0;
+      cursors[4 * p + 3] = lbegin + total;
+      best[2 * p] = 0;
+      best[2 * p + 1] = 0;
       built = c0 <= c1 ? 2 * p : 2 * p + 1;
       fr[built].built = 1;
       fr[built ^ 1u].built = 0;
@@ -286,9 +326,31 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     if (zero) t.zero_list[zoff] = built;
     carry_tasks += total_tasks;
     carry_zero += total_zero;
+    // Partition tasks of both children, in slot order.
+    const uint32_t pl = p < pairs ? div_up(c0, kPartTile) : 0, pr = p < pairs ? div_up(c1, kPartTile) : 0;
+    uint32_t total_part;
+    const uint32_t poff = block_exclusive_u32(pl + pr, scan, &total_part);
+    __syncthreads();
+    s_off[threadIdx.x] = poff;
+    s_slot[threadIdx.x] = pl;
+    s_begin[threadIdx.x] = lbegin;
+    s_end[threadIdx.x] = c0;  // left count
+    scan_right[threadIdx.x] = c1;
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < total_part; j += blockDim.x) {
+      const uint32_t k = owner_of(s_off, nitems, j);
+      const uint32_t q = j - s_off[k];
+      const bool left = q < s_slot[k];
+      const uint32_t cb = left ? s_begin[k] : s_begin[k] + s_end[k];
+      const uint32_t ce = left ? s_begin[k] + s_end[k] : s_begin[k] + s_end[k] + scan_right[k];
+      const uint32_t b = cb + (left ? q : q - s_slot[k]) * kPartTile;
+      ptasks[carry_part + j] = PartTask{2 * (base + k) + (left ? 0u : 1u), b, b + kPartTile < ce ? b + kPartTile : ce, 0u};
+    }
+    carry_part += total_part;
     __syncthreads();
   }
   if (threadIdx.x == 0) {
+    st->n_part[depth & 1] = carry_part;
     st->n_hist_tasks = carry_tasks;
     st->n_zero = carry_zero;
     if (depth < kMaxLevels) {
@@ -903,6 +965,15 @@ __device__ __forceinline__ void built_pair(const BuiltHist& hb, uint32_t bin, bo
   }
   g = v = 0;
   uint32_t k = 0;
+  // Sixteen partial rows in flight per lane, then four: the sum is a chain of
+  // dependent loads otherwise (a 32-tile root node).
+  for (; k + 16 <= hb.ntiles; k += 16) {
+    uint64_t a[16], c[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) load_pair(hb.part + (uint64_t)(k + u) * hb.stride, bin, a[u], c[u]);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) { g += a[u]; v += c[u]; }
+  }
   for (; k + 4 <= hb.ntiles; k += 4) {
     uint64_t a[4], c[4];
 #pragma unroll
@@ -1087,7 +1158,7 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
     NodeEval e;
     node_begin(e, tg, th, mg, mh, eg, eh, t.sp);
     score_node<W, CH>(e, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
-                  xkey[slot_in_block][0], wave_in_item, t.recs + f, t.best, f);
+                  xkey[slot_in_block][0], wave_in_item, t.recs + f, best_bank(t, depth), f);
     return;
   }
   const uint32_t n = st->n_nodes;
@@ -1143,9 +1214,9 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
   node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
   score_node<W, CH>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
-                xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f, t.best + built, f);
+                xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f, best_bank(t, depth) + built, f);
   score_node<W, CH>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
-                xkey[slot_in_block][1], wave_in_item, t.recs + (uint64_t)other * F + f, t.best + other, f);
+                xkey[slot_in_block][1], wave_in_item, t.recs + (uint64_t)other * F + f, best_bank(t, depth) + other, f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1205,10 +1276,14 @@ __device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh,
   }
 }
 
-__global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t depth) {
-  __shared__ uint32_t scan[kSelectThreads / kWave + 1];
-  __shared__ uint32_t s_off[kSelectThreads], s_begin[kSelectThreads], s_end[kSelectThreads];
-  __shared__ uint32_t scan_slot[kSelectThreads];
+// LDS the select bookkeeping needs at the dense root: feature 0's and the
+// chosen feature's bins as binary64 (g, h) and the chosen feature's cuts.
+constexpr size_t kRootStageBytes = 4 * kMaxBins1 * sizeof(double) + kMaxBins1 * sizeof(float);
+
+__device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
+  __shared__ uint32_t scan[kPartThreads / kWave + 1];
+  __shared__ uint32_t s_off[kPartThreads], s_begin[kPartThreads], s_end[kPartThreads];
+  __shared__ uint32_t scan_slot[kPartThreads], s_count[kPartThreads];
   LevelState* st = t.state;
   const uint32_t n = st->n_nodes;
   const uint32_t F = t.cols;
@@ -1224,15 +1299,17 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
   const uint32_t node_base = st->node_count;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const MgbSplitParams& p = t.sp;
+  const unsigned long long* best_keys = best_bank(t, depth);
   // Dense root: feature 0 and the chosen feature staged in LDS by all threads
   // so the serial ordered sums below read LDS, not scattered global words.
   // The chosen feature's cuts are staged too: the threshold search below
   // would otherwise be a chain of dependent global loads.
-  __shared__ double root0[2][kMaxBins1], rootf[2][kMaxBins1];
-  __shared__ float rootcut[kMaxBins1];
+  double (*root0)[kMaxBins1] = reinterpret_cast<double (*)[kMaxBins1]>(stage);
+  double (*rootf)[kMaxBins1] = reinterpret_cast<double (*)[kMaxBins1]>(stage + 2 * kMaxBins1 * sizeof(double));
+  float* rootcut = reinterpret_cast<float*>(stage + 4 * kMaxBins1 * sizeof(double));
   const bool dense_root = depth == 0 && t.dense && n > 0;
   if (dense_root) {
-    const uint64_t key = t.best[0];
+    const uint64_t key = best_keys[0];
     const uint32_t f = key ? ~(uint32_t)key : 0u;
     const uint32_t cf = t.counts[f];
     stage_feature(t.hist[0], t.counts[0], eg, eh, root0);
@@ -1240,7 +1317,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
     for (uint32_t b = threadIdx.x; b < cf; b += blockDim.x) rootcut[b] = t.cuts[(uint64_t)f * t.cut_stride + b];
     __syncthreads();
   }
-  uint32_t carry_expanded = 0, carry_tasks = 0, carry_htasks = 0, carry_zero = 0, carry_rows = 0;
+  uint32_t carry_expanded = 0, carry_htasks = 0, carry_zero = 0, carry_rows = 0, carry_ptasks = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
     const uint32_t i = base + threadIdx.x;
     const bool valid = i < n;
@@ -1250,8 +1327,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
     Frontier node;
     if (valid) {
       node = fr[i];
-      const uint64_t key = t.best[i];
-      t.best[i] = 0;  // cleared for the next level, which reuses the slot
+      const uint64_t key = best_keys[i];
       NodeEval ne;
       node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p);
       parent_w = ne.w;
@@ -1274,7 +1350,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         parent_w = calc_weight(tg, th, p);
         total_h = (float)th;
         if (best.feature >= 0 && (uint32_t)best.feature < F) {
-          // best.feature is the feature of t.best[0], staged in rootcut.
+          // best.feature is the root's best-key feature, staged in rootcut.
           const uint32_t f = (uint32_t)best.feature, count = t.counts[f];
           uint32_t lo = 0, hi = count;
           while (lo < hi) {
@@ -1303,10 +1379,6 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
     }
     uint32_t total_expanded;
     const uint32_t rank = block_exclusive_u32(expand ? 1u : 0u, scan, &total_expanded) + carry_expanded;
-    uint32_t tiles = 0;
-    if (valid) tiles = div_up(node.count, kPartTile);
-    uint32_t total_tasks;
-    const uint32_t toff = block_exclusive_u32(tiles, scan, &total_tasks) + carry_tasks;
     // Next level's plan (plan_next): the smaller child is built (ties left,
     // kernels/boost.metal:661-698) in row tiles, the other subtracted.
     uint32_t lcount = 0, htiles = 0, hzero = 0, hrows = 0;
@@ -1317,12 +1389,17 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
       htiles = div_up(hrows, t.rows_per_tile);
       hzero = htiles != 1;
     }
-    uint32_t total_htasks = 0, total_zero = 0, total_rows = 0;
-    uint32_t hoff = 0, zoff = 0;
+    uint32_t total_htasks = 0, total_zero = 0, total_rows = 0, total_ptasks = 0;
+    uint32_t hoff = 0, zoff = 0, poff = 0, pl = 0, pr = 0;
     if (plan_next) {
       hoff = block_exclusive_u32(htiles, scan, &total_htasks) + carry_htasks;
       zoff = block_exclusive_u32(hzero, scan, &total_zero) + carry_zero;
       block_exclusive_u32(hrows, scan, &total_rows);
+      if (valid && expand) {
+        pl = div_up(lcount, kPartTile);
+        pr = div_up(node.count - lcount, kPartTile);
+      }
+      poff = block_exclusive_u32(pl + pr, scan, &total_ptasks);
     }
     if (valid) {
       MgbTreeNode* rec = t.nodes + node.id;
@@ -1331,12 +1408,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         rec->base_weight = parent_w;
         rec->leaf = parent_w * p.eta;
       }
-      NodeOp op;
-      op.feature = 0; op.last_left_bin = -1; op.default_left = 0;
-      op.leaf = rec->leaf; op.left_leaf = 0; op.right_leaf = 0; op.child_slot = 0;
-      if (!expand) {
-        op.op = kOpLeaf;
-      } else {
+      if (expand) {
         const int32_t left = (int32_t)(node_base + 2 * rank), right = left + 1;
         rec->left = left; rec->right = right;
         rec->feature = best.feature;
@@ -1352,23 +1424,14 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         r.leaf = best.right_w * p.eta; r.cover = best.right_h; r.base_weight = r.leaf;
         t.nodes[left] = l;
         t.nodes[right] = r;
-        op.op = final_level ? kOpFinal : kOpSplit;
-        op.feature = (uint32_t)best.feature;
-        op.last_left_bin = best.default_left ? (int32_t)best.bin - 1 : (int32_t)best.bin;
-        op.default_left = best.default_left;
-        op.left_leaf = l.leaf;
-        op.right_leaf = r.leaf;
-        op.child_slot = 2 * rank;
         if (!final_level) {
           // Both children carry the parent's segment until the next level's
           // plan splits it at the partition's final left cursor.
-          t.cursors[2 * i] = node.begin;
-          t.cursors[2 * i + 1] = node.begin + node.count;
           Frontier lf, rf;
           lf.id = left; lf.begin = node.begin; lf.count = node.count; lf.parent_slot = i; lf.sum_g = best.lg;
-          lf.sum_h = best.lh; lf.built = 0; lf.first_task = 0; lf.ntiles = 0; lf.padding = 0;
+          lf.sum_h = best.lh; lf.built = 0; lf.first_task = 0; lf.ntiles = 0; lf.leaf = l.leaf;
           rf = lf;
-          rf.id = right; rf.sum_g = best.rg; rf.sum_h = best.rh;
+          rf.id = right; rf.sum_g = best.rg; rf.sum_h = best.rh; rf.leaf = r.leaf;
           if (plan_next) {
             lf.count = lcount;
             rf.begin = node.begin + lcount;
@@ -1378,31 +1441,22 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
             b.first_task = hoff;
             b.ntiles = htiles;
             if (hzero) t.zero_list[zoff] = lcount <= rf.count ? 2 * rank : 2 * rank + 1;
+            // The next level's partition cursors and best-feature keys.
+            uint32_t* nc = cursor_bank(t, depth + 1);
+            nc[4 * rank] = lf.begin;
+            nc[4 * rank + 1] = lf.begin + lf.count;
+            nc[4 * rank + 2] = rf.begin;
+            nc[4 * rank + 3] = rf.begin + rf.count;
+            unsigned long long* nb = best_bank(t, depth + 1);
+            nb[2 * rank] = 0;
+            nb[2 * rank + 1] = 0;
           }
           next[2 * rank] = lf;
           next[2 * rank + 1] = rf;
         }
       }
-      t.ops[i] = op;
     }
-    // Partition tiles of this batch's nodes, written by the whole block.
-    s_off[threadIdx.x] = toff - carry_tasks;
-    s_begin[threadIdx.x] = valid ? node.begin : 0;
-    s_end[threadIdx.x] = valid ? node.begin + node.count : 0;
-    __syncthreads();
     const uint32_t nitems = n - base < blockDim.x ? n - base : blockDim.x;
-    for (uint32_t j = threadIdx.x; j < total_tasks; j += blockDim.x) {
-      const uint32_t k = owner_of(s_off, nitems, j);
-      const uint32_t b = s_begin[k] + (j - s_off[k]) * kPartTile;
-      PartTask task;
-      task.slot = base + k;
-      task.begin = b;
-      task.end = b + kPartTile < s_end[k] ? b + kPartTile : s_end[k];
-      task.first = carry_tasks + s_off[k];
-      task.ntasks = (k + 1 < nitems ? s_off[k + 1] : total_tasks) - s_off[k];
-      task.padding[0] = task.padding[1] = task.padding[2] = 0;
-      t.part_tasks[carry_tasks + j] = task;
-    }
     if (plan_next) {
       // Row tiles of the next level's built children, in pair order.
       __syncthreads();
@@ -1419,25 +1473,47 @@ __global__ __launch_bounds__(kSelectThreads) void k_select(Tree t, uint32_t dept
         const uint32_t ntiles = (k + 1 < nitems ? s_off[k + 1] : total_htasks) - s_off[k];
         t.hist_tasks[carry_htasks + j] = HistTask{scan_slot[k], b, e, ntiles == 1 ? 1u : 0u};
       }
+      // Row tiles of the next level's nodes (both children of each split),
+      // for the next level's partition.
+      __syncthreads();
+      s_off[threadIdx.x] = poff;  // non-decreasing; a node that does not split adds no tiles
+      s_begin[threadIdx.x] = valid && expand ? node.begin : 0;
+      s_end[threadIdx.x] = lcount;
+      s_count[threadIdx.x] = valid && expand ? node.count : 0;
+      scan_slot[threadIdx.x] = valid && expand ? 2 * rank : 0u;
+      __syncthreads();
+      PartTask* ntasks = part_bank(t, depth + 1);
+      for (uint32_t j = threadIdx.x; j < total_ptasks; j += blockDim.x) {
+        const uint32_t k = owner_of(s_off, nitems, j);
+        const uint32_t q = j - s_off[k];
+        const uint32_t lt = div_up(s_end[k], kPartTile);
+        const bool left = q < lt;
+        // The node's rows: [begin, begin + lcount) go left, the rest right.
+        const uint32_t nb = s_begin[k];
+        const uint32_t cb = left ? nb : nb + s_end[k];
+        const uint32_t ce = left ? nb + s_end[k] : nb + s_count[k];
+        const uint32_t b = cb + (left ? q : q - lt) * kPartTile;
+        ntasks[carry_ptasks + j] = PartTask{scan_slot[k] + (left ? 0u : 1u), b, b + kPartTile < ce ? b + kPartTile : ce, 0u};
+      }
       carry_htasks += total_htasks;
       carry_zero += total_zero;
       carry_rows += total_rows;
+      carry_ptasks += total_ptasks;
     }
     carry_expanded += total_expanded;
-    carry_tasks += total_tasks;
     __syncthreads();
   }
   if (threadIdx.x == 0) {
     if (plan_next) {
       st->n_hist_tasks = carry_htasks;
       st->n_zero = carry_zero;
+      st->n_part[(depth + 1) & 1] = carry_ptasks;
       if (depth + 1 < kMaxLevels) {
         st->rows_built[depth + 1] = carry_rows;
         st->nodes_built[depth + 1] = carry_expanded;
       }
     }
     st->node_count = node_base + 2 * carry_expanded;
-    st->n_part_tasks = carry_tasks;
     st->n_nodes = final_level ? 0 : 2 * carry_expanded;  // becomes the next level's frontier size
     if (t.node_count_out) *t.node_count_out = node_base + 2 * carry_expanded;
   }
@@ -1477,7 +1553,6 @@ __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint3
   return (int32_t)code <= op.last_left_bin;
 }
 
-constexpr uint32_t kPartThreads = 256;
 constexpr int kPartPer = kPartTile / kPartThreads;  // rows per thread, all loaded up front
 
 // Row ids of a partition tile for this thread (positions begin + k*256 + tid).
@@ -1492,28 +1567,101 @@ __device__ __forceinline__ void load_tile_rows(const uint32_t* rows, const PartT
   }
 }
 
-// One workgroup per tile of up to kPartTile rows of one node.  A split node's
-// left rows fill its segment upwards from the start and its right rows
-// downwards from the end: each tile claims its ranges with one atomic on
-// each of the node's two cursors, then writes ranks (chunk, wave, lane) into
-// them.  The order of rows inside a child depends on which tile claims first;
-// nothing downstream depends on it (histograms are exact integer sums and the
-// margin update is per row).
+// The partition's view of one node of the level: whether it splits, on
+// which bin and direction, and the leaf values -- the select arithmetic for
+// this node alone (no other node's result is needed), so every workgroup of
+// the node computes the same bits the bookkeeping workgroup writes into the
+// tree.
+__device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
+  const Frontier node = t.frontier[depth & 1][slot];
+  const uint64_t key = best_bank(t, depth)[slot];
+  const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
+  const MgbSplitParams& p = t.sp;
+  NodeEval ne;
+  node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p);
+  Cand best;
+  best.feature = -1;
+  best.gain = -INFINITY;
+  if (key) {
+    const uint32_t f = ~(uint32_t)key;
+    best = make_cand(ne, t.recs[(uint64_t)slot * t.cols + f], f, t.counts[f], t.cuts + (uint64_t)f * t.cut_stride,
+                     eg, eh, p);
+  }
+  const bool expand = best.feature >= 0 && (uint32_t)best.feature < t.cols && best.gain > 1.0e-6f &&
+                      best.gain >= p.min_split_loss && depth < t.max_depth;
+  NodeOp op;
+  op.feature = 0; op.last_left_bin = -1; op.default_left = 0;
+  op.leaf = node.leaf; op.left_leaf = 0; op.right_leaf = 0; op.child_slot = 0;
+  if (!expand) {
+    op.op = kOpLeaf;
+    if (node.id == 0) {
+      // A root that does not split: its weight, from the dense root's ordered
+      // binary64 sums of feature 0's bins when the matrix has no missing
+      // value (the same sums the bookkeeping workgroup stages in LDS).
+      float parent_w = ne.w;
+      if (t.dense) {
+        const int64_t* h0 = t.hist[0];
+        double tg = 0, th = 0;
+        for (uint32_t b = 0; b < t.counts[0]; ++b) {
+          tg += stat_value(h0[2 * b], eg);
+          th += stat_value(h0[2 * b + 1], eh);
+        }
+        parent_w = calc_weight(tg, th, p);
+      }
+      op.leaf = parent_w * p.eta;
+    }
+    return op;
+  }
+  op.op = depth + 1 >= t.max_depth ? kOpFinal : kOpSplit;
+  op.feature = (uint32_t)best.feature;
+  op.last_left_bin = best.default_left ? (int32_t)best.bin - 1 : (int32_t)best.bin;
+  op.default_left = best.default_left;
+  op.left_leaf = best.left_w * p.eta;
+  op.right_leaf = best.right_w * p.eta;
+  return op;
+}
+
+// Select and partition of one level in one launch.  The last workgroup does
+// the level's bookkeeping (select_level: tree records, the next frontier, and
+// with unit Hessians the next level's plan); every other workgroup takes
+// partition tiles of up to kPartTile rows of one node, works out that node's
+// split itself (node_op), and moves its rows: a split node's left rows fill
+// its segment upwards from the start and its right rows downwards from the
+// end, each tile claiming its ranges with one atomic on each of the node's
+// two cursors and writing ranks (chunk, wave, lane) into them.  The order of
+// rows inside a child depends on which tile claims first; nothing downstream
+// depends on it (histograms are exact integer sums and the margin update is
+// per row).  Rows of nodes that stop here get their leaf added to the
+// training margin.
 template <typename BinT, bool IDENTITY>
-__global__ __launch_bounds__(kPartThreads) void k_partition(Tree t, uint32_t depth) {
+__global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) {
+  extern __shared__ __align__(16) uint8_t apply_stage[];  // dense-root staging (depth 0 only)
+  if (blockIdx.x == gridDim.x - 1) {
+    select_level(t, depth, apply_stage);
+    return;
+  }
   constexpr uint32_t kWaves = kPartThreads / kWave;
   __shared__ uint32_t wave_left[kPartPer][kWaves], wave_active[kPartPer][kWaves];
   __shared__ uint32_t base_left, base_right;
+  __shared__ NodeOp s_op;
   const LevelState* st = t.state;
-  const uint32_t ntasks = st->n_part_tasks;
+  const uint32_t ntasks = st->n_part[depth & 1];
+  const PartTask* tasks = part_bank(t, depth);
+  uint32_t* cursors = cursor_bank(t, depth);
   const uint32_t* rows = t.rows[depth & 1];
   uint32_t* out = t.rows[(depth + 1) & 1];
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
-    const PartTask task = t.part_tasks[w];
-    const NodeOp op = t.ops[task.slot];
-    if (op.op != kOpLeaf && op.op != kOpFinal && op.op != kOpSplit) continue;
+  uint32_t op_slot = 0xffffffffu;
+  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x - 1) {
+    const PartTask task = tasks[w];
+    if (task.slot != op_slot) {  // uniform: every thread read the same task
+      __syncthreads();
+      if (threadIdx.x == 0) s_op = node_op(t, depth, task.slot);
+      __syncthreads();
+      op_slot = task.slot;
+    }
+    const NodeOp op = s_op;
     uint32_t row[kPartPer];
     bool active[kPartPer];
     load_tile_rows<IDENTITY>(rows, task, row, active);
@@ -1549,8 +1697,8 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(Tree t, uint32_t dep
       uint32_t tl = 0, ta = 0;
       for (int k = 0; k < kPartPer; ++k)
         for (uint32_t q = 0; q < kWaves; ++q) { tl += wave_left[k][q]; ta += wave_active[k][q]; }
-      base_left = atomicAdd(&t.cursors[2 * task.slot], tl);
-      base_right = atomicSub(&t.cursors[2 * task.slot + 1], ta - tl) - (ta - tl);
+      base_left = atomicAdd(&cursors[2 * task.slot], tl);
+      base_right = atomicSub(&cursors[2 * task.slot + 1], ta - tl) - (ta - tl);
     }
     __syncthreads();
     uint32_t done_left = 0, done_active = 0;  // rows of earlier chunks
@@ -1577,7 +1725,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(Tree t, uint32_t dep
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, recs, best, ops, hist_tasks, zero, part_tasks, cursors, partials, total;
+  size_t state, rows, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, partials, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -1598,10 +1746,9 @@ Layout layout(const MgbTreeShape& s) {
   L.frontier = off; off = align_up(off + 2 * (size_t)(2 * L.slots) * sizeof(Frontier));
   L.recs = off; off = align_up(off + (size_t)(2 * L.slots) * s.cols * sizeof(SplitRec));
   L.best = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint64_t));
-  L.ops = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(NodeOp));
   L.hist_tasks = off; off = align_up(off + (size_t)L.max_hist_tasks * sizeof(HistTask));
   L.zero = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint32_t));
-  L.part_tasks = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(PartTask));
+  L.part_tasks = off; off = align_up(off + 2 * (size_t)L.max_part_tasks * sizeof(PartTask));
   L.cursors = off; off = align_up(off + (size_t)(2 * 2 * L.slots) * sizeof(uint32_t));
   {
     // Per-tile partial histograms of multi-tile nodes (dense path only: the
@@ -1688,13 +1835,18 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
   return 0;
 }
 
+// Select + partition of a level: `grid` partition workgroups plus the
+// bookkeeping workgroup; the dense root stages two features in LDS.
 template <typename BinT>
-int launch_partition(const Tree& t, uint32_t depth, uint32_t grid) {
-  if (depth == 0)
-    launch(MGB_PROF_PARTITION, k_partition<BinT, true>, dim3(grid), dim3(kPartThreads), 0, t, depth);
-  else
-    launch(MGB_PROF_PARTITION, k_partition<BinT, false>, dim3(grid), dim3(kPartThreads), 0, t, depth);
-  MGB_LAUNCH_CHECK("k_partition");
+int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
+  const uint32_t lds = depth == 0 && t.dense ? (uint32_t)kRootStageBytes : 0u;
+  auto fn = depth == 0 ? k_apply<BinT, true> : k_apply<BinT, false>;
+  if (lds && hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+    set_error("hipFuncSetAttribute(select LDS) failed");
+    return -1;
+  }
+  launch(MGB_PROF_PARTITION, fn, dim3(grid + 1), dim3(kPartThreads), lds, t, depth);
+  MGB_LAUNCH_CHECK("k_apply");
   return 0;
 }
 
@@ -1739,7 +1891,6 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.frontier[1] = fr + 2 * L.slots;
   t.recs = reinterpret_cast<SplitRec*>(ws + L.recs);
   t.best = reinterpret_cast<unsigned long long*>(ws + L.best);
-  t.ops = reinterpret_cast<NodeOp*>(ws + L.ops);
   t.hist_tasks = reinterpret_cast<HistTask*>(ws + L.hist_tasks);
   t.zero_list = reinterpret_cast<uint32_t*>(ws + L.zero);
   t.part_tasks = reinterpret_cast<PartTask*>(ws + L.part_tasks);
@@ -1754,6 +1905,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.features_per_group = s->features_per_group;
   t.groups = div_up(s->cols, s->features_per_group);
   t.unit_hessian = s->unit_hessian; t.dense = s->dense; t.max_hist_tasks = L.max_hist_tasks;
+  t.max_part_tasks = L.max_part_tasks;
   t.column_levels = s->column_levels;
   t.sparse = s->sparse;
   t.hist_entry = L.hist_entry;
@@ -1827,7 +1979,7 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   t.allowed = features;
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
-  // Unit Hessians: k_select plans each next level (child counts are known
+  // Unit Hessians: the select bookkeeping plans each next level (child counts are known
   // from the count histograms), so k_plan is not launched.
   t.select_plans = t.unit_hessian ? 1u : 0u;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
@@ -1842,9 +1994,7 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
     if (launch_split(t, depth, items)) return -1;
-    launch(MGB_PROF_CONTROL, k_select, dim3(1), dim3(kSelectThreads), 0, t, depth);
-    MGB_LAUNCH_CHECK("k_select");
-    if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
+    if ((m->bin_bytes == 1 ? launch_apply<uint8_t>(t, depth, pgrid) : launch_apply<uint16_t>(t, depth, pgrid)))
       return -1;
   }
   return 0;
@@ -1934,10 +2084,8 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
     uint32_t max_nodes = 1u << depth;
     uint32_t items = depth == 0 ? shape->cols : (max_nodes / 2) * shape->cols;
     if (launch_split(t, depth, items)) return -1;
-    launch(MGB_PROF_CONTROL, k_select, dim3(1), dim3(kSelectThreads), 0, t, depth);
-    MGB_LAUNCH_CHECK("k_select");
     const uint32_t pgrid = level_part_grid(t, depth);
-    if ((m->bin_bytes == 1 ? launch_partition<uint8_t>(t, depth, pgrid) : launch_partition<uint16_t>(t, depth, pgrid)))
+    if ((m->bin_bytes == 1 ? launch_apply<uint8_t>(t, depth, pgrid) : launch_apply<uint16_t>(t, depth, pgrid)))
       return -1;
   }
   return 0;
