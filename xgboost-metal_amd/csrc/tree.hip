@@ -873,19 +873,6 @@ __device__ __forceinline__ void bound_bin(const NodeEval& n, uint64_t vg, uint64
   }
 }
 
-// Exact scoring of the candidates whose upper bound reaches the node's best
-// lower bound.
-__device__ __forceinline__ void eval_bin_bounded(NodeEval& n, uint64_t vg, uint64_t vh, uint64_t lg, uint64_t lh,
-                                                 uint32_t b, uint32_t count, int eg, int eh, float mcw,
-                                                 const MgbSplitParams& p, float hi_f, float hi_b, float node_lo) {
-  if (b >= count) return;
-  if (hi_f > -INFINITY && hi_f >= node_lo) try_candidate(n, lg, lh, b, eg, eh, mcw, p);
-  if (n.has_missing && hi_b > -INFINITY && hi_b >= node_lo) {
-    const uint64_t rg = n.pg - (lg - vg), rh = n.ph - (lh - vh);
-    try_candidate(n, n.tg - rg, n.th - rh, 2 * count - 1 - b, eg, eh, mcw, p);
-  }
-}
-
 __device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll
   for (int d = kWave / 2; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, kWave));
@@ -1077,11 +1064,38 @@ __device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, 
               hi_b[j], lo);
   }
   const float node_lo = item_max_f32<W>(lo, xf, wave_in_item);
+  // The candidates whose upper bound reaches the node's best lower bound, as
+  // a mask (bit 2j: bin j forward, 2j+1: backward), scored exactly one at a
+  // time.  One inlined copy of the binary64 scorer instead of one per bin and
+  // direction keeps the kernel's code within the instruction cache; the
+  // scorer keeps the best by (gain, lowest order), so the visiting order does
+  // not matter.
+  uint32_t mask = 0;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
-    const uint64_t vg = lb.g[j] - (j ? lb.g[j - 1] : 0), vh = lb.h[j] - (j ? lb.h[j - 1] : 0);
-    eval_bin_bounded(n, vg, vh, pre_g + lb.g[j], pre_h + lb.h[j], b0 + j, count, eg, eh, mcw, p, hi_f[j], hi_b[j],
-                     node_lo);
+    if (b0 + j >= count) continue;
+    if (hi_f[j] > -INFINITY && hi_f[j] >= node_lo) mask |= 1u << (2 * j);
+    if (n.has_missing && hi_b[j] > -INFINITY && hi_b[j] >= node_lo) mask |= 2u << (2 * j);
+  }
+  while (mask) {
+    const uint32_t k = (uint32_t)__builtin_ctz(mask);
+    mask &= mask - 1;
+    const uint32_t j = k >> 1;
+    uint64_t ig = lb.g[0], ih = lb.h[0], xg = 0, xh = 0;  // inclusive / exclusive in-lane prefixes
+#pragma unroll
+    for (int q = 1; q < CH; ++q) {
+      if ((uint32_t)q == j) {
+        ig = lb.g[q]; ih = lb.h[q];
+        xg = lb.g[q - 1]; xh = lb.h[q - 1];
+      }
+    }
+    const uint32_t b = b0 + j;
+    const bool backward = (k & 1) != 0;
+    // Backward (missing values go left): the left child is everything but the
+    // present rows at or above bin b.
+    const uint64_t lg = backward ? n.tg - (n.pg - (pre_g + xg)) : pre_g + ig;
+    const uint64_t lh = backward ? n.th - (n.ph - (pre_h + xh)) : pre_h + ih;
+    try_candidate(n, lg, lh, backward ? 2 * count - 1 - b : b, eg, eh, mcw, p);
   }
   const uint64_t mine = candidate_key(n);
   const uint64_t top = item_max_u64<W>(mine, xk, wave_in_item);
