@@ -114,7 +114,13 @@ typedef struct {
    * every row in order, so longer tiles cost no locality and leave fewer
    * per-tile partial histograms for the split kernel to sum. */
   uint32_t root_rows_per_tile;
-  uint32_t padding;
+  /* 1: rows whose quantized gradient pair is (0, 0) -- the rows a subsample
+   * drops -- leave the tree's row list before the root
+   * (kernels/tree_sample_columns.metal.h:4-31 tree_rows_compact_sampled):
+   * histograms and partitions see only the kept rows, and the dropped rows
+   * get their leaf added to the margin by a walk of the finished tree.
+   * mgb_grow_tree only (0 for the CSR driver). */
+  uint32_t compact_sampled;
 } MgbTreeShape;
 
 /* ---- data: quantile cuts and bin matrix ------------------------------- */

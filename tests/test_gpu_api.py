@@ -148,3 +148,27 @@ def test_queued_rounds_equal_drained_rounds(xgb):
     for i in range(5):
         profiled.update(d, i)
     assert _trees(profiled) == _trees(stepwise[:5])
+
+
+@pytest.mark.parametrize("max_bin,missing", [(64, False), (1000, True)])
+def test_compacted_sampled_rows_equal_full_row_list(xgb, max_bin, missing):
+    """A subsample's dropped rows leave the row list before the root and get
+    their leaves from a walk of the finished tree: the trees and the training
+    margins (the cached margins the next round's gradients read) equal those
+    of the full row list, u8 and u16 codes, with and without missing values."""
+    rng = np.random.default_rng(max_bin)
+    X = rng.normal(size=(30000, 12)).astype(np.float32)
+    if missing:
+        X[rng.random(X.shape) < 0.1] = np.nan
+    y = (np.nan_to_num(X[:, 0]) + 0.3 * rng.normal(size=30000) > 0).astype(np.float32)
+    d = xgb.DMatrix(X, label=y)
+    params = {"objective": "binary:logistic", "max_depth": 6, "max_bin": max_bin, "subsample": 0.6,
+              "colsample_bytree": 0.8, "seed": 11}
+    compact = xgb.train(params, d, 6)
+    full = xgb.train(dict(params, hip_compact_sampled=0), d, 6)
+    assert _trees(compact) == _trees(full)
+    # The training margins: the cache of the training matrix against a fresh
+    # prediction of the same rows.
+    fresh = xgb.DMatrix(X)
+    for bst in (compact, full):
+        np.testing.assert_array_equal(bst.predict(d, output_margin=True), bst.predict(fresh, output_margin=True))

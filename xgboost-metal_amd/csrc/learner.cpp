@@ -590,7 +590,7 @@ const uint32_t* Learner::sample_columns(uint32_t cols) {
   return d_features_.as<uint32_t>();
 }
 
-void Learner::grow(DMatrix& data, bool unit_hessian) {
+void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
   const uint32_t depth = (uint32_t)integer("max_depth", 6);
   MgbTreeShape shape{};
   shape.rows = data.rows;
@@ -605,6 +605,9 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
   shape.rows_per_tile = (uint32_t)integer("hip_histogram_rows", tile);
   shape.features_per_group = data.features_per_group;
   shape.unit_hessian = unit_hessian ? 1 : 0;
+  // A subsample's dropped rows (zero gradients) leave the row list before the
+  // root; a walk of the finished tree adds their leaves to the margin.
+  shape.compact_sampled = sampled && integer("hip_compact_sampled", 1) != 0 ? 1 : 0;
   {
     // Root tiles: the root streams every row in order, so a workgroup can take
     // a long tile (its batches software-pipelined) at no cost in locality.
@@ -633,6 +636,7 @@ void Learner::grow(DMatrix& data, bool unit_hessian) {
     // CSR: row tiles are only work units (every tile adds into the node's
     // histogram), so small tiles spread a level over many workgroups.
     shape.sparse = 1;
+    shape.compact_sampled = 0;
     shape.column_levels = 0;
     shape.rows_per_tile = (uint32_t)integer("hip_histogram_rows", 512);
     shape.root_rows_per_tile = 0;
@@ -760,7 +764,7 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
          "gradients");
   // Unit Hessians (every h = 1, so a row count stands in for the Hessian
   // sum) hold for unweighted squared error unless sampling zeroed some rows.
-  grow(data, obj == 0 && data.weights.empty() && gp.subsample >= 1.0f);
+  grow(data, obj == 0 && data.weights.empty() && gp.subsample >= 1.0f, gp.subsample < 1.0f);
   seconds_["train_rounds"] += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   seconds_["quantiles"] = data.sketch_seconds;
   seconds_["bin_matrix"] = data.quantize_seconds;
@@ -785,7 +789,7 @@ void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t 
   sample_rows(data, gp);
   kcheck(mgb_gradient_mass(&gp, d_grad_.as<float>(), d_mass_.as<uint64_t>(), d_scales_.as<float>()),
          "gradient mass");
-  grow(data, false);
+  grow(data, false, gp.subsample < 1.0f);
 }
 
 const float* Learner::predict_device(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end,

@@ -163,7 +163,8 @@ class Learner {
   std::string objective_name() const;
   void configure_check() const;
   void initialize(DMatrix& data, bool custom);
-  void grow(DMatrix& data, bool unit_hessian);
+  // sampled: the round's gradients drop rows (subsample < 1), which leave the row list.
+  void grow(DMatrix& data, bool unit_hessian, bool sampled);
   void configure_rng();
   int bin_layout() const;
   // Per-round row-sampling parameters (src/learner.cpp:679, src/sampling.cpp:11-17).

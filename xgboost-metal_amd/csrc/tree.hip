@@ -10,6 +10,7 @@
 // dispatch for the same purpose).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -36,7 +37,9 @@ struct LevelState {
                           // apply kernel of one level plans the next while it runs)
   uint32_t node_count;    // tree nodes allocated so far
   uint32_t error;
-  uint32_t padding[9];
+  uint32_t kept, dropped;  // row compaction: rows kept (row list [0, kept)) and dropped
+                           // (stored from the end of the list down)
+  uint32_t padding[7];
   // Per level: rows and nodes whose histograms were built directly.
   uint64_t rows_built[kMaxLevels];
   uint32_t nodes_built[kMaxLevels];
@@ -121,6 +124,7 @@ struct Tree {
   const float* scales;
   float* margin;
   MgbTreeNode* nodes;
+  int32_t* split_bins;        // per tree node id: the split's last left bin (the walk of dropped rows)
   uint32_t* node_count_out;
   // Shape.
   uint32_t rows_n, cols, max_bin, bins1;     // bins1 = max_bin + 1
@@ -132,6 +136,7 @@ struct Tree {
   uint32_t column_levels;                    // histogram levels that read `columns`
   uint32_t select_plans;                     // unit Hessians, dense: the select bookkeeping plans the next level
   uint32_t sparse;                           // CSR: missing slots from node totals, no partials
+  uint32_t compact;                          // the root's rows are the kept rows of a subsample
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
@@ -216,23 +221,25 @@ __device__ __forceinline__ float calc_gain(double G, double H, float w, const Mg
 // ---------------------------------------------------------------------------
 __global__ void k_level0(Tree t) {
   LevelState* st = t.state;
-  uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.root_tile) : 0;
+  // The root's rows: [0, N), or the kept rows k_compact_rows listed.
+  const uint32_t n_root = t.compact ? st->kept : t.rows_n;
+  uint32_t tiles = n_root ? div_up(n_root, t.root_tile) : 0;
   if (t.best)
     for (uint32_t i = threadIdx.x; i < 2 * t.slots; i += blockDim.x) t.best[i] = 0;
   for (uint32_t i = threadIdx.x; i < tiles; i += blockDim.x) {
     uint32_t begin = i * t.root_tile;
-    uint32_t end = begin + t.root_tile < t.rows_n ? begin + t.root_tile : t.rows_n;
+    uint32_t end = begin + t.root_tile < n_root ? begin + t.root_tile : n_root;
     t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
   }
-  // The root's partition tasks (row tiles of [0, N)) and cursors.
-  const uint32_t ptiles = t.rows_n ? div_up(t.rows_n, kPartTile) : 0;
+  // The root's partition tasks (row tiles of [0, n_root)) and cursors.
+  const uint32_t ptiles = n_root ? div_up(n_root, kPartTile) : 0;
   if (t.part_tasks)
     for (uint32_t i = threadIdx.x; i < ptiles; i += blockDim.x) {
       const uint32_t b = i * kPartTile;
-      t.part_tasks[i] = PartTask{0u, b, b + kPartTile < t.rows_n ? b + kPartTile : t.rows_n, 0u};
+      t.part_tasks[i] = PartTask{0u, b, b + kPartTile < n_root ? b + kPartTile : n_root, 0u};
     }
   if (threadIdx.x == 0) {
-    st->rows_built[0] = t.rows_n;
+    st->rows_built[0] = n_root;
     st->nodes_built[0] = 1;
     st->n_nodes = 1;
     st->n_hist_tasks = tiles;
@@ -240,18 +247,99 @@ __global__ void k_level0(Tree t) {
     st->n_part[0] = ptiles;
     st->n_part[1] = 0;
     t.cursors[0] = 0;
-    t.cursors[1] = t.rows_n;
+    t.cursors[1] = n_root;
     st->node_count = 1;
     st->error = 0;
     t.zero_list[0] = 0;
     Frontier root;
-    root.id = 0; root.begin = 0; root.count = t.rows_n; root.parent_slot = 0;
+    root.id = 0; root.begin = 0; root.count = n_root; root.parent_slot = 0;
     root.sum_g = 0; root.sum_h = 0; root.built = 1; root.first_task = 0; root.ntiles = tiles; root.leaf = 0.0f;
     t.frontier[0][0] = root;
     MgbTreeNode n;
     n.left = -1; n.right = -1; n.parent = -1; n.feature = -1;
     n.threshold = 0; n.leaf = 0; n.cover = 0; n.gain = 0; n.default_left = 0; n.base_weight = 0;
     if (t.nodes) t.nodes[0] = n;  // the histogram-only entry point has no tree
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sampled-row compaction (kernels/tree_sample_columns.metal.h:4-31
+// tree_rows_compact_sampled, launched at src/tree.cpp:746-750): a row stays
+// in the tree's row list iff its quantized gradient pair is not (0, 0), the
+// rows a subsample drops having zero gradients.  Kept rows fill the list
+// from the front, dropped rows from the back; each workgroup claims its two
+// ranges with one atomic on each counter, so the order of rows within each
+// range depends on scheduling -- nothing downstream depends on it (the
+// histograms are exact integer sums, the margin update is per row).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kCompactThreads = 256;
+constexpr uint32_t kCompactChunks = 64;  // chunks of kCompactThreads rows per workgroup
+constexpr uint32_t kCompactRows = kCompactThreads * kCompactChunks;
+
+__global__ void k_compact_reset(Tree t) {
+  if (threadIdx.x == 0) {
+    t.state->kept = 0;
+    t.state->dropped = 0;
+  }
+}
+
+// One workgroup per kCompactRows consecutive rows, in two passes: the keep
+// bits of every (chunk, wave) go to LDS as ballot masks and are counted, the
+// workgroup claims its ranges with one atomic per counter (few workgroups, so
+// little contention on the two counters), then every row's rank comes from
+// the masks.
+__global__ __launch_bounds__(kCompactThreads) void k_compact_rows(Tree t) {
+  constexpr uint32_t kWaves = kCompactThreads / kWave;
+  __shared__ uint64_t masks[kCompactChunks][kWaves];
+  __shared__ uint32_t wave_count[kWaves];
+  __shared__ uint32_t base_kept, base_dropped;
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  const float sg = t.scales[0], sh = t.scales[1];
+  const uint32_t first = blockIdx.x * kCompactRows;
+  const uint32_t rows = (t.rows_n - first < kCompactRows ? t.rows_n - first : kCompactRows);  // grid: first < N
+  uint32_t kept = 0;
+  for (uint32_t c = 0; c < kCompactChunks; ++c) {
+    const uint32_t i = c * kCompactThreads + threadIdx.x;
+    bool keep = false;
+    if (i < rows) {
+      const float2 v = t.grad[first + i];
+      keep = (int64_t)rintf(v.x * sg) != 0 || (int64_t)rintf(v.y * sh) != 0;
+    }
+    const uint64_t m = __ballot(keep);
+    if (lane == 0) masks[c][wave] = m;
+    kept += (uint32_t)__popcll(m);  // uniform over the wave
+  }
+  if (lane == 0) wave_count[wave] = kept;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t total = 0;
+    for (uint32_t q = 0; q < kWaves; ++q) total += wave_count[q];
+    base_kept = total ? atomicAdd(&t.state->kept, total) : 0u;
+    base_dropped = rows > total ? atomicAdd(&t.state->dropped, rows - total) : 0u;
+  }
+  __syncthreads();
+  uint32_t done_kept = 0;  // kept rows of earlier chunks
+  for (uint32_t c = 0; c < kCompactChunks; ++c) {
+    const uint32_t i = c * kCompactThreads + threadIdx.x;
+    uint32_t wk = 0, ck = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kWaves; ++q) {
+      const uint32_t n = (uint32_t)__popcll(masks[c][q]);
+      if (q < wave) wk += n;
+      ck += n;
+    }
+    if (i < rows) {
+      const uint64_t m = masks[c][wave];
+      const uint32_t rank = (uint32_t)__popcll(m & below);
+      // Rows before this one in the workgroup's range: i (all of them are
+      // present, the range being consecutive rows); kept among them:
+      // done_kept + wk + rank.
+      const uint32_t kept_before = done_kept + wk + rank;
+      if ((m >> lane) & 1u) t.rows[0][base_kept + kept_before] = first + i;
+      else t.rows[0][t.rows_n - 1 - (base_dropped + (i - kept_before))] = first + i;
+    }
+    done_kept += ck;
   }
 }
 
@@ -1431,6 +1519,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
         rec->gain = best.gain;
         rec->base_weight = applied_w;
         rec->cover = applied_h;
+        t.split_bins[node.id] = best.default_left ? (int32_t)best.bin - 1 : (int32_t)best.bin;
         MgbTreeNode l, r;
         l.left = l.right = -1; l.parent = node.id; l.feature = -1; l.threshold = 0;
         l.leaf = best.left_w * p.eta; l.cover = best.left_h; l.gain = 0; l.default_left = 0; l.base_weight = l.leaf;
@@ -1735,11 +1824,57 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   }
 }
 
+// Margin update of the rows a compaction dropped (stored at the end of the
+// row list): each walks the finished tree from the root on its codes, the
+// partition's test at every split (goes_left with the split's last left bin),
+// and adds its leaf's value -- the value the partition adds to the rows it
+// moves (kernels/boost.metal:1738-1763).  kWalkPer rows per thread walk
+// side by side, so their dependent loads overlap.
+constexpr int kWalkPer = 4;
+template <typename BinT>
+__global__ __launch_bounds__(kCompactThreads) void k_walk_dropped(Tree t) {
+  const uint32_t dropped = t.state->dropped;
+  const MgbTreeNode* nodes = t.nodes;
+  constexpr uint32_t kStep = kCompactThreads * kWalkPer;
+  for (uint32_t base = blockIdx.x * kStep; base < dropped; base += gridDim.x * kStep) {
+    uint32_t row[kWalkPer];
+    int32_t at[kWalkPer];
+    bool active[kWalkPer];
+#pragma unroll
+    for (int k = 0; k < kWalkPer; ++k) {
+      const uint32_t j = base + k * kCompactThreads + threadIdx.x;
+      active[k] = j < dropped;
+      row[k] = active[k] ? t.rows[0][t.rows_n - 1 - j] : 0u;
+      at[k] = 0;
+    }
+    // A tree of depth max_depth reaches a leaf in at most max_depth steps.
+    for (uint32_t d = 0; d < t.max_depth; ++d) {
+#pragma unroll
+      for (int k = 0; k < kWalkPer; ++k) {
+        if (!active[k]) continue;
+        const MgbTreeNode n = nodes[at[k]];
+        if (n.left < 0) continue;
+        NodeOp op;
+        op.op = kOpSplit;
+        op.feature = (uint32_t)n.feature;
+        op.last_left_bin = t.split_bins[at[k]];
+        op.default_left = n.default_left;
+        op.leaf = op.left_leaf = op.right_leaf = 0.0f;
+        op.child_slot = 0;
+        at[k] = goes_left<BinT>(t, op, row[k]) ? n.left : n.right;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kWalkPer; ++k)
+      if (active[k]) t.margin[row[k]] = t.margin[row[k]] + nodes[at[k]].leaf;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, partials, total;
+  size_t state, rows, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, split_bins, partials, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -1764,6 +1899,7 @@ Layout layout(const MgbTreeShape& s) {
   L.zero = off; off = align_up(off + (size_t)(2 * L.slots) * sizeof(uint32_t));
   L.part_tasks = off; off = align_up(off + 2 * (size_t)L.max_part_tasks * sizeof(PartTask));
   L.cursors = off; off = align_up(off + (size_t)(2 * 2 * L.slots) * sizeof(uint32_t));
+  L.split_bins = off; off = align_up(off + ((size_t)2 << depth) * sizeof(int32_t));
   {
     // Per-tile partial histograms of multi-tile nodes (dense path only: the
     // CSR histogram adds every tile into the node's own row).
@@ -1779,7 +1915,7 @@ Layout layout(const MgbTreeShape& s) {
 template <typename BinT, int G>
 int launch_hist(const Tree& t, uint32_t depth, bool unit, uint32_t grid) {
   size_t lds = (size_t)G * t.bins1 * (8 + (unit ? 4 : 8));
-  bool identity = depth == 0;
+  bool identity = depth == 0 && !t.compact;  // the root's rows are [0, N) unless compacted
   const bool cols = t.columns != nullptr && depth < t.column_levels;
 #define MGB_HIST_CASE(U, I)                                                                           \
   {                                                                                                   \
@@ -1854,7 +1990,7 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
 template <typename BinT>
 int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
   const uint32_t lds = depth == 0 && t.dense ? (uint32_t)kRootStageBytes : 0u;
-  auto fn = depth == 0 ? k_apply<BinT, true> : k_apply<BinT, false>;
+  auto fn = depth == 0 && !t.compact ? k_apply<BinT, true> : k_apply<BinT, false>;
   if (lds && hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
     set_error("hipFuncSetAttribute(select LDS) failed");
     return -1;
@@ -1909,6 +2045,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.zero_list = reinterpret_cast<uint32_t*>(ws + L.zero);
   t.part_tasks = reinterpret_cast<PartTask*>(ws + L.part_tasks);
   t.cursors = reinterpret_cast<uint32_t*>(ws + L.cursors);
+  t.split_bins = reinterpret_cast<int32_t*>(ws + L.split_bins);
   t.partials = reinterpret_cast<int64_t*>(ws + L.partials);
   t.rows_n = s->rows; t.cols = s->cols; t.max_bin = m->max_bin; t.bins1 = m->max_bin + 1;
   t.row_stride = m->row_stride; t.bin_bytes = m->bin_bytes; t.missing_code = m->missing_code;
@@ -1922,6 +2059,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.max_part_tasks = L.max_part_tasks;
   t.column_levels = s->column_levels;
   t.sparse = s->sparse;
+  t.compact = s->compact_sampled && !s->sparse ? 1u : 0u;
   t.hist_entry = L.hist_entry;
   return t;
 }
@@ -1991,6 +2129,14 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   t.bins = bins; t.columns = columns; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
   t.allowed = features;
+  if (t.compact) {
+    launch(MGB_PROF_CONTROL, k_compact_reset, dim3(1), dim3(64), 0, t);
+    MGB_LAUNCH_CHECK("k_compact_reset");
+    if (t.rows_n) {
+      launch(MGB_PROF_CONTROL, k_compact_rows, dim3(div_up(t.rows_n, kCompactRows)), dim3(kCompactThreads), 0, t);
+      MGB_LAUNCH_CHECK("k_compact_rows");
+    }
+  }
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
   // Unit Hessians: the select bookkeeping plans each next level (child counts are known
@@ -2010,6 +2156,15 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
     if (launch_split(t, depth, items)) return -1;
     if ((m->bin_bytes == 1 ? launch_apply<uint8_t>(t, depth, pgrid) : launch_apply<uint16_t>(t, depth, pgrid)))
       return -1;
+  }
+  if (t.compact) {
+    // Dropped rows: at most N, kWalkPer per thread; the kernel strides over
+    // the device's count, so a bounded grid covers any number.
+    const uint32_t per_block = kCompactThreads * kWalkPer;
+    const uint32_t wgrid = t.rows_n ? std::min<uint32_t>(div_up(t.rows_n, per_block), 4096) : 1;
+    if (m->bin_bytes == 1) launch(MGB_PROF_PARTITION, k_walk_dropped<uint8_t>, dim3(wgrid), dim3(kCompactThreads), 0, t);
+    else launch(MGB_PROF_PARTITION, k_walk_dropped<uint16_t>, dim3(wgrid), dim3(kCompactThreads), 0, t);
+    MGB_LAUNCH_CHECK("k_walk_dropped");
   }
   return 0;
 }
