@@ -1746,7 +1746,6 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   constexpr uint32_t kWaves = kPartThreads / kWave;
   __shared__ uint32_t wave_left[kPartPer][kWaves], wave_active[kPartPer][kWaves];
   __shared__ uint32_t base_left, base_right;
-  __shared__ NodeOp s_op;
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part[depth & 1];
   const PartTask* tasks = part_bank(t, depth);
@@ -1756,18 +1755,19 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   uint32_t op_slot = 0xffffffffu;
+  NodeOp op;
   for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x - 1) {
     const PartTask task = tasks[w];
-    if (task.slot != op_slot) {  // uniform: every thread read the same task
-      __syncthreads();
-      if (threadIdx.x == 0) s_op = node_op(t, depth, task.slot);
-      __syncthreads();
-      op_slot = task.slot;
-    }
-    const NodeOp op = s_op;
+    // The tile's row ids are requested first; every thread then rebuilds the
+    // node's split itself (uniform loads, no barrier), so the two chains of
+    // loads overlap.
     uint32_t row[kPartPer];
     bool active[kPartPer];
     load_tile_rows<IDENTITY>(rows, task, row, active);
+    if (task.slot != op_slot) {  // uniform: every thread read the same task
+      op = node_op(t, depth, task.slot);
+      op_slot = task.slot;
+    }
     if (op.op == kOpLeaf) {
 #pragma unroll
       for (int k = 0; k < kPartPer; ++k)
