@@ -171,14 +171,19 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
  * synchronised; nodes (2^(max_depth+1)-1 records) and node_count are device
  * pointers filled by the time the stream drains.  features (device, cols
  * flags, may be NULL for all) restricts the split search to the tree's
- * column sample (src/tree.cpp:179-180).  columns (device, may be NULL) holds
+ * column sample (src/tree.cpp:179-180).  monotone (device, cols int32 of -1, 0
+ * or 1, may be NULL for none) applies monotone constraints
+ * (src/tree.cpp:15-26, :1083-1086; kernels/boost.metal:902-920): each node
+ * carries bounds on its weight, every weight is clamped to them, a split on an
+ * increasing (decreasing) feature needs left weight <= (>=) right weight,
+ * and the children's bounds meet at the midpoint of their weights.  columns (device, may be NULL) holds
  * the same codes column-major, code(row, f) at columns + (f * rows + row) *
  * bin_bytes: the row partition then reads its split feature's codes from one
  * column instead of one cache line of the row-major matrix per row. */
 int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const void* columns, const float* cuts,
                   const uint32_t* counts, const float* grad, const float* scales, const MgbSplitParams* sp,
-                  const uint32_t* features, void* workspace, size_t workspace_bytes, float* margin,
-                  MgbTreeNode* nodes, uint32_t* node_count);
+                  const uint32_t* features, const int32_t* monotone, void* workspace, size_t workspace_bytes,
+                  float* margin, MgbTreeNode* nodes, uint32_t* node_count);
 
 /* ---- CSR input (src/data.cpp:721-870 Matrix::sparse) ----------------- *
  * indptr holds rows+1 offsets into indices/values; column indices are
@@ -212,13 +217,13 @@ int mgb_quantize_csr(const uint32_t* indices, const float* values, uint64_t nnz,
  * its histogram from the column-major codes instead (colptr, csc_rows as
  * from mgb_csr_to_csc, csc_codes its columns' codes): a few features per
  * workgroup in LDS and plain stores, no device atomics.  The shape must have
- * sparse = 1. */
+ * sparse = 1; features and monotone as for mgb_grow_tree. */
 int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const uint64_t* indptr,
                       const uint32_t* indices, const void* codes, const uint64_t* colptr, const uint32_t* csc_rows,
                       const void* csc_codes, const float* cuts, const uint32_t* counts,
                       const float* grad, const float* scales, const MgbSplitParams* sp, const uint32_t* features,
-                      void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
-                      uint32_t* node_count);
+                      const int32_t* monotone, void* workspace, size_t workspace_bytes, float* margin,
+                      MgbTreeNode* nodes, uint32_t* node_count);
 /* mgb_predict over a CSR matrix of raw values. */
 int mgb_predict_csr(const uint64_t* indptr, const uint32_t* indices, const float* values, uint32_t rows,
                     const MgbTreeNode* nodes, const uint32_t* tree_offsets, uint32_t trees, float* margin);

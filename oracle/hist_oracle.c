@@ -26,6 +26,7 @@
  */
 #include "hist_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -481,18 +482,30 @@ float oracle_gain(double G, double H, float w, const OracleParams* p) {
   return (float)(-sum);
 }
 
+/* kernels/scalar_gain.metal.h:79-80, split_statistics.metal.h:35-36: the
+ * weight clamped to the node's monotone bounds [lower, upper]. */
+static float bounded_weight(double G, double H, const OracleParams* p, float lower, float upper) {
+  float w = oracle_weight(G, H, p);
+  if (w < lower) w = lower;
+  if (upper < w) w = upper;
+  return w;
+}
+
 static int valid_hessian(double H, float min_child_weight) {
   return H > 0 && H >= (double)fabsf(min_child_weight);
 }
 
-/* kernels/boost.metal:902-920 (consider_split). */
+/* kernels/boost.metal:902-920 (consider_split): child weights clamped to
+ * the node's bounds; a monotone feature rejects a split whose left weight is
+ * above (increasing) or below (decreasing) its right weight. */
 static void consider(OracleSplit* best, int64_t lg, int64_t lh, int64_t rg, int64_t rh, float sg, float sh,
                      float threshold, uint32_t default_left, int32_t feature, uint32_t bin, float parent_gain,
-                     const OracleParams* p) {
+                     const OracleParams* p, int monotone, float lower, float upper) {
   double GL = stat_value(lg, sg), HL = stat_value(lh, sh);
   double GR = stat_value(rg, sg), HR = stat_value(rh, sh);
   if (!valid_hessian(HL, p->min_child_weight) || !valid_hessian(HR, p->min_child_weight)) return;
-  float lw = oracle_weight(GL, HL, p), rw = oracle_weight(GR, HR, p);
+  float lw = bounded_weight(GL, HL, p, lower, upper), rw = bounded_weight(GR, HR, p, lower, upper);
+  if ((monotone > 0 && !(lw <= rw)) || (monotone < 0 && !(lw >= rw))) return;
   float gain = (oracle_gain(GL, HL, lw, p) + oracle_gain(GR, HR, rw, p)) - parent_gain;
   if (gain > best->gain) {
     best->gain = gain;
@@ -510,15 +523,16 @@ static void consider(OracleSplit* best, int64_t lg, int64_t lh, int64_t rg, int6
 }
 
 /* kernels/boost.metal:921-1005 (evaluate_feature), numeric features:
- * forward scan (missing right), then backward scan when missing != 0. */
-void oracle_evaluate_feature(const int64_t* fh, uint32_t count, const float* cuts, float minimum, int64_t total_g,
+ * forward scan (missing right), then backward scan when missing != 0; the
+ * node's weight and every child weight clamped to [lower, upper]. */
+static void evaluate_feature(const int64_t* fh, uint32_t count, const float* cuts, float minimum, int64_t total_g,
                              int64_t total_h, float scale_g, float scale_h, const OracleParams* p, int32_t feature,
-                             OracleSplit* out) {
+                             int monotone, float lower, float upper, OracleSplit* out) {
   uint64_t pg = 0, ph = 0;
   for (uint32_t b = 0; b < count; ++b) { pg += (uint64_t)fh[2 * b]; ph += (uint64_t)fh[2 * b + 1]; }
   int64_t miss_g = (int64_t)((uint64_t)total_g - pg), miss_h = (int64_t)((uint64_t)total_h - ph);
   double G = stat_value(total_g, scale_g), H = stat_value(total_h, scale_h);
-  float w = oracle_weight(G, H, p);
+  float w = bounded_weight(G, H, p, lower, upper);
   OracleSplit best;
   memset(&best, 0, sizeof(best));
   best.gain = -INFINITY;
@@ -533,7 +547,7 @@ void oracle_evaluate_feature(const int64_t* fh, uint32_t count, const float* cut
     lg += (uint64_t)fh[2 * b];
     lh += (uint64_t)fh[2 * b + 1];
     consider(&best, (int64_t)lg, (int64_t)lh, (int64_t)((uint64_t)total_g - lg), (int64_t)((uint64_t)total_h - lh),
-             scale_g, scale_h, cuts[b], 0, feature, b, parent_gain, p);
+             scale_g, scale_h, cuts[b], 0, feature, b, parent_gain, p, monotone, lower, upper);
   }
   if (miss_g != 0 || miss_h != 0) {
     uint64_t rg = 0, rh = 0;
@@ -542,10 +556,17 @@ void oracle_evaluate_feature(const int64_t* fh, uint32_t count, const float* cut
       rh += (uint64_t)fh[2 * b + 1];
       float threshold = b == 0 ? minimum : cuts[b - 1];
       consider(&best, (int64_t)((uint64_t)total_g - rg), (int64_t)((uint64_t)total_h - rh), (int64_t)rg, (int64_t)rh,
-               scale_g, scale_h, threshold, 1, feature, (uint32_t)b, parent_gain, p);
+               scale_g, scale_h, threshold, 1, feature, (uint32_t)b, parent_gain, p, monotone, lower, upper);
     }
   }
   *out = best;
+}
+
+void oracle_evaluate_feature(const int64_t* fh, uint32_t count, const float* cuts, float minimum, int64_t total_g,
+                             int64_t total_h, float scale_g, float scale_h, const OracleParams* p, int32_t feature,
+                             OracleSplit* out) {
+  evaluate_feature(fh, count, cuts, minimum, total_g, total_h, scale_g, scale_h, p, feature, 0, -FLT_MAX, FLT_MAX,
+                   out);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -557,6 +578,7 @@ uint32_t oracle_max_nodes(int32_t max_depth) { return (2u << (uint32_t)max_depth
 typedef struct {
   uint32_t id, begin, count;
   int64_t sum_g, sum_h;
+  float lower, upper;  /* monotone bounds of the node's weight (src/tree.cpp:1083-1086) */
 } Frontier;
 
 typedef struct {
@@ -621,6 +643,8 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
   uint32_t nf = 1;
   frontier[0].id = 0; frontier[0].begin = 0; frontier[0].count = q->rows;
   frontier[0].sum_g = frontier[0].sum_h = 0;
+  frontier[0].lower = -FLT_MAX;  /* kernels/tree_sample_columns.metal.h tree_init_bounds */
+  frontier[0].upper = FLT_MAX;
   for (int32_t depth = 0; nf > 0; ++depth) {
     uint32_t nn = 0;
     for (uint32_t k = 0; k < nf; ++k) {
@@ -642,8 +666,9 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
       memset(&best, 0, sizeof(best));
       for (uint32_t f = 0; f < q->cols; ++f) {
         OracleSplit cand;
-        oracle_evaluate_feature(hist + (size_t)f * stride, q->counts[f], q->cuts + (size_t)f * q->max_bin,
-                                q->minima[f], total_g, total_h, sg, sh, p, (int32_t)f, &cand);
+        evaluate_feature(hist + (size_t)f * stride, q->counts[f], q->cuts + (size_t)f * q->max_bin, q->minima[f],
+                         total_g, total_h, sg, sh, p, (int32_t)f, p->monotone ? p->monotone[f] : 0, fr->lower,
+                         fr->upper, &cand);
         if (allowed && !allowed[f]) {
           /* A feature outside the tree's sample offers no split. */
           cand.gain = -INFINITY;
@@ -657,7 +682,7 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
         uint32_t c0 = q->counts[0];
         double tg, th;
         ordered_sum(hist, 0, c0, 0, c0, sg, sh, &tg, &th);
-        parent_weight = oracle_weight(tg, th, p);
+        parent_weight = bounded_weight(tg, th, p, fr->lower, fr->upper);
         total_h_f = (float)th;
         if (best.feature >= 0) {
           uint32_t f = (uint32_t)best.feature, count = q->counts[f];
@@ -677,13 +702,13 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
           ordered_sum(hist + (size_t)f * stride, 0, steps, (int)best.default_left, count, sg, sh, &cg, &ch);
           double og = tg - cg, oh = th - ch;
           double ag = cg + og, ah = ch + oh;
-          applied_weight = oracle_weight(ag, ah, p);
+          applied_weight = bounded_weight(ag, ah, p, fr->lower, fr->upper);
           applied_hessian = (float)ah;
         }
       } else if (best.feature >= 0) {
         double ag = stat_value(best.left_g, sg) + stat_value(best.right_g, sg);
         double ah = stat_value(best.left_hs, sh) + stat_value(best.right_hs, sh);
-        applied_weight = oracle_weight(ag, ah, p);
+        applied_weight = bounded_weight(ag, ah, p, fr->lower, fr->upper);
         applied_hessian = (float)ah;
       }
       OracleNode* node = &nodes[id];
@@ -727,8 +752,20 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
         else tmp_buf[nr++] = row;
       }
       memcpy(row_buf + fr->begin + nl, tmp_buf, (size_t)nr * sizeof(uint32_t));
-      Frontier a = {left, fr->begin, nl, best.left_g, best.left_hs};
-      Frontier b = {right, fr->begin + nl, nr, best.right_g, best.right_hs};
+      /* Children's bounds (src/tree.cpp:1083-1086): the midpoint of the two
+       * child weights caps the left child from above and the right from below
+       * (increasing), or the reverse (decreasing); std::min/std::max order. */
+      Frontier a = {left, fr->begin, nl, best.left_g, best.left_hs, fr->lower, fr->upper};
+      Frontier b = {right, fr->begin + nl, nr, best.right_g, best.right_hs, fr->lower, fr->upper};
+      int mono = p->monotone ? p->monotone[f] : 0;
+      float middle = (best.left_weight + best.right_weight) * 0.5f;
+      if (mono > 0) {
+        if (middle < a.upper) a.upper = middle;
+        if (b.lower < middle) b.lower = middle;
+      } else if (mono < 0) {
+        if (a.lower < middle) a.lower = middle;
+        if (middle < b.upper) b.upper = middle;
+      }
       next[nn++] = a;
       next[nn++] = b;
     }

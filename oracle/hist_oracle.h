@@ -38,6 +38,7 @@ typedef struct {
   float subsample;           /* uniform row sampling when < 1 (src/sampling.cpp:11-74) */
   float colsample_bytree;    /* per-tree feature sampling when < 1 (src/tree.cpp:28-45) */
   uint32_t seed;             /* "seed" parameter; 0 keeps the engine's default state */
+  const int32_t* monotone;   /* per feature -1, 0 or 1 (monotone_constraints); NULL: none */
 } OracleParams;
 
 /* One tree node; field meanings follow the reference's Node plus base_weights

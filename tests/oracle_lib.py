@@ -20,7 +20,8 @@ class OracleParams(ctypes.Structure):
                 ("max_delta_step", ctypes.c_float), ("min_split_loss", ctypes.c_float),
                 ("scale_pos_weight", ctypes.c_float), ("base_score", ctypes.c_float),
                 ("has_base_score", ctypes.c_int32), ("nthread", ctypes.c_int32),
-                ("subsample", ctypes.c_float), ("colsample_bytree", ctypes.c_float), ("seed", ctypes.c_uint32)]
+                ("subsample", ctypes.c_float), ("colsample_bytree", ctypes.c_float), ("seed", ctypes.c_uint32),
+                ("monotone", ctypes.c_void_p)]
 
 
 NODE_DTYPE = np.dtype([("left", "<i4"), ("right", "<i4"), ("parent", "<i4"), ("feature", "<i4"),
@@ -62,11 +63,16 @@ def ptr(a):
 
 def make_params(objective="reg:squarederror", max_depth=6, max_bin=256, eta=0.3, reg_lambda=1.0, reg_alpha=0.0,
                 min_child_weight=1.0, max_delta_step=0.0, min_split_loss=0.0, scale_pos_weight=1.0,
-                base_score=None, fma_contract=1, nthread=0, subsample=1.0, colsample_bytree=1.0, seed=0):
-    return OracleParams(OBJECTIVES[objective], max_depth, max_bin, fma_contract, eta, reg_lambda, reg_alpha,
-                        min_child_weight, max_delta_step, min_split_loss, scale_pos_weight,
-                        0.0 if base_score is None else base_score, 0 if base_score is None else 1, nthread,
-                        subsample, colsample_bytree, seed)
+                base_score=None, fma_contract=1, nthread=0, subsample=1.0, colsample_bytree=1.0, seed=0,
+                monotone=None):
+    """monotone: one -1/0/1 per feature, or None."""
+    mono = None if monotone is None else np.ascontiguousarray(monotone, np.int32)
+    p = OracleParams(OBJECTIVES[objective], max_depth, max_bin, fma_contract, eta, reg_lambda, reg_alpha,
+                     min_child_weight, max_delta_step, min_split_loss, scale_pos_weight,
+                     0.0 if base_score is None else base_score, 0 if base_score is None else 1, nthread,
+                     subsample, colsample_bytree, seed, None if mono is None else mono.ctypes.data)
+    p._monotone = mono  # keeps the array alive while the parameters are
+    return p
 
 
 def sketch_cuts(X, max_bin, weights=None):

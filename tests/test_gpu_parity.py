@@ -454,3 +454,56 @@ def test_bin_layouts_give_identical_trees(xgb, layout, columns, column_levels, m
     ref = O.train(X, y, _oracle_params(params), 4)
     assert_trees_equal(bst, ref)
     np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["dense", "missing", "logistic", "csr", "sampled"])
+def test_monotone_constraints_match_oracle(xgb, case):
+    """Monotone constraints (src/tree.cpp:15-26, :1083-1086;
+    kernels/boost.metal:902-920): node weight bounds, clamped weights, the
+    left/right order on constrained features and the children's midpoint
+    bounds give trees and training margins bit-identical to the oracle's,
+    dense, with missing values, CSR and with row and column sampling, and to
+    rounding for logistic (the oracle is pinned by the monotonicity of its
+    predictions)."""
+    mono = [1, 0, -1, 0, 0, 0, 1]
+    cols = len(mono)
+    rng = np.random.default_rng(17)
+    if case == "csr":
+        cols = 40
+        mono = mono + [0] * (cols - len(mono))
+        indptr, indices, values, _ = W.config3(rows=12000, cols=cols, nnz=12, informative=10, seed=5)
+        X = W.csr_to_dense(indptr, indices, values, cols)
+    else:
+        X, _ = W.config1(rows=20000, cols=cols) if case == "missing" else W.config0(rows=20000, cols=cols)
+    Z = np.nan_to_num(X)
+    y = (np.sin(2 * Z[:, 0]) + Z[:, 0] - np.cos(2 * Z[:, 2]) - Z[:, 2] + Z[:, 6] + 0.3 * Z[:, 1]
+         + 0.2 * rng.normal(size=len(X))).astype(np.float32)
+    params = {"tree_method": "hist", "max_depth": 6, "max_bin": 64, "eta": 0.3,
+              "monotone_constraints": "(" + ",".join(map(str, mono)) + ")"}
+    if case == "logistic":
+        params["objective"] = "binary:logistic"
+        y = (y > np.median(y)).astype(np.float32)
+    if case == "sampled":
+        params.update(subsample=0.8, colsample_bytree=0.7, seed=9)
+    d = xgb.DMatrix(_csr(indptr, indices, values, cols) if case == "csr" else X, label=y)
+    bst = xgb.train(params, d, 6)
+    op = _oracle_params(params)
+    oracle_params = O.make_params(objective=params.get("objective", "reg:squarederror"), max_depth=6, max_bin=64,
+                                  eta=float(np.float32(0.3)), subsample=op.subsample,
+                                  colsample_bytree=op.colsample_bytree, seed=op.seed, monotone=mono)
+    ref = O.train(X, y, oracle_params, 6)
+    if case == "logistic":
+        # Logistic gradients use the device's expf against the host's libm
+        # (bitwise parity unpinned): the same tree shapes, margins to rounding.
+        for t, tree in enumerate(bst.trees_to_json()):
+            n = int(ref["sizes"][t])
+            np.testing.assert_array_equal(tree["left_children"], ref["trees"][t][:n]["left"])
+            np.testing.assert_array_equal(tree["split_indices"], np.maximum(ref["trees"][t][:n]["feature"], 0))
+        np.testing.assert_allclose(bst.predict(d, output_margin=True), ref["margin"], rtol=1e-5, atol=1e-5)
+    else:
+        assert_trees_equal(bst, ref)
+        np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32),
+                                      ref["margin"].view(np.uint32))
+    # The constraints bind: the same data trains other trees without them.
+    free = xgb.train(dict(params, monotone_constraints="()"), d, 6)
+    assert free.trees_to_json() != bst.trees_to_json()

@@ -323,3 +323,41 @@ def test_sampled_training_drops_rows_and_features():
         feats = set(O.sample_columns(12, 0.5, int(draws[2 * t + 1])).tolist())
         used = {int(f) for f in samp["trees"][t]["feature"][: samp["sizes"][t]] if f >= 0}
         assert used <= feats
+
+
+@pytest.mark.parametrize("objective", ["reg:squarederror", "binary:logistic"])
+def test_monotone_constraints_make_predictions_monotone(objective):
+    """Monotone constraints (src/tree.cpp:15-26, 1083-1086; boost.metal:902-920):
+    with +1 on x0 and -1 on x1, every prediction is non-decreasing in x0 and
+    non-increasing in x1 with the other features held fixed, while the
+    unconstrained model on the same data is not (so the check is not vacuous).
+    A flipped sign, a missing clamp or a wrong midpoint fails one of these."""
+    rng = np.random.default_rng(21)
+    rows = 6000
+    X = rng.normal(size=(rows, 4)).astype(np.float32)
+    y = (np.sin(3 * X[:, 0]) + X[:, 0] - np.cos(3 * X[:, 1]) - X[:, 1] + 0.5 * X[:, 2]
+         + 0.2 * rng.normal(size=rows)).astype(np.float32)
+    if objective == "binary:logistic":
+        y = (y > np.median(y)).astype(np.float32)
+    kw = dict(objective=objective, max_depth=5, max_bin=64, eta=0.3)
+    mono = O.train(X, y, O.make_params(monotone=[1, -1, 0, 0], **kw), 12)
+    free = O.train(X, y, O.make_params(**kw), 12)
+    grid = np.linspace(-2.5, 2.5, 101, dtype=np.float32)
+    anchors = rng.normal(size=(20, 4)).astype(np.float32)
+
+    def along(result, feature):
+        out = []
+        for a in anchors:
+            P = np.repeat(a[None, :], len(grid), axis=0)
+            P[:, feature] = grid
+            out.append(O.predict_margin(P, result, 0.0).astype(np.float64))
+        return np.asarray(out)
+
+    d0, d1 = np.diff(along(mono, 0), axis=1), np.diff(along(mono, 1), axis=1)
+    assert (d0 >= 0).all() and (d1 <= 0).all()
+    f0, f1 = np.diff(along(free, 0), axis=1), np.diff(along(free, 1), axis=1)
+    assert (f0 < 0).any() and (f1 > 0).any()
+    # Unconstrained features keep splitting both ways, and an all-zero
+    # constraint vector is the unconstrained model.
+    zero = O.train(X, y, O.make_params(monotone=[0, 0, 0, 0], **kw), 12)
+    np.testing.assert_array_equal(zero["trees"], free["trees"])

@@ -410,9 +410,6 @@ void Learner::configure_check() const {
   for (auto key : {"colsample_bylevel", "colsample_bynode"})
     require(number(key, 1) == 1.0, std::string(key) + " < 1 is not supported yet.");
   require(param("sampling_method", "uniform") == "uniform", "Only sampling_method='uniform' is supported.");
-  auto mono = param("monotone_constraints", "()");
-  for (char c : mono) require(c == '(' || c == ')' || c == '[' || c == ']' || c == ',' || c == '0' || c == ' ',
-                              "monotone_constraints are not supported yet.");
   require(param("interaction_constraints", "").empty() || param("interaction_constraints", "") == "[]",
           "interaction_constraints are not supported yet.");
   for (auto key : {"reg_lambda", "reg_alpha", "min_child_weight", "min_split_loss", "max_delta_step", "learning_rate",
@@ -570,6 +567,44 @@ void shuffle_prefix(std::vector<uint32_t>& order, std::mt19937& engine, size_t p
   }
 }
 
+// src/tree.cpp:15-26: "(1,0,-1)" or "[1,0,-1]", one entry per leading
+// feature (the rest unconstrained), each -1, 0 or 1.
+const int32_t* Learner::monotone_constraints(uint32_t cols) {
+  const std::string text = param("monotone_constraints", "()");
+  if (text != monotone_text_ || monotone_.size() != cols) {
+    std::vector<int32_t> values(cols, 0);
+    std::string json = text;
+    std::replace(json.begin(), json.end(), '(', '[');
+    std::replace(json.begin(), json.end(), ')', ']');
+    if (!json.empty() && json != "[]") {
+      Json list;
+      try {
+        list = Json::parse(json);
+      } catch (const std::exception&) {
+        throw std::runtime_error("monotone_constraints must be a list of -1, 0 or 1: " + text);
+      }
+      require(list.is_array(), "monotone_constraints must be a list of -1, 0 or 1.");
+      require(list.size() <= cols, "monotone_constraints has more entries than features.");
+      for (size_t i = 0; i < list.size(); ++i) {
+        require(list[i].is_number() && list[i].number() == (double)list[i].integer(),
+                "monotone_constraints must be a list of -1, 0 or 1.");
+        const int64_t v = list[i].integer();
+        require(v >= -1 && v <= 1, "Monotone constraints must be -1, 0 or 1.");
+        values[i] = (int32_t)v;
+      }
+    }
+    monotone_ = std::move(values);
+    monotone_text_ = text;
+    monotone_active_ = std::any_of(monotone_.begin(), monotone_.end(), [](int32_t v) { return v != 0; });
+    if (monotone_active_) {
+      d_monotone_.ensure((size_t)cols * sizeof(int32_t));
+      kcheck(mgb_memcpy_h2d(d_monotone_.get(), monotone_.data(), (size_t)cols * sizeof(int32_t)),
+             "monotone constraints upload");
+    }
+  }
+  return monotone_active_ ? d_monotone_.as<int32_t>() : nullptr;
+}
+
 // src/tree.cpp:28-45 (kernels/tree_sample_columns.metal.h): a fresh engine
 // seeded by one draw shuffles the features; the first
 // max(1, floor(n * fraction)) of them are kept.
@@ -669,6 +704,7 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
   auto* nodes = reinterpret_cast<MgbTreeNode*>(d_pending_.as<uint8_t>() + slot_offset);
   auto* count = reinterpret_cast<uint32_t*>(d_pending_.as<uint8_t>() + slot_offset + node_bytes);
   const uint32_t* features = sample_columns(data.cols);
+  const int32_t* monotone = monotone_constraints(data.cols);
   if (data.sparse) {
     const bool root_columns = integer("hip_csr_root_columns", 1) != 0;
     kcheck(mgb_grow_tree_csr(&shape, &data.csr, data.d_indptr.as<uint64_t>(), data.d_indices.as<uint32_t>(),
@@ -676,14 +712,14 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
                              root_columns ? data.d_csc_rows.as<uint32_t>() : nullptr,
                              root_columns ? data.d_csc_codes.get() : nullptr, data.d_cuts.as<float>(),
                              data.d_counts.as<uint32_t>(),
-                             d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, d_tree_ws_.get(),
+                             d_grad_.as<float>(), d_scales_.as<float>(), &sp, features, monotone, d_tree_ws_.get(),
                              d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
            "tree growth");
   } else {
     const void* columns = columns_on ? data.d_columns.get() : nullptr;
     kcheck(mgb_grow_tree(&shape, &data.matrix, data.d_bins.get(), columns, data.d_cuts.as<float>(),
                          data.d_counts.as<uint32_t>(), d_grad_.as<float>(), d_scales_.as<float>(), &sp, features,
-                         d_tree_ws_.get(), d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
+                         monotone, d_tree_ws_.get(), d_tree_ws_.bytes(), margin->as<float>(), nodes, count),
            "tree growth");
   }
   pending_.push_back(Pending{slot_offset, node_bytes, max_nodes});

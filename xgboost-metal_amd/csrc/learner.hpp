@@ -171,6 +171,9 @@ class Learner {
   void sample_rows(DMatrix& data, MgbGradParams& gp);
   // The tree's column sample as per-feature flags on the device, or NULL.
   const uint32_t* sample_columns(uint32_t cols);
+  // Device copy of monotone_constraints for `cols` features (NULL when every
+  // feature is unconstrained).
+  const int32_t* monotone_constraints(uint32_t cols);
   float base_margin_value() const;
   void upload_model();
   DeviceBuffer* margin_cache(DMatrix& data);
@@ -196,6 +199,10 @@ class Learner {
   std::string rng_seed_ = "0";
   DeviceBuffer d_features_;
   std::vector<uint32_t> feature_flags_;
+  DeviceBuffer d_monotone_;
+  std::vector<int32_t> monotone_;         // parsed constraints, cols entries
+  std::string monotone_text_ = "()";      // the parameter they were parsed from
+  bool monotone_active_ = false;
   DeviceBuffer d_eval_pred_, d_metric_ws_;
   // Queued rounds: node records (then the node count) at `offset` in d_pending_.
   struct Pending {

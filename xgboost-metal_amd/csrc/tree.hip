@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cfloat>
 #include <cmath>
 #include <cstring>
 
@@ -54,6 +55,8 @@ struct Frontier {
   uint32_t first_task;    // built nodes: first histogram task (row tile)
   uint32_t ntiles;        // built nodes: number of row tiles
   float leaf;             // the node's leaf value if it does not split
+  float lower, upper;     // monotone bounds of the node's weight (src/tree.cpp:1083-1086)
+  uint32_t padding[2];
 };
 
 struct Cand {
@@ -120,6 +123,7 @@ struct Tree {
   const float* cuts;
   const uint32_t* counts;
   const uint32_t* allowed;    // per feature: nonzero if in the tree's column sample (NULL: all)
+  const int32_t* monotone;    // per feature -1, 0 or 1: monotone constraint (NULL: none)
   const float2* grad;
   const float* scales;
   float* margin;
@@ -198,6 +202,14 @@ __device__ __forceinline__ float calc_weight(double G, double H, const MgbSplitP
   return w;
 }
 
+// A weight clamped to the node's monotone bounds (kernels/scalar_gain.metal.h:79-80,
+// split_statistics.metal.h:35-36); the root's bounds are +-FLT_MAX.
+__device__ __forceinline__ float clamp_weight(float w, float lower, float upper) {
+  if (w < lower) w = lower;
+  if (upper < w) w = upper;
+  return w;
+}
+
 // kernels/scalar_gain.metal.h:91-103.
 __device__ __forceinline__ float calc_gain(double G, double H, float w, const MgbSplitParams& p) {
   if (!(H > 0)) return 0.0f;
@@ -254,6 +266,8 @@ __global__ void k_level0(Tree t) {
     Frontier root;
     root.id = 0; root.begin = 0; root.count = n_root; root.parent_slot = 0;
     root.sum_g = 0; root.sum_h = 0; root.built = 1; root.first_task = 0; root.ntiles = tiles; root.leaf = 0.0f;
+    root.lower = -FLT_MAX; root.upper = FLT_MAX;  // tree_init_bounds
+    root.padding[0] = root.padding[1] = 0;
     t.frontier[0][0] = root;
     MgbTreeNode n;
     n.left = -1; n.right = -1; n.parent = -1; n.feature = -1;
@@ -860,6 +874,8 @@ struct NodeEval {
   uint64_t pg, ph;        // present-bin totals
   double G, H;
   float w, parent_gain;
+  float lower, upper;     // monotone bounds of the node's weight
+  int32_t mono;           // the item's feature's constraint (-1, 0, 1)
   bool has_missing;
   // This lane's best candidate.
   float best_gain;
@@ -868,13 +884,16 @@ struct NodeEval {
 };
 
 __device__ __forceinline__ void node_begin(NodeEval& n, uint64_t tg, uint64_t th, uint64_t mg, uint64_t mh, int eg,
-                                           int eh, const MgbSplitParams& p) {
+                                           int eh, const MgbSplitParams& p, float lower, float upper, int32_t mono) {
   n.tg = tg; n.th = th;
   n.pg = tg - mg; n.ph = th - mh;
   n.has_missing = mg != 0 || mh != 0;
   n.G = stat_value((int64_t)tg, eg);
   n.H = stat_value((int64_t)th, eh);
-  n.w = calc_weight(n.G, n.H, p);
+  n.lower = lower;
+  n.upper = upper;
+  n.mono = mono;
+  n.w = clamp_weight(calc_weight(n.G, n.H, p), lower, upper);
   n.parent_gain = calc_gain(n.G, n.H, n.w, p);
   n.best_gain = -INFINITY;
   n.best_order = 0xffffffffu;
@@ -887,7 +906,11 @@ __device__ __forceinline__ void try_candidate(NodeEval& n, uint64_t lg, uint64_t
   const double GL = stat_value((int64_t)lg, eg), HL = stat_value((int64_t)lh, eh);
   const double GR = stat_value((int64_t)rg, eg), HR = stat_value((int64_t)rh, eh);
   if (!(HL > 0 && HL >= (double)mcw && HR > 0 && HR >= (double)mcw)) return;
-  const float lw = calc_weight(GL, HL, p), rw = calc_weight(GR, HR, p);
+  const float lw = clamp_weight(calc_weight(GL, HL, p), n.lower, n.upper);
+  const float rw = clamp_weight(calc_weight(GR, HR, p), n.lower, n.upper);
+  // A monotone feature's split keeps the left weight at most (increasing) or
+  // at least (decreasing) the right one (kernels/boost.metal:909).
+  if ((n.mono > 0 && !(lw <= rw)) || (n.mono < 0 && !(lw >= rw))) return;
   const float gain = (calc_gain(GL, HL, lw, p) + calc_gain(GR, HR, rw, p)) - n.parent_gain;
   if (gain > -INFINITY && (gain > n.best_gain || (gain == n.best_gain && order < n.best_order))) {
     n.best_gain = gain;
@@ -1215,7 +1238,9 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const uint32_t F = t.cols, B1 = t.bins1, MB = t.max_bin;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const float mcw = fabsf(t.sp.min_child_weight);
-  const bool filter = t.sp.reg_alpha == 0.0f && t.sp.max_delta_step == 0.0f;
+  // The division-free bounds assume unclamped weights and no monotone
+  // rejection: with constraints every valid candidate is scored exactly.
+  const bool filter = t.sp.reg_alpha == 0.0f && t.sp.max_delta_step == 0.0f && !t.monotone;
   const float lambda = t.sp.reg_lambda;
   int64_t* cur = t.hist[depth & 1];
   const uint32_t b0 = (wave_in_item * kWave + lane) * CH;
@@ -1258,7 +1283,8 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
     }
     if (t.allowed && !t.allowed[f]) return;  // outside the tree's column sample
     NodeEval e;
-    node_begin(e, tg, th, mg, mh, eg, eh, t.sp);
+    node_begin(e, tg, th, mg, mh, eg, eh, t.sp, t.frontier[0][0].lower, t.frontier[0][0].upper,
+               t.monotone ? t.monotone[f] : 0);
     score_node<W, CH>(e, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
                   xkey[slot_in_block][0], wave_in_item, t.recs + f, best_bank(t, depth), f);
     return;
@@ -1313,8 +1339,9 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const uint64_t omg = pmg - xmg, omh = pmh - xmh;
   if (store_other && wave_in_item == 0 && lane == 0) store_pair(ob, MB, omg, omh);
   NodeEval ex, eo;
-  node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp);
-  node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp);
+  const int32_t mono = t.monotone ? t.monotone[f] : 0;
+  node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp, fb.lower, fb.upper, mono);
+  node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp, fo.lower, fo.upper, mono);
   score_node<W, CH>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
                 xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f, best_bank(t, depth) + built, f);
   score_node<W, CH>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
@@ -1345,8 +1372,8 @@ __device__ Cand make_cand(const NodeEval& n, const SplitRec& r, uint32_t feature
   c.bin = bin;
   c.default_left = backward;
   c.threshold = backward ? (bin == 0 ? -INFINITY : cuts_f[bin - 1]) : cuts_f[bin];
-  c.left_w = calc_weight(GL, HL, p);
-  c.right_w = calc_weight(GR, HR, p);
+  c.left_w = clamp_weight(calc_weight(GL, HL, p), n.lower, n.upper);
+  c.right_w = clamp_weight(calc_weight(GR, HR, p), n.lower, n.upper);
   c.left_h = (float)HL;
   c.right_h = (float)HR;
   c.lg = (int64_t)lg; c.lh = (int64_t)lh; c.rg = (int64_t)rg; c.rh = (int64_t)rh;
@@ -1431,7 +1458,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
       node = fr[i];
       const uint64_t key = best_keys[i];
       NodeEval ne;
-      node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p);
+      node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p, node.lower, node.upper, 0);
       parent_w = ne.w;
       total_h = (float)ne.H;
       best.feature = -1;
@@ -1449,7 +1476,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
         const uint32_t c0 = t.counts[0];
         double tg, th;
         ordered_sum(root0[0], root0[1], c0, false, c0, &tg, &th);
-        parent_w = calc_weight(tg, th, p);
+        parent_w = clamp_weight(calc_weight(tg, th, p), node.lower, node.upper);
         total_h = (float)th;
         if (best.feature >= 0 && (uint32_t)best.feature < F) {
           // best.feature is the root's best-key feature, staged in rootcut.
@@ -1469,13 +1496,13 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
           ordered_sum(rootf[0], rootf[1], steps, best.default_left != 0, count, &cg, &ch);
           double og = tg - cg, oh = th - ch;
           double ag = cg + og, ah = ch + oh;
-          applied_w = calc_weight(ag, ah, p);
+          applied_w = clamp_weight(calc_weight(ag, ah, p), node.lower, node.upper);
           applied_h = (float)ah;
         }
       } else if (best.feature >= 0) {
         double ag = stat_value(best.lg, eg) + stat_value(best.rg, eg);
         double ah = stat_value(best.lh, eh) + stat_value(best.rh, eh);
-        applied_w = calc_weight(ag, ah, p);
+        applied_w = clamp_weight(calc_weight(ag, ah, p), node.lower, node.upper);
         applied_h = (float)ah;
       }
     }
@@ -1533,8 +1560,21 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
           Frontier lf, rf;
           lf.id = left; lf.begin = node.begin; lf.count = node.count; lf.parent_slot = i; lf.sum_g = best.lg;
           lf.sum_h = best.lh; lf.built = 0; lf.first_task = 0; lf.ntiles = 0; lf.leaf = l.leaf;
+          lf.lower = node.lower; lf.upper = node.upper; lf.padding[0] = lf.padding[1] = 0;
           rf = lf;
           rf.id = right; rf.sum_g = best.rg; rf.sum_h = best.rh; rf.leaf = r.leaf;
+          // Children's bounds (src/tree.cpp:1083-1086): the midpoint of the
+          // child weights caps the left child from above and the right one
+          // from below (increasing), or the reverse (decreasing).
+          const int32_t mono = t.monotone ? t.monotone[best.feature] : 0;
+          const float middle = (best.left_w + best.right_w) * 0.5f;
+          if (mono > 0) {
+            if (middle < lf.upper) lf.upper = middle;
+            if (rf.lower < middle) rf.lower = middle;
+          } else if (mono < 0) {
+            if (lf.lower < middle) lf.lower = middle;
+            if (middle < rf.upper) rf.upper = middle;
+          }
           if (plan_next) {
             lf.count = lcount;
             rf.begin = node.begin + lcount;
@@ -1681,7 +1721,7 @@ __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const MgbSplitParams& p = t.sp;
   NodeEval ne;
-  node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p);
+  node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p, node.lower, node.upper, 0);
   Cand best;
   best.feature = -1;
   best.gain = -INFINITY;
@@ -1709,7 +1749,7 @@ __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
           tg += stat_value(h0[2 * b], eg);
           th += stat_value(h0[2 * b + 1], eh);
         }
-        parent_w = calc_weight(tg, th, p);
+        parent_w = clamp_weight(calc_weight(tg, th, p), node.lower, node.upper);
       }
       op.leaf = parent_w * p.eta;
     }
@@ -2120,8 +2160,8 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape) { return layout(*shap
 
 int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const void* columns,
                   const float* cuts, const uint32_t* counts, const float* grad, const float* scales,
-                  const MgbSplitParams* sp, const uint32_t* features, void* workspace, size_t workspace_bytes,
-                  float* margin, MgbTreeNode* nodes, uint32_t* node_count) {
+                  const MgbSplitParams* sp, const uint32_t* features, const int32_t* monotone, void* workspace,
+                  size_t workspace_bytes, float* margin, MgbTreeNode* nodes, uint32_t* node_count) {
   if (validate(shape, m)) return -1;
   Layout L = layout(*shape);
   if (!workspace || workspace_bytes < L.total) { set_error("mgb_grow_tree: workspace too small"); return -1; }
@@ -2129,6 +2169,7 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   t.bins = bins; t.columns = columns; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
   t.allowed = features;
+  t.monotone = monotone;
   if (t.compact) {
     launch(MGB_PROF_CONTROL, k_compact_reset, dim3(1), dim3(64), 0, t);
     MGB_LAUNCH_CHECK("k_compact_reset");
@@ -2208,7 +2249,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
                       const uint32_t* indices, const void* codes, const uint64_t* colptr, const uint32_t* csc_rows,
                       const void* csc_codes, const float* cuts, const uint32_t* counts,
                       const float* grad, const float* scales, const MgbSplitParams* sp, const uint32_t* features,
-                      void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
+                      const int32_t* monotone, void* workspace, size_t workspace_bytes, float* margin, MgbTreeNode* nodes,
                       uint32_t* node_count) {
   if (!shape || !m) { set_error("null shape or matrix"); return -1; }
   if (!shape->sparse) { set_error("mgb_grow_tree_csr: the tree shape must have sparse = 1"); return -1; }
@@ -2234,6 +2275,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
   t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
   t.allowed = features;
+  t.monotone = monotone;
   t.column_levels = 0;
   launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
   MGB_LAUNCH_CHECK("k_level0");
