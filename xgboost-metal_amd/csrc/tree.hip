@@ -233,14 +233,17 @@ __device__ __forceinline__ float calc_gain(double G, double H, float w, const Mg
 // ---------------------------------------------------------------------------
 __global__ void k_level0(Tree t) {
   LevelState* st = t.state;
-  // The root's rows: [0, N), or the kept rows k_compact_rows listed.
+  // The root's rows: [0, N), or the kept rows k_compact_rows listed.  The
+  // root histogram streams every row in order either way: a dropped row's
+  // gradient pair is (0, 0) and adds nothing, and whole columns read faster
+  // than the kept rows gathered through the list.
   const uint32_t n_root = t.compact ? st->kept : t.rows_n;
-  uint32_t tiles = n_root ? div_up(n_root, t.root_tile) : 0;
+  uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.root_tile) : 0;
   if (t.best)
     for (uint32_t i = threadIdx.x; i < 2 * t.slots; i += blockDim.x) t.best[i] = 0;
   for (uint32_t i = threadIdx.x; i < tiles; i += blockDim.x) {
     uint32_t begin = i * t.root_tile;
-    uint32_t end = begin + t.root_tile < n_root ? begin + t.root_tile : n_root;
+    uint32_t end = begin + t.root_tile < t.rows_n ? begin + t.root_tile : t.rows_n;
     t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
   }
   // The root's partition tasks (row tiles of [0, n_root)) and cursors.
@@ -1955,7 +1958,7 @@ Layout layout(const MgbTreeShape& s) {
 template <typename BinT, int G>
 int launch_hist(const Tree& t, uint32_t depth, bool unit, uint32_t grid) {
   size_t lds = (size_t)G * t.bins1 * (8 + (unit ? 4 : 8));
-  bool identity = depth == 0 && !t.compact;  // the root's rows are [0, N) unless compacted
+  bool identity = depth == 0;  // the root histogram reads rows [0, N) in order
   const bool cols = t.columns != nullptr && depth < t.column_levels;
 #define MGB_HIST_CASE(U, I)                                                                           \
   {                                                                                                   \
