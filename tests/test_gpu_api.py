@@ -172,3 +172,20 @@ def test_compacted_sampled_rows_equal_full_row_list(xgb, max_bin, missing):
     fresh = xgb.DMatrix(X)
     for bst in (compact, full):
         np.testing.assert_array_equal(bst.predict(d, output_margin=True), bst.predict(fresh, output_margin=True))
+
+
+@pytest.mark.parametrize("subsample,max_depth", [(1e-3, 4), (0.5, 1), (0.9, 2)])
+def test_compacted_rows_edge_cases(xgb, subsample, max_depth):
+    """Compaction when a round keeps a handful of rows (or none), and when the
+    root is also the last level (its partition reads the compacted list):
+    trees and training margins equal the full row list's."""
+    import oracle_lib as O
+    X, y = W.config0(rows=3000, cols=6)
+    d = xgb.DMatrix(X, label=y)
+    params = {"max_depth": max_depth, "max_bin": 32, "subsample": subsample, "seed": 4}
+    compact = xgb.train(params, d, 4)
+    full = xgb.train(dict(params, hip_compact_sampled=0), d, 4)
+    assert _trees(compact) == _trees(full)
+    np.testing.assert_array_equal(compact.predict(d, output_margin=True), full.predict(d, output_margin=True))
+    ref = O.train(X, y, O.make_params(max_depth=max_depth, max_bin=32, subsample=subsample, seed=4), 4)
+    np.testing.assert_array_equal(compact.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
