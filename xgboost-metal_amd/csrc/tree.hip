@@ -987,10 +987,30 @@ __device__ __forceinline__ void bound_bin(const NodeEval& n, uint64_t vg, uint64
   }
 }
 
+// Wave maxima as DPP max-scans (the lane moves of wave_inclusive_u32: row_shr
+// 1, 2, 4, 8 within each row of 16 lanes, then row_bcast 15 and 31 across
+// rows), whose last lane holds the wave's maximum; a lane whose source lies
+// outside its row, or a row the broadcast does not write, sees the identity.
+// Six DPP moves instead of six LDS permutes.  Call with every lane active.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_move_or(uint32_t v, uint32_t identity) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, kCtrl, kRowMask, 0xf, false);
+}
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float max_step_f32(float v) {
+  const float o = __uint_as_float(dpp_move_or<kCtrl, kRowMask>(__float_as_uint(v), 0xff800000u));  // -inf
+  return fmaxf(v, o);
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, kWave));
-  return v;
+  v = max_step_f32<kRowShr1, 0xf>(v);
+  v = max_step_f32<kRowShr2, 0xf>(v);
+  v = max_step_f32<kRowShr4, 0xf>(v);
+  v = max_step_f32<kRowShr8, 0xf>(v);
+  v = max_step_f32<kRowBcast15, 0xa>(v);
+  v = max_step_f32<kRowBcast31, 0xc>(v);
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), kWave - 1));
 }
 
 __device__ __forceinline__ void load_pair(const int64_t* h, uint32_t bin, uint64_t& g, uint64_t& v) {
@@ -1017,13 +1037,23 @@ __device__ __forceinline__ uint64_t lane63_u64(uint64_t v) {
   return (uint64_t)lo | ((uint64_t)hi << 32);
 }
 
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint64_t max_step_u64(uint64_t v) {
+  const uint32_t lo = dpp_move_or<kCtrl, kRowMask>((uint32_t)v, 0u);
+  const uint32_t hi = dpp_move_or<kCtrl, kRowMask>((uint32_t)(v >> 32), 0u);
+  const uint64_t o = (uint64_t)lo | ((uint64_t)hi << 32);
+  return o > v ? o : v;
+}
+
+// Unsigned 64-bit wave maximum (identity 0), uniform result.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) {
-    const uint64_t o = __shfl_xor(v, d, kWave);
-    v = o > v ? o : v;
-  }
-  return v;
+  v = max_step_u64<kRowShr1, 0xf>(v);
+  v = max_step_u64<kRowShr2, 0xf>(v);
+  v = max_step_u64<kRowShr4, 0xf>(v);
+  v = max_step_u64<kRowShr8, 0xf>(v);
+  v = max_step_u64<kRowBcast15, 0xa>(v);
+  v = max_step_u64<kRowBcast31, 0xc>(v);
+  return lane63_u64(v);
 }
 
 // A lane's best candidate of one node as a key whose maximum is the largest
