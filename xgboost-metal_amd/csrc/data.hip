@@ -203,13 +203,29 @@ __device__ void mass_flush_and_scale(uint64_t* local, uint64_t* mass, float* sca
 // the round seed times 16807^(row+1) modulo 2^63; the row is kept when the
 // binary64 value of state-1 over 2^63 (the canonical draw of a 63-bit engine)
 // is below subsample, compared in binary32 when subsample < 2^-39.
-__device__ __forceinline__ bool sample_keep(uint32_t seed, uint32_t row, float subsample) {
-  const uint64_t mask = 0x7fffffffffffffffull;
-  uint64_t state = seed ? seed : 1u, factor = 16807u;
-  for (uint64_t e = (uint64_t)row + 1; e; e >>= 1) {
-    if (e & 1) state = (state * factor) & mask;
-    factor = (factor * factor) & mask;
+constexpr uint64_t kStateMask = 0x7fffffffffffffffull;
+
+// base * 16807^e mod 2^63 (square and multiply; products mod 2^64, then the mask).
+__device__ __forceinline__ uint64_t times_16807_pow(uint64_t base, uint64_t e) {
+  uint64_t state = base, factor = 16807u;
+  for (; e; e >>= 1) {
+    if (e & 1) state = (state * factor) & kStateMask;
+    factor = (factor * factor) & kStateMask;
   }
+  return state;
+}
+
+// A thread's rows r, r + S, r + 2S, ...: the first state by square and
+// multiply, each next one by one multiply by 16807^S (exact mod 2^63).
+struct RowSampler {
+  uint64_t state, step;
+  __device__ RowSampler(uint32_t seed, uint32_t first, uint32_t stride, bool on)
+      : state(on ? times_16807_pow(seed ? seed : 1u, (uint64_t)first + 1) : 0),
+        step(on ? times_16807_pow(1u, stride) : 0) {}
+  __device__ __forceinline__ void next() { state = (state * step) & kStateMask; }
+};
+
+__device__ __forceinline__ bool keep_state(uint64_t state, float subsample) {
   const double rounded = (double)(state - 1);
   const float limit = subsample * 0x1p63f;
   if (limit < 0x1p24f) return (float)rounded < limit;
@@ -233,7 +249,9 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
   __shared__ uint64_t local[2 * 256];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < p.rows; r += gridDim.x * blockDim.x) {
+  const uint32_t first = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
+  RowSampler sampler(p.sample_seed, first, stride, p.subsample < 1.0f);
+  for (uint32_t r = first; r < p.rows; r += stride, sampler.next()) {
     float pred = margin[r], label = labels[r];
     float weight = p.has_weight ? weights[r] : 1.0f;
     float g = pred - label, h = 1.0f;
@@ -245,7 +263,7 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
     }
     g = g * weight;
     h = h * weight;
-    if (p.subsample < 1.0f && !sample_keep(p.sample_seed, r, p.subsample)) g = h = 0.0f;
+    if (p.subsample < 1.0f && !keep_state(sampler.state, p.subsample)) g = h = 0.0f;
     grad[r] = make_float2(g, h);
     mass_add(local, g, h);
   }
@@ -258,9 +276,11 @@ __global__ __launch_bounds__(kGradThreads) void k_gradient_mass(MgbGradParams p,
   __shared__ uint64_t local[2 * 256];
   for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < p.rows; r += gridDim.x * blockDim.x) {
+  const uint32_t first = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
+  RowSampler sampler(p.sample_seed, first, stride, p.subsample < 1.0f);
+  for (uint32_t r = first; r < p.rows; r += stride, sampler.next()) {
     float2 v = grad[r];
-    if (p.subsample < 1.0f && !sample_keep(p.sample_seed, r, p.subsample)) {
+    if (p.subsample < 1.0f && !keep_state(sampler.state, p.subsample)) {
       v = make_float2(0.0f, 0.0f);
       grad[r] = v;
     }
