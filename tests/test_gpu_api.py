@@ -189,3 +189,22 @@ def test_compacted_rows_edge_cases(xgb, subsample, max_depth):
     np.testing.assert_array_equal(compact.predict(d, output_margin=True), full.predict(d, output_margin=True))
     ref = O.train(X, y, O.make_params(max_depth=max_depth, max_bin=32, subsample=subsample, seed=4), 4)
     np.testing.assert_array_equal(compact.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def test_monotone_constraints_parameter_errors(xgb):
+    """monotone_constraints as the reference parses it (src/tree.cpp:15-26):
+    "(..)" or "[..]" lists of -1, 0, 1, at most one entry per feature; anything
+    else fails with the reference's messages, and all zeros is unconstrained."""
+    X, y = W.config0(rows=2000, cols=4)
+    d = xgb.DMatrix(X, label=y)
+    base = {"max_depth": 3, "max_bin": 32}
+    for bad, message in [("(2,0)", "must be -1, 0 or 1"), ("(1,0,0,0,1)", "more entries than features"),
+                         ("(1,x)", "list of -1, 0 or 1"), ("(0.5)", "list of -1, 0 or 1")]:
+        with pytest.raises(xgb.core.XGBoostError, match=message.replace("(", r"\(")):
+            xgb.train(dict(base, monotone_constraints=bad), d, 1)
+    free = xgb.train(base, d, 3)
+    for same in ["()", "[]", "(0,0)", "[0, 0, 0, 0]"]:
+        assert _trees(xgb.train(dict(base, monotone_constraints=same), d, 3)) == _trees(free)
+    short = xgb.train(dict(base, monotone_constraints="(1)"), d, 3)
+    longer = xgb.train(dict(base, monotone_constraints="[1,0,0,0]"), d, 3)
+    assert _trees(short) == _trees(longer)
