@@ -208,3 +208,16 @@ def test_monotone_constraints_parameter_errors(xgb):
     short = xgb.train(dict(base, monotone_constraints="(1)"), d, 3)
     longer = xgb.train(dict(base, monotone_constraints="[1,0,0,0]"), d, 3)
     assert _trees(short) == _trees(longer)
+
+
+def test_monotone_constraints_by_feature_name(xgb):
+    """A dict of feature names maps to the positional constraint list."""
+    X, y = W.config0(rows=2000, cols=4)
+    names = ["a", "b", "c", "d"]
+    d = xgb.DMatrix(X, label=y, feature_names=names)
+    base = {"max_depth": 3, "max_bin": 32}
+    by_name = xgb.train(dict(base, monotone_constraints={"c": -1, "a": 1}), d, 3)
+    by_position = xgb.train(dict(base, monotone_constraints="(1,0,-1,0)"), d, 3)
+    assert _trees(by_name) == _trees(by_position)
+    with pytest.raises(ValueError, match="not a subset"):
+        xgb.train(dict(base, monotone_constraints={"z": 1}), d, 1)

@@ -549,6 +549,13 @@ class Booster:
         for key, val in _params_items(params):
             if val is None:
                 continue
+            if key == "monotone_constraints" and isinstance(val, dict):
+                # Constraints by feature name (reference core.py Booster
+                # _configure_constraints): one entry per training feature, in order.
+                names = self.feature_names
+                if names is None or not set(val).issubset(names):
+                    raise ValueError("Constrained features are not a subset of training data feature names")
+                val = tuple(int(val.get(name, 0)) for name in names)
             if key == "eval_metric" and isinstance(val, (list, tuple)):
                 # Each listed metric is one eval_metric setting, in order.
                 for metric in val:
