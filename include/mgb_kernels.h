@@ -163,6 +163,13 @@ int mgb_any_missing(const float* data, uint64_t count, uint32_t* flag);
 /* Output transform of margins: objective 1 (logistic) maps x -> 1/(1+exp(-x)). */
 int mgb_transform(float* data, uint64_t count, uint32_t objective);
 
+/* Host only (no device work): the permutation std::shuffle(0..n-1) draws over
+ * std::mt19937(seed) in the column sample (src/tree.cpp:28-45), with
+ * libstdc++'s draws (model 0, x86-64 builds) or libc++'s (model 1, the
+ * reference's macOS builds); *next_draw (if not NULL) receives the engine's
+ * next output.  Returns -1 for another model. */
+int mgb_std_shuffle(uint32_t seed, uint32_t n, uint32_t model, uint32_t* order, uint32_t* next_draw);
+
 /* ---- one depthwise tree ---------------------------------------------- */
 size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
 /* Grows one depthwise tree on the device and adds its leaves to margin

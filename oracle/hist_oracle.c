@@ -21,8 +21,11 @@
  *  - scoring: exact-rational double-rounding constructions
  *    (tests/test_scalar_weight.py:29-71 of the reference);
  *  - tree: constructed known answers (tests/test_histogram_present.py:81).
- * Parity unpinned: logistic gradients bitwise (libm expf), weighted sketches
- * with tied values (the reference emulates libc++ std::sort permutations).
+ *  - logistic: the sigmoid is upstream XGBoost's expression over the host
+ *    libm's expf, as stock XGBoost computes it (the library's device exp is
+ *    checked against the same libm on all 2^32 inputs, tests/test_expf.py).
+ * Parity unpinned: weighted sketches with tied values (the reference
+ * emulates libc++ std::sort permutations).
  */
 #include "hist_oracle.h"
 
@@ -322,6 +325,23 @@ void oracle_quantize(const float* X, uint32_t rows, uint32_t cols, const float* 
 /* Gradients, base score and fixed-point quantization                       */
 /* ------------------------------------------------------------------------ */
 
+/* Upstream XGBoost's Sigmoid (src/common/math.h), which stock XGBoost's
+ * binary:logistic gradient and prediction transform call:
+ * expf(std::min(-x, 88.7f)) + 1 + 1e-16f, inverted; std::min keeps -x when it
+ * is NaN.  The reference's gradient kernel omits the clamp
+ * (kernels/boost.metal:50) and restates the clamped form elsewhere
+ * (kernels/distributions.metal.h:250); they differ only for x < -88.7. */
+float oracle_sigmoid(float x) {
+  float neg = -x;
+  float arg = 88.7f < neg ? 88.7f : neg;
+  return 1.0f / (expf(arg) + 1.0f + 1e-16f);
+}
+
+/* binary:logistic's prediction transform over an array. */
+void oracle_sigmoid_array(const float* in, float* out, uint64_t count) {
+  for (uint64_t i = 0; i < count; ++i) out[i] = oracle_sigmoid(in[i]);
+}
+
 /* kernels/boost.metal:553-601 (gradients), objectives 0, 1 and 2. */
 void oracle_gradients(int32_t objective, const float* margin, const float* labels, const float* weights,
                       uint32_t rows, float scale_pos_weight, float* grad, float* hess) {
@@ -330,7 +350,7 @@ void oracle_gradients(int32_t objective, const float* margin, const float* label
     float weight = weights ? weights[r] : 1.0f;
     float g = pred - label, h = 1.0f;
     if (objective == ORACLE_OBJ_LOGISTIC || objective == ORACLE_OBJ_LOGITRAW) {
-      float prob = 1.0f / (1.0f + expf(-pred)); /* kernels/boost.metal:50 */
+      float prob = oracle_sigmoid(pred);
       weight *= label == 1.0f ? scale_pos_weight : 1.0f;
       g = prob - label;
       h = fmaxf(prob * (1.0f - prob), 1.0e-16f);
@@ -830,13 +850,73 @@ int oracle_sample_row(uint32_t seed, uint32_t row, float subsample) {
   return rounded < (double)limit;
 }
 
-/* src/tree.cpp:28-45 with libc++'s std::shuffle (as the reference models it,
- * kernels/tree_sample_columns.metal.h): a fresh engine seeded with `seed`,
- * Fisher-Yates from the front where position pos swaps with pos + u, u drawn
- * uniformly from [0, n - pos) by masking engine outputs to the bit width of
- * n - pos - 1 and rejecting values >= n - pos.  The first
- * max(1, floor(n * fraction)) features (binary32 product) are kept, sorted. */
-uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, uint32_t* out) {
+/* Uniform integer in [0, range), 2 <= range <= 2^32, as libstdc++'s
+ * std::uniform_int_distribution draws it from a 32-bit engine (GCC 11 and
+ * later): Lemire's multiply-shift with rejection ("Fast Random Integer
+ * Generation in an Interval", ACM TOMACS 29(1), 2019). */
+static uint32_t uniform_libstdcxx(OracleMT* g, uint64_t range) {
+  uint32_t r32 = (uint32_t)range;
+  uint64_t product = (uint64_t)oracle_mt_next(g) * r32;
+  uint32_t low = (uint32_t)product;
+  if (low < r32) {
+    uint32_t threshold = (uint32_t)(0u - r32) % r32;
+    while (low < threshold) {
+      product = (uint64_t)oracle_mt_next(g) * r32;
+      low = (uint32_t)product;
+    }
+  }
+  return (uint32_t)(product >> 32);
+}
+
+static void swap_u32(uint32_t* v, uint64_t a, uint64_t b) {
+  uint32_t t = v[a];
+  v[a] = v[b];
+  v[b] = t;
+}
+
+/* std::shuffle(v, v + n, mt19937) of either standard library.
+ * libstdc++ (model 0; x86-64 Linux, stock XGBoost's wheels): position i from
+ * 1 upwards swaps with a uniform position in [0, i]; while n^2 < 2^32 the
+ * draws are paired: an even n first swaps position 1 with a draw over
+ * {0, 1}, then positions i, i + 1 share one draw x over [0, (i+1)(i+2)) and
+ * swap with x / (i+2) and x % (i+2).
+ * libc++ (model 1; the reference's macOS builds): position pos from 0
+ * swaps with pos + u, u uniform in [0, n - pos) from one engine output masked
+ * to the bit width of n - pos - 1, values >= n - pos rejected. */
+void oracle_std_shuffle(uint32_t* v, uint32_t n, OracleMT* g, int32_t model) {
+  if (n < 2) return;
+  if (model == 1) {
+    for (uint32_t pos = 0; pos + 1 < n; ++pos) {
+      uint32_t range = n - pos;
+      uint32_t width = 32u - (uint32_t)__builtin_clz(range - 1u);
+      uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
+      uint32_t u;
+      do u = oracle_mt_next(g) & mask; while (u >= range);
+      swap_u32(v, pos, pos + u);
+    }
+    return;
+  }
+  if (0xffffffffull / n >= n) {
+    uint64_t i = 1;
+    if (n % 2 == 0) {
+      swap_u32(v, 1, uniform_libstdcxx(g, 2));
+      i = 2;
+    }
+    for (; i < n; i += 2) {
+      uint64_t b1 = i + 2;
+      uint32_t x = uniform_libstdcxx(g, (i + 1) * b1);
+      swap_u32(v, i, x / b1);
+      swap_u32(v, i + 1, x % b1);
+    }
+    return;
+  }
+  for (uint64_t i = 1; i < n; ++i) swap_u32(v, i, uniform_libstdcxx(g, i + 1));
+}
+
+/* src/tree.cpp:28-45: a fresh engine seeded with `seed` shuffles the n
+ * features (std::shuffle of the given model); the first
+ * max(1, floor(n * fraction)) (binary32 product) are kept, sorted. */
+uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, int32_t model, uint32_t* out) {
   for (uint32_t i = 0; i < n; ++i) out[i] = i;
   if (!(fraction < 1.0f) || n == 0) return n;
   float scaled = floorf((float)n * fraction);
@@ -844,16 +924,7 @@ uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, uint32
   if (keep > n) keep = n;
   OracleMT g;
   oracle_mt_seed(&g, seed);
-  for (uint32_t pos = 0; pos < keep && pos + 1 < n; ++pos) {
-    uint32_t range = n - pos;
-    uint32_t width = 32u - (uint32_t)__builtin_clz(range - 1u);
-    uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
-    uint32_t u;
-    do u = oracle_mt_next(&g) & mask; while (u >= range);
-    uint32_t tmp = out[pos];
-    out[pos] = out[pos + u];
-    out[pos + u] = tmp;
-  }
+  oracle_std_shuffle(out, n, &g, model);
   /* Sort the kept prefix (insertion sort; n is a feature count). */
   for (uint32_t i = 1; i < keep; ++i) {
     uint32_t v = out[i], j = i;
@@ -923,6 +994,8 @@ int oracle_train(const float* X, uint32_t rows, uint32_t cols, const float* labe
   uint8_t* allowed = colsample ? (uint8_t*)malloc(cols) : NULL;
   uint32_t* features = colsample ? (uint32_t*)malloc((size_t)cols * sizeof(uint32_t)) : NULL;
   for (uint32_t t = 0; t < rounds; ++t) {
+    /* src/learner.cpp:668: seed_per_iteration reseeds with the round count. */
+    if (p->seed_per_iteration) oracle_mt_seed(&rng, p->seed * 127u + t);
     if (custom_grad) {
       memcpy(grad, custom_grad + (size_t)t * rows, (size_t)rows * sizeof(float));
       memcpy(hess, custom_hess + (size_t)t * rows, (size_t)rows * sizeof(float));
@@ -937,7 +1010,7 @@ int oracle_train(const float* X, uint32_t rows, uint32_t cols, const float* labe
         if (!oracle_sample_row(seed, r, p->subsample)) grad[r] = hess[r] = 0.0f;
     }
     if (colsample) {
-      uint32_t keep = oracle_sample_columns(cols, p->colsample_bytree, oracle_mt_next(&rng), features);
+      uint32_t keep = oracle_sample_columns(cols, p->colsample_bytree, oracle_mt_next(&rng), p->std_shuffle, features);
       memset(allowed, 0, cols);
       for (uint32_t i = 0; i < keep; ++i) allowed[features[i]] = 1;
     }
@@ -1156,20 +1229,11 @@ void oracle_cv_folds(uint32_t rows, int nfold, uint32_t seed, int shuffle, int s
   uint32_t* order = (uint32_t*)malloc(sizeof(uint32_t) * (rows ? rows : 1));
   for (uint32_t r = 0; r < rows; ++r) order[r] = r;
   if (shuffle && rows > 1) {
-    /* libc++ std::shuffle with mt19937(seed): the same draws as the feature
-     * sample's, over every position. */
+    /* std::shuffle with mt19937(seed), libstdc++'s draws (an x86-64 build of
+     * src/c_api.cpp:1018-1110). */
     OracleMT g;
     oracle_mt_seed(&g, seed);
-    for (uint32_t pos = 0; pos + 1 < rows; ++pos) {
-      uint32_t range = rows - pos;
-      uint32_t width = 32u - (uint32_t)__builtin_clz(range - 1u);
-      uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
-      uint32_t u;
-      do u = oracle_mt_next(&g) & mask; while (u >= range);
-      uint32_t tmp = order[pos];
-      order[pos] = order[pos + u];
-      order[pos + u] = tmp;
-    }
+    oracle_std_shuffle(order, rows, &g, 0);
   }
   if (stratified) {
     /* Stable insertion sort by label (test sizes are small). */

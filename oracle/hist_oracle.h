@@ -39,6 +39,8 @@ typedef struct {
   float colsample_bytree;    /* per-tree feature sampling when < 1 (src/tree.cpp:28-45) */
   uint32_t seed;             /* "seed" parameter; 0 keeps the engine's default state */
   const int32_t* monotone;   /* per feature -1, 0 or 1 (monotone_constraints); NULL: none */
+  int32_t std_shuffle;       /* column sample's std::shuffle: 0 libstdc++ (x86-64), 1 libc++ (macOS) */
+  int32_t seed_per_iteration; /* reseed the engine with seed * 127 + round before each round */
 } OracleParams;
 
 /* One tree node; field meanings follow the reference's Node plus base_weights
@@ -75,6 +77,8 @@ void oracle_quantize(const float* X, uint32_t rows, uint32_t cols, const float* 
 float oracle_base_score(int32_t objective, const float* labels, const float* weights, uint32_t rows,
                         float scale_pos_weight);
 float oracle_base_margin(int32_t objective, float base_score);
+float oracle_sigmoid(float x);
+void oracle_sigmoid_array(const float* in, float* out, uint64_t count);
 void oracle_gradients(int32_t objective, const float* margin, const float* labels, const float* weights,
                       uint32_t rows, float scale_pos_weight, float* grad, float* hess);
 /* Power-of-two fixed-point scale of one gradient column. */
@@ -101,9 +105,12 @@ uint32_t oracle_mt_next(OracleMT* g);
 /* Uniform row sampling: 1 if row `row` is kept in a round whose seed is `seed`
  * (kernels/sampling.metal.h:1-30). */
 int oracle_sample_row(uint32_t seed, uint32_t row, float subsample);
+/* std::shuffle(v, v + n, g) with the draws of libstdc++ (model 0) or libc++
+ * (model 1). */
+void oracle_std_shuffle(uint32_t* v, uint32_t n, OracleMT* g, int32_t model);
 /* Per-tree feature sample of n features: writes the sorted subset to out and
- * returns its size (src/tree.cpp:28-45 with libc++'s std::shuffle). */
-uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, uint32_t* out);
+ * returns its size (src/tree.cpp:28-45, std::shuffle of the given model). */
+uint32_t oracle_sample_columns(uint32_t n, float fraction, uint32_t seed, int32_t model, uint32_t* out);
 
 /* --- training ------------------------------------------------------------ */
 uint32_t oracle_max_nodes(int32_t max_depth);

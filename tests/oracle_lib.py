@@ -21,7 +21,8 @@ class OracleParams(ctypes.Structure):
                 ("scale_pos_weight", ctypes.c_float), ("base_score", ctypes.c_float),
                 ("has_base_score", ctypes.c_int32), ("nthread", ctypes.c_int32),
                 ("subsample", ctypes.c_float), ("colsample_bytree", ctypes.c_float), ("seed", ctypes.c_uint32),
-                ("monotone", ctypes.c_void_p)]
+                ("monotone", ctypes.c_void_p), ("std_shuffle", ctypes.c_int32),
+                ("seed_per_iteration", ctypes.c_int32)]
 
 
 NODE_DTYPE = np.dtype([("left", "<i4"), ("right", "<i4"), ("parent", "<i4"), ("feature", "<i4"),
@@ -34,6 +35,7 @@ SPLIT_DTYPE = np.dtype([("gain", "<f4"), ("threshold", "<f4"), ("left_weight", "
                         ("left_g", "<i8"), ("left_hs", "<i8"), ("right_g", "<i8"), ("right_hs", "<i8")])
 
 OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1, "binary:logitraw": 2}
+SHUFFLE_MODELS = {"libstdc++": 0, "libc++": 1}
 
 _lib = None
 
@@ -52,6 +54,8 @@ def lib():
         _lib.oracle_base_margin.restype = ctypes.c_float
         _lib.oracle_weight.restype = ctypes.c_float
         _lib.oracle_weight.argtypes = [ctypes.c_double, ctypes.c_double, ctypes.POINTER(OracleParams)]
+        _lib.oracle_sigmoid.restype = ctypes.c_float
+        _lib.oracle_sigmoid.argtypes = [ctypes.c_float]
         _lib.oracle_gain.restype = ctypes.c_float
         _lib.oracle_gain.argtypes = [ctypes.c_double, ctypes.c_double, ctypes.c_float, ctypes.POINTER(OracleParams)]
     return _lib
@@ -64,13 +68,16 @@ def ptr(a):
 def make_params(objective="reg:squarederror", max_depth=6, max_bin=256, eta=0.3, reg_lambda=1.0, reg_alpha=0.0,
                 min_child_weight=1.0, max_delta_step=0.0, min_split_loss=0.0, scale_pos_weight=1.0,
                 base_score=None, fma_contract=1, nthread=0, subsample=1.0, colsample_bytree=1.0, seed=0,
-                monotone=None):
-    """monotone: one -1/0/1 per feature, or None."""
+                monotone=None, std_shuffle="libstdc++", seed_per_iteration=0):
+    """monotone: one -1/0/1 per feature, or None.  std_shuffle: the standard
+    library whose std::shuffle draws the column sample ("libstdc++" or
+    "libc++")."""
     mono = None if monotone is None else np.ascontiguousarray(monotone, np.int32)
     p = OracleParams(OBJECTIVES[objective], max_depth, max_bin, fma_contract, eta, reg_lambda, reg_alpha,
                      min_child_weight, max_delta_step, min_split_loss, scale_pos_weight,
                      0.0 if base_score is None else base_score, 0 if base_score is None else 1, nthread,
-                     subsample, colsample_bytree, seed, None if mono is None else mono.ctypes.data)
+                     subsample, colsample_bytree, seed, None if mono is None else mono.ctypes.data,
+                     SHUFFLE_MODELS[std_shuffle], int(seed_per_iteration))
     p._monotone = mono  # keeps the array alive while the parameters are
     return p
 
@@ -124,6 +131,15 @@ def train(X, y, params, rounds, weights=None, custom_grad=None, custom_hess=None
             "cut_counts": counts}
 
 
+def sigmoid(margin):
+    """binary:logistic's prediction transform (upstream XGBoost's Sigmoid
+    over the host libm's expf)."""
+    margin = np.ascontiguousarray(margin, np.float32)
+    out = np.empty_like(margin)
+    lib().oracle_sigmoid_array(ptr(margin), ptr(out), ctypes.c_uint64(margin.size))
+    return out
+
+
 def predict_margin(X, result, base_margin):
     X = np.ascontiguousarray(X, np.float32)
     rows, cols = X.shape
@@ -155,12 +171,25 @@ def sample_rows(seed, rows, subsample):
     return np.array([f(seed, r, subsample) for r in range(rows)], bool)
 
 
-def sample_columns(n, fraction, seed):
+def sample_columns(n, fraction, seed, std_shuffle="libstdc++"):
     out = np.zeros(max(n, 1), np.uint32)
     f = lib().oracle_sample_columns
     f.restype = ctypes.c_uint32
-    k = f(ctypes.c_uint32(n), ctypes.c_float(fraction), ctypes.c_uint32(seed), ptr(out))
+    k = f(ctypes.c_uint32(n), ctypes.c_float(fraction), ctypes.c_uint32(seed), ctypes.c_int32(SHUFFLE_MODELS[std_shuffle]),
+          ptr(out))
     return out[:k]
+
+
+def std_shuffle(n, seed, model="libstdc++"):
+    """std::shuffle of 0..n-1 over std::mt19937(seed); returns the permutation
+    and the engine's next output (which shows how many draws were taken)."""
+    g = (ctypes.c_uint32 * 625)()
+    lib().oracle_mt_seed(g, ctypes.c_uint32(seed))
+    v = np.arange(max(n, 1), dtype=np.uint32)
+    lib().oracle_std_shuffle(ptr(v), ctypes.c_uint32(n), g, ctypes.c_int32(SHUFFLE_MODELS[model]))
+    nxt = lib().oracle_mt_next
+    nxt.restype = ctypes.c_uint32
+    return v[:n], int(nxt(g))
 
 
 def metric_sum(pred, labels, kind, weights=None, parameter=0.0):

@@ -25,7 +25,9 @@ def _oracle_params(params, rounds_override=None):
                          base_score=params.get("base_score"),
                          subsample=float(params.get("subsample", 1.0)),
                          colsample_bytree=float(params.get("colsample_bytree", 1.0)),
-                         seed=int(params.get("seed", 0)))
+                         seed=int(params.get("seed", 0)),
+                         seed_per_iteration=int(params.get("seed_per_iteration", 0)),
+                         std_shuffle=params.get("std_shuffle", "libstdc++"))
 
 
 def assert_trees_equal(bst, oracle_result):
@@ -238,12 +240,10 @@ def test_logistic_parity(xgb):
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(params, d, 10)
     ref = O.train(X, y, _oracle_params(params), 10)
+    assert_trees_equal(bst, ref)
     margin = bst.predict(d, output_margin=True)
-    # The oracle uses the host libm expf; the device uses its own expf, so
-    # logistic gradients agree to rounding (bitwise parity unpinned here).
-    np.testing.assert_allclose(margin, ref["margin"], rtol=1e-5, atol=1e-5)
-    prob = bst.predict(d)
-    np.testing.assert_allclose(prob, 1 / (1 + np.exp(-ref["margin"].astype(np.float64))), rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(margin.view(np.uint32), ref["margin"].view(np.uint32))
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), O.sigmoid(ref["margin"]).view(np.uint32))
 
 
 # ---------------------------------------------------------------------------
@@ -281,6 +281,31 @@ def test_csr_regression_matches_oracle(xgb, max_bin, root_columns):
     np.testing.assert_array_equal(bst.predict(xgb.DMatrix(_csr(indptr, indices, values, cols))).view(np.uint32),
                                   ref["margin"].view(np.uint32))
     np.testing.assert_array_equal(bst.predict(xgb.DMatrix(X)).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def test_config3_logistic_matches_oracle(xgb):
+    """BASELINE config 3's own workload at 50,000 rows: CSR, the full 2,000
+    features with 20 nonzeros a row, its Bernoulli(sigmoid) labels and its
+    parameters (binary:logistic, depth 8, 256 bins, eta 0.1), 5 rounds.
+    Cuts, every tree, the training margins and the probabilities are
+    bit-identical to the oracle run on the dense matrix with NaN at the
+    absent entries."""
+    cols = 2000
+    indptr, indices, values, y = W.config3(rows=50000, cols=cols)
+    X = W.csr_to_dense(indptr, indices, values, cols)
+    params = dict(W.CONFIG_PARAMS[3])
+    d = xgb.DMatrix(_csr(indptr, indices, values, cols), label=y)
+    bst = xgb.train(params, d, 5)
+    ref = O.train(X, y, _oracle_params(params), 5)
+    cut_ptr, cut_values = d.get_quantile_cut()
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    for f in range(cols):
+        c = ref["cut_counts"][f]
+        np.testing.assert_array_equal(cut_values[cut_ptr[f]:cut_ptr[f + 1]].view(np.uint32),
+                                      ref["cuts"][f, :c].view(np.uint32))
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), O.sigmoid(ref["margin"]).view(np.uint32))
 
 
 def test_csr_logistic_weighted_equals_dense(xgb):
@@ -386,14 +411,15 @@ def _config4_small(rows=40000, seed=5):
     return X, y
 
 
-@pytest.mark.parametrize("group", [0, 4])
-def test_sampled_1024_bins_depth10_parity(xgb, group):
+@pytest.mark.parametrize("group,shuffle", [(0, "libstdc++"), (4, "libstdc++"), (0, "libc++")])
+def test_sampled_1024_bins_depth10_parity(xgb, group, shuffle):
     """1024 bins (u16 codes; 8 features per histogram workgroup by the LDS
-    rule, or 4 on request), depth 10, subsample 0.8 and colsample_bytree 0.8:
-    bit-identical trees and margins."""
+    rule, or 4 on request), depth 10, subsample 0.8 and colsample_bytree 0.8,
+    with the column sample drawn by libstdc++'s std::shuffle (the default) or
+    libc++'s: bit-identical trees and margins."""
     X, y = _config4_small()
     params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
-              "subsample": 0.8, "colsample_bytree": 0.8, "hip_histogram_features": group}
+              "subsample": 0.8, "colsample_bytree": 0.8, "hip_histogram_features": group, "std_shuffle": shuffle}
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(params, d, 5)
     ref = O.train(X, y, _oracle_params(params), 5)
@@ -401,25 +427,58 @@ def test_sampled_1024_bins_depth10_parity(xgb, group):
     np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
 
 
+@pytest.mark.parametrize("quantile", [False, True])
+def test_weighted_million_root_literal(xgb, quantile):
+    """The reference's literal 2915099116 (tests/test_scalar_root_statistics.py:
+    66-80) from a DMatrix and a QuantileDMatrix: the root's base weight of a
+    weighted 1,000,000-row depth-1 tree, and the whole tree and margins equal
+    the oracle's."""
+    X, y, weight = W.weighted_million()
+    params = dict(W.WEIGHTED_MILLION_PARAMS)
+    d = (xgb.QuantileDMatrix(X, label=y, weight=weight, max_bin=256) if quantile
+         else xgb.DMatrix(X, label=y, weight=weight))
+    bst = xgb.train(params, d, 1)
+    root = np.float32(bst.trees_to_json()[0]["base_weights"][0])
+    assert int(root.view(np.uint32)) == W.WEIGHTED_MILLION_ROOT_BITS
+    ref = O.train(X, y, _oracle_params(params), 1, weights=weight)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(xgb.DMatrix(X)).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def test_seed_per_iteration_queued_equals_stepwise_and_oracle(xgb):
+    """seed_per_iteration reseeds the engine with seed * 127 + the number of
+    rounds already boosted (src/learner.cpp:668), counting rounds still
+    queued on the device: rounds queued without a host wait, rounds read back
+    one at a time and the oracle grow the same sampled trees."""
+    X, y = W.config0(rows=12000, cols=16)
+    params = {"tree_method": "hist", "max_depth": 5, "max_bin": 64, "eta": 0.3, "subsample": 0.7,
+              "colsample_bytree": 0.6, "seed": 5, "seed_per_iteration": 1}
+    d = xgb.DMatrix(X, label=y)
+    queued = xgb.train(params, d, 6)
+    stepwise = xgb.Booster(params, [d])
+    for i in range(6):
+        stepwise.update(d, i)
+        stepwise.predict(d)  # reads the model back after every round
+    ref = O.train(X, y, _oracle_params(params), 6)
+    assert_trees_equal(queued, ref)
+    assert_trees_equal(stepwise, ref)
+    np.testing.assert_array_equal(queued.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+    # Reseeding matters: without it the same seed draws other samples.
+    plain = O.train(X, y, _oracle_params(dict(params, seed_per_iteration=0)), 6)
+    assert not np.array_equal(plain["margin"], ref["margin"])
+
+
 def test_sampled_logistic_parity(xgb):
-    """The config-4 objective and sampling at a small size.  The first tree is
-    bit-identical; later trees see logistic gradients from the device expf,
-    which agree with libm's to rounding (bitwise parity unpinned), so margins
-    are compared to 1e-5."""
+    """The config-4 objective and sampling at a small size: every tree and
+    the training margins bit-identical to the oracle."""
     X, y = _config4_small()
     params = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
               "subsample": 0.8, "colsample_bytree": 0.8}
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(params, d, 5)
     ref = O.train(X, y, _oracle_params(params), 5)
-    tree0 = bst.trees_to_json()[0]
-    n0 = int(ref["sizes"][0])
-    np.testing.assert_array_equal(tree0["left_children"], ref["trees"][0]["left"][:n0])
-    np.testing.assert_array_equal(np.asarray(tree0["split_conditions"], np.float32).view(np.uint32),
-                                  np.where(ref["trees"][0]["left"][:n0] < 0, ref["trees"][0]["leaf"][:n0],
-                                           ref["trees"][0]["threshold"][:n0]).astype(np.float32).view(np.uint32))
-    margin = bst.predict(d, output_margin=True)
-    np.testing.assert_allclose(margin, ref["margin"], rtol=1e-5, atol=1e-5)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
 
 
 def test_sampling_stream_survives_pickle(xgb):
@@ -462,9 +521,8 @@ def test_monotone_constraints_match_oracle(xgb, case):
     kernels/boost.metal:902-920): node weight bounds, clamped weights, the
     left/right order on constrained features and the children's midpoint
     bounds give trees and training margins bit-identical to the oracle's,
-    dense, with missing values, CSR and with row and column sampling, and to
-    rounding for logistic (the oracle is pinned by the monotonicity of its
-    predictions)."""
+    dense, with missing values, logistic, CSR and with row and column
+    sampling (the oracle is pinned by the monotonicity of its predictions)."""
     mono = [1, 0, -1, 0, 0, 0, 1]
     cols = len(mono)
     rng = np.random.default_rng(17)
@@ -492,18 +550,8 @@ def test_monotone_constraints_match_oracle(xgb, case):
                                   eta=float(np.float32(0.3)), subsample=op.subsample,
                                   colsample_bytree=op.colsample_bytree, seed=op.seed, monotone=mono)
     ref = O.train(X, y, oracle_params, 6)
-    if case == "logistic":
-        # Logistic gradients use the device's expf against the host's libm
-        # (bitwise parity unpinned): the same tree shapes, margins to rounding.
-        for t, tree in enumerate(bst.trees_to_json()):
-            n = int(ref["sizes"][t])
-            np.testing.assert_array_equal(tree["left_children"], ref["trees"][t][:n]["left"])
-            np.testing.assert_array_equal(tree["split_indices"], np.maximum(ref["trees"][t][:n]["feature"], 0))
-        np.testing.assert_allclose(bst.predict(d, output_margin=True), ref["margin"], rtol=1e-5, atol=1e-5)
-    else:
-        assert_trees_equal(bst, ref)
-        np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32),
-                                      ref["margin"].view(np.uint32))
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
     # The constraints bind: the same data trains other trees without them.
     free = xgb.train(dict(params, monotone_constraints="()"), d, 6)
     assert free.trees_to_json() != bst.trees_to_json()

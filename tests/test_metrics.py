@@ -8,8 +8,8 @@ src/c_api.cpp:1018-1110):
 - ROC-AUC: exact pair counting (a positive ranked above a negative counts 1,
   a tie 1/2) with Fractions, and weighted pair sums;
 - PR-AUC: numerical quadrature of precision along each step's straight line;
-- CV folds: partition rules, and the shuffle against numpy's MT19937 with
-  libc++'s masked-rejection draw.
+- CV folds: partition rules, and the shuffle against libstdc++'s std::shuffle
+  (the fixture written by the real one, tests/test_shuffle.py).
 
 The CPU oracle is test infrastructure; the library's folds are checked
 against it here (no GPU needed), the device metrics in test_gpu_metrics.py.
@@ -192,23 +192,16 @@ def test_cv_folds_partition_rules():
     assert not np.array_equal(O.cv_folds(rows, nfold, 43), shuffled)
 
 
-def test_cv_shuffle_follows_mt19937_and_libcxx_draws():
-    """libc++ std::shuffle: position p swaps with p + u, u drawn from one
-    32-bit output masked to the bit width of n - p - 1, rejecting >= n - p;
-    the engine stream comes from numpy's own MT19937."""
-    rows, nfold, seed = 37, 3, 2024
-    bg = np.random.MT19937()
-    bg._legacy_seeding(seed)
-    stream = iter(bg.random_raw(10_000).tolist())
-    order = list(range(rows))
-    for p in range(rows - 1):
-        span = rows - p
-        mask = (1 << (span - 1).bit_length()) - 1
-        while True:
-            u = next(stream) & mask
-            if u < span:
-                break
-        order[p], order[p + u] = order[p + u], order[p]
+def test_cv_shuffle_follows_libstdcxx_draws():
+    """Plain folds take consecutive chunks of the row order std::shuffle
+    draws over mt19937(seed) (libstdc++, as an x86-64 build of
+    src/c_api.cpp:1018-1110), the first rows % nfold folds one row longer;
+    the order is taken from the fixture the real std::shuffle wrote."""
+    import json
+    from pathlib import Path
+    fixture = json.loads((Path(__file__).parent / "golden" / "shuffle_libstdcxx.json").read_text())
+    rows, nfold, seed = 101, 3, 42
+    order = next(c["head"] for c in fixture["cases"] if c["n"] == rows and c["seed"] == seed)
     expect = np.zeros(rows, np.int32)
     pos = 0
     for k in range(nfold):

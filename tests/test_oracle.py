@@ -297,8 +297,7 @@ def test_row_sampling_planted_mistake_is_caught():
 def test_column_sampling_invariants(n, fraction):
     """Sorted distinct features, max(1, floor(n * fraction)) of them, a
     deterministic function of the seed; different seeds give different sets.
-    (The draw order models libc++'s std::shuffle: parity unpinned, no libc++
-    headers in this image.)"""
+    (The draw order itself is pinned by tests/test_shuffle.py.)"""
     keep = max(1, int(np.floor(np.float32(n) * np.float32(fraction))))
     a = O.sample_columns(n, fraction, 12345)
     assert len(a) == keep
@@ -361,3 +360,17 @@ def test_monotone_constraints_make_predictions_monotone(objective):
     # constraint vector is the unconstrained model.
     zero = O.train(X, y, O.make_params(monotone=[0, 0, 0, 0], **kw), 12)
     np.testing.assert_array_equal(zero["trees"], free["trees"])
+
+
+@pytest.mark.parametrize("fma", [1, 0])
+def test_weighted_million_root_literal(fma):
+    """The reference's literal 2915099116 (tests/test_scalar_root_statistics.py:
+    66-80): weighted squared error over 1,000,000 dense rows, depth 1, 256
+    bins.  The root's base weight comes from feature 0's bins summed in bin
+    order in binary64; an exact (or row-order float64) sum of the same
+    gradients gives 2915099417 and a float32 sum 2956438444, so the literal
+    pins the ordered-bin rule, the weighted sketch and the base score."""
+    X, y, weight = W.weighted_million()
+    ref = O.train(X, y, O.make_params(max_depth=1, max_bin=256, seed=9, fma_contract=fma), 1, weights=weight)
+    bits = int(np.float32(ref["trees"][0]["base_weight"][0]).view(np.uint32))
+    assert bits == W.WEIGHTED_MILLION_ROOT_BITS

@@ -93,6 +93,27 @@ def config3(rows=1_000_000, cols=2000, nnz=20, informative=200, seed=1337):
     return indptr, idx.reshape(-1).astype(np.int32), values.reshape(-1), y
 
 
+def weighted_million():
+    """The reference's weighted dense-root construction
+    (tests/test_scalar_root_statistics.py:66-80): 1,000,000 rows of
+    default_rng(43) N(0,1) x 64, y = 2 x0 + x1^2 + N(0, 0.1), the first four
+    columns kept; weights default_rng(144) uniform(0.1, 2).  With depth 1,
+    256 bins and seed 9, one round's root base weight has the bits
+    2915099116 in the reference's CPU oracle build."""
+    rng = np.random.default_rng(43)
+    original = rng.normal(size=(1000000, 64)).astype(np.float32)
+    noise = rng.normal(0, 0.1, len(original))
+    y = (2 * original[:, 0] + original[:, 1] ** 2 + noise).astype(np.float32)
+    X = original[:, :4].copy()
+    del original
+    weight = np.random.default_rng(144).uniform(0.1, 2, len(X)).astype(np.float32)
+    return X, y, weight
+
+
+WEIGHTED_MILLION_ROOT_BITS = 2915099116
+WEIGHTED_MILLION_PARAMS = {"tree_method": "hist", "max_depth": 1, "max_bin": 256, "seed": 9}
+
+
 def csr_to_dense(indptr, indices, values, cols):
     """The dense matrix of a CSR matrix, NaN at the absent entries."""
     rows = len(indptr) - 1

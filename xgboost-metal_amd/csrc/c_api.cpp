@@ -1454,7 +1454,8 @@ int XGBoosterTrainOneIterWithSplitGrad(BoosterHandle, DMatrixHandle, int, char c
   return unsupported("Separate split and leaf gradients");
 }
 // Row folds for xgboost.cv (src/c_api.cpp:1018-1110): rows shuffled by
-// libc++'s std::shuffle over mt19937(seed) when `shuffle`; plain folds take
+// std::shuffle over mt19937(seed) when `shuffle` (libstdc++'s draws, as an
+// x86-64 build of that function makes them); plain folds take
 // consecutive chunks of that order (the first nrows % nfold folds one row
 // longer), stratified folds deal the order, stably sorted by label, round
 // robin.  Fold k tests its rows and trains on the others, both in row order.
@@ -1469,7 +1470,7 @@ int XGDMatrixBuildCVFolds(DMatrixHandle handle, int nfold, unsigned seed, int sh
   std::mt19937 rng(seed);
   std::vector<uint32_t> order(nrows);
   for (uint32_t r = 0; r < nrows; ++r) order[r] = r;
-  if (shuffle && nrows > 1) shuffle_prefix(order, rng, nrows - 1);
+  if (shuffle && nrows > 1) std_shuffle(order, rng, ShuffleModel::libstdcxx);
   std::vector<int> fold(nrows, 0);
   if (stratified) {
     const auto& y = m->labels;

@@ -4,6 +4,7 @@
 
 #include <cmath>
 
+#include "binary32_exp.hpp"
 #include "device_common.hpp"
 
 namespace mgb {
@@ -256,7 +257,9 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
     float weight = p.has_weight ? weights[r] : 1.0f;
     float g = pred - label, h = 1.0f;
     if (p.objective == 1 || p.objective == 2) {
-      float prob = 1.0f / (1.0f + expf(-pred));
+      // Upstream XGBoost's Sigmoid over a binary32 exp with the host libm's
+      // bits (binary32_exp.hpp); kernels/boost.metal:566-570.
+      float prob = mgb::sigmoid_binary32(pred);
       weight *= label == 1.0f ? p.scale_pos_weight : 1.0f;
       g = prob - label;
       h = fmaxf(prob * (1.0f - prob), 1.0e-16f);
@@ -354,10 +357,11 @@ __global__ void k_any_missing(const float* __restrict__ data, uint64_t count, ui
   if (__any(missing) && lane_id() == 0) atomicOr(flag, 1u);
 }
 
-// Prediction transform of binary:logistic (sigmoid of the margin).
+// Prediction transform of binary:logistic (sigmoid of the margin, the same
+// function as the gradient's).
 __global__ void k_transform(float* __restrict__ data, uint64_t count, uint32_t objective) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
-    if (objective == 1) data[i] = 1.0f / (1.0f + expf(-data[i]));
+    if (objective == 1) data[i] = mgb::sigmoid_binary32(data[i]);
   }
 }
 

@@ -536,9 +536,11 @@ void Learner::configure_rng() {
 
 void Learner::sample_rows(DMatrix& data, MgbGradParams& gp) {
   configure_rng();
+  // src/learner.cpp:668: reseed with the number of rounds already boosted,
+  // counting the rounds still queued on the device.
   if (integer("seed_per_iteration", 0))
     rng_.seed(static_cast<std::mt19937::result_type>((uint32_t)std::stoll(param("seed", "0")) * 127u +
-                                                     (uint32_t)trees.size()));
+                                                     (uint32_t)boosted_rounds()));
   const double subsample = number("subsample", 1);
   const auto budget = static_cast<uint64_t>(static_cast<float>(data.rows) * subsample);
   gp.subsample = 1.0f;
@@ -549,22 +551,88 @@ void Learner::sample_rows(DMatrix& data, MgbGradParams& gp) {
   }
 }
 
-// libc++'s std::shuffle over a 32-bit engine, which the reference's builds
-// use: Fisher-Yates from the front, position pos swapping with pos + u, u
-// uniform in [0, n - pos) drawn by masking one engine output to the bit
-// width of n - pos - 1 and rejecting values >= n - pos.  Only the first
-// `positions` positions are drawn (all n - 1 for a full shuffle).
-void shuffle_prefix(std::vector<uint32_t>& order, std::mt19937& engine, size_t positions) {
-  const size_t n = order.size();
-  for (size_t pos = 0; pos < positions && pos + 1 < n; ++pos) {
+// Uniform integer in [0, range), range <= 2^32, the way libstdc++'s
+// std::uniform_int_distribution draws it from a 32-bit engine (GCC 11 and
+// later): Lemire's multiply-shift, "Fast Random Integer Generation in an
+// Interval" (ACM TOMACS 29(1), 2019): the high half of engine() * range,
+// redrawn while the low half falls below 2^32 mod range.
+static uint32_t libstdcxx_uniform(std::mt19937& engine, uint64_t range) {
+  const uint32_t r32 = (uint32_t)range;
+  uint64_t product = (uint64_t)(uint32_t)engine() * r32;
+  uint32_t low = (uint32_t)product;
+  if (low < r32) {
+    const uint32_t threshold = (uint32_t)(0u - r32) % r32;
+    while (low < threshold) {
+      product = (uint64_t)(uint32_t)engine() * r32;
+      low = (uint32_t)product;
+    }
+  }
+  return (uint32_t)(product >> 32);
+}
+
+// std::shuffle as x86-64 Linux builds compile it (libstdc++): position i
+// (from 1 upwards) swaps with a uniform position in [0, i].  While
+// n^2 < 2^32 the draws come in pairs: for an even n position 1 first takes
+// one draw over {0, 1}; then positions i, i + 1 take one draw x over
+// [0, (i + 1)(i + 2)) and swap with x / (i + 2) and x % (i + 2).  Larger n
+// take one draw per position.
+static void shuffle_libstdcxx(std::vector<uint32_t>& v, std::mt19937& engine) {
+  const uint64_t n = v.size();
+  if (n < 2) return;
+  if (0xffffffffull / n >= n) {
+    uint64_t i = 1;
+    if (n % 2 == 0) {
+      std::swap(v[1], v[libstdcxx_uniform(engine, 2)]);
+      i = 2;
+    }
+    for (; i < n; i += 2) {
+      const uint64_t b0 = i + 1, b1 = i + 2;
+      const uint32_t x = libstdcxx_uniform(engine, b0 * b1);
+      std::swap(v[i], v[x / b1]);
+      std::swap(v[i + 1], v[x % b1]);
+    }
+    return;
+  }
+  for (uint64_t i = 1; i < n; ++i) std::swap(v[i], v[libstdcxx_uniform(engine, i + 1)]);
+}
+
+// std::shuffle as the reference's macOS builds compile it (libc++):
+// Fisher-Yates from the front, position pos swapping with pos + u, u uniform
+// in [0, n - pos) drawn by masking one engine output to the bit width of
+// n - pos - 1 and rejecting values >= n - pos.
+static void shuffle_libcxx(std::vector<uint32_t>& v, std::mt19937& engine) {
+  const size_t n = v.size();
+  for (size_t pos = 0; pos + 1 < n; ++pos) {
     const uint64_t range = n - pos;
     uint32_t width = 0;
     while (width < 32 && ((range - 1) >> width)) ++width;
     const uint32_t mask = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
     uint32_t u;
     do u = static_cast<uint32_t>(engine()) & mask; while (u >= range);
-    std::swap(order[pos], order[pos + u]);
+    std::swap(v[pos], v[pos + u]);
   }
+}
+
+void std_shuffle(std::vector<uint32_t>& order, std::mt19937& engine, ShuffleModel model) {
+  if (model == ShuffleModel::libcxx) shuffle_libcxx(order, engine);
+  else shuffle_libstdcxx(order, engine);
+}
+
+extern "C" int mgb_std_shuffle(uint32_t seed, uint32_t n, uint32_t model, uint32_t* order, uint32_t* next_draw) {
+  if (model > 1 || (n && !order)) return -1;
+  std::vector<uint32_t> v(n);
+  for (uint32_t i = 0; i < n; ++i) v[i] = i;
+  std::mt19937 engine(seed);
+  std_shuffle(v, engine, model == 1 ? ShuffleModel::libcxx : ShuffleModel::libstdcxx);
+  for (uint32_t i = 0; i < n; ++i) order[i] = v[i];
+  if (next_draw) *next_draw = (uint32_t)engine();
+  return 0;
+}
+
+ShuffleModel shuffle_model(const std::string& name) {
+  if (name == "libstdc++") return ShuffleModel::libstdcxx;
+  if (name == "libc++") return ShuffleModel::libcxx;
+  throw std::runtime_error("std_shuffle must be \"libstdc++\" or \"libc++\", got \"" + name + "\"");
 }
 
 // src/tree.cpp:15-26: "(1,0,-1)" or "[1,0,-1]", one entry per leading
@@ -607,7 +675,9 @@ const int32_t* Learner::monotone_constraints(uint32_t cols) {
 
 // src/tree.cpp:28-45 (kernels/tree_sample_columns.metal.h): a fresh engine
 // seeded by one draw shuffles the features; the first
-// max(1, floor(n * fraction)) of them are kept.
+// max(1, floor(n * fraction)) of them are kept.  The shuffle follows the
+// standard library named by `std_shuffle` (default libstdc++, as stock
+// XGBoost's x86-64 build; "libc++" gives the reference's macOS draws).
 const uint32_t* Learner::sample_columns(uint32_t cols) {
   const float fraction = fnumber("colsample_bytree", 1.0f);
   if (!(fraction < 1.0f) || cols == 0) return nullptr;
@@ -616,7 +686,7 @@ const uint32_t* Learner::sample_columns(uint32_t cols) {
   for (uint32_t i = 0; i < cols; ++i) order[i] = i;
   const float scaled = std::floor(static_cast<float>(cols) * fraction);
   const uint32_t keep = std::min<uint32_t>(cols, scaled < 1.0f ? 1u : static_cast<uint32_t>(scaled));
-  shuffle_prefix(order, engine, keep);
+  std_shuffle(order, engine, shuffle_model(param("std_shuffle", "libstdc++")));
   feature_flags_.assign(cols, 0u);
   for (uint32_t i = 0; i < keep; ++i) feature_flags_[order[i]] = 1u;
   d_features_.ensure((size_t)cols * sizeof(uint32_t));

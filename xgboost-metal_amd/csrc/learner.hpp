@@ -99,9 +99,13 @@ struct DMatrix {
   const std::vector<float>& get_info(const std::string& field) const;
 };
 
-// libc++'s std::shuffle of `order` with a 32-bit engine, stopped after the
-// first `positions` positions (order.size() - 1 for a full shuffle).
-void shuffle_prefix(std::vector<uint32_t>& order, std::mt19937& engine, size_t positions);
+// std::shuffle of `order` over a 32-bit engine, with the draws of either
+// standard library: libstdc++ (x86-64 Linux builds, stock XGBoost's wheels)
+// or libc++ (the reference's macOS builds).
+enum class ShuffleModel { libstdcxx, libcxx };
+void std_shuffle(std::vector<uint32_t>& order, std::mt19937& engine, ShuffleModel model);
+// "libstdc++" or "libc++"; anything else throws.
+ShuffleModel shuffle_model(const std::string& name);
 
 struct Tree {
   std::vector<MgbTreeNode> nodes;
