@@ -192,6 +192,23 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
                   const uint32_t* features, const int32_t* monotone, void* workspace, size_t workspace_bytes,
                   float* margin, MgbTreeNode* nodes, uint32_t* node_count);
 
+/* mgb_grow_tree without a workspace argument and without allocating: no
+ * counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving or online-update
+ * loops, harnesses that forbid hipMalloc).  The workspace is a static 64 MiB
+ * device array of the library (one per device, held until the process
+ * ends); shapes whose mgb_tree_workspace_bytes exceeds it are rejected with
+ * an error, as is a call while per-kernel timing is on (its events are
+ * created on demand).  Every call on a device shares and overwrites that
+ * device's scratch: the library enqueues all calls on its single stream,
+ * which orders them; calls that ran concurrently on one device would race.
+ * Nothing in the scratch needs to start at zero: each tree initialises its
+ * own state.  Other arguments and results as for mgb_grow_tree. */
+int mgb_grow_tree_noalloc(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const void* columns,
+                          const float* cuts, const uint32_t* counts, const float* grad, const float* scales,
+                          const MgbSplitParams* sp, const uint32_t* features, const int32_t* monotone, float* margin,
+                          MgbTreeNode* nodes, uint32_t* node_count);
+
 /* ---- CSR input (src/data.cpp:721-870 Matrix::sparse) ----------------- *
  * indptr holds rows+1 offsets into indices/values; column indices are
  * strictly increasing within a row; absent entries are missing values. */

@@ -15,6 +15,11 @@ constexpr int kWave = 64;
 
 // The library's single stream and last-error slot (defined in runtime.hip).
 hipStream_t stream();
+// The device the library is bound to (binding device 0 on first use), or -1
+// with the error set.
+int bound_device();
+// True while per-kernel timing (mgb_profile_enable) is on.
+bool profiling_enabled();
 void set_error(std::string message);
 int check(hipError_t status, const char* what);
 

@@ -63,6 +63,10 @@ static int ensure_init() {
   return mgb_init(0);
 }
 
+int bound_device() { return ensure_init() ? -1 : g_device; }
+
+bool profiling_enabled() { return g_profile.on; }
+
 }  // namespace mgb
 
 using namespace mgb;

@@ -14,8 +14,16 @@
 #include <cfloat>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "device_common.hpp"
+
+// Tree workspace of mgb_grow_tree_noalloc, for callers that cannot allocate:
+// one copy per device, from module load until the process ends.  Host code
+// never uses this name as an address: the device address comes from
+// hipGetSymbolAddress (scratch_address below).
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace mgb {
 namespace {
@@ -2241,6 +2249,65 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
     MGB_LAUNCH_CHECK("k_walk_dropped");
   }
   return 0;
+}
+
+}  // extern "C"
+
+namespace mgb {
+namespace {
+
+std::mutex g_scratch_mutex;
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the library's device, looked up once per
+// device with that device current (each device holds its own copy).
+int scratch_address(void** out) {
+  const int dev = bound_device();
+  if (dev < 0) return -1;
+  if (dev >= kMaxDevices) { set_error("mgb_grow_tree_noalloc: device index above 63"); return -1; }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    int current = -1;
+    MGB_CHECK(hipGetDevice(&current));
+    if (current != dev) MGB_CHECK(hipSetDevice(dev));
+    void* ptr = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (current != dev) MGB_CHECK(hipSetDevice(current));
+    MGB_CHECK(status);
+    if (!ptr) { set_error("hipGetSymbolAddress(scratch) returned a null address"); return -1; }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace mgb
+
+extern "C" {
+
+int mgb_grow_tree_noalloc(const MgbTreeShape* shape, const MgbMatrix* m, const void* bins, const void* columns,
+                          const float* cuts, const uint32_t* counts, const float* grad, const float* scales,
+                          const MgbSplitParams* sp, const uint32_t* features, const int32_t* monotone, float* margin,
+                          MgbTreeNode* nodes, uint32_t* node_count) {
+  if (!shape || !m || !sp) { set_error("mgb_grow_tree_noalloc: null shape, matrix or parameters"); return -1; }
+  if (validate(shape, m)) return -1;
+  const size_t need = layout(*shape).total;
+  if (need > kNoAllocScratchBytes) {
+    set_error("mgb_grow_tree_noalloc: this tree shape needs " + std::to_string(need) +
+              " bytes of workspace, above the " + std::to_string(kNoAllocScratchBytes) +
+              "-byte allocation-free scratch; use mgb_grow_tree with a workspace");
+    return -1;
+  }
+  if (profiling_enabled()) {
+    set_error("mgb_grow_tree_noalloc: per-kernel timing creates HIP events; disable mgb_profile_enable first");
+    return -1;
+  }
+  void* ws = nullptr;
+  if (scratch_address(&ws)) return -1;
+  return mgb_grow_tree(shape, m, bins, columns, cuts, counts, grad, scales, sp, features, monotone, ws,
+                       kNoAllocScratchBytes, margin, nodes, node_count);
 }
 
 }  // extern "C"
