@@ -168,6 +168,9 @@ XGB_DLL int XGBoosterGetStrFeatureInfo(BoosterHandle handle, const char* field, 
 /* Engine profile as JSON (device seconds per phase); counterpart of the
  * reference's XGBoosterMetalProfile (c_api.cpp:617-633). */
 XGB_DLL int XGBoosterHipProfile(BoosterHandle handle, const char** out);
+/* Engine extension: copy a matrix's values, labels and weights to the device
+ * now (they are otherwise copied at first use) and wait for the copy. */
+XGB_DLL int XGDMatrixHipUpload(DMatrixHandle handle);
 
 /* --- single process and unsupported inputs --------------------------------
  * One process, one GPU: the communicator reports rank 0 of 1 and its

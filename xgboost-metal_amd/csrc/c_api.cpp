@@ -1063,6 +1063,20 @@ int XGBoosterHipProfile(BoosterHandle handle, const char** out) {
   API_END
 }
 
+// Engine extension: the matrix's values, labels and weights are copied to the
+// device when first used (quantization, prediction); this copies them now and
+// waits, so that a caller can time training on device-resident input, as the
+// reference's DMatrix construction fills its device buffers up front
+// (src/data.cpp:485-520).
+int XGDMatrixHipUpload(DMatrixHandle handle) {
+  API_BEGIN
+  auto& m = matrix(handle);
+  m->upload();
+  m->upload_info();
+  kcheck(mgb_synchronize(), "synchronize");
+  API_END
+}
+
 // ---------------------------------------------------------------------------
 // Other layouts, iterators, slicing (c_api.cpp:195-313)
 // ---------------------------------------------------------------------------

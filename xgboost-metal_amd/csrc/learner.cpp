@@ -807,9 +807,14 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
     const double row_bytes =
         data.sparse ? (double)data.values.size() / std::max(1u, data.rows) * (4 + data.matrix.bin_bytes) + 8 + 12
                     : (double)data.cols * data.matrix.bin_bytes + 12;
+    // Split scan: the root reads its histogram once; below it each sibling
+    // pair reads the parent's and the built child's histograms and writes the
+    // sibling's (16 bytes per feature and bin each).
+    const uint64_t node_hist = (uint64_t)data.cols * (data.hist_bins + 1) * 16;
     for (uint32_t d = 0; d < depth && d < 32; ++d) {
-      hist_bytes_ += (uint64_t)(rows[d] * row_bytes) + (uint64_t)built[d] * data.cols * (data.hist_bins + 1) * 16;
+      hist_bytes_ += (uint64_t)(rows[d] * row_bytes) + (uint64_t)built[d] * node_hist;
       hist_rows_ += rows[d];
+      split_bytes_ += (d == 0 ? 1u : 3u) * (uint64_t)built[d] * node_hist;
     }
   }
 }
@@ -1258,6 +1263,7 @@ Json Learner::profile() const {
   out["kernels"] = kernels;
   out["histogram_bytes"] = Json(hist_bytes_);
   out["histogram_rows"] = Json(hist_rows_);
+  out["split_bytes"] = Json(split_bytes_);
   return out;
 }
 

@@ -10,7 +10,6 @@ from __future__ import annotations
 import ctypes
 import json
 import os
-import sys
 import weakref
 from abc import ABC, abstractmethod
 from typing import Any, Callable, Dict, Iterable, List, Optional, Sequence, Tuple, Union
@@ -100,13 +99,14 @@ def _missing_value(missing: Optional[float]) -> Optional[float]:
 
 
 class DataIter(ABC):
-    """User-defined batch iterator (reference core.py:275).
+    """User-defined batch iterator (the reference's core.py:275 interface).
 
-    ``next(input_data)`` calls ``input_data(data=..., label=..., ...)`` once per
-    batch and returns False after the last; ``reset()`` rewinds.  The batches
-    are concatenated in host memory: ``cache_prefix`` (external memory) is
-    rejected.  Exceptions raised inside the callbacks are held and re-raised
-    after the C call returns, as upstream does.
+    ``next(input_data)`` passes one batch by calling
+    ``input_data(data=..., label=..., weight=..., ...)`` and returns True, or
+    returns False after the last batch; ``reset()`` rewinds.  The engine
+    concatenates the batches in host memory, so ``cache_prefix`` (external
+    memory) is rejected.  An exception raised in ``next`` or ``reset`` ends the
+    iteration and is raised again when the DMatrix construction returns.
     """
 
     def __init__(self, cache_prefix: Optional[str] = None, release_data: bool = True, *, on_host: bool = True,
@@ -114,58 +114,13 @@ class DataIter(ABC):
         self.cache_prefix = cache_prefix
         self.on_host = on_host
         self.min_cache_page_bytes = min_cache_page_bytes
-        self._handle = _ProxyDMatrix()
-        self._exception: Optional[BaseException] = None
-        self._enable_categorical = False
-        self._release = release_data
-        self._temporary_data: Optional[Any] = None
-        self._callbacks: Optional[Tuple[Callable, Callable]] = None
-
-    def get_callbacks(self, enable_categorical: bool) -> Tuple[Callable, Callable]:
-        """C function pointers for reset and next; kept alive by the iterator."""
-        reset = ctypes.CFUNCTYPE(None, ctypes.c_void_p)(self._reset_wrapper)
-        nxt = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)(self._next_wrapper)
-        self._enable_categorical = enable_categorical
-        self._callbacks = (reset, nxt)
-        return reset, nxt
+        self.release_data = release_data
+        self._proxy = _ProxyDMatrix()
 
     @property
     def proxy(self) -> "_ProxyDMatrix":
-        return self._handle
-
-    def _handle_exception(self, fn: Callable, default: Any) -> Any:
-        if self._exception is not None:
-            return default
-        try:
-            return fn()
-        except Exception as e:  # pylint: disable=broad-except
-            # A Python exception cannot cross the C callback: keep it, end
-            # the iteration, and raise it after the C call returns.
-            self._exception = e.with_traceback(sys.exc_info()[2])
-        return default
-
-    def reraise(self) -> None:
-        self._temporary_data = None
-        if self._exception is not None:
-            exc, self._exception = self._exception, None
-            raise exc
-
-    def _reset_wrapper(self, this: None) -> None:
-        if self._release:
-            self._temporary_data = None
-        self._handle_exception(self.reset, None)
-
-    def _next_wrapper(self, this: None) -> int:
-        def input_data(*, data: Any, feature_names: Optional[Sequence[str]] = None,
-                       feature_types: Optional[Sequence[str]] = None, **kwargs: Any) -> None:
-            if feature_names is None:
-                feature_names = _feature_names_of(data)
-            self._temporary_data = self.proxy._set_data(data)
-            self.proxy.set_info(feature_names=feature_names, feature_types=feature_types, **kwargs)
-
-        if self._release:
-            self._temporary_data = None
-        return self._handle_exception(lambda: int(self.next(input_data)), 0)
+        """The proxy matrix each batch is staged in for the C library."""
+        return self._proxy
 
     @abstractmethod
     def reset(self) -> None:
@@ -176,6 +131,68 @@ class DataIter(ABC):
     def next(self, input_data: Callable) -> bool:
         """Pass the next batch to ``input_data``; False when there is none."""
         raise NotImplementedError()
+
+
+_RESET_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p)
+_NEXT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+
+
+class _IterationBridge:
+    """One C call that pulls a DataIter's batches through reset/next
+    function pointers.
+
+    A Python exception cannot unwind through the library's C frames: the
+    first one raised by the iterator is stored, every later callback answers
+    "no more batches", and ``call`` raises it once the C function has
+    returned.  The current batch's arrays stay referenced until the library
+    has copied them (the next callback, or the end of the call when the
+    iterator keeps its data)."""
+
+    def __init__(self, it: DataIter) -> None:
+        self._it = it
+        self._failure: Optional[BaseException] = None
+        self._staged: Any = None
+        self._reset_fn = _RESET_FN(self._on_reset)
+        self._next_fn = _NEXT_FN(self._on_next)
+
+    def _guarded(self, action: Callable[[], Any], on_failure: Any) -> Any:
+        if self._failure is not None:
+            return on_failure
+        try:
+            return action()
+        except Exception as failure:  # pylint: disable=broad-except
+            self._failure = failure
+            return on_failure
+
+    def _on_reset(self, _context: Any) -> None:
+        if self._it.release_data:
+            self._staged = None
+        self._guarded(self._it.reset, None)
+
+    def _on_next(self, _context: Any) -> int:
+        if self._it.release_data:
+            self._staged = None
+        return self._guarded(lambda: 1 if self._it.next(self._stage) else 0, 0)
+
+    def _stage(self, *, data: Any, feature_names: Optional[Sequence[str]] = None,
+               feature_types: Optional[Sequence[str]] = None, **info: Any) -> None:
+        proxy = self._it.proxy
+        self._staged = proxy._set_data(data)
+        proxy.set_info(feature_names=_feature_names_of(data) if feature_names is None else feature_names,
+                       feature_types=feature_types, **info)
+
+    def call(self, invoke: Callable[[Any, Any], int]) -> int:
+        """invoke(reset, next) calls the C function with the two function
+        pointers; the iterator's first exception, if any, is raised after it
+        returns."""
+        try:
+            ret = invoke(self._reset_fn, self._next_fn)
+        finally:
+            self._staged = None
+        if self._failure is not None:
+            failure, self._failure = self._failure, None
+            raise failure
+        return ret
 
 
 class _SingleBatchIter(DataIter):
@@ -245,11 +262,9 @@ class DMatrix:
         """Concatenate an iterator's batches in memory (reference core.py:862)."""
         if it.cache_prefix:
             raise XGBoostError("External memory (cache_prefix) is not supported by this engine")
-        reset, nxt = it.get_callbacks(False)
         config = json.dumps({"missing": _missing_value(missing), "cache_prefix": "", "nthread": 0}).encode()
-        ret = _LIB.XGDMatrixCreateFromCallback(None, it.proxy.handle, reset, nxt, config, ctypes.byref(self.handle))
-        it.reraise()
-        _check_call(ret)
+        _check_call(_IterationBridge(it).call(lambda reset, nxt: _LIB.XGDMatrixCreateFromCallback(
+            None, it.proxy.handle, reset, nxt, config, ctypes.byref(self.handle))))
 
     def __del__(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:
@@ -379,6 +394,12 @@ class DMatrix:
     def feature_types(self, types: Optional[Sequence[str]]) -> None:
         self._set_str_info("feature_type", types)
 
+    def to_device(self) -> "DMatrix":
+        """Engine extension: copy the values, labels and weights to the GPU now
+        (otherwise done when training or prediction first needs them)."""
+        _check_call(_LIB.XGDMatrixHipUpload(self.handle))
+        return self
+
     def get_quantile_cut(self) -> Tuple[np.ndarray, np.ndarray]:
         """Histogram cut points: (indptr, values) per feature."""
         indptr = ctypes.c_char_p()
@@ -451,13 +472,10 @@ class QuantileDMatrix(DMatrix):
             if it.cache_prefix:
                 raise XGBoostError("External memory (cache_prefix) is not supported by this engine")
             self.handle = ctypes.c_void_p()
-            reset, nxt = it.get_callbacks(enable_categorical)
             config = json.dumps({"missing": _missing_value(missing), "nthread": 0, "max_bin": self.max_bin}).encode()
-            ret = _LIB.XGQuantileDMatrixCreateFromCallback(None, it.proxy.handle,
-                                                           ref.handle if ref is not None else None, reset, nxt,
-                                                           config, ctypes.byref(self.handle))
-            it.reraise()
-            _check_call(ret)
+            ref_handle = ref.handle if ref is not None else None
+            _check_call(_IterationBridge(it).call(lambda reset, nxt: _LIB.XGQuantileDMatrixCreateFromCallback(
+                None, it.proxy.handle, ref_handle, reset, nxt, config, ctypes.byref(self.handle))))
             self.set_info(label=label, weight=weight, base_margin=base_margin, feature_names=feature_names,
                           feature_types=feature_types)
             return
