@@ -86,6 +86,13 @@ int mgb_init(int device) {
   // Default priority on purpose: streams of different priorities are not used.
   MGB_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   for (auto& e : g_events) MGB_CHECK(hipEventCreate(&e));
+  // Stream-ordered allocations (the quantile sketch's temporaries) return to
+  // the device's default pool; keep up to 4 GiB of it mapped between passes
+  // instead of releasing it at every synchronisation.
+  hipMemPool_t pool = nullptr;
+  MGB_CHECK(hipDeviceGetDefaultMemPool(&pool, device));
+  uint64_t keep = uint64_t(4) << 30;
+  MGB_CHECK(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep));
   g_device = device;
   return 0;
 }

@@ -1,19 +1,31 @@
 // Weighted quantile sketch on the GPU: the per-feature cut points of the
 // reference's hist method (src/quantile.cpp:22-212, kernels/quantile.metal.h,
-// XGBoost's WQSummary semantics).
+// XGBoost's WQSummary semantics).  Features are processed in groups of at
+// most kChunkEntries entries; for each group:
 //
-//  1. transpose the row-major matrix to columns (coalesced reads per feature);
-//  2. one workgroup per feature finds runs of equal values in row order
-//     (ballot + block scan), with run weights = run length or an in-order
-//     binary32 weight sum;
-//  3. the host plans batches of 2*limit runs (limit = sketch budget);
-//  4. one segmented radix sort orders every batch by (value, position);
-//  5. one workgroup per feature summarizes each batch, prunes, merges it into
-//     the level stack, and finally selects the cuts.  Summaries, prunes and
-//     merges are data-parallel restatements of the serial rules: prune
-//     positions come from binary searches over monotone rank sums, merges from
-//     merge-path ranks, and the error fix-up from prefix maxima, so every
-//     binary32 rounding step is the same operation on the same operands.
+//  1. (dense input) transpose the group's columns (coalesced reads per feature);
+//  2. runs of equal values in row order over each feature's non-missing,
+//     nonzero-weight entries, in 1024-entry blocks: per-block counts, a
+//     per-feature scan over blocks that joins runs crossing block edges, the
+//     runs written at their scanned offsets, then each run's weight (its
+//     length, or the in-order binary32 sum of its entries' weights);
+//  3. the host plans batches of 2*limit runs (limit = sketch budget) from the
+//     per-feature counts;
+//  4. a segmented, stable radix sort orders every batch's runs by value;
+//  5. one workgroup per batch summarizes it and prunes the summary to limit;
+//  6. the serial rule merges batch summaries through a stack of levels like a
+//     binary counter (kernels/quantile.metal.h:317-352): while every merge
+//     yields more than `limit` entries that is a balanced tree, computed here
+//     one level per launch with one workgroup per node; a feature where some
+//     merge yields fewer (many equal values) is redone serially by the
+//     finishing kernel from its batch summaries;
+//  7. one workgroup per feature merges the tree's roots (the stack's final
+//     contents), prunes to the budget and selects the cuts.
+// Summaries, prunes and merges are data-parallel restatements of the serial
+// rules: prune positions come from binary searches over monotone rank sums,
+// merges from merge-path ranks, the error fix-up from prefix maxima, and
+// sequential binary32 sums stay sequential, so every rounding step is the
+// same operation on the same operands.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
@@ -27,14 +39,47 @@ namespace mgb {
 namespace {
 
 constexpr uint32_t kSketchThreads = 1024;
+constexpr uint32_t kBlockEntries = 1024;                 // entries per workgroup in the run passes
+constexpr uint64_t kChunkEntries = uint64_t(1) << 27;    // entries per group of features
+constexpr uint32_t kMaxGroupFeatures = 65535;            // features per group
 
 struct SkEntry { float rmin, rmax, wmin, value; };
 struct SkStats { uint32_t nonmissing, elements, runs, padding; };
-struct SkFeature {
-  uint64_t lvl_offset, work_offset, scratch_offset;  // entries / words
-  uint32_t limit, budget, batches, levels;
-  uint32_t exact_integer, padding;
+
+// Runs of one 1024-entry block of a feature.  `runs` counts the block's first
+// valid entry as a run start; k_run_scan fills the offsets and the last valid
+// value before the block.
+struct SkBlock {
+  uint32_t valid, present, runs, has;
+  float first, last;
+  uint32_t elem_off, run_off;
+  uint32_t prev_has;
+  float prev;
 };
+
+// Plan of one feature.  Tree node n (level l, index k: n = first(l) + k,
+// first(l) = sum over j < l of batches >> j) covers batches
+// [k 2^l, (k + 1) 2^l) and holds at most `limit` entries at
+// tree + n * limit.
+struct SkFeature {
+  uint64_t base;        // first entry of the feature in the group's entry arrays
+  uint64_t tree;        // first SkEntry of its tree nodes
+  uint64_t fin;         // first SkEntry of its finishing buffers
+  uint64_t scratch;     // first word of its per-node scratch (node k of a level: + k * (2 limit + 2))
+  uint64_t fin_scratch; // first word of its finishing scratch
+  uint32_t node_base;   // first slot of its node counts
+  uint32_t limit, budget, batches;
+  uint32_t levels;      // bit_width(batches) + 1: the serial stack's depth
+  uint32_t exact;       // integer run weights summing below 2^24
+  uint32_t final_cap;   // max(budget, limit)
+  uint32_t padding;
+};
+
+__host__ __device__ inline uint32_t level_first(uint32_t batches, uint32_t level) {
+  uint32_t s = 0;
+  for (uint32_t j = 0; j < level && j < 32; ++j) s += batches >> j;
+  return s;
+}
 
 __device__ __forceinline__ uint32_t order_key(float v) {
   uint32_t bits = __float_as_uint(v);
@@ -43,112 +88,222 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 __device__ __forceinline__ float min_next(const SkEntry& e) { return e.rmin + e.wmin; }
 __device__ __forceinline__ float max_prev(const SkEntry& e) { return e.rmax - e.wmin; }
 
-__global__ void k_transpose(const float* __restrict__ X, uint32_t rows, uint32_t cols, float* __restrict__ Xt) {
+// Columns [col0, col0 + ncols) of a row-major rows x cols matrix into
+// column-major Xt (ncols columns of `rows` entries).
+__global__ void k_transpose(const float* __restrict__ X, uint32_t rows, uint32_t cols, uint32_t col0, uint32_t ncols,
+                            float* __restrict__ Xt) {
   __shared__ float tile[32][33];
-  uint32_t c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const uint32_t r0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
   for (uint32_t k = threadIdx.y; k < 32; k += blockDim.y) {
-    uint32_t r = r0 + k, c = c0 + threadIdx.x;
-    if (r < rows && c < cols) tile[k][threadIdx.x] = X[(uint64_t)r * cols + c];
+    const uint32_t r = r0 + k, c = c0 + threadIdx.x;
+    if (r < rows && c < ncols) tile[k][threadIdx.x] = X[(uint64_t)r * cols + col0 + c];
   }
   __syncthreads();
   for (uint32_t k = threadIdx.y; k < 32; k += blockDim.y) {
-    uint32_t c = c0 + k, r = r0 + threadIdx.x;
-    if (r < rows && c < cols) Xt[(uint64_t)c * rows + r] = tile[threadIdx.x][k];
+    const uint32_t c = c0 + k, r = r0 + threadIdx.x;
+    if (r < rows && c < ncols) Xt[(uint64_t)c * rows + r] = tile[threadIdx.x][k];
   }
 }
 
-// Runs of equal values over a feature's non-missing, nonzero-weight entries in
-// row order (kernels/quantile.metal.h:19-140).  Feature f's entries are
-// vals[seg[f] .. seg[f+1]) in row order: a column of the transposed dense
-// matrix (row = position) or of the column-major copy of a CSR matrix (row =
-// row_of[position]); entries absent from a CSR column are missing values and
-// take no part, exactly like NaN entries of a dense column.
-__global__ __launch_bounds__(kSketchThreads) void k_runs(const float* __restrict__ vals, const uint64_t* __restrict__ seg,
-                                                         const uint32_t* __restrict__ row_of,
-                                                         const float* __restrict__ weights,
-                                                         float* __restrict__ run_v, float* __restrict__ run_w,
-                                                         uint32_t* __restrict__ run_start, float* __restrict__ elem_w,
-                                                         SkStats* __restrict__ stats) {
-  __shared__ uint32_t scan[kSketchThreads / kWave + 1];
-  __shared__ uint32_t wave_has[kSketchThreads / kWave];
-  __shared__ float wave_last[kSketchThreads / kWave];
+// One entry per thread of block blockIdx.x of feature blockIdx.y: is it
+// present (not NaN) and valid (present with a nonzero weight), and the last
+// valid value before it within the block.  Also the block's first and last
+// valid values.  `s_*` hold one slot per wave.
+struct EntryView {
+  float v, w;
+  bool present, valid, have_prev;
+  float prev;
+};
+
+__device__ __forceinline__ EntryView view_entry(const float* __restrict__ vals, const uint64_t* __restrict__ seg,
+                                                const uint32_t* __restrict__ row_of, const float* __restrict__ weights,
+                                                uint32_t* s_has, float* s_first, float* s_last, bool& block_has,
+                                                float& block_first, float& block_last) {
+  const uint32_t c = blockIdx.y;
+  const uint64_t base = seg[c];
+  const uint32_t count = (uint32_t)(seg[c + 1] - base);
+  const uint32_t r = blockIdx.x * kBlockEntries + threadIdx.x;
+  const bool in = r < count;
+  EntryView e;
+  e.v = in ? vals[base + r] : __uint_as_float(0x7fc00000u);
+  e.w = (in && weights) ? weights[row_of ? row_of[base + r] : r] : 1.0f;
+  e.present = in && !isnan(e.v);
+  e.valid = e.present && (__float_as_uint(e.w) & 0x7fffffffu) != 0;
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  const uint64_t mask = __ballot(e.valid);
+  const uint64_t below = mask & ((uint64_t(1) << lane) - 1);
+  e.prev = __shfl(e.v, below ? 63 - __clzll(below) : 0, kWave);
+  e.have_prev = below != 0;
+  const float first_in_wave = __shfl(e.v, mask ? __ffsll((long long)mask) - 1 : 0, kWave);
+  const float last_in_wave = __shfl(e.v, mask ? 63 - __clzll(mask) : 0, kWave);
+  if (lane == 0) {
+    s_has[wave] = mask != 0;
+    s_first[wave] = first_in_wave;
+    s_last[wave] = last_in_wave;
+  }
+  __syncthreads();
+  if (!e.have_prev) {
+    for (int k = (int)wave - 1; k >= 0; --k)
+      if (s_has[k]) { e.prev = s_last[k]; e.have_prev = true; break; }
+  }
+  block_has = false;
+  for (uint32_t k = 0; k < waves; ++k)
+    if (s_has[k]) { block_has = true; block_first = s_first[k]; break; }
+  for (int k = (int)waves - 1; k >= 0; --k)
+    if (s_has[k]) { block_last = s_last[k]; break; }
+  return e;
+}
+
+__global__ __launch_bounds__(kSketchThreads) void k_run_count(const float* __restrict__ vals,
+                                                              const uint64_t* __restrict__ seg,
+                                                              const uint32_t* __restrict__ row_of,
+                                                              const float* __restrict__ weights, uint32_t max_blocks,
+                                                              SkBlock* __restrict__ blocks) {
+  __shared__ uint32_t s_has[kSketchThreads / kWave], scan[kSketchThreads / kWave + 1];
+  __shared__ float s_first[kSketchThreads / kWave], s_last[kSketchThreads / kWave];
+  const uint32_t c = blockIdx.y;
+  if ((uint64_t)blockIdx.x * kBlockEntries >= seg[c + 1] - seg[c]) return;  // the whole block is past the feature
+  bool has = false;
+  float first = 0.0f, last = 0.0f;
+  const EntryView e = view_entry(vals, seg, row_of, weights, s_has, s_first, s_last, has, first, last);
+  const bool new_run = e.valid && (!e.have_prev || e.v != e.prev);
+  uint32_t valid, present, runs;
+  block_exclusive_u32(e.valid ? 1u : 0u, scan, &valid);
+  block_exclusive_u32(e.present ? 1u : 0u, scan, &present);
+  block_exclusive_u32(new_run ? 1u : 0u, scan, &runs);
+  if (threadIdx.x == 0) {
+    SkBlock b{};
+    b.valid = valid; b.present = present; b.runs = runs; b.has = has ? 1u : 0u;
+    b.first = first; b.last = last;
+    blocks[(uint64_t)c * max_blocks + blockIdx.x] = b;
+  }
+}
+
+// One workgroup per feature: offsets of its blocks' elements and runs, with a
+// block whose first valid value equals the last valid value before it
+// continuing that run; the feature's totals.
+__global__ __launch_bounds__(kSketchThreads) void k_run_scan(const uint64_t* __restrict__ seg, uint32_t max_blocks,
+                                                             SkBlock* __restrict__ blocks,
+                                                             SkStats* __restrict__ stats) {
+  __shared__ uint32_t s_has[kSketchThreads / kWave], scan[kSketchThreads / kWave + 1];
+  __shared__ float s_last[kSketchThreads / kWave];
   __shared__ uint32_t carry_has;
   __shared__ float carry_last;
-  const uint32_t f = blockIdx.x;
-  const uint64_t base = seg[f];
-  const uint32_t rows = (uint32_t)(seg[f + 1] - base);  // entries of this feature
-  const float* col = vals + base;
+  const uint32_t c = blockIdx.x;
+  const uint64_t count = seg[c + 1] - seg[c];
+  const uint32_t nblocks = (uint32_t)((count + kBlockEntries - 1) / kBlockEntries);
+  SkBlock* fb = blocks + (uint64_t)c * max_blocks;
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
-  uint32_t elements = 0, runs = 0, nonmissing = 0;
-  if (threadIdx.x == 0) { carry_has = 0; carry_last = 0; }
+  uint32_t elements = 0, runs = 0, present = 0;
+  if (threadIdx.x == 0) { carry_has = 0; carry_last = 0.0f; }
   __syncthreads();
-  for (uint32_t t0 = 0; t0 < rows; t0 += blockDim.x) {
-    const uint32_t r = t0 + threadIdx.x;
-    float v = r < rows ? col[r] : __uint_as_float(0x7fc00000u);
-    float w = (r < rows && weights) ? weights[row_of ? row_of[base + r] : r] : 1.0f;
-    const bool present = !isnan(v);
-    const bool valid = present && (__float_as_uint(w) & 0x7fffffffu) != 0;
-    const uint64_t mask = __ballot(valid);
-    const uint64_t below = mask & (lane ? (~0ull >> (64 - lane)) : 0ull);
-    float prev = __shfl(v, below ? 63 - __clzll(below) : 0, kWave);
+  for (uint32_t t0 = 0; t0 < nblocks; t0 += blockDim.x) {
+    const uint32_t b = t0 + threadIdx.x;
+    const bool in = b < nblocks;
+    SkBlock blk{};
+    if (in) blk = fb[b];
+    const bool has = in && blk.has;
+    const uint64_t mask = __ballot(has);
+    const uint64_t below = mask & ((uint64_t(1) << lane) - 1);
+    float prev = __shfl(blk.last, below ? 63 - __clzll(below) : 0, kWave);
     bool have_prev = below != 0;
-    const float last_in_wave = __shfl(v, mask ? 63 - __clzll(mask) : 0, kWave);
-    if (lane == 0) {
-      wave_has[wave] = mask != 0;
-      wave_last[wave] = last_in_wave;
-    }
+    const float last_in_wave = __shfl(blk.last, mask ? 63 - __clzll(mask) : 0, kWave);
+    if (lane == 0) { s_has[wave] = mask != 0; s_last[wave] = last_in_wave; }
     __syncthreads();
     if (!have_prev) {
-      for (int k = (int)wave - 1; k >= 0; --k) {
-        if (wave_has[k]) { prev = wave_last[k]; have_prev = true; break; }
-      }
+      for (int k = (int)wave - 1; k >= 0; --k)
+        if (s_has[k]) { prev = s_last[k]; have_prev = true; break; }
       if (!have_prev && carry_has) { prev = carry_last; have_prev = true; }
     }
-    const bool new_run = valid && (!have_prev || v != prev);
-    uint32_t total_valid, total_runs, total_present;
-    const uint32_t eidx = elements + block_exclusive_u32(valid ? 1u : 0u, scan, &total_valid);
-    const uint32_t ridx = runs + block_exclusive_u32(new_run ? 1u : 0u, scan, &total_runs);
-    block_exclusive_u32(present ? 1u : 0u, scan, &total_present);
-    if (valid && weights) elem_w[base + eidx] = w;
-    if (new_run) { run_v[base + ridx] = v; run_start[base + ridx] = eidx; }
-    elements += total_valid;
-    runs += total_runs;
-    nonmissing += total_present;
-    if (threadIdx.x == 0) {
-      for (int k = (int)waves - 1; k >= 0; --k)
-        if (wave_has[k]) { carry_has = 1; carry_last = wave_last[k]; break; }
+    const uint32_t adj = in ? blk.runs - ((has && have_prev && blk.first == prev) ? 1u : 0u) : 0u;
+    uint32_t te, tr, tp;
+    const uint32_t eoff = elements + block_exclusive_u32(in ? blk.valid : 0u, scan, &te);
+    const uint32_t roff = runs + block_exclusive_u32(adj, scan, &tr);
+    block_exclusive_u32(in ? blk.present : 0u, scan, &tp);
+    if (in) {
+      fb[b].elem_off = eoff;
+      fb[b].run_off = roff;
+      fb[b].prev_has = have_prev ? 1u : 0u;
+      fb[b].prev = prev;
     }
+    elements += te;
+    runs += tr;
+    present += tp;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int k = (int)waves - 1; k >= 0; --k)
+        if (s_has[k]) { carry_has = 1; carry_last = s_last[k]; break; }
     __syncthreads();
   }
-  for (uint32_t k = threadIdx.x; k < runs; k += blockDim.x) {
-    uint32_t s = run_start[base + k];
-    uint32_t e = k + 1 < runs ? run_start[base + k + 1] : elements;
-    float w;
-    if (!weights) {
-      uint32_t len = e - s;
-      w = (float)(len < (1u << 24) ? len : (1u << 24));
-    } else {
-      w = elem_w[base + s];
-      for (uint32_t i = s + 1; i < e; ++i) w = w + elem_w[base + i];
-    }
-    run_w[base + k] = w;
+  if (threadIdx.x == 0) stats[c] = SkStats{present, elements, runs, 0};
+}
+
+// The runs of each block at their scanned offsets: run_v (value), run_start
+// (element index within the feature) and, with weights, each valid entry's
+// weight at its element index.
+__global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __restrict__ vals,
+                                                             const uint64_t* __restrict__ seg,
+                                                             const uint32_t* __restrict__ row_of,
+                                                             const float* __restrict__ weights, uint32_t max_blocks,
+                                                             const SkBlock* __restrict__ blocks,
+                                                             float* __restrict__ run_v, uint32_t* __restrict__ run_start,
+                                                             float* __restrict__ elem_w) {
+  __shared__ uint32_t s_has[kSketchThreads / kWave], scan[kSketchThreads / kWave + 1];
+  __shared__ float s_first[kSketchThreads / kWave], s_last[kSketchThreads / kWave];
+  const uint32_t c = blockIdx.y;
+  const uint64_t base = seg[c];
+  if ((uint64_t)blockIdx.x * kBlockEntries >= seg[c + 1] - base) return;
+  const SkBlock blk = blocks[(uint64_t)c * max_blocks + blockIdx.x];
+  bool has = false;
+  float first = 0.0f, last = 0.0f;
+  EntryView e = view_entry(vals, seg, row_of, weights, s_has, s_first, s_last, has, first, last);
+  if (!e.have_prev && blk.prev_has) { e.prev = blk.prev; e.have_prev = true; }
+  const bool new_run = e.valid && (!e.have_prev || e.v != e.prev);
+  uint32_t tv, tr;
+  const uint32_t eidx = blk.elem_off + block_exclusive_u32(e.valid ? 1u : 0u, scan, &tv);
+  const uint32_t ridx = blk.run_off + block_exclusive_u32(new_run ? 1u : 0u, scan, &tr);
+  if (new_run) {
+    run_v[base + ridx] = e.v;
+    run_start[base + ridx] = eidx;
   }
-  if (threadIdx.x == 0) stats[f] = SkStats{nonmissing, elements, runs, 0};
+  if (e.valid && weights) elem_w[base + eidx] = e.w;
 }
 
-// One workgroup per feature: sort keys (value order, run index) of its runs.
-__global__ void k_keys(const float* __restrict__ run_v, const SkStats* __restrict__ stats,
-                       const uint64_t* __restrict__ seg, uint64_t* __restrict__ keys) {
-  const uint32_t f = blockIdx.x;
-  const uint64_t base = seg[f];
-  const uint32_t runs = stats[f].runs;
-  for (uint32_t k = threadIdx.x; k < runs; k += blockDim.x)
-    keys[base + k] = ((uint64_t)order_key(run_v[base + k]) << 32) | k;
+// Each run's weight: its length (below 2^24) or, with weights, the binary32
+// sum of its entries' weights in row order (kernels/quantile.metal.h:19-140).
+__global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
+                              const uint32_t* __restrict__ run_start, const float* __restrict__ elem_w,
+                              float* __restrict__ run_w) {
+  const uint32_t c = blockIdx.y;
+  const uint64_t base = seg[c];
+  const SkStats st = stats[c];
+  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= st.runs) return;
+  const uint32_t s = run_start[base + k];
+  const uint32_t e = k + 1 < st.runs ? run_start[base + k + 1] : st.elements;
+  float w;
+  if (!elem_w) {
+    const uint32_t len = e - s;
+    w = (float)(len < (1u << 24) ? len : (1u << 24));
+  } else {
+    w = elem_w[base + s];
+    for (uint32_t i = s + 1; i < e; ++i) w = w + elem_w[base + i];
+  }
+  run_w[base + k] = w;
 }
 
-// ---------------------------------------------------------------------------
-// Per-feature reduction.
-// ---------------------------------------------------------------------------
+// Sort keys (value order) and payloads (run index) of every run.
+__global__ void k_sort_keys(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
+                            const float* __restrict__ run_v, uint32_t* __restrict__ keys,
+                            uint32_t* __restrict__ index) {
+  const uint32_t c = blockIdx.y;
+  const uint64_t base = seg[c];
+  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= stats[c].runs) return;
+  keys[base + k] = order_key(run_v[base + k]);
+  index[base + k] = k;
+}
+
 __device__ __forceinline__ uint32_t block_inclusive_max_u32(uint32_t v, uint32_t* shared) {
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
 #pragma unroll
@@ -339,132 +494,222 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
   return count;
 }
 
-// Summary of one sorted batch (kernels/quantile.metal.h:216-240).
-__device__ uint32_t summarize(const uint64_t* keys, const float* run_v, const float* run_w, uint32_t size, bool exact,
-                              SkEntry* out, uint32_t* scratch, uint32_t* scan) {
-  if (!exact) {
-    __shared__ uint32_t result;
-    if (threadIdx.x == 0) {
-      uint32_t n = 0;
-      float total = 0;
-      for (uint32_t i = 0; i < size;) {
-        uint32_t k = (uint32_t)keys[i];
-        float value = run_v[k], weight = run_w[k];
-        uint32_t j = i + 1;
-        while (j < size && run_v[(uint32_t)keys[j]] == value) weight = weight + run_w[(uint32_t)keys[j++]];
-        out[n++] = SkEntry{total, total + weight, weight, value};
-        total = total + weight;
-        i = j;
-      }
-      result = n;
-    }
-    __syncthreads();
-    return result;
-  }
-  // Integer weights with a total below 2^24: every binary32 partial sum is
-  // exact, so a parallel prefix reproduces the serial sums bit for bit.
+
+// Summary of one sorted batch (kernels/quantile.metal.h:216-240): one entry
+// per distinct value, in value order, holding the value's weight w (the
+// binary32 sum of its runs' weights in sort order) and the running binary32
+// total before (rmin) and after (rmax) it.  index[0..size) are the batch's
+// run indices in value order; scratch needs size + 1 words.
+__device__ uint32_t summarize(const uint32_t* __restrict__ index, const float* __restrict__ run_v,
+                              const float* __restrict__ run_w, uint32_t size, bool exact, SkEntry* out,
+                              uint32_t* scratch, uint32_t* scan) {
+  // Group starts (value changes in sort order) and each group's first
+  // position; with integer weights summing below 2^24 (exact) also each
+  // group's weight prefix, since every binary32 partial sum is then exact and
+  // a parallel prefix gives the serial sums bit for bit.
   uint32_t carry_w = 0, carry_s = 0;
   for (uint32_t base = 0; base < size; base += blockDim.x) {
-    uint32_t i = base + threadIdx.x;
+    const uint32_t i = base + threadIdx.x;
     uint32_t w = 0, start = 0;
-    float v = 0;
+    float v = 0.0f;
     if (i < size) {
-      uint32_t k = (uint32_t)keys[i];
-      v = run_v[k];
-      w = (uint32_t)run_w[k];
-      start = i == 0 || run_v[(uint32_t)keys[i - 1]] != v;
+      v = run_v[index[i]];
+      if (exact) w = (uint32_t)run_w[index[i]];
+      start = i == 0 || run_v[index[i - 1]] != v;
     }
-    uint32_t tw, ts;
-    uint32_t pw = block_exclusive_u32(w, scan, &tw) + carry_w;
-    uint32_t ps = block_exclusive_u32(start, scan, &ts) + carry_s;
+    uint32_t tw = 0, ts;
+    const uint32_t pw = (exact ? block_exclusive_u32(w, scan, &tw) : 0u) + carry_w;
+    const uint32_t ps = block_exclusive_u32(start, scan, &ts) + carry_s;
     if (start) {
-      scratch[ps] = pw;
+      scratch[ps] = exact ? pw : i;
       out[ps].value = v;
     }
     carry_w += tw;
     carry_s += ts;
   }
-  if (threadIdx.x == 0) scratch[carry_s] = carry_w;
+  if (threadIdx.x == 0) scratch[carry_s] = exact ? carry_w : size;
   __syncthreads();
   const uint32_t n = carry_s;
+  if (exact) {
+    for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
+      const uint32_t p = scratch[o], q = scratch[o + 1];
+      out[o].rmin = (float)p;
+      out[o].rmax = (float)q;
+      out[o].wmin = (float)(q - p);
+    }
+    __syncthreads();
+    return n;
+  }
+  // Each group's weight: its runs' weights summed in sort order.
   for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
-    uint32_t p = scratch[o], q = scratch[o + 1];
-    out[o].rmin = (float)p;
-    out[o].rmax = (float)q;
-    out[o].wmin = (float)(q - p);
+    const uint32_t s = scratch[o], e = scratch[o + 1];
+    float w = run_w[index[s]];
+    for (uint32_t i = s + 1; i < e; ++i) w = w + run_w[index[i]];
+    out[o].wmin = w;
+  }
+  __syncthreads();
+  // The running total, strictly in order: wave 0 loads 64 weights at a time
+  // and every lane applies the same 64 additions in sequence.
+  if (threadIdx.x < kWave) {
+    const uint32_t lane = threadIdx.x;
+    float total = 0.0f;
+    for (uint32_t g0 = 0; g0 < n; g0 += kWave) {
+      const uint32_t g = g0 + lane;
+      const float w = g < n ? out[g].wmin : 0.0f;
+      const uint32_t count = n - g0 < kWave ? n - g0 : kWave;
+      float before = 0.0f, after = 0.0f;
+      for (uint32_t j = 0; j < count; ++j) {
+        const float wj = __shfl(w, (int)j, kWave);
+        if (lane == j) before = total;
+        total = total + wj;
+        if (lane == j) after = total;
+      }
+      if (g < n) {
+        out[g].rmin = before;
+        out[g].rmax = after;
+      }
+    }
   }
   __syncthreads();
   return n;
 }
 
-__global__ __launch_bounds__(kSketchThreads) void k_reduce(const uint64_t* __restrict__ keys,
-                                                           const float* __restrict__ run_v,
-                                                           const float* __restrict__ run_w,
-                                                           const SkStats* __restrict__ stats,
+// Level 0 of every feature's tree: one workgroup per batch summarizes the
+// batch's sorted runs into the feature's work area and prunes the summary to
+// `limit` entries (the serial rule's first step for each batch,
+// kernels/quantile.metal.h:317-352).
+__global__ __launch_bounds__(kSketchThreads) void k_level0(const uint32_t* __restrict__ table,
                                                            const SkFeature* __restrict__ features,
-                                                           const uint64_t* __restrict__ seg,
-                                                           uint32_t max_bin, SkEntry* __restrict__ levels,
-                                                           SkEntry* __restrict__ work, uint32_t* __restrict__ scratch_u,
-                                                           float* __restrict__ cut_values, float* __restrict__ cuts,
-                                                           uint32_t* __restrict__ counts) {
+                                                           const SkStats* __restrict__ stats,
+                                                           const uint32_t* __restrict__ index,
+                                                           const float* __restrict__ run_v,
+                                                           const float* __restrict__ run_w, SkEntry* __restrict__ work,
+                                                           SkEntry* __restrict__ tree, uint32_t* __restrict__ scratch,
+                                                           uint32_t* __restrict__ node_count) {
+  __shared__ uint32_t scan[kSketchThreads / kWave + 1];
+  const uint32_t c = table[2 * blockIdx.x], b = table[2 * blockIdx.x + 1];
+  const SkFeature fe = features[c];
+  const uint64_t begin = (uint64_t)b * 2 * fe.limit;
+  const uint32_t runs = stats[c].runs;
+  const uint32_t size = (uint32_t)(runs - begin < 2ull * fe.limit ? runs - begin : 2ull * fe.limit);
+  SkEntry* summary = work + fe.base + begin;
+  const uint32_t n = summarize(index + fe.base + begin, run_v + fe.base, run_w + fe.base, size, fe.exact != 0,
+                               summary, scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), scan);
+  const uint32_t m = prune(summary, n, fe.limit, tree + fe.tree + (uint64_t)b * fe.limit, scan);
+  if (threadIdx.x == 0) node_count[fe.node_base + b] = m;
+}
+
+// Level `level` >= 1: node k merges nodes 2k + 1 and 2k of the level below
+// (the serial rule's merge of a new summary into an occupied level) and
+// prunes the merge to `limit`.  A merge of at most `limit` entries stays at
+// its level in the serial rule instead of moving up, so the tree no longer
+// matches it: the feature is marked for the serial rebuild.
+__global__ __launch_bounds__(kSketchThreads) void k_level_up(uint32_t level, const uint32_t* __restrict__ table,
+                                                             const SkFeature* __restrict__ features,
+                                                             SkEntry* __restrict__ work, SkEntry* __restrict__ tree,
+                                                             uint32_t* __restrict__ scratch,
+                                                             uint32_t* __restrict__ node_count,
+                                                             uint32_t* __restrict__ serial) {
+  __shared__ uint32_t scan[kSketchThreads / kWave + 1];
+  __shared__ uint32_t s_serial;
+  const uint32_t c = table[2 * blockIdx.x], k = table[2 * blockIdx.x + 1];
+  // Other workgroups of this level may set the flag meanwhile: one read,
+  // shared, so the whole workgroup takes the same branch.
+  if (threadIdx.x == 0) s_serial = serial[c];
+  __syncthreads();
+  if (s_serial) return;
+  const SkFeature fe = features[c];
+  const uint32_t below = level_first(fe.batches, level - 1), here = level_first(fe.batches, level);
+  const uint32_t newer = below + 2 * k + 1, older = below + 2 * k;
+  const uint32_t na = node_count[fe.node_base + newer], nb = node_count[fe.node_base + older];
+  SkEntry* merged = work + fe.base + (uint64_t)k * 2 * fe.limit;
+  const uint32_t n = combine(tree + fe.tree + (uint64_t)newer * fe.limit, na, tree + fe.tree + (uint64_t)older * fe.limit,
+                             nb, merged, scratch + fe.scratch + (uint64_t)k * (2 * fe.limit + 2), scan);
+  if (n <= fe.limit) {
+    if (threadIdx.x == 0) atomicOr(&serial[c], 1u);
+    return;
+  }
+  const uint32_t m = prune(merged, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, scan);
+  if (threadIdx.x == 0) node_count[fe.node_base + here + k] = m;
+}
+
+// One workgroup per feature: the stack's final contents merged level by level
+// with a prune to max(budget, limit) after each, a prune to the budget, and
+// the cuts (kernels/quantile.metal.h:317-400).  The stack holds, at each level
+// l whose bit is set in the batch count, the tree node over the last complete
+// 2^l batches; a feature marked serial first replays the serial rule over its
+// batch summaries.
+__global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __restrict__ features,
+                                                           const SkEntry* __restrict__ tree,
+                                                           const uint32_t* __restrict__ node_count,
+                                                           const uint32_t* __restrict__ serial,
+                                                           SkEntry* __restrict__ fin, uint32_t* __restrict__ fin_scratch,
+                                                           uint32_t f0, uint32_t max_bin, float* __restrict__ cut_values,
+                                                           float* __restrict__ cuts, uint32_t* __restrict__ counts) {
   __shared__ uint32_t scan[kSketchThreads / kWave + 1];
   __shared__ uint32_t level_count[64];
-  const uint32_t f = blockIdx.x;
-  const SkFeature fe = features[f];
-  const SkStats st = stats[f];
-  const uint64_t base = seg[f];
-  const uint32_t limit = fe.limit;
-  const uint32_t cap = 2 * limit + 2;
-  SkEntry* bufA = work + fe.work_offset;
-  SkEntry* bufB = bufA + cap;
-  uint32_t* scratch = scratch_u + fe.scratch_offset;
-  SkEntry* lvl = levels + fe.lvl_offset;
-  for (uint32_t i = threadIdx.x; i < 64; i += blockDim.x) level_count[i] = 0;
-  __syncthreads();
-  const uint64_t capacity = 2ull * limit;
-  for (uint64_t begin = 0; begin < st.runs; begin += capacity) {
-    uint32_t size = (uint32_t)((st.runs - begin) < capacity ? (st.runs - begin) : capacity);
-    uint32_t n = summarize(keys + base + begin, run_v + base, run_w + base, size, fe.exact_integer != 0, bufA,
-                           scratch, scan);
-    SkEntry* cur = bufA;
-    SkEntry* oth = bufB;
-    uint32_t level = 0;
-    for (;;) {
-      n = prune(cur, n, limit, oth, scan);
-      { SkEntry* t = cur; cur = oth; oth = t; }
-      uint32_t m = level_count[level];
-      if (m) {
-        n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scratch, scan);
+  const uint32_t c = blockIdx.x;
+  const SkFeature fe = features[c];
+  const uint32_t limit = fe.limit, batches = fe.batches;
+  const uint64_t buf = 2ull * fe.final_cap + 2;
+  SkEntry* cur = fin + fe.fin;
+  SkEntry* oth = cur + buf;
+  SkEntry* lvl = oth + buf;  // the serial stack: (levels + 1) x limit
+  uint32_t* scr = fin_scratch + fe.fin_scratch;
+  uint32_t n = 0;
+  if (batches && !serial[c]) {
+    for (uint32_t level = 0; level < fe.levels && level < 32; ++level) {
+      if ((batches >> level) & 1u) {
+        const uint32_t node = level_first(batches, level) + (batches >> level) - 1;
+        n = combine(cur, n, tree + fe.tree + (uint64_t)node * limit, node_count[fe.node_base + node], oth, scr, scan);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      __syncthreads();
-      if (threadIdx.x == 0) level_count[level] = 0;
-      __syncthreads();
-      if (n <= limit) break;
-      ++level;
-    }
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lvl[(uint64_t)level * limit + i] = cur[i];
-    __syncthreads();
-    if (threadIdx.x == 0) level_count[level] = n;
-    __syncthreads();
-  }
-  // Final combine over the levels, then prune to the budget.
-  SkEntry* cur = bufA;
-  SkEntry* oth = bufB;
-  uint32_t n = 0;
-  const uint32_t final_cap = fe.budget > limit ? fe.budget : limit;
-  for (uint32_t level = 0; level < fe.levels && level < 64; ++level) {
-    uint32_t m = level_count[level];
-    if (m) {
-      n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scratch, scan);
+      n = prune(cur, n, fe.final_cap, oth, scan);
       SkEntry* t = cur; cur = oth; oth = t;
     }
-    n = prune(cur, n, final_cap, oth, scan);
-    SkEntry* t = cur; cur = oth; oth = t;
+  } else if (batches) {
+    for (uint32_t i = threadIdx.x; i < 64; i += blockDim.x) level_count[i] = 0;
+    __syncthreads();
+    for (uint32_t b = 0; b < batches; ++b) {
+      n = node_count[fe.node_base + b];
+      const SkEntry* src = tree + fe.tree + (uint64_t)b * limit;
+      for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) cur[i] = src[i];
+      __syncthreads();
+      uint32_t level = 0;
+      for (;;) {
+        const uint32_t m = level_count[level];
+        if (m) {
+          n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan);
+          SkEntry* t = cur; cur = oth; oth = t;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) level_count[level] = 0;
+        __syncthreads();
+        if (n <= limit) break;
+        ++level;
+        n = prune(cur, n, limit, oth, scan);
+        SkEntry* t = cur; cur = oth; oth = t;
+      }
+      for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lvl[(uint64_t)level * limit + i] = cur[i];
+      __syncthreads();
+      if (threadIdx.x == 0) level_count[level] = n;
+      __syncthreads();
+    }
+    n = 0;
+    for (uint32_t level = 0; level < fe.levels && level < 64; ++level) {
+      const uint32_t m = level_count[level];
+      if (m) {
+        n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan);
+        SkEntry* t = cur; cur = oth; oth = t;
+      }
+      n = prune(cur, n, fe.final_cap, oth, scan);
+      SkEntry* t = cur; cur = oth; oth = t;
+    }
   }
   n = prune(cur, n, fe.budget, oth, scan);
   { SkEntry* t = cur; cur = oth; oth = t; }
   // Cuts (kernels/quantile.metal.h:354-400).
+  const uint32_t f = f0 + c;
   float* out = cuts + (uint64_t)f * max_bin;
   for (uint32_t i = threadIdx.x; i < max_bin; i += blockDim.x) out[i] = 0.0f;
   __syncthreads();
@@ -477,25 +722,25 @@ __global__ __launch_bounds__(kSketchThreads) void k_reduce(const uint64_t* __res
     for (uint32_t i = 1 + threadIdx.x; i < size; i += blockDim.x) out[i - 1] = cur[i].value;
     __syncthreads();
     if (threadIdx.x == 0) {
-      float tail = cur[size - 1].value;
+      const float tail = cur[size - 1].value;
       out[size - 1] = tail + (fabsf(tail) + 1e-5f);
       counts[f] = size;
     }
     return;
   }
   // Rank queries in parallel; the order-preserving dedup pass is serial.
-  float* values = cut_values + (uint64_t)f * max_bin;
+  float* values = cut_values + (uint64_t)c * max_bin;
   const double total = (double)cur[size - 1].rmax, denominator = (double)max_bin;
   for (uint32_t i = 1 + threadIdx.x; i < max_bin; i += blockDim.x) {
-    double rank = ((double)i * total) / denominator * 2.0;
+    const double rank = ((double)i * total) / denominator * 2.0;
     uint32_t lo = 1, hi = size - 1;  // cursor = #{j in [1, size-2] : rmin_j + rmax_j <= rank}
     while (lo < hi) {
-      uint32_t mid = lo + (hi - lo) / 2;
+      const uint32_t mid = lo + (hi - lo) / 2;
       if (rank >= (double)(cur[mid].rmin + cur[mid].rmax)) lo = mid + 1;
       else hi = mid;
     }
-    uint32_t cursor = lo - 1;
-    float boundary = min_next(cur[cursor]) + max_prev(cur[cursor + 1]);
+    const uint32_t cursor = lo - 1;
+    const float boundary = min_next(cur[cursor]) + max_prev(cur[cursor + 1]);
     values[i] = cur[cursor + ((isnan(boundary) || rank >= (double)boundary) ? 1u : 0u)].value;
   }
   __syncthreads();
@@ -514,7 +759,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_reduce(const uint64_t* __res
       out[count++] = value;
       last = value;
     }
-    float tail = cur[size - 1].value;
+    const float tail = cur[size - 1].value;
     out[count++] = tail + (fabsf(tail) + 1e-5f);
     counts[f] = count;
   }
@@ -532,95 +777,154 @@ uint32_t sketch_budget(uint32_t bins, uint32_t count) {
 
 uint32_t bit_width(uint32_t v) { return v ? 32u - (uint32_t)__builtin_clz(v) : 0u; }
 
-struct DeviceBuffer {
+// Device memory of one sketch pass, allocated and freed in order on the
+// library stream: a free is queued behind the kernels that use the buffer
+// instead of waiting for the device, and the memory pool keeps it for the
+// next pass.
+struct StreamBuffer {
   void* p = nullptr;
-  ~DeviceBuffer() { if (p) (void)hipFree(p); }
-  int alloc(size_t bytes) { return check(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc(sketch)"); }
+  StreamBuffer() = default;
+  StreamBuffer(const StreamBuffer&) = delete;
+  StreamBuffer& operator=(const StreamBuffer&) = delete;
+  ~StreamBuffer() {
+    if (p) (void)hipFreeAsync(p, stream());
+  }
+  int alloc(size_t bytes) { return check(hipMallocAsync(&p, bytes ? bytes : 16, stream()), "hipMallocAsync(sketch)"); }
+  template <typename T> T* as() const { return static_cast<T*>(p); }
 };
 
-// Cuts of `cols` features whose entries are vals[seg[f] .. seg[f+1]) (device
-// values; host and device copies of the offsets), see k_runs.
-int sketch_segments(const float* vals, const std::vector<uint64_t>& seg_host, const uint32_t* row_of,
-                    uint32_t cols, const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
+template <typename T>
+int upload(StreamBuffer& dst, const std::vector<T>& src) {
+  if (dst.alloc(src.size() * sizeof(T))) return -1;
+  if (!src.empty()) MGB_CHECK(hipMemcpyAsync(dst.p, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice, stream()));
+  return 0;
+}
+
+// Cuts of the features f0 .. f0 + nf - 1 whose entries are
+// vals[seg[c] .. seg[c + 1]) (device values; host offsets, seg[0] = 0), see
+// view_entry for the meaning of row_of and weights.
+int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint32_t* row_of, uint32_t nf, uint32_t f0,
+                 const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
   hipStream_t s = stream();
-  const uint64_t total = seg_host[cols];
+  const uint64_t total = seg[nf];
   // Positions are 32-bit and the segmented sort counts in int.
-  if (total >= (1ull << 31)) { set_error("sketch: more than 2^31 - 1 entries"); return -1; }
-  const uint64_t alloc = total ? total : 1;
-  DeviceBuffer seg_d, run_v, run_w, run_start, elem_w, stats_d, keys_in, keys_out;
-  if (seg_d.alloc((cols + 1) * sizeof(uint64_t)) || run_v.alloc(alloc * 4) || run_w.alloc(alloc * 4) ||
-      run_start.alloc(alloc * 4) || stats_d.alloc(cols * sizeof(SkStats)) || keys_in.alloc(alloc * 8) ||
-      keys_out.alloc(alloc * 8))
+  if (total >= (1ull << 31)) { set_error("sketch: more than 2^31 - 1 entries in one group"); return -1; }
+  uint64_t longest = 0;
+  for (uint32_t c = 0; c < nf; ++c) longest = std::max<uint64_t>(longest, seg[c + 1] - seg[c]);
+  const uint32_t max_blocks = (uint32_t)std::max<uint64_t>(1, (longest + kBlockEntries - 1) / kBlockEntries);
+  const uint64_t E = total ? total : 1;
+  StreamBuffer seg_d, blocks, stats_d, run_v, run_w, region, keys_out, index_out;
+  if (upload(seg_d, seg) || blocks.alloc((uint64_t)nf * max_blocks * sizeof(SkBlock)) ||
+      stats_d.alloc(nf * sizeof(SkStats)) || run_v.alloc(E * 4) || run_w.alloc(E * 4) || region.alloc(E * 16) ||
+      keys_out.alloc(E * 4) || index_out.alloc(E * 4))
     return -1;
-  if (weights && elem_w.alloc(alloc * 4)) return -1;
-  MGB_CHECK(hipMemcpyAsync(seg_d.p, seg_host.data(), (cols + 1) * sizeof(uint64_t), hipMemcpyHostToDevice, s));
-  hipLaunchKernelGGL(k_runs, dim3(cols), dim3(kSketchThreads), 0, s, vals, (const uint64_t*)seg_d.p, row_of, weights,
-                     (float*)run_v.p, (float*)run_w.p, (uint32_t*)run_start.p, (float*)elem_w.p,
-                     (SkStats*)stats_d.p);
-  MGB_LAUNCH_CHECK("k_runs");
-  std::vector<SkStats> stats(cols);
-  MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d.p, cols * sizeof(SkStats), hipMemcpyDeviceToHost, s));
+  // One 16-byte-per-entry region: run starts, sort inputs and entry weights
+  // until the sort, then the summaries' and merges' work area.
+  uint32_t* run_start = region.as<uint32_t>();
+  uint32_t* keys_in = run_start + E;
+  uint32_t* index_in = keys_in + E;
+  float* elem_w = reinterpret_cast<float*>(index_in + E);
+  SkEntry* work = region.as<SkEntry>();
+  const dim3 grid(max_blocks, nf);
+  hipLaunchKernelGGL(k_run_count, grid, dim3(kSketchThreads), 0, s, vals, seg_d.as<uint64_t>(), row_of, weights,
+                     max_blocks, blocks.as<SkBlock>());
+  MGB_LAUNCH_CHECK("k_run_count");
+  hipLaunchKernelGGL(k_run_scan, dim3(nf), dim3(kSketchThreads), 0, s, seg_d.as<uint64_t>(), max_blocks,
+                     blocks.as<SkBlock>(), stats_d.as<SkStats>());
+  MGB_LAUNCH_CHECK("k_run_scan");
+  hipLaunchKernelGGL(k_run_emit, grid, dim3(kSketchThreads), 0, s, vals, seg_d.as<uint64_t>(), row_of, weights,
+                     max_blocks, blocks.as<SkBlock>(), run_v.as<float>(), run_start, elem_w);
+  MGB_LAUNCH_CHECK("k_run_emit");
+  hipLaunchKernelGGL(k_run_weights, grid, dim3(kSketchThreads), 0, s, seg_d.as<uint64_t>(), stats_d.as<SkStats>(),
+                     run_start, weights ? elem_w : nullptr, run_w.as<float>());
+  MGB_LAUNCH_CHECK("k_run_weights");
+  hipLaunchKernelGGL(k_sort_keys, grid, dim3(kSketchThreads), 0, s, seg_d.as<uint64_t>(), stats_d.as<SkStats>(),
+                     run_v.as<float>(), keys_in, index_in);
+  MGB_LAUNCH_CHECK("k_sort_keys");
+  std::vector<SkStats> stats(nf);
+  MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d.p, nf * sizeof(SkStats), hipMemcpyDeviceToHost, s));
   MGB_CHECK(hipStreamSynchronize(s));
-  // Batch plan (src/quantile.cpp:87-122).
-  std::vector<SkFeature> features(cols);
-  std::vector<uint32_t> seg_begin, seg_end;
-  uint64_t lvl_total = 0, work_total = 0, scratch_total = 0;
-  for (uint32_t f = 0; f < cols; ++f) {
-    const SkStats& st = stats[f];
-    uint32_t limit = sketch_budget(max_bin, st.nonmissing);
-    uint32_t budget = sketch_budget(max_bin, st.elements);
-    uint64_t capacity = 2ull * limit;
-    uint32_t batches = 0;
-    for (uint64_t b = 0; b < st.runs; b += capacity) {
-      uint64_t size = std::min<uint64_t>(capacity, st.runs - b);
-      seg_begin.push_back((uint32_t)(seg_host[f] + b));
-      seg_end.push_back((uint32_t)(seg_host[f] + b + size));
-      ++batches;
-    }
-    uint32_t levels = bit_width(std::max(1u, batches)) + 1;
+
+  // Batch plan (src/quantile.cpp:87-122) and tree layout.
+  std::vector<SkFeature> features(nf);
+  std::vector<uint32_t> seg_begin, seg_end, table0;
+  std::vector<std::vector<uint32_t>> tables;  // levels 1, 2, ...
+  uint64_t tree_total = 0, scratch_total = 0, fin_total = 0, fin_scratch_total = 0;
+  uint32_t node_total = 0;
+  for (uint32_t c = 0; c < nf; ++c) {
+    const SkStats& st = stats[c];
     SkFeature fe{};
-    fe.lvl_offset = lvl_total;
-    fe.work_offset = work_total;
-    fe.limit = limit;
-    fe.budget = budget;
-    fe.batches = batches;
-    fe.levels = levels;
-    fe.exact_integer = !weights && st.elements <= (1u << 24);
-    fe.scratch_offset = scratch_total;
-    features[f] = fe;
-    lvl_total += (uint64_t)limit * (levels + 1);
-    work_total += 2 * (2ull * limit + 2);
-    scratch_total += 2ull * limit + 4;
+    fe.base = seg[c];
+    fe.limit = sketch_budget(max_bin, st.nonmissing);
+    fe.budget = sketch_budget(max_bin, st.elements);
+    const uint64_t capacity = 2ull * fe.limit;
+    fe.batches = (uint32_t)((st.runs + capacity - 1) / capacity);
+    fe.levels = bit_width(std::max(1u, fe.batches)) + 1;
+    fe.exact = !weights && st.elements <= (1u << 24);
+    fe.final_cap = std::max(fe.budget, fe.limit);
+    const uint32_t nodes = level_first(fe.batches, 32);
+    fe.node_base = node_total;
+    fe.tree = tree_total;
+    fe.scratch = scratch_total;
+    fe.fin = fin_total;
+    fe.fin_scratch = fin_scratch_total;
+    node_total += nodes;
+    tree_total += (uint64_t)nodes * fe.limit;
+    scratch_total += (uint64_t)fe.batches * (2ull * fe.limit + 2);
+    fin_total += 2 * (2ull * fe.final_cap + 2) + (uint64_t)(fe.levels + 1) * fe.limit;
+    fin_scratch_total += 2ull * fe.final_cap + 4;
+    for (uint32_t b = 0; b < fe.batches; ++b) {
+      const uint64_t begin = (uint64_t)b * capacity;
+      seg_begin.push_back((uint32_t)(seg[c] + begin));
+      seg_end.push_back((uint32_t)(seg[c] + std::min<uint64_t>(st.runs, begin + capacity)));
+      table0.push_back(c);
+      table0.push_back(b);
+    }
+    for (uint32_t level = 1; (fe.batches >> level) != 0; ++level) {
+      if (tables.size() < level) tables.emplace_back();
+      for (uint32_t k = 0; k < (fe.batches >> level); ++k) {
+        tables[level - 1].push_back(c);
+        tables[level - 1].push_back(k);
+      }
+    }
+    features[c] = fe;
   }
-  DeviceBuffer levels_d, work_d, scratch_d, feat_d, values_d, seg_b, seg_e, temp;
-  if (levels_d.alloc(lvl_total * sizeof(SkEntry)) || work_d.alloc(work_total * sizeof(SkEntry)) ||
-      feat_d.alloc(cols * sizeof(SkFeature)) || values_d.alloc((uint64_t)cols * max_bin * 4))
+  StreamBuffer tree, scratch, node_count, serial, fin, fin_scratch, values, features_d, table0_d, seg_b, seg_e, temp;
+  if (tree.alloc(std::max<uint64_t>(tree_total, 1) * sizeof(SkEntry)) || scratch.alloc(std::max<uint64_t>(scratch_total, 1) * 4) ||
+      node_count.alloc(std::max<uint32_t>(node_total, 1) * 4) || serial.alloc(nf * 4) ||
+      fin.alloc(fin_total * sizeof(SkEntry)) || fin_scratch.alloc(fin_scratch_total * 4) ||
+      values.alloc((uint64_t)nf * max_bin * 4) || upload(features_d, features) || upload(table0_d, table0))
     return -1;
-  if (scratch_d.alloc(scratch_total * 4)) return -1;
-  MGB_CHECK(hipMemcpyAsync(feat_d.p, features.data(), cols * sizeof(SkFeature), hipMemcpyHostToDevice, s));
+  MGB_CHECK(hipMemsetAsync(serial.p, 0, nf * 4, s));
   if (!seg_begin.empty()) {
-    hipLaunchKernelGGL(k_keys, dim3(cols), dim3(256), 0, s, (const float*)run_v.p, (const SkStats*)stats_d.p,
-                       (const uint64_t*)seg_d.p, (uint64_t*)keys_in.p);
-    MGB_LAUNCH_CHECK("k_keys");
-    if (seg_b.alloc(seg_begin.size() * 4) || seg_e.alloc(seg_end.size() * 4)) return -1;
-    MGB_CHECK(hipMemcpyAsync(seg_b.p, seg_begin.data(), seg_begin.size() * 4, hipMemcpyHostToDevice, s));
-    MGB_CHECK(hipMemcpyAsync(seg_e.p, seg_end.data(), seg_end.size() * 4, hipMemcpyHostToDevice, s));
+    if (upload(seg_b, seg_begin) || upload(seg_e, seg_end)) return -1;
     size_t temp_bytes = 0;
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortKeys(nullptr, temp_bytes, (const uint64_t*)keys_in.p,
-                                                          (uint64_t*)keys_out.p, (int)total, (int)seg_begin.size(),
-                                                          (const uint32_t*)seg_b.p, (const uint32_t*)seg_e.p, 0, 64,
-                                                          s));
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_bytes, keys_in, keys_out.as<uint32_t>(),
+                                                           index_in, index_out.as<uint32_t>(), (int)total,
+                                                           (int)seg_begin.size(), seg_b.as<uint32_t>(),
+                                                           seg_e.as<uint32_t>(), 0, 32, s));
     if (temp.alloc(temp_bytes)) return -1;
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortKeys(temp.p, temp_bytes, (const uint64_t*)keys_in.p,
-                                                          (uint64_t*)keys_out.p, (int)total, (int)seg_begin.size(),
-                                                          (const uint32_t*)seg_b.p, (const uint32_t*)seg_e.p, 0, 64,
-                                                          s));
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(temp.p, temp_bytes, keys_in, keys_out.as<uint32_t>(),
+                                                           index_in, index_out.as<uint32_t>(), (int)total,
+                                                           (int)seg_begin.size(), seg_b.as<uint32_t>(),
+                                                           seg_e.as<uint32_t>(), 0, 32, s));
+    hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kSketchThreads), 0, s, table0_d.as<uint32_t>(),
+                       features_d.as<SkFeature>(), stats_d.as<SkStats>(), index_out.as<uint32_t>(), run_v.as<float>(),
+                       run_w.as<float>(), work, tree.as<SkEntry>(), scratch.as<uint32_t>(), node_count.as<uint32_t>());
+    MGB_LAUNCH_CHECK("k_level0");
   }
-  hipLaunchKernelGGL(k_reduce, dim3(cols), dim3(kSketchThreads), 0, s, (const uint64_t*)keys_out.p,
-                     (const float*)run_v.p, (const float*)run_w.p, (const SkStats*)stats_d.p,
-                     (const SkFeature*)feat_d.p, (const uint64_t*)seg_d.p, max_bin, (SkEntry*)levels_d.p,
-                     (SkEntry*)work_d.p, (uint32_t*)scratch_d.p, (float*)values_d.p, cuts, counts);
-  MGB_LAUNCH_CHECK("k_reduce");
+  std::vector<StreamBuffer> level_tables(tables.size());
+  for (size_t l = 0; l < tables.size(); ++l) {
+    if (upload(level_tables[l], tables[l])) return -1;
+    hipLaunchKernelGGL(k_level_up, dim3((uint32_t)(tables[l].size() / 2)), dim3(kSketchThreads), 0, s,
+                       (uint32_t)(l + 1), level_tables[l].as<uint32_t>(), features_d.as<SkFeature>(), work,
+                       tree.as<SkEntry>(), scratch.as<uint32_t>(), node_count.as<uint32_t>(), serial.as<uint32_t>());
+    MGB_LAUNCH_CHECK("k_level_up");
+  }
+  hipLaunchKernelGGL(k_finish, dim3(nf), dim3(kSketchThreads), 0, s, features_d.as<SkFeature>(), tree.as<SkEntry>(),
+                     node_count.as<uint32_t>(), serial.as<uint32_t>(), fin.as<SkEntry>(), fin_scratch.as<uint32_t>(), f0,
+                     max_bin, values.as<float>(), cuts, counts);
+  MGB_LAUNCH_CHECK("k_finish");
   MGB_CHECK(hipStreamSynchronize(s));
   return 0;
 }
@@ -636,18 +940,25 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
                     float* cuts, uint32_t* counts) {
   if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
   if (!cols) return 0;
-  const uint64_t total = (uint64_t)rows * cols;
-  if (total >= (1ull << 31)) { set_error("sketch: rows*cols must be below 2^31"); return -1; }
-  DeviceBuffer xt;
-  if (xt.alloc((total ? total : 1) * 4)) return -1;
-  if (rows) {
-    dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(32, 8);
-    hipLaunchKernelGGL(k_transpose, grid, block, 0, stream(), X, rows, cols, (float*)xt.p);
-    MGB_LAUNCH_CHECK("k_transpose");
+  if (rows >= (1u << 31)) { set_error("sketch: rows must be below 2^31"); return -1; }
+  // Feature groups of at most kChunkEntries entries and kMaxGroupFeatures
+  // features (the run passes put the feature in gridDim.y).
+  const uint32_t group = (uint32_t)std::max<uint64_t>(
+      1, std::min<uint64_t>(std::min<uint64_t>(cols, kMaxGroupFeatures), kChunkEntries / std::max(1u, rows)));
+  for (uint32_t f0 = 0; f0 < cols; f0 += group) {
+    const uint32_t nf = std::min(group, cols - f0);
+    StreamBuffer xt;
+    if (xt.alloc(std::max<uint64_t>((uint64_t)rows * nf, 1) * 4)) return -1;
+    if (rows) {
+      const dim3 grid((rows + 31) / 32, (nf + 31) / 32), block(32, 8);
+      hipLaunchKernelGGL(k_transpose, grid, block, 0, stream(), X, rows, cols, f0, nf, xt.as<float>());
+      MGB_LAUNCH_CHECK("k_transpose");
+    }
+    std::vector<uint64_t> seg(nf + 1);
+    for (uint32_t c = 0; c <= nf; ++c) seg[c] = (uint64_t)c * rows;
+    if (sketch_group(xt.as<float>(), seg, nullptr, nf, f0, weights, max_bin, cuts, counts)) return -1;
   }
-  std::vector<uint64_t> seg(cols + 1);
-  for (uint32_t f = 0; f <= cols; ++f) seg[f] = (uint64_t)f * rows;
-  return sketch_segments((const float*)xt.p, seg, nullptr, cols, weights, max_bin, cuts, counts);
+  return 0;
 }
 
 int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint64_t* colptr, uint32_t rows,
@@ -655,10 +966,21 @@ int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint6
   if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
   if (!cols) return 0;
   (void)rows;
-  std::vector<uint64_t> seg(cols + 1);
-  MGB_CHECK(hipMemcpyAsync(seg.data(), colptr, (cols + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost, stream()));
+  std::vector<uint64_t> colptr_host(cols + 1);
+  MGB_CHECK(hipMemcpyAsync(colptr_host.data(), colptr, (cols + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost, stream()));
   MGB_CHECK(hipStreamSynchronize(stream()));
-  return sketch_segments(values, seg, row_of, cols, weights, max_bin, cuts, counts);
+  // Groups of whole columns of at most kChunkEntries entries (a longer column
+  // forms a group of its own) and kMaxGroupFeatures columns.
+  for (uint32_t f0 = 0; f0 < cols;) {
+    uint32_t f1 = f0 + 1;
+    while (f1 < cols && f1 - f0 < kMaxGroupFeatures && colptr_host[f1 + 1] - colptr_host[f0] <= kChunkEntries) ++f1;
+    std::vector<uint64_t> seg(f1 - f0 + 1);
+    for (uint32_t c = 0; c <= f1 - f0; ++c) seg[c] = colptr_host[f0 + c] - colptr_host[f0];
+    const uint64_t first = colptr_host[f0];
+    if (sketch_group(values + first, seg, row_of + first, f1 - f0, f0, weights, max_bin, cuts, counts)) return -1;
+    f0 = f1;
+  }
+  return 0;
 }
 
 }  // extern "C"
