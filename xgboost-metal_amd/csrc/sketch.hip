@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <vector>
 
 #include "device_common.hpp"
@@ -42,6 +43,7 @@ constexpr uint32_t kSketchThreads = 1024;
 constexpr uint32_t kBlockEntries = 1024;                 // entries per workgroup in the run passes
 constexpr uint64_t kChunkEntries = uint64_t(1) << 27;    // entries per group of features
 constexpr uint32_t kMaxGroupFeatures = 65535;            // features per group
+constexpr uint32_t kFinishLds = 96 * 1024;               // k_finish's staging LDS, at most
 
 struct SkEntry { float rmin, rmax, wmin, value; };
 struct SkStats { uint32_t nonmissing, elements, runs, padding; };
@@ -645,9 +647,13 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
                                                            const uint32_t* __restrict__ serial,
                                                            SkEntry* __restrict__ fin, uint32_t* __restrict__ fin_scratch,
                                                            uint32_t f0, uint32_t max_bin, float* __restrict__ cut_values,
-                                                           float* __restrict__ cuts, uint32_t* __restrict__ counts) {
+                                                           uint32_t lds_values, float* __restrict__ cuts,
+                                                           uint32_t* __restrict__ counts) {
   __shared__ uint32_t scan[kSketchThreads / kWave + 1];
   __shared__ uint32_t level_count[64];
+  // lds_values summary values, then max_bin candidate cuts (0 bytes when
+  // lds_values is 0).
+  extern __shared__ float s_stage[];
   const uint32_t c = blockIdx.x;
   const SkFeature fe = features[c];
   const uint32_t limit = fe.limit, batches = fe.batches;
@@ -728,8 +734,12 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
     }
     return;
   }
-  // Rank queries in parallel; the order-preserving dedup pass is serial.
-  float* values = cut_values + (uint64_t)c * max_bin;
+  // Rank queries in parallel; the order-preserving dedup pass is serial, on
+  // values staged in LDS when they fit.
+  const bool staged = size <= lds_values;
+  float* values = staged ? s_stage + lds_values : cut_values + (uint64_t)c * max_bin;
+  if (staged)
+    for (uint32_t i = threadIdx.x; i < size; i += blockDim.x) s_stage[i] = cur[i].value;
   const double total = (double)cur[size - 1].rmax, denominator = (double)max_bin;
   for (uint32_t i = 1 + threadIdx.x; i < max_bin; i += blockDim.x) {
     const double rank = ((double)i * total) / denominator * 2.0;
@@ -745,16 +755,17 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float last = cur[0].value;
+    auto entry = [&](uint32_t j) { return staged ? s_stage[j] : cur[j].value; };
+    float last = entry(0);
     uint32_t next = 1, count = 0;
     for (uint32_t i = 1; i < max_bin; ++i) {
       float value = values[i];
       if (value <= last) {
-        while (next < size && cur[next].value <= last) ++next;
+        while (next < size && entry(next) <= last) ++next;
         if (next == size) break;
-        value = cur[next].value;
-      } else if (next < size && cur[next].value <= value) {
-        do { ++next; } while (next < size && cur[next].value <= value);
+        value = entry(next);
+      } else if (next < size && entry(next) <= value) {
+        do { ++next; } while (next < size && entry(next) <= value);
       }
       out[count++] = value;
       last = value;
@@ -793,12 +804,34 @@ struct StreamBuffer {
   template <typename T> T* as() const { return static_cast<T*>(p); }
 };
 
-template <typename T>
-int upload(StreamBuffer& dst, const std::vector<T>& src) {
-  if (dst.alloc(src.size() * sizeof(T))) return -1;
-  if (!src.empty()) MGB_CHECK(hipMemcpyAsync(dst.p, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice, stream()));
-  return 0;
-}
+// Buffers carved from one stream-ordered allocation: reserve() hands out
+// 256-byte-aligned offsets, commit() allocates once.  Host tables are
+// gathered into a staging image of the arena's first bytes and copied in one
+// transfer.
+struct Arena {
+  StreamBuffer buffer;
+  uint64_t size = 0;
+  std::vector<uint8_t> staged;  // host image of [0, staged.size())
+  uint64_t reserve(uint64_t bytes) {
+    const uint64_t off = size;
+    size += (std::max<uint64_t>(bytes, 1) + 255) / 256 * 256;
+    return off;
+  }
+  template <typename T>
+  uint64_t stage(const std::vector<T>& src) {
+    const uint64_t off = reserve(src.size() * sizeof(T));
+    staged.resize(size);
+    if (!src.empty()) std::memcpy(staged.data() + off, src.data(), src.size() * sizeof(T));
+    return off;
+  }
+  int commit() {
+    if (buffer.alloc(size)) return -1;
+    if (!staged.empty())
+      MGB_CHECK(hipMemcpyAsync(buffer.p, staged.data(), staged.size(), hipMemcpyHostToDevice, stream()));
+    return 0;
+  }
+  template <typename T> T* at(uint64_t off) const { return reinterpret_cast<T*>(buffer.as<uint8_t>() + off); }
+};
 
 // Cuts of the features f0 .. f0 + nf - 1 whose entries are
 // vals[seg[c] .. seg[c + 1]) (device values; host offsets, seg[0] = 0), see
@@ -813,36 +846,46 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   for (uint32_t c = 0; c < nf; ++c) longest = std::max<uint64_t>(longest, seg[c + 1] - seg[c]);
   const uint32_t max_blocks = (uint32_t)std::max<uint64_t>(1, (longest + kBlockEntries - 1) / kBlockEntries);
   const uint64_t E = total ? total : 1;
-  StreamBuffer seg_d, blocks, stats_d, run_v, run_w, region, keys_out, index_out;
-  if (upload(seg_d, seg) || blocks.alloc((uint64_t)nf * max_blocks * sizeof(SkBlock)) ||
-      stats_d.alloc(nf * sizeof(SkStats)) || run_v.alloc(E * 4) || run_w.alloc(E * 4) || region.alloc(E * 16) ||
-      keys_out.alloc(E * 4) || index_out.alloc(E * 4))
-    return -1;
+  Arena a1;
+  const uint64_t o_seg = a1.stage(seg);
+  const uint64_t o_blocks = a1.reserve((uint64_t)nf * max_blocks * sizeof(SkBlock));
+  const uint64_t o_stats = a1.reserve(nf * sizeof(SkStats));
+  const uint64_t o_run_v = a1.reserve(E * 4), o_run_w = a1.reserve(E * 4);
+  const uint64_t o_region = a1.reserve(E * 16);
+  const uint64_t o_keys_out = a1.reserve(E * 4), o_index_out = a1.reserve(E * 4);
+  if (a1.commit()) return -1;
+  const uint64_t* seg_d = a1.at<uint64_t>(o_seg);
+  SkBlock* blocks = a1.at<SkBlock>(o_blocks);
+  SkStats* stats_d = a1.at<SkStats>(o_stats);
+  float* run_v = a1.at<float>(o_run_v);
+  float* run_w = a1.at<float>(o_run_w);
+  uint32_t* keys_out = a1.at<uint32_t>(o_keys_out);
+  uint32_t* index_out = a1.at<uint32_t>(o_index_out);
   // One 16-byte-per-entry region: run starts, sort inputs and entry weights
   // until the sort, then the summaries' and merges' work area.
-  uint32_t* run_start = region.as<uint32_t>();
+  uint32_t* run_start = a1.at<uint32_t>(o_region);
   uint32_t* keys_in = run_start + E;
   uint32_t* index_in = keys_in + E;
   float* elem_w = reinterpret_cast<float*>(index_in + E);
-  SkEntry* work = region.as<SkEntry>();
+  SkEntry* work = a1.at<SkEntry>(o_region);
   const dim3 grid(max_blocks, nf);
-  hipLaunchKernelGGL(k_run_count, grid, dim3(kSketchThreads), 0, s, vals, seg_d.as<uint64_t>(), row_of, weights,
-                     max_blocks, blocks.as<SkBlock>());
+  hipLaunchKernelGGL(k_run_count, grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
+                     max_blocks, blocks);
   MGB_LAUNCH_CHECK("k_run_count");
-  hipLaunchKernelGGL(k_run_scan, dim3(nf), dim3(kSketchThreads), 0, s, seg_d.as<uint64_t>(), max_blocks,
-                     blocks.as<SkBlock>(), stats_d.as<SkStats>());
+  hipLaunchKernelGGL(k_run_scan, dim3(nf), dim3(kSketchThreads), 0, s, seg_d, max_blocks,
+                     blocks, stats_d);
   MGB_LAUNCH_CHECK("k_run_scan");
-  hipLaunchKernelGGL(k_run_emit, grid, dim3(kSketchThreads), 0, s, vals, seg_d.as<uint64_t>(), row_of, weights,
-                     max_blocks, blocks.as<SkBlock>(), run_v.as<float>(), run_start, elem_w);
+  hipLaunchKernelGGL(k_run_emit, grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
+                     max_blocks, blocks, run_v, run_start, elem_w);
   MGB_LAUNCH_CHECK("k_run_emit");
-  hipLaunchKernelGGL(k_run_weights, grid, dim3(kSketchThreads), 0, s, seg_d.as<uint64_t>(), stats_d.as<SkStats>(),
-                     run_start, weights ? elem_w : nullptr, run_w.as<float>());
+  hipLaunchKernelGGL(k_run_weights, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
+                     run_start, weights ? elem_w : nullptr, run_w);
   MGB_LAUNCH_CHECK("k_run_weights");
-  hipLaunchKernelGGL(k_sort_keys, grid, dim3(kSketchThreads), 0, s, seg_d.as<uint64_t>(), stats_d.as<SkStats>(),
-                     run_v.as<float>(), keys_in, index_in);
+  hipLaunchKernelGGL(k_sort_keys, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
+                     run_v, keys_in, index_in);
   MGB_LAUNCH_CHECK("k_sort_keys");
   std::vector<SkStats> stats(nf);
-  MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d.p, nf * sizeof(SkStats), hipMemcpyDeviceToHost, s));
+  MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d, nf * sizeof(SkStats), hipMemcpyDeviceToHost, s));
   MGB_CHECK(hipStreamSynchronize(s));
 
   // Batch plan (src/quantile.cpp:87-122) and tree layout.
@@ -889,41 +932,57 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
     }
     features[c] = fe;
   }
-  StreamBuffer tree, scratch, node_count, serial, fin, fin_scratch, values, features_d, table0_d, seg_b, seg_e, temp;
-  if (tree.alloc(std::max<uint64_t>(tree_total, 1) * sizeof(SkEntry)) || scratch.alloc(std::max<uint64_t>(scratch_total, 1) * 4) ||
-      node_count.alloc(std::max<uint32_t>(node_total, 1) * 4) || serial.alloc(nf * 4) ||
-      fin.alloc(fin_total * sizeof(SkEntry)) || fin_scratch.alloc(fin_scratch_total * 4) ||
-      values.alloc((uint64_t)nf * max_bin * 4) || upload(features_d, features) || upload(table0_d, table0))
-    return -1;
-  MGB_CHECK(hipMemsetAsync(serial.p, 0, nf * 4, s));
+  size_t temp_bytes = 0;
+  if (!seg_begin.empty())
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_bytes, keys_in, keys_out, index_in, index_out,
+                                                           (int)total, (int)seg_begin.size(), (const uint32_t*)nullptr,
+                                                           (const uint32_t*)nullptr, 0, 32, s));
+  Arena a2;
+  const uint64_t o_features = a2.stage(features), o_table0 = a2.stage(table0);
+  const uint64_t o_seg_b = a2.stage(seg_begin), o_seg_e = a2.stage(seg_end);
+  std::vector<uint64_t> o_tables(tables.size());
+  for (size_t l = 0; l < tables.size(); ++l) o_tables[l] = a2.stage(tables[l]);
+  uint32_t max_budget = 1;
+  for (const SkFeature& fe : features) max_budget = std::max(max_budget, fe.budget);
+  const uint64_t o_tree = a2.reserve(tree_total * sizeof(SkEntry)), o_scratch = a2.reserve(scratch_total * 4);
+  const uint64_t o_node_count = a2.reserve((uint64_t)node_total * 4), o_serial = a2.reserve(nf * 4);
+  const uint64_t o_fin = a2.reserve(fin_total * sizeof(SkEntry)), o_fin_scratch = a2.reserve(fin_scratch_total * 4);
+  const uint64_t o_values = a2.reserve((uint64_t)nf * max_bin * 4), o_temp = a2.reserve(temp_bytes);
+  if (a2.commit()) return -1;
+  const SkFeature* features_d = a2.at<SkFeature>(o_features);
+  SkEntry* tree = a2.at<SkEntry>(o_tree);
+  uint32_t* scratch = a2.at<uint32_t>(o_scratch);
+  uint32_t* node_count = a2.at<uint32_t>(o_node_count);
+  uint32_t* serial = a2.at<uint32_t>(o_serial);
+  MGB_CHECK(hipMemsetAsync(serial, 0, nf * 4, s));
   if (!seg_begin.empty()) {
-    if (upload(seg_b, seg_begin) || upload(seg_e, seg_end)) return -1;
-    size_t temp_bytes = 0;
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_bytes, keys_in, keys_out.as<uint32_t>(),
-                                                           index_in, index_out.as<uint32_t>(), (int)total,
-                                                           (int)seg_begin.size(), seg_b.as<uint32_t>(),
-                                                           seg_e.as<uint32_t>(), 0, 32, s));
-    if (temp.alloc(temp_bytes)) return -1;
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(temp.p, temp_bytes, keys_in, keys_out.as<uint32_t>(),
-                                                           index_in, index_out.as<uint32_t>(), (int)total,
-                                                           (int)seg_begin.size(), seg_b.as<uint32_t>(),
-                                                           seg_e.as<uint32_t>(), 0, 32, s));
-    hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kSketchThreads), 0, s, table0_d.as<uint32_t>(),
-                       features_d.as<SkFeature>(), stats_d.as<SkStats>(), index_out.as<uint32_t>(), run_v.as<float>(),
-                       run_w.as<float>(), work, tree.as<SkEntry>(), scratch.as<uint32_t>(), node_count.as<uint32_t>());
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out, index_in,
+                                                           index_out, (int)total, (int)seg_begin.size(),
+                                                           a2.at<uint32_t>(o_seg_b), a2.at<uint32_t>(o_seg_e), 0, 32,
+                                                           s));
+    hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kSketchThreads), 0, s,
+                       a2.at<uint32_t>(o_table0), features_d, stats_d, index_out, run_v, run_w, work, tree, scratch,
+                       node_count);
     MGB_LAUNCH_CHECK("k_level0");
   }
-  std::vector<StreamBuffer> level_tables(tables.size());
   for (size_t l = 0; l < tables.size(); ++l) {
-    if (upload(level_tables[l], tables[l])) return -1;
     hipLaunchKernelGGL(k_level_up, dim3((uint32_t)(tables[l].size() / 2)), dim3(kSketchThreads), 0, s,
-                       (uint32_t)(l + 1), level_tables[l].as<uint32_t>(), features_d.as<SkFeature>(), work,
-                       tree.as<SkEntry>(), scratch.as<uint32_t>(), node_count.as<uint32_t>(), serial.as<uint32_t>());
+                       (uint32_t)(l + 1), a2.at<uint32_t>(o_tables[l]), features_d, work, tree, scratch, node_count,
+                       serial);
     MGB_LAUNCH_CHECK("k_level_up");
   }
-  hipLaunchKernelGGL(k_finish, dim3(nf), dim3(kSketchThreads), 0, s, features_d.as<SkFeature>(), tree.as<SkEntry>(),
-                     node_count.as<uint32_t>(), serial.as<uint32_t>(), fin.as<SkEntry>(), fin_scratch.as<uint32_t>(), f0,
-                     max_bin, values.as<float>(), cuts, counts);
+  // k_finish stages the pruned summary's values and the candidate cuts in LDS
+  // for its serial pass when they fit.
+  const uint32_t lds_values = (uint64_t)(max_budget + max_bin) * 4 <= kFinishLds ? max_budget : 0;
+  const uint32_t lds_bytes = lds_values ? (lds_values + max_bin) * 4 : 0;
+  if (lds_bytes &&
+      hipFuncSetAttribute((const void*)k_finish, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess) {
+    set_error("hipFuncSetAttribute(k_finish LDS) failed");
+    return -1;
+  }
+  hipLaunchKernelGGL(k_finish, dim3(nf), dim3(kSketchThreads), lds_bytes, s, features_d, tree, node_count, serial,
+                     a2.at<SkEntry>(o_fin), a2.at<uint32_t>(o_fin_scratch), f0, max_bin, a2.at<float>(o_values), lds_values,
+                     cuts, counts);
   MGB_LAUNCH_CHECK("k_finish");
   MGB_CHECK(hipStreamSynchronize(s));
   return 0;
