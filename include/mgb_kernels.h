@@ -134,6 +134,10 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
  * (kernels/boost.metal:476-499, src/data.cpp:1210-1306).  Sets *any_missing. */
 int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,
                       uint32_t* any_missing);
+/* mgb_quantize_bins that also writes the codes column-major, code (r, f) at
+ * columns[f * rows + r] (bin_bytes each), from the same pass over X. */
+int mgb_quantize_bins_columns(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m,
+                              void* bins, void* columns, uint32_t* any_missing);
 
 /* ---- gradients -------------------------------------------------------- */
 /* Words of the gradient-mass scratch of mgb_gradients / mgb_gradient_mass:

@@ -2,7 +2,9 @@
 // margin fill and tree prediction.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <string>
 
 #include "binary32_exp.hpp"
 #include "device_common.hpp"
@@ -12,55 +14,104 @@ namespace {
 
 // ---------------------------------------------------------------------------
 // Bin matrix (kernels/boost.metal:476-499): bin = min(#{cuts <= v}, count-1),
-// NaN -> missing code.  One thread per (row, padded feature); the row-major
-// output keeps each row's codes contiguous so a histogram workgroup reads a
-// feature group of a row with one vector load.
+// NaN -> missing code.  A workgroup takes `tile_features` consecutive
+// (padded) features, whose cuts it stages in LDS so that every step of the
+// binary search is an LDS read, and walks its rows in chunks: each chunk's
+// values are read row by row (consecutive threads on consecutive features),
+// quantized into an LDS tile, and written in the output layout's own order
+// (consecutive threads on consecutive codes: along a row for the row-major
+// layout, along a column for the column-major copy).
 // ---------------------------------------------------------------------------
+constexpr uint32_t kQuantThreads = 1024;
+constexpr uint32_t kQuantCutsLds = 68 * 1024;   // bytes of staged cuts per workgroup (64 features of 256 cuts, 16 of 1024)
+constexpr uint32_t kQuantChunkCodes = 8192;     // codes per chunk (LDS tile)
+
+// Address of code (r, f) of a bin matrix.
 template <typename BinT>
-__global__ void k_quantize(const float* __restrict__ X, const float* __restrict__ cuts,
-                           const uint32_t* __restrict__ counts, MgbMatrix m, BinT* __restrict__ bins,
-                           uint32_t* __restrict__ any_missing) {
+__device__ __forceinline__ BinT* code_at(BinT* bins, const MgbMatrix& m, uint64_t r, uint32_t f) {
+  const uint32_t g = f / m.group_features, j = f % m.group_features;
+  return reinterpret_cast<BinT*>(reinterpret_cast<uint8_t*>(bins) + (uint64_t)g * m.group_stride + r * m.row_stride) + j;
+}
+
+// tile_features and chunk_rows are powers of two; the cuts of feature j sit
+// at s_cuts + j * (cut_stride + 1) (an odd stride, so that the searches of
+// different features start in different LDS banks).  columns (may be NULL)
+// receives the same codes column-major: code (r, f) at columns[f * rows + r].
+template <typename BinT>
+__global__ __launch_bounds__(kQuantThreads) void k_quantize(const float* __restrict__ X, const float* __restrict__ cuts,
+                                                            const uint32_t* __restrict__ counts, MgbMatrix m,
+                                                            uint32_t tile_shift, uint32_t chunk_shift, uint32_t chunks,
+                                                            BinT* __restrict__ bins, BinT* __restrict__ columns,
+                                                            uint32_t* __restrict__ any_missing) {
+  extern __shared__ __align__(16) uint8_t q_smem[];
+  const uint32_t tile_features = 1u << tile_shift, chunk_rows = 1u << chunk_shift;
+  const uint32_t stride = m.cut_stride + 1;
+  float* s_cuts = reinterpret_cast<float*>(q_smem);  // tile_features x stride
+  uint32_t* s_count = reinterpret_cast<uint32_t*>(s_cuts + (uint64_t)tile_features * stride);
+  BinT* s_codes = reinterpret_cast<BinT*>(s_count + tile_features);  // chunk_rows x tile_features
   const uint32_t G = m.group_features;
-  const uint32_t groups = (m.cols + G - 1) / G;
-  const uint64_t total = (uint64_t)m.rows * groups * G;
-  // Output order: consecutive threads write consecutive codes of the layout
-  // (a row's groups for row-major, a group's rows for group-major).
-  const bool group_major = m.group_stride != (uint64_t)G * sizeof(BinT);
+  const uint32_t padded = (m.cols + G - 1) / G * G;
+  const uint32_t f0 = blockIdx.y << tile_shift;
+  const uint32_t nf = padded - f0 < tile_features ? padded - f0 : tile_features;
+  for (uint32_t j = threadIdx.x; j < tile_features; j += blockDim.x) s_count[j] = f0 + j < m.cols ? counts[f0 + j] : 0u;
+  for (uint32_t j = 0; j < nf; ++j) {
+    if (f0 + j >= m.cols) break;
+    const float* src = cuts + (uint64_t)(f0 + j) * m.cut_stride;
+    for (uint32_t c = threadIdx.x; c < m.cut_stride; c += blockDim.x) s_cuts[j * stride + c] = src[c];
+  }
+  __syncthreads();
   bool missing = false;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (uint64_t)gridDim.x * blockDim.x) {
-    uint32_t r, g, j;
-    if (group_major) {
-      g = (uint32_t)(i / ((uint64_t)m.rows * G));
-      const uint64_t rem = i % ((uint64_t)m.rows * G);
-      r = (uint32_t)(rem / G);
-      j = (uint32_t)(rem % G);
-    } else {
-      r = (uint32_t)(i / ((uint64_t)groups * G));
-      const uint32_t k = (uint32_t)(i % ((uint64_t)groups * G));
-      g = k / G;
-      j = k % G;
-    }
-    const uint32_t f = g * G + j;
-    BinT code = (BinT)m.missing_code;
-    if (f < m.cols) {
-      float v = X[(uint64_t)r * m.cols + f];
-      uint32_t count = counts[f];
-      if (!isnan(v) && count) {
-        const float* column = cuts + (uint64_t)f * m.cut_stride;
-        uint32_t lo = 0, hi = count;
-        while (lo < hi) {
-          uint32_t mid = lo + (hi - lo) / 2;
-          if (v >= column[mid]) lo = mid + 1;
-          else hi = mid;
+  const uint64_t row0 = (uint64_t)blockIdx.x * chunks << chunk_shift;
+  const uint32_t codes = chunk_rows << tile_shift;
+  for (uint32_t chunk = 0; chunk < chunks; ++chunk) {
+    const uint64_t r0 = row0 + ((uint64_t)chunk << chunk_shift);
+    if (r0 >= m.rows) break;
+    const uint32_t nr = m.rows - r0 < chunk_rows ? (uint32_t)(m.rows - r0) : chunk_rows;
+    // Rows in order, features fastest: consecutive threads read a row's
+    // consecutive values.
+    for (uint32_t i = threadIdx.x; i < codes; i += blockDim.x) {
+      const uint32_t rr = i >> tile_shift, j = i & (tile_features - 1);
+      if (rr >= nr || j >= nf) continue;
+      const uint32_t f = f0 + j;
+      BinT code = (BinT)m.missing_code;
+      if (f < m.cols) {
+        const float v = X[(r0 + rr) * m.cols + f];
+        const uint32_t count = s_count[j];
+        if (!isnan(v) && count) {
+          const float* column = s_cuts + j * stride;
+          uint32_t lo = 0, hi = count;
+          while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            if (v >= column[mid]) lo = mid + 1;
+            else hi = mid;
+          }
+          code = (BinT)(lo < count - 1 ? lo : count - 1);
+        } else {
+          missing = true;
         }
-        code = (BinT)(lo < count - 1 ? lo : count - 1);
-      } else {
-        missing = true;
+      }
+      s_codes[i] = code;
+    }
+    __syncthreads();
+    if (m.row_stride == sizeof(BinT) && G == 1) {
+      // A column-major matrix: consecutive threads along a column.
+      for (uint32_t i = threadIdx.x; i < codes; i += blockDim.x) {
+        const uint32_t rr = i & (chunk_rows - 1), j = i >> chunk_shift;
+        if (rr < nr && j < nf) *code_at(bins, m, r0 + rr, f0 + j) = s_codes[(rr << tile_shift) + j];
+      }
+    } else {
+      for (uint32_t i = threadIdx.x; i < codes; i += blockDim.x) {
+        const uint32_t rr = i >> tile_shift, j = i & (tile_features - 1);
+        if (rr < nr && j < nf) *code_at(bins, m, r0 + rr, f0 + j) = s_codes[i];
       }
     }
-    reinterpret_cast<BinT*>(reinterpret_cast<uint8_t*>(bins) + (uint64_t)g * m.group_stride +
-                            (uint64_t)r * m.row_stride)[j] = code;
+    if (columns) {
+      for (uint32_t i = threadIdx.x; i < codes; i += blockDim.x) {
+        const uint32_t rr = i & (chunk_rows - 1), j = i >> chunk_shift;
+        if (rr < nr && j < nf && f0 + j < m.cols) columns[(uint64_t)(f0 + j) * m.rows + r0 + rr] = s_codes[(rr << tile_shift) + j];
+      }
+    }
+    __syncthreads();
   }
   if (__any(missing) && lane_id() == 0) atomicOr(any_missing, 1u);
 }
@@ -315,22 +366,20 @@ __device__ __forceinline__ void two_sum_add(double& s, double& c, double x) {
   s = t;
 }
 
-__global__ __launch_bounds__(1024) void k_base_score(const float* __restrict__ labels,
-                                                     const float* __restrict__ weights, uint32_t rows,
-                                                     uint32_t objective, float spw, float* __restrict__ out) {
-  __shared__ double sh[4][1024];
-  double s = 0, c = 0, ws = 0, wc = 0;
-  for (uint32_t r = threadIdx.x; r < rows; r += blockDim.x) {
-    float w = weights ? weights[r] : 1.0f;
-    float y = labels[r];
-    if (objective == 1 || objective == 2) w *= y == 1.0f ? spw : 1.0f;
-    two_sum_add(s, c, (double)y * (double)w);
-    two_sum_add(ws, wc, (double)w);
-  }
-  sh[0][threadIdx.x] = s; sh[1][threadIdx.x] = c; sh[2][threadIdx.x] = ws; sh[3][threadIdx.x] = wc;
-  __syncthreads();
-  for (uint32_t d = blockDim.x / 2; d > 0; d >>= 1) {
-    if (threadIdx.x < d) {
+// Weighted label sum and weight sum (src/learner.cpp:316-333) as binary64
+// sums with a compensation term each (two-sum), first per workgroup over a
+// strided share of the rows, then over the workgroups' partials by the last
+// workgroup; the mean is rounded once to binary32.  Products of two binary32
+// values are exact in binary64, and the compensated sums carry about twice
+// binary64's precision, so the result does not depend on the summation order.
+constexpr uint32_t kBaseThreads = 1024;
+constexpr uint32_t kBaseBlocks = 256;
+__device__ double g_base_partials[kBaseBlocks][4];
+__device__ uint32_t g_base_ticket;
+
+__device__ void base_tree(double (*sh)[kBaseThreads], uint32_t n) {
+  for (uint32_t d = kBaseThreads / 2; d > 0; d >>= 1) {
+    if (threadIdx.x < d && threadIdx.x + d < n) {
       double a = sh[0][threadIdx.x], ac = sh[1][threadIdx.x];
       two_sum_add(a, ac, sh[0][threadIdx.x + d]);
       ac += sh[1][threadIdx.x + d];
@@ -341,7 +390,40 @@ __global__ __launch_bounds__(1024) void k_base_score(const float* __restrict__ l
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(kBaseThreads) void k_base_score(const float* __restrict__ labels,
+                                                             const float* __restrict__ weights, uint32_t rows,
+                                                             uint32_t objective, float spw, float* __restrict__ out) {
+  __shared__ double sh[4][kBaseThreads];
+  __shared__ uint32_t s_last;
+  double s = 0, c = 0, ws = 0, wc = 0;
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+    float w = weights ? weights[r] : 1.0f;
+    float y = labels[r];
+    if (objective == 1 || objective == 2) w *= y == 1.0f ? spw : 1.0f;
+    two_sum_add(s, c, (double)y * (double)w);
+    two_sum_add(ws, wc, (double)w);
+  }
+  sh[0][threadIdx.x] = s; sh[1][threadIdx.x] = c; sh[2][threadIdx.x] = ws; sh[3][threadIdx.x] = wc;
+  __syncthreads();
+  base_tree(sh, kBaseThreads);
   if (threadIdx.x == 0) {
+    for (int k = 0; k < 4; ++k) g_base_partials[blockIdx.x][k] = sh[k][0];
+    __threadfence();
+    s_last = atomicAdd(&g_base_ticket, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // The last workgroup: every partial is visible after its fence.
+  __threadfence();
+  const uint32_t n = gridDim.x;
+  for (int k = 0; k < 4; ++k)
+    sh[k][threadIdx.x] = threadIdx.x < n ? __builtin_nontemporal_load(&g_base_partials[threadIdx.x][k]) : 0.0;
+  __syncthreads();
+  base_tree(sh, n);
+  if (threadIdx.x == 0) {
+    g_base_ticket = 0;  // ready for the next call on this stream
     double value = sh[0][0] + sh[1][0], weight = sh[2][0] + sh[3][0];
     float result;
     if (!(weight > 0)) result = objective == 0 && rows == 0 ? 0.0f : 0.5f;
@@ -411,8 +493,8 @@ using namespace mgb;
 
 extern "C" {
 
-int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,
-                      uint32_t* any_missing) {
+static int quantize(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,
+                    void* columns, uint32_t* any_missing) {
   if (!m || !bins || !any_missing) { set_error("mgb_quantize_bins: null argument"); return -1; }
   if (m->bin_bytes != 1 && m->bin_bytes != 2) { set_error("mgb_quantize_bins: bin_bytes must be 1 or 2"); return -1; }
   const uint32_t G = m->group_features;
@@ -427,17 +509,53 @@ int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts,
     set_error("mgb_quantize_bins: row_stride/group_stride describe neither the row-major nor the group-major layout");
     return -1;
   }
-  uint64_t total = (uint64_t)m->rows * groups * G;
-  if (!total) return 0;
-  uint32_t grid = grid_for(total, 256, 65535);
-  if (m->bin_bytes == 1)
-    hipLaunchKernelGGL(k_quantize<uint8_t>, dim3(grid), dim3(256), 0, stream(), X, cuts, counts, *m,
-                       (uint8_t*)bins, any_missing);
-  else
-    hipLaunchKernelGGL(k_quantize<uint16_t>, dim3(grid), dim3(256), 0, stream(), X, cuts, counts, *m,
-                       (uint16_t*)bins, any_missing);
+  if (!m->rows || !m->cols) return 0;
+  if (((uint64_t)m->cut_stride + 1) * 4 > kQuantCutsLds) {
+    set_error("mgb_quantize_bins: cut_stride above " + std::to_string(kQuantCutsLds / 4 - 1) + " cuts per feature");
+    return -1;
+  }
+  // Features per workgroup: the largest power of two (at most 64) whose cuts
+  // fit the staging budget; rows in chunks of kQuantChunkCodes codes, and as
+  // many chunks per workgroup as keep about 2048 workgroups busy.
+  const uint32_t padded = (uint32_t)(groups * G);
+  uint32_t tile_shift = 6;
+  while (tile_shift > 0 && ((((uint64_t)1 << tile_shift) * (m->cut_stride + 1) * 4 > kQuantCutsLds) ||
+                            (1u << (tile_shift - 1)) >= padded))
+    --tile_shift;
+  uint32_t chunk_shift = 0;
+  while ((1u << (chunk_shift + 1 + tile_shift)) <= kQuantChunkCodes) ++chunk_shift;
+  const uint32_t tiles = (padded + (1u << tile_shift) - 1) >> tile_shift;
+  const uint64_t row_chunks = (m->rows + (1ull << chunk_shift) - 1) >> chunk_shift;
+  const uint32_t chunks =
+      (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(8, row_chunks * tiles / 2048));
+  const dim3 grid((uint32_t)((row_chunks + chunks - 1) / chunks), tiles);
+  const uint32_t lds = (1u << tile_shift) * ((m->cut_stride + 1) * 4 + 4) + (1u << (chunk_shift + tile_shift)) * m->bin_bytes;
+  if (m->bin_bytes == 1) {
+    if (check(hipFuncSetAttribute((const void*)k_quantize<uint8_t>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "hipFuncSetAttribute(k_quantize)"))
+      return -1;
+    hipLaunchKernelGGL(k_quantize<uint8_t>, grid, dim3(kQuantThreads), lds, stream(), X, cuts, counts, *m, tile_shift,
+                       chunk_shift, chunks, (uint8_t*)bins, (uint8_t*)columns, any_missing);
+  } else {
+    if (check(hipFuncSetAttribute((const void*)k_quantize<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "hipFuncSetAttribute(k_quantize)"))
+      return -1;
+    hipLaunchKernelGGL(k_quantize<uint16_t>, grid, dim3(kQuantThreads), lds, stream(), X, cuts, counts, *m, tile_shift,
+                       chunk_shift, chunks, (uint16_t*)bins, (uint16_t*)columns, any_missing);
+  }
   MGB_LAUNCH_CHECK("k_quantize");
   return 0;
+}
+
+int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,
+                      uint32_t* any_missing) {
+  return quantize(X, cuts, counts, m, bins, nullptr, any_missing);
+}
+
+int mgb_quantize_bins_columns(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m,
+                              void* bins, void* columns, uint32_t* any_missing) {
+  if (!columns) { set_error("mgb_quantize_bins_columns: null columns"); return -1; }
+  return quantize(X, cuts, counts, m, bins, columns, any_missing);
 }
 
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
@@ -464,7 +582,8 @@ int mgb_gradient_scales(uint64_t* mass, float* scales) {
 
 int mgb_base_score(const float* labels, const float* weights, uint32_t rows, uint32_t objective,
                    float scale_pos_weight, float* out) {
-  hipLaunchKernelGGL(k_base_score, dim3(1), dim3(1024), 0, stream(), labels, weights, rows, objective,
+  const uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>(kBaseBlocks, (rows + kBaseThreads - 1) / kBaseThreads));
+  hipLaunchKernelGGL(k_base_score, dim3(grid), dim3(kBaseThreads), 0, stream(), labels, weights, rows, objective,
                      scale_pos_weight, out);
   MGB_LAUNCH_CHECK("k_base_score");
   return 0;

@@ -300,20 +300,13 @@ void DMatrix::relayout(int layout) {
   matrix.group_stride = group_major ? (uint64_t)rows * gbytes : gbytes;
   d_bins.ensure((size_t)rows * groups * gbytes);
   kcheck(mgb_memset(d_missing.get(), 0, sizeof(uint32_t)), "memset");
-  kcheck(mgb_quantize_bins(d_data.as<float>(), d_cuts.as<float>(), d_counts.as<uint32_t>(), &matrix, d_bins.get(),
-                           d_missing.as<uint32_t>()),
-         "bin matrix");
-  // Column-major copy (one feature's codes contiguous over rows): the row
-  // partition reads a single feature per node, 1-2 bytes a row instead of a
-  // cache line of the row-major matrix.
-  MgbMatrix columns = matrix;
-  columns.group_features = 1;
-  columns.row_stride = matrix.bin_bytes;
-  columns.group_stride = (uint64_t)rows * matrix.bin_bytes;
+  // With the column-major copy (one feature's codes contiguous over rows):
+  // the row partition reads a single feature per node, 1-2 bytes a row
+  // instead of a cache line of the row-major matrix.
   d_columns.ensure((size_t)rows * cols * matrix.bin_bytes);
-  kcheck(mgb_quantize_bins(d_data.as<float>(), d_cuts.as<float>(), d_counts.as<uint32_t>(), &columns,
-                           d_columns.get(), d_missing.as<uint32_t>()),
-         "column codes");
+  kcheck(mgb_quantize_bins_columns(d_data.as<float>(), d_cuts.as<float>(), d_counts.as<uint32_t>(), &matrix,
+                                   d_bins.get(), d_columns.get(), d_missing.as<uint32_t>()),
+         "bin matrix");
   kcheck(mgb_synchronize(), "synchronize");
   quantize_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   quantized_layout = layout;
