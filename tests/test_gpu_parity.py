@@ -445,6 +445,44 @@ def test_weighted_million_root_literal(xgb, quantile):
     np.testing.assert_array_equal(bst.predict(xgb.DMatrix(X)).view(np.uint32), ref["margin"].view(np.uint32))
 
 
+@pytest.mark.parametrize("quantile", [False, True])
+def test_weighted_4096_bin_root_literal(xgb, quantile):
+    """The reference's literal 2990026907 (tests/test_parent_statistics.py:55-68)
+    at max_bin 4096 from a DMatrix and a QuantileDMatrix: the root's base weight
+    of a weighted depth-1 tree; cuts, tree and margins equal the oracle's."""
+    X, y, weight = W.weighted_benchmark()
+    params = dict(W.WEIGHTED_BENCHMARK_PARAMS)
+    d = (xgb.QuantileDMatrix(X, label=y, weight=weight, max_bin=4096) if quantile
+         else xgb.DMatrix(X, label=y, weight=weight))
+    bst = xgb.train(params, d, 1)
+    root = np.float32(bst.trees_to_json()[0]["base_weights"][0])
+    assert int(root.view(np.uint32)) == W.WEIGHTED_BENCHMARK_ROOT_BITS
+    ref = O.train(X, y, _oracle_params(params), 1, weights=weight)
+    cut_ptr, cut_values = d.get_quantile_cut()
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    for f in range(X.shape[1]):
+        np.testing.assert_array_equal(cut_values[cut_ptr[f]:cut_ptr[f + 1]].view(np.uint32),
+                                      ref["cuts"][f, :ref["cut_counts"][f]].view(np.uint32))
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(xgb.DMatrix(X)).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+@pytest.mark.parametrize("max_bin,missing", [(2048, True), (4096, False), (4096, True)])
+def test_large_bin_counts_match_oracle(xgb, max_bin, missing):
+    """More than 1024 bins (u16 codes, one or two features per histogram
+    group, 16 waves per split item): cuts, trees and margins of a depth-6
+    model with and without missing values equal the oracle's."""
+    X, y = W.config1(rows=30000, cols=12) if missing else W.config0(rows=30000, cols=12)
+    params = {"tree_method": "hist", "max_depth": 6, "max_bin": max_bin, "eta": 0.3}
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train(params, d, 3)
+    ref = O.train(X, y, _oracle_params(params), 3)
+    cut_ptr, _ = d.get_quantile_cut()
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))
+
+
 def test_seed_per_iteration_queued_equals_stepwise_and_oracle(xgb):
     """seed_per_iteration reseeds the engine with seed * 127 + the number of
     rounds already boosted (src/learner.cpp:668), counting rounds still

@@ -374,3 +374,15 @@ def test_weighted_million_root_literal(fma):
     ref = O.train(X, y, O.make_params(max_depth=1, max_bin=256, seed=9, fma_contract=fma), 1, weights=weight)
     bits = int(np.float32(ref["trees"][0]["base_weight"][0]).view(np.uint32))
     assert bits == W.WEIGHTED_MILLION_ROOT_BITS
+
+
+@pytest.mark.parametrize("fma", [1, 0])
+def test_weighted_4096_bin_root_literal(fma):
+    """The reference's literal 2990026907 (tests/test_parent_statistics.py:55-68):
+    weighted squared error over 100,000 dense rows with 4096 bins, depth 1 --
+    the root's stored base weight, whose last bit the ordered bin sum fixes."""
+    X, y, weight = W.weighted_benchmark()
+    ref = O.train(X, y, O.make_params(max_depth=1, max_bin=4096, seed=9, fma_contract=fma), 1, weights=weight)
+    assert list(ref["cut_counts"]) == [4096] * 4
+    bits = int(np.float32(ref["trees"][0]["base_weight"][0]).view(np.uint32))
+    assert bits == W.WEIGHTED_BENCHMARK_ROOT_BITS

@@ -111,6 +111,25 @@ def weighted_million():
 
 
 WEIGHTED_MILLION_ROOT_BITS = 2915099116
+
+
+def weighted_benchmark():
+    """The reference's 4096-bin construction (tests/test_parent_statistics.py:
+    55-68): 100,000 rows of default_rng(43) N(0,1) x 32, y = 2 x0 + x1^2 +
+    N(0, 0.1), the first four columns kept; weights default_rng(144)
+    uniform(0.1, 2).  With depth 1, max_bin 4096 and seed 9, one round's root
+    base weight has the bits 2990026907 in the reference's CPU oracle build."""
+    rng = np.random.default_rng(43)
+    original = rng.normal(size=(100000, 32)).astype(np.float32)
+    noise = rng.normal(0, 0.1, len(original))
+    y = (2 * original[:, 0] + original[:, 1] ** 2 + noise).astype(np.float32)
+    X = original[:, :4].copy()
+    weight = np.random.default_rng(144).uniform(0.1, 2.0, len(X)).astype(np.float32)
+    return X, y, weight
+
+
+WEIGHTED_BENCHMARK_ROOT_BITS = 2990026907
+WEIGHTED_BENCHMARK_PARAMS = {"tree_method": "hist", "max_depth": 1, "max_bin": 4096, "seed": 9}
 WEIGHTED_MILLION_PARAMS = {"tree_method": "hist", "max_depth": 1, "max_bin": 256, "seed": 9}
 
 

@@ -1172,7 +1172,7 @@ int XGQuantileDMatrixCreateFromCallback(DataIterHandle iter, DMatrixHandle proxy
   uint32_t bins = 256;
   if (c.contains("max_bin") && !c.at("max_bin").is_null()) {
     const int64_t v = c.at("max_bin").integer();
-    require(v >= 2 && v <= 1086, "max_bin must be in [2, 1086].");
+    require(v >= 2 && v <= 4096, "max_bin must be in [2, 4096].");
     bins = (uint32_t)v;
   }
   auto d = from_iterator(iter, proxy, reset, next, config);

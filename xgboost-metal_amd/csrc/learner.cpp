@@ -409,7 +409,7 @@ void Learner::configure_check() const {
                    "scale_pos_weight"})
     require(number(key, 0) >= 0, std::string("Parameter must be nonnegative: ") + key);
   auto bins = integer("max_bin", 256);
-  require(bins >= 2 && bins <= 1086, "max_bin must be in [2, 1086].");
+  require(bins >= 2 && bins <= 4096, "max_bin must be in [2, 4096].");
 }
 
 float Learner::base_margin_value() const {

@@ -780,20 +780,21 @@ __global__ void k_zero_built(Tree t, uint32_t depth) {
 }
 
 // CSR root histogram from the column-major codes: every row belongs to the
-// root, so a workgroup takes kRootFeatures consecutive features, accumulates
+// root, so a workgroup takes up to kRootFeatures consecutive features (as many
+// as fit 160 KB of LDS), accumulates
 // all their nonzeros in LDS and writes the features' whole bank rows with
 // plain stores -- no device atomics, which at the root would all land on one
 // node's histogram from every XCD at once.
 constexpr uint32_t kRootFeatures = 4;
 constexpr uint32_t kRootThreads = 512;
 template <typename BinT>
-__global__ __launch_bounds__(kRootThreads) void k_histogram_csc_root(Tree t) {
+__global__ __launch_bounds__(kRootThreads) void k_histogram_csc_root(Tree t, uint32_t per_group) {
   extern __shared__ __align__(16) uint8_t smem[];
   unsigned long long* lh = reinterpret_cast<unsigned long long*>(smem);  // [feature][bin][g, h]
   const uint32_t B1 = t.bins1;
-  const uint32_t f0 = blockIdx.x * kRootFeatures;
-  const uint32_t nf = t.cols - f0 < kRootFeatures ? t.cols - f0 : kRootFeatures;
-  for (uint32_t i = threadIdx.x; i < kRootFeatures * B1 * 2; i += blockDim.x) lh[i] = 0;
+  const uint32_t f0 = blockIdx.x * per_group;
+  const uint32_t nf = t.cols - f0 < per_group ? t.cols - f0 : per_group;
+  for (uint32_t i = threadIdx.x; i < per_group * B1 * 2; i += blockDim.x) lh[i] = 0;
   uint64_t bound[kRootFeatures + 1];
 #pragma unroll
   for (uint32_t j = 0; j <= kRootFeatures; ++j) bound[j] = t.csc_colptr[f0 + (j < nf ? j : nf)];
@@ -1436,19 +1437,22 @@ __device__ void ordered_sum(const double* sg, const double* sh, uint32_t steps, 
   *h = b;
 }
 
-constexpr uint32_t kMaxBins1 = 1088;  // max_bin + 1 for max_bin <= 1087
+// Largest max_bin of the tree kernels: the dense root's select stages 4096 + 1
+// bins of two features (147.5 KB of LDS), the split kernel holds 16 waves x
+// 64 lanes x 4 bins in registers, and a 2-feature histogram group fits LDS.
+constexpr uint32_t kMaxBin = 4096;
 
-// Stage feature f's bins as binary64 statistics: out[0][b] = g, out[1][b] = h.
-__device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh, double (*out)[kMaxBins1]) {
+// Stage feature f's bins as binary64 statistics: g[b], h[b].
+__device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh, double* g, double* h) {
   for (uint32_t b = threadIdx.x; b < count; b += blockDim.x) {
-    out[0][b] = stat_value(fh[2 * b], eg);
-    out[1][b] = stat_value(fh[2 * b + 1], eh);
+    g[b] = stat_value(fh[2 * b], eg);
+    h[b] = stat_value(fh[2 * b + 1], eh);
   }
 }
 
 // LDS the select bookkeeping needs at the dense root: feature 0's and the
 // chosen feature's bins as binary64 (g, h) and the chosen feature's cuts.
-constexpr size_t kRootStageBytes = 4 * kMaxBins1 * sizeof(double) + kMaxBins1 * sizeof(float);
+size_t root_stage_bytes(uint32_t bins1) { return 4ull * bins1 * sizeof(double) + (size_t)bins1 * sizeof(float); }
 
 __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   __shared__ uint32_t scan[kPartThreads / kWave + 1];
@@ -1474,16 +1478,18 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   // so the serial ordered sums below read LDS, not scattered global words.
   // The chosen feature's cuts are staged too: the threshold search below
   // would otherwise be a chain of dependent global loads.
-  double (*root0)[kMaxBins1] = reinterpret_cast<double (*)[kMaxBins1]>(stage);
-  double (*rootf)[kMaxBins1] = reinterpret_cast<double (*)[kMaxBins1]>(stage + 2 * kMaxBins1 * sizeof(double));
-  float* rootcut = reinterpret_cast<float*>(stage + 4 * kMaxBins1 * sizeof(double));
+  double* root0g = reinterpret_cast<double*>(stage);
+  double* root0h = root0g + t.bins1;
+  double* rootfg = root0h + t.bins1;
+  double* rootfh = rootfg + t.bins1;
+  float* rootcut = reinterpret_cast<float*>(rootfh + t.bins1);
   const bool dense_root = depth == 0 && t.dense && n > 0;
   if (dense_root) {
     const uint64_t key = best_keys[0];
     const uint32_t f = key ? ~(uint32_t)key : 0u;
     const uint32_t cf = t.counts[f];
-    stage_feature(t.hist[0], t.counts[0], eg, eh, root0);
-    stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, cf, eg, eh, rootf);
+    stage_feature(t.hist[0], t.counts[0], eg, eh, root0g, root0h);
+    stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, cf, eg, eh, rootfg, rootfh);
     for (uint32_t b = threadIdx.x; b < cf; b += blockDim.x) rootcut[b] = t.cuts[(uint64_t)f * t.cut_stride + b];
     __syncthreads();
   }
@@ -1516,7 +1522,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
         // chosen child's bin range (kernels/scalar_root.metal.h:1-105).
         const uint32_t c0 = t.counts[0];
         double tg, th;
-        ordered_sum(root0[0], root0[1], c0, false, c0, &tg, &th);
+        ordered_sum(root0g, root0h, c0, false, c0, &tg, &th);
         parent_w = clamp_weight(calc_weight(tg, th, p), node.lower, node.upper);
         total_h = (float)th;
         if (best.feature >= 0 && (uint32_t)best.feature < F) {
@@ -1534,7 +1540,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
             steps = bin < count ? count - bin : 0;
           }
           double cg, ch;
-          ordered_sum(rootf[0], rootf[1], steps, best.default_left != 0, count, &cg, &ch);
+          ordered_sum(rootfg, rootfh, steps, best.default_left != 0, count, &cg, &ch);
           double og = tg - cg, oh = th - ch;
           double ag = cg + og, ah = ch + oh;
           applied_w = clamp_weight(calc_weight(ag, ah, p), node.lower, node.upper);
@@ -2034,7 +2040,7 @@ int dispatch_hist(const Tree& t, uint32_t depth, uint32_t grid) {
 // Waves per split item with four bins per lane (every bin in registers).
 uint32_t split_waves(uint32_t max_bin) {
   uint32_t w = 1;
-  while (w < 8 && w * kWave * 4 < max_bin) w *= 2;
+  while (w < 16 && w * kWave * 4 < max_bin) w *= 2;
   return w;
 }
 
@@ -2053,7 +2059,8 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
       case 1: launch(MGB_PROF_SPLIT, k_split<1, 4>, grid, block, 0, t, depth); break;
       case 2: launch(MGB_PROF_SPLIT, k_split<2, 4>, grid, block, 0, t, depth); break;
       case 4: launch(MGB_PROF_SPLIT, k_split<4, 4>, grid, block, 0, t, depth); break;
-      default: launch(MGB_PROF_SPLIT, k_split<8, 4>, grid, block, 0, t, depth); break;
+      case 8: launch(MGB_PROF_SPLIT, k_split<8, 4>, grid, block, 0, t, depth); break;
+      default: launch(MGB_PROF_SPLIT, k_split<16, 4>, grid, block, 0, t, depth); break;
     }
   } else {
     switch (w) {
@@ -2070,7 +2077,7 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
 // bookkeeping workgroup; the dense root stages two features in LDS.
 template <typename BinT>
 int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
-  const uint32_t lds = depth == 0 && t.dense ? (uint32_t)kRootStageBytes : 0u;
+  const uint32_t lds = depth == 0 && t.dense ? (uint32_t)root_stage_bytes(t.bins1) : 0u;
   auto fn = depth == 0 && !t.compact ? k_apply<BinT, true> : k_apply<BinT, false>;
   if (lds && hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
     set_error("hipFuncSetAttribute(select LDS) failed");
@@ -2102,7 +2109,7 @@ int validate(const MgbTreeShape* s, const MgbMatrix* m) {
     set_error("root_rows_per_tile must be 0 or >= rows_per_tile");
     return -1;
   }
-  if (m->max_bin < 1 || m->max_bin > 1086) { set_error("max_bin must be in [1, 1086]"); return -1; }
+  if (m->max_bin < 1 || m->max_bin > kMaxBin) { set_error("max_bin must be in [1, " + std::to_string(kMaxBin) + "]"); return -1; }
   if ((size_t)G * (m->max_bin + 1) * 16 > 160 * 1024) { set_error("feature group does not fit in LDS"); return -1; }
   return 0;
 }
@@ -2319,14 +2326,16 @@ namespace {
 // given, else clear the built nodes' rows and add their rows' nonzeros.
 int csr_histogram(const Tree& t, uint32_t bin_bytes, uint32_t depth, bool root_columns, uint32_t hgrid, uint32_t zx) {
   if (depth == 0 && root_columns) {
-    const uint32_t lds = kRootFeatures * t.bins1 * 16;
-    const dim3 grid(div_up(t.cols, kRootFeatures));
+    uint32_t per_group = kRootFeatures;
+    while (per_group > 1 && per_group * t.bins1 * 16 > 160 * 1024) per_group >>= 1;
+    const uint32_t lds = per_group * t.bins1 * 16;
+    const dim3 grid(div_up(t.cols, per_group));
     auto fn = bin_bytes == 1 ? k_histogram_csc_root<uint8_t> : k_histogram_csc_root<uint16_t>;
     if (hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
       set_error("hipFuncSetAttribute(root histogram LDS) failed");
       return -1;
     }
-    launch(MGB_PROF_HISTOGRAM, fn, grid, dim3(kRootThreads), lds, t);
+    launch(MGB_PROF_HISTOGRAM, fn, grid, dim3(kRootThreads), lds, t, per_group);
     MGB_LAUNCH_CHECK("k_histogram_csc_root");
     return 0;
   }
@@ -2359,7 +2368,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
     return -1;
   }
   if (m->bin_bytes != 1 && m->bin_bytes != 2) { set_error("bin_bytes must be 1 or 2"); return -1; }
-  if (m->max_bin < 1 || m->max_bin > 1086) { set_error("max_bin must be in [1, 1086]"); return -1; }
+  if (m->max_bin < 1 || m->max_bin > kMaxBin) { set_error("max_bin must be in [1, " + std::to_string(kMaxBin) + "]"); return -1; }
   if (shape->rows_per_tile < 64) { set_error("rows_per_tile must be >= 64"); return -1; }
   if (!shape->features_per_group) { set_error("features_per_group must be at least 1"); return -1; }
   Layout L = layout(*shape);
