@@ -330,33 +330,11 @@ __device__ __forceinline__ uint32_t block_inclusive_max_u32(uint32_t v, uint32_t
 }
 
 // kernels/quantile.metal.h:192-214 (sketch_prune_serial), data-parallel.
-// The serial loop takes, for each query k in [1, n), n = capacity - 1, the
-// entry i_k whose rank sums rmax + rmin bracket rank_k =
-// 2 (k range / n + begin) (binary32), where i_k + 1 is the first j >= 2 with
-// rank_k < rmax_j + rmin_j, then picks i_k or i_k + 1 by the midpoint test;
-// "append if different from the last" keeps the first k of each run of equal
-// choices.  Both rank_k and the sums are nondecreasing, so the first query
-// that reaches key_j = rmax_j + rmin_j, kmin(j), is a binary search over k on
-// the rank formula alone, and i_k + 1 = j exactly for kmin(j-1) <= k <
-// kmin(j): each entry writes its queries' j into `first` (capacity words),
-// then every query reads it back.  in[0..size) -> out (out != in).
-__device__ __forceinline__ float prune_rank(uint32_t k, float range, uint32_t n, float begin) {
-  return 2.0f * (((float)k * range) / (float)n + begin);
-}
-
-// The first k in [1, n) with prune_rank(k) >= key, or n if there is none.
-__device__ __forceinline__ uint32_t prune_kmin(float key, float range, uint32_t n, float begin) {
-  uint32_t lo = 1, hi = n;
-  while (lo < hi) {
-    const uint32_t mid = lo + (hi - lo) / 2;
-    if (prune_rank(mid, range, n, begin) >= key) hi = mid;
-    else lo = mid + 1;
-  }
-  return lo;
-}
-
-__device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, SkEntry* out, uint32_t* scan,
-                          uint32_t* first) {
+// The serial loop walks i forward while rank_k >= rmax_{i+1} + rmin_{i+1};
+// both ranks and these sums are nondecreasing, so i_k is a binary search and
+// the chosen indices c_k are nondecreasing: "append if c_k != last" keeps the
+// first k of each run of equal c_k.  in[0..size) -> out (out != in).
+__device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, SkEntry* out, uint32_t* scan) {
   __shared__ uint32_t s_last, s_dead;
   __shared__ uint32_t s_wave_tail[kSketchThreads / kWave];
   if (size <= capacity) {
@@ -372,29 +350,6 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
   }
   const float begin = in[0].rmax, range = in[size - 1].rmin - begin;
   const uint32_t n = capacity - 1;
-  // first[k] = j, the first j >= 2 with rank_k < key_j (size if none).
-  if (range >= 0.0f) {
-    // rank_k is nondecreasing in k: first[k] = j for k in
-    // [kmin(j - 1), kmin(j)), with kmin(1) = 1 and kmin(size) = n.
-    for (uint32_t j = 2 + threadIdx.x; j <= size; j += blockDim.x) {
-      const uint32_t k0 = j == 2 ? 1u : prune_kmin(in[j - 1].rmax + in[j - 1].rmin, range, n, begin);
-      const uint32_t k1 = j == size ? n : prune_kmin(in[j].rmax + in[j].rmin, range, n, begin);
-      for (uint32_t k = k0; k < k1; ++k) first[k] = j;
-    }
-  } else {
-    // A summary whose first entry's rmax exceeds its last entry's rmin: the
-    // query ranks decrease, so each query searches the keys itself.
-    for (uint32_t k = 1 + threadIdx.x; k < n; k += blockDim.x) {
-      const float rank = prune_rank(k, range, n, begin);
-      uint32_t lo = 2, hi = size;
-      while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (rank >= in[mid].rmax + in[mid].rmin) lo = mid + 1;
-        else hi = mid;
-      }
-      first[k] = lo;
-    }
-  }
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
   if (threadIdx.x == 0) { out[0] = in[0]; s_last = 0; s_dead = 0; }
   __syncthreads();
@@ -404,8 +359,14 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
     uint32_t choice = 0;
     bool live = false;
     if (k < n) {
-      const float rank = prune_rank(k, range, n, begin);
-      const uint32_t i = first[k] - 1;
+      const float rank = 2.0f * (((float)k * range) / (float)n + begin);
+      uint32_t lo = 2, hi = size;  // first j in [2, size) with rank < rmax_j + rmin_j
+      while (lo < hi) {
+        uint32_t mid = lo + (hi - lo) / 2;
+        if (rank >= in[mid].rmax + in[mid].rmin) lo = mid + 1;
+        else hi = mid;
+      }
+      const uint32_t i = lo - 1;
       if (i < size - 1) {
         live = true;
         choice = rank < min_next(in[i]) + max_prev(in[i + 1]) ? i : i + 1;
@@ -439,63 +400,10 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
   return count;
 }
 
-constexpr uint32_t kRankTile = 4096;  // values of the other summary staged in LDS per chunk
-
-// First position in y[lo, hi) whose value is not below v (hi if none).
-__device__ __forceinline__ uint32_t lower_bound_value(const SkEntry* y, uint32_t lo, uint32_t hi, float v) {
-  while (lo < hi) {
-    const uint32_t mid = lo + (hi - lo) / 2;
-    if (y[mid].value < v) lo = mid + 1;
-    else hi = mid;
-  }
-  return lo;
-}
-
-// visit(i, r) for every i < n with r = #{j < m : y_j < x_i} (x and y
-// strictly increasing).  In chunks of blockDim.x entries of x: the chunk's
-// r lie between those of its first and last entries (two binary searches),
-// and that y range is staged in LDS when it holds at most kRankTile values,
-// else searched in place.
-template <typename Visit>
-__device__ void for_each_rank(const SkEntry* x, uint32_t n, const SkEntry* y, uint32_t m, Visit visit) {
-  __shared__ float tile[kRankTile];
-  __shared__ uint32_t s_lo, s_hi;
-  for (uint32_t base = 0; base < n; base += blockDim.x) {
-    const uint32_t last = (n - base < blockDim.x ? n : base + blockDim.x) - 1;
-    if (threadIdx.x == 0) s_lo = lower_bound_value(y, 0, m, x[base].value);
-    if (threadIdx.x == kWave) s_hi = lower_bound_value(y, 0, m, x[last].value);
-    __syncthreads();
-    const uint32_t lo = s_lo, span = s_hi - s_lo;
-    const bool staged = span <= kRankTile;
-    if (staged)
-      for (uint32_t t = threadIdx.x; t < span; t += blockDim.x) tile[t] = y[lo + t].value;
-    __syncthreads();
-    const uint32_t i = base + threadIdx.x;
-    if (i < n) {
-      const float v = x[i].value;
-      uint32_t r;
-      if (staged) {
-        uint32_t a = 0, b = span;
-        while (a < b) {
-          const uint32_t mid = a + (b - a) / 2;
-          if (tile[mid] < v) a = mid + 1;
-          else b = mid;
-        }
-        r = lo + a;
-      } else {
-        r = lower_bound_value(y, lo, lo + span, v);
-      }
-      visit(i, r);
-    }
-    __syncthreads();
-  }
-}
-
 // kernels/quantile.metal.h:266-311 (sketch_combine_serial), merge-path form.
-// a[0..n) and b[0..m) -> out; out must differ from both.  scratch needs
-// 2n + 1 words (equal-pair prefix, then each a entry's rank in b).
+// a[0..n) and b[0..m) -> out; out must differ from both.
 __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint32_t m, SkEntry* out,
-                            uint32_t* scratch, uint32_t* scan) {
+                            uint32_t* eq_prefix, uint32_t* scan) {
   if (!m) {
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = a[i];
     __syncthreads();
@@ -506,19 +414,19 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
     __syncthreads();
     return m;
   }
-  uint32_t* eq_prefix = scratch;        // #equal-value pairs with a-index < i
-  uint32_t* rank_a = scratch + n + 1;   // #b values below a_i
-  for_each_rank(a, n, b, m, [&](uint32_t i, uint32_t r) { rank_a[i] = r; });
+  // Equal-value pairs, indexed by a: eq_prefix[i] = #pairs with a-index < i.
   uint32_t carry = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
-    const uint32_t i = base + threadIdx.x;
+    uint32_t i = base + threadIdx.x;
     uint32_t eq = 0;
     if (i < n) {
-      const uint32_t r = rank_a[i];
-      eq = r < m && b[r].value == a[i].value;
+      float x = a[i].value;
+      uint32_t lo = 0, hi = m;
+      while (lo < hi) { uint32_t mid = lo + (hi - lo) / 2; if (b[mid].value < x) lo = mid + 1; else hi = mid; }
+      eq = lo < m && b[lo].value == x;
     }
     uint32_t total;
-    const uint32_t off = block_exclusive_u32(eq, scan, &total);
+    uint32_t off = block_exclusive_u32(eq, scan, &total);
     if (i < n) eq_prefix[i] = carry + off;
     carry += total;
   }
@@ -528,7 +436,8 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
   const float tail_a = a[n - 1].rmax, tail_b = b[m - 1].rmax;
   for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
     const SkEntry x = a[i];
-    const uint32_t lo = rank_a[i];
+    uint32_t lo = 0, hi = m;
+    while (lo < hi) { uint32_t mid = lo + (hi - lo) / 2; if (b[mid].value < x.value) lo = mid + 1; else hi = mid; }
     SkEntry r;
     if (lo < m && b[lo].value == x.value) {
       const SkEntry y = b[lo];
@@ -540,16 +449,17 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
     }
     out[i + lo - eq_prefix[i]] = r;
   }
-  for_each_rank(b, m, a, n, [&](uint32_t j, uint32_t lo) {
+  for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) {
     const SkEntry y = b[j];
-    if (lo < n && a[lo].value == y.value) return;
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) { uint32_t mid = lo + (hi - lo) / 2; if (a[mid].value < y.value) lo = mid + 1; else hi = mid; }
+    if (lo < n && a[lo].value == y.value) continue;
     float prev_a = lo > 0 ? min_next(a[lo - 1]) : 0.0f;
     float add = lo < n ? max_prev(a[lo]) : tail_a;
     SkEntry r;
     r.rmin = y.rmin + prev_a; r.rmax = y.rmax + add; r.wmin = y.wmin; r.value = y.value;
     out[j + lo - eq_prefix[lo]] = r;
-  });
-
+  }
   __syncthreads();
   // Error fix-up: rmin = prefix max of rmin; rmax = prefix max of
   // max(rmax, rmin' + wmin).  All values are nonnegative, so binary32 order
@@ -687,8 +597,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_level0(const uint32_t* __res
   SkEntry* summary = work + fe.base + begin;
   const uint32_t n = summarize(index + fe.base + begin, run_v + fe.base, run_w + fe.base, size, fe.exact != 0,
                                summary, scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), scan);
-  const uint32_t m = prune(summary, n, fe.limit, tree + fe.tree + (uint64_t)b * fe.limit, scan,
-                           scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2));
+  const uint32_t m = prune(summary, n, fe.limit, tree + fe.tree + (uint64_t)b * fe.limit, scan);
   if (threadIdx.x == 0) node_count[fe.node_base + b] = m;
 }
 
@@ -722,8 +631,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_level_up(uint32_t level, con
     if (threadIdx.x == 0) atomicOr(&serial[c], 1u);
     return;
   }
-  const uint32_t m = prune(merged, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, scan,
-                           scratch + fe.scratch + (uint64_t)k * (2 * fe.limit + 2));
+  const uint32_t m = prune(merged, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, scan);
   if (threadIdx.x == 0) node_count[fe.node_base + here + k] = m;
 }
 
@@ -762,7 +670,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
         n = combine(cur, n, tree + fe.tree + (uint64_t)node * limit, node_count[fe.node_base + node], oth, scr, scan);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      n = prune(cur, n, fe.final_cap, oth, scan, scr);
+      n = prune(cur, n, fe.final_cap, oth, scan);
       SkEntry* t = cur; cur = oth; oth = t;
     }
   } else if (batches) {
@@ -785,7 +693,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
         __syncthreads();
         if (n <= limit) break;
         ++level;
-        n = prune(cur, n, limit, oth, scan, scr);
+        n = prune(cur, n, limit, oth, scan);
         SkEntry* t = cur; cur = oth; oth = t;
       }
       for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lvl[(uint64_t)level * limit + i] = cur[i];
@@ -800,11 +708,11 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
         n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      n = prune(cur, n, fe.final_cap, oth, scan, scr);
+      n = prune(cur, n, fe.final_cap, oth, scan);
       SkEntry* t = cur; cur = oth; oth = t;
     }
   }
-  n = prune(cur, n, fe.budget, oth, scan, scr);
+  n = prune(cur, n, fe.budget, oth, scan);
   { SkEntry* t = cur; cur = oth; oth = t; }
   // Cuts (kernels/quantile.metal.h:354-400).
   const uint32_t f = f0 + c;
