@@ -158,9 +158,11 @@ def fit_child(args):
                       "bin_matrix_ms": one_time.get("bin_matrix", 0.0) * 1e3}))
 
 
-def run_child(fits, warmup, pred_out):
+def run_child(fits, warmup, pred_out, extra_params=()):
     cmd = [sys.executable, str(Path(__file__).resolve()), "--child", "--fits", str(fits), "--warmup", str(warmup),
            "--pred-out", str(pred_out)]
+    for item in extra_params:
+        cmd += ["--param", item]
     out = subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=900)
     return json.loads(out.stdout.strip().splitlines()[-1])
 
@@ -208,7 +210,7 @@ def main():
     tmp = Path(tempfile.mkdtemp(prefix="bench_"))
     children, cpu, cpu_margin = [], None, None
     for i, n in enumerate(shares):
-        children.append(run_child(n, args.warmup, tmp / f"pred{i}.npy"))
+        children.append(run_child(n, args.warmup, tmp / f"pred{i}.npy", args.param))
         print(f"bench: process {i + 1}: fits {[round(t, 2) for t in children[-1]['fit_ms']]} ms", file=sys.stderr,
               flush=True)
         if i == 0 and not args.no_cpu:

@@ -121,6 +121,14 @@ typedef struct {
    * get their leaf added to the margin by a walk of the finished tree.
    * mgb_grow_tree only (0 for the CSR driver). */
   uint32_t compact_sampled;
+  /* 1: the row partition is stable -- inside each child the rows keep their
+   * order in the parent's row list (kernels/boost.metal:1550-1614) -- at the
+   * cost of one more launch per level (a counting pass that keeps each row
+   * tile's directions and left count; the scatter takes every tile's
+   * positions from the counts of its node's tiles).  0: tiles claim
+   * their ranges with atomics, so the order inside a child follows arrival.
+   * Histograms are exact integer sums, so the trees are identical either way. */
+  uint32_t stable_partition;
 } MgbTreeShape;
 
 /* ---- data: quantile cuts and bin matrix ------------------------------- */
@@ -260,6 +268,12 @@ int mgb_predict_csr(const uint64_t* indptr, const uint32_t* indices, const float
  * subtraction), from the last mgb_grow_tree on this workspace; synchronises. */
 int mgb_tree_level_stats(const MgbTreeShape* shape, const void* workspace, uint64_t* rows_built,
                          uint32_t* nodes_built, uint32_t levels);
+/* Copies to host memory the row list (shape->rows words) that level `depth`
+ * of the last mgb_grow_tree on this workspace read: each node's rows form one
+ * segment of it.  Valid for the last two levels of a tree (the list of level
+ * d is overwritten by the partition of level d + 1); synchronises.  A
+ * diagnostic for the partition's row order, no counterpart in the reference. */
+int mgb_tree_row_list(const MgbTreeShape* shape, const void* workspace, uint32_t depth, uint32_t* rows);
 
 /* ---- kernel-level entry points used by parity tests and the profiler --- */
 /* Histogram of rows [0, count) of row list `rows` (NULL = identity) into

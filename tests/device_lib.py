@@ -21,7 +21,7 @@ class MgbTreeShape(ctypes.Structure):
                 ("max_depth", ctypes.c_uint32), ("rows_per_tile", ctypes.c_uint32),
                 ("features_per_group", ctypes.c_uint32), ("unit_hessian", ctypes.c_uint32), ("dense", ctypes.c_uint32),
                 ("column_levels", ctypes.c_uint32), ("sparse", ctypes.c_uint32), ("root_rows_per_tile", ctypes.c_uint32),
-                ("compact_sampled", ctypes.c_uint32)]
+                ("compact_sampled", ctypes.c_uint32), ("stable_partition", ctypes.c_uint32)]
 
 
 _lib = None

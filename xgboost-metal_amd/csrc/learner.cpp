@@ -706,6 +706,15 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
   // A subsample's dropped rows (zero gradients) leave the row list before the
   // root; a walk of the finished tree adds their leaves to the margin.
   shape.compact_sampled = sampled && integer("hip_compact_sampled", 1) != 0 ? 1 : 0;
+  // 1: children keep their parent's row order (one counting pass more per
+  // level); 0: tiles claim their ranges by atomics in arrival order.  The
+  // trees are the same either way.  Default: stable from 2^19 rows.  Measured
+  // per round: 10M x 128 partition 1.65 ms stable against 2.11 ms by claims
+  // (the claims serialize on a large node's two cursors), 1M x 2000 CSR
+  // 0.36 against 0.45 ms; 262,144 x 64 0.113 against 0.094 ms (the extra
+  // launch per level costs more than the few claims there).
+  const int64_t stable = integer("hip_stable_partition", -1);
+  shape.stable_partition = (stable < 0 ? data.rows >= (1u << 19) : stable != 0) ? 1 : 0;
   {
     // Root tiles: the root streams every row in order, so a workgroup can take
     // a long tile (its batches software-pipelined) at no cost in locality.

@@ -3,7 +3,10 @@
 //   -> LDS-private integer histograms (row tiles x feature groups)
 //   -> fused sibling subtraction + wave64 prefix-scan split evaluation
 //   -> select/apply (argmax over features, node records, child ids)
-//   -> stable ballot+prefix row partition with the margin update fused in.
+//   -> ballot+prefix row partition with the margin update fused in: stable
+//      (a counting pass first, then each child keeps its parent's row order)
+//      or, with one launch fewer, tiles claiming their ranges by atomics (the
+//      order inside a child follows arrival; the trees are the same).
 // All control lives on the device: kernels read work counts written by the
 // previous kernel, so the host enqueues a whole tree without a wait
 // (the reference's GPU-driven tree, src/tree.cpp:455-1029, uses indirect
@@ -30,6 +33,7 @@ namespace {
 
 constexpr uint32_t kPartTile = 1024;      // rows per partition task
 constexpr uint32_t kPartThreads = 256;    // partition (and select bookkeeping) workgroup
+constexpr uint32_t kPartMasks = kPartTile / 64;  // wave64 ballot masks per partition tile
 constexpr uint32_t kSelectThreads = 256;
 constexpr uint32_t kHistThreads = 1024;
 constexpr int kHistUnroll = 4;          // rows in flight per thread
@@ -119,6 +123,10 @@ struct Tree {
   int64_t* partials;          // per (task, feature group): G x (max_bin+1) (g, h) partial histograms
   PartTask* part_tasks;       // two banks of max_part_tasks, by level parity
   uint32_t* cursors;          // per split node: next left position, end of the free right range
+  // Stable partition only (NULL otherwise): per partition task, the ballot
+  // masks of its left rows and its left count.
+  uint64_t* part_masks;
+  uint32_t* part_left;
   // Inputs.
   const void* bins;
   const void* columns;        // column-major codes for the partition (NULL: read bins)
@@ -149,6 +157,7 @@ struct Tree {
   uint32_t select_plans;                     // unit Hessians, dense: the select bookkeeping plans the next level
   uint32_t sparse;                           // CSR: missing slots from node totals, no partials
   uint32_t compact;                          // the root's rows are the kept rows of a subsample
+  uint32_t stable;                           // stable partition (k_part_count before k_apply)
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
@@ -1710,8 +1719,9 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
 }
 
 // ---------------------------------------------------------------------------
-// Row partition (kernels/boost.metal:1316-1614): stable ballot + prefix
-// scatter.  value < threshold <=> bin <= last_left_bin; missing follows
+// Row partition (kernels/boost.metal:1316-1614): ballot + prefix scatter,
+// stable within a tile of kPartTile rows; tiles of one node claim their
+// ranges in arrival order.  value < threshold <=> bin <= last_left_bin; missing follows
 // default_left.  Rows of nodes that stop here get their leaf added to the
 // training margin (prediction cache, kernels/boost.metal:1738-1763).
 // ---------------------------------------------------------------------------
@@ -1811,6 +1821,53 @@ __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
   return op;
 }
 
+// Stable partition, first pass: every tile of a splitting node keeps its
+// rows' directions (one wave64 ballot mask per (chunk, wave), in row-list
+// order) and its left count.  k_apply then takes a tile's positions from the
+// counts of its node's tiles -- left rows from begin + (left rows of earlier
+// tiles), right rows from begin + L + (right rows of earlier tiles) -- so
+// each child keeps the parent's row order (kernels/boost.metal:1550-1614).
+// No workgroup waits for or signals another: the counts cross to k_apply
+// at the kernel boundary.
+template <typename BinT, bool IDENTITY>
+__global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t depth) {
+  constexpr uint32_t kWaves = kPartThreads / kWave;
+  __shared__ uint32_t wave_left[kPartMasks];
+  const LevelState* st = t.state;
+  const uint32_t ntasks = st->n_part[depth & 1];
+  const PartTask* tasks = part_bank(t, depth);
+  const uint32_t* rows = t.rows[depth & 1];
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
+  uint32_t op_slot = 0xffffffffu;
+  NodeOp op;
+  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x) {
+    const PartTask task = tasks[w];
+    uint32_t row[kPartPer];
+    bool active[kPartPer];
+    load_tile_rows<IDENTITY>(rows, task, row, active);
+    if (task.slot != op_slot) {  // uniform: every thread read the same task
+      op = node_op(t, depth, task.slot);
+      op_slot = task.slot;
+    }
+    if (op.op != kOpSplit) continue;  // leaves and the last level move no rows
+#pragma unroll
+    for (int k = 0; k < kPartPer; ++k) {
+      const uint64_t m = __ballot(active[k] && goes_left<BinT>(t, op, row[k]));
+      if (lane == 0) {
+        t.part_masks[(uint64_t)w * kPartMasks + k * kWaves + wave] = m;
+        wave_left[k * kWaves + wave] = (uint32_t)__popcll(m);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t left = 0;
+      for (uint32_t q = 0; q < kPartMasks; ++q) left += wave_left[q];
+      t.part_left[w] = left;
+    }
+    __syncthreads();  // wave_left is reused by the next task
+  }
+}
+
 // Select and partition of one level in one launch.  The last workgroup does
 // the level's bookkeeping (select_level: tree records, the next frontier, and
 // with unit Hessians the next level's plan); every other workgroup takes
@@ -1821,9 +1878,10 @@ __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
 // two cursors and writing ranks (chunk, wave, lane) into them.  The order of
 // rows inside a child depends on which tile claims first; nothing downstream
 // depends on it (histograms are exact integer sums and the margin update is
-// per row).  Rows of nodes that stop here get their leaf added to the
-// training margin.
-template <typename BinT, bool IDENTITY>
+// per row).  STABLE: the tile's directions and positions come from
+// k_part_count instead, and each child keeps the parent's row order.  Rows of
+// nodes that stop here get their leaf added to the training margin.
+template <typename BinT, bool IDENTITY, bool STABLE>
 __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) {
   extern __shared__ __align__(16) uint8_t apply_stage[];  // dense-root staging (depth 0 only)
   if (blockIdx.x == gridDim.x - 1) {
@@ -1832,10 +1890,12 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   }
   constexpr uint32_t kWaves = kPartThreads / kWave;
   __shared__ uint32_t wave_left[kPartPer][kWaves], wave_active[kPartPer][kWaves];
+  __shared__ uint32_t wave_before[kWaves], wave_all[kWaves];  // STABLE: the node's tile counts
   __shared__ uint32_t base_left, base_right;
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part[depth & 1];
   const PartTask* tasks = part_bank(t, depth);
+  const Frontier* frontier = t.frontier[depth & 1];
   uint32_t* cursors = cursor_bank(t, depth);
   const uint32_t* rows = t.rows[depth & 1];
   uint32_t* out = t.rows[(depth + 1) & 1];
@@ -1862,13 +1922,39 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
       continue;
     }
     bool flag[kPartPer];
+    if (STABLE && op.op == kOpSplit) {
+      const uint64_t* masks = t.part_masks + (uint64_t)w * kPartMasks + wave;
 #pragma unroll
-    for (int k = 0; k < kPartPer; ++k) flag[k] = active[k] && goes_left<BinT>(t, op, row[k]);
+      for (int k = 0; k < kPartPer; ++k) flag[k] = (masks[k * kWaves] >> lane) & 1u;
+    } else {
+#pragma unroll
+      for (int k = 0; k < kPartPer; ++k) flag[k] = active[k] && goes_left<BinT>(t, op, row[k]);
+    }
     if (op.op == kOpFinal) {
 #pragma unroll
       for (int k = 0; k < kPartPer; ++k)
         if (active[k]) t.margin[row[k]] = t.margin[row[k]] + (flag[k] ? op.left_leaf : op.right_leaf);
       continue;
+    }
+    uint32_t node_begin = 0, tile = 0;
+    if (STABLE) {
+      // Left rows of the node's tiles before this one, and of all of them (L).
+      node_begin = frontier[task.slot].begin;
+      const uint32_t ntiles = div_up(frontier[task.slot].count, kPartTile);
+      tile = (task.begin - node_begin) / kPartTile;
+      const uint32_t* left = t.part_left + (w - tile);
+      uint32_t before = 0, all = 0;
+      for (uint32_t i = threadIdx.x; i < ntiles; i += kPartThreads) {
+        const uint32_t c = left[i];
+        all += c;
+        if (i < tile) before += c;
+      }
+#pragma unroll
+      for (int d = kWave / 2; d > 0; d >>= 1) {
+        before += __shfl_xor(before, d, kWave);
+        all += __shfl_xor(all, d, kWave);
+      }
+      if (lane == 0) { wave_before[wave] = before; wave_all[wave] = all; }
     }
     uint32_t lrank[kPartPer], arank[kPartPer];
 #pragma unroll
@@ -1884,11 +1970,21 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-      uint32_t tl = 0, ta = 0;
-      for (int k = 0; k < kPartPer; ++k)
-        for (uint32_t q = 0; q < kWaves; ++q) { tl += wave_left[k][q]; ta += wave_active[k][q]; }
-      base_left = atomicAdd(&cursors[2 * task.slot], tl);
-      base_right = atomicSub(&cursors[2 * task.slot + 1], ta - tl) - (ta - tl);
+      if (STABLE) {
+        // The node's earlier tiles hold task.begin - node_begin rows, `before`
+        // of them left; right rows start after all L left rows.
+        uint32_t before = 0, all = 0;
+        for (uint32_t q = 0; q < kWaves; ++q) { before += wave_before[q]; all += wave_all[q]; }
+        base_left = node_begin + before;
+        base_right = node_begin + all + (task.begin - node_begin - before);
+        if (tile == 0) cursors[2 * task.slot] = node_begin + all;  // the final left cursor, for k_plan
+      } else {
+        uint32_t tl = 0, ta = 0;
+        for (int k = 0; k < kPartPer; ++k)
+          for (uint32_t q = 0; q < kWaves; ++q) { tl += wave_left[k][q]; ta += wave_active[k][q]; }
+        base_left = atomicAdd(&cursors[2 * task.slot], tl);
+        base_right = atomicSub(&cursors[2 * task.slot + 1], ta - tl) - (ta - tl);
+      }
     }
     __syncthreads();
     uint32_t done_left = 0, done_active = 0;  // rows of earlier chunks
@@ -1961,7 +2057,8 @@ __global__ __launch_bounds__(kCompactThreads) void k_walk_dropped(Tree t) {
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, split_bins, partials, total;
+  size_t state, rows, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, split_bins, partials;
+  size_t part_masks, part_left, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -1994,6 +2091,12 @@ Layout layout(const MgbTreeShape& s) {
     L.partials = off;
     if (!s.sparse)
       off = align_up(off + (size_t)L.max_hist_tasks * groups * s.features_per_group * (s.max_bin + 1) * 16);
+  }
+  if (s.stable_partition) {
+    L.part_masks = off; off = align_up(off + (size_t)L.max_part_tasks * kPartMasks * sizeof(uint64_t));
+    L.part_left = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
+  } else {
+    L.part_masks = L.part_left = 0;
   }
   L.total = off;
   return L;
@@ -2078,7 +2181,14 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
 template <typename BinT>
 int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
   const uint32_t lds = depth == 0 && t.dense ? (uint32_t)root_stage_bytes(t.bins1) : 0u;
-  auto fn = depth == 0 && !t.compact ? k_apply<BinT, true> : k_apply<BinT, false>;
+  const bool identity = depth == 0 && !t.compact;
+  if (t.stable) {
+    launch(MGB_PROF_PARTITION, identity ? k_part_count<BinT, true> : k_part_count<BinT, false>, dim3(grid),
+           dim3(kPartThreads), 0, t, depth);
+    MGB_LAUNCH_CHECK("k_part_count");
+  }
+  auto fn = identity ? (t.stable ? k_apply<BinT, true, true> : k_apply<BinT, true, false>)
+                     : (t.stable ? k_apply<BinT, false, true> : k_apply<BinT, false, false>);
   if (lds && hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
     set_error("hipFuncSetAttribute(select LDS) failed");
     return -1;
@@ -2148,6 +2258,11 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.column_levels = s->column_levels;
   t.sparse = s->sparse;
   t.compact = s->compact_sampled && !s->sparse ? 1u : 0u;
+  t.stable = s->stable_partition ? 1u : 0u;
+  if (t.stable) {
+    t.part_masks = reinterpret_cast<uint64_t*>(ws + L.part_masks);
+    t.part_left = reinterpret_cast<uint32_t*>(ws + L.part_left);
+  }
   t.hist_entry = L.hist_entry;
   return t;
 }
@@ -2423,6 +2538,16 @@ int mgb_tree_level_stats(const MgbTreeShape* shape, const void* workspace, uint6
     if (rows_built) rows_built[d] = valid ? st.rows_built[d] : 0;
     if (nodes_built) nodes_built[d] = valid ? st.nodes_built[d] : 0;
   }
+  return 0;
+}
+
+int mgb_tree_row_list(const MgbTreeShape* shape, const void* workspace, uint32_t depth, uint32_t* rows) {
+  if (!shape || !workspace || !rows) { set_error("mgb_tree_row_list: null argument"); return -1; }
+  Layout L = layout(*shape);
+  const uint8_t* list = reinterpret_cast<const uint8_t*>(workspace) + L.rows +
+                        (size_t)(depth & 1) * shape->rows * sizeof(uint32_t);
+  MGB_CHECK(hipMemcpyAsync(rows, list, (size_t)shape->rows * sizeof(uint32_t), hipMemcpyDeviceToHost, stream()));
+  MGB_CHECK(hipStreamSynchronize(stream()));
   return 0;
 }
 
