@@ -114,6 +114,11 @@ struct PartTask { uint32_t slot, begin, end, padding; };
 struct Tree {
   LevelState* state;
   uint32_t* rows[2];
+  // Gradient pairs in row-list order: gh[d & 1][i] = grad[rows[d & 1][i]]
+  // for the levels whose histograms gather rows (the partition moves each
+  // row's pair with its id), so the histogram reads them in order instead of
+  // one gathered line per row and feature group.
+  float2* gh[2];
   int64_t* hist[2];
   Frontier* frontier[2];
   SplitRec* recs;             // per (frontier slot, feature): the feature's best candidate
@@ -370,8 +375,12 @@ __global__ __launch_bounds__(kCompactThreads) void k_compact_rows(Tree t) {
       // present, the range being consecutive rows); kept among them:
       // done_kept + wk + rank.
       const uint32_t kept_before = done_kept + wk + rank;
-      if ((m >> lane) & 1u) t.rows[0][base_kept + kept_before] = first + i;
-      else t.rows[0][t.rows_n - 1 - (base_dropped + (i - kept_before))] = first + i;
+      if ((m >> lane) & 1u) {
+        t.rows[0][base_kept + kept_before] = first + i;
+        t.gh[0][base_kept + kept_before] = t.grad[first + i];
+      } else {
+        t.rows[0][t.rows_n - 1 - (base_dropped + (i - kept_before))] = first + i;
+      }
     }
     done_kept += ck;
   }
@@ -480,6 +489,13 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
       st->nodes_built[depth] = pairs;
     }
   }
+}
+
+// Single-histogram entry point (mgb_histogram) on a caller's row list: the
+// gradient pairs of list 0 in list order (the histogram reads them so).
+__global__ void k_gather_pairs(Tree t, uint32_t count) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
+    t.gh[0][i] = t.grad[t.rows[0][i]];
 }
 
 // Single-histogram entry point (mgb_histogram): sum the row-tile partials of
@@ -657,11 +673,14 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
         row[u] = IDENTITY ? at : rows[at];
       }
     };
-    auto fetch_data = [&](const uint32_t (&row)[kU], const bool (&valid)[kU],
+    // Gradient pairs: in row order at an identity root, else from the
+    // level's list at the same positions as the row ids (no gather).
+    const float2* ghl = IDENTITY ? t.grad : t.gh[depth & 1];
+    auto fetch_data = [&](uint32_t base, const uint32_t (&row)[kU], const bool (&valid)[kU],
                           float2 (&gh)[kU], Codes<BinT, G> (&c)[kU]) {
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        gh[u] = t.grad[row[u]];
+        gh[u] = ghl[valid[u] ? base + u * kHistThreads + threadIdx.x : task.begin];
         if constexpr (COLS) c[u].load_cols(gcols, t.rows_n, row[u], fcount);
         else c[u].load(gbins + (uint64_t)row[u] * t.row_stride);
       }
@@ -671,12 +690,12 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     float2 gh_a[kU];
     Codes<BinT, G> c_a[kU];
     fetch_rows(task.begin, row_a, valid_a);
-    fetch_data(row_a, valid_a, gh_a, c_a);
+    fetch_data(task.begin, row_a, valid_a, gh_a, c_a);
     fetch_rows(task.begin + kStep, row_b, valid_b);
     for (uint32_t base = task.begin; base < task.end; base += kStep) {
       float2 gh_b[kU];
       Codes<BinT, G> c_b[kU];
-      fetch_data(row_b, valid_b, gh_b, c_b);
+      fetch_data(base + kStep, row_b, valid_b, gh_b, c_b);
       uint32_t row_c[kU];
       bool valid_c[kU];
       fetch_rows(base + 2 * kStep, row_c, valid_c);
@@ -685,6 +704,9 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
         if (!valid_a[u]) continue;
         const unsigned long long qg = (unsigned long long)(long long)rintf(gh_a[u].x * sg);
         const unsigned long long qh = UNIT ? 0ull : (unsigned long long)(long long)rintf(gh_a[u].y * sh);
+        // A (0, 0) pair adds nothing: the rows a subsample drops, which the
+        // root streams with the kept ones, cost no LDS atomics.
+        if (!UNIT && (qg | qh) == 0) continue;
         if (fcount == (uint32_t)G) {  // full group (uniform): no per-feature test
 #pragma unroll
           for (int k = 0; k < G; ++k) {
@@ -1899,6 +1921,8 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   uint32_t* cursors = cursor_bank(t, depth);
   const uint32_t* rows = t.rows[depth & 1];
   uint32_t* out = t.rows[(depth + 1) & 1];
+  const float2* gh_in = IDENTITY ? t.grad : t.gh[depth & 1];
+  float2* gh_out = t.gh[(depth + 1) & 1];
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   uint32_t op_slot = 0xffffffffu;
@@ -1936,6 +1960,12 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
         if (active[k]) t.margin[row[k]] = t.margin[row[k]] + (flag[k] ? op.left_leaf : op.right_leaf);
       continue;
     }
+    // Each moved row takes its gradient pair along (same positions as its id).
+    float2 gh[kPartPer];
+#pragma unroll
+    for (int k = 0; k < kPartPer; ++k)
+      gh[k] = gh_in[task.begin + k * kPartThreads + threadIdx.x < task.end ? task.begin + k * kPartThreads + threadIdx.x
+                                                                           : task.begin];
     uint32_t node_begin = 0, tile = 0;
     if (STABLE) {
       // Left rows of the node's tiles before this one, and of all of them (L).
@@ -1997,8 +2027,10 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
         cl += l; ca += a;
       }
       if (active[k]) {
-        if (flag[k]) out[base_left + done_left + wl + lrank[k]] = row[k];
-        else out[base_right + (done_active - done_left) + (wa - wl) + (arank[k] - lrank[k])] = row[k];
+        const uint32_t at = flag[k] ? base_left + done_left + wl + lrank[k]
+                                    : base_right + (done_active - done_left) + (wa - wl) + (arank[k] - lrank[k]);
+        out[at] = row[k];
+        gh_out[at] = gh[k];
       }
       done_left += cl;
       done_active += ca;
@@ -2057,7 +2089,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_walk_dropped(Tree t) {
 // Host side: workspace layout and the per-level launch sequence.
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t state, rows, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, split_bins, partials;
+  size_t state, rows, gh, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, split_bins, partials;
   size_t part_masks, part_left, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
@@ -2075,6 +2107,7 @@ Layout layout(const MgbTreeShape& s) {
   size_t off = 0;
   L.state = off; off = align_up(off + sizeof(LevelState));
   L.rows = off; off = align_up(off + 2 * (size_t)s.rows * sizeof(uint32_t));
+  L.gh = off; off = align_up(off + 2 * (size_t)s.rows * sizeof(float2));
   L.hist = off; off = align_up(off + 2 * (size_t)L.slots * L.hist_entry * sizeof(int64_t));
   L.frontier = off; off = align_up(off + 2 * (size_t)(2 * L.slots) * sizeof(Frontier));
   L.recs = off; off = align_up(off + (size_t)(2 * L.slots) * s.cols * sizeof(SplitRec));
@@ -2231,6 +2264,9 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   uint32_t* rows = reinterpret_cast<uint32_t*>(ws + L.rows);
   t.rows[0] = rows;
   t.rows[1] = rows + s->rows;
+  float2* gh = reinterpret_cast<float2*>(ws + L.gh);
+  t.gh[0] = gh;
+  t.gh[1] = gh + s->rows;
   int64_t* hist = reinterpret_cast<int64_t*>(ws + L.hist);
   t.hist[0] = hist;
   t.hist[1] = hist + (size_t)L.slots * L.hist_entry;
@@ -2570,6 +2606,10 @@ int mgb_histogram(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   if (rows) {
     MGB_CHECK(hipMemcpyAsync(t.rows[0], rows, (size_t)count * sizeof(uint32_t), hipMemcpyDeviceToDevice, s));
     depth = 2;  // even depth selects bank 0 and row buffer 0 without the identity shortcut
+    if (count) {
+      hipLaunchKernelGGL(k_gather_pairs, dim3(std::min<uint32_t>(div_up(count, 256), 4096)), dim3(256), 0, s, t, count);
+      MGB_LAUNCH_CHECK("k_gather_pairs");
+    }
   }
   const uint32_t grid = hist_grid(t);
   if ((m->bin_bytes == 1 ? dispatch_hist<uint8_t>(t, depth, grid) : dispatch_hist<uint16_t>(t, depth, grid))) return -1;
