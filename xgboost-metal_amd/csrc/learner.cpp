@@ -813,6 +813,8 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
     // pair reads the parent's and the built child's histograms and writes the
     // sibling's (16 bytes per feature and bin each).
     const uint64_t node_hist = (uint64_t)data.cols * (data.hist_bins + 1) * 16;
+    level_rows_.assign(rows, rows + std::min<uint32_t>(depth, 32));
+    level_nodes_.assign(built, built + std::min<uint32_t>(depth, 32));
     for (uint32_t d = 0; d < depth && d < 32; ++d) {
       hist_bytes_ += (uint64_t)(rows[d] * row_bytes) + (uint64_t)built[d] * node_hist;
       hist_rows_ += rows[d];
@@ -1266,6 +1268,12 @@ Json Learner::profile() const {
   out["histogram_bytes"] = Json(hist_bytes_);
   out["histogram_rows"] = Json(hist_rows_);
   out["split_bytes"] = Json(split_bytes_);
+  // The last profiled tree, per level: rows and nodes whose histograms were built.
+  Json lr = Json::array(), ln = Json::array();
+  for (uint64_t v : level_rows_) lr.push_back(Json(v));
+  for (uint32_t v : level_nodes_) ln.push_back(Json((uint64_t)v));
+  out["level_rows_built"] = lr;
+  out["level_nodes_built"] = ln;
   return out;
 }
 

@@ -875,7 +875,7 @@ __global__ __launch_bounds__(kCsrThreads) void k_histogram_csr(Tree t, uint32_t 
         const uint64_t b = t.csr_indptr[r];
         cnt = (uint32_t)(t.csr_indptr[r + 1] - b);
         s_begin[threadIdx.x] = b;
-        const float2 v = t.grad[r];
+        const float2 v = IDENTITY ? t.grad[i] : t.gh[depth & 1][i];  // the pair at list position i
         s_qg[threadIdx.x] = (unsigned long long)(long long)rintf(v.x * sg);
         s_qh[threadIdx.x] = (unsigned long long)(long long)rintf(v.y * sh);
       }
