@@ -30,7 +30,9 @@ struct Profile {
   hipEvent_t take() {
     hipEvent_t e = nullptr;
     if (!free_events.empty()) { e = free_events.back(); free_events.pop_back(); }
-    else if (hipEventCreate(&e) != hipSuccess) e = nullptr;
+    // No system-scope fence when the event completes: the timestamps bracket
+    // the kernel alone, as the profiler's dispatch records do.
+    else if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) e = nullptr;
     return e;
   }
 };
