@@ -12,7 +12,11 @@ rounds are drained (trees copied back) before the clock stops.  Fits run in
 three fresh child processes (subprocess, never exec), each warmed up first with
 3 rounds on a 16,384-row slice (the reference's GPU protocol); value = median
 fit time.  The steady-state round time on an already quantized matrix is
-reported beside it.
+reported beside it.  One more process times the reference's own 262,144 x 64
+workload (the data its published 222.8 ms is quoted on) and checks that its
+predictions are stock XGBoost's published SHA-256; --config c0 / c1 run the
+same protocol on the reference's 100,000 x 32 d6 workloads (published 107.4 /
+111.2 ms), also against their published SHA-256s.
 
 The roofline object covers the histogram kernel: algorithmic bytes per launch
 (rows built x (F code bytes + 4-byte row id + 8-byte gradient pair) + nodes
@@ -57,6 +61,44 @@ PARAMS = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 8
 
 C4_PARAMS = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
              "subsample": 0.8, "colsample_bytree": 0.8}
+
+
+def _known(case):
+    import workloads as W
+    return W.known_answer_data(case)
+
+
+# Workloads timed on the fit protocol.  c2 is the headline (BASELINE config 2's
+# generator); ref262, c0 and c1 are the reference's own published workloads
+# (benchmarks/controlled_comparison.py:68-72: seed 1337, y = 2 x0 + x1^2 +
+# 0.1 N), whose stock-XGBoost prediction SHA-256s the fits must reproduce, with
+# the reference's published times beside them (README.md:98-104).
+PROTOCOL = {
+    "c2": dict(data=lambda: config2(), depth=8, ref_ms=REFERENCE_MS_100, sha256=None,
+               name="BASELINE config 2: X 262144x64 N(0,1), y = X.w + 0.5 sin(x0 x1) + 0.1 N (seed 1337); "
+                    "reg:squarederror, depth 8, max_bin 256, eta 0.3, lambda 1"),
+    "ref262": dict(data=lambda: _known("dense262"), depth=8, ref_ms=REFERENCE_MS_100, case="dense262",
+                   name="the reference's 262,144x64 d8 workload (controlled_comparison.py: y = 2 x0 + x1^2 + 0.1 N, "
+                        "seed 1337), max_bin 256, eta 0.3"),
+    "c0": dict(data=lambda: _known("dense100"), depth=6, ref_ms=107.4, case="dense100",
+               name="config 0 shape, the reference's 100,000x32 d6 workload (controlled_comparison.py: "
+                    "y = 2 x0 + x1^2 + 0.1 N, seed 1337), max_bin 256, eta 0.3"),
+    "c1": dict(data=lambda: _known("missing100"), depth=6, ref_ms=111.2, case="missing100",
+               name="config 1 shape, the reference's 100,000x32 d6 workload with 15% NaN (controlled_comparison.py), "
+                    "max_bin 256, eta 0.3"),
+}
+
+
+def protocol_params(which):
+    return dict(PARAMS, max_depth=PROTOCOL[which]["depth"])
+
+
+def published_sha256(which):
+    case = PROTOCOL[which].get("case")
+    if not case:
+        return None
+    import workloads as W
+    return W.KNOWN_ANSWERS[case]["prediction_sha256"]
 
 
 def config4(rows=10_000_000, seed=1337, chunk=1 << 20):
@@ -116,37 +158,39 @@ def cpu_threads():
     return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
 
 
-def cpu_baseline(X, y, rounds=100):
+def cpu_baseline(X, y, rounds=100, which="c2"):
     """The CPU oracle trained for the same rounds as one GPU fit (its own
     one-time sketch included); returns the baseline object and its margins."""
     import oracle_lib as O
     threads = cpu_threads()
-    p = O.make_params(max_depth=8, max_bin=256, eta=0.3, nthread=threads)
+    depth = PROTOCOL[which]["depth"]
+    p = O.make_params(max_depth=depth, max_bin=256, eta=0.3, nthread=threads)
     t0 = time.perf_counter()
     ref = O.train(X, y, p, rounds)
     seconds = time.perf_counter() - t0
     return ({"value": round(seconds * 1e3 * 100 / rounds, 1), "unit": "ms/100 rounds", "cores": threads,
              "host_cpu_count": os.cpu_count(), "kind": "port",
-             "sample": f"CPU oracle (C restatement of the reference's hist path, OpenMP over features) on config 2 "
-                       f"262144x64 d8, one fit of {rounds} rounds including its sketch, {threads} threads "
-                       f"({seconds:.1f} s)"}, ref["margin"])
+             "sample": f"CPU oracle (C restatement of the reference's hist path, OpenMP over features) on the "
+                       f"same {X.shape[0]}x{X.shape[1]} d{depth} matrix, one fit of {rounds} rounds including its "
+                       f"sketch, {threads} threads ({seconds:.1f} s)"}, ref["margin"])
 
 
 def fit_child(args):
     """One fresh process: warm-up, then args.fits timed fits; prints one JSON line."""
     import xgboost as xgb
     import device_lib as D
-    X, y = config2()
+    X, y = PROTOCOL[args.workload]["data"]()
+    params = protocol_params(args.workload)
     for _ in range(max(1, args.warmup)):
         warm = xgb.DMatrix(X[:16384], label=y[:16384])
-        xgb.train(dict(PARAMS), warm, 3).predict(warm)
+        xgb.train(dict(params), warm, 3).predict(warm)
     times, one_time = [], {}
     bst = d = None
     for _ in range(args.fits):
         d = xgb.DMatrix(X, label=y).to_device()  # outside the timer: host-to-device copy
         D.check(D.lib().mgb_synchronize())
         t0 = time.perf_counter()
-        bst = xgb.train(dict(PARAMS), d, 100)
+        bst = xgb.train(dict(params), d, 100)
         bst.num_boosted_rounds()  # waits for the queued rounds and copies the trees back
         D.check(D.lib().mgb_synchronize())
         times.append((time.perf_counter() - t0) * 1e3)
@@ -158,9 +202,9 @@ def fit_child(args):
                       "bin_matrix_ms": one_time.get("bin_matrix", 0.0) * 1e3}))
 
 
-def run_child(fits, warmup, pred_out, extra_params=()):
+def run_child(fits, warmup, pred_out, extra_params=(), workload="c2"):
     cmd = [sys.executable, str(Path(__file__).resolve()), "--child", "--fits", str(fits), "--warmup", str(warmup),
-           "--pred-out", str(pred_out)]
+           "--pred-out", str(pred_out), "--workload", workload]
     for item in extra_params:
         cmd += ["--param", item]
     out = subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=900)
@@ -174,14 +218,18 @@ def main():
                     help="timed fits (100 rounds each, quantization included), spread over 3 fresh processes")
     ap.add_argument("--warmup", type=int, default=1, help="warm-up fits (3 rounds, 16,384 rows) per process")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
-                    help="c2 (default): the headline metric; c3: 1M x 2000 CSR, 20 nonzeros a row; "
+    ap.add_argument("--config", choices=["c2", "c0", "c1", "c3", "c4"], default="c2",
+                    help="c2 (default): the headline metric; c0/c1: the fit protocol on the reference's "
+                         "100,000 x 32 d6 workloads (dense / 15%% missing); c3: 1M x 2000 CSR, 20 nonzeros a row; "
                          "c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
+    ap.add_argument("--no-ref", action="store_true",
+                    help="c2: skip the extra process timing the reference's own 262,144 x 64 workload")
     ap.add_argument("--param", action="append", default=[], metavar="KEY=VALUE",
                     help="extra booster parameter for the timed rounds (repeatable), e.g. hip_histogram_rows=2048")
     ap.add_argument("--child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--fits", type=int, default=1, help=argparse.SUPPRESS)
     ap.add_argument("--pred-out", default="", help=argparse.SUPPRESS)
+    ap.add_argument("--workload", default="c2", choices=sorted(PROTOCOL), help=argparse.SUPPRESS)
     args = ap.parse_args()
     extra = {}
     for item in args.param:
@@ -203,37 +251,54 @@ def main():
         return bench_large(xgb, args, args.config)
 
     # Protocol fits in three fresh processes, the CPU leg between the first two.
+    which = args.config
+    spec = PROTOCOL[which]
+    params = protocol_params(which)
     steps = max(1, args.steps)
     shares = [steps // 3 + (1 if i < steps % 3 else 0) for i in range(3)]
     shares = [n for n in shares if n]
-    X, y = config2()
+    X, y = spec["data"]()
     tmp = Path(tempfile.mkdtemp(prefix="bench_"))
     children, cpu, cpu_margin = [], None, None
     for i, n in enumerate(shares):
-        children.append(run_child(n, args.warmup, tmp / f"pred{i}.npy", args.param))
+        children.append(run_child(n, args.warmup, tmp / f"pred{i}.npy", args.param, which))
         print(f"bench: process {i + 1}: fits {[round(t, 2) for t in children[-1]['fit_ms']]} ms", file=sys.stderr,
               flush=True)
         if i == 0 and not args.no_cpu:
-            cpu, cpu_margin = cpu_baseline(X, y, 100)
+            cpu, cpu_margin = cpu_baseline(X, y, 100, which)
             print(f"bench: CPU oracle {cpu['value']} ms/100 rounds on {cpu['cores']} threads", file=sys.stderr,
                   flush=True)
     fits = [t for c in children for t in c["fit_ms"]]
     value = statistics.median(fits)
     gpu_pred = np.load(tmp / "pred0.npy")
     same_across = len({c["prediction_sha256"] for c in children}) == 1
+    reference_workload = None
+    if which == "c2" and not args.no_ref:
+        # The reference's own 262,144 x 64 workload, the one its 222.8 ms is
+        # quoted on, in one more fresh process: its fits and whether the
+        # predictions are stock XGBoost's published ones.
+        ref = run_child(3, args.warmup, tmp / "pred_ref.npy", args.param, "ref262")
+        print(f"bench: reference workload: fits {[round(t, 2) for t in ref['fit_ms']]} ms", file=sys.stderr,
+              flush=True)
+        reference_workload = {"workload": PROTOCOL["ref262"]["name"], "fits_ms": [round(t, 3) for t in ref["fit_ms"]],
+                              "median_ms": round(statistics.median(ref["fit_ms"]), 3),
+                              "vs_reference_222_8_ms": round(statistics.median(ref["fit_ms"]) / REFERENCE_MS_100, 4),
+                              "prediction_sha256": ref["prediction_sha256"],
+                              "equals_published_stock_xgboost_sha256":
+                                  ref["prediction_sha256"] == published_sha256("ref262")}
 
     import xgboost as xgb
     dtrain = xgb.DMatrix(X, label=y)
-    xgb.train(dict(PARAMS), dtrain, 3)  # this process: code loading, sketch and bins (untimed)
+    xgb.train(dict(params), dtrain, 3)  # this process: code loading, sketch and bins (untimed)
 
     # Steady state: rounds on the resident, quantized matrix (no profiling brackets).
-    _, elapsed = time_rounds(xgb, dtrain, 100, profile=False)
+    _, elapsed = time_rounds(xgb, dtrain, 100, profile=False, base=params)
     steady_ms = elapsed * 1e3
 
     # Same rounds with HIP-event brackets per kernel class (the roofline source).
     import device_lib as D
     D.lib().mgb_profile_reset()
-    bst_p, elapsed_p = time_rounds(xgb, dtrain, 100, profile=True)
+    bst_p, elapsed_p = time_rounds(xgb, dtrain, 100, profile=True, base=params)
     prof = bst_p.profile()
     kernels = prof["kernels"]
     hist, split = kernels["histogram"], kernels["split"]
@@ -246,14 +311,16 @@ def main():
     copy_gbps = stream_copy_gbps()
     traffic = None
     traffic_file = ROOT / "profiles" / "histogram_traffic_config2.json"
-    if traffic_file.exists():
+    if which == "c2" and traffic_file.exists():
         try:
             traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
         except ValueError:
             traffic = None
 
+    rows, cols = X.shape
+    depth = spec["depth"]
     line = {
-        "metric": "ms/100 rounds @262,144x64 d8; histogram build HBM GB/s vs peak",
+        "metric": f"ms/100 rounds @{rows:,}x{cols} d{depth}; histogram build HBM GB/s vs peak",
         "value": round(value, 3),
         "unit": "ms/100 rounds",
         "n_gpus": 1,
@@ -262,17 +329,17 @@ def main():
         "ms_per_step": round(value, 3),
         "higher_is_better": False,
         "scaling": "weak",
-        "vs_baseline": round(value / REFERENCE_MS_100, 4),
+        "vs_baseline": round(value / spec["ref_ms"], 4),
         "dtype": "int64",
         "data": "synthetic",
-        "config": {"workload": "BASELINE config 2: X 262144x64 N(0,1), y = X.w + 0.5 sin(x0 x1) + 0.1 N (seed 1337); "
-                               "reg:squarederror, depth 8, max_bin 256, eta 0.3, lambda 1; step = one fit: "
-                               "xgb.train of 100 rounds (quantile sketch, bin matrix and base score included) on a "
-                               "DMatrix already on the GPU, in a fresh process after a warm-up "
-                               "(benchmarks/controlled_comparison.py:82-92); value = median over steps",
-                   "rows": 262144, "features": 64, "max_depth": 8, "max_bin": 256,
-                   "vs_baseline_reference": "222.8 ms, reference Metal engine on M5 Ultra, same shape and "
-                                            "parameters and the same protocol, its own label generator (README.md:101)"},
+        "config": {"workload": spec["name"] + "; step = one fit: xgb.train of 100 rounds (quantile sketch, bin matrix "
+                               "and base score included) on a DMatrix already on the GPU, in a fresh process after a "
+                               "warm-up (benchmarks/controlled_comparison.py:82-92); value = median over steps",
+                   "rows": rows, "features": cols, "max_depth": depth, "max_bin": 256,
+                   "vs_baseline_reference": f"{spec['ref_ms']} ms, reference Metal engine on M5 Ultra, same shape and "
+                                            f"parameters and the same protocol"
+                                            + (", its own label generator (README.md:101)" if which == "c2" else
+                                               ", the same workload (README.md:98-104)")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": "k_histogram", "launches": launches,
@@ -294,6 +361,11 @@ def main():
         "parity": {"prediction_sha256": children[0]["prediction_sha256"],
                    "identical_across_processes": same_across},
     }
+    if published_sha256(which):
+        line["parity"]["equals_published_stock_xgboost_sha256"] = \
+            children[0]["prediction_sha256"] == published_sha256(which)
+    if reference_workload is not None:
+        line["reference_workload"] = reference_workload
     if cpu is not None:
         line["cpu_baseline"] = cpu
         line["parity"]["equal_to_cpu_oracle_bitwise"] = bool(
