@@ -101,23 +101,10 @@ def published_sha256(which):
     return W.KNOWN_ANSWERS[case]["prediction_sha256"]
 
 
-def config4(rows=10_000_000, seed=1337, chunk=1 << 20):
-    """columns 0-63 N(0,1), 64-95 U(0,1), 96-127 integers in
-    [0, 999] as float32; y ~ Bernoulli(sigmoid(X[:, :16] . w + 0.3 N)).  Drawn
-    in row chunks (float32 storage) so the float64 temporaries stay small."""
-    rng = np.random.default_rng(seed)
-    w = rng.normal(size=16)
-    X = np.empty((rows, 128), np.float32)
-    y = np.empty(rows, np.float32)
-    for a in range(0, rows, chunk):
-        b = min(rows, a + chunk)
-        n = b - a
-        X[a:b, :64] = rng.normal(size=(n, 64))
-        X[a:b, 64:96] = rng.random((n, 32))
-        X[a:b, 96:] = rng.integers(0, 1000, size=(n, 32))
-        s = X[a:b, :16].astype(np.float64) @ w + 0.3 * rng.normal(size=n)
-        y[a:b] = rng.random(n) < 1.0 / (1.0 + np.exp(-s))
-    return X, y
+def config4(rows=10_000_000, seed=1337):
+    """BASELINE config 4 (tests/workloads.py holds the generator)."""
+    import workloads as W
+    return W.config4(rows=rows, seed=seed)
 
 
 def time_rounds(xgb, dtrain, rounds, profile, base=PARAMS):

@@ -133,6 +133,25 @@ WEIGHTED_BENCHMARK_PARAMS = {"tree_method": "hist", "max_depth": 1, "max_bin": 4
 WEIGHTED_MILLION_PARAMS = {"tree_method": "hist", "max_depth": 1, "max_bin": 256, "seed": 9}
 
 
+def config4(rows=10_000_000, seed=1337, chunk=1 << 20):
+    """columns 0-63 N(0,1), 64-95 U(0,1), 96-127 integers in
+    [0, 999] as float32; y ~ Bernoulli(sigmoid(X[:, :16] . w + 0.3 N)).  Drawn
+    in row chunks (float32 storage) so the float64 temporaries stay small."""
+    rng = np.random.default_rng(seed)
+    w = rng.normal(size=16)
+    X = np.empty((rows, 128), np.float32)
+    y = np.empty(rows, np.float32)
+    for a in range(0, rows, chunk):
+        b = min(rows, a + chunk)
+        n = b - a
+        X[a:b, :64] = rng.normal(size=(n, 64))
+        X[a:b, 64:96] = rng.random((n, 32))
+        X[a:b, 96:] = rng.integers(0, 1000, size=(n, 32))
+        s = X[a:b, :16].astype(np.float64) @ w + 0.3 * rng.normal(size=n)
+        y[a:b] = rng.random(n) < 1.0 / (1.0 + np.exp(-s))
+    return X, y
+
+
 def csr_to_dense(indptr, indices, values, cols):
     """The dense matrix of a CSR matrix, NaN at the absent entries."""
     rows = len(indptr) - 1
@@ -150,4 +169,6 @@ CONFIG_PARAMS = {
     2: {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 8, "max_bin": 256, "eta": 0.3,
         "lambda": 1},
     3: {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 8, "max_bin": 256, "eta": 0.1},
+    4: {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 10, "max_bin": 1024, "eta": 0.1,
+        "subsample": 0.8, "colsample_bytree": 0.8},
 }
