@@ -87,6 +87,10 @@ __device__ __forceinline__ uint32_t order_key(float v) {
   uint32_t bits = __float_as_uint(v);
   return bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
 }
+// The value of an order key (order_key's inverse).
+__device__ __forceinline__ float key_value(uint32_t key) {
+  return __uint_as_float(key ^ ((key & 0x80000000u) ? 0x80000000u : 0xffffffffu));
+}
 __device__ __forceinline__ float min_next(const SkEntry& e) { return e.rmin + e.wmin; }
 __device__ __forceinline__ float max_prev(const SkEntry& e) { return e.rmax - e.wmin; }
 
@@ -294,16 +298,18 @@ __global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* _
   run_w[base + k] = w;
 }
 
-// Sort keys (value order) and payloads (run index) of every run.
+// Sort keys (value order) and payloads (the run's weight) of every run: the
+// stable sort hands the summaries each batch's values and weights in value
+// order, contiguous, with equal values in run order.
 __global__ void k_sort_keys(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
-                            const float* __restrict__ run_v, uint32_t* __restrict__ keys,
-                            uint32_t* __restrict__ index) {
+                            const float* __restrict__ run_v, const float* __restrict__ run_w,
+                            uint32_t* __restrict__ keys, float* __restrict__ weight) {
   const uint32_t c = blockIdx.y;
   const uint64_t base = seg[c];
   const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= stats[c].runs) return;
   keys[base + k] = order_key(run_v[base + k]);
-  index[base + k] = k;
+  weight[base + k] = run_w[base + k];
 }
 
 __device__ __forceinline__ uint32_t block_inclusive_max_u32(uint32_t v, uint32_t* shared) {
@@ -329,12 +335,54 @@ __device__ __forceinline__ uint32_t block_inclusive_max_u32(uint32_t v, uint32_t
   return before > v ? before : v;
 }
 
+// Two-level searches over a sorted summary: every s-th search key staged in
+// LDS (kSamples at most) narrows a bound to a window of fewer than s entries,
+// which a search over global memory finishes -- the same index as one binary
+// search over the whole array, with log2(s) dependent global loads instead of
+// log2(size) (a 41K-entry summary: 5 instead of 16).
+constexpr uint32_t kSamples = 2048;
+
+__device__ __forceinline__ uint32_t sample_stride(uint32_t size) {
+  uint32_t s = 16;
+  while ((uint64_t)s * kSamples < size) s <<= 1;
+  return s;
+}
+
+// smp[t] = arr[t * s].value for t < ceil(m / s).  Call with the whole
+// workgroup; the caller synchronizes before reading smp.
+__device__ __forceinline__ void sample_values(const SkEntry* arr, uint32_t m, uint32_t s, float* smp) {
+  const uint32_t samples = (m + s - 1) / s;
+  for (uint32_t t = threadIdx.x; t < samples; t += blockDim.x) smp[t] = arr[(uint64_t)t * s].value;
+}
+
+// First i in [0, m) with !(arr[i].value < x), arr sorted by value.
+__device__ __forceinline__ uint32_t lower_bound_sampled(const SkEntry* arr, uint32_t m, const float* smp, uint32_t s,
+                                                        float x) {
+  const uint32_t samples = (m + s - 1) / s;
+  uint32_t lo = 0, hi = samples;  // first sample t with !(smp[t] < x)
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    if (smp[mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  const uint32_t t = lo;
+  lo = t == 0 ? 0u : (t - 1) * s + 1;
+  hi = t < samples ? t * s : m;
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    if (arr[mid].value < x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
 // kernels/quantile.metal.h:192-214 (sketch_prune_serial), data-parallel.
 // The serial loop walks i forward while rank_k >= rmax_{i+1} + rmin_{i+1};
 // both ranks and these sums are nondecreasing, so i_k is a binary search and
 // the chosen indices c_k are nondecreasing: "append if c_k != last" keeps the
 // first k of each run of equal c_k.  in[0..size) -> out (out != in).
-__device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, SkEntry* out, uint32_t* scan) {
+__device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, SkEntry* out, uint32_t* scan,
+                          float* smp) {
   __shared__ uint32_t s_last, s_dead;
   __shared__ uint32_t s_wave_tail[kSketchThreads / kWave];
   if (size <= capacity) {
@@ -351,6 +399,13 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
   const float begin = in[0].rmax, range = in[size - 1].rmin - begin;
   const uint32_t n = capacity - 1;
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  // Sampled keys rmax_j + rmin_j at j = 2 + t * stride.
+  const uint32_t stride = sample_stride(size), samples = size > 2 ? (size - 2 + stride - 1) / stride : 0;
+  __syncthreads();  // smp may still be read by the previous search
+  for (uint32_t t = threadIdx.x; t < samples; t += blockDim.x) {
+    const SkEntry& e = in[2 + (uint64_t)t * stride];
+    smp[t] = e.rmax + e.rmin;
+  }
   if (threadIdx.x == 0) { out[0] = in[0]; s_last = 0; s_dead = 0; }
   __syncthreads();
   uint32_t carry = 0, prev_chunk = 0;
@@ -360,7 +415,17 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
     bool live = false;
     if (k < n) {
       const float rank = 2.0f * (((float)k * range) / (float)n + begin);
-      uint32_t lo = 2, hi = size;  // first j in [2, size) with rank < rmax_j + rmin_j
+      // First j in [2, size) with rank < rmax_j + rmin_j: the first sample
+      // above rank bounds it from above, the one before from below.
+      uint32_t lo = 0, hi = samples;
+      while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (rank >= smp[mid]) lo = mid + 1;
+        else hi = mid;
+      }
+      const uint32_t t = lo;
+      lo = t == 0 ? 2u : 2 + (t - 1) * stride + 1;
+      hi = t < samples ? 2 + t * stride : size;
       while (lo < hi) {
         uint32_t mid = lo + (hi - lo) / 2;
         if (rank >= in[mid].rmax + in[mid].rmin) lo = mid + 1;
@@ -403,7 +468,7 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
 // kernels/quantile.metal.h:266-311 (sketch_combine_serial), merge-path form.
 // a[0..n) and b[0..m) -> out; out must differ from both.
 __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint32_t m, SkEntry* out,
-                            uint32_t* eq_prefix, uint32_t* scan) {
+                            uint32_t* eq_prefix, uint32_t* scan, float* smp) {
   if (!m) {
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = a[i];
     __syncthreads();
@@ -414,6 +479,14 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
     __syncthreads();
     return m;
   }
+  // Sampled values of both summaries (b's in smp, a's in smp + kSamples).
+  const uint32_t sb = sample_stride(m), sa = sample_stride(n);
+  float* smp_b = smp;
+  float* smp_a = smp + kSamples;
+  __syncthreads();  // smp may still be read by the previous search
+  sample_values(b, m, sb, smp_b);
+  sample_values(a, n, sa, smp_a);
+  __syncthreads();
   // Equal-value pairs, indexed by a: eq_prefix[i] = #pairs with a-index < i.
   uint32_t carry = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
@@ -421,8 +494,7 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
     uint32_t eq = 0;
     if (i < n) {
       float x = a[i].value;
-      uint32_t lo = 0, hi = m;
-      while (lo < hi) { uint32_t mid = lo + (hi - lo) / 2; if (b[mid].value < x) lo = mid + 1; else hi = mid; }
+      const uint32_t lo = lower_bound_sampled(b, m, smp_b, sb, x);
       eq = lo < m && b[lo].value == x;
     }
     uint32_t total;
@@ -436,8 +508,7 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
   const float tail_a = a[n - 1].rmax, tail_b = b[m - 1].rmax;
   for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
     const SkEntry x = a[i];
-    uint32_t lo = 0, hi = m;
-    while (lo < hi) { uint32_t mid = lo + (hi - lo) / 2; if (b[mid].value < x.value) lo = mid + 1; else hi = mid; }
+    const uint32_t lo = lower_bound_sampled(b, m, smp_b, sb, x.value);
     SkEntry r;
     if (lo < m && b[lo].value == x.value) {
       const SkEntry y = b[lo];
@@ -451,8 +522,7 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
   }
   for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) {
     const SkEntry y = b[j];
-    uint32_t lo = 0, hi = n;
-    while (lo < hi) { uint32_t mid = lo + (hi - lo) / 2; if (a[mid].value < y.value) lo = mid + 1; else hi = mid; }
+    const uint32_t lo = lower_bound_sampled(a, n, smp_a, sa, y.value);
     if (lo < n && a[lo].value == y.value) continue;
     float prev_a = lo > 0 ? min_next(a[lo - 1]) : 0.0f;
     float add = lo < n ? max_prev(a[lo]) : tail_a;
@@ -500,10 +570,11 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
 // Summary of one sorted batch (kernels/quantile.metal.h:216-240): one entry
 // per distinct value, in value order, holding the value's weight w (the
 // binary32 sum of its runs' weights in sort order) and the running binary32
-// total before (rmin) and after (rmax) it.  index[0..size) are the batch's
-// run indices in value order; scratch needs size + 1 words.
-__device__ uint32_t summarize(const uint32_t* __restrict__ index, const float* __restrict__ run_v,
-                              const float* __restrict__ run_w, uint32_t size, bool exact, SkEntry* out,
+// total before (rmin) and after (rmax) it.  keys[0..size) and wts[0..size)
+// are the batch's runs' order keys and weights in value order; scratch needs
+// size + 1 words.
+__device__ uint32_t summarize(const uint32_t* __restrict__ keys, const float* __restrict__ wts, uint32_t size,
+                              bool exact, SkEntry* out,
                               uint32_t* scratch, uint32_t* scan) {
   // Group starts (value changes in sort order) and each group's first
   // position; with integer weights summing below 2^24 (exact) also each
@@ -515,9 +586,9 @@ __device__ uint32_t summarize(const uint32_t* __restrict__ index, const float* _
     uint32_t w = 0, start = 0;
     float v = 0.0f;
     if (i < size) {
-      v = run_v[index[i]];
-      if (exact) w = (uint32_t)run_w[index[i]];
-      start = i == 0 || run_v[index[i - 1]] != v;
+      v = key_value(keys[i]);
+      if (exact) w = (uint32_t)wts[i];
+      start = i == 0 || key_value(keys[i - 1]) != v;
     }
     uint32_t tw = 0, ts;
     const uint32_t pw = (exact ? block_exclusive_u32(w, scan, &tw) : 0u) + carry_w;
@@ -545,8 +616,8 @@ __device__ uint32_t summarize(const uint32_t* __restrict__ index, const float* _
   // Each group's weight: its runs' weights summed in sort order.
   for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
     const uint32_t s = scratch[o], e = scratch[o + 1];
-    float w = run_w[index[s]];
-    for (uint32_t i = s + 1; i < e; ++i) w = w + run_w[index[i]];
+    float w = wts[s];
+    for (uint32_t i = s + 1; i < e; ++i) w = w + wts[i];
     out[o].wmin = w;
   }
   __syncthreads();
@@ -583,21 +654,21 @@ __device__ uint32_t summarize(const uint32_t* __restrict__ index, const float* _
 __global__ __launch_bounds__(kSketchThreads) void k_level0(const uint32_t* __restrict__ table,
                                                            const SkFeature* __restrict__ features,
                                                            const SkStats* __restrict__ stats,
-                                                           const uint32_t* __restrict__ index,
-                                                           const float* __restrict__ run_v,
-                                                           const float* __restrict__ run_w, SkEntry* __restrict__ work,
+                                                           const uint32_t* __restrict__ keys,
+                                                           const float* __restrict__ wts, SkEntry* __restrict__ work,
                                                            SkEntry* __restrict__ tree, uint32_t* __restrict__ scratch,
                                                            uint32_t* __restrict__ node_count) {
   __shared__ uint32_t scan[kSketchThreads / kWave + 1];
+  __shared__ float s_smp[2 * kSamples];
   const uint32_t c = table[2 * blockIdx.x], b = table[2 * blockIdx.x + 1];
   const SkFeature fe = features[c];
   const uint64_t begin = (uint64_t)b * 2 * fe.limit;
   const uint32_t runs = stats[c].runs;
   const uint32_t size = (uint32_t)(runs - begin < 2ull * fe.limit ? runs - begin : 2ull * fe.limit);
   SkEntry* summary = work + fe.base + begin;
-  const uint32_t n = summarize(index + fe.base + begin, run_v + fe.base, run_w + fe.base, size, fe.exact != 0,
-                               summary, scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), scan);
-  const uint32_t m = prune(summary, n, fe.limit, tree + fe.tree + (uint64_t)b * fe.limit, scan);
+  const uint32_t n = summarize(keys + fe.base + begin, wts + fe.base + begin, size, fe.exact != 0, summary,
+                               scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), scan);
+  const uint32_t m = prune(summary, n, fe.limit, tree + fe.tree + (uint64_t)b * fe.limit, scan, s_smp);
   if (threadIdx.x == 0) node_count[fe.node_base + b] = m;
 }
 
@@ -613,6 +684,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_level_up(uint32_t level, con
                                                              uint32_t* __restrict__ node_count,
                                                              uint32_t* __restrict__ serial) {
   __shared__ uint32_t scan[kSketchThreads / kWave + 1];
+  __shared__ float s_smp[2 * kSamples];
   __shared__ uint32_t s_serial;
   const uint32_t c = table[2 * blockIdx.x], k = table[2 * blockIdx.x + 1];
   // Other workgroups of this level may set the flag meanwhile: one read,
@@ -626,12 +698,12 @@ __global__ __launch_bounds__(kSketchThreads) void k_level_up(uint32_t level, con
   const uint32_t na = node_count[fe.node_base + newer], nb = node_count[fe.node_base + older];
   SkEntry* merged = work + fe.base + (uint64_t)k * 2 * fe.limit;
   const uint32_t n = combine(tree + fe.tree + (uint64_t)newer * fe.limit, na, tree + fe.tree + (uint64_t)older * fe.limit,
-                             nb, merged, scratch + fe.scratch + (uint64_t)k * (2 * fe.limit + 2), scan);
+                             nb, merged, scratch + fe.scratch + (uint64_t)k * (2 * fe.limit + 2), scan, s_smp);
   if (n <= fe.limit) {
     if (threadIdx.x == 0) atomicOr(&serial[c], 1u);
     return;
   }
-  const uint32_t m = prune(merged, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, scan);
+  const uint32_t m = prune(merged, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, scan, s_smp);
   if (threadIdx.x == 0) node_count[fe.node_base + here + k] = m;
 }
 
@@ -650,6 +722,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
                                                            uint32_t lds_values, float* __restrict__ cuts,
                                                            uint32_t* __restrict__ counts) {
   __shared__ uint32_t scan[kSketchThreads / kWave + 1];
+  __shared__ float s_smp[2 * kSamples];
   __shared__ uint32_t level_count[64];
   // lds_values summary values, then max_bin candidate cuts (0 bytes when
   // lds_values is 0).
@@ -667,10 +740,11 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
     for (uint32_t level = 0; level < fe.levels && level < 32; ++level) {
       if ((batches >> level) & 1u) {
         const uint32_t node = level_first(batches, level) + (batches >> level) - 1;
-        n = combine(cur, n, tree + fe.tree + (uint64_t)node * limit, node_count[fe.node_base + node], oth, scr, scan);
+        n = combine(cur, n, tree + fe.tree + (uint64_t)node * limit, node_count[fe.node_base + node], oth, scr, scan,
+                    s_smp);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      n = prune(cur, n, fe.final_cap, oth, scan);
+      n = prune(cur, n, fe.final_cap, oth, scan, s_smp);
       SkEntry* t = cur; cur = oth; oth = t;
     }
   } else if (batches) {
@@ -685,7 +759,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
       for (;;) {
         const uint32_t m = level_count[level];
         if (m) {
-          n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan);
+          n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan, s_smp);
           SkEntry* t = cur; cur = oth; oth = t;
         }
         __syncthreads();
@@ -693,7 +767,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
         __syncthreads();
         if (n <= limit) break;
         ++level;
-        n = prune(cur, n, limit, oth, scan);
+        n = prune(cur, n, limit, oth, scan, s_smp);
         SkEntry* t = cur; cur = oth; oth = t;
       }
       for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lvl[(uint64_t)level * limit + i] = cur[i];
@@ -705,14 +779,14 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
     for (uint32_t level = 0; level < fe.levels && level < 64; ++level) {
       const uint32_t m = level_count[level];
       if (m) {
-        n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan);
+        n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan, s_smp);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      n = prune(cur, n, fe.final_cap, oth, scan);
+      n = prune(cur, n, fe.final_cap, oth, scan, s_smp);
       SkEntry* t = cur; cur = oth; oth = t;
     }
   }
-  n = prune(cur, n, fe.budget, oth, scan);
+  n = prune(cur, n, fe.budget, oth, scan, s_smp);
   { SkEntry* t = cur; cur = oth; oth = t; }
   // Cuts (kernels/quantile.metal.h:354-400).
   const uint32_t f = f0 + c;
@@ -852,7 +926,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   const uint64_t o_stats = a1.reserve(nf * sizeof(SkStats));
   const uint64_t o_run_v = a1.reserve(E * 4), o_run_w = a1.reserve(E * 4);
   const uint64_t o_region = a1.reserve(E * 16);
-  const uint64_t o_keys_out = a1.reserve(E * 4), o_index_out = a1.reserve(E * 4);
+  const uint64_t o_keys_out = a1.reserve(E * 4), o_weight_out = a1.reserve(E * 4);
   if (a1.commit()) return -1;
   const uint64_t* seg_d = a1.at<uint64_t>(o_seg);
   SkBlock* blocks = a1.at<SkBlock>(o_blocks);
@@ -860,13 +934,13 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   float* run_v = a1.at<float>(o_run_v);
   float* run_w = a1.at<float>(o_run_w);
   uint32_t* keys_out = a1.at<uint32_t>(o_keys_out);
-  uint32_t* index_out = a1.at<uint32_t>(o_index_out);
+  uint32_t* weight_out = a1.at<uint32_t>(o_weight_out);
   // One 16-byte-per-entry region: run starts, sort inputs and entry weights
   // until the sort, then the summaries' and merges' work area.
   uint32_t* run_start = a1.at<uint32_t>(o_region);
   uint32_t* keys_in = run_start + E;
-  uint32_t* index_in = keys_in + E;
-  float* elem_w = reinterpret_cast<float*>(index_in + E);
+  uint32_t* weight_in = keys_in + E;
+  float* elem_w = reinterpret_cast<float*>(weight_in + E);
   SkEntry* work = a1.at<SkEntry>(o_region);
   const dim3 grid(max_blocks, nf);
   hipLaunchKernelGGL(k_run_count, grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
@@ -882,7 +956,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
                      run_start, weights ? elem_w : nullptr, run_w);
   MGB_LAUNCH_CHECK("k_run_weights");
   hipLaunchKernelGGL(k_sort_keys, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
-                     run_v, keys_in, index_in);
+                     run_v, run_w, keys_in, reinterpret_cast<float*>(weight_in));
   MGB_LAUNCH_CHECK("k_sort_keys");
   std::vector<SkStats> stats(nf);
   MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d, nf * sizeof(SkStats), hipMemcpyDeviceToHost, s));
@@ -934,7 +1008,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   }
   size_t temp_bytes = 0;
   if (!seg_begin.empty())
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_bytes, keys_in, keys_out, index_in, index_out,
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_bytes, keys_in, keys_out, weight_in, weight_out,
                                                            (int)total, (int)seg_begin.size(), (const uint32_t*)nullptr,
                                                            (const uint32_t*)nullptr, 0, 32, s));
   Arena a2;
@@ -956,12 +1030,13 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   uint32_t* serial = a2.at<uint32_t>(o_serial);
   MGB_CHECK(hipMemsetAsync(serial, 0, nf * 4, s));
   if (!seg_begin.empty()) {
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out, index_in,
-                                                           index_out, (int)total, (int)seg_begin.size(),
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out, weight_in,
+                                                           weight_out, (int)total, (int)seg_begin.size(),
                                                            a2.at<uint32_t>(o_seg_b), a2.at<uint32_t>(o_seg_e), 0, 32,
                                                            s));
     hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kSketchThreads), 0, s,
-                       a2.at<uint32_t>(o_table0), features_d, stats_d, index_out, run_v, run_w, work, tree, scratch,
+                       a2.at<uint32_t>(o_table0), features_d, stats_d, keys_out,
+                       reinterpret_cast<const float*>(weight_out), work, tree, scratch,
                        node_count);
     MGB_LAUNCH_CHECK("k_level0");
   }
