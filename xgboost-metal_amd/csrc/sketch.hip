@@ -466,7 +466,8 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
 }
 
 // kernels/quantile.metal.h:266-311 (sketch_combine_serial), merge-path form.
-// a[0..n) and b[0..m) -> out; out must differ from both.
+// a[0..n) and b[0..m) -> out; out must differ from both.  eq_prefix needs
+// 2n + 1 words.
 __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint32_t m, SkEntry* out,
                             uint32_t* eq_prefix, uint32_t* scan, float* smp) {
   if (!m) {
@@ -487,7 +488,9 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
   sample_values(b, m, sb, smp_b);
   sample_values(a, n, sa, smp_a);
   __syncthreads();
-  // Equal-value pairs, indexed by a: eq_prefix[i] = #pairs with a-index < i.
+  // Equal-value pairs, indexed by a: eq_prefix[i] = #pairs with a-index < i;
+  // each a value's position in b kept in rank_a for the placement below.
+  uint32_t* rank_a = eq_prefix + n + 1;
   uint32_t carry = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
     uint32_t i = base + threadIdx.x;
@@ -495,6 +498,7 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
     if (i < n) {
       float x = a[i].value;
       const uint32_t lo = lower_bound_sampled(b, m, smp_b, sb, x);
+      rank_a[i] = lo;
       eq = lo < m && b[lo].value == x;
     }
     uint32_t total;
@@ -508,7 +512,7 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
   const float tail_a = a[n - 1].rmax, tail_b = b[m - 1].rmax;
   for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
     const SkEntry x = a[i];
-    const uint32_t lo = lower_bound_sampled(b, m, smp_b, sb, x.value);
+    const uint32_t lo = rank_a[i];
     SkEntry r;
     if (lo < m && b[lo].value == x.value) {
       const SkEntry y = b[lo];
