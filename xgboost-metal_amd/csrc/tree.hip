@@ -44,6 +44,9 @@ constexpr uint32_t kMaxLevels = 32;
 // Features per node from which the split kernel reads a node's best key
 // before offering its own (see score_node).
 constexpr uint32_t kContendedFeatures = 512;
+// Stable partition: levels of at most this many nodes are planned by the
+// select bookkeeping from the counting pass's left counts (no k_plan).
+constexpr uint32_t kPlanNodes = 2048;
 
 struct LevelState {
   uint32_t n_nodes;       // frontier size of the current level
@@ -1498,6 +1501,12 @@ __device__ void stage_feature(const int64_t* fh, uint32_t count, int eg, int eh,
 // chosen feature's bins as binary64 (g, h) and the chosen feature's cuts.
 size_t root_stage_bytes(uint32_t bins1) { return 4ull * bins1 * sizeof(double) + (size_t)bins1 * sizeof(float); }
 
+// Whether level `depth`'s bookkeeping plans the next level from the stable
+// partition's counts (the host skips k_plan then; same rule on both sides).
+__host__ __device__ inline bool counts_plan_level(const Tree& t, uint32_t depth) {
+  return !t.select_plans && t.stable && depth < 31 && (1u << depth) <= kPlanNodes;
+}
+
 __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   __shared__ uint32_t scan[kPartThreads / kWave + 1];
   __shared__ uint32_t s_off[kPartThreads], s_begin[kPartThreads], s_end[kPartThreads];
@@ -1511,8 +1520,10 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   // With unit Hessians every row's quantized h is unit_q, so a child's row
   // count is its Hessian sum / unit_q -- exactly the rows the partition will
   // send it -- and the next level can be planned here (k_plan's work) instead
-  // of after the partition.
-  const bool plan_next = t.select_plans && !final_level;
+  // of after the partition.  With the stable partition the counting pass has
+  // already counted every tile's left rows, whatever the Hessians.
+  const bool count_plans = counts_plan_level(t, depth);
+  const bool plan_next = (t.select_plans || count_plans) && !final_level;
   const uint64_t unit_q = plan_next ? (uint64_t)(int64_t)rintf(1.0f * t.scales[1]) : 1;
   const uint32_t node_base = st->node_count;
   const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
@@ -1528,6 +1539,17 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   double* rootfh = rootfg + t.bins1;
   float* rootcut = reinterpret_cast<float*>(rootfh + t.bins1);
   const bool dense_root = depth == 0 && t.dense && n > 0;
+  __shared__ uint32_t s_left[kPlanNodes];  // count_plans: each node's left rows
+  if (plan_next && count_plans) {
+    // Sums over every task; only split nodes' sums are read (a leaf's tasks
+    // keep older counts).
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) s_left[i] = 0;
+    __syncthreads();
+    const uint32_t ntasks = st->n_part[depth & 1];
+    const PartTask* tasks = part_bank(t, depth);
+    for (uint32_t w = threadIdx.x; w < ntasks; w += blockDim.x) atomicAdd(&s_left[tasks[w].slot], t.part_left[w]);
+    __syncthreads();
+  }
   if (dense_root) {
     const uint64_t key = best_keys[0];
     const uint32_t f = key ? ~(uint32_t)key : 0u;
@@ -1603,7 +1625,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
     // kernels/boost.metal:661-698) in row tiles, the other subtracted.
     uint32_t lcount = 0, htiles = 0, hzero = 0, hrows = 0;
     if (plan_next && valid && expand) {
-      lcount = (uint32_t)((uint64_t)best.lh / unit_q);
+      lcount = count_plans ? s_left[i] : (uint32_t)((uint64_t)best.lh / unit_q);
       const uint32_t rcount = node.count - lcount;
       hrows = lcount <= rcount ? lcount : rcount;
       htiles = div_up(hrows, t.rows_per_tile);
@@ -2396,7 +2418,7 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   // from the count histograms), so k_plan is not launched.
   t.select_plans = t.unit_hessian ? 1u : 0u;
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
-    if (depth > 0 && !t.select_plans) {
+    if (depth > 0 && !t.select_plans && !counts_plan_level(t, depth - 1)) {
       launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
@@ -2558,7 +2580,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
   const uint64_t row_int4 = (uint64_t)t.cols * t.bins1;
   const uint32_t zx = (uint32_t)(row_int4 / (256 * 8) + 1 < 64 ? row_int4 / (256 * 8) + 1 : 64);
   for (uint32_t depth = 0; depth < shape->max_depth; ++depth) {
-    if (depth > 0) {
+    if (depth > 0 && !counts_plan_level(t, depth - 1)) {
       launch(MGB_PROF_CONTROL, k_plan, dim3(1), dim3(kSelectThreads), 0, t, depth);
       MGB_LAUNCH_CHECK("k_plan");
     }
