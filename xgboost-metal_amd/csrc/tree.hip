@@ -168,6 +168,7 @@ struct Tree {
   uint32_t select_plans;                     // unit Hessians, dense: the select bookkeeping plans the next level
   uint32_t sparse;                           // CSR: missing slots from node totals, no partials
   uint32_t compact;                          // the root's rows are the kept rows of a subsample
+  uint32_t fused_level0;                     // the root histogram's workgroup 0 runs level0_setup
   uint32_t stable;                           // stable partition (k_part_count before k_apply)
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
@@ -259,7 +260,7 @@ __device__ __forceinline__ float calc_gain(double G, double H, float w, const Mg
 // ---------------------------------------------------------------------------
 // Level 0 set-up: root frontier, root histogram tasks, root tree record.
 // ---------------------------------------------------------------------------
-__global__ void k_level0(Tree t) {
+__device__ void level0_setup(const Tree& t) {
   LevelState* st = t.state;
   // The root's rows: [0, N), or the kept rows k_compact_rows listed.  The
   // root histogram streams every row in order either way: a dropped row's
@@ -305,6 +306,17 @@ __global__ void k_level0(Tree t) {
     n.threshold = 0; n.leaf = 0; n.cover = 0; n.gain = 0; n.default_left = 0; n.base_weight = 0;
     if (t.nodes) t.nodes[0] = n;  // the histogram-only entry point has no tree
   }
+}
+
+__global__ void k_level0(Tree t) { level0_setup(t); }
+
+// Row tile i of the root (the tasks level0_setup lists), for the root's
+// histogram launch, which may run level0_setup itself in one workgroup.
+__device__ __forceinline__ HistTask root_task(const Tree& t, uint32_t i) {
+  const uint32_t tiles = t.rows_n ? div_up(t.rows_n, t.root_tile) : 0;
+  const uint32_t begin = i * t.root_tile;
+  const uint32_t end = begin + t.root_tile < t.rows_n ? begin + t.root_tile : t.rows_n;
+  return HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
 }
 
 // ---------------------------------------------------------------------------
@@ -631,7 +643,10 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
   unsigned long long* lh = lg + G * B1;                        // !UNIT
   uint32_t* lc = reinterpret_cast<uint32_t*>(lg + G * B1);     // UNIT
   const LevelState* st = t.state;
-  const uint32_t ntasks = st->n_hist_tasks;
+  // The root's tasks are its row tiles, computed here (its level-0 set-up
+  // may be running in workgroup 0 of this launch).
+  const uint32_t ntasks = IDENTITY ? (t.rows_n ? div_up(t.rows_n, t.root_tile) : 0u) : st->n_hist_tasks;
+  if (IDENTITY && t.fused_level0 && blockIdx.x == 0) level0_setup(t);
   const uint32_t total = ntasks * t.groups;
   const float sg = t.scales[0], sh = t.scales[1];
   const int64_t unit_q = UNIT ? (int64_t)rintf(1.0f * sh) : 0;
@@ -648,7 +663,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
   const uint8_t* bins = reinterpret_cast<const uint8_t*>(t.bins);
   (void)total;
   for (uint32_t j = local; j < xcd_items; j += per_xcd) {
-    const HistTask task = t.hist_tasks[xcd + 8 * (j / t.groups)];
+    const HistTask task = IDENTITY ? root_task(t, xcd + 8 * (j / t.groups)) : t.hist_tasks[xcd + 8 * (j / t.groups)];
     const uint32_t group = j % t.groups;
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
       lg[i] = 0;
@@ -2412,8 +2427,9 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
       MGB_LAUNCH_CHECK("k_compact_rows");
     }
   }
-  launch(MGB_PROF_CONTROL, k_level0, dim3(1), dim3(256), 0, t);
-  MGB_LAUNCH_CHECK("k_level0");
+  // The root histogram's workgroup 0 does the level-0 set-up (one launch
+  // fewer per tree).
+  t.fused_level0 = 1;
   // Unit Hessians: the select bookkeeping plans each next level (child counts are known
   // from the count histograms), so k_plan is not launched.
   t.select_plans = t.unit_hessian ? 1u : 0u;
