@@ -86,3 +86,18 @@ def test_config3_full_size_paths_agree(xgb):
     fresh = xgb.DMatrix(csr[:200_000])
     np.testing.assert_array_equal(base.predict(d, output_margin=True)[:200_000].view(np.uint32),
                                   base.predict(fresh, output_margin=True).view(np.uint32))
+
+
+def test_config2_full_size_matches_oracle(xgb):
+    """BASELINE config 2's own generator at its full 262,144 x 64, depth 8,
+    against the CPU oracle: the margins after 10 rounds bit for bit (the
+    bench compares the full 100-round fit's predictions the same way)."""
+    import os
+
+    import oracle_lib as O
+    X, y = W.config2()
+    bst = xgb.train(dict(W.CONFIG_PARAMS[2]), xgb.DMatrix(X, label=y), 10)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    ref = O.train(X, y, O.make_params(max_depth=8, max_bin=256, eta=0.3, nthread=threads), 10)
+    got = bst.predict(xgb.DMatrix(X), output_margin=True)
+    np.testing.assert_array_equal(got.view(np.uint32), ref["margin"].view(np.uint32))
