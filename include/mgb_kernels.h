@@ -138,6 +138,13 @@ typedef struct {
  * its temporary device memory and synchronises the stream (one-time set-up). */
 int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights, uint32_t max_bin,
                     float* cuts, uint32_t* counts);
+/* Largest number of entries (present values) the sketch processes as one
+ * group of features; 0 (the default) sizes groups from the free device
+ * memory, about 64 bytes of temporaries per entry within a quarter of it.
+ * Smaller groups bound the sketch's memory at the cost of fewer features in
+ * flight per launch; the cuts are the same for any size.  No counterpart in
+ * the reference (its sketch runs on the host). */
+int mgb_sketch_group_entries(uint64_t entries);
 /* bin = min(#{cuts <= v}, count-1); NaN -> missing code
  * (kernels/boost.metal:476-499, src/data.cpp:1210-1306).  Sets *any_missing. */
 int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,

@@ -3,6 +3,7 @@
 Kernel-level checks go through the kernel C ABI (include/mgb_kernels.h);
 end-to-end checks go through the drop-in API (xgb.train -> C API).
 """
+import ctypes
 import hashlib
 
 import numpy as np
@@ -75,6 +76,25 @@ def test_sketch_cuts_weighted_match_oracle():
     np.testing.assert_array_equal(counts, ocounts)
     for f in range(X.shape[1]):
         np.testing.assert_array_equal(cuts[f, :counts[f]].view(np.uint32), ocuts[f, :counts[f]].view(np.uint32))
+
+
+@pytest.mark.parametrize("group_entries", [1, 3 * 30000, 0])
+def test_sketch_feature_groups_match_oracle(group_entries):
+    # One feature per group, groups of three (3 + 3 + 2) and the default (one
+    # group): the cuts do not depend on how the features are grouped.
+    X, _ = W.config1(rows=30000, cols=8)
+    X[:, 3] = np.round(X[:, 3] * 2)
+    w = np.random.default_rng(5).uniform(0.1, 2.0, len(X)).astype(np.float32)
+    D.check(D.lib().mgb_sketch_group_entries(ctypes.c_uint64(group_entries)))
+    try:
+        got = [D.sketch_cuts(X, 64), D.sketch_cuts(X, 64, w)]
+    finally:
+        D.check(D.lib().mgb_sketch_group_entries(ctypes.c_uint64(0)))
+    for (cuts, counts), weights in zip(got, [None, w]):
+        ocuts, ocounts, _ = O.sketch_cuts(X, 64, weights)
+        np.testing.assert_array_equal(counts, ocounts)
+        for f in range(X.shape[1]):
+            np.testing.assert_array_equal(cuts[f, :counts[f]].view(np.uint32), ocuts[f, :counts[f]].view(np.uint32))
 
 
 @pytest.mark.parametrize("bin_bytes,G,group_major", [(1, 16, False), (1, 4, False), (2, 8, False), (1, 4, True),

@@ -1,7 +1,10 @@
 // Weighted quantile sketch on the GPU: the per-feature cut points of the
 // reference's hist method (src/quantile.cpp:22-212, kernels/quantile.metal.h,
 // XGBoost's WQSummary semantics).  Features are processed in groups of at
-// most kChunkEntries entries; for each group:
+// most group_entries() entries (by default as many as a quarter of the free
+// device memory holds, so on a 288 GB device one group takes every feature of
+// a 10M x 128 matrix and each launch below has all of them in flight); for
+// each group:
 //
 //  1. (dense input) transpose the group's columns (coalesced reads per feature);
 //  2. runs of equal values in row order over each feature's non-missing,
@@ -41,7 +44,8 @@ namespace {
 
 constexpr uint32_t kSketchThreads = 1024;
 constexpr uint32_t kBlockEntries = 1024;                 // entries per workgroup in the run passes
-constexpr uint64_t kChunkEntries = uint64_t(1) << 27;    // entries per group of features
+constexpr uint64_t kGroupBytesPerEntry = 64;              // a group's temporaries per entry (typical)
+constexpr uint64_t kMaxGroupEntries = (uint64_t(1) << 31) - 1;  // 32-bit positions; the sort counts in int
 constexpr uint32_t kMaxGroupFeatures = 65535;            // features per group
 constexpr uint32_t kFinishLds = 96 * 1024;               // k_finish's staging LDS, at most
 
@@ -67,8 +71,7 @@ struct SkFeature {
   uint64_t base;        // first entry of the feature in the group's entry arrays
   uint64_t tree;        // first SkEntry of its tree nodes
   uint64_t fin;         // first SkEntry of its finishing buffers
-  uint64_t scratch;     // first word of its per-node scratch (node k of a level: + k * (2 limit + 2))
-  uint64_t fin_scratch; // first word of its finishing scratch
+  uint64_t scratch;     // first word of its batch summaries' scratch (batch b: + b * (2 limit + 2))
   uint32_t node_base;   // first slot of its node counts
   uint32_t limit, budget, batches;
   uint32_t levels;      // bit_width(batches) + 1: the serial stack's depth
@@ -312,79 +315,129 @@ __global__ void k_sort_keys(const uint64_t* __restrict__ seg, const SkStats* __r
   weight[base + k] = run_w[base + k];
 }
 
-__device__ __forceinline__ uint32_t block_inclusive_max_u32(uint32_t v, uint32_t* shared) {
+// Merges and prunes walk their inputs in tiles of a merge path (merge-path
+// partitioning, Odeh et al. / Green et al.): a tile's boundaries come from
+// one binary search each over global memory, its two input windows are
+// staged in LDS with coalesced loads, and every search inside the tile runs
+// over LDS.  Each entry is read from global memory once per pass instead of
+// once per step of a global binary search.  A workgroup of kThreads threads
+// walks tiles of 2 kThreads steps (two per thread) and searches kThreads tile
+// boundaries at a time.
+constexpr uint32_t kMergeThreads = 256;  // the merge tree's workgroups: four per CU
+constexpr uint32_t kWideLevelNodes = 512;  // merge-tree levels with fewer nodes use kSketchThreads
+
+template <uint32_t kThreads>
+struct MergeLds {
+  static constexpr uint32_t kTile = 2 * kThreads;
+  SkEntry a[kTile + 2];   // window of the first input: one entry either side
+  SkEntry b[kTile + 2];   // window of the second input
+  uint32_t flag[kTile + 1];
+  uint32_t bound[kThreads + 1];
+  uint32_t scan[2 * (kThreads / kWave + 1)];
+};
+
+// Exclusive prefix maximum of v over the workgroup's threads (0 for thread 0);
+// *all receives the maximum over every thread.
+__device__ __forceinline__ uint32_t block_exclusive_max_u32(uint32_t v, uint32_t* shared, uint32_t* all) {
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  uint32_t inc = v;
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
-    uint32_t o = __shfl_up(v, d, kWave);
-    if (lane >= (uint32_t)d) v = o > v ? o : v;
+    const uint32_t o = __shfl_up(inc, d, kWave);
+    if (lane >= (uint32_t)d) inc = o > inc ? o : inc;
   }
-  if (lane == kWave - 1) shared[wave] = v;
+  uint32_t exc = __shfl_up(inc, 1, kWave);
+  if (lane == 0) exc = 0;
+  if (lane == kWave - 1) shared[wave] = inc;
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t run = 0;
     for (uint32_t w = 0; w < waves; ++w) {
-      uint32_t t = shared[w];
+      const uint32_t t = shared[w];
       shared[w] = run;
       run = t > run ? t : run;
     }
+    shared[waves] = run;
   }
   __syncthreads();
-  uint32_t before = shared[wave];
+  const uint32_t before = shared[wave];
+  *all = shared[waves];
   __syncthreads();
-  return before > v ? before : v;
+  return before > exc ? before : exc;
 }
 
-// Two-level searches over a sorted summary: every s-th search key staged in
-// LDS (kSamples at most) narrows a bound to a window of fewer than s entries,
-// which a search over global memory finishes -- the same index as one binary
-// search over the whole array, with log2(s) dependent global loads instead of
-// log2(size) (a 41K-entry summary: 5 instead of 16).
-constexpr uint32_t kSamples = 2048;
-
-__device__ __forceinline__ uint32_t sample_stride(uint32_t size) {
-  uint32_t s = 16;
-  while ((uint64_t)s * kSamples < size) s <<= 1;
-  return s;
-}
-
-// smp[t] = arr[t * s].value for t < ceil(m / s).  Call with the whole
-// workgroup; the caller synchronizes before reading smp.
-__device__ __forceinline__ void sample_values(const SkEntry* arr, uint32_t m, uint32_t s, float* smp) {
-  const uint32_t samples = (m + s - 1) / s;
-  for (uint32_t t = threadIdx.x; t < samples; t += blockDim.x) smp[t] = arr[(uint64_t)t * s].value;
-}
-
-// First i in [0, m) with !(arr[i].value < x), arr sorted by value.
-__device__ __forceinline__ uint32_t lower_bound_sampled(const SkEntry* arr, uint32_t m, const float* smp, uint32_t s,
-                                                        float x) {
-  const uint32_t samples = (m + s - 1) / s;
-  uint32_t lo = 0, hi = samples;  // first sample t with !(smp[t] < x)
+// Number of a[0..len) with value < x (ascending values in LDS).
+__device__ __forceinline__ uint32_t count_below(const SkEntry* a, uint32_t len, float x) {
+  uint32_t lo = 0, hi = len;
   while (lo < hi) {
-    const uint32_t mid = lo + (hi - lo) / 2;
-    if (smp[mid] < x) lo = mid + 1;
+    const uint32_t mid = (lo + hi) >> 1;
+    if (a[mid].value < x) lo = mid + 1;
     else hi = mid;
   }
-  const uint32_t t = lo;
-  lo = t == 0 ? 0u : (t - 1) * s + 1;
-  hi = t < samples ? t * s : m;
+  return lo;
+}
+
+// Number of a[0..len) with value <= x.
+__device__ __forceinline__ uint32_t count_not_above(const SkEntry* a, uint32_t len, float x) {
+  uint32_t lo = 0, hi = len;
   while (lo < hi) {
-    const uint32_t mid = lo + (hi - lo) / 2;
-    if (arr[mid].value < x) lo = mid + 1;
+    const uint32_t mid = (lo + hi) >> 1;
+    if (a[mid].value <= x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Merge path of a[0..n) and b[0..m) by value, an a entry before an equal b
+// entry: how many a entries are among the first d merged ones.
+__device__ __forceinline__ uint32_t merge_split(const SkEntry* a, uint32_t n, const SkEntry* b, uint32_t m,
+                                                uint32_t d) {
+  uint32_t lo = d > m ? d - m : 0, hi = d < n ? d : n;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (a[mid].value <= b[d - mid - 1].value) lo = mid + 1;
     else hi = mid;
   }
   return lo;
 }
 
 // kernels/quantile.metal.h:192-214 (sketch_prune_serial), data-parallel.
-// The serial loop walks i forward while rank_k >= rmax_{i+1} + rmin_{i+1};
-// both ranks and these sums are nondecreasing, so i_k is a binary search and
-// the chosen indices c_k are nondecreasing: "append if c_k != last" keeps the
-// first k of each run of equal c_k.  in[0..size) -> out (out != in).
-__device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, SkEntry* out, uint32_t* scan,
-                          float* smp) {
-  __shared__ uint32_t s_last, s_dead;
-  __shared__ uint32_t s_wave_tail[kSketchThreads / kWave];
+// The serial loop walks i forward while rank_k >= rmax_{i+1} + rmin_{i+1}:
+// for k = 1 .. n-1 (n = capacity - 1), with rank_k = 2 (k range / n + begin),
+// i_k = 1 + #{j in [2, size) : rmax_j + rmin_j <= rank_k}; the entry taken is
+// c_k = i_k or i_k + 1 by the midpoint test, k is live while i_k < size - 1,
+// and c_k is appended when it differs from c_{k-1} (c_0 = 0: out[0] = in[0]),
+// then in[size-1] unless it was the last one taken.  The sums rmax_j + rmin_j
+// are nondecreasing (prefix maxima), so for nondecreasing ranks (range >= 0)
+// the counts are one merge path of the ranks against the sums and every c_k
+// is nondecreasing; a negative range takes one binary search per k.
+__device__ __forceinline__ float prune_rank(uint32_t k, float range, uint32_t n, float begin) {
+  return 2.0f * (((float)k * range) / (float)n + begin);
+}
+
+__device__ __forceinline__ float prune_key(const SkEntry& e) { return e.rmax + e.rmin; }
+
+// Entry sources for prune: a summary in memory, or a batch summary with
+// integer weights kept as its values and the weight prefix at each value
+// (rmin = prefix[j], rmax = prefix[j + 1], wmin = their difference; every one
+// exact in binary32 below 2^24).
+struct EntryArray {
+  const SkEntry* p;
+  __device__ __forceinline__ SkEntry operator[](uint32_t j) const { return p[j]; }
+};
+
+struct ExactSummary {
+  const float* value;
+  const uint32_t* prefix;
+  __device__ __forceinline__ SkEntry operator[](uint32_t j) const {
+    const uint32_t lo = prefix[j], hi = prefix[j + 1];
+    return SkEntry{(float)lo, (float)hi, (float)(hi - lo), value[j]};
+  }
+};
+
+template <uint32_t kThreads, typename Src>
+__device__ uint32_t prune(const Src& in, uint32_t size, uint32_t capacity, SkEntry* out, MergeLds<kThreads>& L) {
+  constexpr uint32_t kMergeTile = MergeLds<kThreads>::kTile, kBoundBatch = kThreads;
   if (size <= capacity) {
     for (uint32_t i = threadIdx.x; i < size; i += blockDim.x) out[i] = in[i];
     __syncthreads();
@@ -398,66 +451,151 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
   }
   const float begin = in[0].rmax, range = in[size - 1].rmin - begin;
   const uint32_t n = capacity - 1;
-  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
-  // Sampled keys rmax_j + rmin_j at j = 2 + t * stride.
-  const uint32_t stride = sample_stride(size), samples = size > 2 ? (size - 2 + stride - 1) / stride : 0;
-  __syncthreads();  // smp may still be read by the previous search
-  for (uint32_t t = threadIdx.x; t < samples; t += blockDim.x) {
-    const SkEntry& e = in[2 + (uint64_t)t * stride];
-    smp[t] = e.rmax + e.rmin;
-  }
-  if (threadIdx.x == 0) { out[0] = in[0]; s_last = 0; s_dead = 0; }
-  __syncthreads();
-  uint32_t carry = 0, prev_chunk = 0;
-  for (uint32_t base = 1; base < n; base += blockDim.x) {
-    const uint32_t k = base + threadIdx.x;
-    uint32_t choice = 0;
-    bool live = false;
-    if (k < n) {
-      const float rank = 2.0f * (((float)k * range) / (float)n + begin);
-      // First j in [2, size) with rank < rmax_j + rmin_j: the first sample
-      // above rank bounds it from above, the one before from below.
-      uint32_t lo = 0, hi = samples;
+  if (threadIdx.x == 0) out[0] = in[0];
+  if (!(range >= 0.0f)) {
+    // Ranks that do not grow with k: the serial walk's i only moves forward,
+    // so i_k = 1 + the largest count so far (a prefix maximum over k, one
+    // binary search per k); k stops at the first i_k = size - 1.
+    uint32_t emitted = 0, prev = 0, cmax = 0;
+    for (uint32_t base = 1; base < n; base += blockDim.x) {
+      const uint32_t k = base + threadIdx.x;
+      const uint32_t chunk = n - base < blockDim.x ? n - base : blockDim.x;
+      float rank = 0.0f;
+      uint32_t c = 0;
+      if (k < n) {
+        rank = prune_rank(k, range, n, begin);
+        uint32_t lo = 2, hi = size;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (rank >= prune_key(in[mid])) lo = mid + 1;
+          else hi = mid;
+        }
+        c = lo - 2;
+      }
+      uint32_t all;
+      uint32_t m = block_exclusive_max_u32(c, L.scan, &all);
+      m = m > cmax ? m : cmax;
+      m = c > m ? c : m;
+      cmax = all > cmax ? all : cmax;
+      const uint32_t i = 1 + m;
+      const bool live = k < n && i < size - 1;
+      const uint32_t choice = live ? (rank < min_next(in[i]) + max_prev(in[i + 1]) ? i : i + 1) : 0xffffffffu;
+      L.flag[threadIdx.x] = choice;
+      __syncthreads();
+      const uint32_t before = threadIdx.x ? L.flag[threadIdx.x - 1] : prev;
+      const bool emit = live && choice != before;
+      uint32_t total;
+      const uint32_t off = block_exclusive_u32(emit ? 1u : 0u, L.scan, &total);
+      if (emit) out[1 + emitted + off] = in[choice];
+      emitted += total;
+      // Live ks are a prefix of the chunk (i_k grows with k).
+      uint32_t lo = 0, hi = chunk;
       while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (rank >= smp[mid]) lo = mid + 1;
+        const uint32_t mid = (lo + hi) >> 1;
+        if (L.flag[mid] != 0xffffffffu) lo = mid + 1;
         else hi = mid;
       }
-      const uint32_t t = lo;
-      lo = t == 0 ? 2u : 2 + (t - 1) * stride + 1;
-      hi = t < samples ? 2 + t * stride : size;
-      while (lo < hi) {
-        uint32_t mid = lo + (hi - lo) / 2;
-        if (rank >= in[mid].rmax + in[mid].rmin) lo = mid + 1;
-        else hi = mid;
-      }
-      const uint32_t i = lo - 1;
-      if (i < size - 1) {
-        live = true;
-        choice = rank < min_next(in[i]) + max_prev(in[i + 1]) ? i : i + 1;
-      }
+      if (lo) prev = L.flag[lo - 1];
+      __syncthreads();
+      if (lo < chunk) break;
     }
-    uint32_t prev = __shfl_up(choice, 1, kWave);
-    if (lane == kWave - 1) s_wave_tail[wave] = choice;
+    uint32_t count = 1 + emitted;
+    if (prev != size - 1) {
+      if (threadIdx.x == 0) out[count] = in[size - 1];
+      ++count;
+    }
     __syncthreads();
-    if (lane == 0) prev = wave == 0 ? prev_chunk : s_wave_tail[wave - 1];
-    const uint32_t chunk_tail = s_wave_tail[waves - 1];
-    const bool emit = live && choice != prev;
-    uint32_t total;
-    const uint32_t off = block_exclusive_u32(emit ? 1u : 0u, scan, &total);
-    if (emit) out[1 + carry + off] = in[choice];
-    carry += total;
-    if (live) atomicMax(&s_last, choice);
-    if (k < n && !live) s_dead = 1;
-    __syncthreads();
-    prev_chunk = chunk_tail;
-    if (s_dead) break;
+    return count;
   }
-  __syncthreads();
-  uint32_t count = 1 + carry;
-  const bool tail = s_last != size - 1;
-  __syncthreads();
-  if (tail) {
+  // Merge path of the ranks (A, x = k - 1) against the sums (B, y = j - 2): a
+  // rank goes before a sum when rank < sum, so the B entries before rank x
+  // are the count above.
+  const uint32_t NA = n - 1, NB = size - 2, total = NA + NB;
+  const uint32_t tiles = (total + kMergeTile - 1) / kMergeTile;
+  uint32_t emitted = 0, prev = 0;
+  bool dead = false;
+  for (uint32_t tb = 0; tb < tiles && !dead; tb += kBoundBatch) {
+    const uint32_t tn = tiles - tb < kBoundBatch ? tiles - tb : kBoundBatch;
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t <= tn; t += blockDim.x) {
+      const uint32_t d = (tb + t) * kMergeTile < total ? (tb + t) * kMergeTile : total;
+      uint32_t lo = d > NB ? d - NB : 0, hi = d < NA ? d : NA;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (prune_rank(mid + 1, range, n, begin) < prune_key(in[d - mid - 1 + 2])) lo = mid + 1;
+        else hi = mid;
+      }
+      L.bound[t] = lo;
+    }
+    __syncthreads();
+    for (uint32_t t = 0; t < tn; ++t) {
+      const uint32_t d0 = (tb + t) * kMergeTile, d1 = d0 + kMergeTile < total ? d0 + kMergeTile : total;
+      const uint32_t x0 = L.bound[t], x1 = L.bound[t + 1];
+      const uint32_t na = x1 - x0, y0 = d0 - x0, y1 = d1 - x1;
+      if (!na) continue;  // sums only: no rank to place
+      // Window: in[y0 + 1 .. min(y1 + 2, size - 1)] at w[0 ..]; B entry y is
+      // in[y + 2] = w[1 + y - y0].
+      SkEntry* w = L.a;
+      const uint32_t wlen = (y1 + 2 < size - 1 ? y1 + 2 : size - 1) - y0;
+      for (uint32_t e = threadIdx.x; e < wlen; e += blockDim.x) w[e] = in[y0 + 1 + e];
+      __syncthreads();
+      uint32_t choice[2];
+      uint32_t flags = 0;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t e = 2 * threadIdx.x + s;
+        choice[s] = 0xffffffffu;
+        if (e < na) {
+          const float rank = prune_rank(x0 + e + 1, range, n, begin);
+          uint32_t lo = 0, hi = y1 - y0;
+          while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (prune_key(w[1 + mid]) <= rank) lo = mid + 1;
+            else hi = mid;
+          }
+          const uint32_t i = 1 + y0 + lo;  // in[i] = w[lo], in[i + 1] = w[lo + 1]
+          if (i < size - 1) choice[s] = rank < min_next(w[lo]) + max_prev(w[lo + 1]) ? i : i + 1;
+        }
+        L.flag[e] = choice[s];
+      }
+      __syncthreads();
+      // Live ranks are a prefix (the counts grow with k).
+      uint32_t emit[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t e = 2 * threadIdx.x + s;
+        const uint32_t before = e ? L.flag[e - 1] : prev;
+        emit[s] = e < na && choice[s] != 0xffffffffu && choice[s] != before;
+        flags += emit[s];
+      }
+      uint32_t tot;
+      const uint32_t off = block_exclusive_u32(flags, L.scan, &tot);
+      uint32_t o = 1 + emitted + off;
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        if (emit[s]) out[o++] = w[choice[s] - y0 - 1];
+      emitted += tot;
+      // The tile's last live choice, and whether a rank was not live.
+      const uint32_t last_flag = L.flag[na - 1];
+      if (last_flag == 0xffffffffu) {
+        dead = true;
+        // First non-live rank of the tile: the live prefix ends before it.
+        uint32_t lo = 0, hi = na;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (L.flag[mid] != 0xffffffffu) lo = mid + 1;
+          else hi = mid;
+        }
+        if (lo) prev = L.flag[lo - 1];
+      } else {
+        prev = last_flag;
+      }
+      __syncthreads();
+      if (dead) break;
+    }
+  }
+  uint32_t count = 1 + emitted;
+  if (prev != size - 1) {
     if (threadIdx.x == 0) out[count] = in[size - 1];
     ++count;
   }
@@ -466,10 +604,16 @@ __device__ uint32_t prune(const SkEntry* in, uint32_t size, uint32_t capacity, S
 }
 
 // kernels/quantile.metal.h:266-311 (sketch_combine_serial), merge-path form.
-// a[0..n) and b[0..m) -> out; out must differ from both.  eq_prefix needs
-// 2n + 1 words.
+// a[0..n) and b[0..m) -> out; out must differ from both.  An a entry whose
+// value b also holds absorbs that b entry (sums of rmin, rmax and wmin); any
+// other entry adds the neighbouring bounds of the other summary: rmin +=
+// min_next of its last entry below, rmax += max_prev of its first entry
+// above (or that summary's last rmax).  Then the error fix-up: rmin = prefix
+// max of rmin; rmax = prefix max of max(rmax, rmin' + wmin).
+template <uint32_t kThreads>
 __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint32_t m, SkEntry* out,
-                            uint32_t* eq_prefix, uint32_t* scan, float* smp) {
+                            MergeLds<kThreads>& L) {
+  constexpr uint32_t kMergeTile = MergeLds<kThreads>::kTile, kBoundBatch = kThreads;
   if (!m) {
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = a[i];
     __syncthreads();
@@ -480,143 +624,176 @@ __device__ uint32_t combine(const SkEntry* a, uint32_t n, const SkEntry* b, uint
     __syncthreads();
     return m;
   }
-  // Sampled values of both summaries (b's in smp, a's in smp + kSamples).
-  const uint32_t sb = sample_stride(m), sa = sample_stride(n);
-  float* smp_b = smp;
-  float* smp_a = smp + kSamples;
-  __syncthreads();  // smp may still be read by the previous search
-  sample_values(b, m, sb, smp_b);
-  sample_values(a, n, sa, smp_a);
-  __syncthreads();
-  // Equal-value pairs, indexed by a: eq_prefix[i] = #pairs with a-index < i;
-  // each a value's position in b kept in rank_a for the placement below.
-  uint32_t* rank_a = eq_prefix + n + 1;
-  uint32_t carry = 0;
-  for (uint32_t base = 0; base < n; base += blockDim.x) {
-    uint32_t i = base + threadIdx.x;
-    uint32_t eq = 0;
-    if (i < n) {
-      float x = a[i].value;
-      const uint32_t lo = lower_bound_sampled(b, m, smp_b, sb, x);
-      rank_a[i] = lo;
-      eq = lo < m && b[lo].value == x;
-    }
-    uint32_t total;
-    uint32_t off = block_exclusive_u32(eq, scan, &total);
-    if (i < n) eq_prefix[i] = carry + off;
-    carry += total;
-  }
-  if (threadIdx.x == 0) eq_prefix[n] = carry;
-  __syncthreads();
-  const uint32_t count = n + m - carry;
   const float tail_a = a[n - 1].rmax, tail_b = b[m - 1].rmax;
-  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const SkEntry x = a[i];
-    const uint32_t lo = rank_a[i];
-    SkEntry r;
-    if (lo < m && b[lo].value == x.value) {
-      const SkEntry y = b[lo];
-      r.rmin = x.rmin + y.rmin; r.rmax = x.rmax + y.rmax; r.wmin = x.wmin + y.wmin; r.value = x.value;
-    } else {
-      float prev_b = lo > 0 ? min_next(b[lo - 1]) : 0.0f;
-      float add = lo < m ? max_prev(b[lo]) : tail_b;
-      r.rmin = x.rmin + prev_b; r.rmax = x.rmax + add; r.wmin = x.wmin; r.value = x.value;
+  const uint32_t total = n + m, tiles = (total + kMergeTile - 1) / kMergeTile;
+  uint32_t pairs = 0;                 // equal pairs whose a entry is in an earlier tile
+  uint32_t run_min = 0, run_max = 0;  // fix-up maxima so far (bit patterns: all values are >= 0)
+  for (uint32_t tb = 0; tb < tiles; tb += kBoundBatch) {
+    const uint32_t tn = tiles - tb < kBoundBatch ? tiles - tb : kBoundBatch;
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t <= tn; t += blockDim.x)
+      L.bound[t] = merge_split(a, n, b, m, (tb + t) * kMergeTile < total ? (tb + t) * kMergeTile : total);
+    __syncthreads();
+    for (uint32_t t = 0; t < tn; ++t) {
+      const uint32_t d0 = (tb + t) * kMergeTile, d1 = d0 + kMergeTile < total ? d0 + kMergeTile : total;
+      const uint32_t i0 = L.bound[t], i1 = L.bound[t + 1];
+      const uint32_t j0 = d0 - i0, j1 = d1 - i1;
+      const uint32_t na = i1 - i0, nb = j1 - j0;
+      // a[i0-1 .. i1] at L.a[0 .. na+1], b[j0-1 .. j1] at L.b[0 .. nb+1]
+      // (the entries that exist).
+      for (uint32_t e = threadIdx.x; e < na + 2; e += blockDim.x)
+        if (i0 + e >= 1 && i0 + e - 1 < n) L.a[e] = a[i0 + e - 1];
+      for (uint32_t e = threadIdx.x; e < nb + 2; e += blockDim.x)
+        if (j0 + e >= 1 && j0 + e - 1 < m) L.b[e] = b[j0 + e - 1];
+      __syncthreads();
+      // The tile's elements: a entries e < na, then b entries; two per thread.
+      uint32_t pos[2], lo[2];
+      SkEntry r[2];
+      bool has[2];
+      uint32_t flags = 0;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t e = 2 * threadIdx.x + s;
+        has[s] = false;
+        lo[s] = 0;
+        if (e < na) {
+          const SkEntry x = L.a[1 + e];
+          // b entries below x: all of the earlier tiles', some of this one's.
+          lo[s] = j0 + count_below(L.b + 1, nb, x.value);
+          const SkEntry& at = L.b[1 + lo[s] - j0];  // b[lo] when lo < m
+          const bool eq = lo[s] < m && at.value == x.value;
+          if (eq) {
+            r[s].rmin = x.rmin + at.rmin; r[s].rmax = x.rmax + at.rmax; r[s].wmin = x.wmin + at.wmin;
+            r[s].value = x.value;
+          } else {
+            const float prev_b = lo[s] > 0 ? min_next(L.b[lo[s] - j0]) : 0.0f;
+            const float add = lo[s] < m ? max_prev(at) : tail_b;
+            r[s].rmin = x.rmin + prev_b; r[s].rmax = x.rmax + add; r[s].wmin = x.wmin; r[s].value = x.value;
+          }
+          has[s] = true;
+          flags += eq ? 1u : 0u;
+          L.flag[e] = eq ? 1u : 0u;
+        }
+      }
+      // Equal pairs among the tile's a entries before each one.
+      uint32_t tile_pairs;
+      uint32_t ex = block_exclusive_u32(flags, L.scan, &tile_pairs);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t e = 2 * threadIdx.x + s;
+        if (e < na) {
+          const uint32_t f = L.flag[e];
+          L.flag[e] = ex;
+          ex += f;
+        }
+      }
+      if (threadIdx.x == 0) L.flag[na] = tile_pairs;
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t e = 2 * threadIdx.x + s;
+        if (e < na) {
+          pos[s] = e + (lo[s] - j0) - L.flag[e];
+        } else if (e < na + nb) {
+          const uint32_t f = e - na;
+          const SkEntry y = L.b[1 + f];
+          // a entries at or below y: this tile's and the earlier ones.
+          const uint32_t ub = i0 + count_not_above(L.a + 1, na, y.value);
+          if (ub > 0 && L.a[ub - i0].value == y.value) continue;  // absorbed by a[ub - 1]
+          const float prev_a = ub > 0 ? min_next(L.a[ub - i0]) : 0.0f;
+          const float add = ub < n ? max_prev(L.a[1 + ub - i0]) : tail_a;
+          r[s].rmin = y.rmin + prev_a; r[s].rmax = y.rmax + add; r[s].wmin = y.wmin; r[s].value = y.value;
+          pos[s] = f + (ub - i0) - L.flag[ub - i0];
+          has[s] = true;
+        }
+      }
+      // An equal pair split by a tile edge: its a entry (the earlier tile's
+      // last) writes the combined entry at the later tile's first position,
+      // which the later tile's positions leave free.  The outputs are local
+      // positions [first, first + count).
+      const uint32_t first = (i0 > 0 && j0 < m && L.a[0].value == L.b[1].value) ? 1u : 0u;
+      const uint32_t split_next = (i1 > 0 && j1 < m && L.a[na].value == L.b[nb + 1].value) ? 1u : 0u;
+      const uint32_t count = (d1 - d0) - L.flag[na] - first + split_next;
+      __syncthreads();  // windows read: L.a becomes the tile's output
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        if (has[s]) L.a[pos[s]] = r[s];
+      __syncthreads();
+      // Fix-up over the tile's outputs in order, two per thread.
+      SkEntry o[2];
+      uint32_t kmin[2], kmax[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t q = 2 * threadIdx.x + s;
+        kmin[s] = 0;
+        if (q < count) { o[s] = L.a[first + q]; kmin[s] = __float_as_uint(o[s].rmin); }
+      }
+      uint32_t all_min;
+      uint32_t pm = block_exclusive_max_u32(kmin[0] > kmin[1] ? kmin[0] : kmin[1], L.scan, &all_min);
+      pm = pm > run_min ? pm : run_min;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t q = 2 * threadIdx.x + s;
+        pm = kmin[s] > pm ? kmin[s] : pm;
+        kmax[s] = 0;
+        if (q < count) {
+          o[s].rmin = __uint_as_float(pm);
+          const float a2 = o[s].rmin + o[s].wmin;
+          kmax[s] = __float_as_uint(o[s].rmax > a2 ? o[s].rmax : a2);
+        }
+      }
+      uint32_t all_max;
+      uint32_t px = block_exclusive_max_u32(kmax[0] > kmax[1] ? kmax[0] : kmax[1], L.scan, &all_max);
+      px = px > run_max ? px : run_max;
+      const uint32_t base = d0 - pairs + first;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t q = 2 * threadIdx.x + s;
+        px = kmax[s] > px ? kmax[s] : px;
+        if (q < count) {
+          o[s].rmax = __uint_as_float(px);
+          out[base + q] = o[s];
+        }
+      }
+      run_min = all_min > run_min ? all_min : run_min;
+      run_max = all_max > run_max ? all_max : run_max;
+      pairs += L.flag[na];
+      __syncthreads();
     }
-    out[i + lo - eq_prefix[i]] = r;
-  }
-  for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) {
-    const SkEntry y = b[j];
-    const uint32_t lo = lower_bound_sampled(a, n, smp_a, sa, y.value);
-    if (lo < n && a[lo].value == y.value) continue;
-    float prev_a = lo > 0 ? min_next(a[lo - 1]) : 0.0f;
-    float add = lo < n ? max_prev(a[lo]) : tail_a;
-    SkEntry r;
-    r.rmin = y.rmin + prev_a; r.rmax = y.rmax + add; r.wmin = y.wmin; r.value = y.value;
-    out[j + lo - eq_prefix[lo]] = r;
   }
   __syncthreads();
-  // Error fix-up: rmin = prefix max of rmin; rmax = prefix max of
-  // max(rmax, rmin' + wmin).  All values are nonnegative, so binary32 order
-  // equals the order of their bit patterns.
-  uint32_t run_min = 0, run_max = 0;
-  for (uint32_t base = 0; base < count; base += blockDim.x) {
-    uint32_t i = base + threadIdx.x;
-    SkEntry e;
-    uint32_t kmin = 0;
-    if (i < count) { e = out[i]; kmin = __float_as_uint(e.rmin); }
-    uint32_t pmin = block_inclusive_max_u32(kmin, scan);
-    pmin = pmin > run_min ? pmin : run_min;
-    uint32_t kmax = 0;
-    if (i < count) {
-      e.rmin = __uint_as_float(pmin);
-      float a2 = e.rmin + e.wmin;
-      kmax = __float_as_uint(e.rmax > a2 ? e.rmax : a2);
-    }
-    uint32_t pmax = block_inclusive_max_u32(kmax, scan);
-    pmax = pmax > run_max ? pmax : run_max;
-    __syncthreads();
-    if (i < count) {
-      e.rmax = __uint_as_float(pmax);
-      out[i] = e;
-    }
-    // Carry the chunk's last prefix values.
-    __shared__ uint32_t carry_min, carry_max;
-    if (threadIdx.x == blockDim.x - 1 || i == count - 1) { carry_min = pmin; carry_max = pmax; }
-    __syncthreads();
-    run_min = carry_min;
-    run_max = carry_max;
-    __syncthreads();
-  }
-  return count;
+  return total - pairs;
 }
-
 
 // Summary of one sorted batch (kernels/quantile.metal.h:216-240): one entry
 // per distinct value, in value order, holding the value's weight w (the
 // binary32 sum of its runs' weights in sort order) and the running binary32
 // total before (rmin) and after (rmax) it.  keys[0..size) and wts[0..size)
 // are the batch's runs' order keys and weights in value order; scratch needs
-// size + 1 words.
+// size + 1 words.  (Integer weights summing below 2^24 take summarize_exact.)
 __device__ uint32_t summarize(const uint32_t* __restrict__ keys, const float* __restrict__ wts, uint32_t size,
-                              bool exact, SkEntry* out,
-                              uint32_t* scratch, uint32_t* scan) {
-  // Group starts (value changes in sort order) and each group's first
-  // position; with integer weights summing below 2^24 (exact) also each
-  // group's weight prefix, since every binary32 partial sum is then exact and
-  // a parallel prefix gives the serial sums bit for bit.
-  uint32_t carry_w = 0, carry_s = 0;
+                              SkEntry* out, uint32_t* scratch, uint32_t* scan) {
+  // Group starts (value changes in sort order) and each group's first position.
+  uint32_t carry_s = 0;
   for (uint32_t base = 0; base < size; base += blockDim.x) {
     const uint32_t i = base + threadIdx.x;
-    uint32_t w = 0, start = 0;
+    uint32_t start = 0;
     float v = 0.0f;
     if (i < size) {
       v = key_value(keys[i]);
-      if (exact) w = (uint32_t)wts[i];
       start = i == 0 || key_value(keys[i - 1]) != v;
     }
-    uint32_t tw = 0, ts;
-    const uint32_t pw = (exact ? block_exclusive_u32(w, scan, &tw) : 0u) + carry_w;
+    uint32_t ts;
     const uint32_t ps = block_exclusive_u32(start, scan, &ts) + carry_s;
     if (start) {
-      scratch[ps] = exact ? pw : i;
+      scratch[ps] = i;
       out[ps].value = v;
     }
-    carry_w += tw;
     carry_s += ts;
   }
-  if (threadIdx.x == 0) scratch[carry_s] = exact ? carry_w : size;
+  if (threadIdx.x == 0) scratch[carry_s] = size;
   __syncthreads();
   const uint32_t n = carry_s;
-  if (exact) {
-    for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
-      const uint32_t p = scratch[o], q = scratch[o + 1];
-      out[o].rmin = (float)p;
-      out[o].rmax = (float)q;
-      out[o].wmin = (float)(q - p);
-    }
-    __syncthreads();
-    return n;
-  }
   // Each group's weight: its runs' weights summed in sort order.
   for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
     const uint32_t s = scratch[o], e = scratch[o + 1];
@@ -651,28 +828,112 @@ __device__ uint32_t summarize(const uint32_t* __restrict__ keys, const float* __
   return n;
 }
 
+// Exclusive prefix sums of two values over the workgroup's threads, with
+// their totals.
+__device__ __forceinline__ void block_exclusive_u32x2(uint32_t a, uint32_t b, uint32_t* shared, uint32_t& ea,
+                                                      uint32_t& eb, uint32_t& ta, uint32_t& tb) {
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  const uint32_t ia = wave_inclusive_u32(a), ib = wave_inclusive_u32(b);
+  if (lane == kWave - 1) { shared[2 * wave] = ia; shared[2 * wave + 1] = ib; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t ra = 0, rb = 0;
+    for (uint32_t w = 0; w < waves; ++w) {
+      const uint32_t xa = shared[2 * w], xb = shared[2 * w + 1];
+      shared[2 * w] = ra; shared[2 * w + 1] = rb;
+      ra += xa; rb += xb;
+    }
+    shared[2 * waves] = ra; shared[2 * waves + 1] = rb;
+  }
+  __syncthreads();
+  ea = shared[2 * wave] + ia - a;
+  eb = shared[2 * wave + 1] + ib - b;
+  ta = shared[2 * waves];
+  tb = shared[2 * waves + 1];
+  __syncthreads();
+}
+
+// Summary of one sorted batch with integer weights summing below 2^24
+// (kernels/quantile.metal.h:216-240): value[g] is the g-th distinct value
+// and prefix[g] the weight of every run before it (prefix[n] the total), so
+// the summary entry is (rmin, rmax, wmin) = (prefix[g], prefix[g + 1], their
+// difference) -- every binary32 partial sum is exact, so the prefix gives the
+// serial sums bit for bit.  Four consecutive runs per thread; scan needs
+// 2 (waves + 1) words.  Returns the number of distinct values.
+__device__ uint32_t summarize_exact(const uint32_t* __restrict__ keys, const float* __restrict__ wts, uint32_t size,
+                                    float* __restrict__ value, uint32_t* __restrict__ prefix, uint32_t* scan) {
+  constexpr uint32_t kPer = 4;
+  const uint32_t chunk = kPer * blockDim.x;
+  uint32_t carry_g = 0, carry_w = 0;
+  for (uint32_t base = 0; base < size; base += chunk) {
+    const uint32_t i0 = base + kPer * threadIdx.x;
+    float v[kPer];
+    uint32_t w[kPer];
+    bool start[kPer];
+    float prev = 0.0f;
+    if (i0 > 0 && i0 < size) prev = key_value(keys[i0 - 1]);
+    uint32_t groups = 0, weight = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+      const uint32_t i = i0 + u;
+      const bool in = i < size;
+      v[u] = in ? key_value(keys[i]) : 0.0f;
+      w[u] = in ? (uint32_t)wts[i] : 0u;
+      start[u] = in && (i == 0 || v[u] != (u ? v[u - 1] : prev));
+      groups += start[u] ? 1u : 0u;
+      weight += w[u];
+    }
+    uint32_t eg, ew, tg, tw;
+    block_exclusive_u32x2(groups, weight, scan, eg, ew, tg, tw);
+    uint32_t g = carry_g + eg, pw = carry_w + ew;
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+      if (start[u]) {
+        value[g] = v[u];
+        prefix[g] = pw;
+        ++g;
+      }
+      pw += w[u];
+    }
+    carry_g += tg;
+    carry_w += tw;
+  }
+  if (threadIdx.x == 0) prefix[carry_g] = carry_w;
+  __syncthreads();
+  return carry_g;
+}
+
 // Level 0 of every feature's tree: one workgroup per batch summarizes the
 // batch's sorted runs into the feature's work area and prunes the summary to
 // `limit` entries (the serial rule's first step for each batch,
 // kernels/quantile.metal.h:317-352).
-__global__ __launch_bounds__(kSketchThreads) void k_level0(const uint32_t* __restrict__ table,
+__global__ __launch_bounds__(kMergeThreads) void k_level0(const uint32_t* __restrict__ table,
                                                            const SkFeature* __restrict__ features,
                                                            const SkStats* __restrict__ stats,
                                                            const uint32_t* __restrict__ keys,
                                                            const float* __restrict__ wts, SkEntry* __restrict__ work,
                                                            SkEntry* __restrict__ tree, uint32_t* __restrict__ scratch,
                                                            uint32_t* __restrict__ node_count) {
-  __shared__ uint32_t scan[kSketchThreads / kWave + 1];
-  __shared__ float s_smp[2 * kSamples];
+  __shared__ MergeLds<kMergeThreads> L;
   const uint32_t c = table[2 * blockIdx.x], b = table[2 * blockIdx.x + 1];
   const SkFeature fe = features[c];
   const uint64_t begin = (uint64_t)b * 2 * fe.limit;
   const uint32_t runs = stats[c].runs;
   const uint32_t size = (uint32_t)(runs - begin < 2ull * fe.limit ? runs - begin : 2ull * fe.limit);
-  SkEntry* summary = work + fe.base + begin;
-  const uint32_t n = summarize(keys + fe.base + begin, wts + fe.base + begin, size, fe.exact != 0, summary,
-                               scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), scan);
-  const uint32_t m = prune(summary, n, fe.limit, tree + fe.tree + (uint64_t)b * fe.limit, scan, s_smp);
+  SkEntry* summary = work + fe.base + begin;  // 16 bytes per run of the batch
+  SkEntry* pruned = tree + fe.tree + (uint64_t)b * fe.limit;
+  uint32_t m;
+  if (fe.exact) {
+    // Values and weight prefixes (2 size + 1 words) instead of 16-byte entries.
+    float* value = reinterpret_cast<float*>(summary);
+    uint32_t* prefix = reinterpret_cast<uint32_t*>(summary) + size;
+    const uint32_t n = summarize_exact(keys + fe.base + begin, wts + fe.base + begin, size, value, prefix, L.scan);
+    m = prune(ExactSummary{value, prefix}, n, fe.limit, pruned, L);
+  } else {
+    const uint32_t n = summarize(keys + fe.base + begin, wts + fe.base + begin, size, summary,
+                                 scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), L.scan);
+    m = prune(EntryArray{summary}, n, fe.limit, pruned, L);
+  }
   if (threadIdx.x == 0) node_count[fe.node_base + b] = m;
 }
 
@@ -681,14 +942,13 @@ __global__ __launch_bounds__(kSketchThreads) void k_level0(const uint32_t* __res
 // prunes the merge to `limit`.  A merge of at most `limit` entries stays at
 // its level in the serial rule instead of moving up, so the tree no longer
 // matches it: the feature is marked for the serial rebuild.
-__global__ __launch_bounds__(kSketchThreads) void k_level_up(uint32_t level, const uint32_t* __restrict__ table,
+template <uint32_t kThreads>
+__global__ __launch_bounds__(kThreads) void k_level_up(uint32_t level, const uint32_t* __restrict__ table,
                                                              const SkFeature* __restrict__ features,
                                                              SkEntry* __restrict__ work, SkEntry* __restrict__ tree,
-                                                             uint32_t* __restrict__ scratch,
                                                              uint32_t* __restrict__ node_count,
                                                              uint32_t* __restrict__ serial) {
-  __shared__ uint32_t scan[kSketchThreads / kWave + 1];
-  __shared__ float s_smp[2 * kSamples];
+  __shared__ MergeLds<kThreads> L;
   __shared__ uint32_t s_serial;
   const uint32_t c = table[2 * blockIdx.x], k = table[2 * blockIdx.x + 1];
   // Other workgroups of this level may set the flag meanwhile: one read,
@@ -702,12 +962,12 @@ __global__ __launch_bounds__(kSketchThreads) void k_level_up(uint32_t level, con
   const uint32_t na = node_count[fe.node_base + newer], nb = node_count[fe.node_base + older];
   SkEntry* merged = work + fe.base + (uint64_t)k * 2 * fe.limit;
   const uint32_t n = combine(tree + fe.tree + (uint64_t)newer * fe.limit, na, tree + fe.tree + (uint64_t)older * fe.limit,
-                             nb, merged, scratch + fe.scratch + (uint64_t)k * (2 * fe.limit + 2), scan, s_smp);
+                             nb, merged, L);
   if (n <= fe.limit) {
     if (threadIdx.x == 0) atomicOr(&serial[c], 1u);
     return;
   }
-  const uint32_t m = prune(merged, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, scan, s_smp);
+  const uint32_t m = prune(EntryArray{merged}, n, fe.limit, tree + fe.tree + (uint64_t)(here + k) * fe.limit, L);
   if (threadIdx.x == 0) node_count[fe.node_base + here + k] = m;
 }
 
@@ -721,16 +981,17 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
                                                            const SkEntry* __restrict__ tree,
                                                            const uint32_t* __restrict__ node_count,
                                                            const uint32_t* __restrict__ serial,
-                                                           SkEntry* __restrict__ fin, uint32_t* __restrict__ fin_scratch,
+                                                           SkEntry* __restrict__ fin,
                                                            uint32_t f0, uint32_t max_bin, float* __restrict__ cut_values,
                                                            uint32_t lds_values, float* __restrict__ cuts,
                                                            uint32_t* __restrict__ counts) {
-  __shared__ uint32_t scan[kSketchThreads / kWave + 1];
-  __shared__ float s_smp[2 * kSamples];
   __shared__ uint32_t level_count[64];
-  // lds_values summary values, then max_bin candidate cuts (0 bytes when
+  // The merges' LDS; once the last prune is done, the same bytes stage
+  // lds_values summary values, then max_bin candidate cuts (nothing when
   // lds_values is 0).
-  extern __shared__ float s_stage[];
+  extern __shared__ __align__(16) uint8_t s_dynamic[];
+  MergeLds<kSketchThreads>& L = *reinterpret_cast<MergeLds<kSketchThreads>*>(s_dynamic);
+  float* s_stage = reinterpret_cast<float*>(s_dynamic);
   const uint32_t c = blockIdx.x;
   const SkFeature fe = features[c];
   const uint32_t limit = fe.limit, batches = fe.batches;
@@ -738,17 +999,15 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
   SkEntry* cur = fin + fe.fin;
   SkEntry* oth = cur + buf;
   SkEntry* lvl = oth + buf;  // the serial stack: (levels + 1) x limit
-  uint32_t* scr = fin_scratch + fe.fin_scratch;
   uint32_t n = 0;
   if (batches && !serial[c]) {
     for (uint32_t level = 0; level < fe.levels && level < 32; ++level) {
       if ((batches >> level) & 1u) {
         const uint32_t node = level_first(batches, level) + (batches >> level) - 1;
-        n = combine(cur, n, tree + fe.tree + (uint64_t)node * limit, node_count[fe.node_base + node], oth, scr, scan,
-                    s_smp);
+        n = combine(cur, n, tree + fe.tree + (uint64_t)node * limit, node_count[fe.node_base + node], oth, L);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      n = prune(cur, n, fe.final_cap, oth, scan, s_smp);
+      n = prune(EntryArray{cur}, n, fe.final_cap, oth, L);
       SkEntry* t = cur; cur = oth; oth = t;
     }
   } else if (batches) {
@@ -763,7 +1022,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
       for (;;) {
         const uint32_t m = level_count[level];
         if (m) {
-          n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan, s_smp);
+          n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, L);
           SkEntry* t = cur; cur = oth; oth = t;
         }
         __syncthreads();
@@ -771,7 +1030,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
         __syncthreads();
         if (n <= limit) break;
         ++level;
-        n = prune(cur, n, limit, oth, scan, s_smp);
+        n = prune(EntryArray{cur}, n, limit, oth, L);
         SkEntry* t = cur; cur = oth; oth = t;
       }
       for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lvl[(uint64_t)level * limit + i] = cur[i];
@@ -783,14 +1042,14 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
     for (uint32_t level = 0; level < fe.levels && level < 64; ++level) {
       const uint32_t m = level_count[level];
       if (m) {
-        n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, scr, scan, s_smp);
+        n = combine(cur, n, lvl + (uint64_t)level * limit, m, oth, L);
         SkEntry* t = cur; cur = oth; oth = t;
       }
-      n = prune(cur, n, fe.final_cap, oth, scan, s_smp);
+      n = prune(EntryArray{cur}, n, fe.final_cap, oth, L);
       SkEntry* t = cur; cur = oth; oth = t;
     }
   }
-  n = prune(cur, n, fe.budget, oth, scan, s_smp);
+  n = prune(EntryArray{cur}, n, fe.budget, oth, L);
   { SkEntry* t = cur; cur = oth; oth = t; }
   // Cuts (kernels/quantile.metal.h:354-400).
   const uint32_t f = f0 + c;
@@ -865,6 +1124,20 @@ uint32_t sketch_budget(uint32_t bins, uint32_t count) {
 }
 
 uint32_t bit_width(uint32_t v) { return v ? 32u - (uint32_t)__builtin_clz(v) : 0u; }
+
+uint64_t g_group_entries = 0;  // mgb_sketch_group_entries; 0: from the free device memory
+
+// Entries per group of features: the set value, else what a quarter of the
+// free device memory holds at kGroupBytesPerEntry.
+uint64_t group_entries() {
+  if (g_group_entries) return std::min(g_group_entries, kMaxGroupEntries);
+  size_t free_bytes = 0, total_bytes = 0;
+  if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return uint64_t(1) << 27;
+  }
+  return std::clamp<uint64_t>(free_bytes / 4 / kGroupBytesPerEntry, uint64_t(1) << 20, kMaxGroupEntries);
+}
 
 // Device memory of one sketch pass, allocated and freed in order on the
 // library stream: a free is queued behind the kernels that use the buffer
@@ -970,7 +1243,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   std::vector<SkFeature> features(nf);
   std::vector<uint32_t> seg_begin, seg_end, table0;
   std::vector<std::vector<uint32_t>> tables;  // levels 1, 2, ...
-  uint64_t tree_total = 0, scratch_total = 0, fin_total = 0, fin_scratch_total = 0;
+  uint64_t tree_total = 0, scratch_total = 0, fin_total = 0;
   uint32_t node_total = 0;
   for (uint32_t c = 0; c < nf; ++c) {
     const SkStats& st = stats[c];
@@ -988,12 +1261,10 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
     fe.tree = tree_total;
     fe.scratch = scratch_total;
     fe.fin = fin_total;
-    fe.fin_scratch = fin_scratch_total;
     node_total += nodes;
     tree_total += (uint64_t)nodes * fe.limit;
     scratch_total += (uint64_t)fe.batches * (2ull * fe.limit + 2);
     fin_total += 2 * (2ull * fe.final_cap + 2) + (uint64_t)(fe.levels + 1) * fe.limit;
-    fin_scratch_total += 2ull * fe.final_cap + 4;
     for (uint32_t b = 0; b < fe.batches; ++b) {
       const uint64_t begin = (uint64_t)b * capacity;
       seg_begin.push_back((uint32_t)(seg[c] + begin));
@@ -1024,7 +1295,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   for (const SkFeature& fe : features) max_budget = std::max(max_budget, fe.budget);
   const uint64_t o_tree = a2.reserve(tree_total * sizeof(SkEntry)), o_scratch = a2.reserve(scratch_total * 4);
   const uint64_t o_node_count = a2.reserve((uint64_t)node_total * 4), o_serial = a2.reserve(nf * 4);
-  const uint64_t o_fin = a2.reserve(fin_total * sizeof(SkEntry)), o_fin_scratch = a2.reserve(fin_scratch_total * 4);
+  const uint64_t o_fin = a2.reserve(fin_total * sizeof(SkEntry));
   const uint64_t o_values = a2.reserve((uint64_t)nf * max_bin * 4), o_temp = a2.reserve(temp_bytes);
   if (a2.commit()) return -1;
   const SkFeature* features_d = a2.at<SkFeature>(o_features);
@@ -1038,29 +1309,35 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
                                                            weight_out, (int)total, (int)seg_begin.size(),
                                                            a2.at<uint32_t>(o_seg_b), a2.at<uint32_t>(o_seg_e), 0, 32,
                                                            s));
-    hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kSketchThreads), 0, s,
+    hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kMergeThreads), 0, s,
                        a2.at<uint32_t>(o_table0), features_d, stats_d, keys_out,
                        reinterpret_cast<const float*>(weight_out), work, tree, scratch,
                        node_count);
     MGB_LAUNCH_CHECK("k_level0");
   }
+  // Levels with many nodes run four 256-thread workgroups per CU; the last
+  // few levels, with fewer nodes than two per CU, give each merge 1,024
+  // threads instead.
   for (size_t l = 0; l < tables.size(); ++l) {
-    hipLaunchKernelGGL(k_level_up, dim3((uint32_t)(tables[l].size() / 2)), dim3(kSketchThreads), 0, s,
-                       (uint32_t)(l + 1), a2.at<uint32_t>(o_tables[l]), features_d, work, tree, scratch, node_count,
-                       serial);
+    const uint32_t nodes = (uint32_t)(tables[l].size() / 2);
+    if (nodes >= kWideLevelNodes)
+      hipLaunchKernelGGL(k_level_up<kMergeThreads>, dim3(nodes), dim3(kMergeThreads), 0, s, (uint32_t)(l + 1),
+                         a2.at<uint32_t>(o_tables[l]), features_d, work, tree, node_count, serial);
+    else
+      hipLaunchKernelGGL(k_level_up<kSketchThreads>, dim3(nodes), dim3(kSketchThreads), 0, s, (uint32_t)(l + 1),
+                         a2.at<uint32_t>(o_tables[l]), features_d, work, tree, node_count, serial);
     MGB_LAUNCH_CHECK("k_level_up");
   }
   // k_finish stages the pruned summary's values and the candidate cuts in LDS
   // for its serial pass when they fit.
   const uint32_t lds_values = (uint64_t)(max_budget + max_bin) * 4 <= kFinishLds ? max_budget : 0;
-  const uint32_t lds_bytes = lds_values ? (lds_values + max_bin) * 4 : 0;
-  if (lds_bytes &&
-      hipFuncSetAttribute((const void*)k_finish, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess) {
+  const uint32_t lds_bytes = std::max<uint32_t>(sizeof(MergeLds<kSketchThreads>), lds_values ? (lds_values + max_bin) * 4 : 0);
+  if (hipFuncSetAttribute((const void*)k_finish, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess) {
     set_error("hipFuncSetAttribute(k_finish LDS) failed");
     return -1;
   }
   hipLaunchKernelGGL(k_finish, dim3(nf), dim3(kSketchThreads), lds_bytes, s, features_d, tree, node_count, serial,
-                     a2.at<SkEntry>(o_fin), a2.at<uint32_t>(o_fin_scratch), f0, max_bin, a2.at<float>(o_values), lds_values,
+                     a2.at<SkEntry>(o_fin), f0, max_bin, a2.at<float>(o_values), lds_values,
                      cuts, counts);
   MGB_LAUNCH_CHECK("k_finish");
   MGB_CHECK(hipStreamSynchronize(s));
@@ -1079,10 +1356,11 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
   if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
   if (!cols) return 0;
   if (rows >= (1u << 31)) { set_error("sketch: rows must be below 2^31"); return -1; }
-  // Feature groups of at most kChunkEntries entries and kMaxGroupFeatures
+  // Feature groups of at most group_entries() entries and kMaxGroupFeatures
   // features (the run passes put the feature in gridDim.y).
+  if (bound_device() < 0) return -1;
   const uint32_t group = (uint32_t)std::max<uint64_t>(
-      1, std::min<uint64_t>(std::min<uint64_t>(cols, kMaxGroupFeatures), kChunkEntries / std::max(1u, rows)));
+      1, std::min<uint64_t>(std::min<uint64_t>(cols, kMaxGroupFeatures), group_entries() / std::max(1u, rows)));
   for (uint32_t f0 = 0; f0 < cols; f0 += group) {
     const uint32_t nf = std::min(group, cols - f0);
     StreamBuffer xt;
@@ -1103,21 +1381,28 @@ int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint6
                         uint32_t cols, const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
   if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
   if (!cols) return 0;
+  if (bound_device() < 0) return -1;
   (void)rows;
   std::vector<uint64_t> colptr_host(cols + 1);
   MGB_CHECK(hipMemcpyAsync(colptr_host.data(), colptr, (cols + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost, stream()));
   MGB_CHECK(hipStreamSynchronize(stream()));
-  // Groups of whole columns of at most kChunkEntries entries (a longer column
-  // forms a group of its own) and kMaxGroupFeatures columns.
+  // Groups of whole columns of at most group_entries() entries (a longer
+  // column forms a group of its own) and kMaxGroupFeatures columns.
+  const uint64_t chunk = group_entries();
   for (uint32_t f0 = 0; f0 < cols;) {
     uint32_t f1 = f0 + 1;
-    while (f1 < cols && f1 - f0 < kMaxGroupFeatures && colptr_host[f1 + 1] - colptr_host[f0] <= kChunkEntries) ++f1;
+    while (f1 < cols && f1 - f0 < kMaxGroupFeatures && colptr_host[f1 + 1] - colptr_host[f0] <= chunk) ++f1;
     std::vector<uint64_t> seg(f1 - f0 + 1);
     for (uint32_t c = 0; c <= f1 - f0; ++c) seg[c] = colptr_host[f0 + c] - colptr_host[f0];
     const uint64_t first = colptr_host[f0];
     if (sketch_group(values + first, seg, row_of + first, f1 - f0, f0, weights, max_bin, cuts, counts)) return -1;
     f0 = f1;
   }
+  return 0;
+}
+
+int mgb_sketch_group_entries(uint64_t entries) {
+  g_group_entries = entries;
   return 0;
 }
 

@@ -1391,13 +1391,18 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
                   xkey[slot_in_block][0], wave_in_item, t.recs + f, best_bank(t, depth), f, t.cols);
     return;
   }
+  // The pair's frontier entries are requested before the level's node count,
+  // so the two loads overlap instead of forming a chain.  The index is
+  // clamped to the level's 2^(depth-1) possible pairs (the grid's last block
+  // may run past them); every item kept below has pair < pairs anyway.
+  const uint32_t pair = item / F, f = item % F;
+  const Frontier* fr = t.frontier[depth & 1];
+  const uint32_t pair_ld = min(pair, (1u << (depth - 1)) - 1);
+  const Frontier a = fr[2 * pair_ld], b = fr[2 * pair_ld + 1];
   const uint32_t n = st->n_nodes;
   const uint32_t pairs = n / 2;
   if (item >= pairs * F) return;
-  const uint32_t pair = item / F, f = item % F;
   if (t.allowed && !t.allowed[f]) return;  // this tree never scores the feature: no sibling either
-  const Frontier* fr = t.frontier[depth & 1];
-  const Frontier a = fr[2 * pair], b = fr[2 * pair + 1];
   const uint32_t built = a.built ? 2 * pair : 2 * pair + 1, other = built ^ 1u;
   const Frontier& fb = a.built ? a : b;
   const Frontier& fo = a.built ? b : a;
