@@ -10,12 +10,14 @@
 //  2. runs of equal values in row order over each feature's non-missing,
 //     nonzero-weight entries, in 1024-entry blocks: per-block counts, a
 //     per-feature scan over blocks that joins runs crossing block edges, the
-//     runs written at their scanned offsets, then each run's weight (its
-//     length, or the in-order binary32 sum of its entries' weights);
+//     runs written at their scanned offsets as sort keys of their values,
+//     then each run's weight as the sort's payload (its length, or the
+//     in-order binary32 sum of its entries' weights);
 //  3. the host plans batches of 2*limit runs (limit = sketch budget) from the
 //     per-feature counts;
 //  4. a segmented, stable radix sort orders every batch's runs by value;
-//  5. one workgroup per batch summarizes it and prunes the summary to limit;
+//  5. one workgroup per batch summarizes it (integer weights: its distinct
+//     values and weight prefixes) and prunes the summary to limit;
 //  6. the serial rule merges batch summaries through a stack of levels like a
 //     binary counter (kernels/quantile.metal.h:317-352): while every merge
 //     yields more than `limit` entries that is a balanced tree, computed here
@@ -43,7 +45,8 @@ namespace mgb {
 namespace {
 
 constexpr uint32_t kSketchThreads = 1024;
-constexpr uint32_t kBlockEntries = 1024;                 // entries per workgroup in the run passes
+constexpr uint32_t kBlockEntries = 1024;                 // entries per block of the run passes
+constexpr uint32_t kRunBlocks = 8;                       // consecutive blocks per workgroup in the run passes
 constexpr uint64_t kGroupBytesPerEntry = 64;              // a group's temporaries per entry (typical)
 constexpr uint64_t kMaxGroupEntries = (uint64_t(1) << 31) - 1;  // 32-bit positions; the sort counts in int
 constexpr uint32_t kMaxGroupFeatures = 65535;            // features per group
@@ -97,6 +100,31 @@ __device__ __forceinline__ float key_value(uint32_t key) {
 __device__ __forceinline__ float min_next(const SkEntry& e) { return e.rmin + e.wmin; }
 __device__ __forceinline__ float max_prev(const SkEntry& e) { return e.rmax - e.wmin; }
 
+// Exclusive prefix sums of two values over the workgroup's threads, with
+// their totals.
+__device__ __forceinline__ void block_exclusive_u32x2(uint32_t a, uint32_t b, uint32_t* shared, uint32_t& ea,
+                                                      uint32_t& eb, uint32_t& ta, uint32_t& tb) {
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  const uint32_t ia = wave_inclusive_u32(a), ib = wave_inclusive_u32(b);
+  if (lane == kWave - 1) { shared[2 * wave] = ia; shared[2 * wave + 1] = ib; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t ra = 0, rb = 0;
+    for (uint32_t w = 0; w < waves; ++w) {
+      const uint32_t xa = shared[2 * w], xb = shared[2 * w + 1];
+      shared[2 * w] = ra; shared[2 * w + 1] = rb;
+      ra += xa; rb += xb;
+    }
+    shared[2 * waves] = ra; shared[2 * waves + 1] = rb;
+  }
+  __syncthreads();
+  ea = shared[2 * wave] + ia - a;
+  eb = shared[2 * wave + 1] + ib - b;
+  ta = shared[2 * waves];
+  tb = shared[2 * waves + 1];
+  __syncthreads();
+}
+
 // Columns [col0, col0 + ncols) of a row-major rows x cols matrix into
 // column-major Xt (ncols columns of `rows` entries).
 __global__ void k_transpose(const float* __restrict__ X, uint32_t rows, uint32_t cols, uint32_t col0, uint32_t ncols,
@@ -114,7 +142,7 @@ __global__ void k_transpose(const float* __restrict__ X, uint32_t rows, uint32_t
   }
 }
 
-// One entry per thread of block blockIdx.x of feature blockIdx.y: is it
+// One entry per thread of block blk of feature blockIdx.y: is it
 // present (not NaN) and valid (present with a nonzero weight), and the last
 // valid value before it within the block.  Also the block's first and last
 // valid values.  `s_*` hold one slot per wave.
@@ -124,18 +152,33 @@ struct EntryView {
   float prev;
 };
 
-__device__ __forceinline__ EntryView view_entry(const float* __restrict__ vals, const uint64_t* __restrict__ seg,
+// The thread's entry of block blk (its value, weight and whether it exists);
+// the kernels load all their blocks' entries before the first is used.
+struct EntryLoad {
+  float v, w;
+  bool in;
+};
+
+__device__ __forceinline__ EntryLoad load_entry(const float* __restrict__ vals, const uint64_t* __restrict__ seg,
                                                 const uint32_t* __restrict__ row_of, const float* __restrict__ weights,
-                                                uint32_t* s_has, float* s_first, float* s_last, bool& block_has,
-                                                float& block_first, float& block_last) {
+                                                uint32_t blk) {
   const uint32_t c = blockIdx.y;
   const uint64_t base = seg[c];
   const uint32_t count = (uint32_t)(seg[c + 1] - base);
-  const uint32_t r = blockIdx.x * kBlockEntries + threadIdx.x;
-  const bool in = r < count;
+  const uint32_t r = blk * kBlockEntries + threadIdx.x;
+  EntryLoad l;
+  l.in = r < count;
+  l.v = l.in ? vals[base + r] : __uint_as_float(0x7fc00000u);
+  l.w = (l.in && weights) ? weights[row_of ? row_of[base + r] : r] : 1.0f;
+  return l;
+}
+
+__device__ __forceinline__ EntryView view_entry(const EntryLoad& l, uint32_t* s_has, float* s_first, float* s_last,
+                                                bool& block_has, float& block_first, float& block_last) {
+  const bool in = l.in;
   EntryView e;
-  e.v = in ? vals[base + r] : __uint_as_float(0x7fc00000u);
-  e.w = (in && weights) ? weights[row_of ? row_of[base + r] : r] : 1.0f;
+  e.v = l.v;
+  e.w = l.w;
   e.present = in && !isnan(e.v);
   e.valid = e.present && (__float_as_uint(e.w) & 0x7fffffffu) != 0;
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
@@ -168,23 +211,38 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_count(const float* __res
                                                               const uint32_t* __restrict__ row_of,
                                                               const float* __restrict__ weights, uint32_t max_blocks,
                                                               SkBlock* __restrict__ blocks) {
-  __shared__ uint32_t s_has[kSketchThreads / kWave], scan[kSketchThreads / kWave + 1];
+  __shared__ uint32_t s_has[kSketchThreads / kWave], counts[kSketchThreads / kWave][3];
   __shared__ float s_first[kSketchThreads / kWave], s_last[kSketchThreads / kWave];
   const uint32_t c = blockIdx.y;
-  if ((uint64_t)blockIdx.x * kBlockEntries >= seg[c + 1] - seg[c]) return;  // the whole block is past the feature
-  bool has = false;
-  float first = 0.0f, last = 0.0f;
-  const EntryView e = view_entry(vals, seg, row_of, weights, s_has, s_first, s_last, has, first, last);
-  const bool new_run = e.valid && (!e.have_prev || e.v != e.prev);
-  uint32_t valid, present, runs;
-  block_exclusive_u32(e.valid ? 1u : 0u, scan, &valid);
-  block_exclusive_u32(e.present ? 1u : 0u, scan, &present);
-  block_exclusive_u32(new_run ? 1u : 0u, scan, &runs);
-  if (threadIdx.x == 0) {
-    SkBlock b{};
-    b.valid = valid; b.present = present; b.runs = runs; b.has = has ? 1u : 0u;
-    b.first = first; b.last = last;
-    blocks[(uint64_t)c * max_blocks + blockIdx.x] = b;
+  const uint32_t nblocks = (uint32_t)((seg[c + 1] - seg[c] + kBlockEntries - 1) / kBlockEntries);
+  const uint32_t b0 = blockIdx.x * kRunBlocks;
+  EntryLoad loads[kRunBlocks];
+#pragma unroll
+  for (uint32_t q = 0; q < kRunBlocks; ++q) loads[q] = load_entry(vals, seg, row_of, weights, b0 + q);
+#pragma unroll
+  for (uint32_t q = 0; q < kRunBlocks; ++q) {
+    const uint32_t blk = b0 + q;
+    if (blk >= nblocks) break;
+    bool has = false;
+    float first = 0.0f, last = 0.0f;
+    const EntryView e = view_entry(loads[q], s_has, s_first, s_last, has, first, last);
+    const bool new_run = e.valid && (!e.have_prev || e.v != e.prev);
+    // Block totals: each wave's counts from its ballots, summed by thread 0.
+    const uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+    const uint32_t cv = (uint32_t)__popcll(__ballot(e.valid));
+    const uint32_t cp = (uint32_t)__popcll(__ballot(e.present));
+    const uint32_t cr = (uint32_t)__popcll(__ballot(new_run));
+    if (lane_id() == 0) { counts[wave][0] = cv; counts[wave][1] = cp; counts[wave][2] = cr; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t valid = 0, present = 0, runs = 0;
+      for (uint32_t w = 0; w < waves; ++w) { valid += counts[w][0]; present += counts[w][1]; runs += counts[w][2]; }
+      SkBlock b{};
+      b.valid = valid; b.present = present; b.runs = runs; b.has = has ? 1u : 0u;
+      b.first = first; b.last = last;
+      blocks[(uint64_t)c * max_blocks + blk] = b;
+    }
+    __syncthreads();
   }
 }
 
@@ -247,42 +305,52 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_scan(const uint64_t* __r
   if (threadIdx.x == 0) stats[c] = SkStats{present, elements, runs, 0};
 }
 
-// The runs of each block at their scanned offsets: run_v (value), run_start
-// (element index within the feature) and, with weights, each valid entry's
-// weight at its element index.
+// The runs of each block at their scanned offsets: the sort key of the run's
+// value (order_key), run_start (element index within the feature) and, with
+// weights, each valid entry's weight at its element index.
 __global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __restrict__ vals,
                                                              const uint64_t* __restrict__ seg,
                                                              const uint32_t* __restrict__ row_of,
                                                              const float* __restrict__ weights, uint32_t max_blocks,
                                                              const SkBlock* __restrict__ blocks,
-                                                             float* __restrict__ run_v, uint32_t* __restrict__ run_start,
+                                                             uint32_t* __restrict__ keys, uint32_t* __restrict__ run_start,
                                                              float* __restrict__ elem_w) {
-  __shared__ uint32_t s_has[kSketchThreads / kWave], scan[kSketchThreads / kWave + 1];
+  __shared__ uint32_t s_has[kSketchThreads / kWave], scan[2 * (kSketchThreads / kWave + 1)];
   __shared__ float s_first[kSketchThreads / kWave], s_last[kSketchThreads / kWave];
   const uint32_t c = blockIdx.y;
   const uint64_t base = seg[c];
-  if ((uint64_t)blockIdx.x * kBlockEntries >= seg[c + 1] - base) return;
-  const SkBlock blk = blocks[(uint64_t)c * max_blocks + blockIdx.x];
-  bool has = false;
-  float first = 0.0f, last = 0.0f;
-  EntryView e = view_entry(vals, seg, row_of, weights, s_has, s_first, s_last, has, first, last);
-  if (!e.have_prev && blk.prev_has) { e.prev = blk.prev; e.have_prev = true; }
-  const bool new_run = e.valid && (!e.have_prev || e.v != e.prev);
-  uint32_t tv, tr;
-  const uint32_t eidx = blk.elem_off + block_exclusive_u32(e.valid ? 1u : 0u, scan, &tv);
-  const uint32_t ridx = blk.run_off + block_exclusive_u32(new_run ? 1u : 0u, scan, &tr);
-  if (new_run) {
-    run_v[base + ridx] = e.v;
-    run_start[base + ridx] = eidx;
+  const uint32_t nblocks = (uint32_t)((seg[c + 1] - base + kBlockEntries - 1) / kBlockEntries);
+  const uint32_t b0 = blockIdx.x * kRunBlocks;
+  EntryLoad loads[kRunBlocks];
+#pragma unroll
+  for (uint32_t q = 0; q < kRunBlocks; ++q) loads[q] = load_entry(vals, seg, row_of, weights, b0 + q);
+#pragma unroll
+  for (uint32_t q = 0; q < kRunBlocks; ++q) {
+    const uint32_t bi = b0 + q;
+    if (bi >= nblocks) break;
+    const SkBlock blk = blocks[(uint64_t)c * max_blocks + bi];
+    bool has = false;
+    float first = 0.0f, last = 0.0f;
+    EntryView e = view_entry(loads[q], s_has, s_first, s_last, has, first, last);
+    if (!e.have_prev && blk.prev_has) { e.prev = blk.prev; e.have_prev = true; }
+    const bool new_run = e.valid && (!e.have_prev || e.v != e.prev);
+    uint32_t ev, er, tv, tr;
+    block_exclusive_u32x2(e.valid ? 1u : 0u, new_run ? 1u : 0u, scan, ev, er, tv, tr);
+    const uint32_t eidx = blk.elem_off + ev, ridx = blk.run_off + er;
+    if (new_run) {
+      keys[base + ridx] = order_key(e.v);
+      run_start[base + ridx] = eidx;
+    }
+    if (e.valid && weights) elem_w[base + eidx] = e.w;
   }
-  if (e.valid && weights) elem_w[base + eidx] = e.w;
 }
 
-// Each run's weight: its length (below 2^24) or, with weights, the binary32
-// sum of its entries' weights in row order (kernels/quantile.metal.h:19-140).
+// Each run's weight, the sort's payload: its length (below 2^24) or, with
+// weights, the binary32 sum of its entries' weights in row order
+// (kernels/quantile.metal.h:19-140).
 __global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
                               const uint32_t* __restrict__ run_start, const float* __restrict__ elem_w,
-                              float* __restrict__ run_w) {
+                              float* __restrict__ weight) {
   const uint32_t c = blockIdx.y;
   const uint64_t base = seg[c];
   const SkStats st = stats[c];
@@ -298,21 +366,7 @@ __global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* _
     w = elem_w[base + s];
     for (uint32_t i = s + 1; i < e; ++i) w = w + elem_w[base + i];
   }
-  run_w[base + k] = w;
-}
-
-// Sort keys (value order) and payloads (the run's weight) of every run: the
-// stable sort hands the summaries each batch's values and weights in value
-// order, contiguous, with equal values in run order.
-__global__ void k_sort_keys(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
-                            const float* __restrict__ run_v, const float* __restrict__ run_w,
-                            uint32_t* __restrict__ keys, float* __restrict__ weight) {
-  const uint32_t c = blockIdx.y;
-  const uint64_t base = seg[c];
-  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= stats[c].runs) return;
-  keys[base + k] = order_key(run_v[base + k]);
-  weight[base + k] = run_w[base + k];
+  weight[base + k] = w;
 }
 
 // Merges and prunes walk their inputs in tiles of a merge path (merge-path
@@ -828,31 +882,6 @@ __device__ uint32_t summarize(const uint32_t* __restrict__ keys, const float* __
   return n;
 }
 
-// Exclusive prefix sums of two values over the workgroup's threads, with
-// their totals.
-__device__ __forceinline__ void block_exclusive_u32x2(uint32_t a, uint32_t b, uint32_t* shared, uint32_t& ea,
-                                                      uint32_t& eb, uint32_t& ta, uint32_t& tb) {
-  const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
-  const uint32_t ia = wave_inclusive_u32(a), ib = wave_inclusive_u32(b);
-  if (lane == kWave - 1) { shared[2 * wave] = ia; shared[2 * wave + 1] = ib; }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t ra = 0, rb = 0;
-    for (uint32_t w = 0; w < waves; ++w) {
-      const uint32_t xa = shared[2 * w], xb = shared[2 * w + 1];
-      shared[2 * w] = ra; shared[2 * w + 1] = rb;
-      ra += xa; rb += xb;
-    }
-    shared[2 * waves] = ra; shared[2 * waves + 1] = rb;
-  }
-  __syncthreads();
-  ea = shared[2 * wave] + ia - a;
-  eb = shared[2 * wave + 1] + ib - b;
-  ta = shared[2 * waves];
-  tb = shared[2 * waves + 1];
-  __syncthreads();
-}
-
 // Summary of one sorted batch with integer weights summing below 2^24
 // (kernels/quantile.metal.h:216-240): value[g] is the g-th distinct value
 // and prefix[g] the weight of every run before it (prefix[n] the total), so
@@ -1186,7 +1215,7 @@ struct Arena {
 
 // Cuts of the features f0 .. f0 + nf - 1 whose entries are
 // vals[seg[c] .. seg[c + 1]) (device values; host offsets, seg[0] = 0), see
-// view_entry for the meaning of row_of and weights.
+// load_entry for the meaning of row_of and weights.
 int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint32_t* row_of, uint32_t nf, uint32_t f0,
                  const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
   hipStream_t s = stream();
@@ -1201,40 +1230,35 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   const uint64_t o_seg = a1.stage(seg);
   const uint64_t o_blocks = a1.reserve((uint64_t)nf * max_blocks * sizeof(SkBlock));
   const uint64_t o_stats = a1.reserve(nf * sizeof(SkStats));
-  const uint64_t o_run_v = a1.reserve(E * 4), o_run_w = a1.reserve(E * 4);
   const uint64_t o_region = a1.reserve(E * 16);
   const uint64_t o_keys_out = a1.reserve(E * 4), o_weight_out = a1.reserve(E * 4);
   if (a1.commit()) return -1;
   const uint64_t* seg_d = a1.at<uint64_t>(o_seg);
   SkBlock* blocks = a1.at<SkBlock>(o_blocks);
   SkStats* stats_d = a1.at<SkStats>(o_stats);
-  float* run_v = a1.at<float>(o_run_v);
-  float* run_w = a1.at<float>(o_run_w);
   uint32_t* keys_out = a1.at<uint32_t>(o_keys_out);
   uint32_t* weight_out = a1.at<uint32_t>(o_weight_out);
-  // One 16-byte-per-entry region: run starts, sort inputs and entry weights
-  // until the sort, then the summaries' and merges' work area.
+  // One 16-byte-per-entry region: run starts, the sort's keys and payloads
+  // and entry weights until the sort, then the summaries' and merges' work
+  // area.
   uint32_t* run_start = a1.at<uint32_t>(o_region);
   uint32_t* keys_in = run_start + E;
   uint32_t* weight_in = keys_in + E;
   float* elem_w = reinterpret_cast<float*>(weight_in + E);
   SkEntry* work = a1.at<SkEntry>(o_region);
-  const dim3 grid(max_blocks, nf);
-  hipLaunchKernelGGL(k_run_count, grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
+  const dim3 grid(max_blocks, nf), run_grid((max_blocks + kRunBlocks - 1) / kRunBlocks, nf);
+  hipLaunchKernelGGL(k_run_count, run_grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
                      max_blocks, blocks);
   MGB_LAUNCH_CHECK("k_run_count");
   hipLaunchKernelGGL(k_run_scan, dim3(nf), dim3(kSketchThreads), 0, s, seg_d, max_blocks,
                      blocks, stats_d);
   MGB_LAUNCH_CHECK("k_run_scan");
-  hipLaunchKernelGGL(k_run_emit, grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
-                     max_blocks, blocks, run_v, run_start, elem_w);
+  hipLaunchKernelGGL(k_run_emit, run_grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
+                     max_blocks, blocks, keys_in, run_start, elem_w);
   MGB_LAUNCH_CHECK("k_run_emit");
   hipLaunchKernelGGL(k_run_weights, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
-                     run_start, weights ? elem_w : nullptr, run_w);
+                     run_start, weights ? elem_w : nullptr, reinterpret_cast<float*>(weight_in));
   MGB_LAUNCH_CHECK("k_run_weights");
-  hipLaunchKernelGGL(k_sort_keys, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
-                     run_v, run_w, keys_in, reinterpret_cast<float*>(weight_in));
-  MGB_LAUNCH_CHECK("k_sort_keys");
   std::vector<SkStats> stats(nf);
   MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d, nf * sizeof(SkStats), hipMemcpyDeviceToHost, s));
   MGB_CHECK(hipStreamSynchronize(s));
