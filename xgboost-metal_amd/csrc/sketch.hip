@@ -15,7 +15,10 @@
 //     in-order binary32 sum of its entries' weights);
 //  3. the host plans batches of 2*limit runs (limit = sketch budget) from the
 //     per-feature counts;
-//  4. a segmented, stable radix sort orders every batch's runs by value;
+//  4. a segmented radix sort orders every batch by value: an exact feature's
+//     (unweighted, below 2^24 entries) as its runs' entries, keys alone --
+//     a value's weight, its runs' lengths summed, is its count in the batch;
+//     any other's as its runs, stably, carrying each run's weight;
 //  5. one workgroup per batch summarizes it (integer weights: its distinct
 //     values and weight prefixes) and prunes the summary to limit;
 //  6. the serial rule merges batch summaries through a stack of levels like a
@@ -305,14 +308,24 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_scan(const uint64_t* __r
   if (threadIdx.x == 0) stats[c] = SkStats{present, elements, runs, 0};
 }
 
-// The runs of each block at their scanned offsets: the sort key of the run's
-// value (order_key), run_start (element index within the feature) and, with
-// weights, each valid entry's weight at its element index.
+// Whether a feature's summaries are exact integer sums: unweighted, fewer
+// than 2^24 valid entries.  Such a feature's batch is sorted as its entries
+// (each of weight 1: a value's weight is its run lengths' sum, its count in
+// the batch) instead of as runs carrying their lengths.
+__host__ __device__ inline bool exact_feature(bool weighted, uint32_t elements) {
+  return !weighted && elements <= (1u << 24);
+}
+
+// The runs of each block at their scanned offsets: run_start (element index
+// within the feature) and the sort keys (order_key) -- of every valid entry at
+// its element index for an exact feature, else of each run at its run index
+// with, under weights, each valid entry's weight at its element index.
 __global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __restrict__ vals,
                                                              const uint64_t* __restrict__ seg,
                                                              const uint32_t* __restrict__ row_of,
                                                              const float* __restrict__ weights, uint32_t max_blocks,
                                                              const SkBlock* __restrict__ blocks,
+                                                             const SkStats* __restrict__ stats,
                                                              uint32_t* __restrict__ keys, uint32_t* __restrict__ run_start,
                                                              float* __restrict__ elem_w) {
   __shared__ uint32_t s_has[kSketchThreads / kWave], scan[2 * (kSketchThreads / kWave + 1)];
@@ -320,6 +333,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __rest
   const uint32_t c = blockIdx.y;
   const uint64_t base = seg[c];
   const uint32_t nblocks = (uint32_t)((seg[c + 1] - base + kBlockEntries - 1) / kBlockEntries);
+  const bool exact = exact_feature(weights != nullptr, stats[c].elements);
   const uint32_t b0 = blockIdx.x * kRunBlocks;
   EntryLoad loads[kRunBlocks];
 #pragma unroll
@@ -337,17 +351,20 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __rest
     uint32_t ev, er, tv, tr;
     block_exclusive_u32x2(e.valid ? 1u : 0u, new_run ? 1u : 0u, scan, ev, er, tv, tr);
     const uint32_t eidx = blk.elem_off + ev, ridx = blk.run_off + er;
-    if (new_run) {
-      keys[base + ridx] = order_key(e.v);
-      run_start[base + ridx] = eidx;
+    if (new_run) run_start[base + ridx] = eidx;
+    if (exact) {
+      if (e.valid) keys[base + eidx] = order_key(e.v);
+    } else {
+      if (new_run) keys[base + ridx] = order_key(e.v);
+      if (e.valid && weights) elem_w[base + eidx] = e.w;
     }
-    if (e.valid && weights) elem_w[base + eidx] = e.w;
   }
 }
 
 // Each run's weight, the sort's payload: its length (below 2^24) or, with
 // weights, the binary32 sum of its entries' weights in row order
-// (kernels/quantile.metal.h:19-140).
+// (kernels/quantile.metal.h:19-140).  Exact features sort their entries and
+// need none.
 __global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
                               const uint32_t* __restrict__ run_start, const float* __restrict__ elem_w,
                               float* __restrict__ weight) {
@@ -355,7 +372,7 @@ __global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* _
   const uint64_t base = seg[c];
   const SkStats st = stats[c];
   const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= st.runs) return;
+  if (k >= st.runs || exact_feature(elem_w != nullptr, st.elements)) return;
   const uint32_t s = run_start[base + k];
   const uint32_t e = k + 1 < st.runs ? run_start[base + k + 1] : st.elements;
   float w;
@@ -884,11 +901,12 @@ __device__ uint32_t summarize(const uint32_t* __restrict__ keys, const float* __
 
 // Summary of one sorted batch with integer weights summing below 2^24
 // (kernels/quantile.metal.h:216-240): value[g] is the g-th distinct value
-// and prefix[g] the weight of every run before it (prefix[n] the total), so
+// and prefix[g] the weight of every key before it (prefix[n] the total), so
 // the summary entry is (rmin, rmax, wmin) = (prefix[g], prefix[g + 1], their
 // difference) -- every binary32 partial sum is exact, so the prefix gives the
-// serial sums bit for bit.  Four consecutive runs per thread; scan needs
-// 2 (waves + 1) words.  Returns the number of distinct values.
+// serial sums bit for bit.  wts null: every weight is 1.  Four consecutive
+// keys per thread; scan needs 2 (waves + 1) words.  Returns the number of
+// distinct values.
 __device__ uint32_t summarize_exact(const uint32_t* __restrict__ keys, const float* __restrict__ wts, uint32_t size,
                                     float* __restrict__ value, uint32_t* __restrict__ prefix, uint32_t* scan) {
   constexpr uint32_t kPer = 4;
@@ -907,7 +925,7 @@ __device__ uint32_t summarize_exact(const uint32_t* __restrict__ keys, const flo
       const uint32_t i = i0 + u;
       const bool in = i < size;
       v[u] = in ? key_value(keys[i]) : 0.0f;
-      w[u] = in ? (uint32_t)wts[i] : 0u;
+      w[u] = in ? (wts ? (uint32_t)wts[i] : 1u) : 0u;
       start[u] = in && (i == 0 || v[u] != (u ? v[u - 1] : prev));
       groups += start[u] ? 1u : 0u;
       weight += w[u];
@@ -932,6 +950,32 @@ __device__ uint32_t summarize_exact(const uint32_t* __restrict__ keys, const flo
   return carry_g;
 }
 
+// Key range of each batch (table: feature, batch) in the sort's arrays: its
+// runs [b 2 limit, min((b + 1) 2 limit, runs)) for a feature sorted as runs;
+// the entries of those runs, from the first one's start to the next batch's
+// first start (or the last entry), for an exact feature.
+__global__ void k_batch_keys(const uint32_t* __restrict__ table, uint32_t count,
+                             const SkFeature* __restrict__ features, const SkStats* __restrict__ stats,
+                             const uint32_t* __restrict__ run_start, uint32_t* __restrict__ key_begin,
+                             uint32_t* __restrict__ key_end) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const uint32_t c = table[2 * i], b = table[2 * i + 1];
+  const SkFeature fe = features[c];
+  const SkStats st = stats[c];
+  const uint32_t base = (uint32_t)fe.base;
+  const uint64_t cap = 2ull * fe.limit;
+  const uint32_t rb = (uint32_t)((uint64_t)b * cap);
+  const uint32_t re = (uint32_t)std::min<uint64_t>((uint64_t)rb + cap, st.runs);
+  if (fe.exact) {
+    key_begin[i] = base + run_start[base + rb];
+    key_end[i] = base + (re == st.runs ? st.elements : run_start[base + re]);
+  } else {
+    key_begin[i] = base + rb;
+    key_end[i] = base + re;
+  }
+}
+
 // Level 0 of every feature's tree: one workgroup per batch summarizes the
 // batch's sorted runs into the feature's work area and prunes the summary to
 // `limit` entries (the serial rule's first step for each batch,
@@ -939,6 +983,8 @@ __device__ uint32_t summarize_exact(const uint32_t* __restrict__ keys, const flo
 __global__ __launch_bounds__(kMergeThreads) void k_level0(const uint32_t* __restrict__ table,
                                                            const SkFeature* __restrict__ features,
                                                            const SkStats* __restrict__ stats,
+                                                           const uint32_t* __restrict__ key_begin,
+                                                           const uint32_t* __restrict__ key_end,
                                                            const uint32_t* __restrict__ keys,
                                                            const float* __restrict__ wts, SkEntry* __restrict__ work,
                                                            SkEntry* __restrict__ tree, uint32_t* __restrict__ scratch,
@@ -946,20 +992,23 @@ __global__ __launch_bounds__(kMergeThreads) void k_level0(const uint32_t* __rest
   __shared__ MergeLds<kMergeThreads> L;
   const uint32_t c = table[2 * blockIdx.x], b = table[2 * blockIdx.x + 1];
   const SkFeature fe = features[c];
-  const uint64_t begin = (uint64_t)b * 2 * fe.limit;
-  const uint32_t runs = stats[c].runs;
-  const uint32_t size = (uint32_t)(runs - begin < 2ull * fe.limit ? runs - begin : 2ull * fe.limit);
-  SkEntry* summary = work + fe.base + begin;  // 16 bytes per run of the batch
+  const uint32_t kb = key_begin[blockIdx.x], size = key_end[blockIdx.x] - kb;
+  // The batch's summary takes the work area of its runs (16 bytes each); it
+  // has at most one entry per run.
+  const uint64_t rb = (uint64_t)b * 2 * fe.limit;
+  const uint32_t runs = (uint32_t)std::min<uint64_t>(2ull * fe.limit, stats[c].runs - rb);
+  SkEntry* summary = work + fe.base + rb;
   SkEntry* pruned = tree + fe.tree + (uint64_t)b * fe.limit;
   uint32_t m;
   if (fe.exact) {
-    // Values and weight prefixes (2 size + 1 words) instead of 16-byte entries.
+    // Sorted entries of weight 1: values and weight prefixes (at most
+    // 2 runs + 1 words) instead of 16-byte entries.
     float* value = reinterpret_cast<float*>(summary);
-    uint32_t* prefix = reinterpret_cast<uint32_t*>(summary) + size;
-    const uint32_t n = summarize_exact(keys + fe.base + begin, wts + fe.base + begin, size, value, prefix, L.scan);
+    uint32_t* prefix = reinterpret_cast<uint32_t*>(summary) + runs;
+    const uint32_t n = summarize_exact(keys + kb, nullptr, size, value, prefix, L.scan);
     m = prune(ExactSummary{value, prefix}, n, fe.limit, pruned, L);
   } else {
-    const uint32_t n = summarize(keys + fe.base + begin, wts + fe.base + begin, size, summary,
+    const uint32_t n = summarize(keys + kb, wts + kb, size, summary,
                                  scratch + fe.scratch + (uint64_t)b * (2 * fe.limit + 2), L.scan);
     m = prune(EntryArray{summary}, n, fe.limit, pruned, L);
   }
@@ -1254,7 +1303,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
                      blocks, stats_d);
   MGB_LAUNCH_CHECK("k_run_scan");
   hipLaunchKernelGGL(k_run_emit, run_grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
-                     max_blocks, blocks, keys_in, run_start, elem_w);
+                     max_blocks, blocks, stats_d, keys_in, run_start, elem_w);
   MGB_LAUNCH_CHECK("k_run_emit");
   hipLaunchKernelGGL(k_run_weights, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
                      run_start, weights ? elem_w : nullptr, reinterpret_cast<float*>(weight_in));
@@ -1263,9 +1312,10 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   MGB_CHECK(hipMemcpyAsync(stats.data(), stats_d, nf * sizeof(SkStats), hipMemcpyDeviceToHost, s));
   MGB_CHECK(hipStreamSynchronize(s));
 
-  // Batch plan (src/quantile.cpp:87-122) and tree layout.
+  // Batch plan (src/quantile.cpp:87-122) and tree layout.  table0 lists the
+  // exact features' batches first: their entries are sorted as keys alone.
   std::vector<SkFeature> features(nf);
-  std::vector<uint32_t> seg_begin, seg_end, table0;
+  std::vector<uint32_t> table0, table0_runs;
   std::vector<std::vector<uint32_t>> tables;  // levels 1, 2, ...
   uint64_t tree_total = 0, scratch_total = 0, fin_total = 0;
   uint32_t node_total = 0;
@@ -1278,7 +1328,7 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
     const uint64_t capacity = 2ull * fe.limit;
     fe.batches = (uint32_t)((st.runs + capacity - 1) / capacity);
     fe.levels = bit_width(std::max(1u, fe.batches)) + 1;
-    fe.exact = !weights && st.elements <= (1u << 24);
+    fe.exact = exact_feature(weights != nullptr, st.elements) ? 1u : 0u;
     fe.final_cap = std::max(fe.budget, fe.limit);
     const uint32_t nodes = level_first(fe.batches, 32);
     fe.node_base = node_total;
@@ -1289,12 +1339,10 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
     tree_total += (uint64_t)nodes * fe.limit;
     scratch_total += (uint64_t)fe.batches * (2ull * fe.limit + 2);
     fin_total += 2 * (2ull * fe.final_cap + 2) + (uint64_t)(fe.levels + 1) * fe.limit;
+    std::vector<uint32_t>& t0 = fe.exact ? table0 : table0_runs;
     for (uint32_t b = 0; b < fe.batches; ++b) {
-      const uint64_t begin = (uint64_t)b * capacity;
-      seg_begin.push_back((uint32_t)(seg[c] + begin));
-      seg_end.push_back((uint32_t)(seg[c] + std::min<uint64_t>(st.runs, begin + capacity)));
-      table0.push_back(c);
-      table0.push_back(b);
+      t0.push_back(c);
+      t0.push_back(b);
     }
     for (uint32_t level = 1; (fe.batches >> level) != 0; ++level) {
       if (tables.size() < level) tables.emplace_back();
@@ -1305,14 +1353,22 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
     }
     features[c] = fe;
   }
-  size_t temp_bytes = 0;
-  if (!seg_begin.empty())
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_bytes, keys_in, keys_out, weight_in, weight_out,
-                                                           (int)total, (int)seg_begin.size(), (const uint32_t*)nullptr,
+  const uint32_t exact_batches = (uint32_t)(table0.size() / 2);
+  table0.insert(table0.end(), table0_runs.begin(), table0_runs.end());
+  const uint32_t batches = (uint32_t)(table0.size() / 2), run_batches = batches - exact_batches;
+  size_t temp_keys = 0, temp_pairs = 0;
+  if (exact_batches)
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortKeys(nullptr, temp_keys, keys_in, keys_out, (int)total,
+                                                          (int)exact_batches, (const uint32_t*)nullptr,
+                                                          (const uint32_t*)nullptr, 0, 32, s));
+  if (run_batches)
+    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, temp_pairs, keys_in, keys_out, weight_in, weight_out,
+                                                           (int)total, (int)run_batches, (const uint32_t*)nullptr,
                                                            (const uint32_t*)nullptr, 0, 32, s));
+  size_t temp_bytes = std::max(temp_keys, temp_pairs);
   Arena a2;
   const uint64_t o_features = a2.stage(features), o_table0 = a2.stage(table0);
-  const uint64_t o_seg_b = a2.stage(seg_begin), o_seg_e = a2.stage(seg_end);
+  const uint64_t o_key_b = a2.reserve((uint64_t)batches * 4), o_key_e = a2.reserve((uint64_t)batches * 4);
   std::vector<uint64_t> o_tables(tables.size());
   for (size_t l = 0; l < tables.size(); ++l) o_tables[l] = a2.stage(tables[l]);
   uint32_t max_budget = 1;
@@ -1328,15 +1384,22 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   uint32_t* node_count = a2.at<uint32_t>(o_node_count);
   uint32_t* serial = a2.at<uint32_t>(o_serial);
   MGB_CHECK(hipMemsetAsync(serial, 0, nf * 4, s));
-  if (!seg_begin.empty()) {
-    MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out, weight_in,
-                                                           weight_out, (int)total, (int)seg_begin.size(),
-                                                           a2.at<uint32_t>(o_seg_b), a2.at<uint32_t>(o_seg_e), 0, 32,
-                                                           s));
-    hipLaunchKernelGGL(k_level0, dim3((uint32_t)seg_begin.size()), dim3(kMergeThreads), 0, s,
-                       a2.at<uint32_t>(o_table0), features_d, stats_d, keys_out,
-                       reinterpret_cast<const float*>(weight_out), work, tree, scratch,
-                       node_count);
+  if (batches) {
+    uint32_t* key_b = a2.at<uint32_t>(o_key_b);
+    uint32_t* key_e = a2.at<uint32_t>(o_key_e);
+    hipLaunchKernelGGL(k_batch_keys, dim3((batches + 255) / 256), dim3(256), 0, s, a2.at<uint32_t>(o_table0), batches,
+                       features_d, stats_d, run_start, key_b, key_e);
+    MGB_LAUNCH_CHECK("k_batch_keys");
+    if (exact_batches)
+      MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortKeys(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out,
+                                                            (int)total, (int)exact_batches, key_b, key_e, 0, 32, s));
+    if (run_batches)
+      MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out,
+                                                             weight_in, weight_out, (int)total, (int)run_batches,
+                                                             key_b + exact_batches, key_e + exact_batches, 0, 32, s));
+    hipLaunchKernelGGL(k_level0, dim3(batches), dim3(kMergeThreads), 0, s, a2.at<uint32_t>(o_table0), features_d,
+                       stats_d, key_b, key_e, keys_out, reinterpret_cast<const float*>(weight_out), work, tree,
+                       scratch, node_count);
     MGB_LAUNCH_CHECK("k_level0");
   }
   // Levels with many nodes run four 256-thread workgroups per CU; the last
