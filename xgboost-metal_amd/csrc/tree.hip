@@ -1489,19 +1489,19 @@ __device__ Cand make_cand(const NodeEval& n, const SplitRec& r, uint32_t feature
   return c;
 }
 
-// Serial binary64 sums of `steps` bins of a feature staged in LDS (forward
-// from bin 0, or backward from bin count-1), in the reference's order.
-__device__ void ordered_sum(const double* sg, const double* sh, uint32_t steps, bool reverse, uint32_t count,
-                            double* g, double* h) {
-  double a = 0, b = 0;
+// Serial binary64 sum of `steps` staged values (forward from index 0, or
+// backward from count-1), in the reference's order.  Every lane of the
+// calling wave runs the same chain (same LDS words: broadcast reads).
+__device__ double serial_sum(const double* v, uint32_t steps, bool reverse, uint32_t count) {
+  double a = 0;
+  if (!reverse) {
 #pragma unroll 16
-  for (uint32_t s = 0; s < steps; ++s) {
-    uint32_t bin = reverse ? count - s - 1 : s;
-    a += sg[bin];
-    b += sh[bin];
+    for (uint32_t s = 0; s < steps; ++s) a += v[s];
+  } else {
+#pragma unroll 16
+    for (uint32_t s = 0; s < steps; ++s) a += v[count - 1 - s];
   }
-  *g = a;
-  *h = b;
+  return a;
 }
 
 // Largest max_bin of the tree kernels: the dense root's select stages 4096 + 1
@@ -1560,6 +1560,10 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   float* rootcut = reinterpret_cast<float*>(rootfh + t.bins1);
   const bool dense_root = depth == 0 && t.dense && n > 0;
   __shared__ uint32_t s_left[kPlanNodes];  // count_plans: each node's left rows
+  __shared__ double s_root[4];             // dense root: feature 0's ordered sums, the chosen child's
+  __shared__ Frontier s_node;              // dense root: the root's frontier entry,
+  __shared__ NodeEval s_ne;                // its totals
+  __shared__ Cand s_best;                  // and its best candidate
   if (plan_next && count_plans) {
     // Sums over every task; only split nodes' sums are read (a leaf's tasks
     // keep older counts).
@@ -1578,6 +1582,48 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
     stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, cf, eg, eh, rootfg, rootfh);
     for (uint32_t b = threadIdx.x; b < cf; b += blockDim.x) rootcut[b] = t.cuts[(uint64_t)f * t.cut_stride + b];
     __syncthreads();
+    // The root's ordered sums (kernels/scalar_root.metal.h:1-105), four
+    // serial chains on four waves at once: feature 0's g and h over all its
+    // bins (waves 0, 1), and g and h over the chosen child's bin range of the
+    // root's best candidate (waves 2, 3; rebuilt here exactly as the node loop
+    // below builds it).
+    static_assert(kPartThreads >= 4 * kWave, "the root's four sums take four waves");
+    const uint32_t chain = threadIdx.x / kWave;
+    if (chain < 4) {
+      double sum = 0;
+      if (chain < 2) {
+        sum = serial_sum(chain == 0 ? root0g : root0h, t.counts[0], false, t.counts[0]);
+      } else {
+        const Frontier node = fr[0];
+        NodeEval ne;
+        node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p, node.lower, node.upper, 0);
+        Cand best;
+        best.feature = -1;
+        best.gain = -INFINITY;
+        if (key) best = make_cand(ne, t.recs[f], f, cf, t.cuts + (uint64_t)f * t.cut_stride, eg, eh, p);
+        if (threadIdx.x == 2 * kWave) {
+          s_node = node;
+          s_ne = ne;
+          s_best = best;
+        }
+        if (best.feature >= 0 && (uint32_t)best.feature < F) {
+          uint32_t lo = 0, hi = cf;
+          while (lo < hi) {
+            uint32_t mid = lo + (hi - lo) / 2;
+            if (rootcut[mid] < best.threshold) lo = mid + 1;
+            else hi = mid;
+          }
+          uint32_t steps = lo + 1 < cf ? lo + 1 : cf;
+          if (best.default_left) {
+            uint32_t bin = best.threshold == -INFINITY ? 0 : lo + 1;
+            steps = bin < cf ? cf - bin : 0;
+          }
+          sum = serial_sum(chain == 2 ? rootfg : rootfh, steps, best.default_left != 0, cf);
+        }
+      }
+      if (lane_id() == 0) s_root[chain] = sum;
+    }
+    __syncthreads();
   }
   uint32_t carry_expanded = 0, carry_htasks = 0, carry_zero = 0, carry_rows = 0, carry_ptasks = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
@@ -1588,45 +1634,37 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
     float applied_w = 0, applied_h = 0, parent_w = 0, total_h = 0;
     Frontier node;
     if (valid) {
-      node = fr[i];
-      const uint64_t key = best_keys[i];
       NodeEval ne;
-      node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p, node.lower, node.upper, 0);
+      if (dense_root) {
+        // The root (i = 0): node, totals and candidate as the sums' pre-pass
+        // built them.
+        node = s_node;
+        ne = s_ne;
+        best = s_best;
+      } else {
+        node = fr[i];
+        const uint64_t key = best_keys[i];
+        node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p, node.lower, node.upper, 0);
+        best.feature = -1;
+        best.gain = -INFINITY;
+        if (key) {
+          const uint32_t f = ~(uint32_t)key;
+          best = make_cand(ne, t.recs[(uint64_t)i * F + f], f, t.counts[f], t.cuts + (uint64_t)f * t.cut_stride, eg,
+                           eh, p);
+        }
+      }
       parent_w = ne.w;
       total_h = (float)ne.H;
-      best.feature = -1;
-      best.gain = -INFINITY;
-      if (key) {
-        const uint32_t f = ~(uint32_t)key;
-        best = make_cand(ne, t.recs[(uint64_t)i * F + f], f, t.counts[f], t.cuts + (uint64_t)f * t.cut_stride, eg, eh,
-                         p);
-      }
       expand = best.feature >= 0 && (uint32_t)best.feature < F && best.gain > 1.0e-6f &&
                best.gain >= p.min_split_loss && depth < t.max_depth;
       if (dense_root) {
         // Dense root: ordered binary64 sums of feature 0's bins, and of the
-        // chosen child's bin range (kernels/scalar_root.metal.h:1-105).
-        const uint32_t c0 = t.counts[0];
-        double tg, th;
-        ordered_sum(root0g, root0h, c0, false, c0, &tg, &th);
+        // chosen child's bin range (wave 0 took them above).
+        const double tg = s_root[0], th = s_root[1];
         parent_w = clamp_weight(calc_weight(tg, th, p), node.lower, node.upper);
         total_h = (float)th;
         if (best.feature >= 0 && (uint32_t)best.feature < F) {
-          // best.feature is the root's best-key feature, staged in rootcut.
-          const uint32_t f = (uint32_t)best.feature, count = t.counts[f];
-          uint32_t lo = 0, hi = count;
-          while (lo < hi) {
-            uint32_t mid = lo + (hi - lo) / 2;
-            if (rootcut[mid] < best.threshold) lo = mid + 1;
-            else hi = mid;
-          }
-          uint32_t steps = lo + 1 < count ? lo + 1 : count;
-          if (best.default_left) {
-            uint32_t bin = best.threshold == -INFINITY ? 0 : lo + 1;
-            steps = bin < count ? count - bin : 0;
-          }
-          double cg, ch;
-          ordered_sum(rootfg, rootfh, steps, best.default_left != 0, count, &cg, &ch);
+          const double cg = s_root[2], ch = s_root[3];
           double og = tg - cg, oh = th - ch;
           double ag = cg + og, ah = ch + oh;
           applied_w = clamp_weight(calc_weight(ag, ah, p), node.lower, node.upper);
