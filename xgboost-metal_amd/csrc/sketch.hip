@@ -10,9 +10,10 @@
 //  2. runs of equal values in row order over each feature's non-missing,
 //     nonzero-weight entries, in 1024-entry blocks: per-block counts, a
 //     per-feature scan over blocks that joins runs crossing block edges, the
-//     runs written at their scanned offsets as sort keys of their values,
-//     then each run's weight as the sort's payload (its length, or the
-//     in-order binary32 sum of its entries' weights);
+//     run starts written at their scanned offsets with the sort keys (an exact
+//     feature's every entry, any other's each run), then each run's weight
+//     as the sort's payload (its length, or the in-order binary32 sum of its
+//     entries' weights);
 //  3. the host plans batches of 2*limit runs (limit = sketch budget) from the
 //     per-feature counts;
 //  4. a segmented radix sort orders every batch by value: an exact feature's
@@ -30,10 +31,11 @@
 //  7. one workgroup per feature merges the tree's roots (the stack's final
 //     contents), prunes to the budget and selects the cuts.
 // Summaries, prunes and merges are data-parallel restatements of the serial
-// rules: prune positions come from binary searches over monotone rank sums,
-// merges from merge-path ranks, the error fix-up from prefix maxima, and
-// sequential binary32 sums stay sequential, so every rounding step is the
-// same operation on the same operands.
+// rules: merges and prunes walk merge-path tiles staged in LDS (a prune is
+// the merge of its nondecreasing ranks with the summary's monotone rank
+// sums), the error fix-up is a prefix maximum, and sequential binary32 sums
+// stay sequential, so every rounding step is the same operation on the same
+// operands.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
