@@ -11,7 +11,9 @@ not depend on the oracle finishing (it would take hours there):
   threshold is one of its feature's cuts.
 
 Config 2 at full size is pinned by the reference's published prediction
-hash (test_gpu_parity.py::test_published_prediction_hashes)."""
+hash (test_gpu_parity.py::test_published_prediction_hashes) and the oracle;
+the quantile sketch beyond 2^24 entries a feature (where integer weight sums
+stop being exact) is checked against the oracle."""
 import json
 
 import numpy as np
@@ -101,3 +103,22 @@ def test_config2_full_size_matches_oracle(xgb):
     ref = O.train(X, y, O.make_params(max_depth=8, max_bin=256, eta=0.3, nthread=threads), 10)
     got = bst.predict(xgb.DMatrix(X), output_margin=True)
     np.testing.assert_array_equal(got.view(np.uint32), ref["margin"].view(np.uint32))
+
+
+def test_sketch_beyond_exact_integer_sums():
+    """Unweighted features with more than 2^24 entries leave the exact path:
+    their batches are sorted as runs carrying their lengths and summarized with
+    serial binary32 sums (the weighted path's rules). One continuous feature
+    and one of 64-row runs over 50 values, against the oracle bit for bit."""
+    import device_lib as D
+    import oracle_lib as O
+    n = (1 << 24) + 200000
+    rng = np.random.default_rng(7)
+    X = np.empty((n, 2), np.float32)
+    X[:, 0] = rng.normal(size=n).astype(np.float32)
+    X[:, 1] = np.repeat(rng.integers(0, 50, size=n // 64 + 1), 64)[:n].astype(np.float32)
+    cuts, counts = D.sketch_cuts(X, 256)
+    ocuts, ocounts, _ = O.sketch_cuts(X, 256)
+    np.testing.assert_array_equal(counts, ocounts)
+    for f in range(X.shape[1]):
+        np.testing.assert_array_equal(cuts[f, :counts[f]].view(np.uint32), ocuts[f, :counts[f]].view(np.uint32))
