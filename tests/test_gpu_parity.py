@@ -275,6 +275,34 @@ def _csr(indptr, indices, values, cols):
     return sp.csr_matrix((values, indices, indptr), shape=(len(indptr) - 1, cols))
 
 
+def test_csr_sketch_feature_groups_match_oracle(xgb):
+    """The CSR sketch (from the column-major copy) over groups of a few
+    hundred entries -- whole columns per group, so many groups -- gives the
+    oracle's cuts, as the default single group does."""
+    cols = 300
+    indptr, indices, values, _ = W.config3(rows=12000, cols=cols, nnz=20, informative=40, seed=23)
+    X = W.csr_to_dense(indptr, indices, values, cols)
+    y = np.nan_to_num(X[:, :40]).sum(axis=1).astype(np.float32)
+    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 4, "max_bin": 256}
+    ref = O.train(X, y, _oracle_params(params), 1)
+    lib = xgb.core._LIB
+    for entries in (2000, 0):
+        assert lib.mgb_sketch_group_entries(ctypes.c_uint64(entries)) == 0
+        try:
+            d = xgb.DMatrix(_csr(indptr, indices, values, cols), label=y)
+            bst = xgb.train(params, d, 1)
+            cut_ptr, cut_values = d.get_quantile_cut()
+        finally:
+            lib.mgb_sketch_group_entries(ctypes.c_uint64(0))
+        np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+        for f in range(cols):
+            c = ref["cut_counts"][f]
+            np.testing.assert_array_equal(cut_values[cut_ptr[f]:cut_ptr[f + 1]].view(np.uint32),
+                                          ref["cuts"][f, :c].view(np.uint32))
+        assert_trees_equal(bst, ref)
+
+
+
 @pytest.mark.parametrize("max_bin,root_columns", [(64, 1), (256, 1), (1024, 1), (256, 0)])
 def test_csr_regression_matches_oracle(xgb, max_bin, root_columns):
     """Squared error on a config-3 style CSR matrix: cuts, trees and margins
