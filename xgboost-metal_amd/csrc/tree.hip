@@ -1235,6 +1235,38 @@ __device__ __forceinline__ float item_max_f32(float v, float* xchg, uint32_t wav
   return v;
 }
 
+// Both children's maxima with one barrier (W > 1).
+template <int W>
+__device__ __forceinline__ void item_max2_f32(float& a, float& b, float* xa, float* xb, uint32_t wave_in_item) {
+  a = wave_max_f32(a);
+  b = wave_max_f32(b);
+  if constexpr (W > 1) {
+    if (lane_id() == 0) { xa[wave_in_item] = a; xb[wave_in_item] = b; }
+    __syncthreads();
+    a = xa[0];
+    b = xb[0];
+    for (uint32_t k = 1; k < (uint32_t)W; ++k) { a = fmaxf(a, xa[k]); b = fmaxf(b, xb[k]); }
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void item_max2_u64(uint64_t& a, uint64_t& b, uint64_t* xa, uint64_t* xb,
+                                              uint32_t wave_in_item) {
+  a = wave_max_u64(a);
+  b = wave_max_u64(b);
+  if constexpr (W > 1) {
+    if (lane_id() == 0) { xa[wave_in_item] = a; xb[wave_in_item] = b; }
+    __syncthreads();
+    a = uniform_u64(xa[0]);
+    b = uniform_u64(xb[0]);
+    for (uint32_t k = 1; k < (uint32_t)W; ++k) {
+      const uint64_t oa = uniform_u64(xa[k]), ob = uniform_u64(xb[k]);
+      a = oa > a ? oa : a;
+      b = ob > b ? ob : b;
+    }
+  }
+}
+
 template <int W>
 __device__ __forceinline__ uint64_t item_max_u64(uint64_t v, uint64_t* xchg, uint32_t wave_in_item) {
   v = wave_max_u64(v);
@@ -1250,32 +1282,26 @@ __device__ __forceinline__ uint64_t item_max_u64(uint64_t v, uint64_t* xchg, uin
   return v;
 }
 
-// Scores one node's candidates held by this lane (bins b0 .. b0+CH-1,
-// in-lane inclusive sums in `lb`, item-exclusive prefix pre_g/pre_h):
-// division-free bounds first, then the exact scorer for every candidate whose
-// upper bound reaches the node's best certain lower bound.  The winner (if
-// any) records its SplitRec and offers its feature to the node's best key.
-template <int W, int CH>
-__device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, uint64_t pre_g, uint64_t pre_h, uint32_t b0,
-                                           uint32_t count, int eg, int eh, float mcw, bool filter, float lambda,
-                                           const MgbSplitParams& p, float* xf, uint64_t* xk, uint32_t wave_in_item,
-                                           SplitRec* rec, unsigned long long* node_best, uint32_t feature,
-                                           uint32_t cols) {
-  float hi_f[CH], hi_b[CH];
-  float lo = -INFINITY;
+// Division-free upper bounds of the lane's candidates (bin j forward and
+// backward) and the lane's best certain lower bound.
+template <int CH>
+__device__ __forceinline__ void bound_lane(const NodeEval& n, const LaneBins<CH>& lb, uint64_t pre_g, uint64_t pre_h,
+                                           uint32_t b0, uint32_t count, int eg, int eh, float mcw, bool filter,
+                                           float lambda, float (&hi_f)[CH], float (&hi_b)[CH], float& lo) {
+  lo = -INFINITY;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const uint64_t vg = lb.g[j] - (j ? lb.g[j - 1] : 0), vh = lb.h[j] - (j ? lb.h[j - 1] : 0);
     bound_bin(n, vg, vh, pre_g + lb.g[j], pre_h + lb.h[j], b0 + j, count, eg, eh, mcw, filter, lambda, hi_f[j],
               hi_b[j], lo);
   }
-  const float node_lo = item_max_f32<W>(lo, xf, wave_in_item);
-  // The candidates whose upper bound reaches the node's best lower bound, as
-  // a mask (bit 2j: bin j forward, 2j+1: backward), scored exactly one at a
-  // time.  One inlined copy of the binary64 scorer instead of one per bin and
-  // direction keeps the kernel's code within the instruction cache; the
-  // scorer keeps the best by (gain, lowest order), so the visiting order does
-  // not matter.
+}
+
+// The candidates whose upper bound reaches the node's best lower bound, as a
+// mask (bit 2j: bin j forward, 2j+1: backward).
+template <int CH>
+__device__ __forceinline__ uint32_t survivors(const NodeEval& n, const float (&hi_f)[CH], const float (&hi_b)[CH],
+                                              float node_lo, uint32_t b0, uint32_t count) {
   uint32_t mask = 0;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
@@ -1283,6 +1309,17 @@ __device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, 
     if (hi_f[j] > -INFINITY && hi_f[j] >= node_lo) mask |= 1u << (2 * j);
     if (n.has_missing && hi_b[j] > -INFINITY && hi_b[j] >= node_lo) mask |= 2u << (2 * j);
   }
+  return mask;
+}
+
+// Scores the surviving candidates exactly, one at a time.  One inlined copy
+// of the binary64 scorer instead of one per bin and direction keeps the
+// kernel's code within the instruction cache; the scorer keeps the best by
+// (gain, lowest order), so the visiting order does not matter.
+template <int CH>
+__device__ __forceinline__ void score_survivors(NodeEval& n, const LaneBins<CH>& lb, uint64_t pre_g, uint64_t pre_h,
+                                                uint32_t b0, uint32_t count, int eg, int eh, float mcw,
+                                                const MgbSplitParams& p, uint32_t mask) {
   while (mask) {
     const uint32_t k = (uint32_t)__builtin_ctz(mask);
     mask &= mask - 1;
@@ -1303,8 +1340,12 @@ __device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, 
     const uint64_t lh = backward ? n.th - (n.ph - (pre_h + xh)) : pre_h + ih;
     try_candidate(n, lg, lh, backward ? 2 * count - 1 - b : b, eg, eh, mcw, p);
   }
-  const uint64_t mine = candidate_key(n);
-  const uint64_t top = item_max_u64<W>(mine, xk, wave_in_item);
+}
+
+// The item's winner (the lane holding the largest key) records its SplitRec
+// and offers its feature to the node's best key.
+__device__ __forceinline__ void offer_best(const NodeEval& n, uint64_t mine, uint64_t top, SplitRec* rec,
+                                           unsigned long long* node_best, uint32_t feature, uint32_t cols) {
   if (top != 0 && mine == top) {
     *rec = SplitRec{n.best_gain, n.best_order, (int64_t)n.best_lg, (int64_t)n.best_lh};
     // With many features a node's items serialize on its one key (2,000
@@ -1316,6 +1357,48 @@ __device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, 
     if (cols < kContendedFeatures || key > __hip_atomic_load(node_best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
       atomicMax(node_best, key);
   }
+}
+
+// Scores one node's candidates held by this lane (bins b0 .. b0+CH-1,
+// in-lane inclusive sums in `lb`, item-exclusive prefix pre_g/pre_h):
+// division-free bounds first, then the exact scorer for every candidate whose
+// upper bound reaches the node's best certain lower bound.  The winner (if
+// any) records its SplitRec and offers its feature to the node's best key.
+template <int W, int CH>
+__device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, uint64_t pre_g, uint64_t pre_h, uint32_t b0,
+                                           uint32_t count, int eg, int eh, float mcw, bool filter, float lambda,
+                                           const MgbSplitParams& p, float* xf, uint64_t* xk, uint32_t wave_in_item,
+                                           SplitRec* rec, unsigned long long* node_best, uint32_t feature,
+                                           uint32_t cols) {
+  float hi_f[CH], hi_b[CH], lo;
+  bound_lane<CH>(n, lb, pre_g, pre_h, b0, count, eg, eh, mcw, filter, lambda, hi_f, hi_b, lo);
+  const float node_lo = item_max_f32<W>(lo, xf, wave_in_item);
+  score_survivors<CH>(n, lb, pre_g, pre_h, b0, count, eg, eh, mcw, p, survivors<CH>(n, hi_f, hi_b, node_lo, b0, count));
+  const uint64_t mine = candidate_key(n);
+  offer_best(n, mine, item_max_u64<W>(mine, xk, wave_in_item), rec, node_best, feature, cols);
+}
+
+// Both children of a pair, with one barrier per exchange (W > 1) instead of
+// one per child.
+template <int W, int CH>
+__device__ __forceinline__ void score_pair(NodeEval& na, const LaneBins<CH>& la, uint64_t pga, uint64_t pha,
+                                           SplitRec* reca, unsigned long long* besta, NodeEval& nb,
+                                           const LaneBins<CH>& lb, uint64_t pgb, uint64_t phb, SplitRec* recb,
+                                           unsigned long long* bestb, uint32_t b0, uint32_t count, int eg, int eh,
+                                           float mcw, bool filter, float lambda, const MgbSplitParams& p,
+                                           float* xfa, float* xfb, uint64_t* xka, uint64_t* xkb,
+                                           uint32_t wave_in_item, uint32_t feature, uint32_t cols) {
+  float ha_f[CH], ha_b[CH], hb_f[CH], hb_b[CH], loa, lob;
+  bound_lane<CH>(na, la, pga, pha, b0, count, eg, eh, mcw, filter, lambda, ha_f, ha_b, loa);
+  bound_lane<CH>(nb, lb, pgb, phb, b0, count, eg, eh, mcw, filter, lambda, hb_f, hb_b, lob);
+  item_max2_f32<W>(loa, lob, xfa, xfb, wave_in_item);
+  score_survivors<CH>(na, la, pga, pha, b0, count, eg, eh, mcw, p, survivors<CH>(na, ha_f, ha_b, loa, b0, count));
+  score_survivors<CH>(nb, lb, pgb, phb, b0, count, eg, eh, mcw, p, survivors<CH>(nb, hb_f, hb_b, lob, b0, count));
+  const uint64_t minea = candidate_key(na), mineb = candidate_key(nb);
+  uint64_t topa = minea, topb = mineb;
+  item_max2_u64<W>(topa, topb, xka, xkb, wave_in_item);
+  offer_best(na, minea, topa, reca, besta, feature, cols);
+  offer_best(nb, mineb, topb, recb, bestb, feature, cols);
 }
 
 // ---------------------------------------------------------------------------
@@ -1449,12 +1532,24 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   const int32_t mono = t.monotone ? t.monotone[f] : 0;
   node_begin(ex, (uint64_t)fb.sum_g, (uint64_t)fb.sum_h, xmg, xmh, eg, eh, t.sp, fb.lower, fb.upper, mono);
   node_begin(eo, (uint64_t)fo.sum_g, (uint64_t)fo.sum_h, omg, omh, eg, eh, t.sp, fo.lower, fo.upper, mono);
-  score_node<W, CH>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
-                xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f, best_bank(t, depth) + built, f,
-                t.cols);
-  score_node<W, CH>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
-                xkey[slot_in_block][1], wave_in_item, t.recs + (uint64_t)other * F + f, best_bank(t, depth) + other, f,
-                t.cols);
+  if constexpr (W > 1 && CH > 1) {
+    // Several waves and bins per lane: both children share each exchange's
+    // barrier (C4's wide levels: split 1.374 -> 1.352 ms per round).  With
+    // one wave per item there is no barrier to share, and with one bin per
+    // lane the pair's longer live ranges cost more than the barrier saves
+    // (C2: 39.2 -> 40.2 ms per fit).
+    score_pair<W, CH>(ex, x, pre[0], pre[1], t.recs + (uint64_t)built * F + f, best_bank(t, depth) + built, eo, o,
+                      pre[2], pre[3], t.recs + (uint64_t)other * F + f, best_bank(t, depth) + other, b0, count, eg, eh,
+                      mcw, filter, lambda, t.sp, xlo[slot_in_block][0], xlo[slot_in_block][1], xkey[slot_in_block][0],
+                      xkey[slot_in_block][1], wave_in_item, f, t.cols);
+  } else {
+    score_node<W, CH>(ex, x, pre[0], pre[1], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][0],
+                      xkey[slot_in_block][0], wave_in_item, t.recs + (uint64_t)built * F + f,
+                      best_bank(t, depth) + built, f, t.cols);
+    score_node<W, CH>(eo, o, pre[2], pre[3], b0, count, eg, eh, mcw, filter, lambda, t.sp, xlo[slot_in_block][1],
+                      xkey[slot_in_block][1], wave_in_item, t.recs + (uint64_t)other * F + f,
+                      best_bank(t, depth) + other, f, t.cols);
+  }
 }
 
 // ---------------------------------------------------------------------------
