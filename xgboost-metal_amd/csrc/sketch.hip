@@ -55,7 +55,7 @@ constexpr uint32_t kRunBlocks = 8;                       // consecutive blocks p
 constexpr uint64_t kGroupBytesPerEntry = 64;              // a group's temporaries per entry (typical)
 constexpr uint64_t kMaxGroupEntries = (uint64_t(1) << 31) - 1;  // 32-bit positions; the sort counts in int
 constexpr uint32_t kMaxGroupFeatures = 65535;            // features per group
-constexpr uint32_t kFinishLds = 96 * 1024;               // k_finish's staging LDS, at most
+constexpr uint32_t kMaxBinSketch = 4096;                 // cut candidates per feature, at most
 
 struct SkEntry { float rmin, rmax, wmin, value; };
 struct SkStats { uint32_t nonmissing, elements, runs, padding; };
@@ -1062,16 +1062,14 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
                                                            const uint32_t* __restrict__ node_count,
                                                            const uint32_t* __restrict__ serial,
                                                            SkEntry* __restrict__ fin,
-                                                           uint32_t f0, uint32_t max_bin, float* __restrict__ cut_values,
-                                                           uint32_t lds_values, float* __restrict__ cuts,
+                                                           uint32_t f0, uint32_t max_bin, uint32_t* __restrict__ picks,
+                                                           float* __restrict__ cuts,
                                                            uint32_t* __restrict__ counts) {
   __shared__ uint32_t level_count[64];
-  // The merges' LDS; once the last prune is done, the same bytes stage
-  // lds_values summary values, then max_bin candidate cuts (nothing when
-  // lds_values is 0).
+  __shared__ uint32_t s_scan[kSketchThreads / kWave + 1];
+  __shared__ uint32_t s_stop;
   extern __shared__ __align__(16) uint8_t s_dynamic[];
   MergeLds<kSketchThreads>& L = *reinterpret_cast<MergeLds<kSketchThreads>*>(s_dynamic);
-  float* s_stage = reinterpret_cast<float*>(s_dynamic);
   const uint32_t c = blockIdx.x;
   const SkFeature fe = features[c];
   const uint32_t limit = fe.limit, batches = fe.batches;
@@ -1151,12 +1149,14 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
     }
     return;
   }
-  // Rank queries in parallel; the order-preserving dedup pass is serial, on
-  // values staged in LDS when they fit.
-  const bool staged = size <= lds_values;
-  float* values = staged ? s_stage + lds_values : cut_values + (uint64_t)c * max_bin;
-  if (staged)
-    for (uint32_t i = threadIdx.x; i < size; i += blockDim.x) s_stage[i] = cur[i].value;
+  // Rank queries in parallel: query i (1 <= i < max_bin) picks entry c_i.
+  // The serial pass that follows (kernels/quantile.metal.h:371-396) emits,
+  // while it can, e_i = c_i's value if it exceeds the last one emitted, else
+  // the next entry above it.  Entry values strictly increase, so in indexes
+  // k_i = max(c_i, k_{i-1} + 1) with k_0 = 0, i.e. k_i = i + max(0, max over
+  // j <= i of (c_j - j)) -- a prefix maximum -- and the pass stops after the
+  // first k_i = size - 1 (no entry is left above it).
+  uint32_t* pick = picks + (uint64_t)c * max_bin;
   const double total = (double)cur[size - 1].rmax, denominator = (double)max_bin;
   for (uint32_t i = 1 + threadIdx.x; i < max_bin; i += blockDim.x) {
     const double rank = ((double)i * total) / denominator * 2.0;
@@ -1168,28 +1168,47 @@ __global__ __launch_bounds__(kSketchThreads) void k_finish(const SkFeature* __re
     }
     const uint32_t cursor = lo - 1;
     const float boundary = min_next(cur[cursor]) + max_prev(cur[cursor + 1]);
-    values[i] = cur[cursor + ((isnan(boundary) || rank >= (double)boundary) ? 1u : 0u)].value;
+    pick[i] = cursor + ((isnan(boundary) || rank >= (double)boundary) ? 1u : 0u);
+  }
+  if (threadIdx.x == 0) s_stop = max_bin;
+  __syncthreads();
+  // Thread t takes queries 1 + kCutsPer t .. kCutsPer (t + 1), in order; the
+  // offset keeps c_j - j + kMaxBinSketch >= 0 for the unsigned maximum.
+  constexpr uint32_t kCutsPer = (kMaxBinSketch + kSketchThreads - 1) / kSketchThreads;
+  uint32_t k[kCutsPer];
+  uint32_t local = 0;
+#pragma unroll
+  for (uint32_t u = 0; u < kCutsPer; ++u) {
+    const uint32_t i = 1 + kCutsPer * threadIdx.x + u;
+    if (i < max_bin) {
+      const uint32_t d = pick[i] + kMaxBinSketch - i;
+      local = d > local ? d : local;
+    }
+  }
+  uint32_t all;
+  uint32_t run = block_exclusive_max_u32(local, s_scan, &all);
+#pragma unroll
+  for (uint32_t u = 0; u < kCutsPer; ++u) {
+    const uint32_t i = 1 + kCutsPer * threadIdx.x + u;
+    k[u] = 0;
+    if (i < max_bin) {
+      const uint32_t d = pick[i] + kMaxBinSketch - i;
+      run = d > run ? d : run;
+      k[u] = i + (run > kMaxBinSketch ? run - kMaxBinSketch : 0u);
+      if (k[u] == size - 1) atomicMin(&s_stop, i);
+    }
   }
   __syncthreads();
+  const uint32_t emitted = s_stop < max_bin ? s_stop : max_bin - 1;
+#pragma unroll
+  for (uint32_t u = 0; u < kCutsPer; ++u) {
+    const uint32_t i = 1 + kCutsPer * threadIdx.x + u;
+    if (i <= emitted) out[i - 1] = cur[k[u]].value;
+  }
   if (threadIdx.x == 0) {
-    auto entry = [&](uint32_t j) { return staged ? s_stage[j] : cur[j].value; };
-    float last = entry(0);
-    uint32_t next = 1, count = 0;
-    for (uint32_t i = 1; i < max_bin; ++i) {
-      float value = values[i];
-      if (value <= last) {
-        while (next < size && entry(next) <= last) ++next;
-        if (next == size) break;
-        value = entry(next);
-      } else if (next < size && entry(next) <= value) {
-        do { ++next; } while (next < size && entry(next) <= value);
-      }
-      out[count++] = value;
-      last = value;
-    }
     const float tail = cur[size - 1].value;
-    out[count++] = tail + (fabsf(tail) + 1e-5f);
-    counts[f] = count;
+    out[emitted] = tail + (fabsf(tail) + 1e-5f);
+    counts[f] = emitted + 1;
   }
 }
 
@@ -1373,8 +1392,6 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   const uint64_t o_key_b = a2.reserve((uint64_t)batches * 4), o_key_e = a2.reserve((uint64_t)batches * 4);
   std::vector<uint64_t> o_tables(tables.size());
   for (size_t l = 0; l < tables.size(); ++l) o_tables[l] = a2.stage(tables[l]);
-  uint32_t max_budget = 1;
-  for (const SkFeature& fe : features) max_budget = std::max(max_budget, fe.budget);
   const uint64_t o_tree = a2.reserve(tree_total * sizeof(SkEntry)), o_scratch = a2.reserve(scratch_total * 4);
   const uint64_t o_node_count = a2.reserve((uint64_t)node_total * 4), o_serial = a2.reserve(nf * 4);
   const uint64_t o_fin = a2.reserve(fin_total * sizeof(SkEntry));
@@ -1417,16 +1434,13 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
                          a2.at<uint32_t>(o_tables[l]), features_d, work, tree, node_count, serial);
     MGB_LAUNCH_CHECK("k_level_up");
   }
-  // k_finish stages the pruned summary's values and the candidate cuts in LDS
-  // for its serial pass when they fit.
-  const uint32_t lds_values = (uint64_t)(max_budget + max_bin) * 4 <= kFinishLds ? max_budget : 0;
-  const uint32_t lds_bytes = std::max<uint32_t>(sizeof(MergeLds<kSketchThreads>), lds_values ? (lds_values + max_bin) * 4 : 0);
+  const uint32_t lds_bytes = sizeof(MergeLds<kSketchThreads>);
   if (hipFuncSetAttribute((const void*)k_finish, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess) {
     set_error("hipFuncSetAttribute(k_finish LDS) failed");
     return -1;
   }
   hipLaunchKernelGGL(k_finish, dim3(nf), dim3(kSketchThreads), lds_bytes, s, features_d, tree, node_count, serial,
-                     a2.at<SkEntry>(o_fin), f0, max_bin, a2.at<float>(o_values), lds_values,
+                     a2.at<SkEntry>(o_fin), f0, max_bin, a2.at<uint32_t>(o_values),
                      cuts, counts);
   MGB_LAUNCH_CHECK("k_finish");
   MGB_CHECK(hipStreamSynchronize(s));
@@ -1442,7 +1456,7 @@ extern "C" {
 
 int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights, uint32_t max_bin,
                     float* cuts, uint32_t* counts) {
-  if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
+  if (max_bin < 2 || max_bin > kMaxBinSketch) { set_error("max_bin must be in [2, 4096]"); return -1; }
   if (!cols) return 0;
   if (rows >= (1u << 31)) { set_error("sketch: rows must be below 2^31"); return -1; }
   // Feature groups of at most group_entries() entries and kMaxGroupFeatures
@@ -1468,7 +1482,7 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
 
 int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint64_t* colptr, uint32_t rows,
                         uint32_t cols, const float* weights, uint32_t max_bin, float* cuts, uint32_t* counts) {
-  if (max_bin < 2) { set_error("max_bin must be at least 2"); return -1; }
+  if (max_bin < 2 || max_bin > kMaxBinSketch) { set_error("max_bin must be in [2, 4096]"); return -1; }
   if (!cols) return 0;
   if (bound_device() < 0) return -1;
   (void)rows;
