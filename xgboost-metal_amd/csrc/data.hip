@@ -194,6 +194,11 @@ __device__ void scales_from_limbs(const uint64_t* limbs, float* scales) {
   }
 }
 
+// kMassCopies copies of the 512 buckets, lanes spread over them: the lanes of
+// a wave often share one bucket (every h of squared error), and LDS atomics
+// on one address serialize.
+constexpr uint32_t kMassCopies = 4;
+
 // Per-workgroup exponent buckets in LDS, reduced to 22 carry-save limbs and
 // published to the workgroup's own slot of the mass buffer; the last
 // workgroup to finish (completion counter) sums the slots and writes the
@@ -213,6 +218,12 @@ __device__ void mass_flush_and_scale(uint64_t* local, uint64_t* mass, float* sca
   (void)sink;
   const uint32_t tid = threadIdx.x;
   if (tid < 2 * kLimbs) limbs[tid] = 0;
+  __syncthreads();
+  for (uint32_t i = tid; i < 512; i += blockDim.x) {
+    uint64_t v = local[i];
+    for (uint32_t k = 1; k < kMassCopies; ++k) v += local[k * 512 + i];
+    local[i] = v;
+  }
   __syncthreads();
   block_carry_save(local, limbs);
   if (tid < 2 * kLimbs)
@@ -289,8 +300,9 @@ __device__ __forceinline__ void mass_add(uint64_t* local, float g, float h) {
   uint64_t mg, mh;
   mass_bucket(g, bg, mg);
   mass_bucket(h, bh, mh);
-  if (mg) atomicAdd((unsigned long long*)&local[bg], (unsigned long long)mg);
-  if (mh) atomicAdd((unsigned long long*)&local[256 + bh], (unsigned long long)mh);
+  uint64_t* copy = local + (lane_id() % kMassCopies) * 512;
+  if (mg) atomicAdd((unsigned long long*)&copy[bg], (unsigned long long)mg);
+  if (mh) atomicAdd((unsigned long long*)&copy[256 + bh], (unsigned long long)mh);
 }
 
 __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, const float* __restrict__ margin,
@@ -298,8 +310,8 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
                                                             const float* __restrict__ weights,
                                                             float2* __restrict__ grad, uint64_t* __restrict__ mass,
                                                             float* __restrict__ scales) {
-  __shared__ uint64_t local[2 * 256];
-  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
+  __shared__ uint64_t local[kMassCopies * 512];
+  for (uint32_t i = threadIdx.x; i < kMassCopies * 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
   const uint32_t first = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
   RowSampler sampler(p.sample_seed, first, stride, p.subsample < 1.0f);
@@ -327,8 +339,8 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
 __global__ __launch_bounds__(kGradThreads) void k_gradient_mass(MgbGradParams p, float2* __restrict__ grad,
                                                                 uint64_t* __restrict__ mass,
                                                                 float* __restrict__ scales) {
-  __shared__ uint64_t local[2 * 256];
-  for (uint32_t i = threadIdx.x; i < 512; i += blockDim.x) local[i] = 0;
+  __shared__ uint64_t local[kMassCopies * 512];
+  for (uint32_t i = threadIdx.x; i < kMassCopies * 512; i += blockDim.x) local[i] = 0;
   __syncthreads();
   const uint32_t first = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
   RowSampler sampler(p.sample_seed, first, stride, p.subsample < 1.0f);
