@@ -623,14 +623,61 @@ struct Codes {
       w[j / per_word] |= code << ((j % per_word) * bits);
     }
   }
-  __device__ __forceinline__ uint32_t get(uint32_t j) const {
-    constexpr uint32_t bits = 8 * sizeof(BinT);
-    constexpr uint32_t per_word = 64 / bits;
-    uint32_t word = j / per_word, shift = (j % per_word) * bits;
-    uint64_t v = w[0];
+  // The G codes rotated by r features: feature (k + r) mod G lands at
+  // position k, read with a constant shift.  One rotation per row replaces a
+  // lane-dependent select and 64-bit shift per feature: dword moves by the
+  // bits of r's dword offset (bit selects under per-lane masks, made once),
+  // then a funnel shift.
+  static constexpr int kBits = 8 * (int)sizeof(BinT);
+  static constexpr int kDwords = (G * kBits + 31) / 32;
+  static constexpr int kSteps = kDwords >= 8 ? 3 : kDwords >= 4 ? 2 : kDwords >= 2 ? 1 : 0;
+  struct Rotation {
+    uint32_t mask[kSteps > 0 ? kSteps : 1];
+    uint32_t bits;
+  };
+  struct Rotated {
+    uint32_t d[kDwords];
+    __device__ __forceinline__ uint32_t get(int k) const {
+      return (d[k * kBits / 32] >> (k * kBits % 32)) & ((1u << kBits) - 1u);
+    }
+  };
+  static __device__ __forceinline__ Rotation rotation(uint32_t r) {
+    Rotation m;
+    const uint32_t sh = r * kBits;
+    m.bits = sh % 32;
 #pragma unroll
-    for (int i = 1; i < kWords; ++i) v = word == (uint32_t)i ? w[i] : v;
-    return (uint32_t)(v >> shift) & ((1u << bits) - 1u);
+    for (int s = 0; s < kSteps; ++s) {
+      m.mask[s] = ((sh / 32) >> (kSteps - 1 - s)) & 1u ? ~0u : 0u;
+      // Kept as a lane value, so each select below is one bitwise op
+      // instead of a compare and a conditional move.
+      asm volatile("" : "+v"(m.mask[s]));
+    }
+    return m;
+  }
+  __device__ __forceinline__ Rotated rotate(const Rotation& m) const {
+    Rotated out;
+    if constexpr (G == 1) {
+      out.d[0] = (uint32_t)w[0];
+    } else if constexpr (G * kBits < 32) {  // 16 bits: u8 codes, G = 2
+      const uint32_t x = (uint32_t)w[0] & 0xFFFFu;
+      out.d[0] = (x | (x << 16)) >> m.bits;
+    } else {
+      uint32_t in[kDwords];
+#pragma unroll
+      for (int i = 0; i < kDwords; ++i) in[i] = (uint32_t)(w[i / 2] >> (32 * (i % 2)));
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const int step = 1 << (kSteps - 1 - s);
+        uint32_t t[kDwords];
+#pragma unroll
+        for (int i = 0; i < kDwords; ++i) t[i] = (in[(i + step) % kDwords] & m.mask[s]) | (in[i] & ~m.mask[s]);
+#pragma unroll
+        for (int i = 0; i < kDwords; ++i) in[i] = t[i];
+      }
+#pragma unroll
+      for (int i = 0; i < kDwords; ++i) out.d[i] = __builtin_amdgcn_alignbit(in[(i + 1) % kDwords], in[i], m.bits);
+    }
+    return out;
   }
 };
 
@@ -657,6 +704,8 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
   const uint32_t xcd_tasks = ntasks > xcd ? (ntasks - xcd + 7) / 8 : 0;
   const uint32_t xcd_items = xcd_tasks * t.groups;
   const uint32_t lane = lane_id();
+  // Lanes rotate through the group's features.
+  const typename Codes<BinT, G>::Rotation rot = Codes<BinT, G>::rotation(lane & (G - 1));
   const uint32_t entries = G * B1;
   const uint32_t* rows = t.rows[depth & 1];
   int64_t* bank = t.hist[depth & 1];
@@ -728,12 +777,14 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
         // A (0, 0) pair adds nothing: the rows a subsample drops, which the
         // root streams with the kept ones, cost no LDS atomics.
         if (!UNIT && (qg | qh) == 0) continue;
+        // A present value's code is below max_bin and the missing code
+        // (0xFF / 0xFFFF) is not: the minimum sends it to the missing slot.
+        const typename Codes<BinT, G>::Rotated rc = c_a[u].rotate(rot);
         if (fcount == (uint32_t)G) {  // full group (uniform): no per-feature test
 #pragma unroll
           for (int k = 0; k < G; ++k) {
             const uint32_t j = (k + lane) & (G - 1);
-            const uint32_t code = c_a[u].get(j);
-            const uint32_t bin = code == t.missing_code ? t.max_bin : code;
+            const uint32_t bin = min(rc.get(k), t.max_bin);
             atomicAdd(&lg[bin * G + j], qg);
             if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
             else atomicAdd(&lh[bin * G + j], qh);
@@ -742,8 +793,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
 #pragma unroll
           for (int k = 0; k < G; ++k) {
             const uint32_t j = (k + lane) & (G - 1);
-            const uint32_t code = c_a[u].get(j);
-            const uint32_t bin = code == t.missing_code ? t.max_bin : code;
+            const uint32_t bin = min(rc.get(k), t.max_bin);
             if (j < fcount) {
               atomicAdd(&lg[bin * G + j], qg);
               if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
