@@ -648,8 +648,7 @@ struct Codes {
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
       m.mask[s] = ((sh / 32) >> (kSteps - 1 - s)) & 1u ? ~0u : 0u;
-      // Kept as a lane value, so each select below is one bitwise op
-      // instead of a compare and a conditional move.
+      // Kept as a lane value for the bit selects below.
       asm volatile("" : "+v"(m.mask[s]));
     }
     return m;
@@ -670,7 +669,10 @@ struct Codes {
         const int step = 1 << (kSteps - 1 - s);
         uint32_t t[kDwords];
 #pragma unroll
-        for (int i = 0; i < kDwords; ++i) t[i] = (in[(i + step) % kDwords] & m.mask[s]) | (in[i] & ~m.mask[s]);
+        for (int i = 0; i < kDwords; ++i) {
+          // v_bfi_b32: (mask & moved) | (~mask & kept), one op per dword.
+          asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(t[i]) : "v"(m.mask[s]), "v"(in[(i + step) % kDwords]), "v"(in[i]));
+        }
 #pragma unroll
         for (int i = 0; i < kDwords; ++i) in[i] = t[i];
       }
@@ -680,6 +682,21 @@ struct Codes {
     return out;
   }
 };
+
+// LDS atomics by byte address (the LDS aperture's 32-bit offsets), so a
+// lane's per-feature base address can be kept in a register with the
+// dynamic LDS base already added.
+typedef __attribute__((address_space(3))) unsigned long long lds_u64_t;
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void lds_add(uint32_t address, unsigned long long v) {
+  __hip_atomic_fetch_add((lds_u64_t*)(uintptr_t)address, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_add(uint32_t address, uint32_t v) {
+  __hip_atomic_fetch_add((lds_u32_t*)(uintptr_t)address, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 template <typename BinT, int G, bool UNIT, bool IDENTITY, bool COLS>
 __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t depth) {
@@ -704,8 +721,21 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
   const uint32_t xcd_tasks = ntasks > xcd ? (ntasks - xcd + 7) / 8 : 0;
   const uint32_t xcd_items = xcd_tasks * t.groups;
   const uint32_t lane = lane_id();
-  // Lanes rotate through the group's features.
+  // Lanes rotate through the group's features: position k of a lane's
+  // rotated codes is feature (k + lane) mod G, whose entry of bin b sits at
+  // byte fa[k] + b * 8G of lg (and of lh; at fc[k] + b * 4G of lc).
   const typename Codes<BinT, G>::Rotation rot = Codes<BinT, G>::rotation(lane & (G - 1));
+  uint32_t fa[G], fc[G];
+  uint32_t h_offset = G * B1 * 8;  // lh after lg
+  asm volatile("" : "+s"(h_offset));  // one add per entry, not folded into the bin's shift
+#pragma unroll
+  for (int k = 0; k < G; ++k) {
+    const uint32_t j = (k + lane) & (G - 1);
+    fa[k] = lds_address(lg + j);
+    fc[k] = lds_address(lc + j);
+    asm volatile("" : "+v"(fa[k]));
+    if constexpr (UNIT) asm volatile("" : "+v"(fc[k]));
+  }
   const uint32_t entries = G * B1;
   const uint32_t* rows = t.rows[depth & 1];
   int64_t* bank = t.hist[depth & 1];
@@ -783,11 +813,11 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
         if (fcount == (uint32_t)G) {  // full group (uniform): no per-feature test
 #pragma unroll
           for (int k = 0; k < G; ++k) {
-            const uint32_t j = (k + lane) & (G - 1);
             const uint32_t bin = min(rc.get(k), t.max_bin);
-            atomicAdd(&lg[bin * G + j], qg);
-            if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
-            else atomicAdd(&lh[bin * G + j], qh);
+            const uint32_t a = fa[k] + bin * (8 * G);
+            lds_add(a, qg);
+            if constexpr (UNIT) lds_add(fc[k] + bin * (4 * G), 1u);
+            else lds_add(a + h_offset, qh);
           }
         } else {
 #pragma unroll
