@@ -36,7 +36,7 @@ constexpr uint32_t kPartThreads = 256;    // partition (and select bookkeeping) 
 constexpr uint32_t kPartMasks = kPartTile / 64;  // wave64 ballot masks per partition tile
 constexpr uint32_t kSelectThreads = 256;
 constexpr uint32_t kHistThreads = 1024;
-constexpr int kHistUnroll = 4;          // rows in flight per thread
+constexpr int kHistUnroll = 2;          // rows per thread per histogram batch
 
 enum : uint32_t { kOpNone = 0, kOpLeaf = 1, kOpSplit = 2, kOpFinal = 3 };
 
@@ -700,7 +700,7 @@ __device__ __forceinline__ void lds_add(uint32_t address, uint32_t v) {
 
 template <typename BinT, int G, bool UNIT, bool IDENTITY, bool COLS>
 __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t depth) {
-  constexpr int kU = Codes<BinT, G>::kBytes >= 32 ? 2 : kHistUnroll;
+  constexpr int kU = kHistUnroll;
   extern __shared__ __align__(16) uint8_t smem[];
   const uint32_t B1 = t.bins1;
   unsigned long long* lg = reinterpret_cast<unsigned long long*>(smem);
@@ -754,12 +754,16 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
     const uint8_t* gbins = bins + (uint64_t)group * t.group_stride;
     const BinT* gcols = COLS ? reinterpret_cast<const BinT*>(t.columns) + (uint64_t)fbase * t.rows_n : nullptr;
-    // kU rows per thread per batch (fewer for 32-byte code chunks, which
-    // would spill), software pipelined: while a
-    // batch's LDS atomics run, the next batch's gradients and codes and the
-    // row ids of the one after are already in flight, so the waves of the
-    // CU (one 1024-thread workgroup when the histogram fills the LDS) keep
-    // memory busy instead of alternating between loading and accumulating.
+    // kU rows per thread per batch, software pipelined: while a batch's LDS
+    // atomics run, the next batch's gradients and codes and the row ids of
+    // the one after are already in flight, so the waves of the CU (one
+    // 1024-thread workgroup when the histogram fills the LDS) keep memory
+    // busy instead of alternating between loading and accumulating.  More
+    // rows in flight lose: the feature groups' workgroups share each row's
+    // code lines through L2, and deeper queues evict them sooner (10M x 128,
+    // 1024 bins, histogram per round at 1 / 2 / 3 / 4 / 6 rows per thread:
+    // 4.94 / 4.56 / 4.68 / 4.72 / 4.91 ms; two batches of data ahead instead
+    // of one at 4 rows: 4.82 ms).
     constexpr uint32_t kStep = kHistThreads * kU;
     // Loads are unconditional (a slot past the task's end reads the task's
     // first row instead and is skipped when accumulating): with no branch
