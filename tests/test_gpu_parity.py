@@ -97,9 +97,16 @@ def test_sketch_feature_groups_match_oracle(group_entries):
             np.testing.assert_array_equal(cuts[f, :counts[f]].view(np.uint32), ocuts[f, :counts[f]].view(np.uint32))
 
 
-@pytest.mark.parametrize("bin_bytes,G,group_major", [(1, 16, False), (1, 4, False), (2, 8, False), (1, 4, True),
-                                                     (2, 4, True), (1, 16, True)])
-def test_bins_and_histogram_match_oracle(bin_bytes, G, group_major):
+@pytest.mark.parametrize("bin_bytes,G,group_major,unit", [
+    (1, 16, False, False), (1, 4, False, False), (2, 8, False, False), (1, 4, True, False), (2, 4, True, False),
+    (1, 16, True, False), (1, 1, False, False), (1, 2, False, False), (2, 2, False, False), (2, 16, False, False),
+    (1, 8, False, True), (2, 1, True, True), (2, 16, False, True), (1, 2, True, True)])
+def test_bins_and_histogram_match_oracle(bin_bytes, G, group_major, unit):
+    """Codes and histograms (the root's identity rows and a gathered row list)
+    against brute-force integer sums, for every feature-group width with u8
+    and u16 codes, row- and group-major layouts, explicit and unit Hessians:
+    21 features leave a partial last group for every G above 1, and missing
+    values go to the missing slot."""
     rng = np.random.default_rng(11)
     X, y = W.config1(rows=9000, cols=21)
     ocuts, ocounts, _ = O.sketch_cuts(X, 64)
@@ -111,12 +118,12 @@ def test_bins_and_histogram_match_oracle(bin_bytes, G, group_major):
     want = np.where(obins == 0xFFFF, code, obins).astype(np.int64)
     np.testing.assert_array_equal(got, want)
     grad = rng.normal(size=len(X)).astype(np.float32)
-    hess = rng.uniform(0.1, 1.0, len(X)).astype(np.float32)
+    hess = np.ones(len(X), np.float32) if unit else rng.uniform(0.1, 1.0, len(X)).astype(np.float32)
     sg, sh = O.gradient_scale(grad), O.gradient_scale(hess)
     qg = np.rint(grad.astype(np.float32) * np.float32(sg)).astype(np.int64)
     qh = np.rint(hess.astype(np.float32) * np.float32(sh)).astype(np.int64)
     for rows_list in [None, np.sort(rng.choice(len(X), 3001, replace=False)).astype(np.uint32)]:
-        hist = D.histogram(m, dbins, rows_list, grad, hess, [sg, sh], G, rows_per_tile=1024)
+        hist = D.histogram(m, dbins, rows_list, grad, hess, [sg, sh], G, unit=unit, rows_per_tile=1024)
         idx = np.arange(len(X)) if rows_list is None else rows_list.astype(np.int64)
         # Brute-force integer sums (mod 2^64) per (feature, bin); bin max_bin = missing.
         for f in range(X.shape[1]):
