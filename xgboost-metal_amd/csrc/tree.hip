@@ -733,6 +733,8 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     const uint32_t j = (k + lane) & (G - 1);
     fa[k] = lds_address(lg + j);
     fc[k] = lds_address(lc + j);
+    // Held in registers as computed (else the compiler rebuilds them from j
+    // for every row).
     asm volatile("" : "+v"(fa[k]));
     if constexpr (UNIT) asm volatile("" : "+v"(fc[k]));
   }
