@@ -138,6 +138,7 @@ struct Tree {
   // masks of its left rows and its left count.
   uint64_t* part_masks;
   uint32_t* part_left;
+  uint32_t* final_order;      // stable partition: the last level's tasks by row range, then 9 XCD list offsets
   // Inputs.
   const void* bins;
   const void* columns;        // column-major codes for the partition (NULL: read bins)
@@ -2164,6 +2165,54 @@ __global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t de
   }
 }
 
+// The last level's margin updates, ordered by row range.  A node's rows are
+// in row order (stable partition), so its tile q of T covers about the
+// (q + 1/2)/T fraction of the row range; every node of the level spans all
+// of it.  In node order, the workgroups resident at one time update margins
+// of rows spread over the whole range, and each margin line (32 rows, from
+// many nodes) is fetched and written back once per node that touches it.
+// Here one workgroup sorts the level's tasks by that fraction (64 buckets,
+// counting sort) and splits the order into 8 contiguous row ranges, one per
+// XCD: the apply kernel's workgroups on an XCD take that XCD's list in
+// order, so the margin lines in flight fit the XCD's L2.  The order only
+// changes which workgroup updates which rows, and when.
+constexpr uint32_t kOrderBuckets = 64;
+constexpr uint32_t kOrderThreads = 1024;
+__device__ __forceinline__ uint32_t order_bucket(const PartTask& task, const Frontier& node) {
+  const uint32_t tiles = div_up(node.count, kPartTile);
+  const uint32_t q = (task.begin - node.begin) / kPartTile;
+  return (uint32_t)(((2ull * q + 1) * kOrderBuckets) / (2ull * tiles));
+}
+__global__ __launch_bounds__(kOrderThreads) void k_final_order(Tree t, uint32_t depth) {
+  __shared__ uint32_t count[kOrderBuckets];
+  const uint32_t ntasks = t.state->n_part[depth & 1];
+  const PartTask* tasks = part_bank(t, depth);
+  const Frontier* frontier = t.frontier[depth & 1];
+  uint32_t* offsets = t.final_order + t.max_part_tasks;  // XCD x: [offsets[x], offsets[x + 1])
+  if (threadIdx.x < kOrderBuckets) count[threadIdx.x] = 0;
+  __syncthreads();
+  for (uint32_t w = threadIdx.x; w < ntasks; w += blockDim.x) {
+    const PartTask task = tasks[w];
+    atomicAdd(&count[order_bucket(task, frontier[task.slot])], 1u);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t pos = 0;
+    for (uint32_t b = 0; b < kOrderBuckets; ++b) {
+      if (b % (kOrderBuckets / 8) == 0) offsets[b / (kOrderBuckets / 8)] = pos;
+      const uint32_t c = count[b];
+      count[b] = pos;
+      pos += c;
+    }
+    offsets[8] = pos;
+  }
+  __syncthreads();
+  for (uint32_t w = threadIdx.x; w < ntasks; w += blockDim.x) {
+    const PartTask task = tasks[w];
+    t.final_order[atomicAdd(&count[order_bucket(task, frontier[task.slot])], 1u)] = w;
+  }
+}
+
 // Select and partition of one level in one launch.  The last workgroup does
 // the level's bookkeeping (select_level: tree records, the next frontier, and
 // with unit Hessians the next level's plan); every other workgroup takes
@@ -2201,7 +2250,15 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   uint32_t op_slot = 0xffffffffu;
   NodeOp op;
-  for (uint32_t w = blockIdx.x; w < ntasks; w += gridDim.x - 1) {
+  // The last level of a stable partition takes its tasks by row range, XCD
+  // by XCD (k_final_order); other levels in task order.
+  const bool ordered = STABLE && depth + 1 >= t.max_depth;
+  const uint32_t xcd = blockIdx.x % 8;
+  const uint32_t first = ordered ? t.final_order[t.max_part_tasks + xcd] + blockIdx.x / 8 : blockIdx.x;
+  const uint32_t last = ordered ? t.final_order[t.max_part_tasks + xcd + 1] : ntasks;
+  const uint32_t stride = ordered ? (gridDim.x - 1 - xcd + 7) / 8 : gridDim.x - 1;
+  for (uint32_t i = first; i < last; i += stride) {
+    const uint32_t w = ordered ? t.final_order[i] : i;
     const PartTask task = tasks[w];
     // The tile's row ids are requested first; every thread then rebuilds the
     // node's split itself (uniform loads, no barrier), so the two chains of
@@ -2364,7 +2421,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_walk_dropped(Tree t) {
 // ---------------------------------------------------------------------------
 struct Layout {
   size_t state, rows, gh, hist, frontier, recs, best, hist_tasks, zero, part_tasks, cursors, split_bins, partials;
-  size_t part_masks, part_left, total;
+  size_t part_masks, part_left, final_order, total;
   uint32_t slots, max_hist_tasks, max_part_tasks;
   uint64_t hist_entry;
 };
@@ -2402,8 +2459,9 @@ Layout layout(const MgbTreeShape& s) {
   if (s.stable_partition) {
     L.part_masks = off; off = align_up(off + (size_t)L.max_part_tasks * kPartMasks * sizeof(uint64_t));
     L.part_left = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
+    L.final_order = off; off = align_up(off + ((size_t)L.max_part_tasks + 9) * sizeof(uint32_t));
   } else {
-    L.part_masks = L.part_left = 0;
+    L.part_masks = L.part_left = L.final_order = 0;
   }
   L.total = off;
   return L;
@@ -2489,7 +2547,12 @@ template <typename BinT>
 int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
   const uint32_t lds = depth == 0 && t.dense ? (uint32_t)root_stage_bytes(t.bins1) : 0u;
   const bool identity = depth == 0 && !t.compact;
-  if (t.stable) {
+  if (t.stable && depth + 1 >= t.max_depth) {
+    // The last level moves no rows: its tasks are ordered for the margin
+    // updates instead of counted.
+    launch(MGB_PROF_PARTITION, k_final_order, dim3(1), dim3(kOrderThreads), 0, t, depth);
+    MGB_LAUNCH_CHECK("k_final_order");
+  } else if (t.stable) {
     launch(MGB_PROF_PARTITION, identity ? k_part_count<BinT, true> : k_part_count<BinT, false>, dim3(grid),
            dim3(kPartThreads), 0, t, depth);
     MGB_LAUNCH_CHECK("k_part_count");
@@ -2572,6 +2635,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   if (t.stable) {
     t.part_masks = reinterpret_cast<uint64_t*>(ws + L.part_masks);
     t.part_left = reinterpret_cast<uint32_t*>(ws + L.part_left);
+    t.final_order = reinterpret_cast<uint32_t*>(ws + L.final_order);
   }
   t.hist_entry = L.hist_entry;
   return t;
