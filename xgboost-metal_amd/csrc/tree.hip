@@ -2679,11 +2679,12 @@ uint64_t level_hist_tasks(const Tree& t, uint32_t depth) {
 
 // Partition workgroups at a level: nodes at depth d (at most 2^d) hold at
 // most N rows, in at most floor(N / tile) + 2^d tiles; the kernel loops over
-// tasks, so 1024 workgroups cover any level.
+// tasks, so 2048 workgroups cover any level (10M x 128: partition 1.70 /
+// 1.67 / 1.71 ms per round with at most 1024 / 2048 / 4096).
 uint32_t level_part_grid(const Tree& t, uint32_t depth) {
   const uint64_t nodes = depth < 32 ? (1ull << depth) : ~0ull >> 1;
   const uint64_t tasks = (uint64_t)t.rows_n / kPartTile + nodes;
-  return (uint32_t)(tasks < 1024 ? tasks : 1024);
+  return (uint32_t)(tasks < 2048 ? tasks : 2048);
 }
 
 }  // namespace
