@@ -2519,7 +2519,12 @@ int launch_split(const Tree& t, uint32_t depth, uint32_t items) {
   const uint32_t w4 = split_waves(t.max_bin);
   if (w4 * kWave * 4 < t.max_bin) { set_error("max_bin too large for the split kernel"); return -1; }
   items = items ? items : 1;
-  const bool spread = (uint64_t)items * w4 < 2048 && w4 * 4 <= 16;
+  // Spread shape (one bin per lane on 4·w4 waves per item) while a level has
+  // few items: under 2048 waves of the four-bin shape up to 512 bins, under
+  // 2048 items at 1024 bins, whose mid levels also sum many tiles' partials
+  // per item (10M x 128: split 1.35 -> 1.31 ms per round; under 4096 items
+  // 1.33; 262,144 x 64 slower with any wider spread).
+  const bool spread = (w4 >= 4 ? (uint64_t)items < 2048 : (uint64_t)items * w4 < 2048) && w4 * 4 <= 16;
   const uint32_t w = spread ? 4 * w4 : w4;
   const dim3 grid(w == 1 ? div_up(items, 4) : items), block(w == 1 ? 4 * kWave : w * kWave);
   if (!spread) {
