@@ -31,9 +31,15 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 namespace mgb {
 namespace {
 
-constexpr uint32_t kPartTile = 1024;      // rows per partition task
+// Rows per partition task: 2048 with the stable partition (the large row
+// counts it runs on: 10M x 128, partition 1.66 -> 1.55 ms per round against
+// 1024; 512: 2.06 ms), 1024 with claims (262,144 x 64: 38.0 against 38.6 ms
+// per fit at 2048).  Tree::part_tile holds the one in use.
+template <bool STABLE>
+constexpr uint32_t kPartTileOf = STABLE ? 2048u : 1024u;
 constexpr uint32_t kPartThreads = 256;    // partition (and select bookkeeping) workgroup
-constexpr uint32_t kPartMasks = kPartTile / 64;  // wave64 ballot masks per partition tile
+template <bool STABLE>
+constexpr uint32_t kPartMasksOf = kPartTileOf<STABLE> / 64;  // wave64 ballot masks per partition tile
 constexpr uint32_t kSelectThreads = 256;
 constexpr uint32_t kHistThreads = 1024;
 constexpr int kHistUnroll = 2;          // rows per thread per histogram batch
@@ -171,6 +177,7 @@ struct Tree {
   uint32_t compact;                          // the root's rows are the kept rows of a subsample
   uint32_t fused_level0;                     // the root histogram's workgroup 0 runs level0_setup
   uint32_t stable;                           // stable partition (k_part_count before k_apply)
+  uint32_t part_tile;                        // rows per partition task (kPartTileOf<stable>)
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
@@ -277,11 +284,11 @@ __device__ void level0_setup(const Tree& t) {
     t.hist_tasks[i] = HistTask{0u, begin, end, tiles == 1 ? 1u : 0u};
   }
   // The root's partition tasks (row tiles of [0, n_root)) and cursors.
-  const uint32_t ptiles = n_root ? div_up(n_root, kPartTile) : 0;
+  const uint32_t ptiles = n_root ? div_up(n_root, t.part_tile) : 0;
   if (t.part_tasks)
     for (uint32_t i = threadIdx.x; i < ptiles; i += blockDim.x) {
-      const uint32_t b = i * kPartTile;
-      t.part_tasks[i] = PartTask{0u, b, b + kPartTile < n_root ? b + kPartTile : n_root, 0u};
+      const uint32_t b = i * t.part_tile;
+      t.part_tasks[i] = PartTask{0u, b, b + t.part_tile < n_root ? b + t.part_tile : n_root, 0u};
     }
   if (threadIdx.x == 0) {
     st->rows_built[0] = n_root;
@@ -477,7 +484,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     carry_tasks += total_tasks;
     carry_zero += total_zero;
     // Partition tasks of both children, in slot order.
-    const uint32_t pl = p < pairs ? div_up(c0, kPartTile) : 0, pr = p < pairs ? div_up(c1, kPartTile) : 0;
+    const uint32_t pl = p < pairs ? div_up(c0, t.part_tile) : 0, pr = p < pairs ? div_up(c1, t.part_tile) : 0;
     uint32_t total_part;
     const uint32_t poff = block_exclusive_u32(pl + pr, scan, &total_part);
     __syncthreads();
@@ -493,8 +500,8 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
       const bool left = q < s_slot[k];
       const uint32_t cb = left ? s_begin[k] : s_begin[k] + s_end[k];
       const uint32_t ce = left ? s_begin[k] + s_end[k] : s_begin[k] + s_end[k] + scan_right[k];
-      const uint32_t b = cb + (left ? q : q - s_slot[k]) * kPartTile;
-      ptasks[carry_part + j] = PartTask{2 * (base + k) + (left ? 0u : 1u), b, b + kPartTile < ce ? b + kPartTile : ce, 0u};
+      const uint32_t b = cb + (left ? q : q - s_slot[k]) * t.part_tile;
+      ptasks[carry_part + j] = PartTask{2 * (base + k) + (left ? 0u : 1u), b, b + t.part_tile < ce ? b + t.part_tile : ce, 0u};
     }
     carry_part += total_part;
     __syncthreads();
@@ -1878,8 +1885,8 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
       zoff = block_exclusive_u32(hzero, scan, &total_zero) + carry_zero;
       block_exclusive_u32(hrows, scan, &total_rows);
       if (valid && expand) {
-        pl = div_up(lcount, kPartTile);
-        pr = div_up(node.count - lcount, kPartTile);
+        pl = div_up(lcount, t.part_tile);
+        pr = div_up(node.count - lcount, t.part_tile);
       }
       poff = block_exclusive_u32(pl + pr, scan, &total_ptasks);
     }
@@ -1982,14 +1989,14 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
       for (uint32_t j = threadIdx.x; j < total_ptasks; j += blockDim.x) {
         const uint32_t k = owner_of(s_off, nitems, j);
         const uint32_t q = j - s_off[k];
-        const uint32_t lt = div_up(s_end[k], kPartTile);
+        const uint32_t lt = div_up(s_end[k], t.part_tile);
         const bool left = q < lt;
         // The node's rows: [begin, begin + lcount) go left, the rest right.
         const uint32_t nb = s_begin[k];
         const uint32_t cb = left ? nb : nb + s_end[k];
         const uint32_t ce = left ? nb + s_end[k] : nb + s_count[k];
-        const uint32_t b = cb + (left ? q : q - lt) * kPartTile;
-        ntasks[carry_ptasks + j] = PartTask{scan_slot[k] + (left ? 0u : 1u), b, b + kPartTile < ce ? b + kPartTile : ce, 0u};
+        const uint32_t b = cb + (left ? q : q - lt) * t.part_tile;
+        ntasks[carry_ptasks + j] = PartTask{scan_slot[k] + (left ? 0u : 1u), b, b + t.part_tile < ce ? b + t.part_tile : ce, 0u};
       }
       carry_htasks += total_htasks;
       carry_zero += total_zero;
@@ -2017,7 +2024,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
 
 // ---------------------------------------------------------------------------
 // Row partition (kernels/boost.metal:1316-1614): ballot + prefix scatter,
-// stable within a tile of kPartTile rows; tiles of one node claim their
+// stable within a tile of part_tile rows; tiles of one node claim their
 // ranges in arrival order.  value < threshold <=> bin <= last_left_bin; missing follows
 // default_left.  Rows of nodes that stop here get their leaf added to the
 // training margin (prediction cache, kernels/boost.metal:1738-1763).
@@ -2050,14 +2057,15 @@ __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint3
   return (int32_t)code <= op.last_left_bin;
 }
 
-constexpr int kPartPer = kPartTile / kPartThreads;  // rows per thread, all loaded up front
+template <bool STABLE>
+constexpr int kPartPerOf = (int)(kPartTileOf<STABLE> / kPartThreads);  // rows per thread, all loaded up front
 
 // Row ids of a partition tile for this thread (positions begin + k*256 + tid).
-template <bool IDENTITY>
-__device__ __forceinline__ void load_tile_rows(const uint32_t* rows, const PartTask& task, uint32_t (&row)[kPartPer],
-                                               bool (&active)[kPartPer]) {
+template <bool IDENTITY, int PER>
+__device__ __forceinline__ void load_tile_rows(const uint32_t* rows, const PartTask& task, uint32_t (&row)[PER],
+                                               bool (&active)[PER]) {
 #pragma unroll
-  for (int k = 0; k < kPartPer; ++k) {
+  for (int k = 0; k < PER; ++k) {
     const uint32_t i = task.begin + k * kPartThreads + threadIdx.x;
     active[k] = i < task.end;
     row[k] = active[k] ? (IDENTITY ? i : rows[i]) : 0u;
@@ -2129,6 +2137,8 @@ __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
 template <typename BinT, bool IDENTITY>
 __global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t depth) {
   constexpr uint32_t kWaves = kPartThreads / kWave;
+  constexpr int kPartPer = kPartPerOf<true>;
+  constexpr uint32_t kPartMasks = kPartMasksOf<true>;
   __shared__ uint32_t wave_left[kPartMasks];
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part[depth & 1];
@@ -2141,7 +2151,7 @@ __global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t de
     const PartTask task = tasks[w];
     uint32_t row[kPartPer];
     bool active[kPartPer];
-    load_tile_rows<IDENTITY>(rows, task, row, active);
+    load_tile_rows<IDENTITY, kPartPer>(rows, task, row, active);
     if (task.slot != op_slot) {  // uniform: every thread read the same task
       op = node_op(t, depth, task.slot);
       op_slot = task.slot;
@@ -2178,9 +2188,9 @@ __global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t de
 // changes which workgroup updates which rows, and when.
 constexpr uint32_t kOrderBuckets = 64;
 constexpr uint32_t kOrderThreads = 1024;
-__device__ __forceinline__ uint32_t order_bucket(const PartTask& task, const Frontier& node) {
-  const uint32_t tiles = div_up(node.count, kPartTile);
-  const uint32_t q = (task.begin - node.begin) / kPartTile;
+__device__ __forceinline__ uint32_t order_bucket(const PartTask& task, const Frontier& node, uint32_t part_tile) {
+  const uint32_t tiles = div_up(node.count, part_tile);
+  const uint32_t q = (task.begin - node.begin) / part_tile;
   return (uint32_t)(((2ull * q + 1) * kOrderBuckets) / (2ull * tiles));
 }
 __global__ __launch_bounds__(kOrderThreads) void k_final_order(Tree t, uint32_t depth) {
@@ -2193,7 +2203,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_final_order(Tree t, uint32_t 
   __syncthreads();
   for (uint32_t w = threadIdx.x; w < ntasks; w += blockDim.x) {
     const PartTask task = tasks[w];
-    atomicAdd(&count[order_bucket(task, frontier[task.slot])], 1u);
+    atomicAdd(&count[order_bucket(task, frontier[task.slot], t.part_tile)], 1u);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -2209,14 +2219,14 @@ __global__ __launch_bounds__(kOrderThreads) void k_final_order(Tree t, uint32_t 
   __syncthreads();
   for (uint32_t w = threadIdx.x; w < ntasks; w += blockDim.x) {
     const PartTask task = tasks[w];
-    t.final_order[atomicAdd(&count[order_bucket(task, frontier[task.slot])], 1u)] = w;
+    t.final_order[atomicAdd(&count[order_bucket(task, frontier[task.slot], t.part_tile)], 1u)] = w;
   }
 }
 
 // Select and partition of one level in one launch.  The last workgroup does
 // the level's bookkeeping (select_level: tree records, the next frontier, and
 // with unit Hessians the next level's plan); every other workgroup takes
-// partition tiles of up to kPartTile rows of one node, works out that node's
+// partition tiles of up to part_tile rows of one node, works out that node's
 // split itself (node_op), and moves its rows: a split node's left rows fill
 // its segment upwards from the start and its right rows downwards from the
 // end, each tile claiming its ranges with one atomic on each of the node's
@@ -2234,6 +2244,9 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
     return;
   }
   constexpr uint32_t kWaves = kPartThreads / kWave;
+  constexpr uint32_t kPartTile = kPartTileOf<STABLE>;
+  constexpr int kPartPer = kPartPerOf<STABLE>;
+  constexpr uint32_t kPartMasks = kPartMasksOf<STABLE>;
   __shared__ uint32_t wave_left[kPartPer][kWaves], wave_active[kPartPer][kWaves];
   __shared__ uint32_t wave_before[kWaves], wave_all[kWaves];  // STABLE: the node's tile counts
   __shared__ uint32_t base_left, base_right;
@@ -2265,7 +2278,7 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
     // loads overlap.
     uint32_t row[kPartPer];
     bool active[kPartPer];
-    load_tile_rows<IDENTITY>(rows, task, row, active);
+    load_tile_rows<IDENTITY, kPartPer>(rows, task, row, active);
     if (task.slot != op_slot) {  // uniform: every thread read the same task
       op = node_op(t, depth, task.slot);
       op_slot = task.slot;
@@ -2434,7 +2447,8 @@ Layout layout(const MgbTreeShape& s) {
   L.slots = 1u << (depth - 1);
   L.hist_entry = (uint64_t)s.cols * (s.max_bin + 1) * 2;
   L.max_hist_tasks = div_up(s.rows ? s.rows : 1, s.rows_per_tile) + L.slots + 1;
-  L.max_part_tasks = div_up(s.rows ? s.rows : 1, kPartTile) + 2 * L.slots + 1;
+  const uint32_t part_tile = s.stable_partition ? kPartTileOf<true> : kPartTileOf<false>;
+  L.max_part_tasks = div_up(s.rows ? s.rows : 1, part_tile) + 2 * L.slots + 1;
   size_t off = 0;
   L.state = off; off = align_up(off + sizeof(LevelState));
   L.rows = off; off = align_up(off + 2 * (size_t)s.rows * sizeof(uint32_t));
@@ -2457,7 +2471,7 @@ Layout layout(const MgbTreeShape& s) {
       off = align_up(off + (size_t)L.max_hist_tasks * groups * s.features_per_group * (s.max_bin + 1) * 16);
   }
   if (s.stable_partition) {
-    L.part_masks = off; off = align_up(off + (size_t)L.max_part_tasks * kPartMasks * sizeof(uint64_t));
+    L.part_masks = off; off = align_up(off + (size_t)L.max_part_tasks * kPartMasksOf<true> * sizeof(uint64_t));
     L.part_left = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
     L.final_order = off; off = align_up(off + ((size_t)L.max_part_tasks + 9) * sizeof(uint32_t));
   } else {
@@ -2637,6 +2651,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.sparse = s->sparse;
   t.compact = s->compact_sampled && !s->sparse ? 1u : 0u;
   t.stable = s->stable_partition ? 1u : 0u;
+  t.part_tile = t.stable ? kPartTileOf<true> : kPartTileOf<false>;
   if (t.stable) {
     t.part_masks = reinterpret_cast<uint64_t*>(ws + L.part_masks);
     t.part_left = reinterpret_cast<uint32_t*>(ws + L.part_left);
@@ -2688,7 +2703,7 @@ uint64_t level_hist_tasks(const Tree& t, uint32_t depth) {
 // 1.67 / 1.71 ms per round with at most 1024 / 2048 / 4096).
 uint32_t level_part_grid(const Tree& t, uint32_t depth) {
   const uint64_t nodes = depth < 32 ? (1ull << depth) : ~0ull >> 1;
-  const uint64_t tasks = (uint64_t)t.rows_n / kPartTile + nodes;
+  const uint64_t tasks = (uint64_t)t.rows_n / t.part_tile + nodes;
   return (uint32_t)(tasks < 2048 ? tasks : 2048);
 }
 
