@@ -31,15 +31,14 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 namespace mgb {
 namespace {
 
-// Rows per partition task: 2048 with the stable partition (the large row
-// counts it runs on: 10M x 128, partition 1.66 -> 1.55 ms per round against
-// 1024; 512: 2.06 ms), 1024 with claims (262,144 x 64: 38.0 against 38.6 ms
-// per fit at 2048).  Tree::part_tile holds the one in use.
-template <bool STABLE>
-constexpr uint32_t kPartTileOf = STABLE ? 2048u : 1024u;
+// Rows per partition task (Tree::part_tile): 2048 for the stable partition
+// of a dense matrix (10M x 128: partition 1.66 -> 1.55 ms per round against
+// 1024; 512: 2.06 ms), else 1024 (262,144 x 64 with claims: 38.0 against
+// 38.6 ms per fit at 2048; 1M x 2000 CSR, whose row test is a search in the
+// row: 0.37 against 0.44 ms per round).  The partition kernels take the rows
+// per thread (part_tile / kPartThreads) as a template argument.
+constexpr uint32_t kPartTileWide = 2048, kPartTileNarrow = 1024;
 constexpr uint32_t kPartThreads = 256;    // partition (and select bookkeeping) workgroup
-template <bool STABLE>
-constexpr uint32_t kPartMasksOf = kPartTileOf<STABLE> / 64;  // wave64 ballot masks per partition tile
 constexpr uint32_t kSelectThreads = 256;
 constexpr uint32_t kHistThreads = 1024;
 constexpr int kHistUnroll = 2;          // rows per thread per histogram batch
@@ -177,7 +176,7 @@ struct Tree {
   uint32_t compact;                          // the root's rows are the kept rows of a subsample
   uint32_t fused_level0;                     // the root histogram's workgroup 0 runs level0_setup
   uint32_t stable;                           // stable partition (k_part_count before k_apply)
-  uint32_t part_tile;                        // rows per partition task (kPartTileOf<stable>)
+  uint32_t part_tile;                        // rows per partition task
   uint64_t hist_entry;                       // int64 words per node histogram
   uint64_t group_stride;                     // bytes between feature groups' codes (see MgbMatrix)
   MgbSplitParams sp;
@@ -2057,8 +2056,6 @@ __device__ __forceinline__ bool goes_left(const Tree& t, const NodeOp& op, uint3
   return (int32_t)code <= op.last_left_bin;
 }
 
-template <bool STABLE>
-constexpr int kPartPerOf = (int)(kPartTileOf<STABLE> / kPartThreads);  // rows per thread, all loaded up front
 
 // Row ids of a partition tile for this thread (positions begin + k*256 + tid).
 template <bool IDENTITY, int PER>
@@ -2134,11 +2131,11 @@ __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
 // each child keeps the parent's row order (kernels/boost.metal:1550-1614).
 // No workgroup waits for or signals another: the counts cross to k_apply
 // at the kernel boundary.
-template <typename BinT, bool IDENTITY>
+template <typename BinT, bool IDENTITY, int PER>
 __global__ __launch_bounds__(kPartThreads) void k_part_count(Tree t, uint32_t depth) {
   constexpr uint32_t kWaves = kPartThreads / kWave;
-  constexpr int kPartPer = kPartPerOf<true>;
-  constexpr uint32_t kPartMasks = kPartMasksOf<true>;
+  constexpr int kPartPer = PER;                      // rows per thread, all loaded up front
+  constexpr uint32_t kPartMasks = PER * kWaves;      // wave64 ballot masks per tile
   __shared__ uint32_t wave_left[kPartMasks];
   const LevelState* st = t.state;
   const uint32_t ntasks = st->n_part[depth & 1];
@@ -2236,7 +2233,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_final_order(Tree t, uint32_t 
 // per row).  STABLE: the tile's directions and positions come from
 // k_part_count instead, and each child keeps the parent's row order.  Rows of
 // nodes that stop here get their leaf added to the training margin.
-template <typename BinT, bool IDENTITY, bool STABLE>
+template <typename BinT, bool IDENTITY, bool STABLE, int PER>
 __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) {
   extern __shared__ __align__(16) uint8_t apply_stage[];  // dense-root staging (depth 0 only)
   if (blockIdx.x == gridDim.x - 1) {
@@ -2244,9 +2241,9 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
     return;
   }
   constexpr uint32_t kWaves = kPartThreads / kWave;
-  constexpr uint32_t kPartTile = kPartTileOf<STABLE>;
-  constexpr int kPartPer = kPartPerOf<STABLE>;
-  constexpr uint32_t kPartMasks = kPartMasksOf<STABLE>;
+  constexpr uint32_t kPartTile = PER * kPartThreads;
+  constexpr int kPartPer = PER;                      // rows per thread, all loaded up front
+  constexpr uint32_t kPartMasks = PER * kWaves;      // wave64 ballot masks per tile
   __shared__ uint32_t wave_left[kPartPer][kWaves], wave_active[kPartPer][kWaves];
   __shared__ uint32_t wave_before[kWaves], wave_all[kWaves];  // STABLE: the node's tile counts
   __shared__ uint32_t base_left, base_right;
@@ -2447,7 +2444,7 @@ Layout layout(const MgbTreeShape& s) {
   L.slots = 1u << (depth - 1);
   L.hist_entry = (uint64_t)s.cols * (s.max_bin + 1) * 2;
   L.max_hist_tasks = div_up(s.rows ? s.rows : 1, s.rows_per_tile) + L.slots + 1;
-  const uint32_t part_tile = s.stable_partition ? kPartTileOf<true> : kPartTileOf<false>;
+  const uint32_t part_tile = s.stable_partition && !s.sparse ? kPartTileWide : kPartTileNarrow;
   L.max_part_tasks = div_up(s.rows ? s.rows : 1, part_tile) + 2 * L.slots + 1;
   size_t off = 0;
   L.state = off; off = align_up(off + sizeof(LevelState));
@@ -2471,7 +2468,7 @@ Layout layout(const MgbTreeShape& s) {
       off = align_up(off + (size_t)L.max_hist_tasks * groups * s.features_per_group * (s.max_bin + 1) * 16);
   }
   if (s.stable_partition) {
-    L.part_masks = off; off = align_up(off + (size_t)L.max_part_tasks * kPartMasksOf<true> * sizeof(uint64_t));
+    L.part_masks = off; off = align_up(off + (size_t)L.max_part_tasks * (part_tile / 64) * sizeof(uint64_t));
     L.part_left = off; off = align_up(off + (size_t)L.max_part_tasks * sizeof(uint32_t));
     L.final_order = off; off = align_up(off + ((size_t)L.max_part_tasks + 9) * sizeof(uint32_t));
   } else {
@@ -2572,12 +2569,18 @@ int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
     launch(MGB_PROF_PARTITION, k_final_order, dim3(1), dim3(kOrderThreads), 0, t, depth);
     MGB_LAUNCH_CHECK("k_final_order");
   } else if (t.stable) {
-    launch(MGB_PROF_PARTITION, identity ? k_part_count<BinT, true> : k_part_count<BinT, false>, dim3(grid),
-           dim3(kPartThreads), 0, t, depth);
+    const bool wide = t.part_tile == kPartTileWide;
+    auto count = identity ? (wide ? k_part_count<BinT, true, 8> : k_part_count<BinT, true, 4>)
+                          : (wide ? k_part_count<BinT, false, 8> : k_part_count<BinT, false, 4>);
+    launch(MGB_PROF_PARTITION, count, dim3(grid), dim3(kPartThreads), 0, t, depth);
     MGB_LAUNCH_CHECK("k_part_count");
   }
-  auto fn = identity ? (t.stable ? k_apply<BinT, true, true> : k_apply<BinT, true, false>)
-                     : (t.stable ? k_apply<BinT, false, true> : k_apply<BinT, false, false>);
+  static_assert(kPartTileWide == 8 * kPartThreads && kPartTileNarrow == 4 * kPartThreads, "partition tiles");
+  const bool wide = t.part_tile == kPartTileWide;
+  auto fn = identity ? (t.stable ? (wide ? k_apply<BinT, true, true, 8> : k_apply<BinT, true, true, 4>)
+                                 : k_apply<BinT, true, false, 4>)
+                     : (t.stable ? (wide ? k_apply<BinT, false, true, 8> : k_apply<BinT, false, true, 4>)
+                                 : k_apply<BinT, false, false, 4>);
   if (lds && hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
     set_error("hipFuncSetAttribute(select LDS) failed");
     return -1;
@@ -2651,7 +2654,7 @@ Tree make_tree(const MgbTreeShape* s, const MgbMatrix* m, const Layout& L, uint8
   t.sparse = s->sparse;
   t.compact = s->compact_sampled && !s->sparse ? 1u : 0u;
   t.stable = s->stable_partition ? 1u : 0u;
-  t.part_tile = t.stable ? kPartTileOf<true> : kPartTileOf<false>;
+  t.part_tile = t.stable && !t.sparse ? kPartTileWide : kPartTileNarrow;
   if (t.stable) {
     t.part_masks = reinterpret_cast<uint64_t*>(ws + L.part_masks);
     t.part_left = reinterpret_cast<uint32_t*>(ws + L.part_left);
