@@ -101,6 +101,16 @@ def _same_with_both_partitions(xgb, dtrain, params, rounds):
                                   claims.predict(dtrain, output_margin=True).view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,depth", [(3000, 1), (3000, 2), (9000, 2), (20000, 3)])
+def test_partition_modes_small_grids(xgb, rows, depth):
+    """Shallow trees on few rows: the last level's partition grid has fewer
+    than 8 workgroups (or just 8 and more), so the stable partition's margin
+    updates run in task order or by row range; both modes give the same
+    trees and bit-identical margins."""
+    X, y = W.config1(rows=rows, cols=12)
+    _same_with_both_partitions(xgb, xgb.DMatrix(X, label=y), {"max_depth": depth, "max_bin": 64}, 3)
+
+
 def test_partition_modes_train_identical_models(xgb):
     X, y = W.config1(rows=30000, cols=16)
     _same_with_both_partitions(xgb, xgb.DMatrix(X, label=y), {"max_depth": 7, "max_bin": 128}, 5)

@@ -2261,8 +2261,9 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
   uint32_t op_slot = 0xffffffffu;
   NodeOp op;
   // The last level of a stable partition takes its tasks by row range, XCD
-  // by XCD (k_final_order); other levels in task order.
-  const bool ordered = STABLE && depth + 1 >= t.max_depth;
+  // by XCD (k_final_order), when every XCD has a partition workgroup; other
+  // levels, and grids of fewer than 8 partition workgroups, in task order.
+  const bool ordered = STABLE && depth + 1 >= t.max_depth && gridDim.x - 1 >= 8;
   const uint32_t xcd = blockIdx.x % 8;
   const uint32_t first = ordered ? t.final_order[t.max_part_tasks + xcd] + blockIdx.x / 8 : blockIdx.x;
   const uint32_t last = ordered ? t.final_order[t.max_part_tasks + xcd + 1] : ntasks;
