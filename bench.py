@@ -4,8 +4,8 @@
 Metric: ms per 100 boosting rounds at 262,144 x 64, depth 8,
 plus histogram-build throughput against MI355X's 8 TB/s HBM peak.
 
-Protocol (the reference's benchmarks/controlled_comparison.py:82-92
-section 2): a step is one fit = xgb.train of 100 rounds on a DMatrix built
+Protocol (the reference's benchmarks/controlled_comparison.py:82-92, with the
+median of three fresh-process fits): a step is one fit = xgb.train of 100 rounds on a DMatrix built
 outside the timer (its values and labels already copied to the GPU), so the
 lazy quantile sketch, bin matrix and base score are inside it; the booster's
 rounds are drained (trees copied back) before the clock stops.  Fits run in
@@ -45,7 +45,7 @@ sys.path.insert(0, str(ROOT / "xgboost-metal_amd" / "python"))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBPS = 8000.0
-REFERENCE_MS_100 = 222.8  # reference Metal engine, 262,144x64 d8, 100 rounds, M5 Ultra
+REFERENCE_MS_100 = 222.8  # the reference's published time: Metal engine, 262,144x64 d8, 100 rounds, M5 Ultra
 
 
 def config2(rows=262144, cols=64, seed=1337):
