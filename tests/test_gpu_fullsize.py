@@ -8,7 +8,8 @@ not depend on the oracle finishing (it would take hours there):
 - the training margins the partition kernels accumulate (the prediction
   cache) equal a fresh prediction that walks the trees, bit for bit;
 - the quantile cuts are strictly increasing per feature, and every split
-  threshold is one of its feature's cuts.
+  threshold is one of its feature's cuts; config 4's 10M x 128 cuts also
+  equal the CPU oracle's bit for bit.
 
 Config 2 at full size is pinned by the reference's published prediction
 hash (test_gpu_parity.py::test_published_prediction_hashes) and the oracle;
@@ -56,15 +57,22 @@ def test_config4_full_size_paths_agree(xgb, config4_data):
 
 
 def test_config4_full_size_cuts(xgb, config4_data):
-    """The sketch's cuts at 10M rows and 1024 bins: strictly increasing per
-    feature, at most max_bin of them, the integer columns' cuts at most one
-    per distinct value (1,000), and every split threshold of a tree one of
-    its feature's cuts."""
+    """The sketch's cuts at 10M rows and 1024 bins equal the CPU oracle's bit
+    for bit for all 128 features (the oracle sketches one feature per
+    thread); and by properties: strictly increasing per feature, at most
+    max_bin of them, the integer columns' cuts at most one per distinct value
+    (1,000), and every split threshold of a tree one of its feature's cuts."""
+    import oracle_lib as O
     X, y = config4_data
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train(dict(W.CONFIG_PARAMS[4], seed=7), d, 1)
     indptr, values = d.get_quantile_cut()
     assert len(indptr) == 129
+    ocuts, ocounts, _ = O.sketch_cuts(X, 1024)
+    np.testing.assert_array_equal(np.diff(indptr), ocounts)
+    for f in range(128):
+        np.testing.assert_array_equal(values[indptr[f]:indptr[f + 1]].view(np.uint32),
+                                      ocuts[f, :ocounts[f]].view(np.uint32), err_msg=f"feature {f}")
     for f in range(128):
         cuts = values[indptr[f]:indptr[f + 1]]
         assert 2 <= len(cuts) <= 1024

@@ -386,3 +386,30 @@ def test_weighted_4096_bin_root_literal(fma):
     assert list(ref["cut_counts"]) == [4096] * 4
     bits = int(np.float32(ref["trees"][0]["base_weight"][0]).view(np.uint32))
     assert bits == W.WEIGHTED_BENCHMARK_ROOT_BITS
+
+
+def test_root_density_changes_the_root_weight():
+    """The reference's root construction (tests/test_scalar_root_statistics.py:
+    10-45): gradients [2^40, -2^40, 3 * 2^-14], Hessians [1, 2, 1], depth 1,
+    the root kept as a leaf (min_split_loss 1e30 stands in for the
+    reference's max_leaves = 1).  A dense root sums feature 0's bins in bin
+    order in binary64, where the first bin (2^40 + 3 * 2^-14, rows 0 and 2)
+    rounds to 2^40 + 2^-12 before the cancellation; a root with a missing
+    value takes the exact integer total, which keeps 3 * 2^-14.  When the root
+    splits, its stored weight comes from the applied children's binary64
+    sums, the rounded value in both cases (tests/test_parent_statistics.py:
+    24-47)."""
+    y = np.zeros(3, np.float32)
+    g = np.asarray([2 ** 40, -2 ** 40, 3 * 2 ** -14], np.float32)
+    h = np.asarray([1, 2, 1], np.float32)
+    rounded = np.float32(-((2.0 ** 40 + 3 * 2.0 ** -14) - 2.0 ** 40) / 5.0)
+    exact = np.float32(-(3 * 2.0 ** -14) / 5.0)
+    assert rounded == np.float32(-2.0 ** -12 / 5.0) and rounded != exact
+    dense = np.asarray([[0, 0], [1, 0], [0, 0]], np.float32)
+    missing = np.asarray([[0, 0], [1, 0], [0, np.nan]], np.float32)
+    for gamma, X, want in [(1e30, dense, rounded), (1e30, missing, exact), (0.0, dense, rounded),
+                           (0.0, missing, rounded)]:
+        params = O.make_params(max_depth=1, max_bin=4, eta=1.0, base_score=0.0, seed=9, min_split_loss=gamma)
+        ref = O.train(X, y, params, 1, custom_grad=g[None, :], custom_hess=h[None, :])
+        assert ref["sizes"][0] == (1 if gamma else 3)
+        assert np.float32(ref["trees"][0][0]["base_weight"]) == want
