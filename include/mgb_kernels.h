@@ -84,12 +84,28 @@ typedef struct {
   float scale_pos_weight, subsample, padding1, padding2;
 } MgbGradParams;
 
-/* Split regularisation (replaces SplitParams, include/metalgb/shared.h:114-119). */
+/* Split regularisation (replaces SplitParams, include/metalgb/shared.h:114-119).
+ * inject_status: a test hook -- its bits are reported in the tree's status
+ * word (see mgb_grow_tree) as if the device had detected them, while every
+ * kernel runs normally; 0 in normal use. */
 typedef struct {
   float reg_lambda, reg_alpha, min_child_weight, max_delta_step;
   float min_split_loss, eta;
   uint32_t max_depth, fma_contract;
+  uint32_t inject_status, padding;
 } MgbSplitParams;
+
+/* Tree status bits (the second word at mgb_grow_tree's node_count), set by
+ * the device when a tree's control state is inconsistent, as the reference's
+ * tree driver sets its error word (kernels/tree_driver.metal.h:56-70).  The
+ * level that finds it stops expanding and writes nothing out of range; the
+ * host refuses the tree (src/tree.cpp:1664-1665). */
+enum {
+  MGB_TREE_STATUS_NODE_ID = 1u,    /* a frontier node's id is outside the tree's node table */
+  MGB_TREE_STATUS_CAPACITY = 2u,   /* children would lie beyond the node table or the frontier */
+  MGB_TREE_STATUS_TASKS = 4u,      /* a level's histogram or partition tasks exceed the workspace */
+  MGB_TREE_STATUS_PARTITION = 8u   /* a child's row count exceeds its parent's */
+};
 
 /* One tree node as the host model consumes it (include/metalgb/shared.h:27-31
  * plus base_weights). */
@@ -182,6 +198,16 @@ int mgb_any_missing(const float* data, uint64_t count, uint32_t* flag);
 /* Output transform of margins: objective 1 (logistic) maps x -> 1/(1+exp(-x)). */
 int mgb_transform(float* data, uint64_t count, uint32_t objective);
 
+/* Host only (no device work): checks one tree's node records as the host
+ * publishes them (src/learner.cpp:36-61 checks the emitted table against the
+ * host replay, src/tree.cpp:1663-1717): status 0; 1 <= count <= max_nodes;
+ * node 0 the root (parent -1); every split node's children are the next two
+ * unused ids in node-id order (left = 2k + 1 for the k-th split node), both
+ * name it as their parent and come after it; leaves have no children and no
+ * feature; split features are below cols and leaf values finite.  Returns 0,
+ * or -1 with the first violation in mgb_last_error(). */
+int mgb_validate_tree(const MgbTreeNode* nodes, uint32_t count, uint32_t status, uint32_t max_nodes, uint32_t cols);
+
 /* Host only (no device work): the permutation std::shuffle(0..n-1) draws over
  * std::mt19937(seed) in the column sample (src/tree.cpp:28-45), with
  * libstdc++'s draws (model 0, x86-64 builds) or libc++'s (model 1, the
@@ -195,7 +221,9 @@ size_t mgb_tree_workspace_bytes(const MgbTreeShape* shape);
  * (src/tree.cpp:455-1029 GPU-driven tree + replay :1663-1717 and the
  * prediction-cache update kernels/boost.metal:1738-1763).  Nothing is
  * synchronised; nodes (2^(max_depth+1)-1 records) and node_count are device
- * pointers filled by the time the stream drains.  features (device, cols
+ * pointers filled by the time the stream drains.  node_count holds two
+ * words: [0] the number of nodes, [1] the tree's status (0, or
+ * MGB_TREE_STATUS_* bits: the tree is not valid).  features (device, cols
  * flags, may be NULL for all) restricts the split search to the tree's
  * column sample (src/tree.cpp:179-180).  monotone (device, cols int32 of -1, 0
  * or 1, may be NULL for none) applies monotone constraints

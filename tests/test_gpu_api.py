@@ -221,3 +221,33 @@ def test_monotone_constraints_by_feature_name(xgb):
     assert _trees(by_name) == _trees(by_position)
     with pytest.raises(ValueError, match="not a subset"):
         xgb.train(dict(base, monotone_constraints={"z": 1}), d, 1)
+
+
+def test_device_status_refuses_round_and_rolls_back(xgb):
+    """A round whose tree the device flags is refused when the model is read
+    (src/learner.cpp:36-61 retire_round, src/tree.cpp:1664-1665): the status
+    word is set from the test parameter hip_inject_tree_status while every
+    kernel runs normally; XGBoostError names the round, the rounds queued
+    after it are dropped with it, and the model keeps the earlier rounds.
+    The training margins are rebuilt from the kept trees, so predictions and
+    further rounds equal those of a model that never saw the refused round."""
+    X, y = W.config1(rows=5000, cols=8)
+    params = {"tree_method": "hist", "max_depth": 4, "max_bin": 32}
+    d = xgb.DMatrix(X, label=y)
+    clean3 = xgb.train(params, d, 3)
+    clean4 = xgb.train(params, d, 4)
+    bst = xgb.Booster(params, [d])
+    for i in range(3):
+        bst.update(d, i)
+    bst.set_param({"hip_inject_tree_status": 2})
+    bst.update(d, 3)
+    bst.set_param({"hip_inject_tree_status": 0})
+    bst.update(d, 4)
+    with pytest.raises(xgb.XGBoostError, match=r"round 3: the device tree is invalid: .*0x2 .*capacity.*1 later"):
+        bst.predict(d)
+    assert bst.num_boosted_rounds() == 3
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), clean3.predict(d).view(np.uint32))
+    bst.update(d, 3)
+    assert bst.num_boosted_rounds() == 4
+    assert _trees(bst) == _trees(clean4)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), clean4.predict(d).view(np.uint32))

@@ -39,7 +39,7 @@ def _grow(p, stable, rows_per_tile=2048):
                            0 if p["weighted"] else 1, 1, 0, 0, 0, 0, 1 if stable else 0)
     sp = MgbSplitParams(1.0, 0.0, 1.0, 0.0, 0.0, 0.3, p["depth"], 1)
     max_nodes = (2 << p["depth"]) - 1
-    nodes, count, margin = D.Device(max_nodes * NODE_BYTES), D.Device(4), D.Device(p["rows"] * 4)
+    nodes, count, margin = D.Device(max_nodes * NODE_BYTES), D.Device(8), D.Device(p["rows"] * 4)
     ws_bytes = D.lib().mgb_tree_workspace_bytes(ctypes.byref(shape))
     ws = D.Device(ws_bytes)
     D.check(D.lib().mgb_grow_tree(ctypes.byref(shape), ctypes.byref(p["m"]), p["bins"].ptr, None, p["cuts"].ptr,

@@ -80,3 +80,67 @@ def test_unsupported_parameters_fail_loudly(xgb):
     d = xgb.DMatrix(np.zeros((4, 2), np.float32), label=np.zeros(4))
     with pytest.raises(xgb.XGBoostError, match="hist"):
         b.update(d, 0)
+
+
+NODE = [("left", "<i4"), ("right", "<i4"), ("parent", "<i4"), ("feature", "<i4"), ("threshold", "<f4"),
+        ("leaf", "<f4"), ("cover", "<f4"), ("gain", "<f4"), ("default_left", "<u4"), ("base_weight", "<f4")]
+
+
+def _validate(nodes, status=0, max_nodes=15, cols=4, count=None):
+    import numpy as np
+    lib = ctypes.CDLL(str(LIB))
+    lib.mgb_last_error.restype = ctypes.c_char_p
+    nodes = np.ascontiguousarray(nodes)
+    rc = lib.mgb_validate_tree(nodes.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint32(len(nodes) if count is None else count),
+                               ctypes.c_uint32(status), ctypes.c_uint32(max_nodes), ctypes.c_uint32(cols))
+    return rc, lib.mgb_last_error().decode()
+
+
+def _depth2_tree():
+    """Root splits (children 1, 2); node 1 splits (children 3, 4); node 2 is a
+    leaf: the node-id order the tree driver emits."""
+    import numpy as np
+    t = np.zeros(5, dtype=np.dtype(NODE))
+    t["left"], t["right"], t["feature"] = -1, -1, -1
+    t["parent"] = [-1, 0, 0, 1, 1]
+    t[0]["left"], t[0]["right"], t[0]["feature"] = 1, 2, 3
+    t[1]["left"], t[1]["right"], t[1]["feature"] = 3, 4, 0
+    return t
+
+
+def _put(t, i, field, value):
+    t[field][i] = value
+
+
+def test_validate_tree_accepts_driver_order():
+    assert _validate(_depth2_tree())[0] == 0
+
+
+@pytest.mark.parametrize("corrupt,message", [
+    (lambda t: _put(t, 1, "left", 5), "not the next unused ids"),
+    (lambda t: _put(t, 3, "parent", 0), "do not name it as their parent"),
+    (lambda t: _put(t, 0, "feature", 4), "splits on feature 4 of 4"),
+    (lambda t: _put(t, 2, "feature", 1), "is a leaf with split feature"),
+    (lambda t: _put(t, 2, "left", 5), "has one child"),
+    (lambda t: _put(t, 0, "parent", 3), "node 0 is not a root"),
+    (lambda t: _put(t, 4, "default_left", 7), "default_left 7"),
+])
+def test_validate_tree_rejects_corrupt_records(corrupt, message):
+    """The checks the learner runs on every queued round's records before it
+    publishes the tree (a refused round raises XGBoostError naming it)."""
+    t = _depth2_tree()
+    corrupt(t)
+    rc, err = _validate(t)
+    assert rc == -1 and message in err
+
+
+def test_validate_tree_rejects_counts_and_status():
+    t = _depth2_tree()
+    rc, err = _validate(t, count=4)  # node 1's children end beyond the count
+    assert rc == -1 and "beyond the node count" in err
+    rc, err = _validate(t, max_nodes=3)
+    assert rc == -1 and "outside [1, 3]" in err
+    rc, err = _validate(t, status=2)
+    assert rc == -1 and "status 0x2" in err and "capacity" in err
+    rc, err = _validate(t, status=0x18)
+    assert rc == -1 and "more rows than its parent" in err and "unknown bits" in err

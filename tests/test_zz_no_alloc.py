@@ -28,7 +28,8 @@ class MgbGradParams(ctypes.Structure):
 class MgbSplitParams(ctypes.Structure):
     _fields_ = [("reg_lambda", ctypes.c_float), ("reg_alpha", ctypes.c_float), ("min_child_weight", ctypes.c_float),
                 ("max_delta_step", ctypes.c_float), ("min_split_loss", ctypes.c_float), ("eta", ctypes.c_float),
-                ("max_depth", ctypes.c_uint32), ("fma_contract", ctypes.c_uint32)]
+                ("max_depth", ctypes.c_uint32), ("fma_contract", ctypes.c_uint32), ("inject_status", ctypes.c_uint32),
+                ("padding", ctypes.c_uint32)]
 
 
 MASS_WORDS = 5640  # MGB_MASS_WORDS
@@ -59,7 +60,7 @@ def _problem(rows, cols, max_bin, depth, G, weighted, seed):
 def _grow(p, noalloc):
     max_nodes = (2 << p["depth"]) - 1
     nodes = D.Device(max_nodes * NODE_BYTES)
-    count = D.Device(4)
+    count = D.Device(8)  # node count, tree status
     margin = D.Device(p["rows"] * 4)
     args_head = (ctypes.byref(p["shape"]), ctypes.byref(p["m"]), p["bins"].ptr, None, p["cuts"].ptr,
                  p["counts"].ptr, p["grad"].ptr, p["scales"].ptr, ctypes.byref(p["sp"]), None, None)
@@ -112,7 +113,7 @@ def test_noalloc_refuses_large_shape_and_timing():
         rc = L.mgb_grow_tree_noalloc(ctypes.byref(p["shape"]), ctypes.byref(p["m"]), p["bins"].ptr, None,
                                      p["cuts"].ptr, p["counts"].ptr, p["grad"].ptr, p["scales"].ptr,
                                      ctypes.byref(p["sp"]), None, None, D.Device(4000 * 4).ptr,
-                                     D.Device(15 * NODE_BYTES).ptr, D.Device(4).ptr)
+                                     D.Device(15 * NODE_BYTES).ptr, D.Device(8).ptr)
     finally:
         D.check(L.mgb_profile_enable(0))
     assert rc == -1

@@ -611,6 +611,68 @@ void std_shuffle(std::vector<uint32_t>& order, std::mt19937& engine, ShuffleMode
   else shuffle_libstdcxx(order, engine);
 }
 
+void set_error(std::string message);  // the library's last-error slot (runtime.hip)
+
+// The first inconsistency of one tree's node records as the device emitted
+// them, or "" (checked before the tree is published, as the reference checks
+// its emitted table against the host replay: src/learner.cpp:36-61,
+// src/tree.cpp:1663-1717).  Split nodes take their children in node-id
+// order: the k-th split node (by id) has children 2k + 1 and 2k + 2.
+static std::string tree_violation(const MgbTreeNode* nodes, uint32_t count, uint32_t status, uint32_t max_nodes,
+                                  uint32_t cols) {
+  if (status) {
+    static const char* const names[] = {"a node id outside the node table", "node or frontier capacity exceeded",
+                                        "task lists exceed the workspace", "a child holds more rows than its parent"};
+    std::string what;
+    for (uint32_t b = 0; b < 4; ++b)
+      if (status & (1u << b)) what += (what.empty() ? "" : ", ") + std::string(names[b]);
+    if (status >> 4) what += (what.empty() ? "" : ", ") + std::string("unknown bits");
+    std::ostringstream hex;
+    hex << std::hex << status;
+    return "the device reported tree status 0x" + hex.str() + " (" + what + ")";
+  }
+  if (count < 1 || count > max_nodes)
+    return "node count " + std::to_string(count) + " is outside [1, " + std::to_string(max_nodes) + "]";
+  if (nodes[0].parent != -1) return "node 0 is not a root (parent " + std::to_string(nodes[0].parent) + ")";
+  uint32_t next = 1;  // the next unused node id
+  for (uint32_t i = 0; i < count; ++i) {
+    const MgbTreeNode& x = nodes[i];
+    const std::string node = "node " + std::to_string(i);
+    if (x.default_left > 1) return node + " has default_left " + std::to_string(x.default_left);
+    if (x.left == -1 && x.right == -1) {
+      if (x.feature != -1) return node + " is a leaf with split feature " + std::to_string(x.feature);
+      continue;
+    }
+    if (x.left < 0 || x.right < 0) return node + " has one child";
+    if ((uint32_t)x.left != next || x.right != x.left + 1)
+      return node + " has children (" + std::to_string(x.left) + ", " + std::to_string(x.right) +
+             "), not the next unused ids (" + std::to_string(next) + ", " + std::to_string(next + 1) + ")";
+    if ((uint32_t)x.right >= count)
+      return node + "'s children lie beyond the node count " + std::to_string(count);
+    if (x.feature < 0 || (uint32_t)x.feature >= cols)
+      return node + " splits on feature " + std::to_string(x.feature) + " of " + std::to_string(cols);
+    if (nodes[x.left].parent != (int32_t)i || nodes[x.right].parent != (int32_t)i)
+      return node + "'s children do not name it as their parent";
+    next += 2;
+  }
+  if (next != count)
+    return "the split nodes' children end at id " + std::to_string(next) + ", not at the node count " +
+           std::to_string(count);
+  return "";
+}
+
+extern "C" int mgb_validate_tree(const MgbTreeNode* nodes, uint32_t count, uint32_t status, uint32_t max_nodes,
+                                 uint32_t cols) {
+  if (!nodes && count) {
+    set_error("mgb_validate_tree: null node records");
+    return -1;
+  }
+  const std::string why = tree_violation(nodes, count, status, max_nodes, cols);
+  if (why.empty()) return 0;
+  set_error(why);
+  return -1;
+}
+
 extern "C" int mgb_std_shuffle(uint32_t seed, uint32_t n, uint32_t model, uint32_t* order, uint32_t* next_draw) {
   if (model > 1 || (n && !order)) return -1;
   std::vector<uint32_t> v(n);
@@ -770,6 +832,9 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
   sp.eta = fnumber("learning_rate", 0.3f);
   sp.max_depth = depth;
   sp.fma_contract = (uint32_t)integer("fma_contract", 1);
+  // Test hook: status bits the device reports for this tree as if it had
+  // found them (every kernel still runs normally); drain() then refuses it.
+  sp.inject_status = (uint32_t)integer("hip_inject_tree_status", 0);
   DeviceBuffer* margin = margin_cache(data);
   const bool profiling = integer("hip_profile", 0) != 0;
   kcheck(mgb_profile_enable(profiling ? 1 : 0), "profile");
@@ -833,12 +898,24 @@ void Learner::drain() {
   rounds.swap(pending_);
   pending_bytes_ = 0;
   for (const Pending& p : rounds) {
-    uint32_t n = 0;
-    std::memcpy(&n, host.data() + p.offset + p.node_bytes, sizeof(uint32_t));
-    require(n >= 1 && n <= p.max_nodes, "device tree driver produced an invalid node count");
+    uint32_t word[2] = {0, 0};  // node count, tree status
+    std::memcpy(word, host.data() + p.offset + p.node_bytes, sizeof(word));
+    const uint32_t n = std::min(word[0], p.max_nodes);
+    const auto* records = reinterpret_cast<const MgbTreeNode*>(host.data() + p.offset);
+    const std::string why = tree_violation(records, word[0], word[1], p.max_nodes, num_feature);
+    if (!why.empty()) {
+      // Every later round took its gradients from this round's margins: drop
+      // them with it, and rebuild the training margins from the trees kept
+      // (src/learner.cpp:36-61 retire_round).
+      const size_t round = trees.size();
+      cache_id_ = 0;
+      cache_trees_ = 0;
+      throw Error("round " + std::to_string(round) + ": the device tree is invalid: " + why +
+                  "; this and the " + std::to_string(rounds.size() - 1 - (&p - rounds.data())) +
+                  " later queued rounds are dropped");
+    }
     Tree tree;
-    tree.nodes.resize(n);
-    std::memcpy(tree.nodes.data(), host.data() + p.offset, (size_t)n * sizeof(MgbTreeNode));
+    tree.nodes.assign(records, records + n);
     trees.push_back(std::move(tree));
   }
 }

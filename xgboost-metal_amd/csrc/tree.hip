@@ -163,6 +163,10 @@ struct Tree {
   MgbTreeNode* nodes;
   int32_t* split_bins;        // per tree node id: the split's last left bin (the walk of dropped rows)
   uint32_t* node_count_out;
+  // The tree's status word (node_count_out + 1; NULL for the histogram-only
+  // entry point): MGB_TREE_STATUS_* bits of inconsistencies the bookkeeping
+  // found, OR-ed in; the tree's set-up starts it at sp.inject_status.
+  uint32_t* status;
   // Shape.
   uint32_t rows_n, cols, max_bin, bins1;     // bins1 = max_bin + 1
   uint32_t row_stride, bin_bytes, missing_code, cut_stride;
@@ -301,6 +305,7 @@ __device__ void level0_setup(const Tree& t) {
     t.cursors[1] = n_root;
     st->node_count = 1;
     st->error = 0;
+    if (t.status) *t.status = t.sp.inject_status;
     t.zero_list[0] = 0;
     Frontier root;
     root.id = 0; root.begin = 0; root.count = n_root; root.parent_slot = 0;
@@ -420,6 +425,9 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
   LevelState* st = t.state;
   Frontier* fr = t.frontier[depth & 1];
   uint32_t pairs = st->n_nodes / 2;
+  __shared__ uint32_t s_status;  // MGB_TREE_STATUS_* bits found by this plan
+  if (threadIdx.x == 0) s_status = 0;
+  __syncthreads();
   const uint32_t* parent_cursors = cursor_bank(t, depth - 1);
   uint32_t* cursors = cursor_bank(t, depth);
   unsigned long long* best = best_bank(t, depth);
@@ -436,6 +444,10 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
       Frontier& rf = fr[2 * p + 1];
       const uint32_t total = lf.count;
       c0 = parent_cursors[2 * lf.parent_slot] - lf.begin;
+      if (c0 > total) {  // the partition left more rows than the parent holds
+        atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_PARTITION);
+        c0 = total;
+      }
       c1 = total - c0;
       lbegin = lf.begin;
       lf.count = c0;
@@ -468,7 +480,9 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     s_end[threadIdx.x] = begin + count;
     __syncthreads();
     const uint32_t nitems = pairs - base < blockDim.x ? pairs - base : blockDim.x;
-    for (uint32_t j = threadIdx.x; j < total_tasks; j += blockDim.x) {
+    if (threadIdx.x == 0 && (uint64_t)carry_tasks + total_tasks > t.max_hist_tasks)
+      atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_TASKS);
+    for (uint32_t j = threadIdx.x; j < total_tasks && carry_tasks + j < t.max_hist_tasks; j += blockDim.x) {
       const uint32_t k = owner_of(s_off, nitems, j);
       const uint32_t b = s_begin[k] + (j - s_off[k]) * t.rows_per_tile;
       const uint32_t e = b + t.rows_per_tile < s_end[k] ? b + t.rows_per_tile : s_end[k];
@@ -479,7 +493,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
       fr[built].first_task = off;
       fr[built].ntiles = tiles;
     }
-    if (zero) t.zero_list[zoff] = built;
+    if (zero && zoff < 2 * t.slots) t.zero_list[zoff] = built;
     carry_tasks += total_tasks;
     carry_zero += total_zero;
     // Partition tasks of both children, in slot order.
@@ -493,7 +507,9 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     s_end[threadIdx.x] = c0;  // left count
     scan_right[threadIdx.x] = c1;
     __syncthreads();
-    for (uint32_t j = threadIdx.x; j < total_part; j += blockDim.x) {
+    if (threadIdx.x == 0 && (uint64_t)carry_part + total_part > t.max_part_tasks)
+      atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_TASKS);
+    for (uint32_t j = threadIdx.x; j < total_part && carry_part + j < t.max_part_tasks; j += blockDim.x) {
       const uint32_t k = owner_of(s_off, nitems, j);
       const uint32_t q = j - s_off[k];
       const bool left = q < s_slot[k];
@@ -505,6 +521,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     carry_part += total_part;
     __syncthreads();
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
     st->n_part[depth & 1] = carry_part;
     st->n_hist_tasks = carry_tasks;
@@ -512,6 +529,14 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
     if (depth < kMaxLevels) {
       st->rows_built[depth] = carry_rows;
       st->nodes_built[depth] = pairs;
+    }
+    if (s_status) {  // the tree is refused: this and the deeper levels get no work
+      st->error |= s_status;
+      if (t.status) atomicOr(t.status, s_status);
+      st->n_part[depth & 1] = 0;
+      st->n_hist_tasks = 0;
+      st->n_zero = 0;
+      st->n_nodes = 0;
     }
   }
 }
@@ -1747,6 +1772,12 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   double* rootfh = rootfg + t.bins1;
   float* rootcut = reinterpret_cast<float*>(rootfh + t.bins1);
   const bool dense_root = depth == 0 && t.dense && n > 0;
+  // Capacities the level's writes must stay within: the node table, the next
+  // frontier bank (2 * slots entries), the histogram and partition task lists.
+  const uint32_t max_nodes = (2u << t.max_depth) - 1u;
+  __shared__ uint32_t s_status;            // MGB_TREE_STATUS_* bits found by this level
+  if (threadIdx.x == 0) s_status = 0;
+  __syncthreads();
   __shared__ uint32_t s_left[kPlanNodes];  // count_plans: each node's left rows
   __shared__ double s_root[4];             // dense root: feature 0's ordered sums, the chosen child's
   __shared__ Frontier s_node;              // dense root: the root's frontier entry,
@@ -1816,11 +1847,17 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   uint32_t carry_expanded = 0, carry_htasks = 0, carry_zero = 0, carry_rows = 0, carry_ptasks = 0;
   for (uint32_t base = 0; base < n; base += blockDim.x) {
     const uint32_t i = base + threadIdx.x;
-    const bool valid = i < n;
+    bool valid = i < n;
     Cand best;
     bool expand = false;
     float applied_w = 0, applied_h = 0, parent_w = 0, total_h = 0;
     Frontier node;
+    if (valid) {
+      if (!dense_root && (fr[i].id < 0 || (uint32_t)fr[i].id >= max_nodes)) {
+        atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_NODE_ID);
+        valid = false;  // nothing of this node is written
+      }
+    }
     if (valid) {
       NodeEval ne;
       if (dense_root) {
@@ -1872,6 +1909,10 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
     uint32_t lcount = 0, htiles = 0, hzero = 0, hrows = 0;
     if (plan_next && valid && expand) {
       lcount = count_plans ? s_left[i] : (uint32_t)((uint64_t)best.lh / unit_q);
+      if (lcount > node.count) {
+        atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_PARTITION);
+        lcount = node.count;
+      }
       const uint32_t rcount = node.count - lcount;
       hrows = lcount <= rcount ? lcount : rcount;
       htiles = div_up(hrows, t.rows_per_tile);
@@ -1895,6 +1936,10 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
       if (node.id == 0) {
         rec->base_weight = parent_w;
         rec->leaf = parent_w * p.eta;
+      }
+      if (expand && ((uint64_t)node_base + 2 * rank + 2 > max_nodes || 2 * rank + 2 > 2 * t.slots)) {
+        atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_CAPACITY);
+        expand = false;  // the children would lie outside the node table or frontier
       }
       if (expand) {
         const int32_t left = (int32_t)(node_base + 2 * rank), right = left + 1;
@@ -1942,7 +1987,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
             b.built = 1;
             b.first_task = hoff;
             b.ntiles = htiles;
-            if (hzero) t.zero_list[zoff] = lcount <= rf.count ? 2 * rank : 2 * rank + 1;
+            if (hzero && zoff < 2 * t.slots) t.zero_list[zoff] = lcount <= rf.count ? 2 * rank : 2 * rank + 1;
             // The next level's partition cursors and best-feature keys.
             uint32_t* nc = cursor_bank(t, depth + 1);
             nc[4 * rank] = lf.begin;
@@ -1968,7 +2013,10 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
       s_end[threadIdx.x] = s_begin[threadIdx.x] + hrows;
       scan_slot[threadIdx.x] = expand ? 2 * rank + (built_left ? 0u : 1u) : 0u;
       __syncthreads();
-      for (uint32_t j = threadIdx.x; j < total_htasks; j += blockDim.x) {
+      if (threadIdx.x == 0 && ((uint64_t)carry_htasks + total_htasks > t.max_hist_tasks ||
+                               (uint64_t)carry_ptasks + total_ptasks > t.max_part_tasks))
+        atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_TASKS);
+      for (uint32_t j = threadIdx.x; j < total_htasks && carry_htasks + j < t.max_hist_tasks; j += blockDim.x) {
         const uint32_t k = owner_of(s_off, nitems, j);
         const uint32_t b = s_begin[k] + (j - s_off[k]) * t.rows_per_tile;
         const uint32_t e = b + t.rows_per_tile < s_end[k] ? b + t.rows_per_tile : s_end[k];
@@ -1985,7 +2033,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
       scan_slot[threadIdx.x] = valid && expand ? 2 * rank : 0u;
       __syncthreads();
       PartTask* ntasks = part_bank(t, depth + 1);
-      for (uint32_t j = threadIdx.x; j < total_ptasks; j += blockDim.x) {
+      for (uint32_t j = threadIdx.x; j < total_ptasks && carry_ptasks + j < t.max_part_tasks; j += blockDim.x) {
         const uint32_t k = owner_of(s_off, nitems, j);
         const uint32_t q = j - s_off[k];
         const uint32_t lt = div_up(s_end[k], t.part_tile);
@@ -2018,6 +2066,16 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
     st->node_count = node_base + 2 * carry_expanded;
     st->n_nodes = final_level ? 0 : 2 * carry_expanded;  // becomes the next level's frontier size
     if (t.node_count_out) *t.node_count_out = node_base + 2 * carry_expanded;
+    if (s_status) {
+      // The tree is refused; the deeper levels get no work (the reference's
+      // driver returns early once its error word is set).
+      st->error |= s_status;
+      if (t.status) atomicOr(t.status, s_status);
+      st->n_nodes = 0;
+      st->n_hist_tasks = 0;
+      st->n_zero = 0;
+      st->n_part[(depth + 1) & 1] = 0;
+    }
   }
 }
 
@@ -2730,6 +2788,7 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
   Tree t = make_tree(shape, m, L, reinterpret_cast<uint8_t*>(workspace));
   t.bins = bins; t.columns = columns; t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
+  t.status = node_count ? node_count + 1 : nullptr;
   t.allowed = features;
   t.monotone = monotone;
   if (t.compact) {
@@ -2898,6 +2957,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
   t.csc_colptr = colptr; t.csc_rows = csc_rows; t.csc_codes = csc_codes;
   t.cuts = cuts; t.counts = counts; t.grad = reinterpret_cast<const float2*>(grad);
   t.scales = scales; t.margin = margin; t.nodes = nodes; t.node_count_out = node_count; t.sp = *sp;
+  t.status = node_count ? node_count + 1 : nullptr;
   t.allowed = features;
   t.monotone = monotone;
   t.column_levels = 0;
