@@ -241,8 +241,10 @@ int mgb_grow_tree(const MgbTreeShape* shape, const MgbMatrix* m, const void* bin
 
 /* mgb_grow_tree without a workspace argument and without allocating: no
  * counterpart in the reference.  For callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving or online-update
- * loops, harnesses that forbid hipMalloc).  The workspace is a static 64 MiB
+ * memory (tight serving or online-update loops, harnesses that forbid
+ * hipMalloc).  The work is queued on the library's own stream, so a HIP graph
+ * capture that the caller begins on another stream does not record it (the
+ * kernels run eagerly, outside the caller's graph).  The workspace is a static 64 MiB
  * device array of the library (one per device, held until the process
  * ends); shapes whose mgb_tree_workspace_bytes exceeds it are rejected with
  * an error, as is a call while per-kernel timing is on (its events are

@@ -1225,15 +1225,16 @@ void oracle_metric_auc(const float* pred, const float* labels, const float* weig
 }
 
 void oracle_cv_folds(uint32_t rows, int nfold, uint32_t seed, int shuffle, int stratified, const float* labels,
-                     int32_t* fold) {
+                     int32_t model, int32_t* fold) {
   uint32_t* order = (uint32_t*)malloc(sizeof(uint32_t) * (rows ? rows : 1));
   for (uint32_t r = 0; r < rows; ++r) order[r] = r;
   if (shuffle && rows > 1) {
-    /* std::shuffle with mt19937(seed), libstdc++'s draws (an x86-64 build of
-     * src/c_api.cpp:1018-1110). */
+    /* std::shuffle with mt19937(seed) (src/c_api.cpp:1018-1110), with
+     * libstdc++'s draws (model 0, an x86-64 build) or libc++'s (model 1, the
+     * reference's macOS builds). */
     OracleMT g;
     oracle_mt_seed(&g, seed);
-    oracle_std_shuffle(order, rows, &g, 0);
+    oracle_std_shuffle(order, rows, &g, model);
   }
   if (stratified) {
     /* Stable insertion sort by label (test sizes are small). */

@@ -137,9 +137,10 @@ void oracle_metric_sum(const float* pred, const float* labels, const float* weig
  * binary64 (kernels/radix_sort.metal.h:427-790). */
 void oracle_metric_auc(const float* pred, const float* labels, const float* weights, uint32_t rows, int pr,
                        double out[3]);
-/* Fold of each row for xgboost.cv (src/c_api.cpp:1018-1110). */
+/* Fold of each row for xgboost.cv (src/c_api.cpp:1018-1110); model selects
+ * std::shuffle's draws as in oracle_std_shuffle. */
 void oracle_cv_folds(uint32_t rows, int nfold, uint32_t seed, int shuffle, int stratified, const float* labels,
-                     int32_t* fold);
+                     int32_t model, int32_t* fold);
 
 #ifdef __cplusplus
 }

@@ -214,9 +214,9 @@ def metric_auc(pred, labels, pr=False, weights=None):
     return out
 
 
-def cv_folds(rows, nfold, seed, shuffle=True, stratified=False, labels=None):
+def cv_folds(rows, nfold, seed, shuffle=True, stratified=False, labels=None, std_shuffle="libstdc++"):
     fold = np.zeros(max(rows, 1), np.int32)
     y = None if labels is None else np.ascontiguousarray(labels, np.float32)
     lib().oracle_cv_folds(ctypes.c_uint32(rows), ctypes.c_int(nfold), ctypes.c_uint32(seed), ctypes.c_int(int(shuffle)),
-                          ctypes.c_int(int(stratified)), ptr(y), ptr(fold))
+                          ctypes.c_int(int(stratified)), ptr(y), ctypes.c_int32(SHUFFLE_MODELS[std_shuffle]), ptr(fold))
     return fold[:rows]

@@ -212,9 +212,12 @@ def test_cv_shuffle_follows_libstdcxx_draws():
     np.testing.assert_array_equal(O.cv_folds(rows, nfold, seed), expect)
 
 
+@pytest.mark.parametrize("model", ["libstdc++", "libc++"])
 @pytest.mark.parametrize("stratified", [False, True])
-def test_library_cv_folds_match_oracle(xgb, stratified):
-    """XGDMatrixBuildCVFolds: each fold's test rows are the oracle's."""
+def test_library_cv_folds_match_oracle(xgb, stratified, model):
+    """XGDMatrixBuildCVFolds: each fold's test rows are the oracle's, with the
+    shuffle draws of the standard library the global config's std_shuffle
+    names (the default libstdc++; libc++ as the reference's macOS builds)."""
     import ctypes
     rows, nfold, seed = 61, 5, 9
     X = np.arange(rows * 2, dtype=np.float32).reshape(rows, 2)
@@ -222,9 +225,15 @@ def test_library_cv_folds_match_oracle(xgb, stratified):
     d = xgb.DMatrix(X, label=y)
     c_train = (ctypes.c_void_p * nfold)()
     c_test = (ctypes.c_void_p * nfold)()
-    assert xgb.core._LIB.XGDMatrixBuildCVFolds(d.handle, nfold, ctypes.c_uint(seed), 1, int(stratified), c_train,
-                                               c_test) == 0
-    expect = O.cv_folds(rows, nfold, seed, stratified=stratified, labels=y)
+    assert xgb.get_config()["std_shuffle"] == "libstdc++"
+    with xgb.config_context(std_shuffle=model):
+        assert xgb.get_config()["std_shuffle"] == model
+        assert xgb.core._LIB.XGDMatrixBuildCVFolds(d.handle, nfold, ctypes.c_uint(seed), 1, int(stratified), c_train,
+                                                   c_test) == 0
+    assert xgb.get_config()["std_shuffle"] == "libstdc++"
+    expect = O.cv_folds(rows, nfold, seed, stratified=stratified, labels=y, std_shuffle=model)
+    if model != "libstdc++" and not stratified:
+        assert not np.array_equal(expect, O.cv_folds(rows, nfold, seed))  # the two models draw differently
     for k in range(nfold):
         test = xgb.DMatrix(ctypes.c_void_p(c_test[k]))
         train = xgb.DMatrix(ctypes.c_void_p(c_train[k]))

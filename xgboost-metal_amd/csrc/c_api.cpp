@@ -37,6 +37,7 @@ thread_local Json g_global_config = [] {
   j["verbosity"] = Json((int64_t)1);
   j["use_rmm"] = Json(false);
   j["nthread"] = Json((int64_t)0);
+  j["std_shuffle"] = Json("libstdc++");  // xgb.cv's fold shuffle (XGDMatrixBuildCVFolds)
   return j;
 }();
 void (*g_log_callback)(const char*) = nullptr;
@@ -1481,10 +1482,20 @@ int XGDMatrixBuildCVFolds(DMatrixHandle handle, int nfold, unsigned seed, int sh
   std::shared_ptr<DMatrix> m = matrix(handle);
   const uint32_t nrows = m->rows;
   require((uint32_t)nfold <= nrows, "Number of folds cannot exceed number of rows.");
+  // The shuffle draws follow the standard library the global config's
+  // "std_shuffle" names, as the column sample follows the booster parameter
+  // of that name: "libstdc++" (the default, stock XGBoost's x86-64 builds)
+  // or "libc++" (the reference's macOS builds).
+  ShuffleModel model = ShuffleModel::libstdcxx;
+  if (g_global_config.contains("std_shuffle")) {
+    const Json& name = g_global_config.at("std_shuffle");
+    require(name.is_string(), "std_shuffle must be \"libstdc++\" or \"libc++\".");
+    model = shuffle_model(name.string());
+  }
   std::mt19937 rng(seed);
   std::vector<uint32_t> order(nrows);
   for (uint32_t r = 0; r < nrows; ++r) order[r] = r;
-  if (shuffle && nrows > 1) std_shuffle(order, rng, ShuffleModel::libstdcxx);
+  if (shuffle && nrows > 1) std_shuffle(order, rng, model);
   std::vector<int> fold(nrows, 0);
   if (stratified) {
     const auto& y = m->labels;

@@ -383,7 +383,10 @@ __device__ __forceinline__ void two_sum_add(double& s, double& c, double x) {
 // strided share of the rows, then over the workgroups' partials by the last
 // workgroup; the mean is rounded once to binary32.  Products of two binary32
 // values are exact in binary64, and the compensated sums carry about twice
-// binary64's precision, so the result does not depend on the summation order.
+// binary64's precision.  The workgroup count and the combining tree are fixed
+// for a given row count, so the result is deterministic for a given row
+// count; the compensation terms themselves are added plainly, so another
+// tree of partial sums could round differently in the last bits.
 constexpr uint32_t kBaseThreads = 1024;
 constexpr uint32_t kBaseBlocks = 256;
 __device__ double g_base_partials[kBaseBlocks][4];

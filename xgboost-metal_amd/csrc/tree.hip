@@ -613,8 +613,9 @@ __global__ __launch_bounds__(kReduceWaves * kWave) void k_reduce_hist(Tree t, ui
 // whatever the bins are (a feature-major layout leaves the banks to the
 // data, about twice the conflict cycles).  Gradients are quantized
 // on the fly: q = (int64) rint(g * scale), exactly as a stored int64 pair.
-// The flush is a plain store when the tile is the node's only tile, else a
-// 64-bit global atomic add into a cleared histogram.
+// The flush is a plain store: into the node's histogram when the tile is the
+// node's only tile, else into the tile's own partial histogram, which the
+// split kernel sums (no device-scope atomics across XCDs).
 // ---------------------------------------------------------------------------
 template <typename BinT, int G>
 struct Codes {

@@ -5,6 +5,7 @@ with depthwise growth: DMatrix, QuantileDMatrix, Booster, train and the
 XGBRegressor/XGBClassifier estimators.
 """
 from . import callback
+from .config import config_context, get_config, set_config
 from .core import Booster, DataIter, DMatrix, QuantileDMatrix, XGBoostError, build_info
 from .sklearn import XGBClassifier, XGBModel, XGBRegressor
 from .training import cv, train
@@ -12,4 +13,4 @@ from .training import cv, train
 __version__ = "3.5.0-dev"
 
 __all__ = ["Booster", "callback", "DataIter", "DMatrix", "QuantileDMatrix", "XGBoostError", "XGBClassifier", "XGBModel", "XGBRegressor",
-           "build_info", "cv", "train", "__version__"]
+           "build_info", "config_context", "cv", "get_config", "set_config", "train", "__version__"]

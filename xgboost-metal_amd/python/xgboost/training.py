@@ -14,7 +14,8 @@ The signatures, defaults and results are the reference package's
   standard deviation over the folds of every train/test metric, as a pandas
   DataFrame when pandas is importable (``as_pandas``) and a dict of lists
   otherwise; early stopping keeps the rounds up to the best one.  Folds are
-  built by the library (``XGDMatrixBuildCVFolds``: shuffled or not,
+  built by the library (``XGDMatrixBuildCVFolds``: shuffled or not, with
+  the ``std_shuffle`` parameter's draws like the column sample,
   stratified or not, from ``seed``) unless ``folds`` gives (train, test)
   index pairs or a splitter object.
 """
@@ -26,6 +27,7 @@ from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
 import numpy as np
 
 from .callback import CallbackContainer, EarlyStopping, EvaluationMonitor, TrainingCallback
+from .config import config_context
 from .core import _LIB, Booster, DMatrix, XGBoostError, _check_call
 
 __all__ = ["train", "cv", "XGBoostError"]
@@ -140,13 +142,17 @@ class _FoldSet:
 
 
 def _fold_matrices(dall: DMatrix, nfold: int, seed: int, stratified: bool, shuffle: bool,
-                   folds: Any) -> List[Tuple[DMatrix, DMatrix]]:
+                   folds: Any, std_shuffle: Optional[str] = None) -> List[Tuple[DMatrix, DMatrix]]:
     if folds is None:
         train_handles = (ctypes.c_void_p * nfold)()
         test_handles = (ctypes.c_void_p * nfold)()
-        _check_call(_LIB.XGDMatrixBuildCVFolds(dall.handle, ctypes.c_int(nfold), ctypes.c_uint(int(seed) & 0xFFFFFFFF),
-                                               ctypes.c_int(int(bool(shuffle))), ctypes.c_int(int(bool(stratified))),
-                                               train_handles, test_handles))
+        # The fold shuffle draws like the column sample: the parameters'
+        # std_shuffle, else the global config's (default libstdc++).
+        with config_context(**({} if std_shuffle is None else {"std_shuffle": std_shuffle})):
+            _check_call(_LIB.XGDMatrixBuildCVFolds(dall.handle, ctypes.c_int(nfold),
+                                                   ctypes.c_uint(int(seed) & 0xFFFFFFFF),
+                                                   ctypes.c_int(int(bool(shuffle))), ctypes.c_int(int(bool(stratified))),
+                                                   train_handles, test_handles))
         return [(DMatrix(ctypes.c_void_p(train_handles[k])), DMatrix(ctypes.c_void_p(test_handles[k])))
                 for k in range(nfold)]
     if hasattr(folds, "split"):  # a scikit-learn style splitter
@@ -184,7 +190,8 @@ def cv(params: Any, dtrain: DMatrix, num_boost_round: int = 10, *, nfold: int = 
     np.random.seed(seed)  # as the reference does: splitters that draw from numpy's global generator
     base, chosen = _metric_list(params, metrics)
     fold_list = []
-    for fold_train, fold_test in _fold_matrices(dtrain, nfold, seed, stratified, shuffle, folds):
+    for fold_train, fold_test in _fold_matrices(dtrain, nfold, seed, stratified, shuffle, folds,
+                                                base.get("std_shuffle")):
         fold_params = dict(base)
         if fpreproc is not None:
             fold_train, fold_test, fold_params = fpreproc(fold_train, fold_test, dict(base))
