@@ -310,6 +310,45 @@ def test_csr_sketch_feature_groups_match_oracle(xgb):
 
 
 
+@pytest.mark.parametrize("group_entries", [0, 20000])
+def test_csr_sketch_skewed_columns_match_oracle(xgb, group_entries):
+    """One dense column among 2,000 nearly empty ones (0 to 3 entries each)
+    and a half-dense one: the sketch's run passes take a work list of each
+    column's blocks, so the skew costs no idle workgroups and no block table
+    sized by the longest column.  Cuts and the first tree equal the oracle's
+    with one group and with groups of about 20,000 entries (the dense
+    columns then form groups of their own)."""
+    rows, cols = 60000, 2002
+    rng = np.random.default_rng(41)
+    per_col = [np.arange(rows), np.sort(rng.choice(rows, rows // 2, replace=False))]
+    per_col += [np.sort(rng.choice(rows, k, replace=False)) for k in rng.integers(0, 4, size=cols - 2)]
+    r = np.concatenate(per_col)
+    c = np.concatenate([np.full(len(v), j) for j, v in enumerate(per_col)])
+    v = rng.normal(size=len(r)).astype(np.float32)
+    v[c == 1] = np.round(v[c == 1] * 4)  # runs of equal values in the half-dense column
+    import scipy.sparse as sp
+    csr = sp.csr_matrix((v, (r, c)), shape=(rows, cols))
+    csr.sort_indices()
+    X = W.csr_to_dense(csr.indptr, csr.indices, csr.data, cols)
+    y = (np.nan_to_num(X[:, 0]) + 0.5 * np.nan_to_num(X[:, 1])).astype(np.float32)
+    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 4, "max_bin": 64}
+    ref = O.train(X, y, _oracle_params(params), 1)
+    lib = xgb.core._LIB
+    assert lib.mgb_sketch_group_entries(ctypes.c_uint64(group_entries)) == 0
+    try:
+        d = xgb.DMatrix(csr, label=y)
+        bst = xgb.train(params, d, 1)
+        cut_ptr, cut_values = d.get_quantile_cut()
+    finally:
+        lib.mgb_sketch_group_entries(ctypes.c_uint64(0))
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    for f in range(cols):
+        k = ref["cut_counts"][f]
+        np.testing.assert_array_equal(cut_values[cut_ptr[f]:cut_ptr[f + 1]].view(np.uint32),
+                                      ref["cuts"][f, :k].view(np.uint32), err_msg=f"feature {f}")
+    assert_trees_equal(bst, ref)
+
+
 @pytest.mark.parametrize("max_bin,root_columns", [(64, 1), (256, 1), (1024, 1), (256, 0)])
 def test_csr_regression_matches_oracle(xgb, max_bin, root_columns):
     """Squared error on a config-3 style CSR matrix: cuts, trees and margins

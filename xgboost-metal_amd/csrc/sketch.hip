@@ -59,10 +59,18 @@ constexpr uint32_t kMaxBinSketch = 4096;                 // cut candidates per f
 
 struct SkEntry { float rmin, rmax, wmin, value; };
 struct SkStats { uint32_t nonmissing, elements, runs, padding; };
+// One workgroup of the run passes: up to kRunBlocks consecutive blocks of one
+// feature, starting at block `first` of feature `feature`, whose blocks start
+// at `block_base` in the group's block table.  The host lists them feature
+// after feature, so a launch has exactly one workgroup per item however
+// unequal the features' lengths are.
+struct SkRunItem { uint32_t feature, first, block_base, padding; };
 
 // Runs of one 1024-entry block of a feature.  `runs` counts the block's first
 // valid entry as a run start; k_run_scan fills the offsets and the last valid
-// value before the block.
+// value before the block.  A group's blocks are stored feature after feature
+// (feature c's block b at block_off[c] + b), so the table grows with the
+// group's entries, not with its feature count times its longest feature.
 struct SkBlock {
   uint32_t valid, present, runs, has;
   float first, last;
@@ -147,7 +155,7 @@ __global__ void k_transpose(const float* __restrict__ X, uint32_t rows, uint32_t
   }
 }
 
-// One entry per thread of block blk of feature blockIdx.y: is it
+// One entry per thread of block blk of feature c: is it
 // present (not NaN) and valid (present with a nonzero weight), and the last
 // valid value before it within the block.  Also the block's first and last
 // valid values.  `s_*` hold one slot per wave.
@@ -166,8 +174,7 @@ struct EntryLoad {
 
 __device__ __forceinline__ EntryLoad load_entry(const float* __restrict__ vals, const uint64_t* __restrict__ seg,
                                                 const uint32_t* __restrict__ row_of, const float* __restrict__ weights,
-                                                uint32_t blk) {
-  const uint32_t c = blockIdx.y;
+                                                uint32_t c, uint32_t blk) {
   const uint64_t base = seg[c];
   const uint32_t count = (uint32_t)(seg[c + 1] - base);
   const uint32_t r = blk * kBlockEntries + threadIdx.x;
@@ -214,16 +221,18 @@ __device__ __forceinline__ EntryView view_entry(const EntryLoad& l, uint32_t* s_
 __global__ __launch_bounds__(kSketchThreads) void k_run_count(const float* __restrict__ vals,
                                                               const uint64_t* __restrict__ seg,
                                                               const uint32_t* __restrict__ row_of,
-                                                              const float* __restrict__ weights, uint32_t max_blocks,
+                                                              const float* __restrict__ weights,
+                                                              const SkRunItem* __restrict__ items,
                                                               SkBlock* __restrict__ blocks) {
   __shared__ uint32_t s_has[kSketchThreads / kWave], counts[kSketchThreads / kWave][3];
   __shared__ float s_first[kSketchThreads / kWave], s_last[kSketchThreads / kWave];
-  const uint32_t c = blockIdx.y;
+  const SkRunItem item = items[blockIdx.x];
+  const uint32_t c = item.feature;
   const uint32_t nblocks = (uint32_t)((seg[c + 1] - seg[c] + kBlockEntries - 1) / kBlockEntries);
-  const uint32_t b0 = blockIdx.x * kRunBlocks;
+  const uint32_t b0 = item.first;
   EntryLoad loads[kRunBlocks];
 #pragma unroll
-  for (uint32_t q = 0; q < kRunBlocks; ++q) loads[q] = load_entry(vals, seg, row_of, weights, b0 + q);
+  for (uint32_t q = 0; q < kRunBlocks; ++q) loads[q] = load_entry(vals, seg, row_of, weights, c, b0 + q);
 #pragma unroll
   for (uint32_t q = 0; q < kRunBlocks; ++q) {
     const uint32_t blk = b0 + q;
@@ -245,7 +254,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_count(const float* __res
       SkBlock b{};
       b.valid = valid; b.present = present; b.runs = runs; b.has = has ? 1u : 0u;
       b.first = first; b.last = last;
-      blocks[(uint64_t)c * max_blocks + blk] = b;
+      blocks[(uint64_t)item.block_base + blk] = b;
     }
     __syncthreads();
   }
@@ -254,7 +263,8 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_count(const float* __res
 // One workgroup per feature: offsets of its blocks' elements and runs, with a
 // block whose first valid value equals the last valid value before it
 // continuing that run; the feature's totals.
-__global__ __launch_bounds__(kSketchThreads) void k_run_scan(const uint64_t* __restrict__ seg, uint32_t max_blocks,
+__global__ __launch_bounds__(kSketchThreads) void k_run_scan(const uint64_t* __restrict__ seg,
+                                                             const uint32_t* __restrict__ block_off,
                                                              SkBlock* __restrict__ blocks,
                                                              SkStats* __restrict__ stats) {
   __shared__ uint32_t s_has[kSketchThreads / kWave], scan[kSketchThreads / kWave + 1];
@@ -264,7 +274,7 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_scan(const uint64_t* __r
   const uint32_t c = blockIdx.x;
   const uint64_t count = seg[c + 1] - seg[c];
   const uint32_t nblocks = (uint32_t)((count + kBlockEntries - 1) / kBlockEntries);
-  SkBlock* fb = blocks + (uint64_t)c * max_blocks;
+  SkBlock* fb = blocks + block_off[c];
   const uint32_t lane = lane_id(), wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
   uint32_t elements = 0, runs = 0, present = 0;
   if (threadIdx.x == 0) { carry_has = 0; carry_last = 0.0f; }
@@ -325,26 +335,28 @@ __host__ __device__ inline bool exact_feature(bool weighted, uint32_t elements) 
 __global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __restrict__ vals,
                                                              const uint64_t* __restrict__ seg,
                                                              const uint32_t* __restrict__ row_of,
-                                                             const float* __restrict__ weights, uint32_t max_blocks,
+                                                             const float* __restrict__ weights,
+                                                             const SkRunItem* __restrict__ items,
                                                              const SkBlock* __restrict__ blocks,
                                                              const SkStats* __restrict__ stats,
                                                              uint32_t* __restrict__ keys, uint32_t* __restrict__ run_start,
                                                              float* __restrict__ elem_w) {
   __shared__ uint32_t s_has[kSketchThreads / kWave], scan[2 * (kSketchThreads / kWave + 1)];
   __shared__ float s_first[kSketchThreads / kWave], s_last[kSketchThreads / kWave];
-  const uint32_t c = blockIdx.y;
+  const SkRunItem item = items[blockIdx.x];
+  const uint32_t c = item.feature;
   const uint64_t base = seg[c];
   const uint32_t nblocks = (uint32_t)((seg[c + 1] - base + kBlockEntries - 1) / kBlockEntries);
   const bool exact = exact_feature(weights != nullptr, stats[c].elements);
-  const uint32_t b0 = blockIdx.x * kRunBlocks;
+  const uint32_t b0 = item.first;
   EntryLoad loads[kRunBlocks];
 #pragma unroll
-  for (uint32_t q = 0; q < kRunBlocks; ++q) loads[q] = load_entry(vals, seg, row_of, weights, b0 + q);
+  for (uint32_t q = 0; q < kRunBlocks; ++q) loads[q] = load_entry(vals, seg, row_of, weights, c, b0 + q);
 #pragma unroll
   for (uint32_t q = 0; q < kRunBlocks; ++q) {
     const uint32_t bi = b0 + q;
     if (bi >= nblocks) break;
-    const SkBlock blk = blocks[(uint64_t)c * max_blocks + bi];
+    const SkBlock blk = blocks[(uint64_t)item.block_base + bi];
     bool has = false;
     float first = 0.0f, last = 0.0f;
     EntryView e = view_entry(loads[q], s_has, s_first, s_last, has, first, last);
@@ -367,25 +379,35 @@ __global__ __launch_bounds__(kSketchThreads) void k_run_emit(const float* __rest
 // weights, the binary32 sum of its entries' weights in row order
 // (kernels/quantile.metal.h:19-140).  Exact features sort their entries and
 // need none.
-__global__ void k_run_weights(const uint64_t* __restrict__ seg, const SkStats* __restrict__ stats,
-                              const uint32_t* __restrict__ run_start, const float* __restrict__ elem_w,
-                              float* __restrict__ weight) {
-  const uint32_t c = blockIdx.y;
+// A feature has at most as many runs as entries, so the run items cover its
+// runs too: item (c, b0) takes runs [b0, b0 + kRunBlocks) * kBlockEntries.
+__global__ __launch_bounds__(kSketchThreads) void k_run_weights(const uint64_t* __restrict__ seg,
+                                                                const SkStats* __restrict__ stats,
+                                                                const SkRunItem* __restrict__ items,
+                                                                const uint32_t* __restrict__ run_start,
+                                                                const float* __restrict__ elem_w,
+                                                                float* __restrict__ weight) {
+  const SkRunItem item = items[blockIdx.x];
+  const uint32_t c = item.feature;
   const uint64_t base = seg[c];
   const SkStats st = stats[c];
-  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= st.runs || exact_feature(elem_w != nullptr, st.elements)) return;
-  const uint32_t s = run_start[base + k];
-  const uint32_t e = k + 1 < st.runs ? run_start[base + k + 1] : st.elements;
-  float w;
-  if (!elem_w) {
-    const uint32_t len = e - s;
-    w = (float)(len < (1u << 24) ? len : (1u << 24));
-  } else {
-    w = elem_w[base + s];
-    for (uint32_t i = s + 1; i < e; ++i) w = w + elem_w[base + i];
+  if (exact_feature(elem_w != nullptr, st.elements)) return;
+  for (uint32_t q = 0; q < kRunBlocks; ++q) {
+    const uint64_t k64 = (uint64_t)(item.first + q) * kBlockEntries + threadIdx.x;
+    if (k64 >= st.runs) break;
+    const uint32_t k = (uint32_t)k64;
+    const uint32_t s = run_start[base + k];
+    const uint32_t e = k + 1 < st.runs ? run_start[base + k + 1] : st.elements;
+    float w;
+    if (!elem_w) {
+      const uint32_t len = e - s;
+      w = (float)(len < (1u << 24) ? len : (1u << 24));
+    } else {
+      w = elem_w[base + s];
+      for (uint32_t i = s + 1; i < e; ++i) w = w + elem_w[base + i];
+    }
+    weight[base + k] = w;
   }
-  weight[base + k] = w;
 }
 
 // Merges and prunes walk their inputs in tiles of a merge path (merge-path
@@ -1292,18 +1314,30 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   const uint64_t total = seg[nf];
   // Positions are 32-bit and the segmented sort counts in int.
   if (total >= (1ull << 31)) { set_error("sketch: more than 2^31 - 1 entries in one group"); return -1; }
-  uint64_t longest = 0;
-  for (uint32_t c = 0; c < nf; ++c) longest = std::max<uint64_t>(longest, seg[c + 1] - seg[c]);
-  const uint32_t max_blocks = (uint32_t)std::max<uint64_t>(1, (longest + kBlockEntries - 1) / kBlockEntries);
+  // The run passes' work list: each feature's blocks of kBlockEntries
+  // entries, stored feature after feature (block_off), and its workgroups of
+  // up to kRunBlocks consecutive blocks (items).
+  std::vector<uint32_t> block_off(nf + 1, 0);
+  std::vector<SkRunItem> items;
+  for (uint32_t c = 0; c < nf; ++c) {
+    const uint32_t nblocks = (uint32_t)((seg[c + 1] - seg[c] + kBlockEntries - 1) / kBlockEntries);
+    block_off[c + 1] = block_off[c] + nblocks;
+    for (uint32_t b = 0; b < nblocks; b += kRunBlocks) items.push_back(SkRunItem{c, b, block_off[c], 0u});
+  }
+  if (items.empty()) items.push_back(SkRunItem{0u, 0u, 0u, 0u});  // no entries: one idle workgroup
   const uint64_t E = total ? total : 1;
   Arena a1;
   const uint64_t o_seg = a1.stage(seg);
-  const uint64_t o_blocks = a1.reserve((uint64_t)nf * max_blocks * sizeof(SkBlock));
+  const uint64_t o_block_off = a1.stage(block_off);
+  const uint64_t o_items = a1.stage(items);
+  const uint64_t o_blocks = a1.reserve((uint64_t)std::max<uint32_t>(block_off[nf], 1) * sizeof(SkBlock));
   const uint64_t o_stats = a1.reserve(nf * sizeof(SkStats));
   const uint64_t o_region = a1.reserve(E * 16);
   const uint64_t o_keys_out = a1.reserve(E * 4), o_weight_out = a1.reserve(E * 4);
   if (a1.commit()) return -1;
   const uint64_t* seg_d = a1.at<uint64_t>(o_seg);
+  const uint32_t* block_off_d = a1.at<uint32_t>(o_block_off);
+  const SkRunItem* items_d = a1.at<SkRunItem>(o_items);
   SkBlock* blocks = a1.at<SkBlock>(o_blocks);
   SkStats* stats_d = a1.at<SkStats>(o_stats);
   uint32_t* keys_out = a1.at<uint32_t>(o_keys_out);
@@ -1316,17 +1350,17 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
   uint32_t* weight_in = keys_in + E;
   float* elem_w = reinterpret_cast<float*>(weight_in + E);
   SkEntry* work = a1.at<SkEntry>(o_region);
-  const dim3 grid(max_blocks, nf), run_grid((max_blocks + kRunBlocks - 1) / kRunBlocks, nf);
+  const dim3 run_grid((uint32_t)items.size());
   hipLaunchKernelGGL(k_run_count, run_grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
-                     max_blocks, blocks);
+                     items_d, blocks);
   MGB_LAUNCH_CHECK("k_run_count");
-  hipLaunchKernelGGL(k_run_scan, dim3(nf), dim3(kSketchThreads), 0, s, seg_d, max_blocks,
+  hipLaunchKernelGGL(k_run_scan, dim3(nf), dim3(kSketchThreads), 0, s, seg_d, block_off_d,
                      blocks, stats_d);
   MGB_LAUNCH_CHECK("k_run_scan");
   hipLaunchKernelGGL(k_run_emit, run_grid, dim3(kSketchThreads), 0, s, vals, seg_d, row_of, weights,
-                     max_blocks, blocks, stats_d, keys_in, run_start, elem_w);
+                     items_d, blocks, stats_d, keys_in, run_start, elem_w);
   MGB_LAUNCH_CHECK("k_run_emit");
-  hipLaunchKernelGGL(k_run_weights, grid, dim3(kSketchThreads), 0, s, seg_d, stats_d,
+  hipLaunchKernelGGL(k_run_weights, run_grid, dim3(kSketchThreads), 0, s, seg_d, stats_d, items_d,
                      run_start, weights ? elem_w : nullptr, reinterpret_cast<float*>(weight_in));
   MGB_LAUNCH_CHECK("k_run_weights");
   std::vector<SkStats> stats(nf);
@@ -1460,7 +1494,7 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
   if (!cols) return 0;
   if (rows >= (1u << 31)) { set_error("sketch: rows must be below 2^31"); return -1; }
   // Feature groups of at most group_entries() entries and kMaxGroupFeatures
-  // features (the run passes put the feature in gridDim.y).
+  // features.
   if (bound_device() < 0) return -1;
   const uint32_t group = (uint32_t)std::max<uint64_t>(
       1, std::min<uint64_t>(std::min<uint64_t>(cols, kMaxGroupFeatures), group_entries() / std::max(1u, rows)));
