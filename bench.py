@@ -22,10 +22,14 @@ The roofline object covers the histogram kernel: algorithmic bytes per launch
 (rows built x (F code bytes + 4-byte row id + 8-byte gradient pair) + nodes
 built x F x (max_bin+1) x 16 bytes of int64 histogram output) divided by the
 kernel's duration, measured with HIP events on the library's stream; the
-split kernel's bytes (parent and built histograms read, sibling written) are
-reported the same way.  cpu_baseline trains the CPU oracle (a port of the
-reference's algorithm, OpenMP over features) for the same 100 rounds on the
-host cores, and its predictions are compared with the GPU fit's bit for bit.
+split kernel's bytes (parent and built histograms read, sibling written) and
+the partition's (per row of a splitting node its id, gradient pair and split
+code read and id and pair written; a stopping node's rows their id and
+margin) are reported the same way.  cpu_baseline trains the CPU oracle (a
+port of the reference's algorithm, OpenMP over features) for the same 100
+rounds on the host cores, and its predictions are compared with the GPU fit's
+bit for bit.  The default run also times config 4 (10M x 128, 1024 bins, the
+HBM-bound workload) in one more fresh process and reports it under "c4".
 """
 import argparse
 import hashlib
@@ -123,6 +127,27 @@ def time_rounds(xgb, dtrain, rounds, profile, base=PARAMS):
     return bst, elapsed
 
 
+def rooflines(prof, rounds):
+    """Histogram, split and partition rooflines of profiled rounds: the
+    algorithmic bytes the library counted on the device over the rounds
+    divided by the kernel class's summed HIP-event time."""
+    out = {}
+    specs = [("roofline", "histogram", "histogram_bytes", "k_histogram"),
+             ("split_roofline", "split", "split_bytes", "k_split"),
+             ("partition_roofline", "partition", "partition_bytes",
+              "k_apply (select + partition; with k_part_count and k_final_order under the stable partition)")]
+    for key, kind, field, kernel in specs:
+        k = prof["kernels"][kind]
+        launches = max(k["launches"], 1)
+        achieved = prof[field] / (k["ms"] * 1e-3) / 1e9 if k["ms"] > 0 else 0.0
+        out[key] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "kernel": kernel, "launches": launches,
+                    "algorithmic_bytes_per_launch": round(prof[field] / launches),
+                    "avg_launch_us": round(k["ms"] * 1e3 / launches, 3),
+                    "ms_per_round": round(k["ms"] / max(rounds, 1), 4)}
+    return out
+
+
 def stream_copy_gbps(mib=1024):
     import ctypes
     import device_lib as D
@@ -211,6 +236,8 @@ def main():
                          "c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
     ap.add_argument("--no-ref", action="store_true",
                     help="c2: skip the extra process timing the reference's own 262,144 x 64 workload")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="c2: skip the extra process timing config 4 (10M x 128, 1024 bins, depth 10)")
     ap.add_argument("--param", action="append", default=[], metavar="KEY=VALUE",
                     help="extra booster parameter for the timed rounds (repeatable), e.g. hip_histogram_rows=2048")
     ap.add_argument("--child", action="store_true", help=argparse.SUPPRESS)
@@ -288,11 +315,7 @@ def main():
     bst_p, elapsed_p = time_rounds(xgb, dtrain, 100, profile=True, base=params)
     prof = bst_p.profile()
     kernels = prof["kernels"]
-    hist, split = kernels["histogram"], kernels["split"]
-    launches = max(hist["launches"], 1)
-    split_launches = max(split["launches"], 1)
-    achieved = prof["histogram_bytes"] / (hist["ms"] * 1e-3) / 1e9 if hist["ms"] > 0 else 0.0
-    split_achieved = prof["split_bytes"] / (split["ms"] * 1e-3) / 1e9 if split["ms"] > 0 else 0.0
+    roof = rooflines(prof, 101)
     breakdown = {k: round(v["ms"] / 101, 4) for k, v in kernels.items() if v["launches"]}
 
     copy_gbps = stream_copy_gbps()
@@ -327,16 +350,9 @@ def main():
                                             f"parameters and the same protocol"
                                             + (", its own label generator (README.md:101)" if which == "c2" else
                                                ", the same workload (README.md:98-104)")},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "k_histogram", "launches": launches,
-                     "algorithmic_bytes_per_launch": round(prof["histogram_bytes"] / launches),
-                     "avg_launch_us": round(hist["ms"] * 1e3 / launches, 3)},
-        "split_roofline": {"bound": "hbm", "achieved": round(split_achieved, 1), "peak": HBM_PEAK_GBPS,
-                           "unit": "GB/s", "frac": round(split_achieved / HBM_PEAK_GBPS, 4), "kernel": "k_split",
-                           "launches": split_launches,
-                           "algorithmic_bytes_per_launch": round(prof["split_bytes"] / split_launches),
-                           "avg_launch_us": round(split["ms"] * 1e3 / split_launches, 3)},
+        "roofline": dict(roof["roofline"], traffic=traffic),
+        "split_roofline": roof["split_roofline"],
+        "partition_roofline": roof["partition_roofline"],
         "fits_ms": [round(t, 3) for t in fits],
         "process_median_ms": [round(statistics.median(c["fit_ms"]), 3) for c in children],
         "steady_state_ms_per_100_rounds": round(steady_ms, 3),
@@ -353,6 +369,8 @@ def main():
             children[0]["prediction_sha256"] == published_sha256(which)
     if reference_workload is not None:
         line["reference_workload"] = reference_workload
+    if which == "c2" and not args.no_c4:
+        line["c4"] = run_c4_child(args.param)
     if cpu is not None:
         line["cpu_baseline"] = cpu
         line["parity"]["equal_to_cpu_oracle_bitwise"] = bool(
@@ -377,6 +395,25 @@ LARGE = {
                         "colsample_bytree 0.8; step = one boosting round on the resident bin matrix",
                shape={"rows": 10_000_000, "features": 128, "max_depth": 10, "max_bin": 1024}),
 }
+
+
+def run_c4_child(extra_params=()):
+    """Config 4 in one more fresh process (subprocess, never exec): its own
+    generator, 2 warm-up rounds, 20 timed steady-state rounds; a failure gives
+    the error instead of the object and leaves the config-2 line intact."""
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--config", "c4", "--steps", "20", "--warmup", "2"]
+    for item in extra_params:
+        cmd += ["--param", item]
+    try:
+        out = subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=420)
+        c4 = json.loads(out.stdout.strip().splitlines()[-1])
+    except (subprocess.SubprocessError, ValueError, IndexError) as e:
+        return {"error": f"{type(e).__name__}: {str(e)[:300]}"}
+    print(f"bench: config 4: {c4['value']} ms/200 rounds, histogram {c4['roofline']['frac']} of peak",
+          file=sys.stderr, flush=True)
+    keep = ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "config", "roofline", "split_roofline",
+            "partition_roofline", "kernel_ms_per_round", "one_time_s")
+    return dict({k: c4[k] for k in keep if k in c4}, ms_per_200_rounds=c4["value"])
 
 
 def bench_large(xgb, args, which):
@@ -410,9 +447,7 @@ def bench_large(xgb, args, which):
     bst_p, _ = time_rounds(xgb, dtrain, steps, profile=True, base=spec["params"])
     prof = bst_p.profile()
     kernels = prof["kernels"]
-    hist = kernels["histogram"]
-    launches = max(hist["launches"], 1)
-    achieved = prof["histogram_bytes"] / (hist["ms"] * 1e-3) / 1e9 if hist["ms"] > 0 else 0.0
+    roof = rooflines(prof, steps + 1)
     rounds = spec["rounds"]
     traffic = None
     tfile = ROOT / "profiles" / f"histogram_traffic_config{which[1]}.json"
@@ -423,11 +458,10 @@ def bench_large(xgb, args, which):
         "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 3),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int64", "data": "synthetic",
         "config": dict({"workload": spec["workload"]}, **spec["shape"]),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "k_histogram" if which == "c4" else "k_histogram_csr (+ k_zero_built, k_root_totals)",
-                     "launches": launches, "algorithmic_bytes_per_launch": round(prof["histogram_bytes"] / launches),
-                     "avg_launch_us": round(hist["ms"] * 1e3 / launches, 3)},
+        "roofline": dict(roof["roofline"], traffic=traffic,
+                         kernel="k_histogram" if which == "c4" else "k_histogram_csr (+ k_zero_built, k_root_totals)"),
+        "split_roofline": roof["split_roofline"],
+        "partition_roofline": roof["partition_roofline"],
         "kernel_ms_per_round": {k: round(v["ms"] / (steps + 1), 4) for k, v in kernels.items() if v["launches"]},
         "one_time_s": {"generate": round(gen_s, 2), "dmatrix_sketch_bins_and_warmup": round(setup_s, 2),
                        "quantile_sketch": round(prof0.get("quantiles", 0.0), 3),

@@ -305,6 +305,14 @@ int mgb_predict_csr(const uint64_t* indptr, const uint32_t* indices, const float
  * subtraction), from the last mgb_grow_tree on this workspace; synchronises. */
 int mgb_tree_level_stats(const MgbTreeShape* shape, const void* workspace, uint64_t* rows_built,
                          uint32_t* nodes_built, uint32_t levels);
+/* Rows the partition of each level of the last mgb_grow_tree on this
+ * workspace handled: rows of the nodes that split there (moved into their
+ * children's segments; at the last level given the child's leaf) and rows of
+ * the nodes that stopped there (their leaf added to the margin);
+ * synchronises.  The partition's algorithmic bytes per level follow from
+ * them; a diagnostic, no counterpart in the reference. */
+int mgb_tree_partition_stats(const MgbTreeShape* shape, const void* workspace, uint32_t* rows_split,
+                             uint32_t* rows_leaf, uint32_t levels);
 /* Copies to host memory the row list (shape->rows words) that level `depth`
  * of the last mgb_grow_tree on this workspace read: each node's rows form one
  * segment of it.  Valid for the last two levels of a tree (the list of level

@@ -885,6 +885,22 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
       hist_rows_ += rows[d];
       split_bytes_ += (d == 0 ? 1u : 3u) * (uint64_t)built[d] * node_hist;
     }
+    // Partition (select and apply, and the stable partition's counting pass):
+    // a row of a splitting node reads its id, its gradient pair and the split
+    // feature's code and writes its id and pair into its child's segment
+    // (4 + 8 + s + 4 + 8 bytes); at the last level it reads its id and code
+    // and updates its margin (4 + s + 8); a row of a stopping node reads its
+    // id and updates its margin (4 + 8).  The code s is one bin code of a
+    // dense matrix; a CSR row's lookup reads its offsets, one column index and
+    // the code (8 + 4 + s).  A subsample's dropped rows (their walk of the
+    // finished tree) are not counted.
+    uint32_t moved[32] = {0}, stopped[32] = {0};
+    kcheck(mgb_tree_partition_stats(&shape, d_tree_ws_.get(), moved, stopped, 32), "partition statistics");
+    const uint64_t code = data.sparse ? 8 + 4 + data.csr.bin_bytes : data.matrix.bin_bytes;
+    for (uint32_t d = 0; d < depth && d < 32; ++d) {
+      const uint64_t split_row = d + 1 == depth ? 4 + code + 8 : 4 + 8 + code + 4 + 8;
+      partition_bytes_ += (uint64_t)moved[d] * split_row + (uint64_t)stopped[d] * (4 + 8);
+    }
   }
 }
 
@@ -1345,6 +1361,7 @@ Json Learner::profile() const {
   out["histogram_bytes"] = Json(hist_bytes_);
   out["histogram_rows"] = Json(hist_rows_);
   out["split_bytes"] = Json(split_bytes_);
+  out["partition_bytes"] = Json(partition_bytes_);
   // The last profiled tree, per level: rows and nodes whose histograms were built.
   Json lr = Json::array(), ln = Json::array();
   for (uint64_t v : level_rows_) lr.push_back(Json(v));

@@ -196,7 +196,7 @@ class Learner {
   size_t uploaded_trees_ = 0;
   std::map<std::string, double> seconds_;
   uint64_t rounds_timed_ = 0;
-  uint64_t hist_bytes_ = 0, hist_rows_ = 0, split_bytes_ = 0;
+  uint64_t hist_bytes_ = 0, hist_rows_ = 0, split_bytes_ = 0, partition_bytes_ = 0;
   std::vector<uint64_t> level_rows_;
   std::vector<uint32_t> level_nodes_;
   // The learner's engine (src/learner.cpp:94-103): default-constructed state

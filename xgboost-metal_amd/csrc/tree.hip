@@ -67,6 +67,10 @@ struct LevelState {
   // Per level: rows and nodes whose histograms were built directly.
   uint64_t rows_built[kMaxLevels];
   uint32_t nodes_built[kMaxLevels];
+  // Per level: rows of the nodes that split there and of those that stopped
+  // (the partition's work: moved rows, margin updates).
+  uint32_t rows_split[kMaxLevels];
+  uint32_t rows_leaf[kMaxLevels];
 };
 
 struct Frontier {
@@ -1777,7 +1781,8 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   // frontier bank (2 * slots entries), the histogram and partition task lists.
   const uint32_t max_nodes = (2u << t.max_depth) - 1u;
   __shared__ uint32_t s_status;            // MGB_TREE_STATUS_* bits found by this level
-  if (threadIdx.x == 0) s_status = 0;
+  __shared__ uint32_t s_rows_split, s_rows_leaf;
+  if (threadIdx.x == 0) s_status = s_rows_split = s_rows_leaf = 0;
   __syncthreads();
   __shared__ uint32_t s_left[kPlanNodes];  // count_plans: each node's left rows
   __shared__ double s_root[4];             // dense root: feature 0's ordered sums, the chosen child's
@@ -1942,6 +1947,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
         atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_CAPACITY);
         expand = false;  // the children would lie outside the node table or frontier
       }
+      atomicAdd(expand ? &s_rows_split : &s_rows_leaf, node.count);
       if (expand) {
         const int32_t left = (int32_t)(node_base + 2 * rank), right = left + 1;
         rec->left = left; rec->right = right;
@@ -2067,6 +2073,10 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
     st->node_count = node_base + 2 * carry_expanded;
     st->n_nodes = final_level ? 0 : 2 * carry_expanded;  // becomes the next level's frontier size
     if (t.node_count_out) *t.node_count_out = node_base + 2 * carry_expanded;
+    if (depth < kMaxLevels) {
+      st->rows_split[depth] = s_rows_split;
+      st->rows_leaf[depth] = s_rows_leaf;
+    }
     if (s_status) {
       // The tree is refused; the deeper levels get no work (the reference's
       // driver returns early once its error word is set).
@@ -2998,6 +3008,22 @@ int mgb_tree_level_stats(const MgbTreeShape* shape, const void* workspace, uint6
     bool valid = d < shape->max_depth;
     if (rows_built) rows_built[d] = valid ? st.rows_built[d] : 0;
     if (nodes_built) nodes_built[d] = valid ? st.nodes_built[d] : 0;
+  }
+  return 0;
+}
+
+int mgb_tree_partition_stats(const MgbTreeShape* shape, const void* workspace, uint32_t* rows_split,
+                             uint32_t* rows_leaf, uint32_t levels) {
+  if (!shape || !workspace) { set_error("mgb_tree_partition_stats: null argument"); return -1; }
+  Layout L = layout(*shape);
+  LevelState st;
+  MGB_CHECK(hipMemcpyAsync(&st, reinterpret_cast<const uint8_t*>(workspace) + L.state, sizeof(st),
+                           hipMemcpyDeviceToHost, stream()));
+  MGB_CHECK(hipStreamSynchronize(stream()));
+  for (uint32_t d = 0; d < levels && d < kMaxLevels; ++d) {
+    const bool valid = d < shape->max_depth;
+    if (rows_split) rows_split[d] = valid ? st.rows_split[d] : 0;
+    if (rows_leaf) rows_leaf[d] = valid ? st.rows_leaf[d] : 0;
   }
   return 0;
 }
