@@ -145,6 +145,14 @@ def rooflines(prof, rounds):
                     "algorithmic_bytes_per_launch": round(prof[field] / launches),
                     "avg_launch_us": round(k["ms"] * 1e3 / launches, 3),
                     "ms_per_round": round(k["ms"] / max(rounds, 1), 4)}
+        sampled = prof.get(field.replace("_bytes", "_bytes_sampled_features"))
+        if sampled is not None and sampled != prof[field] and k["ms"] > 0:
+            # With colsample_bytree the kernels touch only the sampled
+            # features; the bytes above count every feature (F in the
+            # survey's formula), these only the sampled ones.
+            a = sampled / (k["ms"] * 1e-3) / 1e9
+            out[key]["sampled_features"] = {"algorithmic_bytes_per_launch": round(sampled / launches),
+                                            "achieved": round(a, 1), "frac": round(a / HBM_PEAK_GBPS, 4)}
     return out
 
 

@@ -878,12 +878,21 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
     // pair reads the parent's and the built child's histograms and writes the
     // sibling's (16 bytes per feature and bin each).
     const uint64_t node_hist = (uint64_t)data.cols * (data.hist_bins + 1) * 16;
+    // The same with only the tree's column sample (dense matrices): the
+    // kernels read, accumulate and write no other feature below the root
+    // (the root also builds feature 0 for its totals).
+    uint64_t sampled = data.cols;
+    if (features && !data.sparse) sampled = std::count(feature_flags_.begin(), feature_flags_.end(), 1u);
+    const double row_bytes_s = data.sparse ? row_bytes : (double)sampled * data.matrix.bin_bytes + 12;
+    const uint64_t node_hist_s = data.sparse ? node_hist : sampled * (data.hist_bins + 1) * 16;
     level_rows_.assign(rows, rows + std::min<uint32_t>(depth, 32));
     level_nodes_.assign(built, built + std::min<uint32_t>(depth, 32));
     for (uint32_t d = 0; d < depth && d < 32; ++d) {
       hist_bytes_ += (uint64_t)(rows[d] * row_bytes) + (uint64_t)built[d] * node_hist;
+      hist_bytes_sampled_ += (uint64_t)(rows[d] * row_bytes_s) + (uint64_t)built[d] * node_hist_s;
       hist_rows_ += rows[d];
       split_bytes_ += (d == 0 ? 1u : 3u) * (uint64_t)built[d] * node_hist;
+      split_bytes_sampled_ += (d == 0 ? 1u : 3u) * (uint64_t)built[d] * node_hist_s;
     }
     // Partition (select and apply, and the stable partition's counting pass):
     // a row of a splitting node reads its id, its gradient pair and the split
@@ -902,6 +911,19 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
       partition_bytes_ += (uint64_t)moved[d] * split_row + (uint64_t)stopped[d] * (4 + 8);
     }
   }
+}
+
+// A round without rows: no gradient and no Hessian, so the root's weight is 0
+// and it cannot split (its Hessian sum is below any min_child_weight); the
+// tree is that single leaf.  Queued rounds are published first, so the trees
+// stay in round order.
+void Learner::empty_round() {
+  drain();
+  MgbTreeNode leaf{};
+  leaf.left = leaf.right = leaf.parent = leaf.feature = -1;
+  Tree tree;
+  tree.nodes.push_back(leaf);
+  trees.push_back(std::move(tree));
 }
 
 void Learner::drain() {
@@ -1361,6 +1383,8 @@ Json Learner::profile() const {
   out["histogram_bytes"] = Json(hist_bytes_);
   out["histogram_rows"] = Json(hist_rows_);
   out["split_bytes"] = Json(split_bytes_);
+  out["histogram_bytes_sampled_features"] = Json(hist_bytes_sampled_);
+  out["split_bytes_sampled_features"] = Json(split_bytes_sampled_);
   out["partition_bytes"] = Json(partition_bytes_);
   // The last profiled tree, per level: rows and nodes whose histograms were built.
   Json lr = Json::array(), ln = Json::array();

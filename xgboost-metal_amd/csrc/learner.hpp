@@ -169,6 +169,8 @@ class Learner {
   void initialize(DMatrix& data, bool custom);
   // sampled: the round's gradients drop rows (subsample < 1), which leave the row list.
   void grow(DMatrix& data, bool unit_hessian, bool sampled);
+  // A round on a matrix without rows: a single leaf of weight 0, no device work.
+  void empty_round();
   void configure_rng();
   int bin_layout() const;
   // Per-round row-sampling parameters (src/learner.cpp:679, src/sampling.cpp:11-17).
@@ -197,6 +199,7 @@ class Learner {
   std::map<std::string, double> seconds_;
   uint64_t rounds_timed_ = 0;
   uint64_t hist_bytes_ = 0, hist_rows_ = 0, split_bytes_ = 0, partition_bytes_ = 0;
+  uint64_t hist_bytes_sampled_ = 0, split_bytes_sampled_ = 0;  // counting only the column sample's features
   std::vector<uint64_t> level_rows_;
   std::vector<uint32_t> level_nodes_;
   // The learner's engine (src/learner.cpp:94-103): default-constructed state

@@ -646,16 +646,19 @@ struct Codes {
     }
   }
   // Codes of G features of one row from the column-major copy (column j at
-  // col0 + j * stride); columns past the group's last feature (fcount) read
-  // the first column instead and are never accumulated.
-  __device__ __forceinline__ void load_cols(const BinT* col0, uint64_t stride, uint32_t row, uint32_t fcount) {
+  // col0 + j * stride).  Only the columns in gmask (the group's features in
+  // the tree's column sample) are accumulated; the others read column
+  // `other` (one of gmask's, so no extra lines) instead: the loads stay
+  // unconditional and the waits exact.
+  __device__ __forceinline__ void load_cols(const BinT* col0, uint64_t stride, uint32_t row, uint32_t gmask,
+                                            uint32_t other) {
     constexpr uint32_t bits = 8 * sizeof(BinT);
     constexpr uint32_t per_word = 64 / bits;
 #pragma unroll
     for (int i = 0; i < kWords; ++i) w[i] = 0;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      const uint32_t jj = (uint32_t)j < fcount ? (uint32_t)j : 0u;
+      const uint32_t jj = (gmask >> j) & 1u ? (uint32_t)j : other;
       const uint64_t code = col0[jj * stride + row];
       w[j / per_word] |= code << ((j % per_word) * bits);
     }
@@ -783,14 +786,29 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
   for (uint32_t j = local; j < xcd_items; j += per_xcd) {
     const HistTask task = IDENTITY ? root_task(t, xcd + 8 * (j / t.groups)) : t.hist_tasks[xcd + 8 * (j / t.groups)];
     const uint32_t group = j % t.groups;
+    const uint32_t fbase = group * G;
+    const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
+    // The group's features in the tree's column sample (bit k: feature
+    // fbase + k; src/tree.cpp:179-180).  The split kernel never scores the
+    // others in this tree: the root does not read their columns and no level
+    // flushes their bins.  A full group still accumulates every feature (a
+    // per-lane feature test costs more vector work than the LDS atomics it
+    // saves: 10M x 128 histograms 4.48 -> 4.59 ms per round); the unsampled
+    // features' LDS bins are simply never written out.  Uniform over the
+    // workgroup.
+    uint32_t gmask = 0;
+    for (uint32_t k = 0; k < fcount; ++k) gmask |= (!t.allowed || t.allowed[fbase + k]) ? 1u << k : 0u;
+    // The root always builds feature 0: its bins give the root's totals (and
+    // a dense root's ordered sums) whether or not the tree samples it.
+    if (IDENTITY && fbase == 0) gmask |= 1u;
+    if (!gmask) continue;
+    const uint32_t first_sampled = (uint32_t)__builtin_ctz(gmask);
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
       lg[i] = 0;
       if constexpr (UNIT) lc[i] = 0;
       else lh[i] = 0;
     }
     __syncthreads();
-    const uint32_t fbase = group * G;
-    const uint32_t fcount = t.cols - fbase < (uint32_t)G ? t.cols - fbase : (uint32_t)G;
     const uint8_t* gbins = bins + (uint64_t)group * t.group_stride;
     const BinT* gcols = COLS ? reinterpret_cast<const BinT*>(t.columns) + (uint64_t)fbase * t.rows_n : nullptr;
     // kU rows per thread per batch, software pipelined: while a batch's LDS
@@ -824,7 +842,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         gh[u] = ghl[valid[u] ? base + u * kHistThreads + threadIdx.x : task.begin];
-        if constexpr (COLS) c[u].load_cols(gcols, t.rows_n, row[u], fcount);
+        if constexpr (COLS) c[u].load_cols(gcols, t.rows_n, row[u], gmask, first_sampled);
         else c[u].load(gbins + (uint64_t)row[u] * t.row_stride);
       }
     };
@@ -867,7 +885,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
           for (int k = 0; k < G; ++k) {
             const uint32_t j = (k + lane) & (G - 1);
             const uint32_t bin = min(rc.get(k), t.max_bin);
-            if (j < fcount) {
+            if ((gmask >> j) & 1u) {
               atomicAdd(&lg[bin * G + j], qg);
               if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
               else atomicAdd(&lh[bin * G + j], qh);
@@ -895,7 +913,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     // lanes of one feature writes consecutive bins of the feature-major output.
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
       const uint32_t bin = i / G, j = i % G;
-      if (j >= fcount) continue;
+      if (!((gmask >> j) & 1u)) continue;
       int64_t g = (int64_t)lg[i];
       int64_t h = UNIT ? (int64_t)((uint64_t)lc[i] * (uint64_t)unit_q) : (int64_t)lh[i];
       reinterpret_cast<int4*>(out)[j * B1 + bin] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
@@ -1555,8 +1573,11 @@ __global__ __launch_bounds__(W == 1 ? 4 * kWave : W * kWave) void k_split(Tree t
   if (depth == 0) {
     if (item >= F) return;  // uniform per item (W > 1: one item per block)
     const uint32_t f = item, count = t.counts[f];
-    // The root's histogram row is always completed: the select kernel's dense
-    // root sums read it (every feature, sampled or not, is reduced here).
+    // A feature outside the tree's column sample has no root histogram (the
+    // histogram kernel skips it), except feature 0, whose row is always
+    // completed: it gives the root's totals and the select kernel's dense
+    // root sums.
+    if (f != 0 && t.allowed && !t.allowed[f]) return;
     const BuiltHist hb = built_hist(t, cur + (uint64_t)f * B1 * 2, t.frontier[0][0], f);
     LaneBins<CH> x;
 #pragma unroll
