@@ -106,17 +106,25 @@ int mgb_device_count(int* count) {
   return 0;
 }
 
+// Device buffers are stream-ordered allocations from the device's default
+// pool on the library's one stream (the reference pools its round buffers,
+// src/learner.cpp:25-35): a booster built after another reuses the pool's
+// mapped memory instead of mapping new pages, and a free neither waits for
+// the device nor unmaps (the pool keeps up to 4 GiB between uses, see
+// mgb_init).  Every use of a buffer is ordered on the same stream, so a
+// freed buffer is handed out again only after the work that used it.
 int mgb_malloc(void** ptr, size_t bytes) {
   if (ensure_init()) return -1;
   *ptr = nullptr;
   if (!bytes) return 0;
-  MGB_CHECK(hipMalloc(ptr, bytes));
+  MGB_CHECK(hipMallocAsync(ptr, bytes, g_stream));
   return 0;
 }
 
 int mgb_free(void* ptr) {
   if (!ptr) return 0;
-  MGB_CHECK(hipFree(ptr));
+  if (ensure_init()) return -1;
+  MGB_CHECK(hipFreeAsync(ptr, g_stream));
   return 0;
 }
 
