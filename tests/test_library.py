@@ -144,3 +144,34 @@ def test_validate_tree_rejects_counts_and_status():
     assert rc == -1 and "status 0x2" in err and "capacity" in err
     rc, err = _validate(t, status=0x18)
     assert rc == -1 and "more rows than its parent" in err and "unknown bits" in err
+
+
+@pytest.mark.parametrize("quantile", [False, True])
+@pytest.mark.parametrize("params", [
+    {"max_depth": 2, "max_bin": 32, "base_score": 0, "seed": 41},
+    {"max_depth": 10, "max_bin": 32, "seed": 41},
+    {"max_depth": 6, "max_bin": 64, "objective": "binary:logistic"},
+])
+def test_empty_matrix_training_matches_oracle(xgb, quantile, params):
+    """Training on a matrix without rows (the reference's 'empty' engine case,
+    tests/test_gpu_tree.py:51-52) needs no device work: every feature's cuts
+    are the empty summary's sentinel 1e-5, the base score is the weighted
+    mean of no labels (0 for squared error, 0.5 for logistic) unless given,
+    and every round's tree is one leaf of weight 0 -- as the oracle trains
+    it.  Prediction on the empty matrix is empty."""
+    import numpy as np
+    import oracle_lib as O
+    from test_gpu_parity import _oracle_params, assert_trees_equal
+    X, y = np.zeros((0, 7), np.float32), np.zeros(0, np.float32)
+    params = dict(params, tree_method="hist")
+    d = xgb.QuantileDMatrix(X, label=y, max_bin=params["max_bin"]) if quantile else xgb.DMatrix(X, label=y)
+    bst = xgb.train(params, d, 3)
+    ref = O.train(X, y, _oracle_params(params), 3)
+    assert_trees_equal(bst, ref)
+    cut_ptr, cut_values = d.get_quantile_cut()
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    np.testing.assert_array_equal(cut_values, np.full(7, 1e-5, np.float32))
+    assert bst.predict(d).shape == (0,)
+    import json
+    stored = json.loads(bst.save_raw("json"))["learner"]["learner_model_param"]["base_score"]
+    assert np.float32(float(stored.strip("[]"))) == np.float32(ref["base_score"])

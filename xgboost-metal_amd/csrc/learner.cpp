@@ -153,7 +153,8 @@ void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
     return;
   }
   require(!is_quantile || quantile_max_bin == max_bin, "Inconsistent max_bin between QuantileDMatrix and Booster.");
-  require(rows > 0 && cols > 0, "Data must contain at least one row and one feature.");
+  require(cols > 0, "Data must contain at least one feature.");
+  if (rows == 0) return quantize_empty(max_bin, layout, group_request);
   upload();
   upload_info();
   auto t0 = std::chrono::steady_clock::now();
@@ -201,6 +202,32 @@ void DMatrix::quantize(uint32_t max_bin, int layout, uint32_t group_request) {
   relayout(layout);
 }
 
+// A matrix without rows (the reference trains on one, tests/test_gpu_tree.py:
+// 51-52): every feature's summary is empty, whose cuts are the tail sentinel
+// of a zero maximum, 0 + (|0| + 1e-5) (kernels/quantile.metal.h:367, the
+// sketch's empty case); a reference matrix's cuts are taken as they are.
+// There is nothing to bin and no device work.
+void DMatrix::quantize_empty(uint32_t max_bin, int layout, uint32_t group_request) {
+  if (cut_source) {
+    take_cuts(max_bin);
+  } else {
+    counts_host.assign(cols, 1u);
+    cuts_host.assign((size_t)cols * max_bin, 0.0f);
+    for (uint32_t f = 0; f < cols; ++f) cuts_host[(size_t)f * max_bin] = 1e-5f;
+  }
+  uint32_t max_count = 1;
+  for (auto c : counts_host) max_count = std::max(max_count, c);
+  hist_bins = max_count;
+  has_missing = false;
+  matrix = MgbMatrix{};
+  matrix.cols = cols;
+  matrix.max_bin = hist_bins;
+  matrix.cut_stride = max_bin;
+  quantized_max_bin = max_bin;
+  quantized_layout = layout;
+  quantized_group_request = group_request;
+}
+
 // Cuts of the reference matrix (QuantileDMatrix ref=, src/c_api.cpp:225-239):
 // evaluation data binned exactly like the training data.
 void DMatrix::take_cuts(uint32_t max_bin) {
@@ -219,7 +246,8 @@ void DMatrix::take_cuts(uint32_t max_bin) {
 // matrix's with NaN at the absent entries); the bins are one code per nonzero.
 void DMatrix::quantize_sparse(uint32_t max_bin) {
   require(!is_quantile || quantile_max_bin == max_bin, "Inconsistent max_bin between QuantileDMatrix and Booster.");
-  require(rows > 0 && cols > 0, "Data must contain at least one row and one feature.");
+  require(cols > 0, "Data must contain at least one feature.");
+  if (rows == 0) return quantize_empty(max_bin, quantized_layout, quantized_group_request);
   const uint64_t nnz = values.size();
   require(nnz < (1ull << 31), "CSR matrices are limited to 2^31 - 1 stored entries.");
   upload();
@@ -429,14 +457,23 @@ void Learner::initialize(DMatrix& data, bool custom) {
     return;
   }
   num_feature = data.cols;
-  feature_names = data.feature_names;
-  feature_types = data.feature_types;
+  // Feature metadata is not taken from a matrix without rows
+  // (src/learner.cpp:297-298).
+  if (data.rows) {
+    feature_names = data.feature_names;
+    feature_types = data.feature_types;
+  }
   int obj = objective();
   auto given = params_.find("base_score");
   if (given != params_.end()) {
     base_score = std::stof(given->second);
   } else if (custom) {
     base_score = 0.5f;
+  } else if (data.rows == 0) {
+    // The weighted mean of no labels: 0 for squared error, else 0.5 (the
+    // rule mgb_base_score applies when the weight sum is not positive).
+    base_score = obj == 0 ? 0.0f : 0.5f;
+    if (obj == 2) base_score = 0.0f;  // logit(0.5)
   } else {
     // src/learner.cpp:316-333: weighted label mean on the device.
     d_base_.ensure(sizeof(float));
@@ -975,6 +1012,7 @@ void Learner::update(DMatrix& data, int /*iteration*/) {
   data.quantize((uint32_t)integer("max_bin", 256), bin_layout(), (uint32_t)integer("hip_histogram_features", 0));
   auto t0 = std::chrono::steady_clock::now();
   initialize(data, false);
+  if (data.rows == 0) return empty_round();
   DeviceBuffer* margin = margin_cache(data);
   d_grad_.ensure((size_t)data.rows * 2 * sizeof(float));
   if (!d_mass_.get()) {
@@ -1006,6 +1044,7 @@ void Learner::boost(DMatrix& data, const float* grad, const float* hess, size_t 
   require(count == data.rows, "Gradient and Hessian must have one entry per row.");
   data.quantize((uint32_t)integer("max_bin", 256), bin_layout(), (uint32_t)integer("hip_histogram_features", 0));
   initialize(data, true);
+  if (data.rows == 0) return empty_round();
   std::vector<float> gh(2 * count);
   for (size_t i = 0; i < count; ++i) { gh[2 * i] = grad[i]; gh[2 * i + 1] = hess[i]; }
   d_grad_.upload(gh.data(), gh.size() * sizeof(float));

@@ -92,6 +92,8 @@ struct DMatrix {
   uint32_t choose_group(uint32_t request) const;
   void relayout(int layout);
   void quantize_sparse(uint32_t max_bin);
+  // A matrix without rows: cuts only (no device work, nothing to bin).
+  void quantize_empty(uint32_t max_bin, int layout, uint32_t group_request);
   void take_cuts(uint32_t max_bin);
   std::shared_ptr<DMatrix> cut_source;  // QuantileDMatrix ref: take its cuts instead of sketching
   uint64_t nonmissing() const;
