@@ -161,6 +161,14 @@ int mgb_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* w
  * flight per launch; the cuts are the same for any size.  No counterpart in
  * the reference (its sketch runs on the host). */
 int mgb_sketch_group_entries(uint64_t entries);
+/* Host only (no device work), a test hook: the ids 0..n-1 of elements with
+ * these keys in the order the sketch's tie sort leaves them -- the device
+ * code that re-sorts a batch whose equal values carry different zero signs
+ * or weights, with libstdc++'s std::sort steps (stock XGBoost's x86-64
+ * build merges equal sketch values in that order; the reference restates
+ * libc++'s, kernels/sketch_sort.metal.h).  Keys compare as the binary32
+ * values of sketch order keys (unsigned compare for keys below 2^31). */
+int mgb_tie_sort_order(const uint32_t* keys, uint32_t n, uint32_t* order);
 /* bin = min(#{cuts <= v}, count-1); NaN -> missing code
  * (kernels/boost.metal:476-499, src/data.cpp:1210-1306).  Sets *any_missing. */
 int mgb_quantize_bins(const float* X, const float* cuts, const uint32_t* counts, const MgbMatrix* m, void* bins,

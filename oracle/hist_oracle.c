@@ -37,6 +37,7 @@
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+#include <stddef.h>
 
 /* ------------------------------------------------------------------------ */
 /* Quantile sketch (weighted quantile summary, XGBoost WQSummary semantics)  */
@@ -137,28 +138,187 @@ static uint32_t sk_combine(SkEntry* cur, uint32_t n, const SkEntry* other, uint3
   return count;
 }
 
-/* Total order on binary32 values with -0 before +0 (values are never NaN). */
-static uint32_t sk_order_key(float v) {
-  uint32_t bits;
-  memcpy(&bits, &v, 4);
-  return bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+/* std::sort as libstdc++ implements it (GCC 11, bits/stl_algo.h and
+ * bits/stl_heap.h), restated for an array of `size`-byte elements ordered by
+ * `less`: introsort with a depth limit of 2 floor(log2 n), the median of the
+ * second, middle and last elements moved to the front as the pivot, an
+ * unguarded partition, heap sort when the depth runs out, and a final
+ * insertion sort (the first 16 elements guarded, the rest unguarded).
+ * Elements that compare equal end in the order these steps leave them: the
+ * order stock XGBoost's x86-64 build merges equal sketch values in
+ * (tests/golden/sort_ties_libstdcxx.json, written by this image's g++, pins
+ * it). */
+typedef int (*sk_less_fn)(const void* a, const void* b);
+typedef struct {
+  char* base;
+  size_t size;
+  sk_less_fn less;
+  uint64_t* heap_sorts; /* heap-sort fallbacks taken (a test statistic; may be NULL) */
+} SkSort;
+#define SK_AT(s, i) ((s)->base + (size_t)(i) * (s)->size)
+
+static void sk_swap(const SkSort* s, size_t a, size_t b) {
+  char t[16];
+  memcpy(t, SK_AT(s, a), s->size);
+  memcpy(SK_AT(s, a), SK_AT(s, b), s->size);
+  memcpy(SK_AT(s, b), t, s->size);
 }
 
-static int sk_run_order(const void* pa, const void* pb) {
-  const SkRun* a = (const SkRun*)pa;
-  const SkRun* b = (const SkRun*)pb;
-  uint32_t ka = sk_order_key(a->value), kb = sk_order_key(b->value);
-  if (ka != kb) return ka < kb ? -1 : 1;
-  return a->order < b->order ? -1 : (a->order > b->order);
+/* __move_median_to_first */
+static void sk_median_to_first(const SkSort* s, size_t result, size_t a, size_t b, size_t c) {
+  if (s->less(SK_AT(s, a), SK_AT(s, b))) {
+    if (s->less(SK_AT(s, b), SK_AT(s, c))) sk_swap(s, result, b);
+    else if (s->less(SK_AT(s, a), SK_AT(s, c))) sk_swap(s, result, c);
+    else sk_swap(s, result, a);
+  } else if (s->less(SK_AT(s, a), SK_AT(s, c))) {
+    sk_swap(s, result, a);
+  } else if (s->less(SK_AT(s, b), SK_AT(s, c))) {
+    sk_swap(s, result, c);
+  } else {
+    sk_swap(s, result, b);
+  }
 }
 
-/* kernels/quantile.metal.h:216-240 (sketch_summarize_ordered).  Runs are
- * sorted by value (-0 before +0) and then by position, and equal values are
- * merged in that order.  The reference instead reproduces libc++'s std::sort
- * permutation for weighted or signed-zero ties (kernels/sketch_sort.metal.h);
- * that tie order is not restated here (parity unpinned for such ties). */
+/* __unguarded_partition */
+static size_t sk_unguarded_partition(const SkSort* s, size_t first, size_t last, size_t pivot) {
+  for (;;) {
+    while (s->less(SK_AT(s, first), SK_AT(s, pivot))) ++first;
+    --last;
+    while (s->less(SK_AT(s, pivot), SK_AT(s, last))) --last;
+    if (!(first < last)) return first;
+    sk_swap(s, first, last);
+    ++first;
+  }
+}
+
+/* __adjust_heap with __push_heap, over elements [first, first + len) */
+static void sk_adjust_heap(const SkSort* s, size_t first, ptrdiff_t hole, ptrdiff_t len, const char* value) {
+  const ptrdiff_t top = hole;
+  ptrdiff_t child = hole;
+  while (child < (len - 1) / 2) {
+    child = 2 * (child + 1);
+    if (s->less(SK_AT(s, first + child), SK_AT(s, first + child - 1))) --child;
+    memcpy(SK_AT(s, first + hole), SK_AT(s, first + child), s->size);
+    hole = child;
+  }
+  if ((len & 1) == 0 && child == (len - 2) / 2) {
+    child = 2 * (child + 1);
+    memcpy(SK_AT(s, first + hole), SK_AT(s, first + child - 1), s->size);
+    hole = child - 1;
+  }
+  ptrdiff_t parent = (hole - 1) / 2;
+  while (hole > top && s->less(SK_AT(s, first + parent), value)) {
+    memcpy(SK_AT(s, first + hole), SK_AT(s, first + parent), s->size);
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  memcpy(SK_AT(s, first + hole), value, s->size);
+}
+
+/* __partial_sort(first, last, last): __make_heap then __sort_heap */
+static void sk_heap_sort(const SkSort* s, size_t first, size_t last) {
+  char value[16];
+  const ptrdiff_t len = (ptrdiff_t)(last - first);
+  if (s->heap_sorts) ++*s->heap_sorts;
+  if (len < 2) return;
+  for (ptrdiff_t parent = (len - 2) / 2;; --parent) {
+    memcpy(value, SK_AT(s, first + parent), s->size);
+    sk_adjust_heap(s, first, parent, len, value);
+    if (parent == 0) break;
+  }
+  for (size_t end = last; end - first > 1;) {
+    --end;
+    memcpy(value, SK_AT(s, end), s->size);
+    memcpy(SK_AT(s, end), SK_AT(s, first), s->size);
+    sk_adjust_heap(s, first, 0, (ptrdiff_t)(end - first), value);
+  }
+}
+
+/* __introsort_loop */
+static void sk_introsort(const SkSort* s, size_t first, size_t last, int depth) {
+  while (last - first > 16) {
+    if (depth == 0) {
+      sk_heap_sort(s, first, last);
+      return;
+    }
+    --depth;
+    const size_t mid = first + (last - first) / 2;
+    sk_median_to_first(s, first, first + 1, mid, last - 1);
+    const size_t cut = sk_unguarded_partition(s, first + 1, last, first);
+    sk_introsort(s, cut, last, depth);
+    last = cut;
+  }
+}
+
+/* __unguarded_linear_insert */
+static void sk_linear_insert(const SkSort* s, size_t last) {
+  char value[16];
+  memcpy(value, SK_AT(s, last), s->size);
+  size_t next = last - 1;
+  while (s->less(value, SK_AT(s, next))) {
+    memcpy(SK_AT(s, last), SK_AT(s, next), s->size);
+    last = next;
+    --next;
+  }
+  memcpy(SK_AT(s, last), value, s->size);
+}
+
+/* __insertion_sort */
+static void sk_insertion_sort(const SkSort* s, size_t first, size_t last) {
+  char value[16];
+  for (size_t i = first + 1; i < last; ++i) {
+    if (s->less(SK_AT(s, i), SK_AT(s, first))) {
+      memcpy(value, SK_AT(s, i), s->size);
+      memmove(SK_AT(s, first + 1), SK_AT(s, first), (i - first) * s->size);
+      memcpy(SK_AT(s, first), value, s->size);
+    } else {
+      sk_linear_insert(s, i);
+    }
+  }
+}
+
+static void sk_std_sort(void* base, size_t n, size_t size, sk_less_fn less, uint64_t* heap_sorts) {
+  if (n < 2) return;
+  const SkSort s = {(char*)base, size, less, heap_sorts};
+  int lg = 0;
+  while (((size_t)2 << lg) <= n) ++lg; /* std::__lg(n): floor(log2 n) */
+  sk_introsort(&s, 0, n, 2 * lg);
+  if (n > 16) {
+    sk_insertion_sort(&s, 0, 16);
+    for (size_t i = 16; i < n; ++i) sk_linear_insert(&s, i);
+  } else {
+    sk_insertion_sort(&s, 0, n);
+  }
+}
+
+/* The sketch entries' order: the value alone (upstream WQSummary's entries
+ * compare values; -0 and +0 are equal). */
+static int sk_run_less(const void* a, const void* b) { return ((const SkRun*)a)->value < ((const SkRun*)b)->value; }
+
+typedef struct { uint32_t key, id; } SkKeyed;
+static int sk_keyed_less(const void* a, const void* b) { return ((const SkKeyed*)a)->key < ((const SkKeyed*)b)->key; }
+
+/* Test hook: the ids 0..n-1 of elements with the given keys, in the order the
+ * restated std::sort leaves them; returns the heap-sort fallbacks taken. */
+uint64_t oracle_std_sort_order(const uint32_t* keys, uint32_t n, uint32_t* order) {
+  SkKeyed* v = (SkKeyed*)malloc(sizeof(SkKeyed) * (n ? n : 1));
+  for (uint32_t i = 0; i < n; ++i) { v[i].key = keys[i]; v[i].id = i; }
+  uint64_t heap_sorts = 0;
+  sk_std_sort(v, n, sizeof(SkKeyed), sk_keyed_less, &heap_sorts);
+  for (uint32_t i = 0; i < n; ++i) order[i] = v[i].id;
+  free(v);
+  return heap_sorts;
+}
+
+/* kernels/quantile.metal.h:216-240 (sketch_summarize_ordered) over a batch of
+ * runs in row order: they are sorted by value with std::sort (libstdc++'s
+ * steps, above) and equal values are merged in the order it leaves them --
+ * the first one's value (the sign of a zero) and the weights added in that
+ * order, as stock XGBoost's x86-64 build merges them (upstream
+ * WQSummary::Queue::MakeSummary).  The reference reproduces libc++'s order
+ * the same way for its macOS builds (kernels/sketch_sort.metal.h). */
 static uint32_t sk_summarize(SkRun* runs, uint32_t size, uint32_t limit, SkEntry* out) {
-  qsort(runs, size, sizeof(SkRun), sk_run_order);
+  sk_std_sort(runs, size, sizeof(SkRun), sk_run_less, NULL);
   uint32_t n = 0;
   float total = 0;
   for (uint32_t i = 0; i < size;) {

@@ -69,6 +69,10 @@ uint32_t oracle_sketch_budget(uint32_t bins, uint32_t count);
 /* cuts: cols*max_bin floats; counts: cols; minima: cols.  weights may be NULL. */
 int oracle_sketch_cuts(const float* X, uint32_t rows, uint32_t cols, const float* weights,
                        uint32_t max_bin, float* cuts, uint32_t* counts, float* minima);
+/* Test hook: ids 0..n-1 of elements with these keys in the order the
+ * sketch's std::sort restatement (libstdc++'s steps) leaves them; returns the
+ * number of heap-sort fallbacks it took. */
+uint64_t oracle_std_sort_order(const uint32_t* keys, uint32_t n, uint32_t* order);
 /* Row-major bins[r*cols+f]; 0xFFFF marks missing. */
 void oracle_quantize(const float* X, uint32_t rows, uint32_t cols, const float* cuts,
                      const uint32_t* counts, uint32_t max_bin, uint16_t* bins);

@@ -687,3 +687,56 @@ def test_monotone_constraints_match_oracle(xgb, case):
     # The constraints bind: the same data trains other trees without them.
     free = xgb.train(dict(params, monotone_constraints="()"), d, 6)
     assert free.trees_to_json() != bst.trees_to_json()
+
+
+def _tie_columns(rows, seed):
+    """Columns whose batches hold ties the merge order decides: integer values
+    (many equal values in separate runs), zeros of both signs in separate
+    runs, and one with thousands of distinct values (more runs a batch)."""
+    rng = np.random.default_rng(seed)
+    X = np.empty((rows, 4), np.float32)
+    signed_zero = np.where(rng.random(rows) < 0.5, np.float32(-0.0), np.float32(0.0))
+    X[:, 0] = rng.integers(-3, 4, rows)
+    X[:, 1] = np.where(rng.random(rows) < 0.5, signed_zero, rng.choice(np.float32([-1.0, 1.0]), rows))
+    X[:, 2] = rng.integers(-2500, 2500, rows)
+    X[:, 3] = np.where(rng.random(rows) < 0.3, signed_zero, X[:, 2])
+    return X
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("rows,max_bin", [(20000, 256), (200000, 1024)])
+def test_sketch_ties_follow_std_sort(weighted, rows, max_bin):
+    """Equal values in different runs are merged in the order libstdc++'s
+    std::sort leaves them (the oracle's restatement, pinned by
+    tests/golden/sort_ties_libstdcxx.json): which zero represents a mixed
+    +0/-0 group and, with weights, the order a group's weights are added in.
+    Batches of up to 8,000 runs are re-sorted in LDS, longer ones (1,024
+    bins) in device memory.  Cuts bit for bit against the oracle."""
+    X = _tie_columns(rows, 5)
+    w = np.random.default_rng(6).uniform(0.1, 3.0, rows).astype(np.float32) if weighted else None
+    cuts, counts = D.sketch_cuts(X, max_bin, w)
+    ocuts, ocounts, _ = O.sketch_cuts(X, max_bin, w)
+    np.testing.assert_array_equal(counts, ocounts)
+    for f in range(X.shape[1]):
+        np.testing.assert_array_equal(cuts[f, :counts[f]].view(np.uint32), ocuts[f, :counts[f]].view(np.uint32),
+                                      err_msg=f"feature {f}")
+
+
+def test_sketch_ties_train_like_oracle(xgb):
+    """The tie columns through training: weighted regression, depth 6, cuts,
+    trees and margins equal the oracle's."""
+    X = _tie_columns(30000, 8)
+    rng = np.random.default_rng(9)
+    y = (X[:, 0] + 0.001 * X[:, 2] + np.signbit(X[:, 1]) + 0.1 * rng.normal(size=len(X))).astype(np.float32)
+    w = rng.uniform(0.1, 3.0, len(X)).astype(np.float32)
+    params = {"objective": "reg:squarederror", "tree_method": "hist", "max_depth": 6, "max_bin": 64}
+    d = xgb.DMatrix(X, label=y, weight=w)
+    bst = xgb.train(params, d, 4)
+    ref = O.train(X, y, _oracle_params(params), 4, weights=w)
+    cut_ptr, cut_values = d.get_quantile_cut()
+    np.testing.assert_array_equal(np.diff(cut_ptr), ref["cut_counts"])
+    for f in range(X.shape[1]):
+        np.testing.assert_array_equal(cut_values[cut_ptr[f]:cut_ptr[f + 1]].view(np.uint32),
+                                      ref["cuts"][f, :ref["cut_counts"][f]].view(np.uint32))
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d).view(np.uint32), ref["margin"].view(np.uint32))

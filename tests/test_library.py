@@ -175,3 +175,28 @@ def test_empty_matrix_training_matches_oracle(xgb, quantile, params):
     import json
     stored = json.loads(bst.save_raw("json"))["learner"]["learner_model_param"]["base_score"]
     assert np.float32(float(stored.strip("[]"))) == np.float32(ref["base_score"])
+
+
+def test_device_tie_sort_follows_libstdcxx():
+    """The sketch kernel's tie sort (run on the host through its test hook,
+    the same code the device runs for a batch with ties the merge order
+    decides) leaves every case of tests/golden/sort_ties_libstdcxx.json in
+    the order this image's libstdc++ std::sort does.  Class k becomes the
+    order key of the non-negative binary32 value whose bits are k, so the
+    values increase with the class (up to 2^30 classes)."""
+    import json
+    import numpy as np
+    from test_oracle import _sort_fixture_keys
+    lib = ctypes.CDLL(str(LIB))
+    fixture = json.loads((ROOT / "tests" / "golden" / "sort_ties_libstdcxx.json").read_text())
+    for case in fixture["cases"]:
+        n = case["n"]
+        cls = _sort_fixture_keys(case["pattern"], n, case["k"], case["seed"]).astype(np.uint32)
+        keys = (cls | np.uint32(0x80000000)).astype(np.uint32)  # order keys of increasing non-negative values
+        order = np.zeros(max(n, 1), np.uint32)
+        assert lib.mgb_tie_sort_order(keys.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint32(n),
+                                      order.ctypes.data_as(ctypes.c_void_p)) == 0
+        order = order[:n].astype(np.uint64)
+        checksum = int((order * (2 * np.arange(n, dtype=np.uint64) + 1)).sum(dtype=np.uint64))
+        assert checksum == case["checksum"], case
+        assert order[:len(case["order"])].tolist() == case["order"], case

@@ -413,3 +413,39 @@ def test_root_density_changes_the_root_weight():
         ref = O.train(X, y, params, 1, custom_grad=g[None, :], custom_hess=h[None, :])
         assert ref["sizes"][0] == (1 if gamma else 3)
         assert np.float32(ref["trees"][0][0]["base_weight"]) == want
+
+
+def _sort_fixture_keys(pattern, n, k, seed):
+    """The key classes tests/golden/make_sort_fixture.cpp sorts."""
+    mask = (1 << 64) - 1
+    x, out = seed, []
+    for i in range(n):
+        x = (x * 6364136223846793005 + 1442695040888963407) & mask
+        out.append({"r": (x >> 33) % k, "a": i * k // n, "d": (n - 1 - i) * k // n,
+                    "o": (i if i < n // 2 else n - 1 - i) % k, "s": (i * 7919) % k}[pattern])
+    return np.asarray(out, np.uint32)
+
+
+def test_sketch_sort_ties_follow_libstdcxx():
+    """The oracle's std::sort restatement (the sketch's batch sort, whose
+    order decides ties between equal values) leaves every fixture case's
+    elements in the order this image's libstdc++ std::sort does: 798 cases of
+    0 to 20,000 elements, random and patterned key classes with 1 to 2^30
+    classes; the patterned cases reach the heap-sort fallback."""
+    import ctypes
+    import json
+    from pathlib import Path
+    lib = O.lib()
+    lib.oracle_std_sort_order.restype = ctypes.c_uint64
+    fixture = json.loads((Path(__file__).parent / "golden" / "sort_ties_libstdcxx.json").read_text())
+    heap_sorts = 0
+    for case in fixture["cases"]:
+        n = case["n"]
+        keys = _sort_fixture_keys(case["pattern"], n, case["k"], case["seed"])
+        order = np.zeros(max(n, 1), np.uint32)
+        heap_sorts += lib.oracle_std_sort_order(O.ptr(keys), ctypes.c_uint32(n), O.ptr(order))
+        order = order[:n].astype(np.uint64)
+        checksum = int((order * (2 * np.arange(n, dtype=np.uint64) + 1)).sum(dtype=np.uint64))
+        assert checksum == case["checksum"], case
+        assert order[:len(case["order"])].tolist() == case["order"], case
+    assert heap_sorts > 0

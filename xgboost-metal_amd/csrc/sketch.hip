@@ -1000,6 +1000,238 @@ __global__ void k_batch_keys(const uint32_t* __restrict__ table, uint32_t count,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tie order.  Stock XGBoost sorts each batch of (value, weight) entries with
+// std::sort on the value alone and merges equal values in the order it
+// leaves them (upstream WQSummary::Queue::MakeSummary): the first one's
+// value represents the group (the sign of a zero) and the weights are added
+// in that order.  The radix sort orders by key, stably, which gives the same
+// summary unless a group of equal values holds both zeros or (run-weighted
+// batches) runs of different weights; such a batch is re-sorted from its
+// runs in row order with libstdc++'s std::sort steps (x86-64 builds; the
+// reference restates libc++'s for its macOS builds,
+// kernels/sketch_sort.metal.h), by one thread, in LDS when it fits.
+// ---------------------------------------------------------------------------
+// The value of an order key, on the host too (the tie sort below runs there
+// for its test hook, mgb_tie_sort_order).
+__host__ __device__ inline float tie_value(uint32_t key) {
+  const uint32_t bits = key ^ ((key & 0x80000000u) ? 0x80000000u : 0xffffffffu);
+  float v;
+  memcpy(&v, &bits, 4);
+  return v;
+}
+
+struct TieRuns {  // element i: (key[i], weight[i]); compared by the key's value
+  uint32_t* key;
+  uint32_t* weight;
+  __host__ __device__ bool less(uint32_t a, uint32_t b) const { return tie_value(key[a]) < tie_value(key[b]); }
+  __host__ __device__ bool less_value(uint32_t a, uint32_t k) const { return tie_value(key[a]) < tie_value(k); }
+  __host__ __device__ bool value_less(uint32_t k, uint32_t b) const { return tie_value(k) < tie_value(key[b]); }
+  __host__ __device__ void swap(uint32_t a, uint32_t b) {
+    const uint32_t k = key[a], w = weight[a];
+    key[a] = key[b]; weight[a] = weight[b];
+    key[b] = k; weight[b] = w;
+  }
+  __host__ __device__ void move(uint32_t to, uint32_t from) { key[to] = key[from]; weight[to] = weight[from]; }
+};
+
+// __adjust_heap with __push_heap over [first, first + len) (value = (vk, vw)).
+__host__ __device__ void tie_adjust_heap(TieRuns& r, uint32_t first, int64_t hole, int64_t len, uint32_t vk, uint32_t vw) {
+  const int64_t top = hole;
+  int64_t child = hole;
+  while (child < (len - 1) / 2) {
+    child = 2 * (child + 1);
+    if (r.less(first + (uint32_t)child, first + (uint32_t)child - 1)) --child;
+    r.move(first + (uint32_t)hole, first + (uint32_t)child);
+    hole = child;
+  }
+  if ((len & 1) == 0 && child == (len - 2) / 2) {
+    child = 2 * (child + 1);
+    r.move(first + (uint32_t)hole, first + (uint32_t)child - 1);
+    hole = child - 1;
+  }
+  int64_t parent = (hole - 1) / 2;
+  while (hole > top && r.less_value(first + (uint32_t)parent, vk)) {
+    r.move(first + (uint32_t)hole, first + (uint32_t)parent);
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  r.key[first + hole] = vk;
+  r.weight[first + hole] = vw;
+}
+
+// std::sort (libstdc++, GCC 11 bits/stl_algo.h) of r[0, n): introsort with
+// depth 2 floor(log2 n) -- the median of the second, middle and last
+// elements moved to the front, an unguarded partition, heap sort when the
+// depth runs out -- then insertion sort (the first 16 guarded, the rest
+// unguarded).  The loop keeps the pending right parts on a stack instead of
+// recursing; sorting disjoint ranges in another order moves the same
+// elements the same way.  The "unguarded" scans also stop at their range's
+// ends: with the median of three in front they never reach them, so the
+// order is unchanged, and no index leaves the range whatever the input.
+__host__ __device__ void tie_std_sort(TieRuns& r, uint32_t n) {
+  if (n < 2) return;
+  int lg = 0;
+  while (((uint64_t)2 << lg) <= n) ++lg;
+  uint32_t stack_first[72], stack_last[72];
+  int stack_depth[72];
+  int top = 0;
+  stack_first[0] = 0; stack_last[0] = n; stack_depth[0] = 2 * lg;
+  top = 1;
+  while (top > 0) {
+    --top;
+    uint32_t first = stack_first[top], last = stack_last[top];
+    int depth = stack_depth[top];
+    while (last - first > 16) {
+      if (depth == 0) {  // __partial_sort(first, last, last): make_heap, sort_heap
+        const int64_t len = last - first;
+        for (int64_t parent = (len - 2) / 2;; --parent) {
+          tie_adjust_heap(r, first, parent, len, r.key[first + parent], r.weight[first + parent]);
+          if (parent == 0) break;
+        }
+        for (uint32_t end = last; end - first > 1;) {
+          --end;
+          const uint32_t vk = r.key[end], vw = r.weight[end];
+          r.move(end, first);
+          tie_adjust_heap(r, first, 0, (int64_t)(end - first), vk, vw);
+        }
+        break;
+      }
+      --depth;
+      const uint32_t mid = first + (last - first) / 2, a = first + 1, b = mid, c = last - 1;
+      if (r.less(a, b)) {
+        if (r.less(b, c)) r.swap(first, b);
+        else if (r.less(a, c)) r.swap(first, c);
+        else r.swap(first, a);
+      } else if (r.less(a, c)) {
+        r.swap(first, a);
+      } else if (r.less(b, c)) {
+        r.swap(first, c);
+      } else {
+        r.swap(first, b);
+      }
+      uint32_t lo = first + 1, hi = last;
+      for (;;) {
+        while (lo + 1 < last && r.less(lo, first)) ++lo;
+        --hi;
+        while (hi > first && r.less(first, hi)) --hi;
+        if (!(lo < hi)) break;
+        r.swap(lo, hi);
+        ++lo;
+      }
+      // Right part [lo, last) is sorted later (the recursion's callee), the
+      // left part [first, lo) now.
+      stack_first[top] = lo; stack_last[top] = last; stack_depth[top] = depth;
+      ++top;
+      last = lo;
+    }
+  }
+  // __final_insertion_sort
+  const uint32_t guarded = n > 16 ? 16 : n;
+  for (uint32_t i = 1; i < guarded; ++i) {
+    const uint32_t vk = r.key[i], vw = r.weight[i];
+    if (r.value_less(vk, 0)) {
+      for (uint32_t j = i; j > 0; --j) r.move(j, j - 1);
+      r.key[0] = vk; r.weight[0] = vw;
+    } else {
+      uint32_t j = i;
+      while (j > 0 && r.value_less(vk, j - 1)) { r.move(j, j - 1); --j; }
+      r.key[j] = vk; r.weight[j] = vw;
+    }
+  }
+  for (uint32_t i = guarded; i < n; ++i) {
+    const uint32_t vk = r.key[i], vw = r.weight[i];
+    uint32_t j = i;
+    while (j > 0 && r.value_less(vk, j - 1)) { r.move(j, j - 1); --j; }
+    r.key[j] = vk; r.weight[j] = vw;
+  }
+}
+
+constexpr uint32_t kTieThreads = 256;
+constexpr uint32_t kTieLdsRuns = 8000;  // runs sorted in LDS (62.5 KiB); longer batches sort in global memory
+
+// One workgroup per batch (the level-0 table): finds whether the batch has a
+// tie the merge order decides and, if so, writes its sorted keys in
+// std::sort's order (run-weighted batches: keys and weights; exact batches,
+// whose weights are all 1 and sum exactly: the zero group's first key).
+// keys_in/weight_in hold each feature's runs (exact: entries) in row order
+// before the sort; elem_w and weight_in are free for an exact feature's runs.
+__global__ __launch_bounds__(kTieThreads) void k_tie_order(const uint32_t* __restrict__ table,
+                                                            const SkFeature* __restrict__ features,
+                                                            const SkStats* __restrict__ stats,
+                                                            const uint32_t* __restrict__ key_begin,
+                                                            const uint32_t* __restrict__ key_end,
+                                                            const uint32_t* __restrict__ run_start,
+                                                            const uint32_t* __restrict__ keys_in,
+                                                            uint32_t* __restrict__ weight_in, uint32_t* __restrict__ elem_w,
+                                                            uint32_t* __restrict__ keys, uint32_t* __restrict__ wts) {
+  __shared__ uint32_t s_flag;
+  __shared__ uint32_t lds_key[kTieLdsRuns], lds_w[kTieLdsRuns];
+  const uint32_t c = table[2 * blockIdx.x], b = table[2 * blockIdx.x + 1];
+  const SkFeature fe = features[c];
+  const SkStats st = stats[c];
+  const uint32_t kb = key_begin[blockIdx.x], size = key_end[blockIdx.x] - kb;
+  if (threadIdx.x == 0) s_flag = 0;
+  __syncthreads();
+  for (uint32_t i = 1 + threadIdx.x; i < size; i += blockDim.x) {
+    const uint32_t ka = keys[kb + i - 1], kz = keys[kb + i];
+    if (key_value(ka) != key_value(kz)) continue;
+    if (ka != kz || (!fe.exact && wts[kb + i - 1] != wts[kb + i])) s_flag = 1;
+  }
+  __syncthreads();
+  if (!s_flag || threadIdx.x != 0) return;
+  // The batch's runs in row order.
+  const uint64_t rb = (uint64_t)b * 2 * fe.limit;
+  const uint32_t n = (uint32_t)std::min<uint64_t>(2ull * fe.limit, st.runs - rb);
+  const uint32_t base = (uint32_t)fe.base;
+  TieRuns r;
+  if (n <= kTieLdsRuns) {
+    r.key = lds_key;
+    r.weight = lds_w;
+  } else if (fe.exact) {
+    r.key = elem_w + base + rb;
+    r.weight = weight_in + base + rb;
+  } else {
+    r.key = keys + kb;  // this batch's sorted output, overwritten in place
+    r.weight = wts + kb;
+  }
+  for (uint32_t j = 0; j < n; ++j) {
+    const uint32_t run = (uint32_t)rb + j;
+    if (fe.exact) {
+      const uint32_t s0 = run_start[base + run];
+      const uint32_t s1 = run + 1 < st.runs ? run_start[base + run + 1] : st.elements;
+      r.key[j] = keys_in[base + s0];
+      r.weight[j] = s1 - s0;  // a run length (the weights of exact features are never summed as floats)
+    } else {
+      r.key[j] = keys_in[base + run];
+      r.weight[j] = weight_in[base + run];
+    }
+  }
+  tie_std_sort(r, n);
+  if (!fe.exact) {
+    if (r.key != keys + kb)
+      for (uint32_t j = 0; j < n; ++j) { keys[kb + j] = r.key[j]; wts[kb + j] = r.weight[j]; }
+    return;
+  }
+  // Exact batch: the zero group keeps its counts; its first key becomes the
+  // zero std::sort puts first.
+  uint32_t first_zero = 0xffffffffu;
+  for (uint32_t j = 0; j < n; ++j)
+    if (key_value(r.key[j]) == 0.0f) { first_zero = r.key[j]; break; }
+  if (first_zero == 0xffffffffu) return;
+  uint32_t z0 = 0xffffffffu, z1 = 0;
+  for (uint32_t i = 0; i < size; ++i)
+    if (key_value(keys[kb + i]) == 0.0f) {
+      if (z0 == 0xffffffffu) z0 = i;
+      if (keys[kb + i] == first_zero) z1 = i;
+    }
+  if (z0 != 0xffffffffu && keys[kb + z0] != first_zero) {
+    const uint32_t t = keys[kb + z0];
+    keys[kb + z0] = keys[kb + z1];
+    keys[kb + z1] = t;
+  }
+}
+
 // Level 0 of every feature's tree: one workgroup per batch summarizes the
 // batch's sorted runs into the feature's work area and prunes the summary to
 // `limit` entries (the serial rule's first step for each batch,
@@ -1450,6 +1682,10 @@ int sketch_group(const float* vals, const std::vector<uint64_t>& seg, const uint
       MGB_CHECK(hipcub::DeviceSegmentedRadixSort::SortPairs(a2.at<void>(o_temp), temp_bytes, keys_in, keys_out,
                                                              weight_in, weight_out, (int)total, (int)run_batches,
                                                              key_b + exact_batches, key_e + exact_batches, 0, 32, s));
+    hipLaunchKernelGGL(k_tie_order, dim3(batches), dim3(kTieThreads), 0, s, a2.at<uint32_t>(o_table0), features_d,
+                       stats_d, key_b, key_e, run_start, keys_in, weight_in, reinterpret_cast<uint32_t*>(elem_w),
+                       keys_out, weight_out);
+    MGB_LAUNCH_CHECK("k_tie_order");
     hipLaunchKernelGGL(k_level0, dim3(batches), dim3(kMergeThreads), 0, s, a2.at<uint32_t>(o_table0), features_d,
                        stats_d, key_b, key_e, keys_out, reinterpret_cast<const float*>(weight_out), work, tree,
                        scratch, node_count);
@@ -1535,6 +1771,16 @@ int mgb_sketch_cuts_csc(const float* values, const uint32_t* row_of, const uint6
     if (sketch_group(values + first, seg, row_of + first, f1 - f0, f0, weights, max_bin, cuts, counts)) return -1;
     f0 = f1;
   }
+  return 0;
+}
+
+int mgb_tie_sort_order(const uint32_t* keys, uint32_t n, uint32_t* order) {
+  if (n && (!keys || !order)) { set_error("mgb_tie_sort_order: null argument"); return -1; }
+  std::vector<uint32_t> k(keys, keys + n), id(n);
+  for (uint32_t i = 0; i < n; ++i) id[i] = i;
+  TieRuns r{k.data(), id.data()};
+  tie_std_sort(r, n);
+  for (uint32_t i = 0; i < n; ++i) order[i] = id[i];
   return 0;
 }
 
