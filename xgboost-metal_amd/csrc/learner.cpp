@@ -810,8 +810,9 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
   // trees are the same either way.  Default: stable from 2^19 rows.  Measured
   // per round: 10M x 128 partition 1.65 ms stable against 2.11 ms by claims
   // (the claims serialize on a large node's two cursors), 1M x 2000 CSR
-  // 0.36 against 0.45 ms; 262,144 x 64 0.113 against 0.094 ms (the extra
-  // launch per level costs more than the few claims there).
+  // 0.36 against 0.45 ms; 262,144 x 64: 39.1 against 35.2 ms per 100 rounds
+  // (the counting pass's extra launch per level costs more than the few
+  // claims there).
   const int64_t stable = integer("hip_stable_partition", -1);
   shape.stable_partition = (stable < 0 ? data.rows >= (1u << 19) : stable != 0) ? 1 : 0;
   {
