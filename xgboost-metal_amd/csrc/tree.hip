@@ -738,6 +738,14 @@ __device__ __forceinline__ void lds_add(uint32_t address, uint32_t v) {
   __hip_atomic_fetch_add((lds_u32_t*)(uintptr_t)address, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Whether a level histogram holds feature f (present: f is one of the
+// group's columns): every feature in the tree's column sample, and at the
+// root feature 0 as well, whose bins give the root's totals (and a dense
+// root's ordered sums) whether or not the tree samples it.
+__device__ __forceinline__ bool sampled(const Tree& t, uint32_t f, bool present, bool root) {
+  return present && (!t.allowed || t.allowed[f] || (root && f == 0));
+}
+
 template <typename BinT, int G, bool UNIT, bool IDENTITY, bool COLS>
 __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t depth) {
   constexpr int kU = kHistUnroll;
@@ -791,17 +799,22 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     // The group's features in the tree's column sample (bit k: feature
     // fbase + k; src/tree.cpp:179-180).  The split kernel never scores the
     // others in this tree: the root does not read their columns and no level
-    // flushes their bins.  A full group still accumulates every feature (a
-    // per-lane feature test costs more vector work than the LDS atomics it
-    // saves: 10M x 128 histograms 4.48 -> 4.59 ms per round); the unsampled
-    // features' LDS bins are simply never written out.  Uniform over the
-    // workgroup.
-    uint32_t gmask = 0;
-    for (uint32_t k = 0; k < fcount; ++k) gmask |= (!t.allowed || t.allowed[fbase + k]) ? 1u << k : 0u;
-    // The root always builds feature 0: its bins give the root's totals (and
-    // a dense root's ordered sums) whether or not the tree samples it.
-    if (IDENTITY && fbase == 0) gmask |= 1u;
-    if (!gmask) continue;
+    // flushes their bins.  The accumulation still adds every feature of the
+    // group (a per-lane feature test costs more vector work than the LDS
+    // atomics it saves: 10M x 128 histograms 4.48 -> 4.59 ms per round); the
+    // unsampled features' LDS bins are simply never written out.  Uniform
+    // over the workgroup.  Only the column loads hold the mask through the
+    // row loop (the flush reads the sample again): kept live there it pushes
+    // the row-major kernels past 64 VGPRs, one 1024-thread workgroup per CU
+    // instead of two (262144 x 64: +0.5 ms per 100 rounds).
+    // Without a column sample the mask is the group's width (no loop on the
+    // item's critical path ahead of the LDS clear).
+    uint32_t gmask = fcount >= 32 ? ~0u : (1u << fcount) - 1u;
+    if (t.allowed) {
+      gmask = 0;
+      for (uint32_t k = 0; k < fcount; ++k) gmask |= sampled(t, fbase + k, true, IDENTITY) ? 1u << k : 0u;
+      if (!gmask) continue;
+    }
     const uint32_t first_sampled = (uint32_t)__builtin_ctz(gmask);
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
       lg[i] = 0;
@@ -885,7 +898,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
           for (int k = 0; k < G; ++k) {
             const uint32_t j = (k + lane) & (G - 1);
             const uint32_t bin = min(rc.get(k), t.max_bin);
-            if ((gmask >> j) & 1u) {
+            if (j < fcount) {
               atomicAdd(&lg[bin * G + j], qg);
               if constexpr (UNIT) atomicAdd(&lc[bin * G + j], 1u);
               else atomicAdd(&lh[bin * G + j], qh);
@@ -913,7 +926,7 @@ __global__ __launch_bounds__(kHistThreads) void k_histogram(Tree t, uint32_t dep
     // lanes of one feature writes consecutive bins of the feature-major output.
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
       const uint32_t bin = i / G, j = i % G;
-      if (!((gmask >> j) & 1u)) continue;
+      if (!sampled(t, fbase + j, fcount > j, IDENTITY)) continue;
       int64_t g = (int64_t)lg[i];
       int64_t h = UNIT ? (int64_t)((uint64_t)lc[i] * (uint64_t)unit_q) : (int64_t)lh[i];
       reinterpret_cast<int4*>(out)[j * B1 + bin] = make_int4((int)(uint32_t)g, (int)(uint32_t)((uint64_t)g >> 32),
@@ -1968,7 +1981,6 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
         atomicOr(&s_status, (uint32_t)MGB_TREE_STATUS_CAPACITY);
         expand = false;  // the children would lie outside the node table or frontier
       }
-      atomicAdd(expand ? &s_rows_split : &s_rows_leaf, node.count);
       if (expand) {
         const int32_t left = (int32_t)(node_base + 2 * rank), right = left + 1;
         rec->left = left; rec->right = right;
@@ -2029,6 +2041,16 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
           next[2 * rank] = lf;
           next[2 * rank + 1] = rf;
         }
+      }
+    }
+    {
+      // The level's rows of splitting and of stopping nodes: wave sums, one
+      // LDS atomic per wave.
+      const uint32_t split_rows = wave_inclusive_u32(valid && expand ? node.count : 0u);
+      const uint32_t leaf_rows = wave_inclusive_u32(valid && !expand ? node.count : 0u);
+      if (lane_id() == kWave - 1) {
+        if (split_rows) atomicAdd(&s_rows_split, split_rows);
+        if (leaf_rows) atomicAdd(&s_rows_leaf, leaf_rows);
       }
     }
     const uint32_t nitems = n - base < blockDim.x ? n - base : blockDim.x;
