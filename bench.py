@@ -156,6 +156,22 @@ def rooflines(prof, rounds):
     return out
 
 
+def committed_traffic(which):
+    """HBM bytes per launch of each kernel class for this workload, from the
+    committed counter passes (FETCH_SIZE and WRITE_SIZE, calibrated by a copy
+    kernel of known size); None where no pass is committed."""
+    out = {"histogram": None, "split": None, "partition": None}
+    path = ROOT / "profiles" / f"tree_traffic_config{which[1]}.json"
+    if path.exists():
+        try:
+            data = json.loads(path.read_text())
+            for k in out:
+                out[k] = data.get(k, {}).get("hbm_bytes_per_launch")
+        except ValueError:
+            pass
+    return out
+
+
 def stream_copy_gbps(mib=1024):
     import ctypes
     import device_lib as D
@@ -327,13 +343,7 @@ def main():
     breakdown = {k: round(v["ms"] / 101, 4) for k, v in kernels.items() if v["launches"]}
 
     copy_gbps = stream_copy_gbps()
-    traffic = None
-    traffic_file = ROOT / "profiles" / "histogram_traffic_config2.json"
-    if which == "c2" and traffic_file.exists():
-        try:
-            traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
-        except ValueError:
-            traffic = None
+    traffic = committed_traffic(which)
 
     rows, cols = X.shape
     depth = spec["depth"]
@@ -358,9 +368,9 @@ def main():
                                             f"parameters and the same protocol"
                                             + (", its own label generator (README.md:101)" if which == "c2" else
                                                ", the same workload (README.md:98-104)")},
-        "roofline": dict(roof["roofline"], traffic=traffic),
-        "split_roofline": roof["split_roofline"],
-        "partition_roofline": roof["partition_roofline"],
+        "roofline": dict(roof["roofline"], traffic=traffic["histogram"]),
+        "split_roofline": dict(roof["split_roofline"], traffic=traffic["split"]),
+        "partition_roofline": dict(roof["partition_roofline"], traffic=traffic["partition"]),
         "fits_ms": [round(t, 3) for t in fits],
         "process_median_ms": [round(statistics.median(c["fit_ms"]), 3) for c in children],
         "steady_state_ms_per_100_rounds": round(steady_ms, 3),
@@ -457,19 +467,16 @@ def bench_large(xgb, args, which):
     kernels = prof["kernels"]
     roof = rooflines(prof, steps + 1)
     rounds = spec["rounds"]
-    traffic = None
-    tfile = ROOT / "profiles" / f"histogram_traffic_config{which[1]}.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    traffic = committed_traffic(which)
     line = {
         "metric": spec["metric"], "value": round(ms_per_step * rounds, 2), "unit": f"ms/{rounds} rounds",
         "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 3),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int64", "data": "synthetic",
         "config": dict({"workload": spec["workload"]}, **spec["shape"]),
-        "roofline": dict(roof["roofline"], traffic=traffic,
+        "roofline": dict(roof["roofline"], traffic=traffic["histogram"],
                          kernel="k_histogram" if which == "c4" else "k_histogram_csr (+ k_zero_built, k_root_totals)"),
-        "split_roofline": roof["split_roofline"],
-        "partition_roofline": roof["partition_roofline"],
+        "split_roofline": dict(roof["split_roofline"], traffic=traffic["split"]),
+        "partition_roofline": dict(roof["partition_roofline"], traffic=traffic["partition"]),
         "kernel_ms_per_round": {k: round(v["ms"] / (steps + 1), 4) for k, v in kernels.items() if v["launches"]},
         "one_time_s": {"generate": round(gen_s, 2), "dmatrix_sketch_bins_and_warmup": round(setup_s, 2),
                        "quantile_sketch": round(prof0.get("quantiles", 0.0), 3),
