@@ -674,22 +674,24 @@ static std::string tree_violation(const MgbTreeNode* nodes, uint32_t count, uint
   uint32_t next = 1;  // the next unused node id
   for (uint32_t i = 0; i < count; ++i) {
     const MgbTreeNode& x = nodes[i];
-    const std::string node = "node " + std::to_string(i);
-    if (x.default_left > 1) return node + " has default_left " + std::to_string(x.default_left);
+    // The message is built only for a node that fails (every round's trees
+    // pass through here when the model is read).
+    auto node = [i] { return "node " + std::to_string(i); };
+    if (x.default_left > 1) return node() + " has default_left " + std::to_string(x.default_left);
     if (x.left == -1 && x.right == -1) {
-      if (x.feature != -1) return node + " is a leaf with split feature " + std::to_string(x.feature);
+      if (x.feature != -1) return node() + " is a leaf with split feature " + std::to_string(x.feature);
       continue;
     }
-    if (x.left < 0 || x.right < 0) return node + " has one child";
+    if (x.left < 0 || x.right < 0) return node() + " has one child";
     if ((uint32_t)x.left != next || x.right != x.left + 1)
-      return node + " has children (" + std::to_string(x.left) + ", " + std::to_string(x.right) +
+      return node() + " has children (" + std::to_string(x.left) + ", " + std::to_string(x.right) +
              "), not the next unused ids (" + std::to_string(next) + ", " + std::to_string(next + 1) + ")";
     if ((uint32_t)x.right >= count)
-      return node + "'s children lie beyond the node count " + std::to_string(count);
+      return node() + "'s children lie beyond the node count " + std::to_string(count);
     if (x.feature < 0 || (uint32_t)x.feature >= cols)
-      return node + " splits on feature " + std::to_string(x.feature) + " of " + std::to_string(cols);
+      return node() + " splits on feature " + std::to_string(x.feature) + " of " + std::to_string(cols);
     if (nodes[x.left].parent != (int32_t)i || nodes[x.right].parent != (int32_t)i)
-      return node + "'s children do not name it as their parent";
+      return node() + "'s children do not name it as their parent";
     next += 2;
   }
   if (next != count)
