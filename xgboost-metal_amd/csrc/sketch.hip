@@ -1492,19 +1492,19 @@ uint64_t group_entries() {
   return std::clamp<uint64_t>(free_bytes / 4 / kGroupBytesPerEntry, uint64_t(1) << 20, kMaxGroupEntries);
 }
 
-// Device memory of one sketch pass, allocated and freed in order on the
-// library stream: a free is queued behind the kernels that use the buffer
-// instead of waiting for the device, and the memory pool keeps it for the
-// next pass.
+// Device memory of one sketch pass from the library's allocator, in order on
+// the library stream: a free is queued behind the kernels that use the
+// buffer instead of waiting for the device, and the allocator keeps it for
+// the next pass.
 struct StreamBuffer {
   void* p = nullptr;
   StreamBuffer() = default;
   StreamBuffer(const StreamBuffer&) = delete;
   StreamBuffer& operator=(const StreamBuffer&) = delete;
   ~StreamBuffer() {
-    if (p) (void)hipFreeAsync(p, stream());
+    if (p) (void)mgb_free(p);
   }
-  int alloc(size_t bytes) { return check(hipMallocAsync(&p, bytes ? bytes : 16, stream()), "hipMallocAsync(sketch)"); }
+  int alloc(size_t bytes) { return mgb_malloc(&p, bytes ? bytes : 16); }
   template <typename T> T* as() const { return static_cast<T*>(p); }
 };
 

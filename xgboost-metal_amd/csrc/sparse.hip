@@ -116,8 +116,8 @@ uint32_t grid_of(uint64_t work, uint32_t block, uint32_t cap) {
 
 struct Scratch {
   void* p = nullptr;
-  ~Scratch() { if (p) (void)hipFree(p); }
-  int alloc(size_t bytes) { return check(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc(csr)"); }
+  ~Scratch() { if (p) (void)mgb_free(p); }
+  int alloc(size_t bytes) { return mgb_malloc(&p, bytes ? bytes : 16); }
 };
 
 }  // namespace
