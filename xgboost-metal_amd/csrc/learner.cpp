@@ -855,11 +855,14 @@ void Learner::grow(DMatrix& data, bool unit_hessian, bool sampled) {
   const uint32_t max_nodes = (2u << depth) - 1u;
   const size_t node_bytes = (size_t)max_nodes * sizeof(MgbTreeNode);
   // This round's slot in the queue of rounds not yet copied to the host
-  // (up to 64 rounds or 64 MB; a full queue is drained first).
+  // (up to 1,024 rounds or 64 MB; a full queue is drained first).  A drain
+  // waits for every queued round and the device then idles until the host
+  // launches again, so the queue holds a whole fit of the usual round counts
+  // (depth 8: 1,024 rounds in 20 MB; depth 10: 819 rounds).
   const size_t slot_bytes = (node_bytes + 16 + 255) / 256 * 256;
   if (pending_bytes_ + slot_bytes > d_pending_.bytes()) {
     drain();
-    const size_t rounds = std::max<size_t>(1, std::min<size_t>(64, (64u << 20) / slot_bytes));
+    const size_t rounds = std::max<size_t>(1, std::min<size_t>(1024, (64u << 20) / slot_bytes));
     if (d_pending_.bytes() < rounds * slot_bytes) d_pending_.resize(rounds * slot_bytes);
   }
   const size_t slot_offset = pending_bytes_;
@@ -968,34 +971,35 @@ void Learner::empty_round() {
 
 void Learner::drain() {
   if (pending_.empty()) return;
-  // One device-to-host copy (it waits for the queued rounds) of every
-  // pending slot: node records followed by the node count.
-  std::vector<uint8_t> host(pending_bytes_);
-  d_pending_.download(host.data(), pending_bytes_);
   std::vector<Pending> rounds;
   rounds.swap(pending_);
+  const size_t bytes = pending_bytes_;
   pending_bytes_ = 0;
-  for (const Pending& p : rounds) {
-    uint32_t word[2] = {0, 0};  // node count, tree status
-    std::memcpy(word, host.data() + p.offset + p.node_bytes, sizeof(word));
-    const uint32_t n = std::min(word[0], p.max_nodes);
-    const auto* records = reinterpret_cast<const MgbTreeNode*>(host.data() + p.offset);
-    const std::string why = tree_violation(records, word[0], word[1], p.max_nodes, num_feature);
-    if (!why.empty()) {
-      // Every later round took its gradients from this round's margins: drop
-      // them with it, and rebuild the training margins from the trees kept
-      // (src/learner.cpp:36-61 retire_round).
-      const size_t round = trees.size();
-      cache_id_ = 0;
-      cache_trees_ = 0;
-      throw Error("round " + std::to_string(round) + ": the device tree is invalid: " + why +
-                  "; this and the " + std::to_string(rounds.size() - 1 - (&p - rounds.data())) +
-                  " later queued rounds are dropped");
+  // One device-to-host copy (it waits for the queued rounds) of every
+  // pending slot: node records followed by the node count.
+  kcheck(download_pinned(d_pending_.get(), bytes, [&](const uint8_t* host) {
+    for (const Pending& p : rounds) {
+      uint32_t word[2] = {0, 0};  // node count, tree status
+      std::memcpy(word, host + p.offset + p.node_bytes, sizeof(word));
+      const uint32_t n = std::min(word[0], p.max_nodes);
+      const auto* records = reinterpret_cast<const MgbTreeNode*>(host + p.offset);
+      const std::string why = tree_violation(records, word[0], word[1], p.max_nodes, num_feature);
+      if (!why.empty()) {
+        // Every later round took its gradients from this round's margins:
+        // drop them with it, and rebuild the training margins from the trees
+        // kept (src/learner.cpp:36-61 retire_round).
+        const size_t round = trees.size();
+        cache_id_ = 0;
+        cache_trees_ = 0;
+        throw Error("round " + std::to_string(round) + ": the device tree is invalid: " + why +
+                    "; this and the " + std::to_string(rounds.size() - 1 - (&p - rounds.data())) +
+                    " later queued rounds are dropped");
+      }
+      Tree tree;
+      tree.nodes.assign(records, records + n);
+      trees.push_back(std::move(tree));
     }
-    Tree tree;
-    tree.nodes.assign(records, records + n);
-    trees.push_back(std::move(tree));
-  }
+  }), "device-to-host copy of the queued rounds");
 }
 
 void Learner::update(DMatrix& data, int /*iteration*/) {

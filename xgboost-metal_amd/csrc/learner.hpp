@@ -8,6 +8,7 @@
 // (dense/CSR ingest, quantize), src/model.cpp:28-74 (JSON model).
 #pragma once
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -47,6 +48,11 @@ class DeviceBuffer {
 };
 
 void kcheck(int status, const char* what);
+
+// Copies `bytes` of device memory at `src` into a pinned host buffer the
+// library reuses (runtime.hip), waits for the copy, and calls `use` on it
+// while holding the buffer; 0, or -1 with the library's error set.
+int download_pinned(const void* src, size_t bytes, const std::function<void(const uint8_t*)>& use);
 
 struct DMatrix {
   uint64_t id = 0;                    // unique per matrix; keys the prediction cache

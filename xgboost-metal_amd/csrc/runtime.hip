@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <string>
@@ -70,6 +71,39 @@ static int ensure_init() {
 int bound_device() { return ensure_init() ? -1 : g_device; }
 
 bool profiling_enabled() { return g_profile.on; }
+
+// Model data copied back to the host (a drain of queued rounds: every
+// round's node records) lands in one pinned buffer kept for the process:
+// no page faults on freshly allocated host memory and no staging of a
+// pageable copy (262,144 x 64: 2 MB per fit, 0.22 ms of device idle at the
+// end of every fit before).  Grows to the largest request, in 4 MiB steps.
+namespace {
+std::mutex g_pinned_mutex;
+uint8_t* g_pinned = nullptr;
+size_t g_pinned_bytes = 0;
+}  // namespace
+
+int download_pinned(const void* src, size_t bytes, const std::function<void(const uint8_t*)>& use) {
+  if (ensure_init()) return -1;
+  std::lock_guard<std::mutex> lock(g_pinned_mutex);
+  if (g_pinned_bytes < bytes) {
+    if (g_pinned) MGB_CHECK(hipHostFree(g_pinned));
+    g_pinned = nullptr;
+    g_pinned_bytes = 0;
+    const size_t step = size_t(4) << 20;
+    const size_t want = (bytes + step - 1) / step * step;
+    void* p = nullptr;
+    MGB_CHECK(hipHostMalloc(&p, want, hipHostMallocDefault));
+    g_pinned = static_cast<uint8_t*>(p);
+    g_pinned_bytes = want;
+  }
+  if (bytes) {
+    MGB_CHECK(hipMemcpyAsync(g_pinned, src, bytes, hipMemcpyDeviceToHost, g_stream));
+    MGB_CHECK(hipStreamSynchronize(g_stream));
+  }
+  use(g_pinned);
+  return 0;
+}
 
 }  // namespace mgb
 
