@@ -23,6 +23,10 @@ extern "C" {
 int mgb_init(int device);
 const char* mgb_last_error(void);
 int mgb_device_count(int* count);
+/* Device memory ordered on the library's one stream.  A freed buffer is kept
+ * by the library (up to 8 GiB) for the next request of about its size and
+ * only returned to HIP when an allocation would otherwise fail; mgb_free
+ * takes only pointers from mgb_malloc. */
 int mgb_malloc(void** ptr, size_t bytes);
 int mgb_free(void* ptr);
 int mgb_memcpy_h2d(void* dst, const void* src, size_t bytes);
