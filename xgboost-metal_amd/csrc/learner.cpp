@@ -971,13 +971,13 @@ void Learner::empty_round() {
 
 void Learner::drain() {
   if (pending_.empty()) return;
-  std::vector<Pending> rounds;
-  rounds.swap(pending_);
-  const size_t bytes = pending_bytes_;
-  pending_bytes_ = 0;
   // One device-to-host copy (it waits for the queued rounds) of every
-  // pending slot: node records followed by the node count.
-  kcheck(download_pinned(d_pending_.get(), bytes, [&](const uint8_t* host) {
+  // pending slot: node records followed by the node count.  The queue is
+  // taken over only once the copy has succeeded.
+  kcheck(download_pinned(d_pending_.get(), pending_bytes_, [&](const uint8_t* host) {
+    std::vector<Pending> rounds;
+    rounds.swap(pending_);
+    pending_bytes_ = 0;
     for (const Pending& p : rounds) {
       uint32_t word[2] = {0, 0};  // node count, tree status
       std::memcpy(word, host + p.offset + p.node_bytes, sizeof(word));

@@ -162,7 +162,7 @@ int mgb_csr_to_csc(const uint64_t* indptr, const uint32_t* indices, const float*
                      cols, colptr);
   MGB_LAUNCH_CHECK("k_colptr");
   if (csc_cols) MGB_CHECK(hipMemcpyAsync(csc_cols, keys_out.p, nnz * 4, hipMemcpyDeviceToDevice, s));
-  MGB_CHECK(hipStreamSynchronize(s));  // the scratch buffers are freed on return
+  MGB_CHECK(hipStreamSynchronize(s));  // the copy is complete when the call returns
   return 0;
 }
 
