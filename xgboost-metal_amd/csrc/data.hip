@@ -573,9 +573,16 @@ int mgb_quantize_bins_columns(const float* X, const float* cuts, const uint32_t*
   return quantize(X, cuts, counts, m, bins, columns, any_missing);
 }
 
+// Workgroups of the gradient passes: one per kGradRows rows, at most
+// kGradBlocks.  The pass ends in a chain of device-scope atomics and the last
+// workgroup's sum of every workgroup's limbs, so a small matrix takes fewer,
+// fuller workgroups (262,144 rows: 128 workgroups, the gradients 12.6 -> 9.5
+// us per round); 10M rows still fill the chip.
+constexpr uint32_t kGradRows = 2 * kGradThreads;
+
 int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labels, const float* weights,
                   float* grad, uint64_t* mass, float* scales) {
-  uint32_t grid = grid_for(p->rows, kGradThreads, kGradBlocks);
+  uint32_t grid = grid_for(p->rows, kGradRows, kGradBlocks);
   launch(MGB_PROF_GRADIENT, k_gradients, dim3(grid), dim3(kGradThreads), 0, *p, margin, labels, weights,
          (float2*)grad, mass, scales);
   MGB_LAUNCH_CHECK("k_gradients");
@@ -583,7 +590,7 @@ int mgb_gradients(const MgbGradParams* p, const float* margin, const float* labe
 }
 
 int mgb_gradient_mass(const MgbGradParams* p, float* grad, uint64_t* mass, float* scales) {
-  uint32_t grid = grid_for(p->rows, kGradThreads, kGradBlocks);
+  uint32_t grid = grid_for(p->rows, kGradRows, kGradBlocks);
   launch(MGB_PROF_GRADIENT, k_gradient_mass, dim3(grid), dim3(kGradThreads), 0, *p, (float2*)grad, mass, scales);
   MGB_LAUNCH_CHECK("k_gradient_mass");
   return 0;
