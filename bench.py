@@ -28,8 +28,9 @@ code read and id and pair written; a stopping node's rows their id and
 margin) are reported the same way.  cpu_baseline trains the CPU oracle (a
 port of the reference's algorithm, OpenMP over features) for the same 100
 rounds on the host cores, and its predictions are compared with the GPU fit's
-bit for bit.  The default run also times config 4 (10M x 128, 1024 bins, the
-HBM-bound workload) in one more fresh process and reports it under "c4".
+bit for bit.  The default run also times config 3 (1M x 2000 CSR) and config
+4 (10M x 128, 1024 bins, the HBM-bound workload), each in one more fresh
+process, and reports them under "c3" and "c4".
 """
 import argparse
 import hashlib
@@ -260,6 +261,8 @@ def main():
                          "c4: 10M x 128, 1024 bins, depth 10 (HBM-bound check)")
     ap.add_argument("--no-ref", action="store_true",
                     help="c2: skip the extra process timing the reference's own 262,144 x 64 workload")
+    ap.add_argument("--no-c3", action="store_true",
+                    help="c2: skip the extra process timing config 3 (1M x 2000 CSR, depth 8)")
     ap.add_argument("--no-c4", action="store_true",
                     help="c2: skip the extra process timing config 4 (10M x 128, 1024 bins, depth 10)")
     ap.add_argument("--param", action="append", default=[], metavar="KEY=VALUE",
@@ -387,8 +390,10 @@ def main():
             children[0]["prediction_sha256"] == published_sha256(which)
     if reference_workload is not None:
         line["reference_workload"] = reference_workload
+    if which == "c2" and not args.no_c3:
+        line["c3"] = run_large_child("c3", args.param)
     if which == "c2" and not args.no_c4:
-        line["c4"] = run_c4_child(args.param)
+        line["c4"] = run_large_child("c4", args.param)
     if cpu is not None:
         line["cpu_baseline"] = cpu
         line["parity"]["equal_to_cpu_oracle_bitwise"] = bool(
@@ -415,23 +420,25 @@ LARGE = {
 }
 
 
-def run_c4_child(extra_params=()):
-    """Config 4 in one more fresh process (subprocess, never exec): its own
-    generator, 2 warm-up rounds, 20 timed steady-state rounds; a failure gives
-    the error instead of the object and leaves the config-2 line intact."""
-    cmd = [sys.executable, str(Path(__file__).resolve()), "--config", "c4", "--steps", "20", "--warmup", "2"]
+def run_large_child(which, extra_params=()):
+    """Config 3 or 4 in one more fresh process (subprocess, never exec): its
+    own generator, 2 warm-up rounds, 20 timed steady-state rounds; a failure
+    gives {"error": ...} instead of the object and leaves the config-2 line
+    intact."""
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--config", which, "--steps", "20", "--warmup", "2"]
     for item in extra_params:
         cmd += ["--param", item]
     try:
         out = subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=420)
-        c4 = json.loads(out.stdout.strip().splitlines()[-1])
+        res = json.loads(out.stdout.strip().splitlines()[-1])
     except (subprocess.SubprocessError, ValueError, IndexError) as e:
         return {"error": f"{type(e).__name__}: {str(e)[:300]}"}
-    print(f"bench: config 4: {c4['value']} ms/200 rounds, histogram {c4['roofline']['frac']} of peak",
+    rounds = LARGE[which]["rounds"]
+    print(f"bench: config {which[1]}: {res['value']} ms/{rounds} rounds, histogram {res['roofline']['frac']} of peak",
           file=sys.stderr, flush=True)
     keep = ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "config", "roofline", "split_roofline",
             "partition_roofline", "kernel_ms_per_round", "one_time_s")
-    return dict({k: c4[k] for k in keep if k in c4}, ms_per_200_rounds=c4["value"])
+    return dict({k: res[k] for k in keep if k in res}, **{f"ms_per_{rounds}_rounds": res["value"]})
 
 
 def bench_large(xgb, args, which):
