@@ -522,15 +522,20 @@ void oracle_gradients(int32_t objective, const float* margin, const float* label
 
 /* src/learner.cpp:316-333 with kernels/boost.metal:356-423: the weighted label
  * mean in extended precision, rounded once to binary32.  Products of two
- * binary32 values are exact in binary64; the sum is compensated (Neumaier). */
+ * binary32 values are exact in binary64; the sum is compensated (Neumaier).
+ * A logistic objective whose scale_pos_weight is not 1 takes each term as the
+ * binary32 product y * w (the reweighted intercept, boost.metal:379-381). */
 float oracle_base_score(int32_t objective, const float* labels, const float* weights, uint32_t rows,
                         float scale_pos_weight) {
+  const int logistic = objective == ORACLE_OBJ_LOGISTIC || objective == ORACLE_OBJ_LOGITRAW;
+  const int float_product = logistic && fabsf(scale_pos_weight - 1.0f) > 1.0e-6f;
   double s = 0, c = 0, ws = 0, wc = 0;
   for (uint32_t r = 0; r < rows; ++r) {
     float w = weights ? weights[r] : 1.0f;
     float y = labels[r];
-    if (objective == ORACLE_OBJ_LOGISTIC || objective == ORACLE_OBJ_LOGITRAW) w *= y == 1 ? scale_pos_weight : 1;
-    double term = (double)y * (double)w;
+    if (logistic) w *= y == 1 ? scale_pos_weight : 1;
+    const float product = y * w;
+    double term = float_product ? (double)product : (double)y * (double)w;
     double t = s + term;
     c += fabs(s) >= fabs(term) ? (s - t) + term : (term - t) + s;
     s = t;
@@ -545,7 +550,8 @@ float oracle_base_score(int32_t objective, const float* labels, const float* wei
 
 /* src/objectives.cpp:17-31 (score_margins). */
 float oracle_base_margin(int32_t objective, float base_score) {
-  if (objective == ORACLE_OBJ_LOGISTIC || objective == ORACLE_OBJ_LOGITRAW) {
+  /* Only the logistic score maps to a margin; logitraw's score is its margin. */
+  if (objective == ORACLE_OBJ_LOGISTIC) {
     float v = base_score < 1.0e-6f ? 1.0e-6f : (base_score > 1 - 1.0e-6f ? 1 - 1.0e-6f : base_score);
     return -logf(1.0f / v - 1.0f);
   }
@@ -1130,6 +1136,12 @@ int oracle_train(const float* X, uint32_t rows, uint32_t cols, const float* labe
 
   float base_score = p->has_base_score ? p->base_score
                                        : oracle_base_score(p->objective, labels, weights, rows, p->scale_pos_weight);
+  if (!p->has_base_score && p->objective == ORACLE_OBJ_LOGITRAW) {
+    /* logitraw's default score is the logit of the clamped label mean
+     * (kernels/boost.metal:405-423 base_finalize). */
+    const float v = base_score < 1.0e-6f ? 1.0e-6f : (base_score > 1 - 1.0e-6f ? 1 - 1.0e-6f : base_score);
+    base_score = logf(v / (1 - v));
+  }
   if (base_score_out) *base_score_out = base_score;
   float base_margin = oracle_base_margin(p->objective, base_score);
   for (uint32_t r = 0; r < rows; ++r) margin[r] = base_margin;

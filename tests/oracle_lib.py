@@ -108,6 +108,13 @@ def gradient_scale(values):
     return float(lib().oracle_gradient_scale(ptr(v), ctypes.c_uint32(len(v))))
 
 
+def base_score(labels, weights=None, objective=0, scale_pos_weight=1.0):
+    y = np.ascontiguousarray(labels, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    return float(lib().oracle_base_score(ctypes.c_int32(objective), ptr(y), ptr(w) if w is not None else None,
+                                         ctypes.c_uint32(len(y)), ctypes.c_float(scale_pos_weight)))
+
+
 def train(X, y, params, rounds, weights=None, custom_grad=None, custom_hess=None):
     X = np.ascontiguousarray(X, np.float32)
     y = np.ascontiguousarray(y, np.float32)

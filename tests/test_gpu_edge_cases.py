@@ -24,6 +24,7 @@ fresh matrix's prediction.
 The max_leaves = 1 variants of the reference's tests are absent: this engine
 grows depthwise only and rejects max_leaves."""
 import ctypes
+import json
 
 import numpy as np
 import pytest
@@ -440,3 +441,62 @@ def test_config4_generator_matches_oracle(xgb):
     assert_cuts_equal(d, ref)
     assert_trees_equal(bst, ref)
     np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# The reweighted logistic intercept (kernels/boost.metal:379-381): with
+# scale_pos_weight != 1 the base score sums binary32 products y * w.
+# ---------------------------------------------------------------------------
+def _product_rule_rows(count):
+    """Single (label, weight) rows whose base score differs between binary32
+    and exact products (labels below 1, so scale_pos_weight scales no weight):
+    the oracle with scale_pos_weight 2.5 takes binary32 products, with 1 exact
+    ones."""
+    rng = np.random.default_rng(2024)
+    rows = []
+    while len(rows) < count:
+        y = np.float32(rng.uniform(0.05, 0.95))
+        w = np.float32(rng.uniform(0.3, 7.0))
+        if O.base_score([y], [w], objective=1, scale_pos_weight=2.5) != \
+                O.base_score([y], [w], objective=1, scale_pos_weight=1.0):
+            rows.append((y, w))
+    return rows
+
+
+def test_reweighted_logistic_base_score_matches_oracle(xgb):
+    params = {"tree_method": "hist", "objective": "binary:logistic", "scale_pos_weight": 2.5, "max_depth": 2,
+              "max_bin": 8, "eta": 0.5}
+    X = np.asarray([[0.25, -1.0, 3.0]], np.float32)
+    for y, w in _product_rule_rows(4):
+        label = np.asarray([y], np.float32)
+        bst, ref = _fit_and_compare(xgb, X, label, {"weight": np.asarray([w], np.float32)}, params, 2)
+        model = json.loads(bst.save_raw("json"))
+        text = model["learner"]["learner_model_param"]["base_score"]  # "[v]", nine significant digits
+        got = np.float32(json.loads(text)[0] if text.startswith("[") else float(text))
+        want = np.float32(O.base_score(label, [w], objective=1, scale_pos_weight=2.5))
+        assert got.view(np.uint32) == want.view(np.uint32), (y, w)
+
+
+@pytest.mark.parametrize("objective", ["binary:logistic", "binary:logitraw"])
+def test_scale_pos_weight_training_matches_oracle(xgb, objective):
+    """scale_pos_weight end to end: the positive rows' weights in the base
+    score and in every round's gradients (kernels/boost.metal:566-570)."""
+    X, y = W.config1(rows=6000, cols=8, seed=19)
+    labels = (y > np.median(y)).astype(np.float32)
+    weight = np.random.default_rng(5).uniform(0.2, 2.0, len(y)).astype(np.float32)
+    params = {"tree_method": "hist", "objective": objective, "scale_pos_weight": 3.0, "max_depth": 5,
+              "max_bin": 64, "eta": 0.3}
+    _fit_and_compare(xgb, X, labels, {"weight": weight}, params, 5)
+
+
+
+@pytest.mark.parametrize("objective,base_score", [("binary:logitraw", 0.3), ("binary:logitraw", -1.25),
+                                                  ("binary:logistic", 0.3)])
+def test_given_base_score_margin_matches_oracle(xgb, objective, base_score):
+    """A given base_score is the logistic score's probability but logitraw's
+    margin itself (src/objectives.cpp:17-31 score_margins)."""
+    X, y = W.config1(rows=3000, cols=6, seed=23)
+    labels = (y > 0).astype(np.float32)
+    params = {"tree_method": "hist", "objective": objective, "base_score": base_score, "max_depth": 4,
+              "max_bin": 32, "eta": 0.3}
+    _fit_and_compare(xgb, X, labels, {}, params, 3)

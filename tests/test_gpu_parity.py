@@ -23,6 +23,7 @@ def _oracle_params(params, rounds_override=None):
                          min_child_weight=float(params.get("min_child_weight", 1.0)),
                          max_delta_step=float(params.get("max_delta_step", 0.0)),
                          min_split_loss=float(params.get("gamma", 0.0)),
+                         scale_pos_weight=float(np.float32(params.get("scale_pos_weight", 1.0))),
                          base_score=params.get("base_score"),
                          subsample=float(params.get("subsample", 1.0)),
                          colsample_bytree=float(params.get("colsample_bytree", 1.0)),

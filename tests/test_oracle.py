@@ -449,3 +449,72 @@ def test_sketch_sort_ties_follow_libstdcxx():
         assert checksum == case["checksum"], case
         assert order[:len(case["order"])].tolist() == case["order"], case
     assert heap_sorts > 0
+
+
+def round_rational_f32(q):
+    """A positive rational rounded to binary32, to nearest, ties to even."""
+    assert q > 0
+    e = q.numerator.bit_length() - q.denominator.bit_length()
+    if Fraction(2) ** e > q:
+        e -= 1
+    e = max(e, -126)
+    scaled = q * Fraction(2) ** (23 - e)  # the binary32 significand's units at q's binade
+    m = scaled.numerator // scaled.denominator
+    rest = scaled - m
+    if rest > Fraction(1, 2) or (rest == Fraction(1, 2) and m % 2):
+        m += 1
+    return np.float32(float(Fraction(m) * Fraction(2) ** (e - 23)))
+
+
+def base_closed_form(y, w, scale_pos_weight, float_product):
+    """The weighted label mean of a logistic objective, exactly, rounded once
+    to binary32 (src/learner.cpp:316-333): terms y * w taken as binary32
+    products (the reweighted intercept, kernels/boost.metal:379-381) or exact."""
+    y = np.asarray(y, np.float32)
+    w = np.where(y == 1, np.asarray(w, np.float32) * np.float32(scale_pos_weight), np.asarray(w, np.float32))
+    w = w.astype(np.float32)
+    num = sum(Fraction(float(np.float32(a * b))) if float_product else Fraction(float(a)) * Fraction(float(b))
+              for a, b in zip(y, w))
+    return round_rational_f32(num / sum(Fraction(float(b)) for b in w))
+
+
+def _product_rounding_rows(count):
+    """Single-row (label, weight) pairs whose binary32 product y * w moves the
+    rounded mean off y: the two rules give different base scores on them."""
+    rng = np.random.default_rng(2024)
+    rows = []
+    while len(rows) < count:
+        y = np.float32(rng.uniform(0.05, 0.95))
+        w = np.float32(rng.uniform(0.3, 7.0))
+        if base_closed_form([y], [w], 2.5, True) != base_closed_form([y], [w], 2.5, False):
+            rows.append((y, w))
+    return rows
+
+
+def test_round_rational_f32_matches_numpy_on_representable_and_tie_values():
+    for v in (1.0, 0.1, 3.0e-38, 1.5, 123456.789):
+        f = np.float32(v)
+        assert round_rational_f32(Fraction(float(f))) == f
+    one_ulp = Fraction(2) ** -23
+    assert round_rational_f32(1 + one_ulp / 2) == np.float32(1.0)            # tie: to even
+    assert round_rational_f32(1 + 3 * one_ulp / 2) == np.float32(1 + 2 * 2.0 ** -23)
+
+
+@pytest.mark.parametrize("scale_pos_weight", [2.5, 1.0])
+def test_base_score_of_reweighted_logistic_sums_binary32_products(scale_pos_weight):
+    """With scale_pos_weight != 1 the logistic intercept sums binary32
+    products y * w; with 1, exact products.  The single-row cases are chosen
+    so that the two rules round to different binary32 means, so a base score
+    that took the other rule fails here."""
+    for y, w in _product_rounding_rows(6):
+        got = np.float32(O.base_score([y], [w], objective=1, scale_pos_weight=scale_pos_weight))
+        want = base_closed_form([y], [w], scale_pos_weight, scale_pos_weight != 1.0)
+        assert got.view(np.uint32) == want.view(np.uint32), (y, w)
+    rng = np.random.default_rng(7)
+    y = rng.uniform(0, 1, 5000).astype(np.float32)
+    y[::7] = 1.0
+    w = rng.uniform(0.1, 3.0, 5000).astype(np.float32)
+    got = np.float32(O.base_score(y, w, objective=1, scale_pos_weight=scale_pos_weight))
+    want = base_closed_form(y, w, scale_pos_weight, scale_pos_weight != 1.0)
+    assert got.view(np.uint32) == want.view(np.uint32)
+

@@ -412,12 +412,18 @@ __global__ __launch_bounds__(kBaseThreads) void k_base_score(const float* __rest
                                                              uint32_t objective, float spw, float* __restrict__ out) {
   __shared__ double sh[4][kBaseThreads];
   __shared__ uint32_t s_last;
+  // A logistic objective whose scale_pos_weight is not 1 sums the binary32
+  // products y * w (the reweighted intercept, kernels/boost.metal:379-381);
+  // otherwise the products are exact in binary64.
+  const bool logistic = objective == 1 || objective == 2;
+  const bool float_product = logistic && fabsf(spw - 1.0f) > 1.0e-6f;
   double s = 0, c = 0, ws = 0, wc = 0;
   for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
     float w = weights ? weights[r] : 1.0f;
     float y = labels[r];
-    if (objective == 1 || objective == 2) w *= y == 1.0f ? spw : 1.0f;
-    two_sum_add(s, c, (double)y * (double)w);
+    if (logistic) w *= y == 1.0f ? spw : 1.0f;
+    const float product = y * w;
+    two_sum_add(s, c, float_product ? (double)product : (double)y * (double)w);
     two_sum_add(ws, wc, (double)w);
   }
   sh[0][threadIdx.x] = s; sh[1][threadIdx.x] = c; sh[2][threadIdx.x] = ws; sh[3][threadIdx.x] = wc;
