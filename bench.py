@@ -207,7 +207,8 @@ def cpu_baseline(X, y, rounds=100, which="c2"):
     seconds = time.perf_counter() - t0
     return ({"value": round(seconds * 1e3 * 100 / rounds, 1), "unit": "ms/100 rounds", "cores": threads,
              "host_cpu_count": os.cpu_count(), "kind": "port",
-             "sample": f"CPU oracle (C restatement of the reference's hist path, OpenMP over features) on the "
+             "sample": f"CPU oracle (C restatement of the reference's hist path; histograms and split search "
+                       f"OpenMP-parallel over features) on the "
                        f"same {X.shape[0]}x{X.shape[1]} d{depth} matrix, one fit of {rounds} rounds including its "
                        f"sketch, {threads} threads ({seconds:.1f} s)"}, ref["margin"])
 

@@ -778,21 +778,30 @@ typedef struct {
 } Quantized;
 
 /* Histogram of one node, parallel over features (results are exact integers
- * and independent of the thread count). */
+ * and independent of the thread count).  The node's fixed-point pairs are
+ * gathered once into `pairs` (2 x count words) in row-list order, so each
+ * feature reads them in sequence. */
 static void node_histogram(const Quantized* q, const uint32_t* rows, uint32_t count, const int64_t* qg,
-                           const int64_t* qh, int64_t* hist) {
+                           const int64_t* qh, int64_t* pairs, int64_t* hist) {
   size_t stride = (size_t)(q->max_bin + 1) * 2;
-#pragma omp parallel for schedule(dynamic, 1)
-  for (int64_t f = 0; f < (int64_t)q->cols; ++f) {
-    uint64_t* h = (uint64_t*)(hist + (size_t)f * stride);
-    memset(h, 0, stride * sizeof(int64_t));
-    const uint16_t* column = q->bins_cm + (size_t)f * q->rows;
-    for (uint32_t i = 0; i < count; ++i) {
-      uint32_t r = rows[i];
-      uint32_t bin = column[r];
-      if (bin == 0xFFFF) bin = q->max_bin;
-      h[2 * bin] += (uint64_t)qg[r];
-      h[2 * bin + 1] += (uint64_t)qh[r];
+#pragma omp parallel
+  {
+#pragma omp for schedule(static)
+    for (int64_t i = 0; i < (int64_t)count; ++i) {
+      pairs[2 * i] = qg[rows[i]];
+      pairs[2 * i + 1] = qh[rows[i]];
+    }
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t f = 0; f < (int64_t)q->cols; ++f) {
+      uint64_t* h = (uint64_t*)(hist + (size_t)f * stride);
+      memset(h, 0, stride * sizeof(int64_t));
+      const uint16_t* column = q->bins_cm + (size_t)f * q->rows;
+      for (uint32_t i = 0; i < count; ++i) {
+        uint32_t bin = column[rows[i]];
+        if (bin == 0xFFFF) bin = q->max_bin;
+        h[2 * bin] += (uint64_t)pairs[2 * i];
+        h[2 * bin + 1] += (uint64_t)pairs[2 * i + 1];
+      }
     }
   }
 }
@@ -826,6 +835,8 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
   for (uint32_t r = 0; r < q->rows; ++r) row_buf[r] = r;
   Frontier* frontier = (Frontier*)malloc(sizeof(Frontier) * (max_nodes + 1));
   Frontier* next = (Frontier*)malloc(sizeof(Frontier) * (max_nodes + 1));
+  OracleSplit* cands = (OracleSplit*)malloc(sizeof(OracleSplit) * (q->cols ? q->cols : 1));
+  int64_t* pairs = (int64_t*)malloc(sizeof(int64_t) * 2 * (q->rows ? q->rows : 1));
   uint32_t nf = 1;
   frontier[0].id = 0; frontier[0].begin = 0; frontier[0].count = q->rows;
   frontier[0].sum_g = frontier[0].sum_h = 0;
@@ -840,7 +851,7 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
         for (uint32_t i = 0; i < fr->count; ++i) leaf_of_row[row_buf[fr->begin + i]] = id;
         continue;
       }
-      node_histogram(q, row_buf + fr->begin, fr->count, qg, qh, hist);
+      node_histogram(q, row_buf + fr->begin, fr->count, qg, qh, pairs, hist);
       int64_t total_g = fr->sum_g, total_h = fr->sum_h;
       if (depth == 0) {
         /* Root: present + missing of feature 0 (equal for every feature). */
@@ -848,20 +859,24 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
         for (uint32_t bin = 0; bin <= q->max_bin; ++bin) { a += (uint64_t)hist[2 * bin]; b += (uint64_t)hist[2 * bin + 1]; }
         total_g = (int64_t)a; total_h = (int64_t)b;
       }
-      OracleSplit best;
-      memset(&best, 0, sizeof(best));
-      for (uint32_t f = 0; f < q->cols; ++f) {
-        OracleSplit cand;
+      /* Every feature's best candidate (in parallel: each is a function of
+       * its own histogram row), then the first strictly greater gain in
+       * feature order. */
+#pragma omp parallel for schedule(dynamic, 1)
+      for (int64_t f = 0; f < (int64_t)q->cols; ++f) {
         evaluate_feature(hist + (size_t)f * stride, q->counts[f], q->cuts + (size_t)f * q->max_bin, q->minima[f],
                          total_g, total_h, sg, sh, p, (int32_t)f, p->monotone ? p->monotone[f] : 0, fr->lower,
-                         fr->upper, &cand);
+                         fr->upper, &cands[f]);
         if (allowed && !allowed[f]) {
           /* A feature outside the tree's sample offers no split. */
-          cand.gain = -INFINITY;
-          cand.feature = -1;
+          cands[f].gain = -INFINITY;
+          cands[f].feature = -1;
         }
-        if (f == 0 || cand.gain > best.gain) best = cand;
       }
+      OracleSplit best;
+      memset(&best, 0, sizeof(best));
+      for (uint32_t f = 0; f < q->cols; ++f)
+        if (f == 0 || cands[f].gain > best.gain) best = cands[f];
       float applied_weight = 0, applied_hessian = 0;
       float parent_weight = best.parent_weight, total_h_f = best.total_h;
       if (depth == 0 && q->dense) {
@@ -962,6 +977,8 @@ static uint32_t grow_tree(const Quantized* q, const OracleParams* p, const int64
   }
   free(frontier);
   free(next);
+  free(cands);
+  free(pairs);
   return node_count;
 }
 
