@@ -16,6 +16,8 @@ fresh matrix's prediction.
   at tile boundaries 1 ... 4,099, one-sided tiles with empty children, and a
   full depth-10 frontier (left children 2 * arange(511) + 1), each with the
   stable and the atomic-claim partition;
+- full trees beyond the reference's depths: depth 12, 14 and 16 (the
+  deepest this engine takes), dense with either partition and CSR;
 - the x86 form of the gain (no fused multiply-add) on both sides;
 - device gradients and fixed-point scales against the oracle's directly;
 - BASELINE config 4's own generator (128 columns, Bernoulli labels) with its
@@ -282,6 +284,57 @@ def test_full_and_pruned_deep_frontiers(xgb, quantile, pruned, stable):
         assert len(left) == 1023 + 2 * expanded
     else:
         assert expanded == 512 and len(left) == 2047
+
+
+def bit_patterns(bits):
+    """Every `bits`-bit pattern once, y = sum over set bits j of 1 + j/64:
+    each bit splits any node's rows in half with a gain of at least a
+    quarter of its rows, the highest remaining bit strictly best, so the
+    tree is full to depth `bits` (y = the pattern's value instead loses its
+    last splits to binary32 cancellation against the parent's gain beyond
+    depth 10)."""
+    values = np.arange(1 << bits, dtype=np.uint32)
+    X = ((values[:, None] >> np.arange(bits, dtype=np.uint32)) & 1).astype(np.float32)
+    return X, (X @ (1 + np.arange(bits, dtype=np.float32) / 64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("stable", [0, 1])
+@pytest.mark.parametrize("depth", [12, 14, 16])
+def test_full_frontiers_beyond_depth_ten(xgb, depth, stable):
+    """Every depth-bit pattern once: a full tree to the deepest depth the
+    engine takes (16), whose last levels hold up to 2^15 nodes -- past the
+    2,048 that a level's bookkeeping plans from the counting pass, so the
+    separate planning launch takes those levels."""
+    X, y = bit_patterns(depth)
+    params = {"tree_method": "hist", "max_depth": depth, "max_bin": 2, "min_child_weight": 1, "lambda": 0,
+              "base_score": 0, "eta": 0.3, "seed": 71, "hip_stable_partition": stable}
+    bst, _ = _fit_and_compare(xgb, X, y, {}, params, 1)
+    left = np.asarray(bst.trees_to_json()[0]["left_children"])
+    internal = (1 << depth) - 1
+    np.testing.assert_array_equal(left[:internal], 2 * np.arange(internal) + 1)
+    assert len(left) == 2 * internal + 1
+
+
+@pytest.mark.parametrize("depth", [12, 14])
+def test_csr_full_frontiers_beyond_depth_ten(xgb, depth):
+    """The same patterns as a CSR matrix whose zero bits are absent
+    (missing): every split is present against missing, down to depth 14."""
+    import scipy.sparse as sp
+    X, y = bit_patterns(depth)
+    csr = sp.csr_matrix(X)
+    csr.eliminate_zeros()
+    dense = np.where(X == 0, np.float32(np.nan), X).astype(np.float32)
+    params = {"tree_method": "hist", "max_depth": depth, "max_bin": 2, "min_child_weight": 1, "lambda": 0,
+              "base_score": 0, "eta": 0.3, "seed": 71}
+    d = xgb.DMatrix(csr, label=y)
+    bst = xgb.train(params, d, 1)
+    ref = O.train(dense, y, _oracle_params(params), 1)
+    assert_cuts_equal(d, ref)
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32),
+                                  ref["margin"].view(np.uint32))
+    left = np.asarray(bst.trees_to_json()[0]["left_children"])
+    assert len(left) == 2 * ((1 << depth) - 1) + 1
 
 
 @pytest.mark.parametrize("depth", [9, 10])
