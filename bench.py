@@ -149,8 +149,9 @@ def rooflines(prof, rounds):
         sampled = prof.get(field.replace("_bytes", "_bytes_sampled_features"))
         if sampled is not None and sampled != prof[field] and k["ms"] > 0:
             # With colsample_bytree the kernels touch only the sampled
-            # features; the bytes above count every feature (F in the
-            # survey's formula), these only the sampled ones.
+            # features; the bytes above count every feature (F in
+            # R_built·(F·s + 12) + N_built·F·(B+1)·16), these only the
+            # sampled ones.
             a = sampled / (k["ms"] * 1e-3) / 1e9
             out[key]["sampled_features"] = {"algorithmic_bytes_per_launch": round(sampled / launches),
                                             "achieved": round(a, 1), "frac": round(a / HBM_PEAK_GBPS, 4)}
