@@ -1138,6 +1138,16 @@ __device__ __forceinline__ void try_candidate(NodeEval& n, uint64_t lg, uint64_t
   }
 }
 
+// The binary32 nearest the binary64 value of a 64-bit integer, times 2^-e:
+// both halves convert to binary64 exactly (the high word signed) and one
+// fused multiply-add rounds their sum, so the result lies within
+// 2^-24 + 2^-53 of the integer's value relatively, whatever its sign (no
+// absolute value first: five vector operations against nine).
+__device__ __forceinline__ float scaled_f32(uint64_t v, int e) {
+  const double d = fma((double)(int32_t)(uint32_t)(v >> 32), 4294967296.0, (double)(uint32_t)v);
+  return ldexpf((float)d, -e);
+}
+
 // Division-free bounds on a candidate's float gain.  With reg_alpha = 0 and
 // max_delta_step = 0 the scorer's child gain is -(2Gw + (H+lambda)w^2) for the
 // float weight w = -G/(H+lambda) (1+d), |d| <= 2^-24, which is exactly
@@ -1150,11 +1160,6 @@ __device__ __forceinline__ void try_candidate(NodeEval& n, uint64_t lg, uint64_t
 // be the first strictly greater candidate.  lo = -inf: not certainly valid
 // (it takes no part in the node's best lower bound); hi = -inf: certainly
 // invalid (Hessian sums not positive or below min_child_weight).
-__device__ __forceinline__ float magnitude_f32(uint64_t v) {
-  const uint64_t m = (int64_t)v < 0 ? 0 - v : v;
-  return fmaf((float)(uint32_t)(m >> 32), 4294967296.0f, (float)(uint32_t)m);
-}
-
 __device__ __forceinline__ void gain_bounds(const NodeEval& n, uint64_t lg, uint64_t lh, int eg, int eh, float mcw,
                                             bool filter, float lambda, float& lo, float& hi) {
   const uint64_t rg = n.tg - lg, rh = n.th - lh;
@@ -1162,7 +1167,7 @@ __device__ __forceinline__ void gain_bounds(const NodeEval& n, uint64_t lg, uint
   hi = -INFINITY;
   if ((int64_t)lh <= 0 || (int64_t)rh <= 0) return;  // HL > 0 or HR > 0 fails (the conversion keeps the sign)
   // hl, hr are within 2^-22 of HL, HR while they stay normal floats.
-  const float hl = ldexpf(magnitude_f32(lh), -eh), hr = ldexpf(magnitude_f32(rh), -eh);
+  const float hl = scaled_f32(lh, eh), hr = scaled_f32(rh, eh);
   constexpr float tol = 0x1p-20f;
   if (mcw > 0x1p-100f && (hl < mcw * (1.0f - tol) || hr < mcw * (1.0f - tol))) return;
   const float need = fmaxf(mcw * (1.0f + tol), 0x1p-100f);
@@ -1173,8 +1178,8 @@ __device__ __forceinline__ void gain_bounds(const NodeEval& n, uint64_t lg, uint
   // rounding is relative; otherwise the candidate is scored exactly.
   const float dl = hl + lambda, dr = hr + lambda;
   if (!(dl >= 0x1p-100f && dr >= 0x1p-100f && dl <= 0x1p100f && dr <= 0x1p100f)) return;
-  const float gl = ldexpf(magnitude_f32(lg), -eg), gr = ldexpf(magnitude_f32(rg), -eg);
-  if ((gl != 0.0f && gl < 0x1p-50f) || (gr != 0.0f && gr < 0x1p-50f)) return;
+  const float gl = scaled_f32(lg, eg), gr = scaled_f32(rg, eg);  // signed: only their squares are used
+  if ((gl != 0.0f && fabsf(gl) < 0x1p-50f) || (gr != 0.0f && fabsf(gr) < 0x1p-50f)) return;
   const float al = (gl * gl) * __builtin_amdgcn_rcpf(dl);
   const float ar = (gr * gr) * __builtin_amdgcn_rcpf(dr);
   const float m = (al + ar) + fabsf(n.parent_gain);
