@@ -114,14 +114,35 @@ struct NodeOp {
 
 struct HistTask { uint32_t slot, begin, end, single; };
 
-// Per-node best-feature key: (gain order << 32) | ~feature, so the maximum is
-// the largest gain and, among equal gains, the lowest feature -- the serial
-// first-strictly-greater scan over features (kernels/boost.metal:1245-1265).
-// +0 and -0 map to one key; 0 means no valid candidate.
-__device__ __forceinline__ uint64_t best_key(float gain, uint32_t feature) {
-  uint32_t bits = gain == 0.0f ? 0u : __float_as_uint(gain);
-  uint32_t order = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
-  return ((uint64_t)order << 32) | (uint64_t)(~feature);
+// Per-node best-feature key: (gain order << 32) | a low word that falls as the
+// feature rises, so the maximum is the largest gain and, among equal gains,
+// the lowest feature -- the serial first-strictly-greater scan over features
+// (kernels/boost.metal:1245-1265).  +0 and -0 map to one key; 0 means no
+// valid candidate.  Up to kKeyFeatures features the low word is
+// (kKeyFeatures - feature) << 16 | backward << 15 | bin: the partition reads
+// a split's feature, bin and direction off the key, with no load of the
+// feature's record after it; with more features it is ~feature.  A feature
+// offers one candidate per node, so the bin bits never decide between keys.
+constexpr uint32_t kKeyFeatures = 65535;
+__device__ __forceinline__ uint64_t best_key(float gain, uint32_t feature, uint32_t order, uint32_t count,
+                                             uint32_t cols) {
+  const uint32_t bits = gain == 0.0f ? 0u : __float_as_uint(gain);
+  const uint32_t rank = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+  uint32_t low = ~feature;
+  if (cols <= kKeyFeatures) {
+    const uint32_t backward = order >= count ? 1u : 0u;
+    const uint32_t bin = backward ? 2 * count - 1 - order : order;  // < 2^15 (max_bin <= 4096)
+    low = ((kKeyFeatures - feature) << 16) | (backward << 15) | bin;
+  }
+  return ((uint64_t)rank << 32) | (uint64_t)low;
+}
+__device__ __forceinline__ uint32_t key_feature(uint64_t key, uint32_t cols) {
+  return cols <= kKeyFeatures ? kKeyFeatures - (uint32_t)((key >> 16) & 0xffffu) : ~(uint32_t)key;
+}
+// The gain a key was made from (-0 comes back as +0).
+__device__ __forceinline__ float key_gain(uint64_t key) {
+  const uint32_t rank = (uint32_t)(key >> 32);
+  return __uint_as_float((rank & 0x80000000u) ? rank ^ 0x80000000u : ~rank);
 }
 struct PartTask { uint32_t slot, begin, end, padding; };
 
@@ -1504,7 +1525,8 @@ __device__ __forceinline__ void score_survivors(NodeEval& n, const LaneBins<CH>&
 // The item's winner (the lane holding the largest key) records its SplitRec
 // and offers its feature to the node's best key.
 __device__ __forceinline__ void offer_best(const NodeEval& n, uint64_t mine, uint64_t top, SplitRec* rec,
-                                           unsigned long long* node_best, uint32_t feature, uint32_t cols) {
+                                           unsigned long long* node_best, uint32_t feature, uint32_t count,
+                                           uint32_t cols) {
   if (top != 0 && mine == top) {
     *rec = SplitRec{n.best_gain, n.best_order, (int64_t)n.best_lg, (int64_t)n.best_lh};
     // With many features a node's items serialize on its one key (2,000
@@ -1512,7 +1534,7 @@ __device__ __forceinline__ void offer_best(const NodeEval& n, uint64_t mine, uin
     // any value read is a lower bound: a key at or below it cannot win and
     // skips the atomic.  With few features the read's round trip costs more
     // than the contention (64 features: 0.125 -> 0.163 ms per round).
-    const unsigned long long key = best_key(n.best_gain, feature);
+    const unsigned long long key = best_key(n.best_gain, feature, n.best_order, count, cols);
     if (cols < kContendedFeatures || key > __hip_atomic_load(node_best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
       atomicMax(node_best, key);
   }
@@ -1534,7 +1556,7 @@ __device__ __forceinline__ void score_node(NodeEval& n, const LaneBins<CH>& lb, 
   const float node_lo = item_max_f32<W>(lo, xf, wave_in_item);
   score_survivors<CH>(n, lb, pre_g, pre_h, b0, count, eg, eh, mcw, p, survivors<CH>(n, hi_f, hi_b, node_lo, b0, count));
   const uint64_t mine = candidate_key(n);
-  offer_best(n, mine, item_max_u64<W>(mine, xk, wave_in_item), rec, node_best, feature, cols);
+  offer_best(n, mine, item_max_u64<W>(mine, xk, wave_in_item), rec, node_best, feature, count, cols);
 }
 
 // Both children of a pair, with one barrier per exchange (W > 1) instead of
@@ -1556,8 +1578,8 @@ __device__ __forceinline__ void score_pair(NodeEval& na, const LaneBins<CH>& la,
   const uint64_t minea = candidate_key(na), mineb = candidate_key(nb);
   uint64_t topa = minea, topb = mineb;
   item_max2_u64<W>(topa, topb, xka, xkb, wave_in_item);
-  offer_best(na, minea, topa, reca, besta, feature, cols);
-  offer_best(nb, mineb, topb, recb, bestb, feature, cols);
+  offer_best(na, minea, topa, reca, besta, feature, count, cols);
+  offer_best(nb, mineb, topb, recb, bestb, feature, count, cols);
 }
 
 // ---------------------------------------------------------------------------
@@ -1840,7 +1862,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
   }
   if (dense_root) {
     const uint64_t key = best_keys[0];
-    const uint32_t f = key ? ~(uint32_t)key : 0u;
+    const uint32_t f = key ? key_feature(key, F) : 0u;
     const uint32_t cf = t.counts[f];
     stage_feature(t.hist[0], t.counts[0], eg, eh, root0g, root0h);
     stage_feature(t.hist[0] + (uint64_t)f * t.bins1 * 2, cf, eg, eh, rootfg, rootfh);
@@ -1918,7 +1940,7 @@ __device__ void select_level(const Tree& t, uint32_t depth, uint8_t* stage) {
         best.feature = -1;
         best.gain = -INFINITY;
         if (key) {
-          const uint32_t f = ~(uint32_t)key;
+          const uint32_t f = key_feature(key, F);
           best = make_cand(ne, t.recs[(uint64_t)i * F + f], f, t.counts[f], t.cuts + (uint64_t)f * t.cut_stride, eg,
                            eh, p);
         }
@@ -2194,15 +2216,32 @@ __device__ __forceinline__ void load_tile_rows(const uint32_t* rows, const PartT
 __device__ NodeOp node_op(const Tree& t, uint32_t depth, uint32_t slot) {
   const Frontier node = t.frontier[depth & 1][slot];
   const uint64_t key = best_bank(t, depth)[slot];
-  const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   const MgbSplitParams& p = t.sp;
+  if (key && depth + 1 < t.max_depth && t.cols <= kKeyFeatures) {
+    // A split above the last level only moves rows, by the feature, bin and
+    // direction the key carries: no record load, no candidate rebuilt.  The
+    // expansion test is the one below on the same gain.
+    const float gain = key_gain(key);
+    const uint32_t f = key_feature(key, t.cols);
+    if (f < t.cols && gain > 1.0e-6f && gain >= p.min_split_loss) {
+      const uint32_t bin = (uint32_t)key & 0x7fffu, backward = ((uint32_t)key >> 15) & 1u;
+      NodeOp op;
+      op.op = kOpSplit;
+      op.feature = f;
+      op.last_left_bin = backward ? (int32_t)bin - 1 : (int32_t)bin;
+      op.default_left = backward;
+      op.leaf = node.leaf; op.left_leaf = 0; op.right_leaf = 0; op.child_slot = 0;
+      return op;
+    }
+  }
+  const int eg = scale_exponent(t.scales[0]), eh = scale_exponent(t.scales[1]);
   NodeEval ne;
   node_begin(ne, (uint64_t)node.sum_g, (uint64_t)node.sum_h, 0, 0, eg, eh, p, node.lower, node.upper, 0);
   Cand best;
   best.feature = -1;
   best.gain = -INFINITY;
   if (key) {
-    const uint32_t f = ~(uint32_t)key;
+    const uint32_t f = key_feature(key, t.cols);
     best = make_cand(ne, t.recs[(uint64_t)slot * t.cols + f], f, t.counts[f], t.cuts + (uint64_t)f * t.cut_stride,
                      eg, eh, p);
   }
