@@ -311,6 +311,39 @@ def test_csr_sketch_feature_groups_match_oracle(xgb):
 
 
 
+@pytest.mark.parametrize("sparse", [True, False])
+def test_features_beyond_65535_match_oracle(xgb, sparse):
+    """66,000 features, the label carried by features 65,900 (in every row)
+    and 100 (in half of them): past 65,535 features a node's best-split key
+    holds the feature alone and the partition rebuilds the split from the
+    feature's record, so trees splitting on feature 65,900 check that path,
+    as CSR and as a dense matrix with the absent entries missing."""
+    import scipy.sparse as sp
+    rows, cols = 2000, 66000
+    rng = np.random.default_rng(3)
+    r = np.repeat(np.arange(rows), 6)
+    c = rng.integers(0, cols, size=rows * 6)
+    v = rng.normal(size=rows * 6).astype(np.float32)
+    strong = rng.normal(size=rows).astype(np.float32)
+    weak = rng.normal(size=rows).astype(np.float32)
+    half = rng.random(rows) < 0.5
+    r = np.concatenate([r, np.arange(rows), np.nonzero(half)[0]])
+    c = np.concatenate([c, np.full(rows, 65900), np.full(half.sum(), 100)])
+    v = np.concatenate([v, strong, weak[half]])
+    csr = sp.csr_matrix((v, (r, c)), shape=(rows, cols))
+    csr.sum_duplicates()
+    csr.sort_indices()
+    y = ((strong + 0.7 * np.where(half, weak, 0)) > 0).astype(np.float32)
+    X = W.csr_to_dense(csr.indptr, csr.indices, csr.data.astype(np.float32), cols)
+    params = {"objective": "binary:logistic", "tree_method": "hist", "max_depth": 4, "max_bin": 16, "eta": 0.3}
+    d = xgb.DMatrix(csr if sparse else X, label=y)
+    bst = xgb.train(params, d, 2)
+    ref = O.train(X, y, _oracle_params(params), 2)
+    assert 65900 in [int(n["feature"]) for n in ref["trees"][0][:ref["sizes"][0]]]
+    assert_trees_equal(bst, ref)
+    np.testing.assert_array_equal(bst.predict(d, output_margin=True).view(np.uint32), ref["margin"].view(np.uint32))
+
+
 @pytest.mark.parametrize("group_entries", [0, 20000])
 def test_csr_sketch_skewed_columns_match_oracle(xgb, group_entries):
     """One dense column among 2,000 nearly empty ones (0 to 3 entries each)
