@@ -1722,9 +1722,10 @@ __global__ __launch_bounds__(W == 1 ? kSplitPack * kWave : W * kWave) void k_spl
   if constexpr (W > 1 && CH > 1) {
     // Several waves and bins per lane: both children share each exchange's
     // barrier (C4's wide levels: split 1.374 -> 1.352 ms per round).  With
-    // one wave per item there is no barrier to share, and with one bin per
-    // lane the pair's longer live ranges cost more than the barrier saves
-    // (C2: 39.2 -> 40.2 ms per fit).
+    // one wave per item there is no barrier to share (scored together
+    // anyway: C2 unchanged, 1M x 2000 CSR split 0.749 -> 0.784 ms per round),
+    // and with one bin per lane the pair's longer live ranges cost more than
+    // the barrier saves (C2: 39.2 -> 40.2 ms per fit).
     score_pair<W, CH>(ex, x, pre[0], pre[1], t.recs + (uint64_t)built * F + f, best_bank(t, depth) + built, eo, o,
                       pre[2], pre[3], t.recs + (uint64_t)other * F + f, best_bank(t, depth) + other, b0, count, eg, eh,
                       mcw, filter, lambda, t.sp, xlo[slot_in_block][0], xlo[slot_in_block][1], xkey[slot_in_block][0],
