@@ -2514,8 +2514,16 @@ __global__ __launch_bounds__(kPartThreads) void k_apply(Tree t, uint32_t depth) 
         uint32_t tl = 0, ta = 0;
         for (int k = 0; k < kPartPer; ++k)
           for (uint32_t q = 0; q < kWaves; ++q) { tl += wave_left[k][q]; ta += wave_active[k][q]; }
-        base_left = atomicAdd(&cursors[2 * task.slot], tl);
-        base_right = atomicSub(&cursors[2 * task.slot + 1], ta - tl) - (ta - tl);
+        // Both cursors (left: low word, rising from the node's start; right:
+        // high word, falling from its end) in one 64-bit atomic: the low word
+        // never carries (it stays below the node's end), and adding
+        // (2^32 - right rows) << 32 subtracts them from the high word.
+        const uint32_t tr = ta - tl;
+        const unsigned long long old =
+            atomicAdd(reinterpret_cast<unsigned long long*>(&cursors[2 * task.slot]),
+                      (unsigned long long)tl | ((unsigned long long)(0u - tr) << 32));
+        base_left = (uint32_t)old;
+        base_right = (uint32_t)(old >> 32) - tr;
       }
     }
     __syncthreads();
