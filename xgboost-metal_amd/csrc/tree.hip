@@ -224,9 +224,10 @@ __device__ __forceinline__ uint32_t* cursor_bank(const Tree& t, uint32_t depth) 
   return t.cursors + (uint64_t)(depth & 1) * 2 * t.slots;
 }
 // A node's best key is spread over kKeyWays words, one 64-byte line: feature
-// f offers into word f mod kKeyWays, and the node's key is the words'
-// maximum.  One word for all of a node's features serialized their atomics
-// (262,144 x 64: 32.8 -> 32.0 ms per 100 rounds with eight words).
+// f offers into word f mod kKeyWays (below kContendedFeatures features; see
+// offer_best), and the node's key is the words' maximum.  One word for all
+// of a node's features serialized their atomics (262,144 x 64: 32.8 -> 32.0
+// ms per 100 rounds with eight words).
 constexpr uint32_t kKeyWays = 8;
 __device__ __forceinline__ unsigned long long* best_bank(const Tree& t, uint32_t depth) {
   return t.best + (uint64_t)(depth & 1) * t.slots * kKeyWays;
@@ -1548,8 +1549,12 @@ __device__ __forceinline__ void offer_best(const NodeEval& n, uint64_t mine, uin
     // skips the atomic.  With few features the read's round trip costs more
     // than the contention (64 features: 0.125 -> 0.163 ms per round).
     const unsigned long long key = best_key(n.best_gain, feature, n.best_order, count, cols);
-    unsigned long long* word = node_best + feature % kKeyWays;
-    if (cols < kContendedFeatures || key > __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    // Few features spread their offers over the node's words; many offer
+    // into its first word only, so the value read is the node's best so far
+    // (eight words there: 1M x 2000 CSR split 0.74 -> 1.07 ms per round).
+    const bool contended = cols >= kContendedFeatures;
+    unsigned long long* word = node_best + (contended ? 0u : feature % kKeyWays);
+    if (!contended || key > __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
       atomicMax(word, key);
   }
 }
