@@ -2402,8 +2402,8 @@ __global__ __launch_bounds__(kOrderThreads) void k_final_order(Tree t, uint32_t 
 // partition tiles of up to part_tile rows of one node, works out that node's
 // split itself (node_op), and moves its rows: a split node's left rows fill
 // its segment upwards from the start and its right rows downwards from the
-// end, each tile claiming its ranges with one atomic on each of the node's
-// two cursors and writing ranks (chunk, wave, lane) into them.  The order of
+// end, each tile claiming both ranges with one 64-bit atomic on the node's
+// two adjacent cursor words and writing ranks (chunk, wave, lane) into them.  The order of
 // rows inside a child depends on which tile claims first; nothing downstream
 // depends on it (histograms are exact integer sums and the margin update is
 // per row).  STABLE: the tile's directions and positions come from
