@@ -126,7 +126,7 @@ typedef struct {
  * rows of shallow nodes are dense enough that one feature column per load
  * beats partial rows of the row-major matrix (0: never). */
 typedef struct {
-  uint32_t rows, cols, max_bin, max_depth;
+  uint32_t rows, cols, max_bin, max_depth;  /* rows below 2^31, max_depth 1..16 */
   uint32_t rows_per_tile, features_per_group, unit_hessian, dense;
   uint32_t column_levels;
   uint32_t sparse;  /* 1: the workspace is for mgb_grow_tree_csr (no per-tile partial histograms) */

@@ -200,3 +200,27 @@ def test_device_tie_sort_follows_libstdcxx():
         checksum = int((order * (2 * np.arange(n, dtype=np.uint64) + 1)).sum(dtype=np.uint64))
         assert checksum == case["checksum"], case
         assert order[:len(case["order"])].tolist() == case["order"], case
+
+
+@pytest.mark.parametrize("sparse", [False, True])
+def test_grow_tree_rejects_rows_from_two_to_the_31(sparse):
+    """Both tree drivers refuse 2^31 rows or more before any device work (row
+    positions in the kernels are 32-bit and run past a task's end); the check
+    is host-side, so it runs without a GPU."""
+    import device_lib as D
+    lib = D.lib()
+    shape = D.MgbTreeShape(rows=1 << 31, cols=4, max_bin=16, max_depth=3, rows_per_tile=1024,
+                           features_per_group=4, sparse=1 if sparse else 0)
+    if sparse:
+        class Csr(ctypes.Structure):
+            _fields_ = [("rows", ctypes.c_uint32), ("cols", ctypes.c_uint32), ("max_bin", ctypes.c_uint32),
+                        ("cut_stride", ctypes.c_uint32), ("bin_bytes", ctypes.c_uint32),
+                        ("missing_code", ctypes.c_uint32), ("nnz", ctypes.c_uint64)]
+        m = Csr(rows=1 << 31, cols=4, max_bin=16, cut_stride=16, bin_bytes=1, missing_code=255, nnz=0)
+        rc = lib.mgb_grow_tree_csr(ctypes.byref(shape), ctypes.byref(m), *([None] * 18))
+    else:
+        m = D.MgbMatrix(rows=1 << 31, cols=4, row_stride=4, bin_bytes=1, max_bin=16, cut_stride=16,
+                        missing_code=255, group_features=4, group_stride=4)
+        rc = lib.mgb_grow_tree(ctypes.byref(shape), ctypes.byref(m), *([None] * 14))
+    assert rc == -1
+    assert "below 2^31" in lib.mgb_last_error().decode()

@@ -2783,9 +2783,15 @@ int launch_apply(const Tree& t, uint32_t depth, uint32_t grid) {
   return 0;
 }
 
+// Row positions inside the kernels are 32-bit and run up to two batches past
+// a task's end (the histogram's prefetch), so row counts stay below 2^31, the
+// sketch's own limit.
+constexpr uint32_t kMaxTreeRows = 0x7fffffffu;
+
 int validate(const MgbTreeShape* s, const MgbMatrix* m) {
   if (!s || !m) { set_error("null shape or matrix"); return -1; }
   if (s->max_depth < 1 || s->max_depth > 16) { set_error("max_depth must be in [1, 16]"); return -1; }
+  if (s->rows > kMaxTreeRows) { set_error("rows must be below 2^31"); return -1; }
   if (s->rows != m->rows || s->cols != m->cols || s->max_bin != m->max_bin) {
     set_error("tree shape does not match the bin matrix");
     return -1;
@@ -3071,6 +3077,7 @@ int mgb_grow_tree_csr(const MgbTreeShape* shape, const MgbCsrMatrix* m, const ui
   if (!shape || !m) { set_error("null shape or matrix"); return -1; }
   if (!shape->sparse) { set_error("mgb_grow_tree_csr: the tree shape must have sparse = 1"); return -1; }
   if (shape->max_depth < 1 || shape->max_depth > 16) { set_error("max_depth must be in [1, 16]"); return -1; }
+  if (shape->rows > kMaxTreeRows) { set_error("rows must be below 2^31"); return -1; }
   if (shape->rows != m->rows || shape->cols != m->cols || shape->max_bin != m->max_bin) {
     set_error("tree shape does not match the CSR matrix");
     return -1;
