@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kGradThreads) void k_gradients(MgbGradParams p, con
   __syncthreads();
   const uint32_t first = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
   RowSampler sampler(p.sample_seed, first, stride, p.subsample < 1.0f);
-  for (uint32_t r = first; r < p.rows; r += stride, sampler.next()) {
+  for (uint64_t r = first; r < p.rows; r += stride, sampler.next()) {
     float pred = margin[r], label = labels[r];
     float weight = p.has_weight ? weights[r] : 1.0f;
     float g = pred - label, h = 1.0f;
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(kGradThreads) void k_gradient_mass(MgbGradParams p,
   __syncthreads();
   const uint32_t first = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
   RowSampler sampler(p.sample_seed, first, stride, p.subsample < 1.0f);
-  for (uint32_t r = first; r < p.rows; r += stride, sampler.next()) {
+  for (uint64_t r = first; r < p.rows; r += stride, sampler.next()) {
     float2 v = grad[r];
     if (p.subsample < 1.0f && !keep_state(sampler.state, p.subsample)) {
       v = make_float2(0.0f, 0.0f);
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(kBaseThreads) void k_base_score(const float* __rest
   const bool logistic = objective == 1 || objective == 2;
   const bool float_product = logistic && fabsf(spw - 1.0f) > 1.0e-6f;
   double s = 0, c = 0, ws = 0, wc = 0;
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+  for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
     float w = weights ? weights[r] : 1.0f;
     float y = labels[r];
     if (logistic) w *= y == 1.0f ? spw : 1.0f;
@@ -483,7 +483,7 @@ __global__ void k_fill(float* __restrict__ data, uint64_t count, float value) {
 __global__ void k_predict(const float* __restrict__ X, uint32_t rows, uint32_t cols,
                           const MgbTreeNode* __restrict__ nodes, const uint32_t* __restrict__ offsets,
                           uint32_t trees, float* __restrict__ margin) {
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+  for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
     const float* row = X + (uint64_t)r * cols;
     float sum = margin[r];
     for (uint32_t t = 0; t < trees; ++t) {

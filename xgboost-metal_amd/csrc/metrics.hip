@@ -137,7 +137,7 @@ struct MassSum {
 // Ascending uint32 keys for descending prediction order; +0 and -0 share one.
 __global__ void k_auc_keys(const float* __restrict__ pred, uint32_t rows, uint32_t* __restrict__ keys,
                            uint32_t* __restrict__ index) {
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += (uint64_t)gridDim.x * blockDim.x) {
     uint32_t b = __float_as_uint(pred[i]);
     if ((b & 0x7fffffffu) == 0) b = 0;
     const uint32_t ascending = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -150,7 +150,7 @@ __global__ void k_auc_keys(const float* __restrict__ pred, uint32_t rows, uint32
 // binary64 (kernels/radix_sort.metal.h:316-323).
 __global__ void k_auc_mass(const uint32_t* __restrict__ order, const float* __restrict__ labels,
                            const float* __restrict__ weights, uint32_t rows, Mass* __restrict__ mass) {
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += (uint64_t)gridDim.x * blockDim.x) {
     const uint32_t r = order[i];
     const float y = labels[r], w = weights ? weights[r] : 1.0f;
     mass[i] = Mass{(double)fabsf(y * w), (double)fabsf((1.0f - y) * w)};
@@ -209,7 +209,7 @@ __global__ void k_auc_area(const Mass* __restrict__ steps, const Mass* __restric
   const uint32_t runs = *runs_ptr;
   const Mass last_before = before[runs - 1], last = steps[runs - 1];
   const double positives = last_before.tp + last.tp;
-  for (uint32_t s = blockIdx.x * blockDim.x + threadIdx.x; s < runs; s += gridDim.x * blockDim.x) {
+  for (uint64_t s = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; s < runs; s += (uint64_t)gridDim.x * blockDim.x) {
     const Mass step = steps[s], prev = before[s];
     area[s] = pr ? pr_step_area(prev, step, positives) : step.fp * (2.0 * prev.tp + step.tp) * 0.5;
   }

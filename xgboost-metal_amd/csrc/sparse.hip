@@ -16,7 +16,7 @@ namespace {
 
 // row_of[k] = the row that owns nonzero k.
 __global__ void k_row_of(const uint64_t* __restrict__ indptr, uint32_t rows, uint32_t* __restrict__ row_of) {
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x)
+  for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x)
     for (uint64_t k = indptr[r]; k < indptr[r + 1]; ++k) row_of[k] = r;
 }
 
@@ -38,7 +38,7 @@ __global__ void k_gather_csc(const uint32_t* __restrict__ perm, const uint32_t* 
 // colptr[f] = first position of column f in the column-sorted indices.
 __global__ void k_colptr(const uint32_t* __restrict__ sorted_cols, uint64_t nnz, uint32_t cols,
                          uint64_t* __restrict__ colptr) {
-  for (uint32_t f = blockIdx.x * blockDim.x + threadIdx.x; f <= cols; f += gridDim.x * blockDim.x) {
+  for (uint64_t f = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; f <= cols; f += (uint64_t)gridDim.x * blockDim.x) {
     uint64_t lo = 0, hi = nnz;
     while (lo < hi) {
       const uint64_t mid = lo + (hi - lo) / 2;
@@ -91,7 +91,7 @@ __device__ __forceinline__ int64_t find_in_row(const uint32_t* __restrict__ indi
 __global__ void k_predict_csr(const uint64_t* __restrict__ indptr, const uint32_t* __restrict__ indices,
                               const float* __restrict__ values, uint32_t rows, const MgbTreeNode* __restrict__ nodes,
                               const uint32_t* __restrict__ offsets, uint32_t trees, float* __restrict__ margin) {
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+  for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
     const uint64_t b = indptr[r], e = indptr[r + 1];
     float sum = margin[r];
     for (uint32_t t = 0; t < trees; ++t) {

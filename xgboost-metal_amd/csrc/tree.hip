@@ -583,7 +583,7 @@ __global__ __launch_bounds__(kSelectThreads) void k_plan(Tree t, uint32_t depth)
 // Single-histogram entry point (mgb_histogram) on a caller's row list: the
 // gradient pairs of list 0 in list order (the histogram reads them so).
 __global__ void k_gather_pairs(Tree t, uint32_t count) {
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
     t.gh[0][i] = t.grad[t.rows[0][i]];
 }
 
@@ -989,7 +989,7 @@ __global__ __launch_bounds__(kCsrThreads) void k_root_totals(Tree t) {
   __shared__ uint64_t part[kCsrThreads / kWave][2];
   const float sg = t.scales[0], sh = t.scales[1];
   uint64_t g = 0, h = 0;
-  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < t.rows_n; r += gridDim.x * blockDim.x) {
+  for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < t.rows_n; r += (uint64_t)gridDim.x * blockDim.x) {
     const float2 v = t.grad[r];
     g += (uint64_t)(int64_t)rintf(v.x * sg);
     h += (uint64_t)(int64_t)rintf(v.y * sh);
