@@ -607,13 +607,30 @@ void predict_into_results(Learner& b, DMatrix& d, const char* config) {
   std::lock_guard<std::recursive_mutex> lock(b.mutex);
   Json c = config && *config ? Json::parse(config) : Json::object();
   const int64_t type = c.contains("type") ? c.at("type").integer() : 0;
-  require(type == 0 || type == 1, "Only value (type 0) and margin (type 1) predictions are supported.");
+  require(type >= 0 && type <= 6, "Invalid prediction type.");
+  require(type != 4 && type != 5, "Interaction contributions (prediction types 4 and 5) are not supported.");
   const uint32_t begin = c.contains("iteration_begin") ? (uint32_t)c.at("iteration_begin").integer() : 0;
   const uint32_t end = c.contains("iteration_end") ? (uint32_t)c.at("iteration_end").integer() : 0;
   const bool strict = c.contains("strict_shape") && c.at("strict_shape").is_bool() && c.at("strict_shape").boolean();
-  g_results.floats = b.predict(d, type == 1, begin, end);
   g_results.shape.clear();
   g_results.shape.push_back(d.rows);
+  if (type >= 2) {
+    // Leaf and contribution predictions cover rounds [0, end) only
+    // (src/learner.cpp:467-469).
+    require(begin == 0 || b.trees.empty(),
+            "Leaf and contribution predictions support only iteration end; use model slicing for a nonzero start.");
+    g_results.floats = b.predict_explain(d, (int)type, end);
+    if (type == 6) {
+      const uint64_t n = d.rows ? g_results.floats.size() / d.rows : 0;
+      g_results.shape.push_back(n);
+      if (strict) { g_results.shape.push_back(1); g_results.shape.push_back(1); }
+    } else {
+      if (strict) g_results.shape.push_back(1);
+      g_results.shape.push_back((uint64_t)d.cols + 1);
+    }
+    return;
+  }
+  g_results.floats = b.predict(d, type == 1, begin, end);
   if (strict) g_results.shape.push_back(1);
 }
 

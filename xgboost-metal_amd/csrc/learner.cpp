@@ -1103,6 +1103,79 @@ const float* Learner::predict_device(DMatrix& data, bool output_margin, uint32_t
   return d_out;
 }
 
+namespace {
+
+// Cover-weighted mean leaf value of every node of a tree, children before
+// parents (a node's children have larger ids), and the tree's depth.
+uint32_t node_means(const std::vector<MgbTreeNode>& t, float* means) {
+  std::vector<uint32_t> depth(t.size(), 0);
+  uint32_t deepest = 0;
+  for (size_t i = 0; i < t.size(); ++i) {
+    if (t[i].left >= 0) {
+      require((size_t)t[i].left > i && (size_t)t[i].right > i && (size_t)t[i].left < t.size() &&
+                  (size_t)t[i].right < t.size(),
+              "Tree nodes must list children after their parent.");
+      depth[t[i].left] = depth[t[i].right] = depth[i] + 1;
+      deepest = std::max(deepest, depth[i] + 1);
+    }
+  }
+  for (size_t k = t.size(); k-- > 0;) {
+    const MgbTreeNode& n = t[k];
+    means[k] = n.left < 0 ? n.leaf
+                          : (means[n.left] * t[n.left].cover + means[n.right] * t[n.right].cover) / n.cover;
+  }
+  return deepest;
+}
+
+}  // namespace
+
+std::vector<float> Learner::predict_explain(DMatrix& data, int type, uint32_t end) {
+  drain();
+  require(type == 2 || type == 3 || type == 6, "Prediction type must be 2, 3 or 6 here.");
+  if (end == 0 || end > trees.size()) end = (uint32_t)trees.size();
+  if (initialized)
+    require(data.cols == num_feature, "Feature shape mismatch: expected " + std::to_string(num_feature) + ", got " +
+                                          std::to_string(data.cols));
+  const uint64_t width = type == 6 ? end : (uint64_t)data.cols + 1;
+  std::vector<float> out((size_t)data.rows * width, 0.0f);
+  if (!data.rows) return out;
+  if (type == 6 && end == 0) return out;
+  data.upload();
+  upload_model();
+  DeviceBuffer d_out;
+  d_out.ensure(out.size() * sizeof(float));
+  const uint64_t* indptr = data.sparse ? data.d_indptr.as<uint64_t>() : nullptr;
+  const uint32_t* indices = data.sparse ? data.d_indices.as<uint32_t>() : nullptr;
+  const float* X = data.sparse ? data.d_values.as<float>() : data.d_data.as<float>();
+  if (type == 6) {
+    kcheck(mgb_predict_leaf(X, indptr, indices, data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
+                            d_model_offsets_.as<uint32_t>(), end, d_out.as<float>()),
+           "leaf prediction");
+  } else {
+    std::vector<float> means;
+    uint32_t deepest = 0;
+    for (uint32_t t = 0; t < end; ++t) {
+      const size_t at = means.size();
+      means.resize(at + trees[t].nodes.size());
+      deepest = std::max(deepest, node_means(trees[t].nodes, means.data() + at));
+    }
+    if (means.empty()) means.resize(1);
+    d_model_means_.upload(means.data(), means.size() * sizeof(float));
+    DeviceBuffer d_base;
+    if (!data.base_margin.empty()) {
+      require(data.base_margin.size() == data.rows, "base_margin must have one value per row.");
+      d_base.upload(data.base_margin.data(), data.rows * sizeof(float));
+    }
+    kcheck(mgb_predict_contribs(X, indptr, indices, data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
+                                d_model_means_.as<float>(), d_model_offsets_.as<uint32_t>(), end, deepest,
+                                type == 3 ? 1u : 0u, d_base.get() ? d_base.as<float>() : nullptr,
+                                base_margin_value(), d_out.as<float>()),
+           "contribution prediction");
+  }
+  kcheck(mgb_memcpy_d2h(out.data(), d_out.get(), out.size() * sizeof(float)), "device-to-host copy");
+  return out;
+}
+
 std::vector<float> Learner::predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end) {
   std::vector<float> out(data.rows);
   if (!data.rows) return out;

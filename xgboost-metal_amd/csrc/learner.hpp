@@ -138,6 +138,10 @@ class Learner {
   void boost(DMatrix& data, const float* grad, const float* hess, size_t count);
   // Predictions (margin when output_margin) for rounds [begin, end); end 0 = all.
   std::vector<float> predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end);
+  // Leaf indices (type 6: rows x trees) or feature contributions (type 2
+  // exact, 3 approximate: rows x (cols + 1), the bias last) of rounds
+  // [0, end); end 0 = all (src/learner.cpp:455-560).
+  std::vector<float> predict_explain(DMatrix& data, int type, uint32_t end);
   // The same predictions left on the device: in `scratch`, or in the
   // training-matrix cache when that holds them already.
   const float* predict_device(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end, DeviceBuffer& scratch);
@@ -202,6 +206,8 @@ class Learner {
   DeviceBuffer d_grad_, d_mass_, d_scales_, d_tree_ws_, d_node_count_, d_base_;
   // Model on the device for prediction.
   DeviceBuffer d_model_nodes_, d_model_offsets_;
+  DeviceBuffer d_model_means_;  // each node's cover-weighted mean leaf value (contributions)
+  size_t means_version_ = SIZE_MAX;
   size_t model_version_ = SIZE_MAX, model_trees_ = 0;
   size_t uploaded_trees_ = 0;
   std::map<std::string, double> seconds_;

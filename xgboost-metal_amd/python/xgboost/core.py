@@ -645,11 +645,15 @@ class Booster:
                 pred_contribs: bool = False, approx_contribs: bool = False, pred_interactions: bool = False,
                 validate_features: bool = True, training: bool = False,
                 iteration_range: Tuple[int, int] = (0, 0), strict_shape: bool = False) -> np.ndarray:
-        if pred_leaf or pred_contribs or pred_interactions:
-            raise XGBoostError("pred_leaf/pred_contribs are not supported by this engine")
         if not isinstance(data, DMatrix):
             raise TypeError("Expecting data to be a DMatrix object")
-        config = {"type": 1 if output_margin else 0, "training": bool(training),
+        # One prediction type at a time (reference core.py:2603-2614): 1 margin,
+        # 2 / 3 exact / approximate contributions, 4 / 5 interactions, 6 leaf.
+        kinds = [t for flag, t in ((output_margin, 1), (pred_contribs, 3 if approx_contribs else 2),
+                                   (pred_interactions, 5 if approx_contribs else 4), (pred_leaf, 6)) if flag]
+        if len(kinds) > 1:
+            raise ValueError("One type of prediction at a time.")
+        config = {"type": kinds[0] if kinds else 0, "training": bool(training),
                   "iteration_begin": int(iteration_range[0]), "iteration_end": int(iteration_range[1]),
                   "strict_shape": bool(strict_shape)}
         shape = ctypes.POINTER(c_bst_ulong)()
