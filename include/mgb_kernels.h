@@ -343,7 +343,7 @@ int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode*
                 uint32_t trees, float* margin);
 
 /* ---- leaf indices and feature contributions -------------------------- *
- * (src/learner.cpp:455-560 Learner::predict types 6, 2 and 3.)  Rows are
+ * (src/learner.cpp:455-560 Learner::predict types 6 and 2-5.)  Rows are
  * dense (X: rows x cols floats, indptr NULL) or CSR (X holds the values,
  * indptr rows+1 offsets, indices strictly increasing column ids a row;
  * absent entries are missing); trees [tree_offsets[0], ...) of `nodes`.
@@ -354,13 +354,18 @@ int mgb_predict(const float* X, uint32_t rows, uint32_t cols, const MgbTreeNode*
  * node_means holds each node's cover-weighted mean leaf value at the node's
  * index in `nodes`.  approximate = 0: exact path-dependent TreeSHAP (trees of
  * depth <= 16, max_depth the deepest tree's); 1: each split's feature gets the
- * change of the node mean along the row's path. */
+ * change of the node mean along the row's path.  interactions = 1: each row
+ * is a (cols + 1) x (cols + 1) matrix at out + r * (cols + 1)^2 -- exact: SHAP
+ * interaction values (off the diagonal half the change of feature j's value
+ * between feature i always present and always absent, on it feature i's
+ * value less its interactions); approximate: the approximate values on the
+ * diagonal -- with the bias in the last element (types 4 and 5). */
 int mgb_predict_leaf(const float* X, const uint64_t* indptr, const uint32_t* indices, uint32_t rows, uint32_t cols,
                      const MgbTreeNode* nodes, const uint32_t* tree_offsets, uint32_t trees, float* out);
 int mgb_predict_contribs(const float* X, const uint64_t* indptr, const uint32_t* indices, uint32_t rows,
                          uint32_t cols, const MgbTreeNode* nodes, const float* node_means,
                          const uint32_t* tree_offsets, uint32_t trees, uint32_t max_depth, uint32_t approximate,
-                         const float* base, float base_value, float* out);
+                         uint32_t interactions, const float* base, float base_value, float* out);
 
 /* ---- evaluation metrics (src/metrics.cpp:8-159) ------------------------- */
 /* Elementwise metric kinds, numbered as the reference's metric table

@@ -1,5 +1,5 @@
-"""Leaf indices and feature contributions on the GPU (reference
-src/learner.cpp:455-560, prediction types 6, 2 and 3), checked against
+"""Leaf indices, feature contributions and their interactions on the GPU
+(reference src/learner.cpp:455-560, prediction types 2 to 6), checked against
 references computed here from the saved model JSON:
 
 - leaf ids: a plain walk of every tree (value < threshold goes left, NaN
@@ -9,7 +9,10 @@ references computed here from the saved model JSON:
 - exact contributions: Shapley values by their definition, over every subset
   of the features, with the path-dependent value function TreeSHAP computes
   (a tree's expectation where the subset fixes a feature the walk follows the
-  row, elsewhere the children are weighted by their cover), in binary64.
+  row, elsewhere the children are weighted by their cover), in binary64;
+- exact interactions: the Shapley interaction index by its definition, and on
+  the diagonal each feature's value less its interactions; approximate ones
+  carry the approximate contributions on the diagonal.
 
 The kernels compute in binary32, so contributions compare within 2e-5 of the
 margin's scale; leaf ids are exact.  Local accuracy (contributions plus bias
@@ -74,6 +77,28 @@ def _shapley(trees, x, cols):
                 s = set(s)
                 phi[f] += w * sum(t.expect(x, s | {f}) - t.expect(x, s) for t in trees)
     return phi
+
+
+def _interactions(trees, x, cols):
+    """SHAP interaction values by their definition: off the diagonal the
+    Shapley interaction index over every subset of the other features, on it
+    the feature's Shapley value less its interactions."""
+    def f(s):
+        return sum(t.expect(x, s) for t in trees)
+    phi = _shapley(trees, x, cols)
+    m = np.zeros((cols + 1, cols + 1))
+    for i in range(cols):
+        for j in range(cols):
+            if i == j:
+                continue
+            others = [g for g in range(cols) if g not in (i, j)]
+            for size in range(cols - 1):
+                w = math.factorial(size) * math.factorial(cols - size - 2) / (2 * math.factorial(cols - 1))
+                for s in combinations(others, size):
+                    s = set(s)
+                    m[i, j] += w * (f(s | {i, j}) - f(s | {i}) - f(s | {j}) + f(s))
+        m[i, i] = phi[i] - sum(m[i, j] for j in range(cols) if j != i)
+    return m
 
 
 def _saabas(trees, x, cols):
@@ -168,12 +193,39 @@ def test_deep_trees_are_locally_accurate_and_shaped(xgb):
     assert bst.predict(d, pred_leaf=True, iteration_range=(0, 2)).shape == (len(X), 2)
 
 
-def test_interactions_and_nonzero_start_are_refused(xgb):
+def test_interactions_match_definitions(xgb):
+    X, y = _data(rows=40, cols=5, seed=5)
+    d = xgb.DMatrix(X, label=y)
+    bst = xgb.train({"max_depth": 3, "max_bin": 32, "eta": 0.5}, d, 3)
+    trees = _trees(bst)
+    margin = bst.predict(d, output_margin=True).astype(np.float64)
+    scale = max(1.0, float(np.abs(margin).max()))
+    exact = bst.predict(d, pred_interactions=True).astype(np.float64)
+    assert exact.shape == (len(X), 6, 6)
+    contribs = bst.predict(d, pred_contribs=True).astype(np.float64)
+    for i, x in enumerate(X[:12]):
+        ref = _interactions(trees, x, 5)
+        np.testing.assert_allclose(exact[i, :5, :5], ref[:5, :5], rtol=0, atol=2e-5 * scale)
+    np.testing.assert_allclose(exact[:, :5, :5].sum(axis=2), contribs[:, :5], rtol=0, atol=2e-5 * scale)
+    np.testing.assert_allclose(exact[:, 5, 5], contribs[:, 5], rtol=0, atol=1e-6 * scale)
+    np.testing.assert_array_equal(exact[:, 5, :5], 0.0)
+    np.testing.assert_array_equal(exact[:, :5, 5], 0.0)
+    np.testing.assert_allclose(exact.sum(axis=(1, 2)), margin, rtol=0, atol=2e-5 * scale)
+    approx = bst.predict(d, pred_interactions=True, approx_contribs=True)
+    saabas = bst.predict(d, pred_contribs=True, approx_contribs=True)
+    assert approx.shape == (len(X), 6, 6)
+    np.testing.assert_array_equal(np.diagonal(approx, axis1=1, axis2=2), saabas)
+    off = approx.copy()
+    off[:, np.arange(6), np.arange(6)] = 0.0
+    np.testing.assert_array_equal(off, 0.0)
+    assert bst.predict(d, pred_interactions=True, strict_shape=True).shape == (len(X), 1, 6, 6)
+
+
+def test_nonzero_start_and_two_types_are_refused(xgb):
     X, y = _data(rows=40, cols=4)
     d = xgb.DMatrix(X, label=y)
     bst = xgb.train({"max_depth": 2}, d, 3)
-    with pytest.raises(xgb.XGBoostError, match="Interaction contributions"):
-        bst.predict(d, pred_interactions=True)
+    assert bst.predict(d, pred_leaf=True, iteration_range=(0, 1)).shape == (len(X),)
     with pytest.raises(xgb.XGBoostError, match="only iteration end"):
         bst.predict(d, pred_contribs=True, iteration_range=(1, 3))
     with pytest.raises(ValueError, match="One type of prediction"):

@@ -608,7 +608,6 @@ void predict_into_results(Learner& b, DMatrix& d, const char* config) {
   Json c = config && *config ? Json::parse(config) : Json::object();
   const int64_t type = c.contains("type") ? c.at("type").integer() : 0;
   require(type >= 0 && type <= 6, "Invalid prediction type.");
-  require(type != 4 && type != 5, "Interaction contributions (prediction types 4 and 5) are not supported.");
   const uint32_t begin = c.contains("iteration_begin") ? (uint32_t)c.at("iteration_begin").integer() : 0;
   const uint32_t end = c.contains("iteration_end") ? (uint32_t)c.at("iteration_end").integer() : 0;
   const bool strict = c.contains("strict_shape") && c.at("strict_shape").is_bool() && c.at("strict_shape").boolean();
@@ -621,12 +620,20 @@ void predict_into_results(Learner& b, DMatrix& d, const char* config) {
             "Leaf and contribution predictions support only iteration end; use model slicing for a nonzero start.");
     g_results.floats = b.predict_explain(d, (int)type, end);
     if (type == 6) {
-      const uint64_t n = d.rows ? g_results.floats.size() / d.rows : 0;
-      g_results.shape.push_back(n);
-      if (strict) { g_results.shape.push_back(1); g_results.shape.push_back(1); }
+      // (src/learner.cpp:549-551): one tree gives a vector, strict_shape
+      // rows x rounds x groups x parallel trees.
+      const uint64_t n = d.rows ? g_results.floats.size() / d.rows : (uint64_t)b.trees.size();
+      if (strict) {
+        g_results.shape.push_back(n);
+        g_results.shape.push_back(1);
+        g_results.shape.push_back(1);
+      } else if (n != 1) {
+        g_results.shape.push_back(n);
+      }
     } else {
       if (strict) g_results.shape.push_back(1);
       g_results.shape.push_back((uint64_t)d.cols + 1);
+      if (type == 4 || type == 5) g_results.shape.push_back((uint64_t)d.cols + 1);
     }
     return;
   }

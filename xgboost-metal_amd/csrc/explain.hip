@@ -1,6 +1,7 @@
 // Prediction beyond values and margins (reference src/learner.cpp:455-560
-// Learner::predict types 2, 3 and 6): each row's leaf index in every tree,
-// and per-feature contributions to its margin -- exact path-dependent
+// Learner::predict types 2 to 6): each row's leaf index in every tree, its
+// per-feature contributions to its margin and their pairwise interactions --
+// exact path-dependent
 // TreeSHAP (Lundberg, Erion and Lee 2018, "Consistent individualized feature
 // attribution for tree ensembles", Algorithm 2) or the approximation that
 // credits each split's feature with the change of the cover-weighted node
@@ -65,15 +66,21 @@ __global__ void k_predict_leaf(const float* __restrict__ X, const uint64_t* __re
 
 // Row r's contributions: out[r * (cols + 1) + f] for feature f, and the bias
 // (the base margin plus every tree's root mean) at f = cols.
+// With `interactions` the row is a (cols + 1) x (cols + 1) matrix holding
+// these values on its diagonal (the reference's approximate interactions,
+// kernels/boost.metal:2183).
 __global__ void k_contribs_approx(const float* __restrict__ X, const uint64_t* __restrict__ indptr,
                                   const uint32_t* __restrict__ indices, uint32_t rows, uint32_t cols,
                                   const MgbTreeNode* __restrict__ nodes, const float* __restrict__ means,
                                   const uint32_t* __restrict__ offsets, uint32_t trees,
-                                  const float* __restrict__ base, float base_value, float* __restrict__ out) {
+                                  const float* __restrict__ base, float base_value, uint32_t interactions,
+                                  float* __restrict__ out) {
+  const uint64_t width = (uint64_t)cols + 1, elements = interactions ? width * width : width;
+  const uint64_t stride = interactions ? width + 1 : 1;
   for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
     const RowView x = row_view(X, indptr, indices, r, cols);
-    float* phi = out + r * (cols + 1);
-    for (uint32_t f = 0; f < cols; ++f) phi[f] = 0.0f;
+    float* phi = out + r * elements;
+    for (uint64_t e = 0; e < elements; ++e) phi[e] = 0.0f;
     float bias = base ? base[r] : base_value;
     for (uint32_t t = 0; t < trees; ++t) {
       const MgbTreeNode* tree = nodes + offsets[t];
@@ -84,11 +91,11 @@ __global__ void k_contribs_approx(const float* __restrict__ X, const uint64_t* _
       while (tree[id].left >= 0) {
         const uint32_t f = (uint32_t)tree[id].feature;
         id = child_of(tree[id], x(f));
-        if (f < cols) phi[f] += mean[id] - here;
+        if (f < cols) phi[f * stride] += mean[id] - here;
         here = mean[id];
       }
     }
-    phi[cols] = bias;
+    phi[elements - 1] = bias;
   }
 }
 
@@ -156,13 +163,76 @@ constexpr uint32_t kShapDepth = 16;
 constexpr uint32_t kShapPath = (kShapDepth + 2) * (kShapDepth + 3) / 2;
 
 // A node still to visit: its path is its parent's segment (at `parent`,
-// `len` elements) extended by (feature, zero, one).
+// `len` elements), extended by (feature, zero, one) unless `extend` is 0 (the
+// split was on the conditioned feature, which never enters the path);
+// `share` is the part of the conditioned walk that reaches the node.
 struct ShapFrame {
   int32_t node;
   uint32_t len, parent;
-  float zero, one;
+  float zero, one, share;
   int32_t feature;
+  uint32_t extend;
 };
+
+// Adds scale x tree's exact contributions of row x to phi[f * stride]
+// (feature f).  condition 0: plain TreeSHAP; +1 / -1: Shapley values of the
+// other features with feature `fixed` always present / always absent (the
+// conditioned walk of SHAP interaction values).  Returns false, having added
+// a part only, for a tree deeper than kShapDepth.
+__device__ bool shap_tree(const MgbTreeNode* __restrict__ tree, const RowView& x, uint32_t cols, float* phi,
+                          uint32_t stride, float scale, int condition, int32_t fixed, PathElem* path,
+                          ShapFrame* stack) {
+  uint32_t top = 0;
+  stack[top++] = ShapFrame{0, 0, 0, 1.0f, 1.0f, 1.0f, -1, 1u};
+  while (top) {
+    const ShapFrame fr = stack[--top];
+    if (fr.share == 0.0f) continue;
+    const uint32_t seg = fr.parent + fr.len + 1;
+    // The host admits trees of depth <= kShapDepth only, which never reach
+    // these limits.
+    if (seg + fr.len >= kShapPath || top + 2 > kShapDepth + 2) return false;
+    for (uint32_t i = 0; i < fr.len; ++i) path[seg + i] = path[fr.parent + i];
+    PathElem* p = path + seg;
+    if (fr.extend) path_extend(p, fr.len, fr.zero, fr.one, fr.feature);
+    uint32_t last = fr.extend ? fr.len : fr.len - 1;
+    const MgbTreeNode n = tree[fr.node];
+    if (n.left < 0) {
+      for (uint32_t i = 1; i <= last; ++i) {
+        const float w = path_unwound_sum(p, last, i);
+        if ((uint32_t)p[i].feature < cols)
+          phi[(uint64_t)p[i].feature * stride] += scale * (w * (p[i].one - p[i].zero) * n.leaf * fr.share);
+      }
+      continue;
+    }
+    const int32_t hot = child_of(n, x((uint32_t)n.feature));
+    const int32_t cold = hot == n.left ? n.right : n.left;
+    const float hot_zero = tree[hot].cover / n.cover, cold_zero = tree[cold].cover / n.cover;
+    // A feature already on the path is unwound, and its fractions carry
+    // into both children.
+    float in_zero = 1.0f, in_one = 1.0f;
+    uint32_t k = 0;
+    while (k <= last && p[k].feature != n.feature) ++k;
+    if (k <= last) {
+      in_zero = p[k].zero;
+      in_one = p[k].one;
+      path_unwind(p, last, k);
+      --last;
+    }
+    // The conditioned feature: present, the walk follows the row; absent,
+    // it splits by cover; neither child extends the path with it.
+    float hot_share = fr.share, cold_share = fr.share;
+    const bool on_fixed = condition != 0 && n.feature == fixed;
+    if (on_fixed && condition > 0) cold_share = 0.0f;
+    if (on_fixed && condition < 0) {
+      hot_share *= hot_zero;
+      cold_share *= cold_zero;
+    }
+    const uint32_t extend = on_fixed ? 0u : 1u;
+    stack[top++] = ShapFrame{cold, last + 1, seg, cold_zero * in_zero, 0.0f, cold_share, n.feature, extend};
+    stack[top++] = ShapFrame{hot, last + 1, seg, hot_zero * in_zero, in_one, hot_share, n.feature, extend};
+  }
+  return true;
+}
 
 __global__ __launch_bounds__(64) void k_contribs_shap(const float* __restrict__ X, const uint64_t* __restrict__ indptr,
                                                       const uint32_t* __restrict__ indices, uint32_t rows,
@@ -179,50 +249,53 @@ __global__ __launch_bounds__(64) void k_contribs_shap(const float* __restrict__ 
     for (uint32_t f = 0; f < cols; ++f) phi[f] = 0.0f;
     float bias = base ? base[r] : base_value;
     for (uint32_t t = 0; t < trees; ++t) {
-      const MgbTreeNode* tree = nodes + offsets[t];
       bias += means[offsets[t]];
-      uint32_t top = 0;
-      stack[top++] = ShapFrame{0, 0, 0, 1.0f, 1.0f, -1};
-      while (top) {
-        const ShapFrame fr = stack[--top];
-        const uint32_t seg = fr.parent + fr.len + 1;
-        // The host admits trees of depth <= kShapDepth only, which never
-        // reach these limits; a deeper tree stops here with a NaN bias.
-        if (seg + fr.len >= kShapPath || top + 2 > kShapDepth + 2) {
-          bias = __uint_as_float(0x7fc00000u);
-          break;
-        }
-        for (uint32_t i = 0; i < fr.len; ++i) path[seg + i] = path[fr.parent + i];
-        PathElem* p = path + seg;
-        path_extend(p, fr.len, fr.zero, fr.one, fr.feature);
-        uint32_t last = fr.len;
-        const MgbTreeNode n = tree[fr.node];
-        if (n.left < 0) {
-          for (uint32_t i = 1; i <= last; ++i) {
-            const float w = path_unwound_sum(p, last, i);
-            if ((uint32_t)p[i].feature < cols) phi[p[i].feature] += w * (p[i].one - p[i].zero) * n.leaf;
-          }
-          continue;
-        }
-        const int32_t hot = child_of(n, x((uint32_t)n.feature));
-        const int32_t cold = hot == n.left ? n.right : n.left;
-        const float hot_zero = tree[hot].cover / n.cover, cold_zero = tree[cold].cover / n.cover;
-        // A feature already on the path is unwound, and its fractions carry
-        // into both children.
-        float in_zero = 1.0f, in_one = 1.0f;
-        uint32_t k = 0;
-        while (k <= last && p[k].feature != n.feature) ++k;
-        if (k <= last) {
-          in_zero = p[k].zero;
-          in_one = p[k].one;
-          path_unwind(p, last, k);
-          --last;
-        }
-        stack[top++] = ShapFrame{cold, last + 1, seg, cold_zero * in_zero, 0.0f, n.feature};
-        stack[top++] = ShapFrame{hot, last + 1, seg, hot_zero * in_zero, in_one, n.feature};
-      }
+      if (!shap_tree(nodes + offsets[t], x, cols, phi, 1, 1.0f, 0, -1, path, stack))
+        bias = __uint_as_float(0x7fc00000u);  // a NaN bias marks the row
     }
     phi[cols] = bias;
+  }
+}
+
+// SHAP interaction values of row r, a (cols + 1) x (cols + 1) matrix at
+// out + r * (cols + 1)^2: off the diagonal, half the change of feature j's
+// value between feature i always present and always absent; on it, feature
+// i's value less its interactions; the bias in the last corner.
+__global__ __launch_bounds__(64) void k_interactions_shap(const float* __restrict__ X,
+                                                          const uint64_t* __restrict__ indptr,
+                                                          const uint32_t* __restrict__ indices, uint32_t rows,
+                                                          uint32_t cols, const MgbTreeNode* __restrict__ nodes,
+                                                          const float* __restrict__ means,
+                                                          const uint32_t* __restrict__ offsets, uint32_t trees,
+                                                          const float* __restrict__ base, float base_value,
+                                                          float* __restrict__ out) {
+  PathElem path[kShapPath];
+  ShapFrame stack[kShapDepth + 2];
+  const uint64_t width = (uint64_t)cols + 1;
+  for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
+    const RowView x = row_view(X, indptr, indices, r, cols);
+    float* m = out + r * width * width;
+    for (uint64_t e = 0; e < width * width; ++e) m[e] = 0.0f;
+    float bias = base ? base[r] : base_value;
+    bool ok = true;
+    for (uint32_t t = 0; t < trees; ++t) {
+      bias += means[offsets[t]];
+      ok &= shap_tree(nodes + offsets[t], x, cols, m, (uint32_t)width + 1, 1.0f, 0, -1, path, stack);
+    }
+    for (uint32_t i = 0; i < cols; ++i) {
+      float* row_i = m + (uint64_t)i * width;
+      for (uint32_t t = 0; t < trees; ++t) {
+        ok &= shap_tree(nodes + offsets[t], x, cols, row_i, 1, 0.5f, 1, (int32_t)i, path, stack);
+        ok &= shap_tree(nodes + offsets[t], x, cols, row_i, 1, -0.5f, -1, (int32_t)i, path, stack);
+      }
+      // Feature i never enters its own conditioned walks, so row_i[i] still
+      // holds its value.
+      float sum = 0.0f;
+      for (uint32_t j = 0; j < cols; ++j)
+        if (j != i) sum += row_i[j];
+      row_i[i] -= sum;
+    }
+    m[width * width - 1] = ok ? bias : __uint_as_float(0x7fc00000u);
   }
 }
 
@@ -256,7 +329,7 @@ int mgb_predict_leaf(const float* X, const uint64_t* indptr, const uint32_t* ind
 int mgb_predict_contribs(const float* X, const uint64_t* indptr, const uint32_t* indices, uint32_t rows,
                          uint32_t cols, const MgbTreeNode* nodes, const float* node_means,
                          const uint32_t* tree_offsets, uint32_t trees, uint32_t max_depth, uint32_t approximate,
-                         const float* base, float base_value, float* out) {
+                         uint32_t interactions, const float* base, float base_value, float* out) {
   if (!rows) return 0;
   if (!X || !nodes || !node_means || !tree_offsets || !out || (indptr && !indices)) {
     set_error("mgb_predict_contribs: null argument");
@@ -268,8 +341,12 @@ int mgb_predict_contribs(const float* X, const uint64_t* indptr, const uint32_t*
   }
   if (approximate) {
     launch(MGB_PROF_PREDICT, k_contribs_approx, dim3(explain_grid(rows, 256)), dim3(256), 0, X, indptr, indices,
-           rows, cols, nodes, node_means, tree_offsets, trees, base, base_value, out);
+           rows, cols, nodes, node_means, tree_offsets, trees, base, base_value, interactions ? 1u : 0u, out);
     MGB_LAUNCH_CHECK("k_contribs_approx");
+  } else if (interactions) {
+    launch(MGB_PROF_PREDICT, k_interactions_shap, dim3(explain_grid(rows, 64)), dim3(64), 0, X, indptr, indices,
+           rows, cols, nodes, node_means, tree_offsets, trees, base, base_value, out);
+    MGB_LAUNCH_CHECK("k_interactions_shap");
   } else {
     launch(MGB_PROF_PREDICT, k_contribs_shap, dim3(explain_grid(rows, 64)), dim3(64), 0, X, indptr, indices, rows,
            cols, nodes, node_means, tree_offsets, trees, base, base_value, out);

@@ -1131,12 +1131,14 @@ uint32_t node_means(const std::vector<MgbTreeNode>& t, float* means) {
 
 std::vector<float> Learner::predict_explain(DMatrix& data, int type, uint32_t end) {
   drain();
-  require(type == 2 || type == 3 || type == 6, "Prediction type must be 2, 3 or 6 here.");
+  require(type >= 2 && type <= 6, "Prediction type must be 2 to 6 here.");
+  const bool interactions = type == 4 || type == 5;
   if (end == 0 || end > trees.size()) end = (uint32_t)trees.size();
   if (initialized)
     require(data.cols == num_feature, "Feature shape mismatch: expected " + std::to_string(num_feature) + ", got " +
                                           std::to_string(data.cols));
-  const uint64_t width = type == 6 ? end : (uint64_t)data.cols + 1;
+  const uint64_t columns = (uint64_t)data.cols + 1;
+  const uint64_t width = type == 6 ? end : (interactions ? columns * columns : columns);
   std::vector<float> out((size_t)data.rows * width, 0.0f);
   if (!data.rows) return out;
   if (type == 6 && end == 0) return out;
@@ -1168,7 +1170,8 @@ std::vector<float> Learner::predict_explain(DMatrix& data, int type, uint32_t en
     }
     kcheck(mgb_predict_contribs(X, indptr, indices, data.rows, data.cols, d_model_nodes_.as<MgbTreeNode>(),
                                 d_model_means_.as<float>(), d_model_offsets_.as<uint32_t>(), end, deepest,
-                                type == 3 ? 1u : 0u, d_base.get() ? d_base.as<float>() : nullptr,
+                                type == 3 || type == 5 ? 1u : 0u, interactions ? 1u : 0u,
+                                d_base.get() ? d_base.as<float>() : nullptr,
                                 base_margin_value(), d_out.as<float>()),
            "contribution prediction");
   }

@@ -138,8 +138,9 @@ class Learner {
   void boost(DMatrix& data, const float* grad, const float* hess, size_t count);
   // Predictions (margin when output_margin) for rounds [begin, end); end 0 = all.
   std::vector<float> predict(DMatrix& data, bool output_margin, uint32_t begin, uint32_t end);
-  // Leaf indices (type 6: rows x trees) or feature contributions (type 2
-  // exact, 3 approximate: rows x (cols + 1), the bias last) of rounds
+  // Leaf indices (type 6: rows x trees), feature contributions (type 2
+  // exact, 3 approximate: rows x (cols + 1), the bias last) or their
+  // interactions (4 exact, 5 approximate: rows x (cols + 1)^2) of rounds
   // [0, end); end 0 = all (src/learner.cpp:455-560).
   std::vector<float> predict_explain(DMatrix& data, int type, uint32_t end);
   // The same predictions left on the device: in `scratch`, or in the
