@@ -1,14 +1,14 @@
 // Prediction beyond values and margins (reference src/learner.cpp:455-560
 // Learner::predict types 2 to 6): each row's leaf index in every tree, its
 // per-feature contributions to its margin and their pairwise interactions --
-// exact path-dependent
-// TreeSHAP (Lundberg, Erion and Lee 2018, "Consistent individualized feature
-// attribution for tree ensembles", Algorithm 2) or the approximation that
-// credits each split's feature with the change of the cover-weighted node
-// mean along the row's path.  Rows are dense (X with `cols` values a row) or
-// CSR (indptr/indices/values; absent entries are missing), walked with the
-// predictor's rule: value < threshold goes left, NaN follows default_left.
-// One thread per row walks every tree, so a row's sums need no atomics.
+// exact path-dependent TreeSHAP (Lundberg, Erion and Lee 2018, "Consistent
+// individualized feature attribution for tree ensembles", Algorithm 2), or
+// the approximation that credits each split's feature with the change of the
+// cover-weighted node mean along the row's path.  Rows are dense (X with
+// `cols` values a row) or CSR (indptr/indices/values; absent entries are
+// missing), walked with the predictor's rule: value < threshold goes left,
+// NaN follows default_left.  One thread per row walks every tree, so a row's
+// sums need no atomics.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
