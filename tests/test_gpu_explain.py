@@ -230,3 +230,17 @@ def test_nonzero_start_and_two_types_are_refused(xgb):
         bst.predict(d, pred_contribs=True, iteration_range=(1, 3))
     with pytest.raises(ValueError, match="One type of prediction"):
         bst.predict(d, pred_leaf=True, pred_contribs=True)
+
+
+def test_interpret_shap_values_split_the_bias(xgb):
+    X, y = _data(rows=50, cols=4, seed=9)
+    model = xgb.XGBRegressor(n_estimators=4, max_depth=3, max_bin=32)
+    model.fit(X, y)
+    values, bias = xgb.interpret.shap_values(model, X)
+    contribs = model.get_booster().predict(xgb.DMatrix(X), pred_contribs=True)
+    np.testing.assert_array_equal(values, contribs[:, :-1])
+    np.testing.assert_array_equal(bias, contribs[:, -1])
+    with pytest.raises(NotImplementedError):
+        xgb.interpret.shap_values(model, X, X_background=X)
+    with pytest.raises(ValueError):
+        xgb.interpret.shap_values(model.get_booster(), xgb.DMatrix(X), missing=0.0)
