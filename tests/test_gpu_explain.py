@@ -244,3 +244,19 @@ def test_interpret_shap_values_split_the_bias(xgb):
         xgb.interpret.shap_values(model, X, X_background=X)
     with pytest.raises(ValueError):
         xgb.interpret.shap_values(model.get_booster(), xgb.DMatrix(X), missing=0.0)
+
+
+def test_empty_matrix_and_untrained_model(xgb):
+    X, y = _data(rows=30, cols=4)
+    d = xgb.DMatrix(X, label=y)
+    fresh = xgb.Booster({"max_depth": 2}, [d])
+    contribs = fresh.predict(d, pred_contribs=True)
+    assert contribs.shape == (30, 5)
+    np.testing.assert_array_equal(contribs[:, :4], 0.0)
+    np.testing.assert_allclose(contribs[:, 4], fresh.predict(d, output_margin=True), rtol=0, atol=1e-6)
+    assert fresh.predict(d, pred_leaf=True).shape == (30, 0)
+    bst = xgb.train({"max_depth": 2}, d, 2)
+    empty = xgb.DMatrix(np.zeros((0, 4), dtype=np.float32))
+    assert bst.predict(empty, pred_contribs=True).shape == (0, 5)
+    assert bst.predict(empty, pred_interactions=True).shape == (0, 5, 5)
+    assert bst.predict(empty, pred_leaf=True).size == 0

@@ -224,3 +224,24 @@ def test_grow_tree_rejects_rows_from_two_to_the_31(sparse):
         rc = lib.mgb_grow_tree(ctypes.byref(shape), ctypes.byref(m), *([None] * 14))
     assert rc == -1
     assert "below 2^31" in lib.mgb_last_error().decode()
+
+
+def test_explain_entry_points_validate_on_the_host():
+    """The leaf and contribution entry points refuse null buffers and trees
+    deeper than exact TreeSHAP's limit before any device work, and return at
+    once for an empty matrix (no GPU needed)."""
+    import device_lib as D
+    lib = D.lib()
+    one = ctypes.c_uint32(1)
+    assert lib.mgb_predict_leaf(None, None, None, ctypes.c_uint32(0), one, None, None, one, None) == 0
+    assert lib.mgb_predict_leaf(None, None, None, one, one, None, None, one, None) == -1
+    assert "null argument" in lib.mgb_last_error().decode()
+    buf = ctypes.create_string_buffer(64)
+    args = [buf, None, None, one, one, buf, buf, buf, one, ctypes.c_uint32(17), ctypes.c_uint32(0),
+            ctypes.c_uint32(0), None, ctypes.c_float(0.0), buf]
+    assert lib.mgb_predict_contribs(*args) == -1
+    assert "depth at most 16" in lib.mgb_last_error().decode()
+    args[1] = buf  # CSR offsets without column ids
+    args[10] = ctypes.c_uint32(1)
+    assert lib.mgb_predict_contribs(*args) == -1
+    assert "null argument" in lib.mgb_last_error().decode()
