@@ -260,3 +260,21 @@ def test_empty_matrix_and_untrained_model(xgb):
     assert bst.predict(empty, pred_contribs=True).shape == (0, 5)
     assert bst.predict(empty, pred_interactions=True).shape == (0, 5, 5)
     assert bst.predict(empty, pred_leaf=True).size == 0
+
+
+def test_estimator_apply_returns_leaf_ids(xgb):
+    X, y = _data(rows=50, cols=4, seed=13)
+    model = xgb.XGBRegressor(n_estimators=3, max_depth=3, max_bin=32)
+    model.fit(X, y)
+    leaves = model.apply(X)
+    assert leaves.shape == (50, 3)
+    np.testing.assert_array_equal(leaves, model.get_booster().predict(xgb.DMatrix(X), pred_leaf=True))
+    trees = _trees(model.get_booster())
+    np.testing.assert_array_equal(leaves, np.array([[t.leaf(x) for t in trees] for x in X], dtype=np.float32))
+
+
+def test_classifier_apply(xgb):
+    X, y = _data(rows=40, cols=4, seed=17)
+    model = xgb.XGBClassifier(n_estimators=2, max_depth=2, max_bin=16)
+    model.fit(X, (y > 0).astype(np.int64))
+    np.testing.assert_array_equal(model.apply(X), model.get_booster().predict(xgb.DMatrix(X), pred_leaf=True))

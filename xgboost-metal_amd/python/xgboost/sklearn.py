@@ -104,6 +104,12 @@ class XGBModel:
         except AttributeError:
             return (0, 0)
 
+    def apply(self, X: Any, iteration_range: Any = None) -> np.ndarray:
+        """Leaf index each row reaches in every tree, rows x trees (reference
+        sklearn.py:1509); the rounds end at the early-stopping best unless given."""
+        return self.get_booster().predict(self._dmatrix(X), pred_leaf=True,
+                                          iteration_range=self._iteration_range(iteration_range))
+
     @property
     def best_iteration(self) -> int:
         return self.get_booster().best_iteration
